@@ -1,0 +1,104 @@
+/*
+ * g2v.h -- C ABI of the MI355X (gfx950) Gaussian-to-Voxel splatting library (libg2v_hip.so).
+ *
+ * Drop-in boundary for the reference's pybind11 module CudaGaussianVoxelizer._C
+ * (src/bindings.cpp:7-64 of lunarlab-gatech/ShelfGaussian-CudaGaussianVoxelizer).
+ * Every entry point takes plain device pointers, sizes and an explicit HIP stream (passed as
+ * void*, a hipStream_t); nothing allocates device memory: outputs and workspaces belong to the
+ * caller, whose sizes come from the *_workspace queries.  Entry points return G2V_OK or an
+ * error code; g2v_last_error() gives the message (thread-local).  Nothing calls exit().
+ *
+ * Conventions (reference include/utils.cuh:50-80, src/cuda_gaussian_voxelizer.cu:1511-1519):
+ *   dims  X = (int)((r[3]-r[0])/s[0]) in float32 (likewise Y, Z); grid tensors are C-contiguous
+ *         (X, Y, Z[, C]);  tiles 4x4x4, Tx = ceil(X/4);  tile id (tx*Ty + ty)*Tz + tz.
+ *   means (N,3), opacity (N,), covariances (N,9 row-major 3x3), features (N,C): float32.
+ *   cov_inv (N,9) float32; lb, ub (N,3) int32 inclusive voxel box (0,-1 when empty);
+ *   nvox (N,) int32; g2t_offsets (N+1,) int32; g2t_tile_ids (M,) int32.
+ */
+#ifndef G2V_H
+#define G2V_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define G2V_OK 0
+#define G2V_ERR_INVALID 1   /* bad argument (shape, null pointer, workspace too small) */
+#define G2V_ERR_HIP 2       /* a HIP runtime call failed */
+#define G2V_ERR_LIMIT 3     /* problem exceeds a 32-bit index (pairs, grid cells) */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* g2v_last_error(void);
+
+/* ABI version of this library. */
+int g2v_abi_version(void);
+
+/* Voxel and tile grid of a (voxel_size, voxel_range) pair, host only.
+ * Reference: src/cuda_gaussian_voxelizer.cu:1511-1519. */
+int g2v_grid_dims(const float voxel_size[3], const float voxel_range[6], int dims[3], int tiles[3]);
+
+/* ---- forward ------------------------------------------------------------------------------
+ * The reference forward (cuda_gaussian_voxelizer_forward, src/cuda_gaussian_voxelizer.cu:1484-1918,
+ * bound at src/bindings.cpp:8-28) is split in two calls because the length M of the
+ * Gaussian->Tile CSR is data dependent and the caller allocates g2t_tile_ids:
+ *
+ * g2v_forward_plan: per-Gaussian box, inverse covariance, voxel count and G->T row offsets
+ * (reference .cu:1575-1631).  Synchronises the stream once to return M in *num_pairs. */
+size_t g2v_forward_plan_workspace(int n);
+int g2v_forward_plan(int n, const float* means3D, const float* covariances,
+                     const float voxel_size[3], const float voxel_range[6],
+                     float* cov_inv, int* valid_voxel_lb, int* valid_voxel_ub,
+                     int* num_voxels_per_gaussian, int* g2t_offsets,
+                     void* workspace, size_t workspace_bytes, long long* num_pairs, void* stream);
+
+/* g2v_forward_splat: G->T fill, radix sort into the Tile->Gaussian CSR, per-tile splat of the
+ * density and, when feat_dim > 0, of the density-weighted feature average (reference
+ * .cu:1634-1904).  density (X,Y,Z) and grid_feats (X,Y,Z,feat_dim) are written completely;
+ * features may be NULL when feat_dim == 0.  Asynchronous. */
+size_t g2v_forward_splat_workspace(int n, long long num_pairs, const float voxel_size[3],
+                                   const float voxel_range[6]);
+int g2v_forward_splat(int n, int feat_dim, const float* means3D, const float* opacity,
+                      const float* features, const float voxel_size[3], const float voxel_range[6],
+                      const float* cov_inv, const int* valid_voxel_lb, const int* valid_voxel_ub,
+                      const int* g2t_offsets, long long num_pairs, int* g2t_tile_ids,
+                      float* density, float* grid_feats,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- backward -----------------------------------------------------------------------------
+ * Replaces cuda_gaussian_voxelizer_backward (src/cuda_gaussian_voxelizer.cu:1920-2057, bound at
+ * src/bindings.cpp:30-64).  Writes grad_means (N,3), grad_cov (N,9, symmetric), grad_opacity (N,)
+ * and, when feat_dim > 0, grad_features (N,feat_dim).  grad_feats/grid_feats/features may be
+ * NULL when feat_dim == 0.  Asynchronous; atomic-free and deterministic. */
+size_t g2v_backward_workspace(int n, int feat_dim, long long num_pairs, const float voxel_size[3],
+                              const float voxel_range[6]);
+int g2v_backward(int n, int feat_dim, const float* grad_density, const float* grad_feats,
+                 const float* means3D, const float* opacity, const float* cov_inv,
+                 const float voxel_size[3], const float voxel_range[6],
+                 const int* valid_voxel_lb, const int* valid_voxel_ub,
+                 const int* num_voxels_per_gaussian, const int* g2t_offsets,
+                 const int* g2t_tile_ids, long long num_pairs, const float* density,
+                 const float* grid_feats, const float* features,
+                 float* grad_means, float* grad_cov, float* grad_opacity, float* grad_features,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- Tile->Gaussian CSR (inspection) -------------------------------------------------------
+ * The internal Tile->Gaussian CSR of the forward, for parity tests: the stable sort of the G->T
+ * pairs by tile (sorted_tiles, sorted_gauss: M each; reference .cu:1673-1691), the list bounds of
+ * every tile (tile_offsets: T+1), and the run-length encoding of the sorted tiles (unique_tiles,
+ * counts: T each, runs_offsets: T+1, *num_runs on the device; reference .cu:1708-1772). */
+size_t g2v_t2g_workspace(int n, long long num_pairs, const float voxel_size[3],
+                         const float voxel_range[6]);
+int g2v_build_t2g(int n, const float voxel_size[3], const float voxel_range[6],
+                  const int* valid_voxel_lb, const int* valid_voxel_ub, const int* g2t_offsets,
+                  const int* g2t_tile_ids, long long num_pairs, int* sorted_tiles,
+                  int* sorted_gauss, int* tile_offsets, int* unique_tiles, int* counts,
+                  int* runs_offsets, int* num_runs, void* workspace, size_t workspace_bytes,
+                  void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* G2V_H */

@@ -1,0 +1,252 @@
+"""Drop-in for the reference's pybind11 module ``CudaGaussianVoxelizer._C`` (src/bindings.cpp:7-64).
+
+Same function names, keyword arguments, tuple layouts and error behaviour (``RuntimeError``)
+as the reference; the work is done by libg2v_hip.so through its C ABI (include/g2v.h) on the
+caller's current HIP stream.  Outputs and workspaces come from PyTorch's caching allocator.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+__all__ = ["gaussian_voxelizer_forward", "gaussian_voxelizer_backward",
+           "CudaFeatsCosinelossForward", "CudaFeatsCosinelossBackward", "build_t2g", "grid_dims"]
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _host_values(t, n, name):
+    """Host floats of voxel_size / voxel_range.  Device tensors are read once per version."""
+    if isinstance(t, torch.Tensor):
+        if t.numel() != n:
+            raise RuntimeError(f"{name} must have {n} elements, got {t.numel()}")
+        if t.device.type == "cpu":
+            return [float(v) for v in t.detach().reshape(-1).to(torch.float32).tolist()]
+        cached = t.__dict__.get("_g2v_host")
+        if cached is not None and cached[0] == t._version:
+            return cached[1]
+        vals = [float(v) for v in t.detach().reshape(-1).to(torch.float32).cpu().tolist()]
+        t.__dict__["_g2v_host"] = (t._version, vals)
+        return vals
+    vals = [float(v) for v in t]
+    if len(vals) != n:
+        raise RuntimeError(f"{name} must have {n} elements, got {len(vals)}")
+    return vals
+
+
+def grid_dims(voxel_size, voxel_range):
+    """((X, Y, Z), (Tx, Ty, Tz)) as the forward computes them (reference .cu:1511-1519)."""
+    lib = _lib.load()
+    vs = _lib.floats(_host_values(voxel_size, 3, "voxel_size"))
+    vr = _lib.floats(_host_values(voxel_range, 6, "voxel_range"))
+    dims = (ctypes.c_int * 3)()
+    tiles = (ctypes.c_int * 3)()
+    _lib.check(lib.g2v_grid_dims(vs, vr, dims, tiles), "g2v_grid_dims")
+    return tuple(dims), tuple(tiles)
+
+
+def _f32_input(t, name, shape=None):
+    if not isinstance(t, torch.Tensor):
+        raise RuntimeError(f"{name} must be a tensor")
+    if t.device.type != "cuda":
+        raise RuntimeError(f"{name} must be a GPU tensor, got {t.device}")
+    if t.dtype != torch.float32:
+        raise RuntimeError(f"expected scalar type Float for {name} but found {t.dtype}")
+    if shape is not None:
+        t = t.reshape(shape)
+    return t.detach().contiguous()
+
+
+def _check_saved(t, name, dtype, device):
+    if not isinstance(t, torch.Tensor) or t.dtype != dtype or not t.is_contiguous() or t.device != device:
+        raise RuntimeError(f"{name} must be a contiguous {dtype} tensor on {device}")
+
+
+def _stream(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def gaussian_voxelizer_forward(means3D, opacity, covariances, voxel_size, voxel_range, features=None):
+    """Gaussian voxelization forward pass.
+
+    Args:
+        means3D (N,3), opacity (N,) (or (N,1)), covariances (N,9) row-major 3x3 (or (N,3,3)),
+        voxel_size (3,), voxel_range (6,) [x_min, y_min, z_min, x_max, y_max, z_max],
+        features (N,C) or None.  All float32 on the GPU.
+    Returns the reference's 9-tuple (src/cuda_gaussian_voxelizer.cu:1913):
+        density (X,Y,Z), cov_inv (N,9), valid_voxel_lb (N,3) int32, valid_voxel_ub (N,3) int32,
+        num_voxels_per_gaussian (N,) int32, grid_feats (X,Y,Z,C) (C = 0 without features),
+        g2t_offsets (N+1,) int32, g2t_tile_ids (M,) int32, forward time in seconds.
+    """
+    lib = _lib.load()
+    means = _f32_input(means3D, "means3D")
+    if means.dim() != 2 or means.shape[1] != 3:
+        raise RuntimeError(f"means3D must be (N, 3), got {tuple(means.shape)}")
+    n = means.shape[0]
+    dev = means.device
+    op = _f32_input(opacity, "opacity", (n,))
+    cov = _f32_input(covariances, "covariances", (n, 9))
+    feats = None
+    C = 0
+    if features is not None:
+        feats = _f32_input(features, "features")
+        if feats.dim() != 2 or feats.shape[0] != n:
+            raise RuntimeError(f"features must be (N, C) with N = {n}, got {tuple(feats.shape)}")
+        C = feats.shape[1]
+        if C == 0:
+            feats = None
+    vs_h = _host_values(voxel_size, 3, "voxel_size")
+    vr_h = _host_values(voxel_range, 6, "voxel_range")
+    vs, vr = _lib.floats(vs_h), _lib.floats(vr_h)
+    (X, Y, Z), _ = grid_dims(vs_h, vr_h)
+
+    with torch.cuda.device(dev):
+        stream = _stream(dev)
+        cur = torch.cuda.current_stream(dev)
+        i32 = dict(dtype=torch.int32, device=dev)
+        f32 = dict(dtype=torch.float32, device=dev)
+        cov_inv = torch.empty(n, 9, **f32)
+        lb = torch.empty(n, 3, **i32)
+        ub = torch.empty(n, 3, **i32)
+        nvox = torch.empty(n, **i32)
+        g2t_offsets = torch.empty(n + 1, **i32)
+        ws = torch.empty(lib.g2v_forward_plan_workspace(n), dtype=torch.uint8, device=dev)
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record(cur)
+        M = ctypes.c_longlong(0)
+        _lib.check(lib.g2v_forward_plan(n, _ptr(means), _ptr(cov), vs, vr, _ptr(cov_inv), _ptr(lb),
+                                        _ptr(ub), _ptr(nvox), _ptr(g2t_offsets), _ptr(ws),
+                                        ws.numel(), ctypes.byref(M), stream),
+                   "gaussian_voxelizer_forward (plan)")
+        M = int(M.value)
+        g2t_tile_ids = torch.empty(M, **i32)
+        density = torch.empty(X, Y, Z, **f32)
+        grid_feats = torch.empty(X, Y, Z, C, **f32)
+        ws2 = torch.empty(lib.g2v_forward_splat_workspace(n, M, vs, vr), dtype=torch.uint8, device=dev)
+        _lib.check(lib.g2v_forward_splat(n, C, _ptr(means), _ptr(op), _ptr(feats), vs, vr,
+                                         _ptr(cov_inv), _ptr(lb), _ptr(ub), _ptr(g2t_offsets), M,
+                                         _ptr(g2t_tile_ids), _ptr(density), _ptr(grid_feats),
+                                         _ptr(ws2), ws2.numel(), stream),
+                   "gaussian_voxelizer_forward (splat)")
+        stop.record(cur)
+        stop.synchronize()
+        fwd_sec = start.elapsed_time(stop) / 1000.0
+    return (density, cov_inv, lb, ub, nvox, grid_feats, g2t_offsets, g2t_tile_ids, fwd_sec)
+
+
+def gaussian_voxelizer_backward(grad_output, grad_feats_output, means3D, opacity, cov_inv, voxel_size,
+                                voxel_range, valid_voxel_lb, valid_voxel_ub, num_voxels_per_gaussian,
+                                g2t_offsets, g2t_tile_ids, density, grid_feats, features=None):
+    """Gaussian voxelization backward pass (reference src/cuda_gaussian_voxelizer.cu:1920-2057).
+
+    Returns the reference's 5-tuple: grad_means (N,3), grad_cov (N,9), grad_opacity (N,),
+    grad_feats (N,C) (N,0 without features), backward time in seconds.
+    """
+    lib = _lib.load()
+    if not isinstance(means3D, torch.Tensor) or means3D.device.type != "cuda":
+        raise RuntimeError("means3D must be a GPU tensor")
+    dev = means3D.device
+    f32, i32 = torch.float32, torch.int32
+    for t, name in ((grad_output, "grad_output"), (means3D, "means3D"), (opacity, "opacity"),
+                    (cov_inv, "cov_inv"), (density, "density"), (grid_feats, "grid_feats")):
+        _check_saved(t, name, f32, dev)
+    for t, name in ((valid_voxel_lb, "valid_voxel_lb"), (valid_voxel_ub, "valid_voxel_ub"),
+                    (num_voxels_per_gaussian, "num_voxels_per_gaussian"), (g2t_offsets, "g2t_offsets"),
+                    (g2t_tile_ids, "g2t_tile_ids")):
+        _check_saved(t, name, i32, dev)
+    n = means3D.shape[0]
+    if g2t_offsets.numel() != n + 1:
+        raise RuntimeError(f"g2t_offsets must have N+1 = {n + 1} elements, got {g2t_offsets.numel()}")
+    vs_h = _host_values(voxel_size, 3, "voxel_size")
+    vr_h = _host_values(voxel_range, 6, "voxel_range")
+    vs, vr = _lib.floats(vs_h), _lib.floats(vr_h)
+    (X, Y, Z), _ = grid_dims(vs_h, vr_h)
+    if tuple(grad_output.shape) != (X, Y, Z):
+        raise RuntimeError(f"grad_output must be {(X, Y, Z)}, got {tuple(grad_output.shape)}")
+    C = 0
+    feats = gF = None
+    if features is not None:
+        _check_saved(features, "features", f32, dev)
+        C = features.shape[1]
+        if C > 0:
+            feats = features
+            _check_saved(grad_feats_output, "grad_feats_output", f32, dev)
+            if tuple(grad_feats_output.shape) != (X, Y, Z, C) or tuple(grid_feats.shape) != (X, Y, Z, C):
+                raise RuntimeError("grad_feats_output and grid_feats must be (X, Y, Z, C)")
+            gF = grad_feats_output
+    M = g2t_tile_ids.numel()
+
+    with torch.cuda.device(dev):
+        stream = _stream(dev)
+        cur = torch.cuda.current_stream(dev)
+        grad_means = torch.empty(n, 3, dtype=f32, device=dev)
+        grad_cov = torch.empty(n, 9, dtype=f32, device=dev)
+        grad_opacity = torch.empty(n, dtype=f32, device=dev)
+        grad_feats = torch.empty(n, C, dtype=f32, device=dev)
+        ws = torch.empty(max(1, lib.g2v_backward_workspace(n, C, M, vs, vr)), dtype=torch.uint8, device=dev)
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record(cur)
+        _lib.check(lib.g2v_backward(n, C, _ptr(grad_output), _ptr(gF), _ptr(means3D), _ptr(opacity),
+                                    _ptr(cov_inv), vs, vr, _ptr(valid_voxel_lb), _ptr(valid_voxel_ub),
+                                    _ptr(num_voxels_per_gaussian), _ptr(g2t_offsets), _ptr(g2t_tile_ids),
+                                    M, _ptr(density), _ptr(grid_feats), _ptr(feats),
+                                    _ptr(grad_means), _ptr(grad_cov), _ptr(grad_opacity),
+                                    _ptr(grad_feats), _ptr(ws), ws.numel(), stream),
+                   "gaussian_voxelizer_backward")
+        stop.record(cur)
+        stop.synchronize()
+        bwd_sec = start.elapsed_time(stop) / 1000.0
+    return (grad_means, grad_cov, grad_opacity, grad_feats, bwd_sec)
+
+
+def build_t2g(voxel_size, voxel_range, valid_voxel_lb, valid_voxel_ub, g2t_offsets, g2t_tile_ids):
+    """The forward's internal Tile->Gaussian CSR, for inspection and parity tests.
+
+    Returns a dict: sorted_tiles (M,), sorted_gauss (M,), tile_offsets (T+1,), and the run-length
+    encoding unique_tiles (U,), counts (U,), runs_offsets (U+1,), num_runs.
+    """
+    lib = _lib.load()
+    dev = g2t_offsets.device
+    n = g2t_offsets.numel() - 1
+    M = g2t_tile_ids.numel()
+    vs, vr = _lib.floats(_host_values(voxel_size, 3, "voxel_size")), _lib.floats(_host_values(voxel_range, 6, "voxel_range"))
+    (_, tiles) = grid_dims(list(vs), list(vr))
+    T = tiles[0] * tiles[1] * tiles[2]
+    with torch.cuda.device(dev):
+        i32 = dict(dtype=torch.int32, device=dev)
+        out = dict(sorted_tiles=torch.empty(M, **i32), sorted_gauss=torch.empty(M, **i32),
+                   tile_offsets=torch.empty(T + 1, **i32), unique_tiles=torch.empty(T, **i32),
+                   counts=torch.empty(T, **i32), runs_offsets=torch.empty(T + 1, **i32),
+                   num_runs=torch.empty(1, **i32))
+        ws = torch.empty(lib.g2v_t2g_workspace(n, M, vs, vr), dtype=torch.uint8, device=dev)
+        _lib.check(lib.g2v_build_t2g(n, vs, vr, _ptr(valid_voxel_lb), _ptr(valid_voxel_ub),
+                                     _ptr(g2t_offsets), _ptr(g2t_tile_ids), M, _ptr(out["sorted_tiles"]),
+                                     _ptr(out["sorted_gauss"]), _ptr(out["tile_offsets"]),
+                                     _ptr(out["unique_tiles"]), _ptr(out["counts"]),
+                                     _ptr(out["runs_offsets"]), _ptr(out["num_runs"]), _ptr(ws),
+                                     ws.numel(), _stream(dev)),
+                   "build_t2g")
+        U = int(out["num_runs"].item())
+    out["num_runs"] = U
+    out["unique_tiles"] = out["unique_tiles"][:U]
+    out["counts"] = out["counts"][:U]
+    out["runs_offsets"] = out["runs_offsets"][:U + 1]
+    return out
+
+
+def CudaFeatsCosinelossForward(voxel_label, occ_gt_mask_camera, grid_feats, pseudo_dino_gt):
+    """Not part of the G2V splatting path (reference src/cuda_feats_loss.cu); not provided."""
+    raise NotImplementedError("CudaFeatsCosinelossForward is outside the G2V splatting path of this build")
+
+
+def CudaFeatsCosinelossBackward(grad_output, voxel_label, occ_gt_mask_camera, grid_feats, pseudo_dino_gt,
+                                num_valid_voxel):
+    """Not part of the G2V splatting path (reference src/cuda_feats_loss.cu); not provided."""
+    raise NotImplementedError("CudaFeatsCosinelossBackward is outside the G2V splatting path of this build")

@@ -1,0 +1,87 @@
+"""MI355X (gfx950) Gaussian-to-Voxel splatting with the reference's Python API.
+
+Mirrors CudaGaussianVoxelizer/__init__.py of lunarlab-gatech/ShelfGaussian-CudaGaussianVoxelizer
+(lines 1-96): ``PyCudaGaussianVoxelizer(voxel_size, voxel_range)`` returns
+``(density, grid_feats, stats)``; ``stats`` is a CPU float32 tensor ``[fwd_sec, bwd_sec]``,
+the backward time being filled in when ``.backward()`` runs.  The kernels live in
+libg2v_hip.so (C ABI in include/g2v.h), reached through the ``_C`` module.
+"""
+import torch
+import torch.nn as nn
+
+from . import _C
+from ._C import gaussian_voxelizer_forward, gaussian_voxelizer_backward
+from ._C import CudaFeatsCosinelossForward, CudaFeatsCosinelossBackward
+
+__all__ = ["PyCudaGaussianVoxelizer", "PyCudaFeatsCosineLoss", "_C",
+           "gaussian_voxelizer_forward", "gaussian_voxelizer_backward"]
+
+
+class _CudaGaussianVoxelizeFunction(torch.autograd.Function):
+    """Autograd wrapper (reference CudaGaussianVoxelizer/__init__.py:10-47)."""
+
+    @staticmethod
+    def forward(ctx, means3D, opacity, covariances, voxel_size, voxel_range, features):
+        (density, cov_inv, valid_voxel_lb, valid_voxel_ub, num_valid_voxel, grid_feats, g2t_offsets,
+         g2t_tile_ids, fwd_sec) = gaussian_voxelizer_forward(means3D, opacity, covariances, voxel_size,
+                                                             voxel_range, features)
+        stats = torch.zeros(2, dtype=torch.float32, device="cpu")
+        stats[0] = fwd_sec
+        ctx.save_for_backward(means3D, opacity, voxel_size, voxel_range, cov_inv, valid_voxel_lb,
+                              valid_voxel_ub, num_valid_voxel, g2t_offsets, g2t_tile_ids, density,
+                              grid_feats, features, stats)
+        ctx.mark_non_differentiable(stats)
+        ctx.opacity_shape = opacity.shape
+        ctx.cov_shape = covariances.shape
+        return density, grid_feats, stats
+
+    @staticmethod
+    def backward(ctx, grad_density_output, grad_feats_output, grad_stats):
+        (means32, op32, voxsz32, voxrg32, cov_inv, valid_voxel_lb, valid_voxel_ub, num_valid_voxel,
+         g2t_offsets, g2t_tile_ids, density, grid_feats, features, stats) = ctx.saved_tensors
+        gout32 = grad_density_output.to(torch.float32).contiguous()
+        grad_feats_output = grad_feats_output.to(torch.float32).contiguous()
+        means32 = means32.detach().contiguous()
+        op32 = op32.detach().reshape(-1).contiguous()
+        feats = None if features is None else features.detach().contiguous()
+        grad_means3D, grad_cov, grad_opacity, grad_feats, bwd_sec = gaussian_voxelizer_backward(
+            gout32, grad_feats_output, means32, op32, cov_inv, voxsz32, voxrg32, valid_voxel_lb,
+            valid_voxel_ub, num_valid_voxel, g2t_offsets, g2t_tile_ids, density, grid_feats, feats)
+        stats[1] = bwd_sec
+        # gradients take the shapes of the inputs ((N,) or (N,1) opacity, (N,9) or (N,3,3) cov)
+        grad_opacity = grad_opacity.reshape(ctx.opacity_shape)
+        grad_cov = grad_cov.reshape(ctx.cov_shape)
+        return (grad_means3D, grad_opacity, grad_cov, None, None,
+                grad_feats if features is not None else None)
+
+
+class PyCudaGaussianVoxelizer(nn.Module):
+    """Splats Gaussians (and their features) into a dense voxel grid of 4x4x4 tiles.
+
+    Reference CudaGaussianVoxelizer/__init__.py:69-82.
+    """
+
+    def __init__(self, voxel_size=[0.4, 0.4, 0.4], voxel_range=[-40, -40, -1, 40, 40, 5.4]):
+        super().__init__()
+        self.voxel_size = torch.tensor(voxel_size, dtype=torch.float32, device="cuda")
+        self.voxel_range = torch.tensor(voxel_range, dtype=torch.float32, device="cuda")
+        # host copies, so the forward never reads the device tensors back
+        _C._host_values(self.voxel_size, 3, "voxel_size")
+        _C._host_values(self.voxel_range, 6, "voxel_range")
+
+    def forward(self, means3D, opacity, covariances, features=None):
+        return _CudaGaussianVoxelizeFunction.apply(means3D, opacity, covariances, self.voxel_size,
+                                                   self.voxel_range, features)
+
+
+class PyCudaFeatsCosineLoss(nn.Module):
+    """Present for API compatibility only: the cosine loss (reference src/cuda_feats_loss.cu) is
+    outside the G2V splatting path of this build and raises ``NotImplementedError``."""
+
+    def __init__(self, voxel_size=[0.4, 0.4, 0.4], voxel_range=[-40, -40, -1, 40, 40, 5.4]):
+        super().__init__()
+        self.voxel_size = torch.tensor(voxel_size, dtype=torch.float32, device="cuda")
+        self.voxel_range = torch.tensor(voxel_range, dtype=torch.float32, device="cuda")
+
+    def forward(self, voxel_label, occ_gt_mask_camera, d_grid_feats, pseudo_dino_gt):
+        return CudaFeatsCosinelossForward(voxel_label, occ_gt_mask_camera, d_grid_feats, pseudo_dino_gt)

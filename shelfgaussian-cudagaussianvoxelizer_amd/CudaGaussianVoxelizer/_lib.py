@@ -1,0 +1,68 @@
+"""ctypes binding of libg2v_hip.so, the gfx950 HIP library behind ``_C`` (C ABI: include/g2v.h).
+
+Loading fails loudly: there is no CPU fallback for the G2V path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_NAME = "libg2v_hip.so"
+LIB_PATH = os.path.join(_HERE, LIB_NAME)
+
+G2V_OK = 0
+_ERRORS = {1: "invalid argument", 2: "HIP runtime error", 3: "size limit exceeded"}
+
+# (name, restype, argtypes) of every exported entry point of include/g2v.h
+_vp, _i, _ll, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_size_t
+_f3 = ctypes.POINTER(ctypes.c_float)
+_ip = ctypes.POINTER(ctypes.c_int)
+_llp = ctypes.POINTER(ctypes.c_longlong)
+SIGNATURES = {
+    "g2v_last_error": (ctypes.c_char_p, []),
+    "g2v_abi_version": (_i, []),
+    "g2v_grid_dims": (_i, [_f3, _f3, _ip, _ip]),
+    "g2v_forward_plan_workspace": (_sz, [_i]),
+    "g2v_forward_plan": (_i, [_i, _vp, _vp, _f3, _f3, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _llp, _vp]),
+    "g2v_forward_splat_workspace": (_sz, [_i, _ll, _f3, _f3]),
+    "g2v_forward_splat": (_i, [_i, _i, _vp, _vp, _vp, _f3, _f3, _vp, _vp, _vp, _vp, _ll, _vp, _vp,
+                               _vp, _vp, _sz, _vp]),
+    "g2v_backward_workspace": (_sz, [_i, _i, _ll, _f3, _f3]),
+    "g2v_backward": (_i, [_i, _i, _vp, _vp, _vp, _vp, _vp, _f3, _f3, _vp, _vp, _vp, _vp, _vp, _ll,
+                          _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "g2v_t2g_workspace": (_sz, [_i, _ll, _f3, _f3]),
+    "g2v_build_t2g": (_i, [_i, _f3, _f3, _vp, _vp, _vp, _vp, _ll, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                           _vp, _sz, _vp]),
+}
+
+_lib = None
+
+
+def load():
+    """Load (once) and return the ctypes handle of libg2v_hip.so."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is missing: build the HIP library first "
+            "(python shelfgaussian-cudagaussianvoxelizer_amd/build.py); there is no CPU fallback")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def check(rc: int, what: str):
+    if rc != G2V_OK:
+        msg = load().g2v_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed ({_ERRORS.get(rc, rc)}): {msg}")
+
+
+def floats(values):
+    vals = [float(v) for v in values]
+    return (ctypes.c_float * len(vals))(*vals)

@@ -1,0 +1,315 @@
+// C ABI of libg2v_hip.so (declared in include/g2v.h): argument checks, workspace carving and
+// the launch sequence of each entry point.  Replaces the pybind11 binding and host
+// orchestration of the reference (src/bindings.cpp:7-64, src/cuda_gaussian_voxelizer.cu:1484-2057).
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/g2v.h"
+#include "g2v_internal.h"
+
+using namespace g2v;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* where) {
+    return fail(G2V_ERR_HIP, "%s: %s", where, hipGetErrorString(e));
+}
+
+#define G2V_HIP(call)                                   \
+    do {                                                \
+        hipError_t e_ = (call);                         \
+        if (e_ != hipSuccess) return hip_fail(e_, #call); \
+    } while (0)
+
+// Grid of (voxel_size, voxel_range) in float32, truncated like the reference (.cu:1512-1519).
+int make_grid(const float* vs, const float* vr, Grid& G) {
+    if (!vs || !vr) return fail(G2V_ERR_INVALID, "voxel_size / voxel_range must not be null");
+    for (int a = 0; a < 3; ++a) {
+        const float q = (vr[a + 3] - vr[a]) / vs[a];
+        if (!(q >= 1.0f) || !(q < 2147483648.0f))
+            return fail(G2V_ERR_INVALID, "grid axis %d has %g voxels (range %g..%g, size %g)", a,
+                        (double)q, (double)vr[a], (double)vr[a + 3], (double)vs[a]);
+        G.r0[a] = vr[a];
+        G.r1[a] = vr[a + 3];
+        G.s[a] = vs[a];
+        G.dims[a] = (int)q;
+        G.tiles[a] = (G.dims[a] + kTile - 1) / kTile;
+    }
+    const double cells = (double)G.dims[0] * G.dims[1] * G.dims[2];
+    if (cells >= 2147483647.0) return fail(G2V_ERR_LIMIT, "grid has %.0f voxels (limit 2^31-1)", cells);
+    return G2V_OK;
+}
+
+int num_tiles(const Grid& G) { return G.tiles[0] * G.tiles[1] * G.tiles[2]; }
+
+struct SplatBufs {
+    int* gauss_ids;
+    int* sorted_tiles;
+    int* sorted_gauss;
+    int* tile_offsets;
+    void* sort_ws;
+    size_t bytes;
+};
+
+SplatBufs carve_splat(void* ws, int n, int64_t M, const Grid& G) {
+    (void)n;
+    const int64_t m = M > 0 ? M : 1;
+    const int T = num_tiles(G);
+    Carver c(ws, (size_t)-1);
+    SplatBufs b;
+    b.gauss_ids = c.take<int>(m);
+    b.sorted_tiles = c.take<int>(m);
+    b.sorted_gauss = c.take<int>(m);
+    b.tile_offsets = c.take<int>(T + 1);
+    b.sort_ws = c.take<char>(sort_workspace(M, T));
+    b.bytes = c.off + 256;
+    return b;
+}
+
+// G->T gauss ids, stable sort by tile, tile offsets: the Tile->Gaussian CSR.
+int build_t2g(const Grid& G, int n, const int* lb, const int* ub, const int* g2t_offsets,
+              int* g2t_tile_ids_out, const int* g2t_tile_ids_in, int64_t M, const SplatBufs& b,
+              hipStream_t s) {
+    const int T = num_tiles(G);
+    if (M > 0) {
+        G2V_HIP(launch_fill_g2t(G, n, lb, ub, g2t_offsets, g2t_tile_ids_out, b.gauss_ids, s));
+        const int* keys = g2t_tile_ids_out ? g2t_tile_ids_out : g2t_tile_ids_in;
+        G2V_HIP(radix_sort_pairs(keys, b.gauss_ids, b.sorted_tiles, b.sorted_gauss, M, T, b.sort_ws, s));
+    }
+    G2V_HIP(launch_tile_offsets(b.sorted_tiles, M, T, b.tile_offsets, s));
+    return G2V_OK;
+}
+
+int check_ws(const void* ws, size_t have, size_t need, const char* what) {
+    if (need > have) return fail(G2V_ERR_INVALID, "%s workspace too small: %zu < %zu bytes", what, have, need);
+    if (!ws && need > 0) return fail(G2V_ERR_INVALID, "%s workspace is null", what);
+    return G2V_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* g2v_last_error(void) { return g_err; }
+
+int g2v_abi_version(void) { return 1; }
+
+int g2v_grid_dims(const float voxel_size[3], const float voxel_range[6], int dims[3], int tiles[3]) {
+    Grid G;
+    const int rc = make_grid(voxel_size, voxel_range, G);
+    if (rc != G2V_OK) return rc;
+    for (int a = 0; a < 3; ++a) {
+        if (dims) dims[a] = G.dims[a];
+        if (tiles) tiles[a] = G.tiles[a];
+    }
+    return G2V_OK;
+}
+
+size_t g2v_forward_plan_workspace(int n) {
+    Carver c(nullptr, (size_t)-1);
+    c.take<long long>(1);
+    c.take<char>(scan_workspace(n > 0 ? n : 1));
+    return c.off + 256;
+}
+
+int g2v_forward_plan(int n, const float* means3D, const float* covariances,
+                     const float voxel_size[3], const float voxel_range[6], float* cov_inv,
+                     int* valid_voxel_lb, int* valid_voxel_ub, int* num_voxels_per_gaussian,
+                     int* g2t_offsets, void* workspace, size_t workspace_bytes,
+                     long long* num_pairs, void* stream) {
+    g_err[0] = 0;
+    if (n < 0) return fail(G2V_ERR_INVALID, "n = %d", n);
+    if (!num_pairs || !g2t_offsets) return fail(G2V_ERR_INVALID, "num_pairs / g2t_offsets null");
+    if (n > 0 && (!means3D || !covariances || !cov_inv || !valid_voxel_lb || !valid_voxel_ub ||
+                  !num_voxels_per_gaussian))
+        return fail(G2V_ERR_INVALID, "null input/output pointer");
+    Grid G;
+    int rc = make_grid(voxel_size, voxel_range, G);
+    if (rc != G2V_OK) return rc;
+    rc = check_ws(workspace, workspace_bytes, g2v_forward_plan_workspace(n), "plan");
+    if (rc != G2V_OK) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    Carver c(workspace, workspace_bytes);
+    long long* total = c.take<long long>(1);
+    void* scan_ws = c.take<char>(scan_workspace(n > 0 ? n : 1));
+
+    G2V_HIP(launch_boxes(G, n, means3D, covariances, cov_inv, valid_voxel_lb, valid_voxel_ub,
+                         num_voxels_per_gaussian, g2t_offsets, s));
+    long long M = 0;
+    if (n > 0) {
+        G2V_HIP(scan_i32(g2t_offsets + 1, g2t_offsets + 1, n, true, total, scan_ws, s));
+        G2V_HIP(hipMemcpyAsync(&M, total, sizeof(long long), hipMemcpyDeviceToHost, s));
+    }
+    G2V_HIP(hipStreamSynchronize(s));
+    if (M > 2147483647ll)
+        return fail(G2V_ERR_LIMIT, "%lld Gaussian-tile pairs exceed the int32 CSR (limit 2^31-1)", M);
+    *num_pairs = M;
+    return G2V_OK;
+}
+
+size_t g2v_forward_splat_workspace(int n, long long num_pairs, const float voxel_size[3],
+                                   const float voxel_range[6]) {
+    Grid G;
+    if (make_grid(voxel_size, voxel_range, G) != G2V_OK) return 0;
+    return carve_splat(nullptr, n, num_pairs, G).bytes;
+}
+
+int g2v_forward_splat(int n, int feat_dim, const float* means3D, const float* opacity,
+                      const float* features, const float voxel_size[3], const float voxel_range[6],
+                      const float* cov_inv, const int* valid_voxel_lb, const int* valid_voxel_ub,
+                      const int* g2t_offsets, long long num_pairs, int* g2t_tile_ids,
+                      float* density, float* grid_feats, void* workspace, size_t workspace_bytes,
+                      void* stream) {
+    g_err[0] = 0;
+    if (n < 0 || feat_dim < 0 || num_pairs < 0)
+        return fail(G2V_ERR_INVALID, "n = %d, feat_dim = %d, num_pairs = %lld", n, feat_dim, num_pairs);
+    if (num_pairs > 2147483647ll) return fail(G2V_ERR_LIMIT, "num_pairs = %lld exceeds int32", num_pairs);
+    if (!density) return fail(G2V_ERR_INVALID, "density is null");
+    if (feat_dim > 0 && (!grid_feats || (n > 0 && !features)))
+        return fail(G2V_ERR_INVALID, "feat_dim = %d needs features and grid_feats", feat_dim);
+    if (num_pairs > 0 && (!g2t_tile_ids || !g2t_offsets || !means3D || !opacity || !cov_inv ||
+                          !valid_voxel_lb || !valid_voxel_ub))
+        return fail(G2V_ERR_INVALID, "null input/output pointer");
+    Grid G;
+    int rc = make_grid(voxel_size, voxel_range, G);
+    if (rc != G2V_OK) return rc;
+    if ((double)G.dims[0] * G.dims[1] * G.dims[2] * (double)feat_dim >= 9.2e18)
+        return fail(G2V_ERR_LIMIT, "grid_feats too large");
+    const SplatBufs need = carve_splat(nullptr, n, num_pairs, G);
+    rc = check_ws(workspace, workspace_bytes, need.bytes, "splat");
+    if (rc != G2V_OK) return rc;
+    const SplatBufs b = carve_splat(workspace, n, num_pairs, G);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    rc = build_t2g(G, n, valid_voxel_lb, valid_voxel_ub, g2t_offsets, g2t_tile_ids, nullptr,
+                   num_pairs, b, s);
+    if (rc != G2V_OK) return rc;
+    if (feat_dim > 0)
+        G2V_HIP(launch_forward_feats(G, feat_dim, means3D, opacity, cov_inv, valid_voxel_lb,
+                                     valid_voxel_ub, b.tile_offsets, b.sorted_gauss, (int)num_pairs,
+                                     features, density, grid_feats, s));
+    else
+        G2V_HIP(launch_forward_density(G, means3D, opacity, cov_inv, valid_voxel_lb, valid_voxel_ub,
+                                       b.tile_offsets, b.sorted_gauss, (int)num_pairs, density, s));
+    return G2V_OK;
+}
+
+size_t g2v_backward_workspace(int n, int feat_dim, long long num_pairs, const float voxel_size[3],
+                              const float voxel_range[6]) {
+    Grid G;
+    if (make_grid(voxel_size, voxel_range, G) != G2V_OK) return 0;
+    if (feat_dim <= 0) return 256;
+    Carver c(nullptr, (size_t)-1);
+    c.take<char>(carve_splat(nullptr, n, num_pairs, G).bytes);
+    c.take<char>(backward_feats_workspace(G, n, feat_dim, num_pairs));
+    return c.off + 256;
+}
+
+int g2v_backward(int n, int feat_dim, const float* grad_density, const float* grad_feats,
+                 const float* means3D, const float* opacity, const float* cov_inv,
+                 const float voxel_size[3], const float voxel_range[6], const int* valid_voxel_lb,
+                 const int* valid_voxel_ub, const int* num_voxels_per_gaussian,
+                 const int* g2t_offsets, const int* g2t_tile_ids, long long num_pairs,
+                 const float* density, const float* grid_feats, const float* features,
+                 float* grad_means, float* grad_cov, float* grad_opacity, float* grad_features,
+                 void* workspace, size_t workspace_bytes, void* stream) {
+    g_err[0] = 0;
+    (void)num_voxels_per_gaussian;
+    if (n < 0 || feat_dim < 0 || num_pairs < 0)
+        return fail(G2V_ERR_INVALID, "n = %d, feat_dim = %d, num_pairs = %lld", n, feat_dim, num_pairs);
+    if (num_pairs > 2147483647ll) return fail(G2V_ERR_LIMIT, "num_pairs = %lld exceeds int32", num_pairs);
+    if (n == 0) return G2V_OK;
+    if (!grad_density || !means3D || !opacity || !cov_inv || !valid_voxel_lb || !valid_voxel_ub ||
+        !grad_means || !grad_cov || !grad_opacity)
+        return fail(G2V_ERR_INVALID, "null input/output pointer");
+    if (feat_dim > 0 && (!grad_feats || !grid_feats || !features || !grad_features || !density ||
+                         !g2t_offsets || (num_pairs > 0 && !g2t_tile_ids)))
+        return fail(G2V_ERR_INVALID, "feat_dim = %d needs the feature tensors, density and the CSR", feat_dim);
+    Grid G;
+    int rc = make_grid(voxel_size, voxel_range, G);
+    if (rc != G2V_OK) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (feat_dim == 0) {
+        G2V_HIP(launch_backward_density(G, n, grad_density, means3D, opacity, cov_inv, valid_voxel_lb,
+                                        valid_voxel_ub, grad_means, grad_cov, grad_opacity, s));
+        return G2V_OK;
+    }
+    rc = check_ws(workspace, workspace_bytes,
+                  g2v_backward_workspace(n, feat_dim, num_pairs, voxel_size, voxel_range), "backward");
+    if (rc != G2V_OK) return rc;
+    Carver c(workspace, workspace_bytes);
+    void* splat_ws = c.take<char>(carve_splat(nullptr, n, num_pairs, G).bytes);
+    void* feats_ws = c.take<char>(backward_feats_workspace(G, n, feat_dim, num_pairs));
+    const SplatBufs b = carve_splat(splat_ws, n, num_pairs, G);
+    rc = build_t2g(G, n, valid_voxel_lb, valid_voxel_ub, g2t_offsets, nullptr, g2t_tile_ids,
+                   num_pairs, b, s);
+    if (rc != G2V_OK) return rc;
+    G2V_HIP(launch_backward_feats(G, n, feat_dim, grad_density, grad_feats, means3D, opacity, cov_inv,
+                                  valid_voxel_lb, valid_voxel_ub, g2t_offsets, num_pairs,
+                                  b.tile_offsets, b.sorted_gauss, density, grid_feats, features,
+                                  grad_means, grad_cov, grad_opacity, grad_features, feats_ws, s));
+    return G2V_OK;
+}
+
+size_t g2v_t2g_workspace(int n, long long num_pairs, const float voxel_size[3],
+                         const float voxel_range[6]) {
+    Grid G;
+    if (make_grid(voxel_size, voxel_range, G) != G2V_OK) return 0;
+    const int T = num_tiles(G);
+    Carver c(nullptr, (size_t)-1);
+    c.take<char>(carve_splat(nullptr, n, num_pairs, G).bytes);
+    c.take<int>(T > 0 ? T : 1);
+    c.take<char>(scan_workspace(T));
+    return c.off + 256;
+}
+
+int g2v_build_t2g(int n, const float voxel_size[3], const float voxel_range[6],
+                  const int* valid_voxel_lb, const int* valid_voxel_ub, const int* g2t_offsets,
+                  const int* g2t_tile_ids, long long num_pairs, int* sorted_tiles,
+                  int* sorted_gauss, int* tile_offsets, int* unique_tiles, int* counts,
+                  int* runs_offsets, int* num_runs, void* workspace, size_t workspace_bytes,
+                  void* stream) {
+    g_err[0] = 0;
+    if (n < 0 || num_pairs < 0) return fail(G2V_ERR_INVALID, "n = %d, num_pairs = %lld", n, num_pairs);
+    if (!tile_offsets || !unique_tiles || !counts || !runs_offsets || !num_runs ||
+        (num_pairs > 0 && (!sorted_tiles || !sorted_gauss || !g2t_tile_ids || !g2t_offsets ||
+                           !valid_voxel_lb || !valid_voxel_ub)))
+        return fail(G2V_ERR_INVALID, "null pointer");
+    Grid G;
+    int rc = make_grid(voxel_size, voxel_range, G);
+    if (rc != G2V_OK) return rc;
+    rc = check_ws(workspace, workspace_bytes, g2v_t2g_workspace(n, num_pairs, voxel_size, voxel_range), "t2g");
+    if (rc != G2V_OK) return rc;
+    const int T = num_tiles(G);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    Carver c(workspace, workspace_bytes);
+    void* splat_ws = c.take<char>(carve_splat(nullptr, n, num_pairs, G).bytes);
+    void* rle_ws = c.take<char>(0);
+    const SplatBufs b = carve_splat(splat_ws, n, num_pairs, G);
+    rc = build_t2g(G, n, valid_voxel_lb, valid_voxel_ub, g2t_offsets, nullptr, g2t_tile_ids,
+                   num_pairs, b, s);
+    if (rc != G2V_OK) return rc;
+    if (num_pairs > 0) {
+        G2V_HIP(hipMemcpyAsync(sorted_tiles, b.sorted_tiles, num_pairs * sizeof(int),
+                               hipMemcpyDeviceToDevice, s));
+        G2V_HIP(hipMemcpyAsync(sorted_gauss, b.sorted_gauss, num_pairs * sizeof(int),
+                               hipMemcpyDeviceToDevice, s));
+    }
+    G2V_HIP(hipMemcpyAsync(tile_offsets, b.tile_offsets, (T + 1) * sizeof(int),
+                           hipMemcpyDeviceToDevice, s));
+    G2V_HIP(launch_rle(b.tile_offsets, T, unique_tiles, counts, runs_offsets, num_runs, rle_ws, s));
+    return G2V_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,444 @@
+// Gaussian->Tile and Tile->Gaussian CSR build for gfx950.
+//
+//   k_boxes          per-Gaussian 3-sigma box, tile box, inverse covariance
+//                    (reference src/cuda_gaussian_voxelizer.cu:348-536, :201-220)
+//   scan_i32         device-wide scan (replaces cub::DeviceScan, reference .cu:1605-1615, :1758-1772)
+//   k_fill_g2t       row-major G->T rows (reference .cu:228-286)
+//   radix_sort_pairs stable LSD radix sort over only ceil(log2 T) key bits
+//                    (replaces cub::DeviceRadixSort::SortPairs over 32 bits, reference .cu:1673-1691)
+//   k_tile_offsets   run boundaries of the sorted tile ids for every tile, empty ones included
+//                    (replaces cub::DeviceRunLengthEncode + scan, reference .cu:1708-1772)
+//   k_rle_*          unique tiles / run lengths / run offsets / number of runs
+#include "g2v_internal.h"
+
+namespace g2v {
+
+// ------------------------------------------------------------------------------------------
+// Boxes
+// ------------------------------------------------------------------------------------------
+
+// float -> int32 the way the hardware converts (saturating, NaN -> 0), written out so the
+// compiler cannot treat an out-of-range conversion as undefined.
+__device__ __forceinline__ int cvt_sat(float f) {
+    if (!(f == f)) return 0;
+    if (f >= 2147483648.0f) return 2147483647;
+    if (f < -2147483648.0f) return (int)0x80000000;
+    return (int)f;
+}
+
+__global__ void __launch_bounds__(256) k_boxes(Grid G, int n, const float* __restrict__ means,
+                                               const float* __restrict__ cov,
+                                               float* __restrict__ cov_inv, int* __restrict__ lb,
+                                               int* __restrict__ ub, int* __restrict__ nvox,
+                                               int* __restrict__ g2t_offsets) {
+#pragma clang fp contract(off)
+    const int g = blockIdx.x * 256 + threadIdx.x;
+    if (g == 0) g2t_offsets[0] = 0;
+    if (g >= n) return;
+    int lo[3], hi[3];
+    bool empty = false;
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        const float sig = sqrtf(cov[g * 9 + 4 * a]);
+        const float ts = 3.0f * sig;
+        const float m = means[g * 3 + a];
+        float lower = m - ts;
+        float upper = m + ts;
+        lower = fmaxf(lower, G.r0[a]);
+        upper = fminf(upper, G.r1[a]);
+        const float ql = (lower - G.r0[a]) / G.s[a];
+        const float qh = (upper - G.r0[a]) / G.s[a];
+        lo[a] = max(cvt_sat(floorf(ql)), 0);
+        hi[a] = min(cvt_sat(floorf(qh)), G.dims[a] - 1);
+        empty |= lo[a] > hi[a];
+    }
+    if (empty) {
+#pragma unroll
+        for (int a = 0; a < 3; ++a) { lb[g * 3 + a] = 0; ub[g * 3 + a] = -1; }
+        nvox[g] = 0;
+        g2t_offsets[g + 1] = 0;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) cov_inv[g * 9 + k] = 0.0f;
+        return;
+    }
+    int nv = 1, nt = 1;
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        lb[g * 3 + a] = lo[a];
+        ub[g * 3 + a] = hi[a];
+        nv *= hi[a] - lo[a] + 1;
+        const int tl = max(lo[a] / kTile, 0);
+        const int th = min(hi[a] / kTile, G.tiles[a] - 1);
+        nt *= th - tl + 1;
+    }
+    nvox[g] = nv;
+    g2t_offsets[g + 1] = nt;
+
+    float A[9];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) A[k] = cov[g * 9 + k];
+    float det = A[0] * (A[4] * A[8] - A[5] * A[7]) - A[1] * (A[3] * A[8] - A[5] * A[6]) +
+                A[2] * (A[3] * A[7] - A[4] * A[6]);
+    if (fabsf(det) < 1e-6f) det = 1e-6f;
+    const float inv_det = 1.0f / det;
+    float* o = cov_inv + g * 9;
+    o[0] = (A[4] * A[8] - A[5] * A[7]) * inv_det;
+    o[1] = -(A[1] * A[8] - A[2] * A[7]) * inv_det;
+    o[2] = (A[1] * A[5] - A[2] * A[4]) * inv_det;
+    o[3] = -(A[3] * A[8] - A[5] * A[6]) * inv_det;
+    o[4] = (A[0] * A[8] - A[2] * A[6]) * inv_det;
+    o[5] = -(A[0] * A[5] - A[2] * A[3]) * inv_det;
+    o[6] = (A[3] * A[7] - A[4] * A[6]) * inv_det;
+    o[7] = -(A[0] * A[7] - A[1] * A[6]) * inv_det;
+    o[8] = (A[0] * A[4] - A[1] * A[3]) * inv_det;
+}
+
+hipError_t launch_boxes(const Grid& G, int n, const float* means, const float* cov, float* cov_inv,
+                        int* lb, int* ub, int* nvox, int* g2t_offsets, hipStream_t s) {
+    const int blocks = (int)ceil_div(n > 0 ? n : 1, 256);
+    hipLaunchKernelGGL(k_boxes, dim3(blocks), dim3(256), 0, s, G, n, means, cov, cov_inv, lb, ub,
+                       nvox, g2t_offsets);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------------
+// Device-wide scan: per-tile reduce -> scan of tile totals -> per-tile scan with carry-in.
+// ------------------------------------------------------------------------------------------
+
+// Inclusive scan of one value per thread over the block (256 threads = 4 waves).
+__device__ __forceinline__ long long block_incl_scan(long long v, long long* sh /*[4]*/, long long& total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const long long t = __shfl_up(v, off, 64);
+        if (lane >= off) v += t;
+    }
+    if (lane == 63) sh[wave] = v;
+    __syncthreads();
+    long long carry = 0;
+    for (int w = 0; w < wave; ++w) carry += sh[w];
+    total = sh[0] + sh[1] + sh[2] + sh[3];
+    __syncthreads();
+    return v + carry;
+}
+
+__global__ void __launch_bounds__(kScanThreads) k_scan_reduce(const int* __restrict__ in, int64_t n,
+                                                              long long* __restrict__ partials) {
+    __shared__ long long sh[4];
+    const int64_t base = (int64_t)blockIdx.x * kScanTile;
+    long long sum = 0;
+#pragma unroll
+    for (int r = 0; r < kScanItems; ++r) {
+        const int64_t i = base + (int64_t)r * kScanThreads + threadIdx.x;
+        if (i < n) sum += in[i];
+    }
+    long long total;
+    block_incl_scan(sum, sh, total);
+    if (threadIdx.x == 0) partials[blockIdx.x] = total;
+}
+
+// Exclusive scan of the per-tile totals by one workgroup, looping over chunks with a carry.
+__global__ void __launch_bounds__(kScanThreads) k_scan_partials(long long* __restrict__ partials,
+                                                                int64_t nb,
+                                                                long long* __restrict__ total_dev) {
+    __shared__ long long sh[4];
+    long long carry = 0;
+    for (int64_t base = 0; base < nb; base += kScanThreads) {
+        const int64_t i = base + threadIdx.x;
+        const long long v = i < nb ? partials[i] : 0;
+        long long total;
+        const long long inc = block_incl_scan(v, sh, total);
+        if (i < nb) partials[i] = carry + inc - v;
+        carry += total;
+    }
+    if (threadIdx.x == 0 && total_dev) *total_dev = carry;
+}
+
+__global__ void __launch_bounds__(kScanThreads) k_scan_apply(const int* in, int* out, int64_t n,
+                                                             const long long* __restrict__ partials,
+                                                             int inclusive) {
+    __shared__ long long sh[4];
+    const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
+    int v[kScanItems];
+    long long local = 0;
+#pragma unroll
+    for (int r = 0; r < kScanItems; ++r) {
+        const int64_t i = base + r;
+        v[r] = i < n ? in[i] : 0;
+        local += v[r];
+    }
+    long long total;
+    const long long inc = block_incl_scan(local, sh, total);
+    long long run = partials[blockIdx.x] + inc - local;
+#pragma unroll
+    for (int r = 0; r < kScanItems; ++r) {
+        const int64_t i = base + r;
+        const long long nxt = run + v[r];
+        if (i < n) out[i] = (int)(inclusive ? nxt : run);
+        run = nxt;
+    }
+}
+
+size_t scan_workspace(int64_t n) {
+    return (size_t)(ceil_div(n > 0 ? n : 1, kScanTile) + 1) * sizeof(long long) + 256;
+}
+
+hipError_t scan_i32(const int* in, int* out, int64_t n, bool inclusive, long long* total_dev,
+                    void* ws, hipStream_t s) {
+    const int64_t nb = ceil_div(n > 0 ? n : 1, kScanTile);
+    long long* partials = static_cast<long long*>(ws);
+    hipLaunchKernelGGL(k_scan_reduce, dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, n, partials);
+    hipLaunchKernelGGL(k_scan_partials, dim3(1), dim3(kScanThreads), 0, s, partials, nb, total_dev);
+    hipLaunchKernelGGL(k_scan_apply, dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, out, n,
+                       (const long long*)partials, inclusive ? 1 : 0);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------------
+// G->T fill: one wave per Gaussian enumerates its tile box row-major (x slowest, z fastest).
+// tile_ids may be null (only the Gaussian id of every pair is regenerated).
+// ------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) k_fill_g2t(Grid G, int n, const int* __restrict__ lb,
+                                                  const int* __restrict__ ub,
+                                                  const int* __restrict__ g2t_offsets,
+                                                  int* __restrict__ tile_ids,
+                                                  int* __restrict__ gauss_ids) {
+    const int lane = threadIdx.x & 63;
+    const int g = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (g >= n) return;
+    const int base = g2t_offsets[g];
+    const int cnt = g2t_offsets[g + 1] - base;
+    if (cnt <= 0) return;
+    const int tx0 = lb[g * 3] / kTile, ty0 = lb[g * 3 + 1] / kTile, tz0 = lb[g * 3 + 2] / kTile;
+    const int dy = ub[g * 3 + 1] / kTile - ty0 + 1;
+    const int dz = ub[g * 3 + 2] / kTile - tz0 + 1;
+    const int dyz = dy * dz;
+    for (int i = lane; i < cnt; i += 64) {
+        const int lx = i / dyz, r = i - lx * dyz;
+        const int ly = r / dz, lz = r - ly * dz;
+        if (tile_ids) tile_ids[base + i] = ((tx0 + lx) * G.tiles[1] + (ty0 + ly)) * G.tiles[2] + (tz0 + lz);
+        gauss_ids[base + i] = g;
+    }
+}
+
+hipError_t launch_fill_g2t(const Grid& G, int n, const int* lb, const int* ub,
+                           const int* g2t_offsets, int* tile_ids, int* gauss_ids, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_fill_g2t, dim3((unsigned)ceil_div(n, 4)), dim3(256), 0, s, G, n, lb, ub,
+                       g2t_offsets, tile_ids, gauss_ids);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------------
+// Stable LSD radix sort, digits of <= 8 bits, only ceil(log2 T) key bits.
+//   per pass: k_radix_hist (digit counts per 4096-key block, digit-major) -> exclusive scan
+//             -> k_radix_scatter (stable rank: ballot match inside a wave, LDS across waves)
+// ------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(kSortThreads) k_radix_hist(const int* __restrict__ keys, int64_t M,
+                                                             int shift, int dbits, int nblk,
+                                                             int* __restrict__ ghist) {
+    __shared__ int h[256];
+    const int radix = 1 << dbits;
+    for (int d = threadIdx.x; d < radix; d += kSortThreads) h[d] = 0;
+    __syncthreads();
+    const int64_t base = (int64_t)blockIdx.x * kSortTile;
+#pragma unroll 4
+    for (int r = 0; r < kSortRounds; ++r) {
+        const int64_t i = base + (int64_t)r * kSortThreads + threadIdx.x;
+        if (i < M) atomicAdd(&h[(keys[i] >> shift) & (radix - 1)], 1);
+    }
+    __syncthreads();
+    for (int d = threadIdx.x; d < radix; d += kSortThreads) ghist[(int64_t)d * nblk + blockIdx.x] = h[d];
+}
+
+__global__ void __launch_bounds__(kSortThreads) k_radix_scatter(
+    const int* __restrict__ keys_in, const int* __restrict__ vals_in, int* __restrict__ keys_out,
+    int* __restrict__ vals_out, int64_t M, int shift, int dbits, int nblk,
+    const int* __restrict__ gscan) {
+    __shared__ int wave_cnt[4][256];
+    __shared__ int running[256];
+    const int radix = 1 << dbits;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int d = threadIdx.x; d < radix; d += kSortThreads) {
+        running[d] = gscan[(int64_t)d * nblk + blockIdx.x];
+        wave_cnt[0][d] = wave_cnt[1][d] = wave_cnt[2][d] = wave_cnt[3][d] = 0;
+    }
+    __syncthreads();
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    const int64_t base = (int64_t)blockIdx.x * kSortTile;
+    for (int r = 0; r < kSortRounds; ++r) {
+        const int64_t rbase = base + (int64_t)r * kSortThreads;
+        if (rbase >= M) break;  // uniform across the block
+        const int64_t i = rbase + threadIdx.x;
+        const bool valid = i < M;
+        const int k = valid ? keys_in[i] : 0;
+        const int v = valid ? vals_in[i] : 0;
+        const int d = (k >> shift) & (radix - 1);
+        uint64_t peers = __ballot(valid);
+        for (int b = 0; b < dbits; ++b) {
+            const bool bit = (d >> b) & 1;
+            const uint64_t m = __ballot(valid && bit);
+            peers &= bit ? m : ~m;
+        }
+        const int rank = __popcll(peers & lt_mask);
+        if (valid && rank == 0) wave_cnt[wave][d] = __popcll(peers);
+        __syncthreads();
+        if (valid) {
+            int pos = running[d] + rank;
+            for (int w = 0; w < wave; ++w) pos += wave_cnt[w][d];
+            keys_out[pos] = k;
+            vals_out[pos] = v;
+        }
+        __syncthreads();
+        for (int dd = threadIdx.x; dd < radix; dd += kSortThreads) {
+            running[dd] += wave_cnt[0][dd] + wave_cnt[1][dd] + wave_cnt[2][dd] + wave_cnt[3][dd];
+            wave_cnt[0][dd] = wave_cnt[1][dd] = wave_cnt[2][dd] = wave_cnt[3][dd] = 0;
+        }
+        __syncthreads();
+    }
+}
+
+int sort_key_bits(int num_tiles) {
+    int bits = 0;
+    while (bits < 31 && (1ll << bits) < (long long)num_tiles) ++bits;
+    return bits;
+}
+
+static void sort_plan(int num_tiles, int& passes, int& dbits) {
+    const int bits = sort_key_bits(num_tiles);
+    passes = (bits + 7) / 8;
+    dbits = passes ? (bits + passes - 1) / passes : 0;
+}
+
+// Carves the sort workspace; with a null base it only measures it.
+struct SortBufs {
+    int* pk;
+    int* pv;
+    int* hist;
+    void* scan_ws;
+    size_t bytes;
+};
+
+static SortBufs carve_sort(void* ws, int64_t M, int num_tiles) {
+    int passes, dbits;
+    sort_plan(num_tiles, passes, dbits);
+    const int64_t m = M > 0 ? M : 1;
+    const int64_t nblk = ceil_div(m, kSortTile);
+    const int64_t hist_n = (int64_t)(1 << dbits) * nblk;
+    Carver c(ws, (size_t)-1);
+    SortBufs b;
+    b.pk = c.take<int>(m);
+    b.pv = c.take<int>(m);
+    b.hist = c.take<int>(hist_n);
+    b.scan_ws = c.take<char>(scan_workspace(hist_n));
+    b.bytes = c.off + 256;
+    return b;
+}
+
+size_t sort_workspace(int64_t M, int num_tiles) { return carve_sort(nullptr, M, num_tiles).bytes; }
+
+hipError_t radix_sort_pairs(const int* keys_in, const int* vals_in, int* keys_out, int* vals_out,
+                            int64_t M, int num_tiles, void* ws, hipStream_t s) {
+    if (M <= 0) return hipSuccess;
+    int passes, dbits;
+    sort_plan(num_tiles, passes, dbits);
+    if (passes == 0) {  // single tile: already sorted
+        hipError_t e = hipMemcpyAsync(keys_out, keys_in, M * sizeof(int), hipMemcpyDeviceToDevice, s);
+        if (e != hipSuccess) return e;
+        return hipMemcpyAsync(vals_out, vals_in, M * sizeof(int), hipMemcpyDeviceToDevice, s);
+    }
+    const int nblk = (int)ceil_div(M, kSortTile);
+    const int64_t hist_n = (int64_t)(1 << dbits) * nblk;
+    const SortBufs b = carve_sort(ws, M, num_tiles);
+    int* pk = b.pk;
+    int* pv = b.pv;
+    int* hist = b.hist;
+    void* scan_ws = b.scan_ws;
+    const int* src_k = keys_in;
+    const int* src_v = vals_in;
+    for (int p = 0; p < passes; ++p) {
+        // the last pass writes the caller's output; earlier passes alternate so that holds
+        const bool to_out = ((passes - 1 - p) % 2) == 0;
+        int* dk = to_out ? keys_out : pk;
+        int* dv = to_out ? vals_out : pv;
+        const int shift = p * dbits;
+        hipLaunchKernelGGL(k_radix_hist, dim3(nblk), dim3(kSortThreads), 0, s, src_k, M, shift, dbits,
+                           nblk, hist);
+        hipError_t e = scan_i32(hist, hist, hist_n, false, nullptr, scan_ws, s);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(k_radix_scatter, dim3(nblk), dim3(kSortThreads), 0, s, src_k, src_v, dk, dv,
+                           M, shift, dbits, nblk, (const int*)hist);
+        src_k = dk;
+        src_v = dv;
+    }
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------------
+// Tile offsets for every tile from the sorted keys: toff[t] = first sorted index with key >= t.
+// ------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) k_tile_offsets(const int* __restrict__ keys, int64_t M, int T,
+                                                      int* __restrict__ toff) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i > M) return;
+    // keys are clamped to [0, T-1] so that a malformed CSR cannot write outside toff
+    if (i < M) {
+        const int k = min(max(keys[i], 0), T - 1);
+        const int prev = (i == 0) ? -1 : min(max(keys[i - 1], 0), T - 1);
+        for (int t = prev + 1; t <= k; ++t) toff[t] = (int)i;
+    } else {
+        const int last = (M == 0) ? -1 : min(max(keys[M - 1], 0), T - 1);
+        for (int t = last + 1; t <= T; ++t) toff[t] = (int)M;
+    }
+}
+
+hipError_t launch_tile_offsets(const int* sorted_keys, int64_t M, int T, int* tile_offsets,
+                               hipStream_t s) {
+    hipLaunchKernelGGL(k_tile_offsets, dim3((unsigned)ceil_div(M + 1, 256)), dim3(256), 0, s,
+                       sorted_keys, M, T, tile_offsets);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------------
+// Run-length encoding of the sorted tile ids (unique tiles, run lengths, run offsets, count).
+// ------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) k_rle_flags(const int* __restrict__ toff, int T,
+                                                   int* __restrict__ flags) {
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    if (t < T) flags[t] = toff[t + 1] > toff[t] ? 1 : 0;
+}
+
+__global__ void __launch_bounds__(256) k_rle_write(const int* __restrict__ toff, int T,
+                                                   const int* __restrict__ pos,
+                                                   int* __restrict__ unique_tiles,
+                                                   int* __restrict__ counts,
+                                                   int* __restrict__ runs_offsets,
+                                                   int* __restrict__ num_runs) {
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    if (t < T && toff[t + 1] > toff[t]) {
+        unique_tiles[pos[t]] = t;
+        counts[pos[t]] = toff[t + 1] - toff[t];
+        runs_offsets[pos[t]] = toff[t];
+    }
+    if (t == T) {
+        const int U = T > 0 ? pos[T - 1] + (toff[T] > toff[T - 1] ? 1 : 0) : 0;
+        runs_offsets[U] = toff[T];
+        *num_runs = U;
+    }
+}
+
+hipError_t launch_rle(const int* tile_offsets, int T, int* unique_tiles, int* counts,
+                      int* runs_offsets, int* num_runs, void* ws, hipStream_t s) {
+    Carver c(ws, (size_t)-1);
+    int* flags = c.take<int>(T > 0 ? T : 1);
+    void* scan_ws = c.take<char>(scan_workspace(T));
+    const int blocks = (int)ceil_div(T + 1, 256);
+    hipLaunchKernelGGL(k_rle_flags, dim3(blocks), dim3(256), 0, s, tile_offsets, T, flags);
+    hipError_t e = scan_i32(flags, flags, T, false, nullptr, scan_ws, s);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_rle_write, dim3(blocks), dim3(256), 0, s, tile_offsets, T, (const int*)flags,
+                       unique_tiles, counts, runs_offsets, num_runs);
+    return hipGetLastError();
+}
+
+}  // namespace g2v

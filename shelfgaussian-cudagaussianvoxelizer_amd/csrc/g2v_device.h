@@ -1,0 +1,133 @@
+// Device-side helpers shared by the G2V kernels (gfx950 / CDNA4, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace g2v {
+
+constexpr int kTile = 4;                 // 4x4x4 voxel tiles (reference include/utils.cuh:50-52)
+constexpr int kVoxPerTile = 64;          // one voxel per lane of a wave64
+constexpr float kEps = 1e-6f;            // density clamp (reference include/utils.cuh:80)
+constexpr int kWave = 64;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Grid geometry passed by value to every kernel.
+struct Grid {
+    float r0[3];      // range lower corner
+    float r1[3];      // range upper corner
+    float s[3];       // voxel size
+    int dims[3];      // X, Y, Z
+    int tiles[3];     // Tx, Ty, Tz
+};
+
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Voxel (x, y, z) of in-tile voxel index lv (x slowest, z fastest; reference .cu:43-55).
+__device__ __forceinline__ void tile_voxel(const Grid& G, int tile, int lv, int& x, int& y, int& z) {
+    const int tyz = G.tiles[1] * G.tiles[2];
+    const int tx = tile / tyz;
+    const int rem = tile - tx * tyz;
+    const int ty = rem / G.tiles[2];
+    const int tz = rem - ty * G.tiles[2];
+    x = tx * kTile + (lv >> 4);
+    y = ty * kTile + ((lv >> 2) & 3);
+    z = tz * kTile + (lv & 3);
+}
+
+__device__ __forceinline__ bool in_grid(const Grid& G, int x, int y, int z) {
+    return x < G.dims[0] && y < G.dims[1] && z < G.dims[2];
+}
+
+__device__ __forceinline__ int64_t voxel_index(const Grid& G, int x, int y, int z) {
+    return ((int64_t)x * G.dims[1] + y) * G.dims[2] + z;
+}
+
+// Gaussian parameters used by the splat: mean, inverse covariance (row-major), opacity, box.
+struct GaussParams {
+    float mu[3];
+    float A[9];
+    float o;
+    int lb[3], ub[3];
+};
+
+__device__ __forceinline__ void load_params(GaussParams& p, int g, const float* __restrict__ means,
+                                            const float* __restrict__ cov_inv,
+                                            const float* __restrict__ opacity,
+                                            const int* __restrict__ lb, const int* __restrict__ ub) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k) p.mu[k] = means[g * 3 + k];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) p.A[k] = cov_inv[g * 9 + k];
+    p.o = opacity[g];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) { p.lb[k] = lb[g * 3 + k]; p.ub[k] = ub[g * 3 + k]; }
+}
+
+__device__ __forceinline__ bool in_box(const GaussParams& p, int x, int y, int z) {
+    return !(x < p.lb[0] || x > p.ub[0] || y < p.lb[1] || y > p.ub[1] || z < p.lb[2] || z > p.ub[2]);
+}
+
+// e = exp(-0.5 dx^T A dx), q = A dx, dx = centre - mu  (reference .cu:1239-1245)
+__device__ __forceinline__ float eval_gauss(const GaussParams& p, float cx, float cy, float cz,
+                                            float& qx, float& qy, float& qz) {
+    const float d0 = cx - p.mu[0], d1 = cy - p.mu[1], d2 = cz - p.mu[2];
+    qx = p.A[0] * d0 + p.A[1] * d1 + p.A[2] * d2;
+    qy = p.A[3] * d0 + p.A[4] * d1 + p.A[5] * d2;
+    qz = p.A[6] * d0 + p.A[7] * d1 + p.A[8] * d2;
+    const float m = d0 * qx + d1 * qy + d2 * qz;
+    return __expf(-0.5f * m);
+}
+
+__device__ __forceinline__ float centre(const Grid& G, int a, int i) {
+    return fmaf((float)i + 0.5f, G.s[a], G.r0[a]);
+}
+
+// Split x into bf16 hi + bf16 lo with x ~= hi + lo (relative residual about 2^-17).
+__device__ __forceinline__ void split_bf16(float x, __bf16& hi, __bf16& lo) {
+    hi = (__bf16)x;
+    lo = (__bf16)(x - (float)hi);
+}
+
+__device__ __forceinline__ void split8(const float (&v)[8], bf16x8& hi, bf16x8& lo) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        __bf16 h = (__bf16)v[i];
+        hi[i] = h;
+        lo[i] = (__bf16)(v[i] - (float)h);
+    }
+}
+
+// acc += (a_hi + a_lo) (b_hi + b_lo) without the lo*lo term: three bf16 MFMAs, fp32 accumulate.
+__device__ __forceinline__ f32x16 mfma3_32x32x16(const bf16x8& ah, const bf16x8& al, const bf16x8& bh,
+                                                 const bf16x8& bl, f32x16 acc) {
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh, acc, 0, 0, 0);
+    return acc;
+}
+
+// Wave64 sum (every lane gets the total).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Load 8 consecutive floats p[0..7] where only the first `valid` (0..8) are in bounds; the
+// rest read as 0.  `vec_ok` says p is 16-byte aligned so two dwordx4 loads can be used.
+__device__ __forceinline__ void load8(const float* __restrict__ p, int valid, bool vec_ok, float (&v)[8]) {
+    if (valid >= 8 && vec_ok) {
+        const float4 a = *reinterpret_cast<const float4*>(p);
+        const float4 b = *reinterpret_cast<const float4*>(p + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = (i < valid) ? p[i] : 0.0f;
+    }
+}
+
+}  // namespace g2v

@@ -1,0 +1,92 @@
+// Host-side declarations shared by the G2V translation units (not part of the C-ABI).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "g2v_device.h"
+
+namespace g2v {
+
+// ---- workspace carving ------------------------------------------------------------------
+struct Carver {
+    char* base;
+    size_t off = 0;
+    size_t cap;
+    Carver(void* p, size_t c) : base(static_cast<char*>(p)), cap(c) {}
+    template <typename T>
+    T* take(size_t count) {
+        off = (off + 255) & ~size_t(255);
+        T* p = reinterpret_cast<T*>(base ? base + off : nullptr);
+        off += count * sizeof(T);
+        return p;
+    }
+    bool fits() const { return off <= cap; }
+};
+
+// ---- CSR build (g2v_csr.hip) ------------------------------------------------------------
+constexpr int kScanThreads = 256;
+constexpr int kScanItems = 16;
+constexpr int kScanTile = kScanThreads * kScanItems;
+constexpr int kSortThreads = 256;
+constexpr int kSortRounds = 16;
+constexpr int kSortTile = kSortThreads * kSortRounds;
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+size_t scan_workspace(int64_t n);
+// In-place or out-of-place scan of n int32 values (inclusive or exclusive); the int64 total
+// is written to *total_dev (device pointer) when it is not null.
+hipError_t scan_i32(const int* in, int* out, int64_t n, bool inclusive, long long* total_dev,
+                    void* ws, hipStream_t s);
+
+hipError_t launch_boxes(const Grid& G, int n, const float* means, const float* cov, float* cov_inv,
+                        int* lb, int* ub, int* nvox, int* g2t_offsets, hipStream_t s);
+hipError_t launch_fill_g2t(const Grid& G, int n, const int* lb, const int* ub,
+                           const int* g2t_offsets, int* tile_ids, int* gauss_ids, hipStream_t s);
+
+int sort_key_bits(int num_tiles);
+size_t sort_workspace(int64_t M, int num_tiles);
+// Stable LSD radix sort of (key < num_tiles, value) pairs.  Inputs are not modified; the
+// sorted pairs land in keys_out/vals_out.
+hipError_t radix_sort_pairs(const int* keys_in, const int* vals_in, int* keys_out, int* vals_out,
+                            int64_t M, int num_tiles, void* ws, hipStream_t s);
+hipError_t launch_tile_offsets(const int* sorted_keys, int64_t M, int T, int* tile_offsets,
+                               hipStream_t s);
+hipError_t launch_rle(const int* tile_offsets, int T, int* unique_tiles, int* counts,
+                      int* runs_offsets, int* num_runs, void* ws, hipStream_t s);
+
+// ---- forward (g2v_forward.hip) ------------------------------------------------------------
+hipError_t launch_forward_density(const Grid& G, const float* means, const float* opacity,
+                                  const float* cov_inv, const int* lb, const int* ub,
+                                  const int* tile_offsets, const int* sorted_gauss, int M,
+                                  float* density, hipStream_t s);
+hipError_t launch_forward_feats(const Grid& G, int C, const float* means, const float* opacity,
+                                const float* cov_inv, const int* lb, const int* ub,
+                                const int* tile_offsets, const int* sorted_gauss, int M,
+                                const float* features, float* density, float* grid_feats,
+                                hipStream_t s);
+
+// ---- backward (g2v_backward.hip) ----------------------------------------------------------
+hipError_t launch_backward_density(const Grid& G, int n, const float* grad_density,
+                                   const float* means, const float* opacity, const float* cov_inv,
+                                   const int* lb, const int* ub, float* grad_means, float* grad_cov,
+                                   float* grad_opacity, hipStream_t s);
+size_t backward_feats_workspace(const Grid& G, int n, int C, int64_t M);
+hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_density,
+                                 const float* grad_feats, const float* means, const float* opacity,
+                                 const float* cov_inv, const int* lb, const int* ub,
+                                 const int* g2t_offsets, int64_t M, const int* tile_offsets,
+                                 const int* sorted_gauss, const float* density,
+                                 const float* grid_feats, const float* features,
+                                 float* grad_means, float* grad_cov, float* grad_opacity,
+                                 float* grad_features, void* ws, hipStream_t s);
+
+// XCD-aware block -> item mapping: consecutive items land on the same XCD (shared L2).
+__device__ __forceinline__ int xcd_remap(int b, int nblocks) {
+    constexpr int kXcd = 8;
+    const int per = (nblocks + kXcd - 1) / kXcd;
+    return (b % kXcd) * per + b / kXcd;
+}
+
+}  // namespace g2v

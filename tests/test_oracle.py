@@ -1,0 +1,370 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the checker of the HIP path.
+
+Every oracle function is checked against something other than its own formula:
+  grid_dims       known grid sizes of the benchmark configs and float32 truncation cases
+  gaussian_boxes  hand-computed boxes (inside, clipped, outside on every face, exact voxel
+                  boundaries, zero and negative variance), invariants, the C restatement
+  invert_3x3      numpy.linalg.inv and the determinant clamp
+  g2t_csr/t2g_csr the toy CSR of the reference README figure (img/g2v_method.png), brute-force
+                  enumeration of tile/box intersections, numpy.lexsort, the C restatement
+  forward_f64     closed forms: single Gaussian, identical features, one-hot features, D < eps
+  backward_f64    central finite differences of forward_f64 and torch autograd (float64);
+                  a planted mistake shows the finite-difference check catches a wrong factor
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import g2v_oracle as O
+from oracle import g2v_oracle_c as OC
+from tests import workloads as W
+
+VS = np.array([0.4, 0.4, 0.4], np.float32)
+VR_SMALL = np.array(W.RANGE_SMALL, np.float32)
+VR_PAPER = np.array(W.RANGE_PAPER, np.float32)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _build_c_oracle():
+    OC.build()
+
+
+# ------------------------------------------------------------------------------ grid dims
+@pytest.mark.parametrize("vs,vr,dims", [
+    ([0.4] * 3, W.RANGE_PAPER, (200, 200, 16)),
+    ([0.4] * 3, W.RANGE_SMALL, (50, 50, 8)),
+    ([0.3] * 3, [0, 0, 0, 0.9, 0.9, 0.9], (2, 2, 2)),        # 0.9f/0.3f = 2.9999998 -> 2
+    ([0.1] * 3, [-1.3, -1.3, -1.3, 1.3, 1.3, 1.3], (25, 25, 25)),  # 25.999998 -> 25
+])
+def test_grid_dims(vs, vr, dims):
+    d, t = O.grid_dims(vs, vr)
+    assert d == dims
+    assert t == tuple((x + 3) // 4 for x in dims)
+
+
+# ------------------------------------------------------------------------------ boxes
+def _box(mu, var, vr=VR_SMALL, vs=VS, cov=None):
+    cov = np.diag(np.asarray(var, np.float32)).reshape(1, 9) if cov is None else np.asarray(cov, np.float32).reshape(1, 9)
+    return O.gaussian_boxes(np.asarray(mu, np.float32).reshape(1, 3), cov, vs, vr)
+
+
+def test_box_inside_hand_computed():
+    # grid x: -10..10 step 0.4 (50 voxels); mu = 0.1, sigma = 1 -> [-2.9, 3.1]
+    b = _box([0.1, 0.1, 0.6], [1.0, 1.0, 0.01])
+    # (-2.9 + 10) / 0.4 = 17.75 -> 17; (3.1 + 10) / 0.4 = 32.75 -> 32
+    assert b["lb"][0, 0] == 17 and b["ub"][0, 0] == 32
+    # z: sigma 0.1 -> [0.3, 0.9]; (0.3 + 1) / 0.4 = 3.25 -> 3; (0.9 + 1) / 0.4 = 4.75 -> 4
+    assert b["lb"][0, 2] == 3 and b["ub"][0, 2] == 4
+    assert b["nvox"][0] == 16 * 16 * 2
+    assert tuple(b["tile_lo"][0]) == (4, 4, 0) and tuple(b["tile_hi"][0]) == (8, 8, 1)
+    assert b["ntiles"][0] == 5 * 5 * 2
+
+
+@pytest.mark.parametrize("axis", [0, 1, 2])
+@pytest.mark.parametrize("side", [-1, 1])
+def test_box_outside_each_face_is_empty(axis, side):
+    mu = np.zeros(3, np.float32)
+    lo, hi = VR_SMALL[:3], VR_SMALL[3:]
+    mu[axis] = (hi[axis] + 3.5) if side > 0 else (lo[axis] - 3.5)
+    b = _box(mu, [1.0, 1.0, 1.0])
+    assert b["nvox"][0] == 0 and b["ntiles"][0] == 0
+    assert tuple(b["lb"][0]) == (0, 0, 0) and tuple(b["ub"][0]) == (-1, -1, -1)
+    assert tuple(b["tile_lo"][0]) == (0, 0, 0) and tuple(b["tile_hi"][0]) == (-1, -1, -1)
+    assert not b["cov_inv"].any()
+
+
+def test_box_centred_outside_but_overlapping_is_clipped():
+    # centred 1.5 m beyond x_max = 10 with sigma 1: [8.5, 13.5] clipped to [8.5, 10]
+    b = _box([11.5, 0.0, 0.0], [1.0, 1.0, 1.0])
+    assert b["lb"][0, 0] == int(np.floor((8.5 + 10) / 0.4)) == 46
+    assert b["ub"][0, 0] == 49        # (10 + 10) / 0.4 = 50 -> clamped to X - 1
+    assert b["nvox"][0] > 0
+
+
+def test_box_exact_voxel_boundary():
+    # sigma = 0.4/3 exactly representable? use sigma with 3*sigma = 0.8 -> var = (0.8/3)^2
+    # choose mu - 3 sigma = -9.2 exactly (voxel 2 starts at -10 + 0.8 = -9.2)
+    var = np.float32((np.float32(0.8) / np.float32(3.0)) ** 2)
+    sig = np.sqrt(var, dtype=np.float32)
+    mu = np.float32(-9.2) + np.float32(3.0) * sig
+    b = _box([mu, 0, 0], [var, 1, 1])
+    lower = np.float32(mu - np.float32(3.0) * sig)
+    assert b["lb"][0, 0] == int(np.floor(np.float32(lower + np.float32(10.0)) / np.float32(0.4)))
+
+
+def test_box_zero_variance_is_single_voxel():
+    b = _box([0.1, 0.1, 0.1], [0.0, 0.0, 0.0])
+    # (0.1 + 10) / 0.4 = 25.25 -> 25; z: (0.1 + 1) / 0.4 = 2.75 -> 2
+    assert tuple(b["lb"][0]) == (25, 25, 2) and tuple(b["ub"][0]) == (25, 25, 2)
+    assert b["nvox"][0] == 1
+
+
+def test_box_negative_variance_spans_axis():
+    # sqrt(-1) = NaN; fmaxf/fminf drop the NaN and the box becomes the whole axis
+    b = _box([0.0, 0.0, 0.0], [-1.0, 1.0, 1.0])
+    assert b["lb"][0, 0] == 0 and b["ub"][0, 0] == 49
+
+
+def test_inverse_matches_numpy_and_clamp():
+    rng = np.random.default_rng(0)
+    R = np.linalg.qr(rng.standard_normal((64, 3, 3)))[0]
+    var = rng.uniform(0.5, 2.5, (64, 3))
+    cov = (R * var[:, None, :]) @ R.transpose(0, 2, 1)
+    inv = O.invert_3x3(cov.reshape(-1, 9).astype(np.float32)).reshape(-1, 3, 3)
+    np.testing.assert_allclose(inv, np.linalg.inv(cov), rtol=2e-5, atol=2e-6)
+    # singular: det = 0 -> det := 1e-6 (the adjugate divided by 1e-6)
+    sing = np.array([[1, 2, 3, 2, 4, 6, 1, 1, 1]], np.float32)
+    adj = O.invert_3x3(sing) * np.float32(1e-6)
+    A = sing.reshape(3, 3).astype(np.float64)
+    cof = np.array([[A[1, 1] * A[2, 2] - A[1, 2] * A[2, 1], -(A[0, 1] * A[2, 2] - A[0, 2] * A[2, 1]), A[0, 1] * A[1, 2] - A[0, 2] * A[1, 1]],
+                    [-(A[1, 0] * A[2, 2] - A[1, 2] * A[2, 0]), A[0, 0] * A[2, 2] - A[0, 2] * A[2, 0], -(A[0, 0] * A[1, 2] - A[0, 2] * A[1, 0])],
+                    [A[1, 0] * A[2, 1] - A[1, 1] * A[2, 0], -(A[0, 0] * A[2, 1] - A[0, 1] * A[2, 0]), A[0, 0] * A[1, 1] - A[0, 1] * A[1, 0]]])
+    np.testing.assert_allclose(adj.reshape(3, 3), cof, rtol=1e-5, atol=1e-6)
+    # small negative determinant is replaced by +1e-6 (sign flip, as the reference does)
+    neg = np.diag([-1e-3, 1e-3, 1e-3]).astype(np.float32).reshape(1, 9)
+    assert O.invert_3x3(neg)[0, 0] > 0
+
+
+def test_box_invariants_random():
+    w = W.Workload("inv", 3000, None, voxel_range=W.RANGE_PAPER, var_range=(0.05, 30.0), mean_pad=12.0)
+    m, o, c, _ = W.generate(w, seed=3)
+    b = O.gaussian_boxes(m.numpy(), c.numpy(), VS, VR_PAPER)
+    dims = np.array(b["dims"])
+    empty = b["nvox"] == 0
+    assert ((b["lb"][~empty] >= 0) & (b["lb"][~empty] <= b["ub"][~empty]) & (b["ub"][~empty] < dims)).all()
+    assert (b["lb"][empty] == 0).all() and (b["ub"][empty] == -1).all()
+    np.testing.assert_array_equal(b["tile_lo"][~empty], b["lb"][~empty] // 4)
+    np.testing.assert_array_equal(b["tile_hi"][~empty], b["ub"][~empty] // 4)
+    np.testing.assert_array_equal(b["nvox"], np.where(empty, 0, np.prod(b["ub"] - b["lb"] + 1, axis=1)))
+    assert empty.any() and (~empty).any()
+
+
+def test_boxes_numpy_equals_c_restatement():
+    for seed, (rng_, pad, var) in enumerate([(W.RANGE_SMALL, 0.0, (0.5, 2.5)), (W.RANGE_PAPER, 4.0, (2.0, 12.0)),
+                                             (W.RANGE_PAPER, 0.0, (0.001, 0.05))]):
+        w = W.Workload("x", 4000, None, voxel_range=rng_, var_range=var, mean_pad=pad)
+        m, o, c, _ = W.generate(w, seed=seed)
+        vr = np.array(rng_, np.float32)
+        a = O.gaussian_boxes(m.numpy(), c.numpy(), VS, vr)
+        b = OC.boxes(m.numpy(), c.numpy(), VS, vr)
+        for k in ("lb", "ub", "nvox", "tile_lo", "tile_hi", "ntiles"):
+            np.testing.assert_array_equal(a[k], b[k], err_msg=k)
+        np.testing.assert_array_equal(a["cov_inv"].view(np.int32), b["cov_inv"].view(np.int32))
+
+
+# ------------------------------------------------------------------------------ CSR
+def test_toy_csr_of_readme_figure():
+    """img/g2v_method.png: G1->{1,2,4}, G2->{2,5,6}, G3->{5,6,8,9} (0-based Gaussians 0..2)."""
+    rows = [[1, 2, 4], [2, 5, 6], [5, 6, 8, 9]]
+    tid = np.array(sum(rows, []), np.int32)
+    gid = np.array(sum([[g] * len(r) for g, r in enumerate(rows)], []), np.int32)
+    off = np.concatenate([[0], np.cumsum([len(r) for r in rows])])
+    assert off.tolist() == [0, 3, 6, 10]
+    t = O.t2g_csr(tid, gid, 10)
+    assert t["unique_tiles"].tolist() == [1, 2, 4, 5, 6, 8, 9]
+    assert t["runs_offsets"].tolist() == [0, 1, 3, 4, 6, 8, 9, 10]
+    lists = [t["sorted_gauss"][a:b].tolist() for a, b in zip(t["runs_offsets"][:-1], t["runs_offsets"][1:])]
+    assert lists == [[0], [0, 1], [0], [1, 2], [1, 2], [2], [2]]
+    assert t["num_runs"] == 7
+    assert t["tile_offsets"].tolist() == [0, 0, 1, 3, 3, 4, 6, 8, 8, 9, 10]
+    # the C restatement (counting sort) agrees
+    toff = np.zeros(11, np.int32)
+    sg = np.zeros(10, np.int32)
+    import ctypes
+    OC.lib().g2vo_t2g(ctypes.c_longlong(10), tid.ctypes.data_as(OC._ip), gid.ctypes.data_as(OC._ip), 10,
+                      toff.ctypes.data_as(OC._ip), sg.ctypes.data_as(OC._ip))
+    np.testing.assert_array_equal(toff, t["tile_offsets"])
+    np.testing.assert_array_equal(sg, t["sorted_gauss"])
+
+
+def _brute_force_t2g(tile_lo, tile_hi, tiles):
+    Tx, Ty, Tz = tiles
+    lists = []
+    for tx in range(Tx):
+        for ty in range(Ty):
+            for tz in range(Tz):
+                p = np.array([tx, ty, tz])
+                inside = ((tile_lo <= p) & (p <= tile_hi)).all(axis=1)
+                lists.append(np.nonzero(inside)[0].tolist())
+    return lists
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_csr_against_brute_force(seed):
+    w = W.Workload("csr", 300, None, voxel_range=W.RANGE_SMALL, var_range=(0.05, 4.0), mean_pad=3.0)
+    m, o, c, _ = W.generate(w, seed=seed)
+    b = O.gaussian_boxes(m.numpy(), c.numpy(), VS, VR_SMALL)
+    off, tid, gid = O.g2t_csr(b["tile_lo"], b["tile_hi"], b["tiles"])
+    T = int(np.prod(b["tiles"]))
+    t = O.t2g_csr(tid, gid, T)
+    lists = _brute_force_t2g(b["tile_lo"], b["tile_hi"], b["tiles"])
+    for tt in range(T):
+        assert t["sorted_gauss"][t["tile_offsets"][tt]:t["tile_offsets"][tt + 1]].tolist() == lists[tt]
+    # each G->T row is ascending and lists exactly the tiles of the box
+    Ty, Tz = b["tiles"][1], b["tiles"][2]
+    for g in range(len(off) - 1):
+        row = tid[off[g]:off[g + 1]]
+        assert (np.diff(row) > 0).all()
+        assert len(row) == b["ntiles"][g]
+        exp = sorted(tt for tt in range(T) if g in lists[tt])
+        assert row.tolist() == exp
+    # stable sort == lexsort on (gauss, tile)
+    order = np.lexsort((gid, tid))
+    np.testing.assert_array_equal(t["sorted_gauss"], gid[order])
+    np.testing.assert_array_equal(t["sorted_tiles"], tid[order])
+    # C restatement
+    coff, ctid, cgid, ctoff, csg = OC.csr(b["tile_lo"], b["tile_hi"], b["tiles"])
+    np.testing.assert_array_equal(coff, off)
+    np.testing.assert_array_equal(ctid, tid)
+    np.testing.assert_array_equal(ctoff, t["tile_offsets"])
+    np.testing.assert_array_equal(csg, t["sorted_gauss"])
+
+
+# ------------------------------------------------------------------------------ forward
+def _tiny_scene(n=6, C=5, seed=0, vr=(-2.0, -2.0, -1.0, 2.0, 2.0, 1.0), vs=(0.4, 0.4, 0.4)):
+    w = W.Workload("tiny", n, C, voxel_range=vr, voxel_size=vs, var_range=(0.1, 0.6))
+    m, o, c, f = W.generate(w, seed=seed)
+    m, o, c = m.numpy(), o.numpy(), c.numpy()
+    f = None if f is None else f.numpy()
+    b = O.gaussian_boxes(m, c, vs, vr)
+    return m, o, c, f, b, np.array(vs, np.float32), np.array(vr, np.float32)
+
+
+def test_forward_single_gaussian_closed_form():
+    m, o, c, f, b, vs, vr = _tiny_scene(n=1, C=3)
+    D, F = O.forward_f64(m, o, c, f, b["lb"], b["ub"], vs, vr)
+    (X, Y, Z), _ = O.grid_dims(vs, vr)
+    Ainv = np.linalg.inv(c.reshape(3, 3).astype(np.float64))
+    lb, ub = b["lb"][0], b["ub"][0]
+    for x in range(X):
+        for y in range(Y):
+            for z in range(Z):
+                inside = lb[0] <= x <= ub[0] and lb[1] <= y <= ub[1] and lb[2] <= z <= ub[2]
+                ctr = vr[:3].astype(np.float64) + (np.array([x, y, z]) + 0.5) * vs
+                d = ctr - m[0]
+                exp = o[0] * np.exp(-0.5 * d @ Ainv @ d) if inside else 0.0
+                assert D[x, y, z] == pytest.approx(exp, rel=1e-12, abs=1e-300)
+                if inside and exp >= 1e-6:
+                    np.testing.assert_allclose(F[x, y, z], f[0], rtol=1e-12)
+
+
+def test_forward_identical_and_one_hot_features():
+    m, o, c, f, b, vs, vr = _tiny_scene(n=8, C=8, seed=1)
+    same = np.tile(np.arange(1, 9, dtype=np.float32)[None, :], (8, 1))
+    D, F = O.forward_f64(m, o, c, same, b["lb"], b["ub"], vs, vr)
+    big = D >= 1e-6
+    np.testing.assert_allclose(F[big], np.broadcast_to(same[0], F[big].shape), rtol=1e-12)
+    onehot = np.eye(8, dtype=np.float32)
+    D2, F2 = O.forward_f64(m, o, c, onehot, b["lb"], b["ub"], vs, vr)
+    # F2[..., g] = w_g / max(D, eps): the columns sum to D / max(D, eps)
+    np.testing.assert_allclose(F2.sum(-1), D2 / np.maximum(D2, 1e-6), rtol=1e-12, atol=1e-15)
+    small = (D2 > 0) & (D2 < 1e-6)
+    if small.any():  # D < eps divides by eps, not by D
+        np.testing.assert_allclose(F2[small].sum(-1), D2[small] / 1e-6, rtol=1e-12)
+
+
+# ------------------------------------------------------------------------------ backward
+def _loss_grads_fd(m, o, c, f, b, vs, vr, gD, gF, h=1e-6):
+    def loss(m_, o_, c_, f_):
+        D, F = O.forward_f64(m_, o_, c_, f_, b["lb"], b["ub"], vs, vr)
+        return float((D * gD).sum() + (F * gF).sum())
+    out = []
+    for arr, idx in ((m, 0), (o, 1), (c, 2), (f, 3)):
+        g = np.zeros(arr.shape)
+        flat = arr.astype(np.float64).reshape(-1)
+        for i in range(flat.size):
+            args = [m.astype(np.float64), o.astype(np.float64), c.astype(np.float64), f.astype(np.float64)]
+            p = flat.copy(); p[i] += h
+            q = flat.copy(); q[i] -= h
+            args[idx] = p.reshape(arr.shape)
+            lp = loss(*args)
+            args[idx] = q.reshape(arr.shape)
+            lq = loss(*args)
+            g.reshape(-1)[i] = (lp - lq) / (2 * h)
+        out.append(g)
+    return out
+
+
+def _sym(gc):
+    g = gc.reshape(-1, 3, 3)
+    return (0.5 * (g + g.transpose(0, 2, 1))).reshape(-1, 9)
+
+
+def test_backward_closed_form_matches_finite_differences():
+    m, o, c, f, b, vs, vr = _tiny_scene(n=4, C=3, seed=2)
+    (X, Y, Z), _ = O.grid_dims(vs, vr)
+    rng = np.random.default_rng(5)
+    gD = rng.standard_normal((X, Y, Z))
+    gF = rng.standard_normal((X, Y, Z, 3))
+    fd = _loss_grads_fd(m, o, c, f, b, vs, vr, gD, gF)
+    gm, gc, go, gf = O.backward_f64(gD, gF, m, o, c, f, b["lb"], b["ub"], vs, vr)
+    for got, exp in ((gm, fd[0]), (go, fd[1]), (gf, fd[3])):
+        assert O.rel_err(got, exp) < 1e-6
+    # finite differences perturb each of the 9 entries separately: compare the symmetric part
+    assert O.rel_err(_sym(gc), _sym(fd[2])) < 1e-6
+
+
+def test_planted_mistake_is_caught_by_finite_differences():
+    """A covariance gradient missing its 0.5 factor must fail the same check."""
+    m, o, c, f, b, vs, vr = _tiny_scene(n=3, C=2, seed=4)
+    (X, Y, Z), _ = O.grid_dims(vs, vr)
+    rng = np.random.default_rng(6)
+    gD = rng.standard_normal((X, Y, Z))
+    gF = rng.standard_normal((X, Y, Z, 2))
+    fd = _loss_grads_fd(m, o, c, f, b, vs, vr, gD, gF)
+    _, gc, _, _ = O.backward_f64(gD, gF, m, o, c, f, b["lb"], b["ub"], vs, vr)
+    assert O.rel_err(_sym(2.0 * gc), _sym(fd[2])) > 0.5
+
+
+def test_backward_matches_torch_autograd():
+    m, o, c, f, b, vs, vr = _tiny_scene(n=10, C=6, seed=7, vr=(-3.0, -3.0, -1.0, 3.0, 3.0, 1.0))
+    # exactly symmetric covariances: autograd's mean gradient is 0.5 (A + A^T) dx, the closed form
+    # (like the reference kernel) uses A dx; they agree only for symmetric A
+    c = (0.5 * (c.reshape(-1, 3, 3) + c.reshape(-1, 3, 3).transpose(0, 2, 1))).reshape(-1, 9).astype(np.float32)
+    (X, Y, Z), _ = O.grid_dims(vs, vr)
+    rng = np.random.default_rng(8)
+    gD = rng.standard_normal((X, Y, Z))
+    gF = rng.standard_normal((X, Y, Z, 6))
+    # independent float64 torch forward, differentiated by autograd
+    tm, to, tc, tf = (torch.tensor(a, dtype=torch.float64, requires_grad=True) for a in (m, o, c, f))
+    Ainv = torch.linalg.inv(tc.view(-1, 3, 3))
+    dens = torch.zeros(X * Y * Z, dtype=torch.float64)
+    fs = torch.zeros(X * Y * Z, 6, dtype=torch.float64)
+    for g in range(len(m)):
+        lb, ub = b["lb"][g], b["ub"][g]
+        if (ub < lb).any():
+            continue
+        idx = torch.tensor(np.stack(np.meshgrid(*[np.arange(lb[a], ub[a] + 1) for a in range(3)], indexing="ij"), -1).reshape(-1, 3))
+        ctr = torch.tensor(vr[:3], dtype=torch.float64) + (idx + 0.5) * torch.tensor(vs, dtype=torch.float64)
+        d = ctr - tm[g]
+        w = to[g] * torch.exp(-0.5 * ((d @ Ainv[g]) * d).sum(-1))
+        lin = (idx[:, 0] * Y + idx[:, 1]) * Z + idx[:, 2]
+        dens = dens.index_add(0, lin, w)
+        fs = fs.index_add(0, lin, w[:, None] * tf[g][None, :])
+    F = fs / dens.clamp_min(1e-6)[:, None]
+    loss = (dens * torch.tensor(gD).reshape(-1)).sum() + (F * torch.tensor(gF).reshape(-1, 6)).sum()
+    loss.backward()
+    gm, gc, go, gf = O.backward_f64(gD, gF, m, o, c, f, b["lb"], b["ub"], vs, vr)
+    assert O.rel_err(gm, tm.grad.numpy()) < 1e-10
+    assert O.rel_err(go, to.grad.numpy()) < 1e-10
+    assert O.rel_err(gf, tf.grad.numpy()) < 1e-10
+    assert O.rel_err(_sym(gc), _sym(tc.grad.numpy())) < 1e-9
+
+
+def test_c_oracle_matches_numpy_oracle():
+    w = W.Workload("c", 200, 16, voxel_range=W.RANGE_SMALL, var_range=(0.3, 1.5))
+    m, o, c, f = (t.numpy() for t in W.generate(w, seed=9))
+    b = O.gaussian_boxes(m, c, VS, VR_SMALL)
+    off, tid, gid, toff, sg = OC.csr(b["tile_lo"], b["tile_hi"], b["tiles"])
+    Ainv = np.linalg.inv(c.reshape(-1, 3, 3).astype(np.float64)).reshape(-1, 9)
+    Dn, Fn = O.forward_f64(m, o, c, f, b["lb"], b["ub"], VS, VR_SMALL)
+    Dc, Fc = OC.forward(m, o, Ainv, b["lb"], b["ub"], VS, VR_SMALL, toff, sg, f, b["dims"])
+    assert O.rel_err(Dc, Dn) < 1e-13 and O.rel_err(Fc, Fn) < 1e-12
+    rng = np.random.default_rng(10)
+    gD = rng.standard_normal(b["dims"]).astype(np.float32)
+    gF = rng.standard_normal(tuple(b["dims"]) + (16,)).astype(np.float32)
+    Df, Ff = Dn.astype(np.float32), Fn.astype(np.float32)
+    gn = O.backward_f64(gD, gF, m, o, c, f, b["lb"], b["ub"], VS, VR_SMALL, density=Df, grid_feats=Ff)
+    gc_ = OC.backward(m, o, Ainv, b["lb"], b["ub"], VS, VR_SMALL, off, tid, f, Df, Ff, gD, gF)
+    for a, bb in zip(gn, gc_):
+        assert O.rel_err(bb, a) < 1e-10
