@@ -1,0 +1,230 @@
+#!/usr/bin/env python3
+"""Benchmark of the Gaussian-to-Voxel splatting hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3] [--no-cpu]
+
+One step = one forward + one backward of the G2V splat through the reference-compatible
+boundary (``_C.gaussian_voxelizer_forward`` then ``_C.gaussian_voxelizer_backward``) on the
+benchmark configuration (BASELINE config 3 by default: 18k Gaussians x 1024-D features into a
+200x200x16 grid, all-ones upstream gradients materialised before timing).  Inputs are resident
+in HBM before the timed region; synthetic data from tests/workloads.py.
+
+Prints ONE JSON line with ms/step (the metric), forward/backward ms, achieved HBM GB/s over the
+compulsory bytes, the roofline of the dominant kernel (per-kernel HIP events recorded by the
+library over the timed steps) and the CPU baseline (the C oracle on a bounded sample, host
+cores, extrapolated to one full step).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "shelfgaussian-cudagaussianvoxelizer_amd")
+for p in (ROOT, PKG):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+METRIC = "G2V fwd+bwd ms/step, 18k Gaussians×1024-D, 200×200×16 grid; achieved HBM GB/s"
+HBM_PEAK_GBPS = 8000.0
+FP32_PEAK_TFLOPS = 157.3
+BF16_PEAK_TFLOPS = 2500.0
+PUBLISHED_FWD_BWD_MS = 3200.0   # README Table 13, 1x L40S, 18k Gaussians x 1024-D
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=3, help="BASELINE config (1-5)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-sample", type=float, default=1.0,
+                    help="fraction of tiles (forward) and Gaussians (backward) the CPU baseline runs")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="also run a plain device copy of this size (PMC scale reference)")
+    return ap.parse_args()
+
+
+def algorithmic_bytes(N, C, V, M, T):
+    """Compulsory HBM bytes per step: every input read once, every output written once."""
+    fwd = 4 * (13 * N + N * C + V + V * C + (N + 1) + M + 16 * N)
+    bwd = 4 * (2 * V + V * C + N * C + 4 * N + 16 * N + (N + 1) + M + 13 * N + N * C)
+    # per-kernel algorithmic bytes (inputs it must read + outputs it must write)
+    per_kernel = {
+        "k_fwd_feats": 4 * (N * C + 19 * N + (T + 1) + M + V + V * C),
+        "k_fwd_density": 4 * (19 * N + (T + 1) + M + V),
+        "k_voxel_dot": 4 * (2 * V * C + 2 * V),
+        "k_bwd_tile": 4 * (V * C + N * C + 3 * V + 19 * N + (N + 1) + (T + 1) + M + 10 * M),
+        "k_bwd_gauss": 4 * (V * C + V + 10 * M + 19 * N + (N + 1) + 13 * N + N * C),
+        "k_bwd_density": 4 * (V + 19 * N + 13 * N),
+    }
+    return fwd, bwd, per_kernel
+
+
+def cpu_baseline(w, host, gpu_out, frac):
+    """The C oracle (a port of the reference algorithm, float64) on a bounded sample, extrapolated."""
+    import numpy as np
+    from oracle import g2v_oracle as O
+    from oracle import g2v_oracle_c as OC
+    m, o, c, f, gD, gF = host
+    vs, vr = np.array(w.voxel_size, np.float32), np.array(w.voxel_range, np.float32)
+    threads = OC.max_threads()
+    t0 = time.perf_counter()
+    b = OC.boxes(m, c, vs, vr)
+    (X, Y, Z), tiles = O.grid_dims(vs, vr)
+    off, tid, gid, toff, sg = OC.csr(b["tile_lo"], b["tile_hi"], tiles)
+    t_csr = time.perf_counter() - t0
+    Ainv = b["cov_inv"].astype(np.float64)
+    T = len(toff) - 1
+    n = m.shape[0]
+    # forward: 8 tile ranges spread over the grid, frac of all tiles in total
+    per = max(1, int(T * frac / 8))
+    t_fwd = 0.0
+    done_tiles = 0
+    for k in range(8):
+        a = min(T - per, (k * T) // 8)
+        t0 = time.perf_counter()
+        OC.forward(m, o, Ainv, b["lb"], b["ub"], vs, vr, toff, sg, f, (X, Y, Z), tile_range=(a, a + per),
+                   nthreads=threads)
+        t_fwd += time.perf_counter() - t0
+        done_tiles += per
+    # backward: a contiguous range of Gaussians (their order is random)
+    ng = max(1, int(n * frac))
+    dens, grid = gpu_out
+    t0 = time.perf_counter()
+    OC.backward(m, o, Ainv, b["lb"], b["ub"], vs, vr, off, tid, f, dens, grid, gD, gF, g_range=(0, ng),
+                nthreads=threads)
+    t_bwd = time.perf_counter() - t0
+    full_ms = 1e3 * (t_csr + t_fwd * T / done_tiles + t_bwd * n / ng)
+    return {"value": round(full_ms, 1), "unit": "ms", "cores": threads, "kind": "port",
+            "sample": (f"C oracle (float64 port of the reference tile-major forward and Gaussian-major "
+                       f"backward, OpenMP) on {done_tiles}/{T} tiles and {ng}/{n} Gaussians of the same "
+                       f"workload, plus the full box+CSR build; extrapolated to one full step "
+                       f"(measured {t_csr + t_fwd + t_bwd:.1f} s)"),
+            "fwd_ms": round(1e3 * (t_csr + t_fwd * T / done_tiles), 1),
+            "bwd_ms": round(1e3 * t_bwd * n / ng, 1)}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
+              "(the G2V path runs on a single MI355X; see DESIGN.md for how it would shard)",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from CudaGaussianVoxelizer import _C, _lib
+    from tests import workloads as W
+
+    w = W.CONFIGS[args.config]
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    m, o, c, f = W.generate(w, seed=0)
+    gD, gF = W.upstream_grads(w)
+    C = 0 if f is None else f.shape[1]
+    (X, Y, Z), (Tx, Ty, Tz) = _C.grid_dims(w.voxel_size, w.voxel_range)
+    if gF is None:
+        gF = torch.zeros(X, Y, Z, 0)
+    md, od, cd = m.to(dev), o.to(dev), c.to(dev)
+    fd = None if f is None else f.to(dev)
+    gDd, gFd = gD.to(dev), gF.to(dev)
+    vs = torch.tensor(w.voxel_size, dtype=torch.float32, device=dev)
+    vr = torch.tensor(w.voxel_range, dtype=torch.float32, device=dev)
+
+    def step():
+        out = _C.gaussian_voxelizer_forward(md, od, cd, vs, vr, fd)
+        g = _C.gaussian_voxelizer_backward(gDd, gFd, md, od, out[1], vs, vr, out[2], out[3], out[4],
+                                           out[6], out[7], out[0], out[5], fd)
+        return out, g
+
+    for _ in range(args.warmup):
+        out, g = step()
+        del out, g
+    torch.cuda.synchronize()
+    _lib.profile_reset()
+    _lib.profile_enable(True)
+    fwd_s = bwd_s = 0.0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out, g = step()
+        fwd_s += out[8]
+        bwd_s += g[4]
+        last = (out, g)
+        del out, g
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    _lib.profile_enable(False)
+    prof = _lib.profile_report()
+    ms = (t1 - t0) * 1e3 / args.steps
+    out, g = last
+    N = m.shape[0]
+    V = X * Y * Z
+    T = Tx * Ty * Tz
+    M = int(out[7].numel())
+    P = int(out[4].to(torch.int64).sum().item())         # in-box (Gaussian, voxel) pairs
+    fwd_b, bwd_b, per_kernel = algorithmic_bytes(N, C, V, M, T)
+    gbps = (fwd_b + bwd_b) / (ms * 1e-3) / 1e9
+
+    if args.copy_probe_mib > 0:   # a plain copy of known size, the scale of the PMC byte counters
+        src = torch.empty(args.copy_probe_mib << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    kernels = {k: {"launches": n_, "avg_ms": round(t_ / max(n_, 1), 4), "total_ms_per_step": round(t_ / args.steps, 4)}
+               for k, (n_, t_) in sorted(prof.items(), key=lambda kv: -kv[1][1])}
+    dom = max(prof.items(), key=lambda kv: kv[1][1])[0] if prof else None
+    roofline = None
+    if dom:
+        n_, t_ = prof[dom]
+        avg_s = t_ / n_ * 1e-3
+        bytes_k = per_kernel.get(dom)
+        traffic = None
+        tpath = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+        if os.path.exists(tpath):
+            with open(tpath) as fh:
+                tr = json.load(fh).get(f"cfg{args.config}", {}).get(dom)
+            if tr:
+                traffic = tr.get("bytes_per_launch")
+        if bytes_k is not None:
+            ach = bytes_k / avg_s / 1e9
+            roofline = {"kernel": dom, "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
+                        "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                        "algorithmic_bytes": bytes_k, "avg_ms": round(avg_s * 1e3, 4)}
+
+    cpu = None
+    if not args.no_cpu and args.gpus == 1:
+        import numpy as np
+        host = (m.numpy(), o.numpy(), c.numpy(), None if f is None else f.numpy(), gD.numpy(),
+                None if C == 0 else gF.numpy())
+        gpu_out = (out[0].cpu().numpy(), None if C == 0 else out[5].cpu().numpy())
+        del out, g, last
+        cpu = cpu_baseline(w, host, gpu_out, args.cpu_sample)
+
+    flops = 2.0 * P * C + 4.0 * P * C    # forward W.F + backward (G.F^T and W^T.G) contractions
+    res = {
+        "metric": METRIC, "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": round(ms / PUBLISHED_FWD_BWD_MS, 6) if args.config == 3 else None,
+        "vs_baseline_note": "value / 3200 ms (README Table 13 FW+BW on 1x L40S); lower is better",
+        "dtype": "f32", "compute": "fp32 in/out; contractions as 3-term bf16-split MFMA with fp32 accumulation",
+        "data": "synthetic (tests/workloads.py, seed 0; upstream grads per config)",
+        "config": {"workload": w.name, "n_gaussians": N, "feat_dim": C, "grid": [X, Y, Z], "tiles": [Tx, Ty, Tz],
+                   "g2t_pairs": M, "inbox_pairs": P, "upstream_grads": w.grads},
+        "fwd_ms": round(fwd_s * 1e3 / args.steps, 4), "bwd_ms": round(bwd_s * 1e3 / args.steps, 4),
+        "hbm_gbps": round(gbps, 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
+        "compulsory_bytes": fwd_b + bwd_b,
+        "fp32_equiv_tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+        "roofline": roofline, "kernels": kernels, "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -97,6 +97,17 @@ int g2v_build_t2g(int n, const float voxel_size[3], const float voxel_range[6],
                   int* runs_offsets, int* num_runs, void* workspace, size_t workspace_bytes,
                   void* stream);
 
+/* ---- per-kernel timing (benchmarks) --------------------------------------------------------
+ * No counterpart in the reference (which times the whole forward/backward with one CUDA event
+ * pair, src/cuda_gaussian_voxelizer.cu:1549-1555, :1905-1913).  While enabled, every kernel launch
+ * of the library is bracketed by two HIP events on its stream.  g2v_profile_collect() waits for
+ * the recorded events and returns the number of distinct kernels; g2v_profile_entry(i, ...) gives
+ * the name, launch count and total milliseconds of kernel i since the last reset. */
+int g2v_profile_enable(int on);
+int g2v_profile_reset(void);
+int g2v_profile_collect(void);
+int g2v_profile_entry(int i, char* name, int name_len, long long* launches, double* total_ms);
+
 #ifdef __cplusplus
 }
 #endif

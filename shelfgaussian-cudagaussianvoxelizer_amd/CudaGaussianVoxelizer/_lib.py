@@ -34,6 +34,10 @@ SIGNATURES = {
     "g2v_t2g_workspace": (_sz, [_i, _ll, _f3, _f3]),
     "g2v_build_t2g": (_i, [_i, _f3, _f3, _vp, _vp, _vp, _vp, _ll, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                            _vp, _sz, _vp]),
+    "g2v_profile_enable": (_i, [_i]),
+    "g2v_profile_reset": (_i, []),
+    "g2v_profile_collect": (_i, []),
+    "g2v_profile_entry": (_i, [_i, ctypes.c_char_p, _i, _llp, ctypes.POINTER(ctypes.c_double)]),
 }
 
 _lib = None
@@ -66,3 +70,26 @@ def check(rc: int, what: str):
 def floats(values):
     vals = [float(v) for v in values]
     return (ctypes.c_float * len(vals))(*vals)
+
+
+def profile_enable(on: bool = True):
+    """Bracket every kernel launch of the library with HIP events (per-kernel timing)."""
+    load().g2v_profile_enable(1 if on else 0)
+
+
+def profile_reset():
+    load().g2v_profile_reset()
+
+
+def profile_report():
+    """{kernel name: (launches, total ms)} accumulated since the last reset."""
+    lib = load()
+    n = lib.g2v_profile_collect()
+    out = {}
+    buf = ctypes.create_string_buffer(128)
+    cnt = ctypes.c_longlong(0)
+    ms = ctypes.c_double(0.0)
+    for i in range(n):
+        check(lib.g2v_profile_entry(i, buf, 128, ctypes.byref(cnt), ctypes.byref(ms)), "g2v_profile_entry")
+        out[buf.value.decode()] = (int(cnt.value), float(ms.value))
+    return out

@@ -87,7 +87,7 @@ hipError_t launch_backward_density(const Grid& G, int n, const float* grad_densi
                                    const int* lb, const int* ub, float* grad_means, float* grad_cov,
                                    float* grad_opacity, hipStream_t s) {
     if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_bwd_density, dim3((unsigned)ceil_div(n, 4)), dim3(256), 0, s, G, n,
+    G2V_LAUNCH(k_bwd_density, dim3((unsigned)ceil_div(n, 4)), dim3(256), 0, s, G, n,
                        grad_density, means, opacity, cov_inv, lb, ub, grad_means, grad_cov,
                        grad_opacity);
     return hipGetLastError();
@@ -369,15 +369,15 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
     float* tv = cv.take<float>(V > 0 ? V : 1);
     float* partials = cv.take<float>((M > 0 ? M : 1) * kNumGrads);
     if (V > 0)
-        hipLaunchKernelGGL(k_voxel_dot, dim3((unsigned)ceil_div(V, 4)), dim3(256), 0, s, V, C,
+        G2V_LAUNCH(k_voxel_dot, dim3((unsigned)ceil_div(V, 4)), dim3(256), 0, s, V, C,
                            grad_feats, grid_feats, density, tv);
     if (M > 0 && T > 0) {
         const int blocks = (int)ceil_div(T, 8) * 8;
-        hipLaunchKernelGGL(k_bwd_tile, dim3(blocks), dim3(kBtThreads), 0, s, G, C, grad_density,
+        G2V_LAUNCH(k_bwd_tile, dim3(blocks), dim3(kBtThreads), 0, s, G, C, grad_density,
                            grad_feats, means, opacity, cov_inv, lb, ub, g2t_offsets, tile_offsets,
                            sorted_gauss, (int)M, density, (const float*)tv, features, partials);
     }
-    hipLaunchKernelGGL(k_bwd_gauss, dim3(n), dim3(kBgThreads), 0, s, G, n, C, (int)M, grad_feats, means,
+    G2V_LAUNCH(k_bwd_gauss, dim3(n), dim3(kBgThreads), 0, s, G, n, C, (int)M, grad_feats, means,
                        opacity, cov_inv, lb, ub, g2t_offsets, density, (const float*)partials,
                        grad_means, grad_cov, grad_opacity, grad_features);
     return hipGetLastError();

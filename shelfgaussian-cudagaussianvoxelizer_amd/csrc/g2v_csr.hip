@@ -96,7 +96,7 @@ __global__ void __launch_bounds__(256) k_boxes(Grid G, int n, const float* __res
 hipError_t launch_boxes(const Grid& G, int n, const float* means, const float* cov, float* cov_inv,
                         int* lb, int* ub, int* nvox, int* g2t_offsets, hipStream_t s) {
     const int blocks = (int)ceil_div(n > 0 ? n : 1, 256);
-    hipLaunchKernelGGL(k_boxes, dim3(blocks), dim3(256), 0, s, G, n, means, cov, cov_inv, lb, ub,
+    G2V_LAUNCH(k_boxes, dim3(blocks), dim3(256), 0, s, G, n, means, cov, cov_inv, lb, ub,
                        nvox, g2t_offsets);
     return hipGetLastError();
 }
@@ -187,9 +187,9 @@ hipError_t scan_i32(const int* in, int* out, int64_t n, bool inclusive, long lon
                     void* ws, hipStream_t s) {
     const int64_t nb = ceil_div(n > 0 ? n : 1, kScanTile);
     long long* partials = static_cast<long long*>(ws);
-    hipLaunchKernelGGL(k_scan_reduce, dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, n, partials);
-    hipLaunchKernelGGL(k_scan_partials, dim3(1), dim3(kScanThreads), 0, s, partials, nb, total_dev);
-    hipLaunchKernelGGL(k_scan_apply, dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, out, n,
+    G2V_LAUNCH(k_scan_reduce, dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, n, partials);
+    G2V_LAUNCH(k_scan_partials, dim3(1), dim3(kScanThreads), 0, s, partials, nb, total_dev);
+    G2V_LAUNCH(k_scan_apply, dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, out, n,
                        (const long long*)partials, inclusive ? 1 : 0);
     return hipGetLastError();
 }
@@ -224,7 +224,7 @@ __global__ void __launch_bounds__(256) k_fill_g2t(Grid G, int n, const int* __re
 hipError_t launch_fill_g2t(const Grid& G, int n, const int* lb, const int* ub,
                            const int* g2t_offsets, int* tile_ids, int* gauss_ids, hipStream_t s) {
     if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_fill_g2t, dim3((unsigned)ceil_div(n, 4)), dim3(256), 0, s, G, n, lb, ub,
+    G2V_LAUNCH(k_fill_g2t, dim3((unsigned)ceil_div(n, 4)), dim3(256), 0, s, G, n, lb, ub,
                        g2t_offsets, tile_ids, gauss_ids);
     return hipGetLastError();
 }
@@ -362,11 +362,11 @@ hipError_t radix_sort_pairs(const int* keys_in, const int* vals_in, int* keys_ou
         int* dk = to_out ? keys_out : pk;
         int* dv = to_out ? vals_out : pv;
         const int shift = p * dbits;
-        hipLaunchKernelGGL(k_radix_hist, dim3(nblk), dim3(kSortThreads), 0, s, src_k, M, shift, dbits,
+        G2V_LAUNCH(k_radix_hist, dim3(nblk), dim3(kSortThreads), 0, s, src_k, M, shift, dbits,
                            nblk, hist);
         hipError_t e = scan_i32(hist, hist, hist_n, false, nullptr, scan_ws, s);
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(k_radix_scatter, dim3(nblk), dim3(kSortThreads), 0, s, src_k, src_v, dk, dv,
+        G2V_LAUNCH(k_radix_scatter, dim3(nblk), dim3(kSortThreads), 0, s, src_k, src_v, dk, dv,
                            M, shift, dbits, nblk, (const int*)hist);
         src_k = dk;
         src_v = dv;
@@ -394,7 +394,7 @@ __global__ void __launch_bounds__(256) k_tile_offsets(const int* __restrict__ ke
 
 hipError_t launch_tile_offsets(const int* sorted_keys, int64_t M, int T, int* tile_offsets,
                                hipStream_t s) {
-    hipLaunchKernelGGL(k_tile_offsets, dim3((unsigned)ceil_div(M + 1, 256)), dim3(256), 0, s,
+    G2V_LAUNCH(k_tile_offsets, dim3((unsigned)ceil_div(M + 1, 256)), dim3(256), 0, s,
                        sorted_keys, M, T, tile_offsets);
     return hipGetLastError();
 }
@@ -433,10 +433,10 @@ hipError_t launch_rle(const int* tile_offsets, int T, int* unique_tiles, int* co
     int* flags = c.take<int>(T > 0 ? T : 1);
     void* scan_ws = c.take<char>(scan_workspace(T));
     const int blocks = (int)ceil_div(T + 1, 256);
-    hipLaunchKernelGGL(k_rle_flags, dim3(blocks), dim3(256), 0, s, tile_offsets, T, flags);
+    G2V_LAUNCH(k_rle_flags, dim3(blocks), dim3(256), 0, s, tile_offsets, T, flags);
     hipError_t e = scan_i32(flags, flags, T, false, nullptr, scan_ws, s);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_rle_write, dim3(blocks), dim3(256), 0, s, tile_offsets, T, (const int*)flags,
+    G2V_LAUNCH(k_rle_write, dim3(blocks), dim3(256), 0, s, tile_offsets, T, (const int*)flags,
                        unique_tiles, counts, runs_offsets, num_runs);
     return hipGetLastError();
 }

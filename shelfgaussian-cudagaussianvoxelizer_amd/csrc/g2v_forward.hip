@@ -58,7 +58,7 @@ hipError_t launch_forward_density(const Grid& G, const float* means, const float
     if (T <= 0) return hipSuccess;
     const int groups = (int)ceil_div(T, 4);
     const int blocks = (int)ceil_div(groups, 8) * 8;
-    hipLaunchKernelGGL(k_fwd_density, dim3(blocks), dim3(256), 0, s, G, means, opacity, cov_inv, lb,
+    G2V_LAUNCH(k_fwd_density, dim3(blocks), dim3(256), 0, s, G, means, opacity, cov_inv, lb,
                        ub, tile_offsets, sorted_gauss, M, density);
     return hipGetLastError();
 }
@@ -229,7 +229,7 @@ hipError_t launch_forward_feats(const Grid& G, int C, const float* means, const 
         return launch_forward_density(G, means, opacity, cov_inv, lb, ub, tile_offsets, sorted_gauss,
                                       M, density, s);
     const int blocks = (int)ceil_div(T, 8) * 8;
-    hipLaunchKernelGGL(k_fwd_feats, dim3(blocks), dim3(kFwdThreads), 0, s, G, C, means, opacity,
+    G2V_LAUNCH(k_fwd_feats, dim3(blocks), dim3(kFwdThreads), 0, s, G, C, means, opacity,
                        cov_inv, lb, ub, tile_offsets, sorted_gauss, M, features, density, grid_feats);
     return hipGetLastError();
 }

@@ -82,6 +82,26 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
                                  float* grad_means, float* grad_cov, float* grad_opacity,
                                  float* grad_features, void* ws, hipStream_t s);
 
+// Brackets one kernel launch with HIP events when profiling is enabled (g2v_profile.hip).
+class ProfMark {
+  public:
+    ProfMark(const char* name, hipStream_t s);
+    ~ProfMark();
+    ProfMark(const ProfMark&) = delete;
+    ProfMark& operator=(const ProfMark&) = delete;
+
+  private:
+    const char* name_;
+    hipStream_t s_;
+    void* a_;
+};
+
+#define G2V_LAUNCH(kernel, grid, block, shmem, stream, ...)                      \
+    do {                                                                        \
+        ::g2v::ProfMark g2v_pm_(#kernel, stream);                               \
+        hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);     \
+    } while (0)
+
 // XCD-aware block -> item mapping: consecutive items land on the same XCD (shared L2).
 __device__ __forceinline__ int xcd_remap(int b, int nblocks) {
     constexpr int kXcd = 8;
