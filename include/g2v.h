@@ -68,20 +68,31 @@ int g2v_forward_splat(int n, int feat_dim, const float* means3D, const float* op
 
 /* ---- backward -----------------------------------------------------------------------------
  * Replaces cuda_gaussian_voxelizer_backward (src/cuda_gaussian_voxelizer.cu:1920-2057, bound at
- * src/bindings.cpp:30-64).  Writes grad_means (N,3), grad_cov (N,9, symmetric), grad_opacity (N,)
- * and, when feat_dim > 0, grad_features (N,feat_dim).  grad_feats/grid_feats/features may be
- * NULL when feat_dim == 0.  Asynchronous; atomic-free and deterministic. */
-size_t g2v_backward_workspace(int n, int feat_dim, long long num_pairs, const float voxel_size[3],
-                              const float voxel_range[6]);
+ * src/bindings.cpp:30-64), in two calls like the forward:
+ *
+ * g2v_backward_plan: with features, counts the (region, Gaussian) pairs of the feature-gradient
+ * phase (regions of 2x2x4 tiles) into plan_workspace and synchronises the stream once to return
+ * their number; without features it does nothing and returns 0. */
+size_t g2v_backward_plan_workspace(int n);
+int g2v_backward_plan(int n, int feat_dim, const float voxel_size[3], const float voxel_range[6],
+                      const int* valid_voxel_lb, const int* valid_voxel_ub, void* plan_workspace,
+                      size_t plan_workspace_bytes, long long* num_region_pairs, void* stream);
+
+/* g2v_backward: writes grad_means (N,3), grad_cov (N,9, symmetric), grad_opacity (N,) and, when
+ * feat_dim > 0, grad_features (N,feat_dim).  grad_feats/grid_feats/features may be NULL when
+ * feat_dim == 0.  plan_workspace is the one given to g2v_backward_plan.  Asynchronous;
+ * atomic-free and deterministic. */
+size_t g2v_backward_workspace(int n, int feat_dim, long long num_pairs, long long num_region_pairs,
+                              const float voxel_size[3], const float voxel_range[6]);
 int g2v_backward(int n, int feat_dim, const float* grad_density, const float* grad_feats,
                  const float* means3D, const float* opacity, const float* cov_inv,
                  const float voxel_size[3], const float voxel_range[6],
                  const int* valid_voxel_lb, const int* valid_voxel_ub,
                  const int* num_voxels_per_gaussian, const int* g2t_offsets,
-                 const int* g2t_tile_ids, long long num_pairs, const float* density,
-                 const float* grid_feats, const float* features,
+                 const int* g2t_tile_ids, long long num_pairs, long long num_region_pairs,
+                 const float* density, const float* grid_feats, const float* features,
                  float* grad_means, float* grad_cov, float* grad_opacity, float* grad_features,
-                 void* workspace, size_t workspace_bytes, void* stream);
+                 const void* plan_workspace, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- Tile->Gaussian CSR (inspection) -------------------------------------------------------
  * The internal Tile->Gaussian CSR of the forward, for parity tests: the stable sort of the G->T

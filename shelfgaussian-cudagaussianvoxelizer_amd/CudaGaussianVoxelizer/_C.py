@@ -189,16 +189,22 @@ def gaussian_voxelizer_backward(grad_output, grad_feats_output, means3D, opacity
         grad_cov = torch.empty(n, 9, dtype=f32, device=dev)
         grad_opacity = torch.empty(n, dtype=f32, device=dev)
         grad_feats = torch.empty(n, C, dtype=f32, device=dev)
-        ws = torch.empty(max(1, lib.g2v_backward_workspace(n, C, M, vs, vr)), dtype=torch.uint8, device=dev)
+        plan_ws = torch.empty(max(1, lib.g2v_backward_plan_workspace(n)), dtype=torch.uint8, device=dev)
         start = torch.cuda.Event(enable_timing=True)
         stop = torch.cuda.Event(enable_timing=True)
         start.record(cur)
+        MR = ctypes.c_longlong(0)
+        _lib.check(lib.g2v_backward_plan(n, C, vs, vr, _ptr(valid_voxel_lb), _ptr(valid_voxel_ub), _ptr(plan_ws),
+                                         plan_ws.numel(), ctypes.byref(MR), stream),
+                   "gaussian_voxelizer_backward (plan)")
+        MR = int(MR.value)
+        ws = torch.empty(max(1, lib.g2v_backward_workspace(n, C, M, MR, vs, vr)), dtype=torch.uint8, device=dev)
         _lib.check(lib.g2v_backward(n, C, _ptr(grad_output), _ptr(gF), _ptr(means3D), _ptr(opacity),
                                     _ptr(cov_inv), vs, vr, _ptr(valid_voxel_lb), _ptr(valid_voxel_ub),
                                     _ptr(num_voxels_per_gaussian), _ptr(g2t_offsets), _ptr(g2t_tile_ids),
-                                    M, _ptr(density), _ptr(grid_feats), _ptr(feats),
+                                    M, MR, _ptr(density), _ptr(grid_feats), _ptr(feats),
                                     _ptr(grad_means), _ptr(grad_cov), _ptr(grad_opacity),
-                                    _ptr(grad_feats), _ptr(ws), ws.numel(), stream),
+                                    _ptr(grad_feats), _ptr(plan_ws), _ptr(ws), ws.numel(), stream),
                    "gaussian_voxelizer_backward")
         stop.record(cur)
         stop.synchronize()

@@ -1,4 +1,4 @@
-// Backward of the G2V splat for gfx950, atomic-free
+// Backward of the G2V splat for gfx950, atomic-free and deterministic
 // (reference src/cuda_gaussian_voxelizer.cu:1226-1482, :1920-2057).
 //
 // Per (Gaussian g, voxel v in its box): e = exp(-0.5 dx^T A dx), w = o e, q = A dx,
@@ -6,14 +6,19 @@
 //     gw = gD_v + (u_gv - t_v) inv        (gw = gD_v without features)
 //     d mu += gw w q,  d Sigma += 0.5 gw w q q^T (symmetric),  d o += gw e,  d f_g += gF_v w inv
 //
-// Kernels:
-//   k_bwd_density   features=None: one wave per Gaussian over its box voxels, wave reduction.
-//   k_voxel_dot     t_v for every voxel (the reference's bmm, .cu:1995-1996).
-//   k_bwd_tile      tile-major: U^T = G_tile (64 x C) . F_list^T on the matrix cores (3-term bf16
-//                   split), then gw and the ten geometric partial sums of every (tile, Gaussian)
-//                   pair, stored at the pair's Gaussian->Tile CSR slot.
-//   k_bwd_gauss     Gaussian-major: sums the pair partials of its CSR row (fixed order) and
-//                   gathers d f_g over its box voxels.  Every output row has one owner.
+// With features the work is split in three phases so that every gF row is read from HBM
+// twice instead of once per overlapping Gaussian (the reference re-reads it per pair):
+//   A  k_bwd_tile    one workgroup per 4x4x4 tile: U^T = G_tile (64 x C) . F_list^T on the matrix
+//                    cores (3-term bf16 split, fp32 accumulate); t_v from U (sum_g [w>0] w u / D is
+//                    sum_c gF F); gw; the ten geometric partial sums of each (tile, Gaussian) pair,
+//                    stored at the pair's G->T CSR slot; the split weights w/max(D,eps) of the pair.
+//   B  k_bwd_region  one workgroup per (region of 2x2xRZ tiles, 64-channel chunk): for every tile
+//                    of the region, (pairs x 64 voxels) . (64 voxels x 64 channels) on the matrix
+//                    cores, accumulated in LDS rows owned by the region's Gaussians; writes one
+//                    partial d f row per (region, Gaussian) pair at its G->R CSR slot.
+//   C  k_bwd_gauss   one workgroup per Gaussian: fixed-order sums of its geometric partials and
+//                    of its region partial rows.
+// Without features, k_bwd_density walks each Gaussian's box with one wave.
 #include "g2v_internal.h"
 
 namespace g2v {
@@ -46,6 +51,24 @@ __device__ __forceinline__ void write_grads(const float (&gr)[kNumGrads], int g,
     c[3] = gr[6]; c[4] = gr[4]; c[5] = gr[8];
     c[6] = gr[7]; c[7] = gr[8]; c[8] = gr[5];
     grad_opacity[g] = gr[9];
+}
+
+// Regions of the feature-gradient phase: 2 x 2 tiles in x, y and up to 4 tiles in z.
+struct Regions {
+    int cell[3];   // voxels per region along each axis
+    int n[3];      // region grid
+    int total;
+};
+
+static Regions make_regions(const Grid& G) {
+    Regions R;
+    const int rz = min(G.tiles[2], 4);
+    R.cell[0] = 2 * kTile;
+    R.cell[1] = 2 * kTile;
+    R.cell[2] = rz * kTile;
+    for (int a = 0; a < 3; ++a) R.n[a] = (G.dims[a] + R.cell[a] - 1) / R.cell[a];
+    R.total = R.n[0] * R.n[1] * R.n[2];
+    return R;
 }
 
 // ------------------------------------------------------------------------------------------
@@ -87,60 +110,56 @@ hipError_t launch_backward_density(const Grid& G, int n, const float* grad_densi
                                    const int* lb, const int* ub, float* grad_means, float* grad_cov,
                                    float* grad_opacity, hipStream_t s) {
     if (n <= 0) return hipSuccess;
-    G2V_LAUNCH(k_bwd_density, dim3((unsigned)ceil_div(n, 4)), dim3(256), 0, s, G, n,
-                       grad_density, means, opacity, cov_inv, lb, ub, grad_means, grad_cov,
-                       grad_opacity);
+    G2V_LAUNCH(k_bwd_density, dim3((unsigned)ceil_div(n, 4)), dim3(256), 0, s, G, n, grad_density, means,
+               opacity, cov_inv, lb, ub, grad_means, grad_cov, grad_opacity);
     return hipGetLastError();
 }
 
 // ------------------------------------------------------------------------------------------
-// t_v = (D_v >= eps) ? sum_c gF_vc F_vc : 0, one wave per voxel.
+// Features split once into bf16 hi/lo rows padded to Cp channels (zeros beyond C).
 // ------------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) k_voxel_dot(int64_t V, int C, const float* __restrict__ gF,
-                                                   const float* __restrict__ F,
-                                                   const float* __restrict__ D,
-                                                   float* __restrict__ t) {
-    const int lane = threadIdx.x & 63;
-    const int64_t v = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (v >= V) return;
-    const float* a = gF + v * C;
-    const float* b = F + v * C;
-    float s = 0.0f;
-    if ((C & 3) == 0) {
-        for (int c = lane * 4; c < C; c += 256) {
-            const float4 x = *reinterpret_cast<const float4*>(a + c);
-            const float4 y = *reinterpret_cast<const float4*>(b + c);
-            s += x.x * y.x + x.y * y.y + x.z * y.z + x.w * y.w;
-        }
-    } else {
-        for (int c = lane; c < C; c += 64) s += a[c] * b[c];
-    }
-    s = wave_sum(s);
-    if (lane == 0) t[v] = (D[v] >= kEps) ? s : 0.0f;
+__global__ void __launch_bounds__(256) k_split_rows(const float* __restrict__ src, int64_t rows, int C,
+                                                    int Cp, __bf16* __restrict__ hi,
+                                                    __bf16* __restrict__ lo) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * Cp) return;
+    const int64_t r = i / Cp;
+    const int c = (int)(i - r * Cp);
+    const float v = c < C ? src[r * C + c] : 0.0f;
+    __bf16 h, l;
+    split_bf16(v, h, l);
+    hi[i] = h;
+    lo[i] = l;
 }
 
 // ------------------------------------------------------------------------------------------
-// Tile-major geometric partials (MFMA for U).
+// Phase A: tile-major U, t_v, gw, geometric partials, split weights.
 // ------------------------------------------------------------------------------------------
-constexpr int kBtThreads = 256;      // 4 waves: (voxel block mb = wave & 1) x (Gaussian group wave >> 1)
-constexpr int kBtNbw = 4;            // 32-Gaussian N blocks per wave per pass
-constexpr int kBtPass = 2 * kBtNbw * 32;  // Gaussians per pass (256)
+constexpr int kBtThreads = 512;                        // 8 waves
+constexpr int kBtGroups = 4;                           // Gaussian groups (wave >> 1)
+constexpr int kBtNbw = 3;                              // 32-Gaussian N blocks per wave per pass
+constexpr int kBtPass = kBtGroups * kBtNbw * 32;       // 384 Gaussians per pass
+constexpr int kBtKc = 64;                              // channels of G staged per LDS chunk
+constexpr int kWtRow = 128;                            // bf16 per pair: 64 hi then 64 lo
 
 struct BtSmem {
+    bf16x8 ahi[2][kBtKc / 16][2][64];   // A operand (G tile), hi: [buffer][k step][voxel block][lane]
+    bf16x8 alo[2][kBtKc / 16][2][64];
     int vlin[64];
-    float gD[64], inv[64], tv[64];
+    float gD[64], inv[64], tv[64], D[64];
     int gid[kBtPass];
-    float xch[2][kBtPass][kNumGrads + 1];
+    float tpart[kBtGroups][64];
+    float xch[2][kBtPass][kNumGrads];
 };
 
 __global__ void __launch_bounds__(kBtThreads, 2) k_bwd_tile(
-    Grid G, int C, const float* __restrict__ gD, const float* __restrict__ gF,
+    Grid G, int C, int Cp, const float* __restrict__ gD, const float* __restrict__ gF,
     const float* __restrict__ means, const float* __restrict__ opacity,
     const float* __restrict__ cov_inv, const int* __restrict__ lb, const int* __restrict__ ub,
     const int* __restrict__ g2t_offsets, const int* __restrict__ toff,
     const int* __restrict__ sorted_gauss, int M, const float* __restrict__ density,
-    const float* __restrict__ tvox, const float* __restrict__ features,
-    float* __restrict__ pair_partials) {
+    const float* __restrict__ grid_feats, const __bf16* __restrict__ fhi,
+    const __bf16* __restrict__ flo, float* __restrict__ pair_partials, __bf16* __restrict__ wt) {
     __shared__ BtSmem sm;
     const int T = G.tiles[0] * G.tiles[1] * G.tiles[2];
     const int tile = uniform(xcd_remap(blockIdx.x, gridDim.x));
@@ -152,6 +171,7 @@ __global__ void __launch_bounds__(kBtThreads, 2) k_bwd_tile(
     const int mb = wave & 1, ngrp = wave >> 1;
     const int tyz = G.tiles[1] * G.tiles[2];
     const int tx = tile / tyz, ty = (tile - tx * tyz) / G.tiles[2], tz = tile % G.tiles[2];
+    const bool vec_ok = (C & 3) == 0;
 
     if (threadIdx.x < 64) {
         int x, y, z;
@@ -160,62 +180,159 @@ __global__ void __launch_bounds__(kBtThreads, 2) k_bwd_tile(
         const int64_t v = ok ? voxel_index(G, x, y, z) : 0;
         sm.vlin[threadIdx.x] = ok ? (int)v : -1;
         sm.gD[threadIdx.x] = ok ? gD[v] : 0.0f;
+        sm.D[threadIdx.x] = ok ? density[v] : 0.0f;
         sm.inv[threadIdx.x] = ok ? 1.0f / fmaxf(density[v], kEps) : 0.0f;
-        sm.tv[threadIdx.x] = ok ? tvox[v] : 0.0f;
+        sm.tv[threadIdx.x] = 0.0f;
     }
-    const bool vec_ok = (C & 3) == 0;
+    __syncthreads();
+
+    // Lists longer than one pass: t_v = sum_c gF_vc F_vc straight from grid_feats.
+    const bool multi = Ng > kBtPass;
+    if (multi) {
+        for (int k = 0; k < 8; ++k) {
+            const int r = wave * 8 + k;
+            const int v = sm.vlin[r];
+            if (v < 0) continue;
+            const float* a = gF + (int64_t)v * C;
+            const float* b = grid_feats + (int64_t)v * C;
+            float s = 0.0f;
+            for (int c = lane; c < C; c += 64) s += a[c] * b[c];
+            s = wave_sum(s);
+            if (lane == 0) sm.tv[r] = density[v] >= kEps ? s : 0.0f;
+        }
+    }
 
     for (int pbase = 0; pbase < Ng; pbase += kBtPass) {
         const int pcount = min(kBtPass, Ng - pbase);
         __syncthreads();
         for (int k = threadIdx.x; k < kBtPass; k += kBtThreads)
             sm.gid[k] = k < pcount ? sorted_gauss[j0 + pbase + k] : -1;
+
+        // stage G chunk 0 into buffer 0
+        const int sv = threadIdx.x >> 3, sq = threadIdx.x & 7;   // staging: voxel, 8-channel group
+        const int srow = sm.vlin[sv];
+        auto stage = [&](int chunk, int buf) {
+            const int c = chunk * kBtKc + sq * 8;
+            float v8[8];
+            const int valid = max(0, min(8, C - c));
+            if (srow >= 0 && valid > 0) load8(gF + (int64_t)srow * C + c, valid, vec_ok, v8);
+            else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v8[i] = 0.0f;
+            }
+            bf16x8 h, l;
+            split8(v8, h, l);
+            const int s = sq >> 1, L = (sq & 1) * 32 + (sv & 31);
+            sm.ahi[buf][s][sv >> 5][L] = h;
+            sm.alo[buf][s][sv >> 5][L] = l;
+        };
+        stage(0, 0);
         __syncthreads();
 
         f32x16 acc[kBtNbw];
 #pragma unroll
         for (int j = 0; j < kBtNbw; ++j) acc[j] = f32x16{};
-        int nact = 0;  // active N blocks of this wave (uniform)
+        int nact = 0;
 #pragma unroll
-        for (int j = 0; j < kBtNbw; ++j) nact += ((ngrp + 2 * j) * 32 < pcount) ? 1 : 0;
+        for (int j = 0; j < kBtNbw; ++j) nact += ((ngrp + kBtGroups * j) * 32 < pcount) ? 1 : 0;
+        int gcol[kBtNbw];
+#pragma unroll
+        for (int j = 0; j < kBtNbw; ++j) gcol[j] = sm.gid[(ngrp + kBtGroups * j) * 32 + (lane & 31)];
 
-        const int arow = sm.vlin[mb * 32 + (lane & 31)];
-        const int koff = (lane >> 5) * 8;
-        for (int c0 = 0; c0 < C; c0 += 16) {
-            const int c = c0 + koff;
-            const int valid = max(0, min(8, C - c));
-            float av[8];
-            if (arow >= 0) load8(gF + (int64_t)arow * C + c, valid, vec_ok, av);
-            else {
+        const int nchunks = (Cp + kBtKc - 1) / kBtKc;
+        for (int ch = 0; ch < nchunks; ++ch) {
+            const int buf = ch & 1;
+            if (ch + 1 < nchunks) stage(ch + 1, buf ^ 1);
+            const int ksteps = min(kBtKc, Cp - ch * kBtKc) >> 4;
+            for (int s = 0; s < ksteps; ++s) {
+                const int c = ch * kBtKc + s * 16 + (lane >> 5) * 8;
+                const bf16x8 ah = sm.ahi[buf][s][mb][lane];
+                const bf16x8 al = sm.alo[buf][s][mb][lane];
 #pragma unroll
-                for (int i = 0; i < 8; ++i) av[i] = 0.0f;
-            }
-            bf16x8 ah, al;
-            split8(av, ah, al);
-#pragma unroll
-            for (int j = 0; j < kBtNbw; ++j) {
-                if (j < nact) {
-                    const int g = sm.gid[(ngrp + 2 * j) * 32 + (lane & 31)];
-                    float bv[8];
-                    if (g >= 0) load8(features + (int64_t)g * C + c, valid, vec_ok, bv);
-                    else {
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) bv[i] = 0.0f;
+                for (int j = 0; j < kBtNbw; ++j) {
+                    if (j < nact) {
+                        bf16x8 bh = {}, bl = {};
+                        if (gcol[j] >= 0) {
+                            bh = *reinterpret_cast<const bf16x8*>(fhi + (int64_t)gcol[j] * Cp + c);
+                            bl = *reinterpret_cast<const bf16x8*>(flo + (int64_t)gcol[j] * Cp + c);
+                        }
+                        acc[j] = mfma3_32x32x16(ah, al, bh, bl, acc[j]);
                     }
-                    bf16x8 bh, bl;
-                    split8(bv, bh, bl);
-                    acc[j] = mfma3_32x32x16(ah, al, bh, bl, acc[j]);
                 }
             }
+            __syncthreads();
         }
 
-        // gw and geometric partials of each (tile, Gaussian) pair held by this lane's column
+        // ---- epilogue 1: split weights w / max(D, eps) of every pair; t_v from U (single pass)
+        float rowt[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) rowt[i] = 0.0f;
 #pragma unroll
         for (int j = 0; j < kBtNbw; ++j) {
-            const int slot = (ngrp + 2 * j) * 32 + (lane & 31);
+            const int slot = (ngrp + kBtGroups * j) * 32 + (lane & 31);
+            const int g = (j < nact) ? gcol[j] : -1;
+            if (g < 0) continue;
+            GaussParams p;
+            load_params(p, g, means, cov_inv, opacity, lb, ub);
+            __bf16* wrow = wt + (int64_t)(j0 + pbase + slot) * kWtRow;
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                __bf16 hs[4], ls[4];
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii) {
+                    const int i = q4 * 4 + ii;
+                    const int r = mb * 32 + 8 * q4 + 4 * (lane >> 5) + ii;
+                    float w = 0.0f;
+                    if (sm.vlin[r] >= 0) {
+                        const int x = tx * kTile + (r >> 4), y = ty * kTile + ((r >> 2) & 3), z = tz * kTile + (r & 3);
+                        if (in_box(p, x, y, z)) {
+                            float qx, qy, qz;
+                            w = p.o * eval_gauss(p, centre(G, 0, x), centre(G, 1, y), centre(G, 2, z), qx, qy, qz);
+                        }
+                    }
+                    const float wtil = w * sm.inv[r];
+                    split_bf16(wtil, hs[ii], ls[ii]);
+                    rowt[i] += (w > 0.0f ? wtil : 0.0f) * acc[j][i];
+                }
+                const int r0 = mb * 32 + 8 * q4 + 4 * (lane >> 5);
+                typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+                bf16x4 hv = {hs[0], hs[1], hs[2], hs[3]};
+                bf16x4 lv = {ls[0], ls[1], ls[2], ls[3]};
+                *reinterpret_cast<bf16x4*>(wrow + r0) = hv;
+                *reinterpret_cast<bf16x4*>(wrow + 64 + r0) = lv;
+            }
+        }
+        if (!multi) {
+            // rows are shared by the 32 lanes of each half-wave: reduce over them
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                float v = rowt[i];
+#pragma unroll
+                for (int off = 1; off < 32; off <<= 1) v += __shfl_xor(v, off, 64);
+                rowt[i] = v;
+            }
+            if ((lane & 31) == 0) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    sm.tpart[ngrp][mb * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3)] = rowt[i];
+            }
+            __syncthreads();
+            if (threadIdx.x < 64) {
+                const int r = threadIdx.x;
+                const float s = ((sm.tpart[0][r] + sm.tpart[1][r]) + sm.tpart[2][r]) + sm.tpart[3][r];
+                // sum_g [w>0] w u / max(D, eps) = sum_c gF F; zero where D < eps (reference .cu:1450)
+                sm.tv[r] = (sm.vlin[r] >= 0 && sm.D[r] >= kEps) ? s : 0.0f;
+            }
+            __syncthreads();
+        }
+
+        // ---- epilogue 2: gw and the geometric partials of each pair
+#pragma unroll
+        for (int j = 0; j < kBtNbw; ++j) {
+            const int slot = (ngrp + kBtGroups * j) * 32 + (lane & 31);
+            const int g = (j < nact) ? gcol[j] : -1;
             float gr[kNumGrads] = {};
-            const int g = sm.gid[slot];
-            if (j < nact && g >= 0) {
+            if (g >= 0) {
                 GaussParams p;
                 load_params(p, g, means, cov_inv, opacity, lb, ub);
 #pragma unroll
@@ -252,25 +369,146 @@ __global__ void __launch_bounds__(kBtThreads, 2) k_bwd_tile(
 }
 
 // ------------------------------------------------------------------------------------------
-// Gaussian-major: reduce the pair partials of a CSR row; gather d f_g over the box voxels.
+// Phase B: per-region partial feature gradients, accumulated in LDS.
+// ------------------------------------------------------------------------------------------
+constexpr int kBrThreads = 256;   // 4 waves
+constexpr int kBrCc = 64;         // channels per work item
+constexpr int kBrRows = 448;      // region rows held in LDS at a time
+constexpr int kBrBatch = 256;     // tile entries mapped to rows at a time (8 row blocks)
+constexpr int kBrAccLd = kBrCc + 4;
+
+struct BrSmem {
+    float acc[kBrRows][kBrAccLd];
+    bf16x8 bhi[4][2][64];          // B operand (G chunk): [k step of 16 voxels][channel block][lane]
+    bf16x8 blo[4][2][64];
+    int rows[kBrRows];             // Gaussian of each local row (ascending)
+    int rmap[kBrBatch];            // tile entry -> local row, -1 outside this row group
+};
+
+__global__ void __launch_bounds__(kBrThreads, 1) k_bwd_region(
+    Grid G, Regions RG, int C, int nchunk, const float* __restrict__ gF,
+    const int* __restrict__ toff, const int* __restrict__ sorted_gauss, int M,
+    const int* __restrict__ roff, const int* __restrict__ r_pairs, const int* __restrict__ r_gauss,
+    int MR, const __bf16* __restrict__ wt, float* __restrict__ gpart) {
+    __shared__ BrSmem sm;
+    const int idx = xcd_remap(blockIdx.x, gridDim.x);
+    const int R = uniform(idx / nchunk);
+    const int chunk = uniform(idx - R * nchunk);
+    if (R >= RG.total) return;
+    const int c0 = chunk * kBrCc;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int rnyz = RG.n[1] * RG.n[2];
+    const int rx = R / rnyz, ry = (R - rx * rnyz) / RG.n[2], rz = R % RG.n[2];
+    const int tpr_z = RG.cell[2] / kTile;
+    const int jr0 = uniform(min(max(roff[R], 0), MR));
+    const int KR = uniform(min(max(roff[R + 1], jr0), MR)) - jr0;
+    if (KR <= 0) return;
+
+    for (int rg0 = 0; rg0 < KR; rg0 += kBrRows) {
+        const int nrows = min(kBrRows, KR - rg0);
+        __syncthreads();
+        for (int k = threadIdx.x; k < nrows; k += kBrThreads) sm.rows[k] = r_gauss[r_pairs[jr0 + rg0 + k]];
+        for (int k = threadIdx.x; k < nrows * kBrCc; k += kBrThreads) sm.acc[k / kBrCc][k % kBrCc] = 0.0f;
+
+        for (int ltx = 0; ltx < 2; ++ltx)
+        for (int lty = 0; lty < 2; ++lty)
+        for (int ltz = 0; ltz < tpr_z; ++ltz) {
+            const int tx = rx * 2 + ltx, ty = ry * 2 + lty, tz = rz * tpr_z + ltz;
+            if (tx >= G.tiles[0] || ty >= G.tiles[1] || tz >= G.tiles[2]) continue;
+            const int t = (tx * G.tiles[1] + ty) * G.tiles[2] + tz;
+            const int jt0 = uniform(min(max(toff[t], 0), M));
+            const int Nt = uniform(min(max(toff[t + 1], jt0), M)) - jt0;
+            if (Nt <= 0) continue;
+            __syncthreads();   // previous users of bhi/blo/rmap are done
+            {   // stage the G chunk of this tile as the B operand: thread = (channel, voxel octets)
+                const int c = threadIdx.x & 63, oq = threadIdx.x >> 6;
+                const bool cok = c0 + c < C;
+                for (int o = oq; o < 8; o += 4) {
+                    float v8[8];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const int lv = o * 8 + i;
+                        int x, y, z;
+                        tile_voxel(G, t, lv, x, y, z);
+                        v8[i] = (cok && in_grid(G, x, y, z)) ? gF[voxel_index(G, x, y, z) * C + c0 + c] : 0.0f;
+                    }
+                    bf16x8 h, l;
+                    split8(v8, h, l);
+                    const int s = o >> 1, L = (o & 1) * 32 + (c & 31);
+                    sm.bhi[s][c >> 5][L] = h;
+                    sm.blo[s][c >> 5][L] = l;
+                }
+            }
+            for (int kb0 = 0; kb0 < Nt; kb0 += kBrBatch) {
+                const int nb = min(kBrBatch, Nt - kb0);
+                if (kb0 > 0) __syncthreads();
+                for (int k = threadIdx.x; k < kBrBatch; k += kBrThreads) {
+                    int lr = -1;
+                    if (k < nb) {
+                        const int g = sorted_gauss[jt0 + kb0 + k];
+                        int lo = 0, hi = nrows;   // rows are ascending: binary search
+                        while (lo < hi) {
+                            const int mid = (lo + hi) >> 1;
+                            if (sm.rows[mid] < g) lo = mid + 1;
+                            else hi = mid;
+                        }
+                        if (lo < nrows && sm.rows[lo] == g) lr = lo;
+                    }
+                    sm.rmap[k] = lr;
+                }
+                __syncthreads();
+                const int nblk = (nb + 31) >> 5;
+                for (int rb = wave; rb < nblk; rb += 4) {
+                    const int row = rb * 32 + (lane & 31);
+                    const bool valid = row < nb;
+                    const __bf16* wrow = wt + (int64_t)(jt0 + kb0 + row) * kWtRow + (lane >> 5) * 8;
+                    f32x16 a0 = f32x16{}, a1 = f32x16{};
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) {
+                        bf16x8 ah = {}, al = {};
+                        if (valid) {
+                            ah = *reinterpret_cast<const bf16x8*>(wrow + s * 16);
+                            al = *reinterpret_cast<const bf16x8*>(wrow + 64 + s * 16);
+                        }
+                        a0 = mfma3_32x32x16(ah, al, sm.bhi[s][0][lane], sm.blo[s][0][lane], a0);
+                        a1 = mfma3_32x32x16(ah, al, sm.bhi[s][1][lane], sm.blo[s][1][lane], a1);
+                    }
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int k = rb * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+                        const int lr = k < nb ? sm.rmap[k] : -1;
+                        if (lr >= 0) {
+                            sm.acc[lr][lane & 31] += a0[i];
+                            sm.acc[lr][32 + (lane & 31)] += a1[i];
+                        }
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        // one partial row per (region, Gaussian) pair, at the pair's G->R slot
+        const int cw = min(kBrCc, C - c0);
+        for (int k = threadIdx.x; k < nrows * kBrCc; k += kBrThreads) {
+            const int r = k / kBrCc, c = k % kBrCc;
+            if (c < cw) gpart[(int64_t)r_pairs[jr0 + rg0 + r] * C + c0 + c] = sm.acc[r][c];
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Phase C: per Gaussian, fixed-order sums of the geometric partials and the region rows.
 // ------------------------------------------------------------------------------------------
 constexpr int kBgThreads = 256;
 
 __global__ void __launch_bounds__(kBgThreads) k_bwd_gauss(
-    Grid G, int n, int C, int M, const float* __restrict__ gF, const float* __restrict__ means,
-    const float* __restrict__ opacity, const float* __restrict__ cov_inv,
-    const int* __restrict__ lb, const int* __restrict__ ub, const int* __restrict__ g2t_offsets,
-    const float* __restrict__ density, const float* __restrict__ pair_partials,
-    float* __restrict__ grad_means, float* __restrict__ grad_cov, float* __restrict__ grad_opacity,
-    float* __restrict__ grad_features) {
+    int n, int C, int M, int MR, const int* __restrict__ g2t_offsets,
+    const float* __restrict__ pair_partials, const int* __restrict__ g2r_offsets,
+    const float* __restrict__ gpart, float* __restrict__ grad_means, float* __restrict__ grad_cov,
+    float* __restrict__ grad_opacity, float* __restrict__ grad_features) {
     __shared__ float red[4][kNumGrads];
-    __shared__ float coef[kBgThreads];
-    __shared__ int vrow[kBgThreads];
     const int g = blockIdx.x;
     if (g >= n) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-
-    // 1. geometric gradients: fixed-order sum of this Gaussian's pair partials
     const int p0 = min(max(g2t_offsets[g], 0), M), p1 = min(max(g2t_offsets[g + 1], p0), M);
     float gr[kNumGrads] = {};
     for (int p = p0 + threadIdx.x; p < p1; p += kBgThreads) {
@@ -290,68 +528,108 @@ __global__ void __launch_bounds__(kBgThreads) k_bwd_gauss(
         for (int k = 0; k < kNumGrads; ++k) tot[k] = ((red[0][k] + red[1][k]) + red[2][k]) + red[3][k];
         write_grads(tot, g, grad_means, grad_cov, grad_opacity);
     }
-
-    // 2. d f_g = sum_v gF_v w_gv / max(D_v, eps) over the voxels of the box
-    GaussParams p;
-    load_params(p, g, means, cov_inv, opacity, lb, ub);
-    const int ex = p.ub[0] - p.lb[0] + 1, ey = p.ub[1] - p.lb[1] + 1, ez = p.ub[2] - p.lb[2] + 1;
-    const int nv = (ex > 0 && ey > 0 && ez > 0) ? ex * ey * ez : 0;
-    const int eyz = ey * ez;
-    const bool vec = (C & 3) == 0;
-    for (int cb = 0; cb < C; cb += 4 * kBgThreads) {
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-        const int c = cb + threadIdx.x * 4;
-        for (int vb = 0; vb < nv; vb += kBgThreads) {
-            __syncthreads();
-            const int i = vb + threadIdx.x;
-            if (i < nv) {
-                const int ix = i / eyz, r = i - ix * eyz;
-                const int iy = r / ez, iz = r - iy * ez;
-                const int x = p.lb[0] + ix, y = p.lb[1] + iy, z = p.lb[2] + iz;
-                float qx, qy, qz;
-                const float e = eval_gauss(p, centre(G, 0, x), centre(G, 1, y), centre(G, 2, z), qx, qy, qz);
-                const int64_t v = voxel_index(G, x, y, z);
-                coef[threadIdx.x] = p.o * e / fmaxf(density[v], kEps);
-                vrow[threadIdx.x] = (int)v;
+    const int r0 = min(max(g2r_offsets[g], 0), MR), r1 = min(max(g2r_offsets[g + 1], r0), MR);
+    float* out = grad_features + (int64_t)g * C;
+    if ((C & 3) == 0) {
+        for (int c = threadIdx.x * 4; c < C; c += kBgThreads * 4) {
+            float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int r = r0; r < r1; ++r) {
+                const float4 v = *reinterpret_cast<const float4*>(gpart + (int64_t)r * C + c);
+                s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
             }
-            __syncthreads();
-            const int cnt = min(kBgThreads, nv - vb);
-            if (c < C) {
-                if (vec) {
-                    for (int k = 0; k < cnt; ++k) {
-                        const float4 x = *reinterpret_cast<const float4*>(gF + (int64_t)vrow[k] * C + c);
-                        const float cf = coef[k];
-                        acc.x += cf * x.x; acc.y += cf * x.y; acc.z += cf * x.z; acc.w += cf * x.w;
-                    }
-                } else {
-                    for (int k = 0; k < cnt; ++k) {
-                        const float* row = gF + (int64_t)vrow[k] * C + c;
-                        const float cf = coef[k];
-                        acc.x += cf * row[0];
-                        if (c + 1 < C) acc.y += cf * row[1];
-                        if (c + 2 < C) acc.z += cf * row[2];
-                        if (c + 3 < C) acc.w += cf * row[3];
-                    }
-                }
-            }
+            *reinterpret_cast<float4*>(out + c) = s;
         }
-        if (c < C) {
-            float* o = grad_features + (int64_t)g * C + c;
-            o[0] = acc.x;
-            if (c + 1 < C) o[1] = acc.y;
-            if (c + 2 < C) o[2] = acc.z;
-            if (c + 3 < C) o[3] = acc.w;
+    } else {
+        for (int c = threadIdx.x; c < C; c += kBgThreads) {
+            float s = 0.0f;
+            for (int r = r0; r < r1; ++r) s += gpart[(int64_t)r * C + c];
+            out[c] = s;
         }
     }
 }
 
-size_t backward_feats_workspace(const Grid& G, int n, int C, int64_t M) {
-    (void)n; (void)C;
-    const int64_t V = (int64_t)G.dims[0] * G.dims[1] * G.dims[2];
-    Carver c(nullptr, (size_t)-1);
-    c.take<float>(V > 0 ? V : 1);                       // t_v
-    c.take<float>((M > 0 ? M : 1) * kNumGrads);         // pair partials
-    return c.off + 256;
+// ------------------------------------------------------------------------------------------
+// Host side
+// ------------------------------------------------------------------------------------------
+static int padded_channels(int C) { return (C + 15) & ~15; }
+
+struct PlanBufs {
+    int* g2r_offsets;
+    long long* total;
+    void* scan_ws;
+    size_t bytes;
+};
+
+static PlanBufs carve_plan(void* ws, int n) {
+    Carver c(ws, (size_t)-1);
+    PlanBufs b;
+    b.g2r_offsets = c.take<int>(n + 1);
+    b.total = c.take<long long>(1);
+    b.scan_ws = c.take<char>(scan_workspace(n > 0 ? n : 1));
+    b.bytes = c.off + 256;
+    return b;
+}
+
+size_t backward_plan_workspace(int n) { return carve_plan(nullptr, n).bytes; }
+
+hipError_t backward_plan(const Grid& G, int n, const int* lb, const int* ub, void* plan_ws,
+                         long long* num_region_pairs, hipStream_t s) {
+    const Regions RG = make_regions(G);
+    const PlanBufs b = carve_plan(plan_ws, n);
+    hipError_t e = launch_cell_count(n, lb, ub, RG.cell, b.g2r_offsets, s);
+    if (e != hipSuccess) return e;
+    long long MR = 0;
+    if (n > 0) {
+        e = scan_i32(b.g2r_offsets + 1, b.g2r_offsets + 1, n, true, b.total, b.scan_ws, s);
+        if (e != hipSuccess) return e;
+        e = hipMemcpyAsync(&MR, b.total, sizeof(long long), hipMemcpyDeviceToHost, s);
+        if (e != hipSuccess) return e;
+    }
+    e = hipStreamSynchronize(s);
+    *num_region_pairs = MR;
+    return e;
+}
+
+struct FeatBufs {
+    __bf16* fhi;
+    __bf16* flo;
+    float* partials;
+    __bf16* wt;
+    int* r_cells;
+    int* r_pairs;
+    int* r_gauss;
+    int* r_cells_sorted;
+    int* r_pairs_sorted;
+    int* roff;
+    void* sort_ws;
+    float* gpart;
+    size_t bytes;
+};
+
+static FeatBufs carve_feats(void* ws, const Grid& G, int n, int C, int64_t M, int64_t MR) {
+    const Regions RG = make_regions(G);
+    const int Cp = padded_channels(C);
+    const int64_t m = M > 0 ? M : 1, mr = MR > 0 ? MR : 1;
+    Carver c(ws, (size_t)-1);
+    FeatBufs b;
+    b.fhi = c.take<__bf16>((int64_t)(n > 0 ? n : 1) * Cp);
+    b.flo = c.take<__bf16>((int64_t)(n > 0 ? n : 1) * Cp);
+    b.partials = c.take<float>(m * kNumGrads);
+    b.wt = c.take<__bf16>(m * kWtRow);
+    b.r_cells = c.take<int>(mr);
+    b.r_pairs = c.take<int>(mr);
+    b.r_gauss = c.take<int>(mr);
+    b.r_cells_sorted = c.take<int>(mr);
+    b.r_pairs_sorted = c.take<int>(mr);
+    b.roff = c.take<int>(RG.total + 1);
+    b.sort_ws = c.take<char>(sort_workspace(MR, RG.total));
+    b.gpart = c.take<float>(mr * (C > 0 ? C : 1));
+    b.bytes = c.off + 256;
+    return b;
+}
+
+size_t backward_feats_workspace(const Grid& G, int n, int C, int64_t M, int64_t MR) {
+    return carve_feats(nullptr, G, n, C, M, MR).bytes;
 }
 
 hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_density,
@@ -360,26 +638,46 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
                                  const int* g2t_offsets, int64_t M, const int* tile_offsets,
                                  const int* sorted_gauss, const float* density,
                                  const float* grid_feats, const float* features,
-                                 float* grad_means, float* grad_cov, float* grad_opacity,
-                                 float* grad_features, void* ws, hipStream_t s) {
+                                 const void* plan_ws, int64_t MR, float* grad_means, float* grad_cov,
+                                 float* grad_opacity, float* grad_features, void* ws, hipStream_t s) {
     if (n <= 0) return hipSuccess;
-    const int64_t V = (int64_t)G.dims[0] * G.dims[1] * G.dims[2];
+    const Regions RG = make_regions(G);
     const int T = G.tiles[0] * G.tiles[1] * G.tiles[2];
-    Carver cv(ws, (size_t)-1);
-    float* tv = cv.take<float>(V > 0 ? V : 1);
-    float* partials = cv.take<float>((M > 0 ? M : 1) * kNumGrads);
-    if (V > 0)
-        G2V_LAUNCH(k_voxel_dot, dim3((unsigned)ceil_div(V, 4)), dim3(256), 0, s, V, C,
-                           grad_feats, grid_feats, density, tv);
+    const int Cp = padded_channels(C);
+    const FeatBufs b = carve_feats(ws, G, n, C, M, MR);
+    const PlanBufs pb = carve_plan(const_cast<void*>(plan_ws), n);
+    hipError_t e;
+
+    // features as bf16 hi/lo rows (B operand of phase A)
+    const int64_t fcount = (int64_t)n * Cp;
+    G2V_LAUNCH(k_split_rows, dim3((unsigned)ceil_div(fcount, 256)), dim3(256), 0, s, features, (int64_t)n, C, Cp,
+               b.fhi, b.flo);
     if (M > 0 && T > 0) {
         const int blocks = (int)ceil_div(T, 8) * 8;
-        G2V_LAUNCH(k_bwd_tile, dim3(blocks), dim3(kBtThreads), 0, s, G, C, grad_density,
-                           grad_feats, means, opacity, cov_inv, lb, ub, g2t_offsets, tile_offsets,
-                           sorted_gauss, (int)M, density, (const float*)tv, features, partials);
+        G2V_LAUNCH(k_bwd_tile, dim3(blocks), dim3(kBtThreads), 0, s, G, C, Cp, grad_density, grad_feats, means,
+                   opacity, cov_inv, lb, ub, g2t_offsets, tile_offsets, sorted_gauss, (int)M, density,
+                   grid_feats, (const __bf16*)b.fhi, (const __bf16*)b.flo, b.partials, b.wt);
     }
-    G2V_LAUNCH(k_bwd_gauss, dim3(n), dim3(kBgThreads), 0, s, G, n, C, (int)M, grad_feats, means,
-                       opacity, cov_inv, lb, ub, g2t_offsets, density, (const float*)partials,
-                       grad_means, grad_cov, grad_opacity, grad_features);
+    // Region -> Gaussian CSR (pairs carry their G->R slot so partial rows land Gaussian-major)
+    if (MR > 0) {
+        e = launch_fill_cells(n, lb, ub, pb.g2r_offsets, RG.cell, RG.n, b.r_cells, b.r_pairs, b.r_gauss, s);
+        if (e != hipSuccess) return e;
+        e = radix_sort_pairs(b.r_cells, b.r_pairs, b.r_cells_sorted, b.r_pairs_sorted, MR, RG.total, b.sort_ws, s);
+        if (e != hipSuccess) return e;
+    }
+    e = launch_tile_offsets(b.r_cells_sorted, MR, RG.total, b.roff, s);
+    if (e != hipSuccess) return e;
+    if (MR > 0 && M > 0) {
+        const int nchunk = (C + kBrCc - 1) / kBrCc;
+        const int64_t items = (int64_t)RG.total * nchunk;
+        const int blocks = (int)ceil_div(items, 8) * 8;
+        G2V_LAUNCH(k_bwd_region, dim3(blocks), dim3(kBrThreads), 0, s, G, RG, C, nchunk, grad_feats, tile_offsets,
+                   sorted_gauss, (int)M, (const int*)b.roff, (const int*)b.r_pairs_sorted,
+                   (const int*)b.r_gauss, (int)MR, (const __bf16*)b.wt, b.gpart);
+    }
+    G2V_LAUNCH(k_bwd_gauss, dim3(n), dim3(kBgThreads), 0, s, n, C, (int)M, (int)MR, g2t_offsets,
+               (const float*)b.partials, (const int*)pb.g2r_offsets, (const float*)b.gpart, grad_means,
+               grad_cov, grad_opacity, grad_features);
     return hipGetLastError();
 }
 

@@ -205,14 +205,39 @@ int g2v_forward_splat(int n, int feat_dim, const float* means3D, const float* op
     return G2V_OK;
 }
 
-size_t g2v_backward_workspace(int n, int feat_dim, long long num_pairs, const float voxel_size[3],
-                              const float voxel_range[6]) {
+size_t g2v_backward_plan_workspace(int n) { return backward_plan_workspace(n > 0 ? n : 0); }
+
+int g2v_backward_plan(int n, int feat_dim, const float voxel_size[3], const float voxel_range[6],
+                      const int* valid_voxel_lb, const int* valid_voxel_ub, void* plan_workspace,
+                      size_t plan_workspace_bytes, long long* num_region_pairs, void* stream) {
+    g_err[0] = 0;
+    if (n < 0 || feat_dim < 0) return fail(G2V_ERR_INVALID, "n = %d, feat_dim = %d", n, feat_dim);
+    if (!num_region_pairs) return fail(G2V_ERR_INVALID, "num_region_pairs is null");
+    *num_region_pairs = 0;
+    if (n == 0 || feat_dim == 0) return G2V_OK;
+    if (!valid_voxel_lb || !valid_voxel_ub) return fail(G2V_ERR_INVALID, "null box pointer");
+    Grid G;
+    int rc = make_grid(voxel_size, voxel_range, G);
+    if (rc != G2V_OK) return rc;
+    rc = check_ws(plan_workspace, plan_workspace_bytes, backward_plan_workspace(n), "backward plan");
+    if (rc != G2V_OK) return rc;
+    long long MR = 0;
+    G2V_HIP(backward_plan(G, n, valid_voxel_lb, valid_voxel_ub, plan_workspace, &MR,
+                          static_cast<hipStream_t>(stream)));
+    if (MR > 2147483647ll)
+        return fail(G2V_ERR_LIMIT, "%lld region-Gaussian pairs exceed the int32 CSR", MR);
+    *num_region_pairs = MR;
+    return G2V_OK;
+}
+
+size_t g2v_backward_workspace(int n, int feat_dim, long long num_pairs, long long num_region_pairs,
+                              const float voxel_size[3], const float voxel_range[6]) {
     Grid G;
     if (make_grid(voxel_size, voxel_range, G) != G2V_OK) return 0;
     if (feat_dim <= 0) return 256;
     Carver c(nullptr, (size_t)-1);
     c.take<char>(carve_splat(nullptr, n, num_pairs, G).bytes);
-    c.take<char>(backward_feats_workspace(G, n, feat_dim, num_pairs));
+    c.take<char>(backward_feats_workspace(G, n, feat_dim, num_pairs, num_region_pairs));
     return c.off + 256;
 }
 
@@ -221,21 +246,24 @@ int g2v_backward(int n, int feat_dim, const float* grad_density, const float* gr
                  const float voxel_size[3], const float voxel_range[6], const int* valid_voxel_lb,
                  const int* valid_voxel_ub, const int* num_voxels_per_gaussian,
                  const int* g2t_offsets, const int* g2t_tile_ids, long long num_pairs,
-                 const float* density, const float* grid_feats, const float* features,
-                 float* grad_means, float* grad_cov, float* grad_opacity, float* grad_features,
-                 void* workspace, size_t workspace_bytes, void* stream) {
+                 long long num_region_pairs, const float* density, const float* grid_feats,
+                 const float* features, float* grad_means, float* grad_cov, float* grad_opacity,
+                 float* grad_features, const void* plan_workspace, void* workspace,
+                 size_t workspace_bytes, void* stream) {
     g_err[0] = 0;
     (void)num_voxels_per_gaussian;
-    if (n < 0 || feat_dim < 0 || num_pairs < 0)
-        return fail(G2V_ERR_INVALID, "n = %d, feat_dim = %d, num_pairs = %lld", n, feat_dim, num_pairs);
-    if (num_pairs > 2147483647ll) return fail(G2V_ERR_LIMIT, "num_pairs = %lld exceeds int32", num_pairs);
+    if (n < 0 || feat_dim < 0 || num_pairs < 0 || num_region_pairs < 0)
+        return fail(G2V_ERR_INVALID, "n = %d, feat_dim = %d, num_pairs = %lld, num_region_pairs = %lld", n,
+                    feat_dim, num_pairs, num_region_pairs);
+    if (num_pairs > 2147483647ll || num_region_pairs > 2147483647ll)
+        return fail(G2V_ERR_LIMIT, "pair counts exceed int32");
     if (n == 0) return G2V_OK;
     if (!grad_density || !means3D || !opacity || !cov_inv || !valid_voxel_lb || !valid_voxel_ub ||
         !grad_means || !grad_cov || !grad_opacity)
         return fail(G2V_ERR_INVALID, "null input/output pointer");
     if (feat_dim > 0 && (!grad_feats || !grid_feats || !features || !grad_features || !density ||
-                         !g2t_offsets || (num_pairs > 0 && !g2t_tile_ids)))
-        return fail(G2V_ERR_INVALID, "feat_dim = %d needs the feature tensors, density and the CSR", feat_dim);
+                         !g2t_offsets || !plan_workspace || (num_pairs > 0 && !g2t_tile_ids)))
+        return fail(G2V_ERR_INVALID, "feat_dim = %d needs the feature tensors, density, the CSR and the plan workspace", feat_dim);
     Grid G;
     int rc = make_grid(voxel_size, voxel_range, G);
     if (rc != G2V_OK) return rc;
@@ -246,11 +274,12 @@ int g2v_backward(int n, int feat_dim, const float* grad_density, const float* gr
         return G2V_OK;
     }
     rc = check_ws(workspace, workspace_bytes,
-                  g2v_backward_workspace(n, feat_dim, num_pairs, voxel_size, voxel_range), "backward");
+                  g2v_backward_workspace(n, feat_dim, num_pairs, num_region_pairs, voxel_size, voxel_range),
+                  "backward");
     if (rc != G2V_OK) return rc;
     Carver c(workspace, workspace_bytes);
     void* splat_ws = c.take<char>(carve_splat(nullptr, n, num_pairs, G).bytes);
-    void* feats_ws = c.take<char>(backward_feats_workspace(G, n, feat_dim, num_pairs));
+    void* feats_ws = c.take<char>(backward_feats_workspace(G, n, feat_dim, num_pairs, num_region_pairs));
     const SplatBufs b = carve_splat(splat_ws, n, num_pairs, G);
     rc = build_t2g(G, n, valid_voxel_lb, valid_voxel_ub, g2t_offsets, nullptr, g2t_tile_ids,
                    num_pairs, b, s);
@@ -258,7 +287,8 @@ int g2v_backward(int n, int feat_dim, const float* grad_density, const float* gr
     G2V_HIP(launch_backward_feats(G, n, feat_dim, grad_density, grad_feats, means3D, opacity, cov_inv,
                                   valid_voxel_lb, valid_voxel_ub, g2t_offsets, num_pairs,
                                   b.tile_offsets, b.sorted_gauss, density, grid_feats, features,
-                                  grad_means, grad_cov, grad_opacity, grad_features, feats_ws, s));
+                                  plan_workspace, num_region_pairs, grad_means, grad_cov, grad_opacity,
+                                  grad_features, feats_ws, s));
     return G2V_OK;
 }
 

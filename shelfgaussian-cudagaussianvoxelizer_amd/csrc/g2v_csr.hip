@@ -230,6 +230,66 @@ hipError_t launch_fill_g2t(const Grid& G, int n, const int* lb, const int* ub,
 }
 
 // ------------------------------------------------------------------------------------------
+// Cells: coarser boxes of `cell` voxels per axis (the backward's regions of 2x2xRZ tiles).
+// k_cell_count writes each Gaussian's cell count to offsets[g+1] (offsets[0] = 0);
+// k_fill_cells enumerates each Gaussian's cell box row-major like k_fill_g2t and also writes
+// the pair index of every entry (the value the sort carries).
+// ------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) k_cell_count(int n, const int* __restrict__ lb,
+                                                    const int* __restrict__ ub, int cx, int cy, int cz,
+                                                    int* __restrict__ offsets) {
+    const int g = blockIdx.x * 256 + threadIdx.x;
+    if (g == 0) offsets[0] = 0;
+    if (g >= n) return;
+    const int ex = ub[g * 3] / cx - lb[g * 3] / cx + 1;
+    const int ey = ub[g * 3 + 1] / cy - lb[g * 3 + 1] / cy + 1;
+    const int ez = ub[g * 3 + 2] / cz - lb[g * 3 + 2] / cz + 1;
+    const bool empty = ub[g * 3] < lb[g * 3] || ub[g * 3 + 1] < lb[g * 3 + 1] || ub[g * 3 + 2] < lb[g * 3 + 2];
+    offsets[g + 1] = empty ? 0 : ex * ey * ez;
+}
+
+__global__ void __launch_bounds__(256) k_fill_cells(int n, const int* __restrict__ lb,
+                                                    const int* __restrict__ ub,
+                                                    const int* __restrict__ offsets, int cx, int cy,
+                                                    int cz, int ny, int nz, int* __restrict__ cell_ids,
+                                                    int* __restrict__ pair_ids,
+                                                    int* __restrict__ gauss_ids) {
+    const int lane = threadIdx.x & 63;
+    const int g = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (g >= n) return;
+    const int base = offsets[g];
+    const int cnt = offsets[g + 1] - base;
+    if (cnt <= 0) return;
+    const int x0 = lb[g * 3] / cx, y0 = lb[g * 3 + 1] / cy, z0 = lb[g * 3 + 2] / cz;
+    const int dy = ub[g * 3 + 1] / cy - y0 + 1;
+    const int dz = ub[g * 3 + 2] / cz - z0 + 1;
+    const int dyz = dy * dz;
+    for (int i = lane; i < cnt; i += 64) {
+        const int lx = i / dyz, r = i - lx * dyz;
+        const int ly = r / dz, lz = r - ly * dz;
+        cell_ids[base + i] = ((x0 + lx) * ny + (y0 + ly)) * nz + (z0 + lz);
+        pair_ids[base + i] = base + i;
+        gauss_ids[base + i] = g;
+    }
+}
+
+hipError_t launch_cell_count(int n, const int* lb, const int* ub, const int cell[3], int* offsets,
+                             hipStream_t s) {
+    G2V_LAUNCH(k_cell_count, dim3((unsigned)ceil_div(n > 0 ? n : 1, 256)), dim3(256), 0, s, n, lb, ub,
+               cell[0], cell[1], cell[2], offsets);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_cells(int n, const int* lb, const int* ub, const int* offsets, const int cell[3],
+                             const int ncells[3], int* cell_ids, int* pair_ids, int* gauss_ids,
+                             hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    G2V_LAUNCH(k_fill_cells, dim3((unsigned)ceil_div(n, 4)), dim3(256), 0, s, n, lb, ub, offsets, cell[0],
+               cell[1], cell[2], ncells[1], ncells[2], cell_ids, pair_ids, gauss_ids);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------------
 // Stable LSD radix sort, digits of <= 8 bits, only ceil(log2 T) key bits.
 //   per pass: k_radix_hist (digit counts per 4096-key block, digit-major) -> exclusive scan
 //             -> k_radix_scatter (stable rank: ballot match inside a wave, LDS across waves)

@@ -45,6 +45,12 @@ hipError_t launch_boxes(const Grid& G, int n, const float* means, const float* c
 hipError_t launch_fill_g2t(const Grid& G, int n, const int* lb, const int* ub,
                            const int* g2t_offsets, int* tile_ids, int* gauss_ids, hipStream_t s);
 
+hipError_t launch_cell_count(int n, const int* lb, const int* ub, const int cell[3], int* offsets,
+                             hipStream_t s);
+hipError_t launch_fill_cells(int n, const int* lb, const int* ub, const int* offsets, const int cell[3],
+                             const int ncells[3], int* cell_ids, int* pair_ids, int* gauss_ids,
+                             hipStream_t s);
+
 int sort_key_bits(int num_tiles);
 size_t sort_workspace(int64_t M, int num_tiles);
 // Stable LSD radix sort of (key < num_tiles, value) pairs.  Inputs are not modified; the
@@ -72,15 +78,19 @@ hipError_t launch_backward_density(const Grid& G, int n, const float* grad_densi
                                    const float* means, const float* opacity, const float* cov_inv,
                                    const int* lb, const int* ub, float* grad_means, float* grad_cov,
                                    float* grad_opacity, hipStream_t s);
-size_t backward_feats_workspace(const Grid& G, int n, int C, int64_t M);
+size_t backward_plan_workspace(int n);
+// Counts the (region, Gaussian) pairs of the feature-gradient phase; synchronises the stream.
+hipError_t backward_plan(const Grid& G, int n, const int* lb, const int* ub, void* plan_ws,
+                         long long* num_region_pairs, hipStream_t s);
+size_t backward_feats_workspace(const Grid& G, int n, int C, int64_t M, int64_t MR);
 hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_density,
                                  const float* grad_feats, const float* means, const float* opacity,
                                  const float* cov_inv, const int* lb, const int* ub,
                                  const int* g2t_offsets, int64_t M, const int* tile_offsets,
                                  const int* sorted_gauss, const float* density,
                                  const float* grid_feats, const float* features,
-                                 float* grad_means, float* grad_cov, float* grad_opacity,
-                                 float* grad_features, void* ws, hipStream_t s);
+                                 const void* plan_ws, int64_t MR, float* grad_means, float* grad_cov,
+                                 float* grad_opacity, float* grad_features, void* ws, hipStream_t s);
 
 // Brackets one kernel launch with HIP events when profiling is enabled (g2v_profile.hip).
 class ProfMark {

@@ -75,8 +75,8 @@ def test_invalid_arguments_fail_before_any_launch():
     # features requested without tensors
     rc = lib.g2v_backward(4, 8, ctypes.c_void_p(16), None, ctypes.c_void_p(16), ctypes.c_void_p(16),
                           ctypes.c_void_p(16), vs, vr, ctypes.c_void_p(16), ctypes.c_void_p(16), None,
-                          None, None, 0, None, None, None, ctypes.c_void_p(16), ctypes.c_void_p(16),
-                          ctypes.c_void_p(16), None, None, 0, None)
+                          None, None, 0, 0, None, None, None, ctypes.c_void_p(16), ctypes.c_void_p(16),
+                          ctypes.c_void_p(16), None, None, None, 0, None)
     assert rc == 1 and b"feat_dim" in lib.g2v_last_error()
 
 
@@ -87,7 +87,8 @@ def test_workspace_queries_grow_with_problem():
     a = lib.g2v_forward_splat_workspace(1000, 10_000, vs, vr)
     b = lib.g2v_forward_splat_workspace(1000, 1_000_000, vs, vr)
     assert 0 < a < b
-    assert lib.g2v_backward_workspace(1000, 64, 10_000, vs, vr) > lib.g2v_backward_workspace(1000, 0, 10_000, vs, vr)
+    assert lib.g2v_backward_workspace(1000, 64, 10_000, 2000, vs, vr) > lib.g2v_backward_workspace(1000, 0, 10_000, 0, vs, vr)
+    assert lib.g2v_backward_workspace(1000, 64, 10_000, 4000, vs, vr) > lib.g2v_backward_workspace(1000, 64, 10_000, 2000, vs, vr)
     assert lib.g2v_forward_plan_workspace(200_000) > lib.g2v_forward_plan_workspace(10)
 
 
