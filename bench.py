@@ -49,20 +49,35 @@ def parse():
     return ap.parse_args()
 
 
-def algorithmic_bytes(N, C, V, M, T):
-    """Compulsory HBM bytes per step: every input read once, every output written once."""
+def algorithmic_bytes(N, C, V, M, T, MR):
+    """Compulsory HBM bytes per step (every input read once, every output written once) and, per
+    kernel, the bytes its own inputs and outputs take when each is moved once.  The intermediates
+    of the feature backward count for the kernels that produce and consume them: the split pair
+    weights (256 B per G->T pair) and the partial feature-gradient rows (C floats per
+    (region, Gaussian) pair)."""
     fwd = 4 * (13 * N + N * C + V + V * C + (N + 1) + M + 16 * N)
     bwd = 4 * (2 * V + V * C + N * C + 4 * N + 16 * N + (N + 1) + M + 13 * N + N * C)
-    # per-kernel algorithmic bytes (inputs it must read + outputs it must write)
+    params = 4 * 19 * N                      # means, opacity, cov_inv, lb, ub
     per_kernel = {
-        "k_fwd_feats": 4 * (N * C + 19 * N + (T + 1) + M + V + V * C),
-        "k_fwd_density": 4 * (19 * N + (T + 1) + M + V),
-        "k_voxel_dot": 4 * (2 * V * C + 2 * V),
-        "k_bwd_tile": 4 * (V * C + N * C + 3 * V + 19 * N + (N + 1) + (T + 1) + M + 10 * M),
-        "k_bwd_gauss": 4 * (V * C + V + 10 * M + 19 * N + (N + 1) + 13 * N + N * C),
-        "k_bwd_density": 4 * (V + 19 * N + 13 * N),
+        "k_fwd_feats": 4 * (N * C + (T + 1) + M + V + V * C) + params,
+        "k_fwd_density": 4 * ((T + 1) + M + V) + params,
+        "k_bwd_tile": 4 * (V * C + N * C + 2 * V + (N + 1) + (T + 1) + M + 10 * M) + 256 * M + params,
+        "k_bwd_region": 4 * (V * C + (T + 1) + M + 2 * MR + MR * C) + 256 * M,
+        "k_bwd_gauss": 4 * (10 * M + MR * C + 2 * (N + 1) + 13 * N + N * C),
+        "k_bwd_density": 4 * (V + 13 * N) + params,
     }
     return fwd, bwd, per_kernel
+
+
+def region_pairs(lb, ub, tiles_z):
+    """Number of (region, Gaussian) pairs of the feature backward (regions of 8x8x(4*min(Tz,4)) voxels)."""
+    import numpy as np
+    cell = np.array([8, 8, 4 * min(tiles_z, 4)])
+    lb = np.asarray(lb, np.int64)
+    ub = np.asarray(ub, np.int64)
+    ok = (ub >= lb).all(axis=1)
+    ext = ub // cell - lb // cell + 1
+    return int(np.where(ok, ext.prod(axis=1), 0).sum())
 
 
 def cpu_baseline(w, host, gpu_out, frac):
@@ -167,7 +182,8 @@ def main():
     T = Tx * Ty * Tz
     M = int(out[7].numel())
     P = int(out[4].to(torch.int64).sum().item())         # in-box (Gaussian, voxel) pairs
-    fwd_b, bwd_b, per_kernel = algorithmic_bytes(N, C, V, M, T)
+    MR = region_pairs(out[2].cpu().numpy(), out[3].cpu().numpy(), Tz) if C else 0
+    fwd_b, bwd_b, per_kernel = algorithmic_bytes(N, C, V, M, T, MR)
     gbps = (fwd_b + bwd_b) / (ms * 1e-3) / 1e9
 
     if args.copy_probe_mib > 0:   # a plain copy of known size, the scale of the PMC byte counters
@@ -216,7 +232,7 @@ def main():
         "dtype": "f32", "compute": "fp32 in/out; contractions as 3-term bf16-split MFMA with fp32 accumulation",
         "data": "synthetic (tests/workloads.py, seed 0; upstream grads per config)",
         "config": {"workload": w.name, "n_gaussians": N, "feat_dim": C, "grid": [X, Y, Z], "tiles": [Tx, Ty, Tz],
-                   "g2t_pairs": M, "inbox_pairs": P, "upstream_grads": w.grads},
+                   "g2t_pairs": M, "region_pairs": MR, "inbox_pairs": P, "upstream_grads": w.grads},
         "fwd_ms": round(fwd_s * 1e3 / args.steps, 4), "bwd_ms": round(bwd_s * 1e3 / args.steps, 4),
         "hbm_gbps": round(gbps, 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
         "compulsory_bytes": fwd_b + bwd_b,

@@ -57,7 +57,7 @@ int g2v_forward_plan(int n, const float* means3D, const float* covariances,
  * density and, when feat_dim > 0, of the density-weighted feature average (reference
  * .cu:1634-1904).  density (X,Y,Z) and grid_feats (X,Y,Z,feat_dim) are written completely;
  * features may be NULL when feat_dim == 0.  Asynchronous. */
-size_t g2v_forward_splat_workspace(int n, long long num_pairs, const float voxel_size[3],
+size_t g2v_forward_splat_workspace(int n, int feat_dim, long long num_pairs, const float voxel_size[3],
                                    const float voxel_range[6]);
 int g2v_forward_splat(int n, int feat_dim, const float* means3D, const float* opacity,
                       const float* features, const float voxel_size[3], const float voxel_range[6],

@@ -128,7 +128,7 @@ def gaussian_voxelizer_forward(means3D, opacity, covariances, voxel_size, voxel_
         g2t_tile_ids = torch.empty(M, **i32)
         density = torch.empty(X, Y, Z, **f32)
         grid_feats = torch.empty(X, Y, Z, C, **f32)
-        ws2 = torch.empty(lib.g2v_forward_splat_workspace(n, M, vs, vr), dtype=torch.uint8, device=dev)
+        ws2 = torch.empty(lib.g2v_forward_splat_workspace(n, C, M, vs, vr), dtype=torch.uint8, device=dev)
         _lib.check(lib.g2v_forward_splat(n, C, _ptr(means), _ptr(op), _ptr(feats), vs, vr,
                                          _ptr(cov_inv), _ptr(lb), _ptr(ub), _ptr(g2t_offsets), M,
                                          _ptr(g2t_tile_ids), _ptr(density), _ptr(grid_feats),

@@ -143,16 +143,16 @@ constexpr int kBtKc = 64;                              // channels of G staged p
 constexpr int kWtRow = 128;                            // bf16 per pair: 64 hi then 64 lo
 
 struct BtSmem {
-    bf16x8 ahi[2][kBtKc / 16][2][64];   // A operand (G tile), hi: [buffer][k step][voxel block][lane]
+    bf16x8 ahi[2][kBtKc / 16][2][64];   // A operand (G tile), hi: [buffer][k step][voxel block][slot]
     bf16x8 alo[2][kBtKc / 16][2][64];
     int vlin[64];
     float gD[64], inv[64], tv[64], D[64];
-    int gid[kBtPass];
+    ParamTile<kBtPass> pt;              // parameters of this pass's list entries
     float tpart[kBtGroups][64];
     float xch[2][kBtPass][kNumGrads];
 };
 
-__global__ void __launch_bounds__(kBtThreads, 2) k_bwd_tile(
+__global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
     Grid G, int C, int Cp, const float* __restrict__ gD, const float* __restrict__ gF,
     const float* __restrict__ means, const float* __restrict__ opacity,
     const float* __restrict__ cov_inv, const int* __restrict__ lb, const int* __restrict__ ub,
@@ -198,68 +198,92 @@ __global__ void __launch_bounds__(kBtThreads, 2) k_bwd_tile(
             float s = 0.0f;
             for (int c = lane; c < C; c += 64) s += a[c] * b[c];
             s = wave_sum(s);
-            if (lane == 0) sm.tv[r] = density[v] >= kEps ? s : 0.0f;
+            if (lane == 0) sm.tv[r] = sm.D[r] >= kEps ? s : 0.0f;
         }
     }
+
+    // staging of G chunks: thread = (voxel sv, 8-channel group sq), coalesced 32-byte reads
+    const int sv = threadIdx.x >> 3, sq = threadIdx.x & 7;
+    const int nks = Cp >> 4;                       // K steps of 16 channels
+    const int nchunks = (nks + 3) >> 2;            // 4 K steps per staged chunk
+    auto load_g = [&](int chunk, float (&v8)[8]) {
+        const int srow = sm.vlin[sv];
+        const int c = chunk * kBtKc + sq * 8;
+        const int valid = max(0, min(8, C - c));
+        if (srow >= 0 && valid > 0) load8(gF + (int64_t)srow * C + c, valid, vec_ok, v8);
+        else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v8[i] = 0.0f;
+        }
+    };
+    auto write_g = [&](const float (&v8)[8], int buf) {
+        bf16x8 h, l;
+        split8(v8, h, l);
+        // XOR swizzle of the 16-byte slot: the 8 channel groups of one voxel land in different
+        // LDS banks (the MFMA-side read applies the same permutation)
+        const int s = sq >> 1, L = (sq & 1) * 32 + (sv & 31);
+        const int Ls = L ^ ((2 * s + (sq & 1)) & 15);
+        sm.ahi[buf][s][sv >> 5][Ls] = h;
+        sm.alo[buf][s][sv >> 5][Ls] = l;
+    };
 
     for (int pbase = 0; pbase < Ng; pbase += kBtPass) {
         const int pcount = min(kBtPass, Ng - pbase);
         __syncthreads();
-        for (int k = threadIdx.x; k < kBtPass; k += kBtThreads)
-            sm.gid[k] = k < pcount ? sorted_gauss[j0 + pbase + k] : -1;
-
-        // stage G chunk 0 into buffer 0
-        const int sv = threadIdx.x >> 3, sq = threadIdx.x & 7;   // staging: voxel, 8-channel group
-        const int srow = sm.vlin[sv];
-        auto stage = [&](int chunk, int buf) {
-            const int c = chunk * kBtKc + sq * 8;
+        stage_params(sm.pt, sorted_gauss + j0 + pbase, pcount, means, cov_inv, opacity, lb, ub);
+        {
             float v8[8];
-            const int valid = max(0, min(8, C - c));
-            if (srow >= 0 && valid > 0) load8(gF + (int64_t)srow * C + c, valid, vec_ok, v8);
-            else {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) v8[i] = 0.0f;
-            }
-            bf16x8 h, l;
-            split8(v8, h, l);
-            const int s = sq >> 1, L = (sq & 1) * 32 + (sv & 31);
-            sm.ahi[buf][s][sv >> 5][L] = h;
-            sm.alo[buf][s][sv >> 5][L] = l;
-        };
-        stage(0, 0);
+            load_g(0, v8);
+            write_g(v8, 0);
+        }
         __syncthreads();
 
         f32x16 acc[kBtNbw];
 #pragma unroll
         for (int j = 0; j < kBtNbw; ++j) acc[j] = f32x16{};
         int nact = 0;
-#pragma unroll
-        for (int j = 0; j < kBtNbw; ++j) nact += ((ngrp + kBtGroups * j) * 32 < pcount) ? 1 : 0;
         int gcol[kBtNbw];
 #pragma unroll
-        for (int j = 0; j < kBtNbw; ++j) gcol[j] = sm.gid[(ngrp + kBtGroups * j) * 32 + (lane & 31)];
-
-        const int nchunks = (Cp + kBtKc - 1) / kBtKc;
-        for (int ch = 0; ch < nchunks; ++ch) {
-            const int buf = ch & 1;
-            if (ch + 1 < nchunks) stage(ch + 1, buf ^ 1);
-            const int ksteps = min(kBtKc, Cp - ch * kBtKc) >> 4;
-            for (int s = 0; s < ksteps; ++s) {
-                const int c = ch * kBtKc + s * 16 + (lane >> 5) * 8;
-                const bf16x8 ah = sm.ahi[buf][s][mb][lane];
-                const bf16x8 al = sm.alo[buf][s][mb][lane];
+        for (int j = 0; j < kBtNbw; ++j) {
+            nact += ((ngrp + kBtGroups * j) * 32 < pcount) ? 1 : 0;
+            gcol[j] = sm.pt.gid[(ngrp + kBtGroups * j) * 32 + (lane & 31)];
+        }
+        // B operand (split features of this lane's Gaussians), prefetched one K step ahead
+        bf16x8 bnh[kBtNbw], bnl[kBtNbw];
+        auto load_b = [&](int ks) {
+            const int c = ks * 16 + (lane >> 5) * 8;
 #pragma unroll
-                for (int j = 0; j < kBtNbw; ++j) {
-                    if (j < nact) {
-                        bf16x8 bh = {}, bl = {};
-                        if (gcol[j] >= 0) {
-                            bh = *reinterpret_cast<const bf16x8*>(fhi + (int64_t)gcol[j] * Cp + c);
-                            bl = *reinterpret_cast<const bf16x8*>(flo + (int64_t)gcol[j] * Cp + c);
-                        }
-                        acc[j] = mfma3_32x32x16(ah, al, bh, bl, acc[j]);
-                    }
+            for (int j = 0; j < kBtNbw; ++j) {
+                bnh[j] = bf16x8{};
+                bnl[j] = bf16x8{};
+                if (j < nact && gcol[j] >= 0) {
+                    bnh[j] = *reinterpret_cast<const bf16x8*>(fhi + (int64_t)gcol[j] * Cp + c);
+                    bnl[j] = *reinterpret_cast<const bf16x8*>(flo + (int64_t)gcol[j] * Cp + c);
                 }
             }
+        };
+        load_b(0);
+        for (int ch = 0; ch < nchunks; ++ch) {
+            const int buf = ch & 1;
+            float pre[8];
+            if (ch + 1 < nchunks) load_g(ch + 1, pre);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const int ks = ch * 4 + s;
+                if (ks < nks) {
+                    bf16x8 bh[kBtNbw], bl[kBtNbw];
+#pragma unroll
+                    for (int j = 0; j < kBtNbw; ++j) { bh[j] = bnh[j]; bl[j] = bnl[j]; }
+                    if (ks + 1 < nks) load_b(ks + 1);
+                    const int ls = lane ^ ((2 * s + (lane >> 5)) & 15);
+                    const bf16x8 ah = sm.ahi[buf][s][mb][ls];
+                    const bf16x8 al = sm.alo[buf][s][mb][ls];
+#pragma unroll
+                    for (int j = 0; j < kBtNbw; ++j)
+                        if (j < nact) acc[j] = mfma3_32x32x16(ah, al, bh[j], bl[j], acc[j]);
+                }
+            }
+            if (ch + 1 < nchunks) write_g(pre, buf ^ 1);
             __syncthreads();
         }
 
@@ -273,7 +297,7 @@ __global__ void __launch_bounds__(kBtThreads, 2) k_bwd_tile(
             const int g = (j < nact) ? gcol[j] : -1;
             if (g < 0) continue;
             GaussParams p;
-            load_params(p, g, means, cov_inv, opacity, lb, ub);
+            read_params(sm.pt, slot, p);
             __bf16* wrow = wt + (int64_t)(j0 + pbase + slot) * kWtRow;
 #pragma unroll
             for (int q4 = 0; q4 < 4; ++q4) {
@@ -334,7 +358,7 @@ __global__ void __launch_bounds__(kBtThreads, 2) k_bwd_tile(
             float gr[kNumGrads] = {};
             if (g >= 0) {
                 GaussParams p;
-                load_params(p, g, means, cov_inv, opacity, lb, ub);
+                read_params(sm.pt, slot, p);
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const int r = mb * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
@@ -356,9 +380,9 @@ __global__ void __launch_bounds__(kBtThreads, 2) k_bwd_tile(
         }
         __syncthreads();
         for (int slot = threadIdx.x; slot < pcount; slot += kBtThreads) {
-            const int g = sm.gid[slot];
-            const int tx0 = lb[g * 3] / kTile, ty0 = lb[g * 3 + 1] / kTile, tz0 = lb[g * 3 + 2] / kTile;
-            const int dy = ub[g * 3 + 1] / kTile - ty0 + 1, dz = ub[g * 3 + 2] / kTile - tz0 + 1;
+            const int g = sm.pt.gid[slot];
+            const int tx0 = sm.pt.lb[0][slot] / kTile, ty0 = sm.pt.lb[1][slot] / kTile, tz0 = sm.pt.lb[2][slot] / kTile;
+            const int dy = sm.pt.ub[1][slot] / kTile - ty0 + 1, dz = sm.pt.ub[2][slot] / kTile - tz0 + 1;
             const int64_t pair = (int64_t)g2t_offsets[g] + ((tx - tx0) * dy + (ty - ty0)) * dz + (tz - tz0);
             if (pair < 0 || pair >= M) continue;   // malformed CSR: never write outside the buffer
             float* out = pair_partials + pair * kNumGrads;
@@ -369,26 +393,113 @@ __global__ void __launch_bounds__(kBtThreads, 2) k_bwd_tile(
 }
 
 // ------------------------------------------------------------------------------------------
-// Phase B: per-region partial feature gradients, accumulated in LDS.
+// Region row of every Tile->Gaussian entry: the position of its Gaussian in the (ascending)
+// Gaussian list of the region that holds its tile.
 // ------------------------------------------------------------------------------------------
-constexpr int kBrThreads = 256;   // 4 waves
+__global__ void __launch_bounds__(256) k_region_gids(int MR, const int* __restrict__ r_pairs_sorted,
+                                                     const int* __restrict__ r_gauss,
+                                                     int* __restrict__ r_gids) {
+    const int j = blockIdx.x * 256 + threadIdx.x;
+    if (j < MR) r_gids[j] = r_gauss[r_pairs_sorted[j]];
+}
+
+__global__ void __launch_bounds__(256) k_region_rowmap(Grid G, Regions RG, int M, int MR,
+                                                       const int* __restrict__ sorted_tiles,
+                                                       const int* __restrict__ sorted_gauss,
+                                                       const int* __restrict__ roff,
+                                                       const int* __restrict__ r_gids,
+                                                       int* __restrict__ rowmap) {
+    const int j = blockIdx.x * 256 + threadIdx.x;
+    if (j >= M) return;
+    const int t = sorted_tiles[j], g = sorted_gauss[j];
+    const int tyz = G.tiles[1] * G.tiles[2];
+    const int tx = t / tyz, ty = (t - tx * tyz) / G.tiles[2], tz = t % G.tiles[2];
+    const int tpz = RG.cell[2] / kTile;
+    const int R = ((tx >> 1) * RG.n[1] + (ty >> 1)) * RG.n[2] + tz / tpz;
+    const int a = min(max(roff[R], 0), MR);
+    const int b = min(max(roff[R + 1], a), MR);
+    int lo = a, hi = b;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (r_gids[mid] < g) lo = mid + 1;
+        else hi = mid;
+    }
+    rowmap[j] = (lo < b && r_gids[lo] == g) ? lo - a : -1;
+}
+
+// ------------------------------------------------------------------------------------------
+// Phase B: per-region partial feature gradients, accumulated in LDS.
+//
+// Work item = (region, 64-channel chunk); 8 waves.  The region's tile lists are walked as units
+// of (tile, batch of up to 256 list entries).  Per unit, wave w multiplies row block w of the
+// split pair weights (32 pairs x 64 voxels) by the tile's gF chunk (64 voxels x 64 channels, the
+// B operand in LDS) and adds the 32 x 64 result to the LDS rows of those Gaussians.  Each
+// Gaussian appears once per tile list, so every LDS row has one writer per unit and the sums are
+// deterministic.  Software pipeline, one unit ahead: while unit q is multiplied, the B operand and
+// the row map of unit q+1 are written to the other LDS buffers, the weights of unit q+1 are loaded
+// into registers, and the gF values of unit q+2 are loaded into registers.
+// ------------------------------------------------------------------------------------------
+constexpr int kBrThreads = 512;   // 8 waves
 constexpr int kBrCc = 64;         // channels per work item
-constexpr int kBrRows = 448;      // region rows held in LDS at a time
-constexpr int kBrBatch = 256;     // tile entries mapped to rows at a time (8 row blocks)
+constexpr int kBrRows = 400;      // region rows held in LDS at a time
+constexpr int kBrBatch = 256;     // tile entries per unit: one 32-row block per wave
 constexpr int kBrAccLd = kBrCc + 4;
+constexpr int kBrMaxTiles = 16;   // tiles per region (2 x 2 x up to 4)
 
 struct BrSmem {
-    float acc[kBrRows][kBrAccLd];
-    bf16x8 bhi[4][2][64];          // B operand (G chunk): [k step of 16 voxels][channel block][lane]
-    bf16x8 blo[4][2][64];
-    int rows[kBrRows];             // Gaussian of each local row (ascending)
-    int rmap[kBrBatch];            // tile entry -> local row, -1 outside this row group
+    float acc[kBrRows + 1][kBrAccLd];   // region rows; row kBrRows is a dummy that absorbs
+                                        // the results of padding entries
+    bf16x8 bhi[2][4][2][64];       // B operand (gF chunk): [buffer][k step of 16 voxels][channel block][lane]
+    bf16x8 blo[2][4][2][64];
+    alignas(16) int rmap[2][kBrBatch];   // unit entry -> local row, kBrRows if it has none
+    int rslot[kBrRows];            // G->R slot of each local row (where its partial row goes)
+    int tl_t[kBrMaxTiles], tl_j[kBrMaxTiles], tl_n[kBrMaxTiles];
+    int ntl;
+    int nunits;                    // units (tile list slices of kBrBatch entries) of the region
 };
+
+// gF values of one tile for the staging thread (channel c, voxel octet o): voxels o*8 .. o*8+7.
+// The loads are unconditional (indices clamped into the grid) so they stay in flight until the
+// values are staged; the returned bit mask marks the values that are real (bit i: value i).
+__device__ __forceinline__ unsigned br_load_tile(const Grid& G, int C, int c0, int t, int c, int o,
+                                                 const float* __restrict__ gF, float (&v)[8]) {
+    const int tyz = G.tiles[1] * G.tiles[2];
+    const int tx = t / tyz, ty = (t - tx * tyz) / G.tiles[2], tz = t % G.tiles[2];
+    const int x = tx * kTile + (o >> 1);
+    const int y0 = ty * kTile + ((o & 1) << 1);
+    const int z0 = tz * kTile;
+    const bool ok = (c0 + c < C) && x < G.dims[0];
+    const int64_t Y = G.dims[1], Z = G.dims[2];
+    const int64_t xc = min(x, G.dims[0] - 1);
+    const float* p = gF + min(c0 + c, C - 1);
+    unsigned mask = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int y = y0 + (i >> 2), z = z0 + (i & 3);
+        const int64_t yc = min(y, G.dims[1] - 1), zc = min(z, G.dims[2] - 1);
+        v[i] = p[((xc * Y + yc) * Z + zc) * C];
+        mask |= (ok && y < G.dims[1] && z < G.dims[2]) ? (1u << i) : 0u;
+    }
+    return mask;
+}
+
+// A operand of one wave's row block of a unit: 4 K steps (16 voxels each), hi and lo.  Rows past
+// the unit's end read the unit's first row: the MFMA rows they feed are routed to the dummy row.
+__device__ __forceinline__ void br_load_w(const __bf16* __restrict__ wt, int j, int nb, int lane,
+                                          int wave, bf16x8 (&ah)[4], bf16x8 (&al)[4]) {
+    const int row = wave * 32 + (lane & 31);
+    const __bf16* wrow = wt + (int64_t)(j + (row < nb ? row : 0)) * kWtRow + (lane >> 5) * 8;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        ah[s] = *reinterpret_cast<const bf16x8*>(wrow + s * 16);
+        al[s] = *reinterpret_cast<const bf16x8*>(wrow + 64 + s * 16);
+    }
+}
 
 __global__ void __launch_bounds__(kBrThreads, 1) k_bwd_region(
     Grid G, Regions RG, int C, int nchunk, const float* __restrict__ gF,
-    const int* __restrict__ toff, const int* __restrict__ sorted_gauss, int M,
-    const int* __restrict__ roff, const int* __restrict__ r_pairs, const int* __restrict__ r_gauss,
+    const int* __restrict__ toff, const int* __restrict__ rowmap, int M,
+    const int* __restrict__ roff, const int* __restrict__ r_pairs, const int* __restrict__ r_gids,
     int MR, const __bf16* __restrict__ wt, float* __restrict__ gpart) {
     __shared__ BrSmem sm;
     const int idx = xcd_remap(blockIdx.x, gridDim.x);
@@ -397,100 +508,156 @@ __global__ void __launch_bounds__(kBrThreads, 1) k_bwd_region(
     if (R >= RG.total) return;
     const int c0 = chunk * kBrCc;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int rnyz = RG.n[1] * RG.n[2];
-    const int rx = R / rnyz, ry = (R - rx * rnyz) / RG.n[2], rz = R % RG.n[2];
-    const int tpr_z = RG.cell[2] / kTile;
     const int jr0 = uniform(min(max(roff[R], 0), MR));
     const int KR = uniform(min(max(roff[R + 1], jr0), MR)) - jr0;
     if (KR <= 0) return;
 
+    if (threadIdx.x == 0) {
+        const int rnyz = RG.n[1] * RG.n[2];
+        const int rx = R / rnyz, ry = (R - rx * rnyz) / RG.n[2], rz = R % RG.n[2];
+        const int tpz = RG.cell[2] / kTile;
+        int k = 0, nu = 0;
+        for (int a = 0; a < 2; ++a)
+            for (int b = 0; b < 2; ++b)
+                for (int cz = 0; cz < tpz; ++cz) {
+                    const int tx = rx * 2 + a, ty = ry * 2 + b, tz = rz * tpz + cz;
+                    if (tx >= G.tiles[0] || ty >= G.tiles[1] || tz >= G.tiles[2]) continue;
+                    const int t = (tx * G.tiles[1] + ty) * G.tiles[2] + tz;
+                    const int j0 = min(max(toff[t], 0), M);
+                    const int n = min(max(toff[t + 1], j0), M) - j0;
+                    if (n <= 0) continue;
+                    sm.tl_t[k] = t;
+                    sm.tl_j[k] = j0;
+                    sm.tl_n[k] = n;
+                    nu += (n + kBrBatch - 1) / kBrBatch;
+                    ++k;
+                }
+        sm.ntl = k;
+        sm.nunits = nu;
+    }
+    const int sc = threadIdx.x & 63, so = threadIdx.x >> 6;   // staging: channel, voxel octet
+
     for (int rg0 = 0; rg0 < KR; rg0 += kBrRows) {
         const int nrows = min(kBrRows, KR - rg0);
         __syncthreads();
-        for (int k = threadIdx.x; k < nrows; k += kBrThreads) sm.rows[k] = r_gauss[r_pairs[jr0 + rg0 + k]];
-        for (int k = threadIdx.x; k < nrows * kBrCc; k += kBrThreads) sm.acc[k / kBrCc][k % kBrCc] = 0.0f;
+        const int ntl = uniform(sm.ntl);
 
-        for (int ltx = 0; ltx < 2; ++ltx)
-        for (int lty = 0; lty < 2; ++lty)
-        for (int ltz = 0; ltz < tpr_z; ++ltz) {
-            const int tx = rx * 2 + ltx, ty = ry * 2 + lty, tz = rz * tpr_z + ltz;
-            if (tx >= G.tiles[0] || ty >= G.tiles[1] || tz >= G.tiles[2]) continue;
-            const int t = (tx * G.tiles[1] + ty) * G.tiles[2] + tz;
-            const int jt0 = uniform(min(max(toff[t], 0), M));
-            const int Nt = uniform(min(max(toff[t + 1], jt0), M)) - jt0;
-            if (Nt <= 0) continue;
-            __syncthreads();   // previous users of bhi/blo/rmap are done
-            {   // stage the G chunk of this tile as the B operand: thread = (channel, voxel octets)
-                const int c = threadIdx.x & 63, oq = threadIdx.x >> 6;
-                const bool cok = c0 + c < C;
-                for (int o = oq; o < 8; o += 4) {
-                    float v8[8];
+        for (int k = threadIdx.x; k < nrows * kBrCc; k += kBrThreads) sm.acc[k >> 6][k & 63] = 0.0f;
+        for (int k = threadIdx.x; k < nrows; k += kBrThreads) sm.rslot[k] = r_pairs[jr0 + rg0 + k];
+
+        // A unit is (tile list index k, entries [kb, kb + kBrBatch) of that tile's list).  Each
+        // pipeline stage walks the units with its own cursor; cursors saturate at the last unit,
+        // so every stage can load unconditionally (the extra loads past the end are discarded).
+        struct Cur { int k, kb; };
+        auto advance = [&](Cur& c) {
+            if (c.kb + kBrBatch < uniform(sm.tl_n[c.k])) c.kb += kBrBatch;
+            else if (c.k + 1 < ntl) { c.k += 1; c.kb = 0; }
+        };
+        auto unit_nb = [&](const Cur& c) { return min(kBrBatch, uniform(sm.tl_n[c.k]) - c.kb); };
+        auto unit_j = [&](const Cur& c) { return uniform(sm.tl_j[c.k]) + c.kb; };
+
+        // gF chunk of a unit (B operand) and the raw row-map entry of this thread (entry re;
+        // threads >= kBrBatch carry a duplicate).  Nothing is computed from the loaded values
+        // until they are staged, so the loads stay in flight across the MFMAs.
+        const int re = threadIdx.x;
+        float pre[8];
+        unsigned pmask = 0;
+        int prm = 0;
+        bool pval = false;
+        auto load_pre = [&](const Cur& c) {
+            const int nb = unit_nb(c);
+            pmask = br_load_tile(G, C, c0, uniform(sm.tl_t[c.k]), sc, so, gF, pre);
+            pval = re < nb;
+            prm = rowmap[unit_j(c) + min(re, nb - 1)];
+        };
+        auto stage = [&](int buf) {
+            float u[8];
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        const int lv = o * 8 + i;
-                        int x, y, z;
-                        tile_voxel(G, t, lv, x, y, z);
-                        v8[i] = (cok && in_grid(G, x, y, z)) ? gF[voxel_index(G, x, y, z) * C + c0 + c] : 0.0f;
-                    }
-                    bf16x8 h, l;
-                    split8(v8, h, l);
-                    const int s = o >> 1, L = (o & 1) * 32 + (c & 31);
-                    sm.bhi[s][c >> 5][L] = h;
-                    sm.blo[s][c >> 5][L] = l;
-                }
+            for (int i = 0; i < 8; ++i) u[i] = (pmask >> i) & 1u ? pre[i] : 0.0f;
+            bf16x8 h, l;
+            split8(u, h, l);
+            const int s = so >> 1, L = (so & 1) * 32 + (sc & 31);
+            sm.bhi[buf][s][sc >> 5][L] = h;
+            sm.blo[buf][s][sc >> 5][L] = l;
+            const int lr = prm - rg0;
+            if (re < kBrBatch) sm.rmap[buf][re] = (pval && lr >= 0 && lr < nrows) ? lr : kBrRows;
+        };
+        // MFMA of one unit and the accumulation of its 32 x 64 results into the LDS rows.
+        auto compute = [&](const Cur& c, int buf, const bf16x8 (&wh)[4], const bf16x8 (&wl)[4]) {
+            const int nb = unit_nb(c);
+            if (wave * 32 >= nb) return;
+            f32x16 a0 = f32x16{}, a1 = f32x16{};
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                a0 = mfma3_32x32x16(wh[s], wl[s], sm.bhi[buf][s][0][lane], sm.blo[buf][s][0][lane], a0);
+                a1 = mfma3_32x32x16(wh[s], wl[s], sm.bhi[buf][s][1][lane], sm.blo[buf][s][1][lane], a1);
             }
-            for (int kb0 = 0; kb0 < Nt; kb0 += kBrBatch) {
-                const int nb = min(kBrBatch, Nt - kb0);
-                if (kb0 > 0) __syncthreads();
-                for (int k = threadIdx.x; k < kBrBatch; k += kBrThreads) {
-                    int lr = -1;
-                    if (k < nb) {
-                        const int g = sorted_gauss[jt0 + kb0 + k];
-                        int lo = 0, hi = nrows;   // rows are ascending: binary search
-                        while (lo < hi) {
-                            const int mid = (lo + hi) >> 1;
-                            if (sm.rows[mid] < g) lo = mid + 1;
-                            else hi = mid;
-                        }
-                        if (lo < nrows && sm.rows[lo] == g) lr = lo;
-                    }
-                    sm.rmap[k] = lr;
-                }
-                __syncthreads();
-                const int nblk = (nb + 31) >> 5;
-                for (int rb = wave; rb < nblk; rb += 4) {
-                    const int row = rb * 32 + (lane & 31);
-                    const bool valid = row < nb;
-                    const __bf16* wrow = wt + (int64_t)(jt0 + kb0 + row) * kWtRow + (lane >> 5) * 8;
-                    f32x16 a0 = f32x16{}, a1 = f32x16{};
+            // D row i of this lane is unit entry ke = wave*32 + 8*(i/4) + 4*(lane/32) + i%4.
+            // Entries of one unit map to distinct rows (or the dummy row), so all rows are read
+            // first and written after, without branches.
+            int lr[16];
 #pragma unroll
-                    for (int s = 0; s < 4; ++s) {
-                        bf16x8 ah = {}, al = {};
-                        if (valid) {
-                            ah = *reinterpret_cast<const bf16x8*>(wrow + s * 16);
-                            al = *reinterpret_cast<const bf16x8*>(wrow + 64 + s * 16);
-                        }
-                        a0 = mfma3_32x32x16(ah, al, sm.bhi[s][0][lane], sm.blo[s][0][lane], a0);
-                        a1 = mfma3_32x32x16(ah, al, sm.bhi[s][1][lane], sm.blo[s][1][lane], a1);
-                    }
+            for (int qq = 0; qq < 4; ++qq) {
+                const int ke = wave * 32 + 8 * qq + 4 * (lane >> 5);
+                const int4 r4 = *reinterpret_cast<const int4*>(&sm.rmap[buf][ke]);
+                lr[4 * qq + 0] = ke + 0 < nb ? r4.x : kBrRows;
+                lr[4 * qq + 1] = ke + 1 < nb ? r4.y : kBrRows;
+                lr[4 * qq + 2] = ke + 2 < nb ? r4.z : kBrRows;
+                lr[4 * qq + 3] = ke + 3 < nb ? r4.w : kBrRows;
+            }
+            const int cl = lane & 31;
+            float v0[16], v1[16];
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        const int k = rb * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-                        const int lr = k < nb ? sm.rmap[k] : -1;
-                        if (lr >= 0) {
-                            sm.acc[lr][lane & 31] += a0[i];
-                            sm.acc[lr][32 + (lane & 31)] += a1[i];
-                        }
-                    }
-                }
+            for (int i = 0; i < 16; ++i) {
+                v0[i] = sm.acc[lr[i]][cl];
+                v1[i] = sm.acc[lr[i]][32 + cl];
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                sm.acc[lr[i]][cl] = v0[i] + a0[i];
+                sm.acc[lr[i]][32 + cl] = v1[i] + a1[i];
+            }
+        };
+
+        // Software pipeline: in the step of unit q, the weights of unit q+1 are loaded into the
+        // free register set, the gF values of unit q+1 (loaded one step earlier) are staged into
+        // the other LDS buffer, the gF values of unit q+2 are loaded, and unit q is multiplied.
+        // Two steps per loop iteration swap the weight register sets, so nothing is copied.
+        Cur cc{0, 0};
+        Cur cw = cc;
+        advance(cw);
+        Cur cp = cw;
+        advance(cp);
+        bf16x8 ah[4], al[4], bh[4], bl[4];
+        auto step = [&](int q, const bf16x8 (&wh)[4], const bf16x8 (&wl)[4], bf16x8 (&nh)[4],
+                        bf16x8 (&nl)[4]) {
+            br_load_w(wt, unit_j(cw), unit_nb(cw), lane, wave, nh, nl);
+            stage((q + 1) & 1);
+            load_pre(cp);
+            compute(cc, q & 1, wh, wl);
+            advance(cc);
+            advance(cw);
+            advance(cp);
+            __syncthreads();
+        };
+        const int nunits = sm.nunits;
+        if (nunits > 0) {
+            load_pre(cc);
+            br_load_w(wt, unit_j(cc), unit_nb(cc), lane, wave, ah, al);
+            stage(0);
+            load_pre(cw);
+            __syncthreads();
+            for (int q = 0;; q += 2) {
+                step(q, ah, al, bh, bl);
+                if (q + 1 >= nunits) break;
+                step(q + 1, bh, bl, ah, al);
+                if (q + 2 >= nunits) break;
             }
         }
-        __syncthreads();
         // one partial row per (region, Gaussian) pair, at the pair's G->R slot
-        const int cw = min(kBrCc, C - c0);
-        for (int k = threadIdx.x; k < nrows * kBrCc; k += kBrThreads) {
-            const int r = k / kBrCc, c = k % kBrCc;
-            if (c < cw) gpart[(int64_t)r_pairs[jr0 + rg0 + r] * C + c0 + c] = sm.acc[r][c];
+        const int cwid = min(kBrCc, C - c0);
+        for (int r = so; r < nrows; r += kBrThreads / 64) {
+            if (sc < cwid) gpart[(int64_t)sm.rslot[r] * C + c0 + sc] = sm.acc[r][sc];
         }
     }
 }
@@ -600,6 +767,8 @@ struct FeatBufs {
     int* r_gauss;
     int* r_cells_sorted;
     int* r_pairs_sorted;
+    int* r_gids;
+    int* rowmap;
     int* roff;
     void* sort_ws;
     float* gpart;
@@ -621,6 +790,8 @@ static FeatBufs carve_feats(void* ws, const Grid& G, int n, int C, int64_t M, in
     b.r_gauss = c.take<int>(mr);
     b.r_cells_sorted = c.take<int>(mr);
     b.r_pairs_sorted = c.take<int>(mr);
+    b.r_gids = c.take<int>(mr);
+    b.rowmap = c.take<int>(m);
     b.roff = c.take<int>(RG.total + 1);
     b.sort_ws = c.take<char>(sort_workspace(MR, RG.total));
     b.gpart = c.take<float>(mr * (C > 0 ? C : 1));
@@ -636,7 +807,7 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
                                  const float* grad_feats, const float* means, const float* opacity,
                                  const float* cov_inv, const int* lb, const int* ub,
                                  const int* g2t_offsets, int64_t M, const int* tile_offsets,
-                                 const int* sorted_gauss, const float* density,
+                                 const int* sorted_tiles, const int* sorted_gauss, const float* density,
                                  const float* grid_feats, const float* features,
                                  const void* plan_ws, int64_t MR, float* grad_means, float* grad_cov,
                                  float* grad_opacity, float* grad_features, void* ws, hipStream_t s) {
@@ -668,12 +839,16 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
     e = launch_tile_offsets(b.r_cells_sorted, MR, RG.total, b.roff, s);
     if (e != hipSuccess) return e;
     if (MR > 0 && M > 0) {
+        G2V_LAUNCH(k_region_gids, dim3((unsigned)ceil_div(MR, 256)), dim3(256), 0, s, (int)MR,
+                   (const int*)b.r_pairs_sorted, (const int*)b.r_gauss, b.r_gids);
+        G2V_LAUNCH(k_region_rowmap, dim3((unsigned)ceil_div(M, 256)), dim3(256), 0, s, G, RG, (int)M, (int)MR,
+                   sorted_tiles, sorted_gauss, (const int*)b.roff, (const int*)b.r_gids, b.rowmap);
         const int nchunk = (C + kBrCc - 1) / kBrCc;
         const int64_t items = (int64_t)RG.total * nchunk;
         const int blocks = (int)ceil_div(items, 8) * 8;
         G2V_LAUNCH(k_bwd_region, dim3(blocks), dim3(kBrThreads), 0, s, G, RG, C, nchunk, grad_feats, tile_offsets,
-                   sorted_gauss, (int)M, (const int*)b.roff, (const int*)b.r_pairs_sorted,
-                   (const int*)b.r_gauss, (int)MR, (const __bf16*)b.wt, b.gpart);
+                   (const int*)b.rowmap, (int)M, (const int*)b.roff, (const int*)b.r_pairs_sorted,
+                   (const int*)b.r_gids, (int)MR, (const __bf16*)b.wt, b.gpart);
     }
     G2V_LAUNCH(k_bwd_gauss, dim3(n), dim3(kBgThreads), 0, s, n, C, (int)M, (int)MR, g2t_offsets,
                (const float*)b.partials, (const int*)pb.g2r_offsets, (const float*)b.gpart, grad_means,

@@ -60,11 +60,11 @@ struct SplatBufs {
     int* sorted_gauss;
     int* tile_offsets;
     void* sort_ws;
+    uint32_t* fpk;      // features as packed bf16 (hi, lo) pairs, forward only
     size_t bytes;
 };
 
-SplatBufs carve_splat(void* ws, int n, int64_t M, const Grid& G) {
-    (void)n;
+SplatBufs carve_splat(void* ws, int n, int64_t M, const Grid& G, int feat_dim = 0) {
     const int64_t m = M > 0 ? M : 1;
     const int T = num_tiles(G);
     Carver c(ws, (size_t)-1);
@@ -74,6 +74,7 @@ SplatBufs carve_splat(void* ws, int n, int64_t M, const Grid& G) {
     b.sorted_gauss = c.take<int>(m);
     b.tile_offsets = c.take<int>(T + 1);
     b.sort_ws = c.take<char>(sort_workspace(M, T));
+    b.fpk = feat_dim > 0 ? c.take<uint32_t>((int64_t)(n + 1) * packed_channels(feat_dim)) : nullptr;
     b.bytes = c.off + 256;
     return b;
 }
@@ -159,11 +160,11 @@ int g2v_forward_plan(int n, const float* means3D, const float* covariances,
     return G2V_OK;
 }
 
-size_t g2v_forward_splat_workspace(int n, long long num_pairs, const float voxel_size[3],
+size_t g2v_forward_splat_workspace(int n, int feat_dim, long long num_pairs, const float voxel_size[3],
                                    const float voxel_range[6]) {
     Grid G;
     if (make_grid(voxel_size, voxel_range, G) != G2V_OK) return 0;
-    return carve_splat(nullptr, n, num_pairs, G).bytes;
+    return carve_splat(nullptr, n, num_pairs, G, feat_dim).bytes;
 }
 
 int g2v_forward_splat(int n, int feat_dim, const float* means3D, const float* opacity,
@@ -187,18 +188,18 @@ int g2v_forward_splat(int n, int feat_dim, const float* means3D, const float* op
     if (rc != G2V_OK) return rc;
     if ((double)G.dims[0] * G.dims[1] * G.dims[2] * (double)feat_dim >= 9.2e18)
         return fail(G2V_ERR_LIMIT, "grid_feats too large");
-    const SplatBufs need = carve_splat(nullptr, n, num_pairs, G);
+    const SplatBufs need = carve_splat(nullptr, n, num_pairs, G, feat_dim);
     rc = check_ws(workspace, workspace_bytes, need.bytes, "splat");
     if (rc != G2V_OK) return rc;
-    const SplatBufs b = carve_splat(workspace, n, num_pairs, G);
+    const SplatBufs b = carve_splat(workspace, n, num_pairs, G, feat_dim);
     hipStream_t s = static_cast<hipStream_t>(stream);
     rc = build_t2g(G, n, valid_voxel_lb, valid_voxel_ub, g2t_offsets, g2t_tile_ids, nullptr,
                    num_pairs, b, s);
     if (rc != G2V_OK) return rc;
     if (feat_dim > 0)
         G2V_HIP(launch_forward_feats(G, feat_dim, means3D, opacity, cov_inv, valid_voxel_lb,
-                                     valid_voxel_ub, b.tile_offsets, b.sorted_gauss, (int)num_pairs,
-                                     features, density, grid_feats, s));
+                                     valid_voxel_ub, b.tile_offsets, b.sorted_gauss, (int)num_pairs, n,
+                                     features, b.fpk, density, grid_feats, s));
     else
         G2V_HIP(launch_forward_density(G, means3D, opacity, cov_inv, valid_voxel_lb, valid_voxel_ub,
                                        b.tile_offsets, b.sorted_gauss, (int)num_pairs, density, s));
@@ -286,7 +287,7 @@ int g2v_backward(int n, int feat_dim, const float* grad_density, const float* gr
     if (rc != G2V_OK) return rc;
     G2V_HIP(launch_backward_feats(G, n, feat_dim, grad_density, grad_feats, means3D, opacity, cov_inv,
                                   valid_voxel_lb, valid_voxel_ub, g2t_offsets, num_pairs,
-                                  b.tile_offsets, b.sorted_gauss, density, grid_feats, features,
+                                  b.tile_offsets, b.sorted_tiles, b.sorted_gauss, density, grid_feats, features,
                                   plan_workspace, num_region_pairs, grad_means, grad_cov, grad_opacity,
                                   grad_features, feats_ws, s));
     return G2V_OK;

@@ -66,6 +66,57 @@ __device__ __forceinline__ void load_params(GaussParams& p, int g, const float* 
     for (int k = 0; k < 3; ++k) { p.lb[k] = lb[g * 3 + k]; p.ub[k] = ub[g * 3 + k]; }
 }
 
+// Parameters of K consecutive entries of a Gaussian list, staged in LDS as structure of
+// arrays (consecutive entries in consecutive banks; a wave-uniform entry is a broadcast read).
+template <int K>
+struct ParamTile {
+    float mu[3][K];
+    float A[9][K];
+    float o[K];
+    int lb[3][K];
+    int ub[3][K];
+    int gid[K];   // Gaussian id, -1 past the end of the list
+};
+
+// Cooperative load of list entries [0, count) (Gaussian ids list[0..count)) into pt.
+template <int K>
+__device__ __forceinline__ void stage_params(ParamTile<K>& pt, const int* __restrict__ list, int count,
+                                             const float* __restrict__ means,
+                                             const float* __restrict__ cov_inv,
+                                             const float* __restrict__ opacity,
+                                             const int* __restrict__ lb, const int* __restrict__ ub) {
+    for (int k = threadIdx.x; k < K; k += blockDim.x) {
+        if (k < count) {
+            const int g = list[k];
+            pt.gid[k] = g;
+#pragma unroll
+            for (int a = 0; a < 3; ++a) {
+                pt.mu[a][k] = means[g * 3 + a];
+                pt.lb[a][k] = lb[g * 3 + a];
+                pt.ub[a][k] = ub[g * 3 + a];
+            }
+#pragma unroll
+            for (int a = 0; a < 9; ++a) pt.A[a][k] = cov_inv[g * 9 + a];
+            pt.o[k] = opacity[g];
+        } else {
+            pt.gid[k] = -1;
+        }
+    }
+}
+
+template <int K>
+__device__ __forceinline__ void read_params(const ParamTile<K>& pt, int k, GaussParams& p) {
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        p.mu[a] = pt.mu[a][k];
+        p.lb[a] = pt.lb[a][k];
+        p.ub[a] = pt.ub[a][k];
+    }
+#pragma unroll
+    for (int a = 0; a < 9; ++a) p.A[a] = pt.A[a][k];
+    p.o = pt.o[k];
+}
+
 __device__ __forceinline__ bool in_box(const GaussParams& p, int x, int y, int z) {
     return !(x < p.lb[0] || x > p.ub[0] || y < p.lb[1] || y > p.ub[1] || z < p.lb[2] || z > p.ub[2]);
 }

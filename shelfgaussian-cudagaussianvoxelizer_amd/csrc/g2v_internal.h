@@ -63,15 +63,18 @@ hipError_t launch_rle(const int* tile_offsets, int T, int* unique_tiles, int* co
                       int* runs_offsets, int* num_runs, void* ws, hipStream_t s);
 
 // ---- forward (g2v_forward.hip) ------------------------------------------------------------
+// Channels of the packed feature rows of the forward (a multiple of one wave's 32 channels).
+inline int packed_channels(int C) { return (C + 31) & ~31; }
+
 hipError_t launch_forward_density(const Grid& G, const float* means, const float* opacity,
                                   const float* cov_inv, const int* lb, const int* ub,
                                   const int* tile_offsets, const int* sorted_gauss, int M,
                                   float* density, hipStream_t s);
 hipError_t launch_forward_feats(const Grid& G, int C, const float* means, const float* opacity,
                                 const float* cov_inv, const int* lb, const int* ub,
-                                const int* tile_offsets, const int* sorted_gauss, int M,
-                                const float* features, float* density, float* grid_feats,
-                                hipStream_t s);
+                                const int* tile_offsets, const int* sorted_gauss, int M, int n,
+                                const float* features, uint32_t* fpk, float* density,
+                                float* grid_feats, hipStream_t s);
 
 // ---- backward (g2v_backward.hip) ----------------------------------------------------------
 hipError_t launch_backward_density(const Grid& G, int n, const float* grad_density,
@@ -87,7 +90,7 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
                                  const float* grad_feats, const float* means, const float* opacity,
                                  const float* cov_inv, const int* lb, const int* ub,
                                  const int* g2t_offsets, int64_t M, const int* tile_offsets,
-                                 const int* sorted_gauss, const float* density,
+                                 const int* sorted_tiles, const int* sorted_gauss, const float* density,
                                  const float* grid_feats, const float* features,
                                  const void* plan_ws, int64_t MR, float* grad_means, float* grad_cov,
                                  float* grad_opacity, float* grad_features, void* ws, hipStream_t s);
