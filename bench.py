@@ -200,7 +200,7 @@ def main():
     if dom:
         n_, t_ = prof[dom]
         avg_s = t_ / n_ * 1e-3
-        bytes_k = per_kernel.get(dom)
+        bytes_k = per_kernel.get(dom.split("<")[0])   # template arguments are not part of the name
         traffic = None
         tpath = os.path.join(ROOT, "profiles", "pmc_traffic.json")
         if os.path.exists(tpath):

@@ -116,50 +116,104 @@ hipError_t launch_backward_density(const Grid& G, int n, const float* grad_densi
 }
 
 // ------------------------------------------------------------------------------------------
-// Features split once into bf16 hi/lo rows padded to Cp channels (zeros beyond C).
+// Features split once into 32-channel chunks of bf16 hi/lo: chunk k of row g is 128 contiguous
+// bytes, hi[32] then lo[32].  Row n and the channels >= C are zero.
 // ------------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) k_split_rows(const float* __restrict__ src, int64_t rows, int C,
-                                                    int Cp, __bf16* __restrict__ hi,
-                                                    __bf16* __restrict__ lo) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= rows * Cp) return;
-    const int64_t r = i / Cp;
-    const int c = (int)(i - r * Cp);
-    const float v = c < C ? src[r * C + c] : 0.0f;
+constexpr int kBtKc = 32;                  // channels per chunk
+constexpr int kBtRowBytes = kBtKc * 4;     // bytes of one row's chunk (hi and lo)
+
+__global__ void __launch_bounds__(256) k_split_chunks(const float* __restrict__ src, int n, int C, int nchk,
+                                                      __bf16* __restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;   // (row, channel), channels fastest
+    const int Cq = nchk * kBtKc;
+    if (i >= (int64_t)(n + 1) * Cq) return;
+    const int64_t r = i / Cq;
+    const int c = (int)(i - r * Cq);
+    const float v = (r < n && c < C) ? src[r * C + c] : 0.0f;
     __bf16 h, l;
     split_bf16(v, h, l);
-    hi[i] = h;
-    lo[i] = l;
+    __bf16* row = dst + (r * nchk + c / kBtKc) * (2 * kBtKc);
+    row[c % kBtKc] = h;
+    row[kBtKc + c % kBtKc] = l;
 }
 
 // ------------------------------------------------------------------------------------------
 // Phase A: tile-major U, t_v, gw, geometric partials, split weights.
 // ------------------------------------------------------------------------------------------
 constexpr int kBtThreads = 512;                        // 8 waves
+constexpr int kBtWaves = kBtThreads / 64;
 constexpr int kBtGroups = 4;                           // Gaussian groups (wave >> 1)
-constexpr int kBtNbw = 3;                              // 32-Gaussian N blocks per wave per pass
-constexpr int kBtPass = kBtGroups * kBtNbw * 32;       // 384 Gaussians per pass
-constexpr int kBtKc = 64;                              // channels of G staged per LDS chunk
+constexpr int kBtNbw = 2;                              // 32-Gaussian N blocks per wave per pass
+constexpr int kBtPass = kBtGroups * kBtNbw * 32;       // 256 Gaussians per pass
+constexpr int kBtStages = 3;                           // F chunks resident in LDS (loaded 2 ahead)
+constexpr int kBtDma = kBtPass / 8 / kBtWaves;         // 1 KB direct-to-LDS loads per wave per chunk
 constexpr int kWtRow = 128;                            // bf16 per pair: 64 hi then 64 lo
 
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Direct-to-LDS loads: lane l writes its 16 (or 4) bytes from gptr at LDS address lds + 16*l
+// (4*l).  Issued as inline assembly so that the compiler does not attach conservative waits to
+// later LDS reads; every consumer waits explicitly (wait_vm) and meets the other waves at a
+// barrier.  M0 carries the wave-uniform LDS base and needs one wait state before the load.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(lds_ptr_t)p;
+}
+__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :: "v"(gptr), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* gptr, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+                 :: "v"(gptr), "s"(lds) : "memory", "m0");
+}
+
 struct BtSmem {
-    bf16x8 ahi[2][kBtKc / 16][2][64];   // A operand (G tile), hi: [buffer][k step][voxel block][slot]
-    bf16x8 alo[2][kBtKc / 16][2][64];
+    union {
+        // F chunk rows of the pass's Gaussians; the 16-byte slot q of row r sits at q ^ (r&7), so the
+        // 8 lanes of one LDS cycle (8 consecutive rows) hit 8 different 16-byte bank groups
+        unsigned char frow[kBtStages][kBtPass * kBtRowBytes];
+        float xch[2][kBtPass][kNumGrads];   // epilogue exchange, used after the K loop has drained
+    } u;
+    float graw[kBtStages][64][kBtKc];   // G chunks as loaded (fp32, voxel-major)
+    bf16x8 ahi[2][2][2][64];   // A operand (G chunk), hi: [buffer][k step][voxel block][lane]
+    bf16x8 alo[2][2][2][64];
     int vlin[64];
     float gD[64], inv[64], tv[64], D[64];
-    ParamTile<kBtPass> pt;              // parameters of this pass's list entries
+    ParamTile<kBtPass> pt;     // parameters of this pass's list entries
     float tpart[kBtGroups][64];
-    float xch[2][kBtPass][kNumGrads];
 };
 
+// s_waitcnt immediate that waits for vmcnt <= n and leaves the other counters alone.
+__device__ constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
+
+// Waits until at most n vector-memory loads of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(N));
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// Workgroup barrier for LDS hand-offs only: waits for this wave's LDS operations and meets the
+// other waves, without the release fence of __syncthreads (that fence would also wait for every
+// outstanding global load, including the direct-to-LDS loads kept in flight on purpose).  The
+// caller has already waited (vmcnt) for the direct-to-LDS loads the next step reads.
+__device__ __forceinline__ void lds_barrier() {
+    __asm__ __volatile__("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((15 << 0) | (7 << 4) | (0 << 8) | (3 << 14));   // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    __asm__ __volatile__("" ::: "memory");
+}
+
+template <bool VEC>
 __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
-    Grid G, int C, int Cp, const float* __restrict__ gD, const float* __restrict__ gF,
+    Grid G, int n, int C, int nchk, const float* __restrict__ gD, const float* __restrict__ gF,
     const float* __restrict__ means, const float* __restrict__ opacity,
     const float* __restrict__ cov_inv, const int* __restrict__ lb, const int* __restrict__ ub,
     const int* __restrict__ g2t_offsets, const int* __restrict__ toff,
     const int* __restrict__ sorted_gauss, int M, const float* __restrict__ density,
-    const float* __restrict__ grid_feats, const __bf16* __restrict__ fhi,
-    const __bf16* __restrict__ flo, float* __restrict__ pair_partials, __bf16* __restrict__ wt) {
+    const float* __restrict__ grid_feats, const __bf16* __restrict__ fsp,
+    float* __restrict__ pair_partials, __bf16* __restrict__ wt) {
     __shared__ BtSmem sm;
     const int T = G.tiles[0] * G.tiles[1] * G.tiles[2];
     const int tile = uniform(xcd_remap(blockIdx.x, gridDim.x));
@@ -171,7 +225,6 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
     const int mb = wave & 1, ngrp = wave >> 1;
     const int tyz = G.tiles[1] * G.tiles[2];
     const int tx = tile / tyz, ty = (tile - tx * tyz) / G.tiles[2], tz = tile % G.tiles[2];
-    const bool vec_ok = (C & 3) == 0;
 
     if (threadIdx.x < 64) {
         int x, y, z;
@@ -202,41 +255,81 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
         }
     }
 
-    // staging of G chunks: thread = (voxel sv, 8-channel group sq), coalesced 32-byte reads
+    // G staging: direct-to-LDS loads of the raw chunk (voxel rows clamped to a valid row, channels
+    // clamped into the row), then thread (voxel sv, channel quad sq) masks, splits and writes its
+    // four channels into the A operand.  VEC: one 16-byte load per lane, lane = (voxel, quad);
+    // otherwise four 4-byte loads per lane, each covering two voxel rows.
+    constexpr int kNG = VEC ? 1 : 4;   // G loads per wave per chunk
     const int sv = threadIdx.x >> 3, sq = threadIdx.x & 7;
-    const int nks = Cp >> 4;                       // K steps of 16 channels
-    const int nchunks = (nks + 3) >> 2;            // 4 K steps per staged chunk
-    auto load_g = [&](int chunk, float (&v8)[8]) {
-        const int srow = sm.vlin[sv];
-        const int c = chunk * kBtKc + sq * 8;
-        const int valid = max(0, min(8, C - c));
-        if (srow >= 0 && valid > 0) load8(gF + (int64_t)srow * C + c, valid, vec_ok, v8);
-        else {
+    const int grow = sm.vlin[sv];
+    const float* gsrc[kNG];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v8[i] = 0.0f;
+    for (int k = 0; k < kNG; ++k) {
+        const int v = VEC ? sv : wave * 8 + 2 * k + (lane >> 5);
+        gsrc[k] = gF + (int64_t)max(sm.vlin[v], 0) * C;
+    }
+    auto dma_g = [&](int chunk, int stage) {
+#pragma unroll
+        for (int k = 0; k < kNG; ++k) {
+            if (VEC) {
+                const int c = min(chunk * kBtKc + 4 * sq, C - 4);
+                dma16(gsrc[k] + c, uniform(lds_addr(&sm.graw[stage][wave * 8][0])));
+            } else {
+                const int c = min(chunk * kBtKc + (lane & 31), C - 1);
+                dma4(gsrc[k] + c, uniform(lds_addr(&sm.graw[stage][wave * 8 + 2 * k][0])));
+            }
         }
     };
-    auto write_g = [&](const float (&v8)[8], int buf) {
-        bf16x8 h, l;
-        split8(v8, h, l);
-        // XOR swizzle of the 16-byte slot: the 8 channel groups of one voxel land in different
-        // LDS banks (the MFMA-side read applies the same permutation)
-        const int s = sq >> 1, L = (sq & 1) * 32 + (sv & 31);
-        const int Ls = L ^ ((2 * s + (sq & 1)) & 15);
-        sm.ahi[buf][s][sv >> 5][Ls] = h;
-        sm.alo[buf][s][sv >> 5][Ls] = l;
+    auto write_g = [&](int chunk, int stage, int buf) {
+        const int c = chunk * kBtKc + 4 * sq;
+        const float4 v4 = *reinterpret_cast<const float4*>(&sm.graw[stage][sv][4 * sq]);
+        const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+        typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+        bf16x4 hv, lv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            __bf16 hh, ll;
+            split_bf16((grow >= 0 && c + e < C) ? v[e] : 0.0f, hh, ll);
+            hv[e] = hh;
+            lv[e] = ll;
+        }
+        // channels 4sq..4sq+3 of the chunk: K step sq/4, k group (sq/2)&1, half sq&1 of the slot
+        const int s = sq >> 2, L = ((sq >> 1) & 1) * 32 + (sv & 31);
+        *reinterpret_cast<bf16x4*>(reinterpret_cast<char*>(&sm.ahi[buf][s][sv >> 5][L]) + (sq & 1) * 8) = hv;
+        *reinterpret_cast<bf16x4*>(reinterpret_cast<char*>(&sm.alo[buf][s][sv >> 5][L]) + (sq & 1) * 8) = lv;
     };
+
+    const uint32_t fstride = (uint32_t)nchk * kBtRowBytes;   // bytes of one Gaussian's split row
+    const char* fbase = reinterpret_cast<const char*>(fsp);
 
     for (int pbase = 0; pbase < Ng; pbase += kBtPass) {
         const int pcount = min(kBtPass, Ng - pbase);
         __syncthreads();
         stage_params(sm.pt, sorted_gauss + j0 + pbase, pcount, means, cov_inv, opacity, lb, ub);
-        {
-            float v8[8];
-            load_g(0, v8);
-            write_g(v8, 0);
-        }
         __syncthreads();
+
+        // F rows by direct-to-LDS loads: row group rg = wave + kBtWaves*i (8 rows, 1 KB) is
+        // loaded by this wave; lane = (row rg*8 + lane/8, slot lane%8) and slot p carries the
+        // 16-byte piece p ^ (row&7) of the row's chunk.  Rows past the list read the zero
+        // row; a group wholly past it reads one 16-byte piece of the zero row in every lane.
+        // Every wave issues exactly kBtDma loads per chunk, so the wait counts below are exact.
+        uint32_t doff[kBtDma];
+#pragma unroll
+        for (int i = 0; i < kBtDma; ++i) {
+            const int rg = wave + kBtWaves * i;
+            const int r = rg * 8 + (lane >> 3);
+            const int g = r < pcount ? sm.pt.gid[r] : n;
+            const int piece = (lane & 7) ^ (r & 7);
+            doff[i] = (rg * 8 < pcount) ? (uint32_t)g * fstride + (uint32_t)piece * 16u : (uint32_t)n * fstride;
+        }
+        auto dma_f = [&](int chunk, int buf) {
+#pragma unroll
+            for (int i = 0; i < kBtDma; ++i) {
+                const int rg = wave + kBtWaves * i;
+                dma16(fbase + (doff[i] + (uint32_t)chunk * kBtRowBytes),
+                      uniform(lds_addr(&sm.u.frow[buf][rg * 8 * kBtRowBytes])));
+            }
+        };
 
         f32x16 acc[kBtNbw];
 #pragma unroll
@@ -248,44 +341,52 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             nact += ((ngrp + kBtGroups * j) * 32 < pcount) ? 1 : 0;
             gcol[j] = sm.pt.gid[(ngrp + kBtGroups * j) * 32 + (lane & 31)];
         }
-        // B operand (split features of this lane's Gaussians), prefetched one K step ahead
-        bf16x8 bnh[kBtNbw], bnl[kBtNbw];
-        auto load_b = [&](int ks) {
-            const int c = ks * 16 + (lane >> 5) * 8;
+        nact = uniform(nact);
+        const int h = lane >> 5;
+        auto compute = [&](int buf, int abuf) {
 #pragma unroll
-            for (int j = 0; j < kBtNbw; ++j) {
-                bnh[j] = bf16x8{};
-                bnl[j] = bf16x8{};
-                if (j < nact && gcol[j] >= 0) {
-                    bnh[j] = *reinterpret_cast<const bf16x8*>(fhi + (int64_t)gcol[j] * Cp + c);
-                    bnl[j] = *reinterpret_cast<const bf16x8*>(flo + (int64_t)gcol[j] * Cp + c);
+            for (int s = 0; s < 2; ++s) {
+                const bf16x8 ah = sm.ahi[abuf][s][mb][lane];
+                const bf16x8 al = sm.alo[abuf][s][mb][lane];
+#pragma unroll
+                for (int j = 0; j < kBtNbw; ++j) {
+                    if (j < nact) {
+                        const int r = (ngrp + kBtGroups * j) * 32 + (lane & 31);
+                        const int sw = r & 7;
+                        const unsigned char* rowp = &sm.u.frow[buf][r * kBtRowBytes];
+                        const bf16x8 bh = *reinterpret_cast<const bf16x8*>(rowp + (((2 * s + h) ^ sw) << 4));
+                        const bf16x8 bl = *reinterpret_cast<const bf16x8*>(rowp + (((4 + 2 * s + h) ^ sw) << 4));
+                        acc[j] = mfma3_32x32x16(ah, al, bh, bl, acc[j]);
+                    }
                 }
             }
         };
-        load_b(0);
-        for (int ch = 0; ch < nchunks; ++ch) {
-            const int buf = ch & 1;
-            float pre[8];
-            if (ch + 1 < nchunks) load_g(ch + 1, pre);
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const int ks = ch * 4 + s;
-                if (ks < nks) {
-                    bf16x8 bh[kBtNbw], bl[kBtNbw];
-#pragma unroll
-                    for (int j = 0; j < kBtNbw; ++j) { bh[j] = bnh[j]; bl[j] = bnl[j]; }
-                    if (ks + 1 < nks) load_b(ks + 1);
-                    const int ls = lane ^ ((2 * s + (lane >> 5)) & 15);
-                    const bf16x8 ah = sm.ahi[buf][s][mb][ls];
-                    const bf16x8 al = sm.alo[buf][s][mb][ls];
-#pragma unroll
-                    for (int j = 0; j < kBtNbw; ++j)
-                        if (j < nact) acc[j] = mfma3_32x32x16(ah, al, bh[j], bl[j], acc[j]);
-                }
-            }
-            if (ch + 1 < nchunks) write_g(pre, buf ^ 1);
-            __syncthreads();
+
+        // Pipeline over chunks (every load is direct-to-LDS).  Step ch starts with the A operand
+        // and the F rows of chunk ch in LDS and the raw G values of chunk ch+1 complete; it loads
+        // the F rows of chunk ch+2 and the G values of chunk ch+3, multiplies chunk ch, writes the
+        // A operand of chunk ch+1, and waits until only its own loads are outstanding.
+        const int clast = nchk - 1;
+        dma_g(0, 0);
+        dma_f(0, 0);
+        dma_g(min(1, clast), 1);
+        dma_f(min(1, clast), 1);
+        dma_g(min(2, clast), 2);
+        wait_vm<kBtDma + kNG>();      // G(0), F(0), G(1) complete
+        lds_barrier();
+        write_g(0, 0, 0);
+        lds_barrier();
+        for (int ch = 0; ch < nchk; ++ch) {
+            dma_f(min(ch + 2, clast), (ch + 2) % kBtStages);
+            dma_g(min(ch + 3, clast), (ch + 3) % kBtStages);
+            compute(ch % kBtStages, ch & 1);
+            write_g(ch + 1, (ch + 1) % kBtStages, (ch + 1) & 1);
+            wait_vm<kBtDma + kNG>();  // F(ch+1) and G(ch+2) complete
+            lds_barrier();
         }
+        // drain the surplus loads of the last steps before the F buffers are reused
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        __syncthreads();
 
         // ---- epilogue 1: split weights w / max(D, eps) of every pair; t_v from U (single pass)
         float rowt[16];
@@ -375,7 +476,7 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             for (int k = 0; k < kNumGrads; ++k) gr[k] += __shfl_xor(gr[k], 32, 64);
             if (lane < 32) {
 #pragma unroll
-                for (int k = 0; k < kNumGrads; ++k) sm.xch[mb][slot][k] = gr[k];
+                for (int k = 0; k < kNumGrads; ++k) sm.u.xch[mb][slot][k] = gr[k];
             }
         }
         __syncthreads();
@@ -387,7 +488,7 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             if (pair < 0 || pair >= M) continue;   // malformed CSR: never write outside the buffer
             float* out = pair_partials + pair * kNumGrads;
 #pragma unroll
-            for (int k = 0; k < kNumGrads; ++k) out[k] = sm.xch[0][slot][k] + sm.xch[1][slot][k];
+            for (int k = 0; k < kNumGrads; ++k) out[k] = sm.u.xch[0][slot][k] + sm.u.xch[1][slot][k];
         }
     }
 }
@@ -718,7 +819,7 @@ __global__ void __launch_bounds__(kBgThreads) k_bwd_gauss(
 // ------------------------------------------------------------------------------------------
 // Host side
 // ------------------------------------------------------------------------------------------
-static int padded_channels(int C) { return (C + 15) & ~15; }
+static int feature_chunks(int C) { return (C + kBtKc - 1) / kBtKc; }
 
 struct PlanBufs {
     int* g2r_offsets;
@@ -758,8 +859,7 @@ hipError_t backward_plan(const Grid& G, int n, const int* lb, const int* ub, voi
 }
 
 struct FeatBufs {
-    __bf16* fhi;
-    __bf16* flo;
+    __bf16* fsp;
     float* partials;
     __bf16* wt;
     int* r_cells;
@@ -777,12 +877,10 @@ struct FeatBufs {
 
 static FeatBufs carve_feats(void* ws, const Grid& G, int n, int C, int64_t M, int64_t MR) {
     const Regions RG = make_regions(G);
-    const int Cp = padded_channels(C);
     const int64_t m = M > 0 ? M : 1, mr = MR > 0 ? MR : 1;
     Carver c(ws, (size_t)-1);
     FeatBufs b;
-    b.fhi = c.take<__bf16>((int64_t)(n > 0 ? n : 1) * Cp);
-    b.flo = c.take<__bf16>((int64_t)(n > 0 ? n : 1) * Cp);
+    b.fsp = c.take<__bf16>((int64_t)(n + 1) * feature_chunks(C) * 2 * kBtKc);
     b.partials = c.take<float>(m * kNumGrads);
     b.wt = c.take<__bf16>(m * kWtRow);
     b.r_cells = c.take<int>(mr);
@@ -814,20 +912,26 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
     if (n <= 0) return hipSuccess;
     const Regions RG = make_regions(G);
     const int T = G.tiles[0] * G.tiles[1] * G.tiles[2];
-    const int Cp = padded_channels(C);
+    const int nchk = feature_chunks(C);
+    if (!split_rows_fit(n, C)) return hipErrorInvalidValue;   // byte offsets of the split rows are 32-bit
     const FeatBufs b = carve_feats(ws, G, n, C, M, MR);
     const PlanBufs pb = carve_plan(const_cast<void*>(plan_ws), n);
     hipError_t e;
 
-    // features as bf16 hi/lo rows (B operand of phase A)
-    const int64_t fcount = (int64_t)n * Cp;
-    G2V_LAUNCH(k_split_rows, dim3((unsigned)ceil_div(fcount, 256)), dim3(256), 0, s, features, (int64_t)n, C, Cp,
-               b.fhi, b.flo);
+    // features as 32-channel chunks of bf16 hi/lo (B operand of phase A), plus a zero row
+    const int64_t fcount = (int64_t)(n + 1) * nchk * kBtKc;
+    G2V_LAUNCH(k_split_chunks, dim3((unsigned)ceil_div(fcount, 256)), dim3(256), 0, s, features, n, C, nchk,
+               b.fsp);
     if (M > 0 && T > 0) {
         const int blocks = (int)ceil_div(T, 8) * 8;
-        G2V_LAUNCH(k_bwd_tile, dim3(blocks), dim3(kBtThreads), 0, s, G, C, Cp, grad_density, grad_feats, means,
-                   opacity, cov_inv, lb, ub, g2t_offsets, tile_offsets, sorted_gauss, (int)M, density,
-                   grid_feats, (const __bf16*)b.fhi, (const __bf16*)b.flo, b.partials, b.wt);
+        if ((C & 3) == 0)
+            G2V_LAUNCH(k_bwd_tile<true>, dim3(blocks), dim3(kBtThreads), 0, s, G, n, C, nchk, grad_density,
+                       grad_feats, means, opacity, cov_inv, lb, ub, g2t_offsets, tile_offsets, sorted_gauss,
+                       (int)M, density, grid_feats, (const __bf16*)b.fsp, b.partials, b.wt);
+        else
+            G2V_LAUNCH(k_bwd_tile<false>, dim3(blocks), dim3(kBtThreads), 0, s, G, n, C, nchk, grad_density,
+                       grad_feats, means, opacity, cov_inv, lb, ub, g2t_offsets, tile_offsets, sorted_gauss,
+                       (int)M, density, grid_feats, (const __bf16*)b.fsp, b.partials, b.wt);
     }
     // Region -> Gaussian CSR (pairs carry their G->R slot so partial rows land Gaussian-major)
     if (MR > 0) {

@@ -178,6 +178,8 @@ int g2v_forward_splat(int n, int feat_dim, const float* means3D, const float* op
         return fail(G2V_ERR_INVALID, "n = %d, feat_dim = %d, num_pairs = %lld", n, feat_dim, num_pairs);
     if (num_pairs > 2147483647ll) return fail(G2V_ERR_LIMIT, "num_pairs = %lld exceeds int32", num_pairs);
     if (!density) return fail(G2V_ERR_INVALID, "density is null");
+    if (feat_dim > 0 && !packed_fits(n, feat_dim))
+        return fail(G2V_ERR_LIMIT, "n = %d x feat_dim = %d exceeds the packed feature rows (4 GiB)", n, feat_dim);
     if (feat_dim > 0 && (!grid_feats || (n > 0 && !features)))
         return fail(G2V_ERR_INVALID, "feat_dim = %d needs features and grid_feats", feat_dim);
     if (num_pairs > 0 && (!g2t_tile_ids || !g2t_offsets || !means3D || !opacity || !cov_inv ||
@@ -265,6 +267,8 @@ int g2v_backward(int n, int feat_dim, const float* grad_density, const float* gr
     if (feat_dim > 0 && (!grad_feats || !grid_feats || !features || !grad_features || !density ||
                          !g2t_offsets || !plan_workspace || (num_pairs > 0 && !g2t_tile_ids)))
         return fail(G2V_ERR_INVALID, "feat_dim = %d needs the feature tensors, density, the CSR and the plan workspace", feat_dim);
+    if (feat_dim > 0 && !split_rows_fit(n, feat_dim))
+        return fail(G2V_ERR_LIMIT, "n = %d x feat_dim = %d exceeds the split feature rows (4 GiB)", n, feat_dim);
     Grid G;
     int rc = make_grid(voxel_size, voxel_range, G);
     if (rc != G2V_OK) return rc;

@@ -96,38 +96,46 @@ __device__ __forceinline__ void unpack8(const uint32_t (&u)[8], bf16x8& hi, bf16
 }
 
 // ------------------------------------------------------------------------------------------
-// Feature splat (MFMA 32x32x16 bf16, 3-term split).
+// Feature splat (MFMA 32x32x16 bf16, 3-term split), channel-quad layout.
+//
+// A wave owns 64 voxels x 128 channels: 2 voxel blocks x 4 channel blocks of 32x32.  Column j of
+// channel block c is channel 4j + c (of the wave's 128), so the B fragment of lane (j, h) for
+// all four channel blocks comes from one 16-byte load per Gaussian row (4 packed channels), and
+// the four results of one output row sit in one lane as 4 consecutive channels (float4 store).
+// Per K step (16 Gaussians) a wave issues 8 dwordx4 gathers, 32 byte permutes and 24 MFMAs.
 // ------------------------------------------------------------------------------------------
-constexpr int kFwdThreads = 512;               // 8 waves
-constexpr int kFwdKMax = 256;                  // Gaussians held in LDS per K chunk (multiple of 16)
-constexpr int kFwdKSteps = kFwdKMax / 16;
+constexpr int kFwdThreads = 256;               // 4 waves
 constexpr int kFwdWaves = kFwdThreads / 64;
-constexpr int kFwdChanPerWave = 32;            // one 32-wide N block per wave
+constexpr int kFwdChanPerWave = 128;
 constexpr int kFwdChanPerPass = kFwdChanPerWave * kFwdWaves;
+constexpr int kFwdKMax = 256;                  // Gaussians held in LDS per K chunk (multiple of 32)
+constexpr int kFwdKSteps = kFwdKMax / 16;
+constexpr int kFwdPB = 64;                     // list entries whose parameters are staged at a time
 
-constexpr int kFwdPB = 8 * kFwdWaves;          // list entries staged at a time: one octet per wave
+static_assert(kFwdChanPerWave == kPackedChannelAlign, "packed rows are padded to one wave's channels");
 
 struct FwdSmem {
     bf16x8 whi[kFwdKSteps][2][64];   // A operand, hi part: [k step][voxel block][lane]
     bf16x8 wlo[kFwdKSteps][2][64];   // A operand, lo part
-    alignas(16) int gid[kFwdKMax];   // Gaussian id of each K slot (the zero row n for padding)
+    alignas(16) uint32_t roff[kFwdKMax];   // byte offset of each K slot's packed row (zero row for padding)
     ParamTile<kFwdPB> pt;            // parameters of the entries being turned into weights
     float dpart[kFwdWaves][64];      // per-wave partial densities
     alignas(16) float inv_den[64];   // 1 / max(D, eps)
     alignas(16) int vlin[64];        // linear voxel index, -1 outside the grid
 };
 
-// Builds the split W for K slots [kbeg, kbeg + klen) of the tile list into LDS, 32 entries at a
-// time (their parameters staged cooperatively in LDS, one octet of 8 entries per wave); adds the
-// raw density of this wave's entries to dacc (one voxel per lane).
+// Builds the split W for K slots [kbeg, kbeg + 16*ksteps) of the tile list into LDS (slots past
+// klen get weight 0 and the zero row), kFwdPB entries at a time; wave w builds octets w, w+4, ...
+// of each batch for the lane's voxel.  Adds the raw density of the entries to dacc.
 __device__ __forceinline__ void fwd_build_w(FwdSmem& sm, const Grid& G, int j0, int kbeg, int klen,
                                             int ksteps, bool add_density, float& dacc,
                                             const float* __restrict__ means,
                                             const float* __restrict__ opacity,
                                             const float* __restrict__ cov_inv,
                                             const int* __restrict__ lb, const int* __restrict__ ub,
-                                            const int* __restrict__ sorted_gauss, int zero_row,
-                                            int x, int y, int z, float cx, float cy, float cz) {
+                                            const int* __restrict__ sorted_gauss, uint32_t row_bytes,
+                                            uint32_t zero_off, int x, int y, int z, float cx,
+                                            float cy, float cz) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nslots = ksteps * 16;
     for (int b0 = 0; b0 < nslots; b0 += kFwdPB) {
@@ -135,12 +143,11 @@ __device__ __forceinline__ void fwd_build_w(FwdSmem& sm, const Grid& G, int j0, 
         stage_params(sm.pt, sorted_gauss + j0 + kbeg + b0, max(0, min(kFwdPB, klen - b0)), means, cov_inv,
                      opacity, lb, ub);
         __syncthreads();
-        const int o = (b0 >> 3) + wave;   // octet of K slots handled by this wave
-        if (o * 8 < nslots) {
+        for (int oc = wave; oc * 8 < min(kFwdPB, nslots - b0); oc += kFwdWaves) {
             float wv[8];
 #pragma unroll 2
             for (int i = 0; i < 8; ++i) {
-                const int k = wave * 8 + i;
+                const int k = oc * 8 + i;
                 const int g = sm.pt.gid[k];
                 float w = 0.0f;
                 if (g >= 0) {
@@ -153,10 +160,11 @@ __device__ __forceinline__ void fwd_build_w(FwdSmem& sm, const Grid& G, int j0, 
                     if (add_density) dacc += w;
                 }
                 wv[i] = (w > 0.0f) ? w : 0.0f;   // feature gate of the reference (.cu:936)
-                if (lane == 0) sm.gid[o * 8 + i] = g >= 0 ? g : zero_row;
+                if (lane == 0) sm.roff[b0 + k] = g >= 0 ? (uint32_t)g * row_bytes : zero_off;
             }
             bf16x8 h, l;
             split8(wv, h, l);
+            const int o = (b0 >> 3) + oc;     // octet index within the chunk
             const int s = o >> 1, mb = lane >> 5;
             const int slot = (o & 1) * 32 + (lane & 31);
             sm.whi[s][mb][slot] = h;
@@ -176,6 +184,7 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
     const int tile = uniform(xcd_remap(blockIdx.x, gridDim.x));
     if (tile >= T) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int jl = lane & 31, kh = lane >> 5;
 
     int x, y, z;
     tile_voxel(G, tile, lane, x, y, z);
@@ -185,12 +194,20 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
     const int j0 = uniform(min(max(toff[tile], 0), M));
     const int Ng = uniform(min(max(toff[tile + 1], j0), M)) - j0;
     const int nkc = (Ng + kFwdKMax - 1) / kFwdKMax;
+    const uint32_t row_bytes = (uint32_t)Cp * 4u;
+    const uint32_t zero_off = (uint32_t)n * row_bytes;
+    const char* fbase = reinterpret_cast<const char*>(fpk);
     float dacc = 0.0f;
 
     for (int cbase = 0; cbase < C; cbase += kFwdChanPerPass) {
-        f32x16 acc[2];
-        acc[0] = f32x16{};
-        acc[1] = f32x16{};
+        const int cw0 = cbase + wave * kFwdChanPerWave;          // first channel of this wave
+        const bool has_ch = cw0 < C;                               // wave-uniform
+        const uint32_t lane_off = (uint32_t)(cw0 + 4 * jl) * 4u;  // byte offset of the lane's quad
+        f32x16 acc[2][4];
+#pragma unroll
+        for (int vb = 0; vb < 2; ++vb)
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) acc[vb][cb] = f32x16{};
 
         for (int kc = 0; kc < nkc; ++kc) {
             const int kbeg = kc * kFwdKMax;
@@ -199,38 +216,50 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
             if (nkc > 1 || cbase == 0) {
                 __syncthreads();  // previous readers of W are done
                 fwd_build_w(sm, G, j0, kbeg, klen, ksteps, cbase == 0, dacc, means, opacity,
-                            cov_inv, lb, ub, sorted_gauss, n, x, y, z, cx, cy, cz);
+                            cov_inv, lb, ub, sorted_gauss, row_bytes, zero_off, x, y, z, cx, cy, cz);
                 __syncthreads();
             }
-            const int c = cbase + wave * kFwdChanPerWave + (lane & 31);
-            if (cbase + wave * kFwdChanPerWave < Cp) {   // wave-uniform: this wave has channels
-                // packed pairs of K step ks for this lane's channel; padding reads the zero row
-                auto gather = [&](int ks, uint32_t (&u)[8]) {
-                    const int* gp = &sm.gid[ks * 16 + (lane >> 5) * 8];
-                    const int4 ga = *reinterpret_cast<const int4*>(gp);
-                    const int4 gb = *reinterpret_cast<const int4*>(gp + 4);
-                    const int gs[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
+            if (has_ch) {
+                // packed quads of K step ks: rows of slots ks*16 + 8*kh + i, channels cw0+4jl..+3
+                auto gather = [&](int ks, uint4 (&u)[8]) {
+                    const uint32_t* rp = &sm.roff[ks * 16 + kh * 8];
+                    const uint4 ra = *reinterpret_cast<const uint4*>(rp);
+                    const uint4 rb = *reinterpret_cast<const uint4*>(rp + 4);
+                    const uint32_t rs[8] = {ra.x, ra.y, ra.z, ra.w, rb.x, rb.y, rb.z, rb.w};
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) u[i] = fpk[(int64_t)gs[i] * Cp + c];
+                    for (int i = 0; i < 8; ++i)
+                        u[i] = *reinterpret_cast<const uint4*>(fbase + (size_t)(rs[i] + lane_off));
                 };
-                auto step = [&](int ks, const uint32_t (&u)[8]) {
-                    bf16x8 bh, bl;
-                    unpack8(u, bh, bl);
+                auto step = [&](int ks, const uint4 (&u)[8]) {
+                    const bf16x8 ah0 = sm.whi[ks][0][lane], al0 = sm.wlo[ks][0][lane];
+                    const bf16x8 ah1 = sm.whi[ks][1][lane], al1 = sm.wlo[ks][1][lane];
 #pragma unroll
-                    for (int mb = 0; mb < 2; ++mb)
-                        acc[mb] = mfma3_32x32x16(sm.whi[ks][mb][lane], sm.wlo[ks][mb][lane], bh, bl, acc[mb]);
+                    for (int cb = 0; cb < 4; ++cb) {
+                        uint32_t q[8];
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) q[i] = u[i][cb];
+                        bf16x8 bh, bl;
+                        unpack8(q, bh, bl);
+                        acc[0][cb] = mfma3_32x32x16(ah0, al0, bh, bl, acc[0][cb]);
+                        acc[1][cb] = mfma3_32x32x16(ah1, al1, bh, bl, acc[1][cb]);
+                    }
                 };
                 // loads and steps are unconditional (ksteps is even, the prefetch index is
-                // clamped) so the next step's gather stays in flight across this step's MFMAs
-                uint32_t ua[8], ub[8];
+                // clamped) so the next step's gather stays in flight across this step's MFMAs;
+                // the scheduling barriers keep the compiler from sinking the gathers to their use
+                uint4 ua[8], ub[8];
                 const int klast = ksteps - 1;
                 if (ksteps > 0) {
                     gather(0, ua);
                     for (int ks = 0; ks < ksteps; ks += 2) {
                         gather(ks + 1, ub);
+                        __builtin_amdgcn_sched_barrier(0);
                         step(ks, ua);
+                        __builtin_amdgcn_sched_barrier(0);
                         gather(min(ks + 2, klast), ua);
+                        __builtin_amdgcn_sched_barrier(0);
                         step(ks + 1, ub);
+                        __builtin_amdgcn_sched_barrier(0);
                     }
                 }
             }
@@ -249,21 +278,35 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
             __syncthreads();
         }
 
-        // epilogue: D layout of 32x32 MFMA -> row = 8*(i/4) + 4*(lane/32) + i%4, col = lane%32
-        const int c = cbase + wave * kFwdChanPerWave + (lane & 31);
-        if (c < C) {
+        // epilogue: D row of element i = 8*(i/4) + 4*kh + i%4 (voxel), column jl -> channels
+        // cw0 + 4*jl + cb for channel block cb
+        if (has_ch) {
+            const int c0 = cw0 + 4 * jl;
 #pragma unroll
-            for (int mb = 0; mb < 2; ++mb) {
+            for (int vb = 0; vb < 2; ++vb) {
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int r0 = mb * 32 + 8 * q + 4 * (lane >> 5);
+                for (int qd = 0; qd < 4; ++qd) {
+                    const int r0 = vb * 32 + 8 * qd + 4 * kh;
                     const int4 vl = *reinterpret_cast<const int4*>(&sm.vlin[r0]);
                     const float4 iv = *reinterpret_cast<const float4*>(&sm.inv_den[r0]);
                     const int vs[4] = {vl.x, vl.y, vl.z, vl.w};
                     const float is[4] = {iv.x, iv.y, iv.z, iv.w};
 #pragma unroll
-                    for (int ii = 0; ii < 4; ++ii)
-                        if (vs[ii] >= 0) grid_feats[(int64_t)vs[ii] * C + c] = acc[mb][q * 4 + ii] * is[ii];
+                    for (int ii = 0; ii < 4; ++ii) {
+                        const int e = qd * 4 + ii;
+                        const float4 v = make_float4(acc[vb][0][e] * is[ii], acc[vb][1][e] * is[ii],
+                                                     acc[vb][2][e] * is[ii], acc[vb][3][e] * is[ii]);
+                        if (vs[ii] < 0) continue;
+                        float* dst = grid_feats + (int64_t)vs[ii] * C + c0;
+                        if ((C & 3) == 0) {
+                            if (c0 < C) *reinterpret_cast<float4*>(dst) = v;
+                        } else {
+                            if (c0 + 0 < C) dst[0] = v.x;
+                            if (c0 + 1 < C) dst[1] = v.y;
+                            if (c0 + 2 < C) dst[2] = v.z;
+                            if (c0 + 3 < C) dst[3] = v.w;
+                        }
+                    }
                 }
             }
         }
@@ -282,6 +325,7 @@ hipError_t launch_forward_feats(const Grid& G, int C, const float* means, const 
                                       M, density, s);
     const int Cp = packed_channels(C);
     const int64_t count = (int64_t)(n + 1) * Cp;
+    if (count * 4 > (int64_t)UINT32_MAX) return hipErrorInvalidValue;   // byte offsets are 32-bit
     G2V_LAUNCH(k_split_pack, dim3((unsigned)ceil_div(count, 256)), dim3(256), 0, s, features, n, C, Cp, fpk);
     const int blocks = (int)ceil_div(T, 8) * 8;
     G2V_LAUNCH(k_fwd_feats, dim3(blocks), dim3(kFwdThreads), 0, s, G, C, means, opacity,

@@ -63,8 +63,13 @@ hipError_t launch_rle(const int* tile_offsets, int T, int* unique_tiles, int* co
                       int* runs_offsets, int* num_runs, void* ws, hipStream_t s);
 
 // ---- forward (g2v_forward.hip) ------------------------------------------------------------
-// Channels of the packed feature rows of the forward (a multiple of one wave's 32 channels).
-inline int packed_channels(int C) { return (C + 31) & ~31; }
+// Channels of the packed feature rows of the forward (a multiple of one wave's 128 channels).
+constexpr int kPackedChannelAlign = 128;
+inline int packed_channels(int C) { return (C + kPackedChannelAlign - 1) & ~(kPackedChannelAlign - 1); }
+// Packed feature rows are addressed with 32-bit byte offsets.
+inline bool packed_fits(int n, int C) { return (int64_t)(n + 1) * packed_channels(C) * 4 <= (int64_t)UINT32_MAX; }
+// The split feature rows of the backward (32-channel chunks, 4 bytes per channel) likewise.
+inline bool split_rows_fit(int n, int C) { return (int64_t)(n + 1) * ((C + 31) / 32) * 128 <= (int64_t)UINT32_MAX; }
 
 hipError_t launch_forward_density(const Grid& G, const float* means, const float* opacity,
                                   const float* cov_inv, const int* lb, const int* ub,
