@@ -12,10 +12,10 @@
 //                    cores (3-term bf16 split, fp32 accumulate); t_v from U (sum_g [w>0] w u / D is
 //                    sum_c gF F); gw; the ten geometric partial sums of each (tile, Gaussian) pair,
 //                    stored at the pair's G->T CSR slot; the split weights w/max(D,eps) of the pair.
-//   B  k_bwd_region  one workgroup per (region of 2x2xRZ tiles, 64-channel chunk): for every tile
-//                    of the region, (pairs x 64 voxels) . (64 voxels x 64 channels) on the matrix
-//                    cores, accumulated in LDS rows owned by the region's Gaussians; writes one
-//                    partial d f row per (region, Gaussian) pair at its G->R CSR slot.
+//   B  k_bwd_region  one workgroup per (region of 2x2xRZ tiles, 128-channel chunk): for every
+//                    tile of the region, (region rows x 64 voxels) . (64 voxels x 128 channels) on
+//                    the matrix cores, accumulated in registers (a wave owns 32 region rows);
+//                    writes one partial d f row per (region, Gaussian) pair at its G->R CSR slot.
 //   C  k_bwd_gauss   one workgroup per Gaussian: fixed-order sums of its geometric partials and
 //                    of its region partial rows.
 // Without features, k_bwd_density walks each Gaussian's box with one wave.
@@ -504,12 +504,24 @@ __global__ void __launch_bounds__(256) k_region_gids(int MR, const int* __restri
     if (j < MR) r_gids[j] = r_gauss[r_pairs_sorted[j]];
 }
 
-__global__ void __launch_bounds__(256) k_region_rowmap(Grid G, Regions RG, int M, int MR,
-                                                       const int* __restrict__ sorted_tiles,
-                                                       const int* __restrict__ sorted_gauss,
-                                                       const int* __restrict__ roff,
-                                                       const int* __restrict__ r_gids,
-                                                       int* __restrict__ rowmap) {
+constexpr int kBrSlots = 16;   // tiles per region (2 x 2 x up to 4), slot ((tx&1)*2 + (ty&1))*RZ + tz%RZ
+
+// Fills n ints with v (also used where a stream may be captured: no memset nodes).
+__global__ void __launch_bounds__(256) k_fill_i32(int64_t n, int v, int* __restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) dst[i] = v;
+}
+
+// Row table of phase B: for region row r (its position in the region's ascending Gaussian list,
+// at G->R slot roff[R] + r) and tile slot s, table[(roff[R] + r) * kBrSlots + s] is the
+// Tile->Gaussian index of the pair (tile, Gaussian), or M (the zero row of the split weights)
+// when the Gaussian does not touch that tile.  The table is filled with M beforehand.
+__global__ void __launch_bounds__(256) k_region_table(Grid G, Regions RG, int M, int MR,
+                                                      const int* __restrict__ sorted_tiles,
+                                                      const int* __restrict__ sorted_gauss,
+                                                      const int* __restrict__ roff,
+                                                      const int* __restrict__ r_gids,
+                                                      int* __restrict__ table) {
     const int j = blockIdx.x * 256 + threadIdx.x;
     if (j >= M) return;
     const int t = sorted_tiles[j], g = sorted_gauss[j];
@@ -517,6 +529,7 @@ __global__ void __launch_bounds__(256) k_region_rowmap(Grid G, Regions RG, int M
     const int tx = t / tyz, ty = (t - tx * tyz) / G.tiles[2], tz = t % G.tiles[2];
     const int tpz = RG.cell[2] / kTile;
     const int R = ((tx >> 1) * RG.n[1] + (ty >> 1)) * RG.n[2] + tz / tpz;
+    const int slot = ((tx & 1) * 2 + (ty & 1)) * tpz + tz % tpz;
     const int a = min(max(roff[R], 0), MR);
     const int b = min(max(roff[R + 1], a), MR);
     int lo = a, hi = b;
@@ -525,83 +538,72 @@ __global__ void __launch_bounds__(256) k_region_rowmap(Grid G, Regions RG, int M
         if (r_gids[mid] < g) lo = mid + 1;
         else hi = mid;
     }
-    rowmap[j] = (lo < b && r_gids[lo] == g) ? lo - a : -1;
+    if (lo < b && r_gids[lo] == g) table[(int64_t)lo * kBrSlots + slot] = j;
 }
 
 // ------------------------------------------------------------------------------------------
-// Phase B: per-region partial feature gradients, accumulated in LDS.
+// Phase B: per-region partial feature gradients, accumulated in registers.
 //
-// Work item = (region, 64-channel chunk); 8 waves.  The region's tile lists are walked as units
-// of (tile, batch of up to 256 list entries).  Per unit, wave w multiplies row block w of the
-// split pair weights (32 pairs x 64 voxels) by the tile's gF chunk (64 voxels x 64 channels, the
-// B operand in LDS) and adds the 32 x 64 result to the LDS rows of those Gaussians.  Each
-// Gaussian appears once per tile list, so every LDS row has one writer per unit and the sums are
-// deterministic.  Software pipeline, one unit ahead: while unit q is multiplied, the B operand and
-// the row map of unit q+1 are written to the other LDS buffers, the weights of unit q+1 are loaded
-// into registers, and the gF values of unit q+2 are loaded into registers.
+// Work item = (region, 128-channel chunk); 8 waves.  Wave w owns 32 rows of the region's
+// Gaussian list (rows 256p + 32w .. +31 in pass p) and 128 channels: 4 accumulator blocks of
+// 32 x 32.  For every tile of the region the tile's gF chunk (64 voxels x 128 channels) is staged
+// in LDS, split hi/lo in the MFMA B layout, and each wave adds
+//     (its 32 rows x 64 voxels of split pair weights) . (64 voxels x 128 channels)
+// where a row whose Gaussian does not touch the tile reads the zero row of the weights.  Every
+// row is owned by one lane set and summed over the tiles in a fixed order: no atomics, no LDS
+// accumulators.  Software pipeline one tile ahead: while tile k is multiplied, the weights of
+// tile k+1 are loaded into the other register set, the gF values of tile k+1 are written to the
+// other LDS buffer, and the gF values of tile k+2 are loaded into registers.
 // ------------------------------------------------------------------------------------------
 constexpr int kBrThreads = 512;   // 8 waves
-constexpr int kBrCc = 64;         // channels per work item
-constexpr int kBrRows = 400;      // region rows held in LDS at a time
-constexpr int kBrBatch = 256;     // tile entries per unit: one 32-row block per wave
-constexpr int kBrAccLd = kBrCc + 4;
-constexpr int kBrMaxTiles = 16;   // tiles per region (2 x 2 x up to 4)
+constexpr int kBrWaves = kBrThreads / 64;
+constexpr int kBrCc = 128;        // channels per work item
+constexpr int kBrPass = kBrWaves * 32;   // region rows per pass
+static_assert(kBrPass * kBrSlots % kBrThreads == 0 && kBrPass <= kBrThreads, "row-table staging shape");
 
 struct BrSmem {
-    float acc[kBrRows + 1][kBrAccLd];   // region rows; row kBrRows is a dummy that absorbs
-                                        // the results of padding entries
-    bf16x8 bhi[2][4][2][64];       // B operand (gF chunk): [buffer][k step of 16 voxels][channel block][lane]
-    bf16x8 blo[2][4][2][64];
-    alignas(16) int rmap[2][kBrBatch];   // unit entry -> local row, kBrRows if it has none
-    int rslot[kBrRows];            // G->R slot of each local row (where its partial row goes)
-    int tl_t[kBrMaxTiles], tl_j[kBrMaxTiles], tl_n[kBrMaxTiles];
+    bf16x8 bhi[2][4][4][64];   // B operand (gF chunk): [buffer][k step of 16 voxels][channel block][lane]
+    bf16x8 blo[2][4][4][64];
+    int tab[kBrPass][kBrSlots];           // row table of this pass's rows (M: absent pair)
+    int rslot[kBrPass];                   // G->R slot of each row of the pass
+    int tl_t[kBrSlots], tl_s[kBrSlots];   // tiles of the region (inside the grid) and their slots
     int ntl;
-    int nunits;                    // units (tile list slices of kBrBatch entries) of the region
 };
 
-// gF values of one tile for the staging thread (channel c, voxel octet o): voxels o*8 .. o*8+7.
-// The loads are unconditional (indices clamped into the grid) so they stay in flight until the
-// values are staged; the returned bit mask marks the values that are real (bit i: value i).
-__device__ __forceinline__ unsigned br_load_tile(const Grid& G, int C, int c0, int t, int c, int o,
-                                                 const float* __restrict__ gF, float (&v)[8]) {
+// gF of one tile for the staging thread (channel c of the chunk, voxel octets o0 and o0 + 4).
+// The loads are unconditional (indices clamped into the grid); bit i + 8k of the returned mask
+// marks value v[k][i] as real.
+__device__ __forceinline__ unsigned br_load_tile(const Grid& G, int C, int c0, int t, int c, int o0,
+                                                 const float* __restrict__ gF, float (&v)[2][8]) {
     const int tyz = G.tiles[1] * G.tiles[2];
     const int tx = t / tyz, ty = (t - tx * tyz) / G.tiles[2], tz = t % G.tiles[2];
-    const int x = tx * kTile + (o >> 1);
-    const int y0 = ty * kTile + ((o & 1) << 1);
-    const int z0 = tz * kTile;
-    const bool ok = (c0 + c < C) && x < G.dims[0];
     const int64_t Y = G.dims[1], Z = G.dims[2];
-    const int64_t xc = min(x, G.dims[0] - 1);
+    const bool cok = c0 + c < C;
     const float* p = gF + min(c0 + c, C - 1);
     unsigned mask = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int y = y0 + (i >> 2), z = z0 + (i & 3);
-        const int64_t yc = min(y, G.dims[1] - 1), zc = min(z, G.dims[2] - 1);
-        v[i] = p[((xc * Y + yc) * Z + zc) * C];
-        mask |= (ok && y < G.dims[1] && z < G.dims[2]) ? (1u << i) : 0u;
+    for (int k = 0; k < 2; ++k) {
+        const int o = o0 + 4 * k;
+        const int x = tx * kTile + (o >> 1);
+        const int y0 = ty * kTile + ((o & 1) << 1);
+        const int z0 = tz * kTile;
+        const int64_t xc = min(x, G.dims[0] - 1);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int y = y0 + (i >> 2), z = z0 + (i & 3);
+            const int64_t yc = min(y, G.dims[1] - 1), zc = min(z, G.dims[2] - 1);
+            v[k][i] = p[((xc * Y + yc) * Z + zc) * C];
+            mask |= (cok && x < G.dims[0] && y < G.dims[1] && z < G.dims[2]) ? (1u << (i + 8 * k)) : 0u;
+        }
     }
     return mask;
 }
 
-// A operand of one wave's row block of a unit: 4 K steps (16 voxels each), hi and lo.  Rows past
-// the unit's end read the unit's first row: the MFMA rows they feed are routed to the dummy row.
-__device__ __forceinline__ void br_load_w(const __bf16* __restrict__ wt, int j, int nb, int lane,
-                                          int wave, bf16x8 (&ah)[4], bf16x8 (&al)[4]) {
-    const int row = wave * 32 + (lane & 31);
-    const __bf16* wrow = wt + (int64_t)(j + (row < nb ? row : 0)) * kWtRow + (lane >> 5) * 8;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        ah[s] = *reinterpret_cast<const bf16x8*>(wrow + s * 16);
-        al[s] = *reinterpret_cast<const bf16x8*>(wrow + 64 + s * 16);
-    }
-}
-
 __global__ void __launch_bounds__(kBrThreads, 1) k_bwd_region(
     Grid G, Regions RG, int C, int nchunk, const float* __restrict__ gF,
-    const int* __restrict__ toff, const int* __restrict__ rowmap, int M,
-    const int* __restrict__ roff, const int* __restrict__ r_pairs, const int* __restrict__ r_gids,
-    int MR, const __bf16* __restrict__ wt, float* __restrict__ gpart) {
+    const int* __restrict__ toff, int M, const int* __restrict__ roff,
+    const int* __restrict__ r_pairs, const int* __restrict__ table, int MR,
+    const __bf16* __restrict__ wt, float* __restrict__ gpart) {
     __shared__ BrSmem sm;
     const int idx = xcd_remap(blockIdx.x, gridDim.x);
     const int R = uniform(idx / nchunk);
@@ -617,148 +619,119 @@ __global__ void __launch_bounds__(kBrThreads, 1) k_bwd_region(
         const int rnyz = RG.n[1] * RG.n[2];
         const int rx = R / rnyz, ry = (R - rx * rnyz) / RG.n[2], rz = R % RG.n[2];
         const int tpz = RG.cell[2] / kTile;
-        int k = 0, nu = 0;
+        int k = 0;
         for (int a = 0; a < 2; ++a)
             for (int b = 0; b < 2; ++b)
                 for (int cz = 0; cz < tpz; ++cz) {
                     const int tx = rx * 2 + a, ty = ry * 2 + b, tz = rz * tpz + cz;
                     if (tx >= G.tiles[0] || ty >= G.tiles[1] || tz >= G.tiles[2]) continue;
                     const int t = (tx * G.tiles[1] + ty) * G.tiles[2] + tz;
-                    const int j0 = min(max(toff[t], 0), M);
-                    const int n = min(max(toff[t + 1], j0), M) - j0;
-                    if (n <= 0) continue;
+                    if (min(max(toff[t + 1], 0), M) <= min(max(toff[t], 0), M)) continue;   // empty list
                     sm.tl_t[k] = t;
-                    sm.tl_j[k] = j0;
-                    sm.tl_n[k] = n;
-                    nu += (n + kBrBatch - 1) / kBrBatch;
+                    sm.tl_s[k] = (a * 2 + b) * tpz + cz;
                     ++k;
                 }
         sm.ntl = k;
-        sm.nunits = nu;
     }
-    const int sc = threadIdx.x & 63, so = threadIdx.x >> 6;   // staging: channel, voxel octet
+    __syncthreads();
+    const int ntl = uniform(sm.ntl);
+    if (ntl == 0) return;   // every row stays zero: phase C reads no partial row of this region
 
-    for (int rg0 = 0; rg0 < KR; rg0 += kBrRows) {
-        const int nrows = min(kBrRows, KR - rg0);
-        __syncthreads();
-        const int ntl = uniform(sm.ntl);
-
-        for (int k = threadIdx.x; k < nrows * kBrCc; k += kBrThreads) sm.acc[k >> 6][k & 63] = 0.0f;
-        for (int k = threadIdx.x; k < nrows; k += kBrThreads) sm.rslot[k] = r_pairs[jr0 + rg0 + k];
-
-        // A unit is (tile list index k, entries [kb, kb + kBrBatch) of that tile's list).  Each
-        // pipeline stage walks the units with its own cursor; cursors saturate at the last unit,
-        // so every stage can load unconditionally (the extra loads past the end are discarded).
-        struct Cur { int k, kb; };
-        auto advance = [&](Cur& c) {
-            if (c.kb + kBrBatch < uniform(sm.tl_n[c.k])) c.kb += kBrBatch;
-            else if (c.k + 1 < ntl) { c.k += 1; c.kb = 0; }
-        };
-        auto unit_nb = [&](const Cur& c) { return min(kBrBatch, uniform(sm.tl_n[c.k]) - c.kb); };
-        auto unit_j = [&](const Cur& c) { return uniform(sm.tl_j[c.k]) + c.kb; };
-
-        // gF chunk of a unit (B operand) and the raw row-map entry of this thread (entry re;
-        // threads >= kBrBatch carry a duplicate).  Nothing is computed from the loaded values
-        // until they are staged, so the loads stay in flight across the MFMAs.
-        const int re = threadIdx.x;
-        float pre[8];
-        unsigned pmask = 0;
-        int prm = 0;
-        bool pval = false;
-        auto load_pre = [&](const Cur& c) {
-            const int nb = unit_nb(c);
-            pmask = br_load_tile(G, C, c0, uniform(sm.tl_t[c.k]), sc, so, gF, pre);
-            pval = re < nb;
-            prm = rowmap[unit_j(c) + min(re, nb - 1)];
-        };
-        auto stage = [&](int buf) {
+    const int sc = threadIdx.x & (kBrCc - 1), so = threadIdx.x >> 7;   // staging: channel, octets so, so+4
+    const int h = lane >> 5, cl = lane & 31;
+    float pre[2][8];
+    unsigned pmask = 0;
+    auto stage = [&](int buf) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
             float u[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) u[i] = (pmask >> i) & 1u ? pre[i] : 0.0f;
-            bf16x8 h, l;
-            split8(u, h, l);
-            const int s = so >> 1, L = (so & 1) * 32 + (sc & 31);
-            sm.bhi[buf][s][sc >> 5][L] = h;
-            sm.blo[buf][s][sc >> 5][L] = l;
-            const int lr = prm - rg0;
-            if (re < kBrBatch) sm.rmap[buf][re] = (pval && lr >= 0 && lr < nrows) ? lr : kBrRows;
-        };
-        // MFMA of one unit and the accumulation of its 32 x 64 results into the LDS rows.
-        auto compute = [&](const Cur& c, int buf, const bf16x8 (&wh)[4], const bf16x8 (&wl)[4]) {
-            const int nb = unit_nb(c);
-            if (wave * 32 >= nb) return;
-            f32x16 a0 = f32x16{}, a1 = f32x16{};
+            for (int i = 0; i < 8; ++i) u[i] = (pmask >> (i + 8 * k)) & 1u ? pre[k][i] : 0.0f;
+            bf16x8 hh, ll;
+            split8(u, hh, ll);
+            const int o = so + 4 * k;   // voxel octet: k step o/2, k group o&1
+            sm.bhi[buf][o >> 1][sc >> 5][(o & 1) * 32 + (sc & 31)] = hh;
+            sm.blo[buf][o >> 1][sc >> 5][(o & 1) * 32 + (sc & 31)] = ll;
+        }
+    };
+
+    for (int rp = 0; rp < KR; rp += kBrPass) {
+        const int lrow = wave * 32 + cl;                  // this lane's row of the pass (A operand row)
+        const bool wave_rows = rp + wave * 32 < KR;       // wave-uniform
+        auto load_w = [&](int k, bf16x8 (&wh)[4], bf16x8 (&wl)[4]) {
+            const int j = sm.tab[lrow][sm.tl_s[k]];
+            const __bf16* wrow = wt + (int64_t)j * kWtRow + h * 8;
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                a0 = mfma3_32x32x16(wh[s], wl[s], sm.bhi[buf][s][0][lane], sm.blo[buf][s][0][lane], a0);
-                a1 = mfma3_32x32x16(wh[s], wl[s], sm.bhi[buf][s][1][lane], sm.blo[buf][s][1][lane], a1);
+                wh[s] = *reinterpret_cast<const bf16x8*>(wrow + s * 16);
+                wl[s] = *reinterpret_cast<const bf16x8*>(wrow + 64 + s * 16);
             }
-            // D row i of this lane is unit entry ke = wave*32 + 8*(i/4) + 4*(lane/32) + i%4.
-            // Entries of one unit map to distinct rows (or the dummy row), so all rows are read
-            // first and written after, without branches.
-            int lr[16];
+        };
+        f32x16 acc[4];
 #pragma unroll
-            for (int qq = 0; qq < 4; ++qq) {
-                const int ke = wave * 32 + 8 * qq + 4 * (lane >> 5);
-                const int4 r4 = *reinterpret_cast<const int4*>(&sm.rmap[buf][ke]);
-                lr[4 * qq + 0] = ke + 0 < nb ? r4.x : kBrRows;
-                lr[4 * qq + 1] = ke + 1 < nb ? r4.y : kBrRows;
-                lr[4 * qq + 2] = ke + 2 < nb ? r4.z : kBrRows;
-                lr[4 * qq + 3] = ke + 3 < nb ? r4.w : kBrRows;
-            }
-            const int cl = lane & 31;
-            float v0[16], v1[16];
+        for (int cb = 0; cb < 4; ++cb) acc[cb] = f32x16{};
+        auto compute = [&](int buf, const bf16x8 (&wh)[4], const bf16x8 (&wl)[4]) {
+            if (!wave_rows) return;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                v0[i] = sm.acc[lr[i]][cl];
-                v1[i] = sm.acc[lr[i]][32 + cl];
-            }
+            for (int s = 0; s < 4; ++s)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                sm.acc[lr[i]][cl] = v0[i] + a0[i];
-                sm.acc[lr[i]][32 + cl] = v1[i] + a1[i];
-            }
+                for (int cb = 0; cb < 4; ++cb)
+                    acc[cb] = mfma3_32x32x16(wh[s], wl[s], sm.bhi[buf][s][cb][lane], sm.blo[buf][s][cb][lane], acc[cb]);
         };
 
-        // Software pipeline: in the step of unit q, the weights of unit q+1 are loaded into the
-        // free register set, the gF values of unit q+1 (loaded one step earlier) are staged into
-        // the other LDS buffer, the gF values of unit q+2 are loaded, and unit q is multiplied.
-        // Two steps per loop iteration swap the weight register sets, so nothing is copied.
-        Cur cc{0, 0};
-        Cur cw = cc;
-        advance(cw);
-        Cur cp = cw;
-        advance(cp);
+        // prologue: tile 0 staged and its weights loaded; gF of tile 1 in registers
+        const int klast = ntl - 1;
         bf16x8 ah[4], al[4], bh[4], bl[4];
-        auto step = [&](int q, const bf16x8 (&wh)[4], const bf16x8 (&wl)[4], bf16x8 (&nh)[4],
-                        bf16x8 (&nl)[4]) {
-            br_load_w(wt, unit_j(cw), unit_nb(cw), lane, wave, nh, nl);
-            stage((q + 1) & 1);
-            load_pre(cp);
-            compute(cc, q & 1, wh, wl);
-            advance(cc);
-            advance(cw);
-            advance(cp);
+        __syncthreads();   // the previous pass is done with both buffers and the row tables
+        {
+            // all loads first, then the LDS stores (rows past the region read its last row)
+            constexpr int kPer = kBrPass * kBrSlots / kBrThreads;
+            int tv[kPer];
+#pragma unroll
+            for (int q = 0; q < kPer; ++q) {
+                const int e = threadIdx.x + q * kBrThreads;
+                const int r = min(rp + e / kBrSlots, KR - 1);
+                tv[q] = table[(int64_t)(jr0 + r) * kBrSlots + e % kBrSlots];
+            }
+            const int rs = r_pairs[jr0 + min(rp + (int)(threadIdx.x % kBrPass), KR - 1)];
+#pragma unroll
+            for (int q = 0; q < kPer; ++q) {
+                const int e = threadIdx.x + q * kBrThreads;
+                sm.tab[e / kBrSlots][e % kBrSlots] = rp + e / kBrSlots < KR ? tv[q] : M;
+            }
+            if (threadIdx.x < kBrPass) sm.rslot[threadIdx.x] = rs;
+        }
+        __syncthreads();
+        pmask = br_load_tile(G, C, c0, sm.tl_t[0], sc, so, gF, pre);
+        load_w(0, ah, al);
+        stage(0);
+        pmask = br_load_tile(G, C, c0, sm.tl_t[min(1, klast)], sc, so, gF, pre);
+        __syncthreads();
+        auto step = [&](int k, const bf16x8 (&wh)[4], const bf16x8 (&wl)[4], bf16x8 (&nh)[4], bf16x8 (&nl)[4]) {
+            load_w(min(k + 1, klast), nh, nl);
+            stage((k + 1) & 1);
+            pmask = br_load_tile(G, C, c0, sm.tl_t[min(k + 2, klast)], sc, so, gF, pre);
+            compute(k & 1, wh, wl);
             __syncthreads();
         };
-        const int nunits = sm.nunits;
-        if (nunits > 0) {
-            load_pre(cc);
-            br_load_w(wt, unit_j(cc), unit_nb(cc), lane, wave, ah, al);
-            stage(0);
-            load_pre(cw);
-            __syncthreads();
-            for (int q = 0;; q += 2) {
-                step(q, ah, al, bh, bl);
-                if (q + 1 >= nunits) break;
-                step(q + 1, bh, bl, ah, al);
-                if (q + 2 >= nunits) break;
-            }
+        for (int k = 0;; k += 2) {
+            step(k, ah, al, bh, bl);
+            if (k + 1 >= ntl) break;
+            step(k + 1, bh, bl, ah, al);
+            if (k + 2 >= ntl) break;
         }
-        // one partial row per (region, Gaussian) pair, at the pair's G->R slot
-        const int cwid = min(kBrCc, C - c0);
-        for (int r = so; r < nrows; r += kBrThreads / 64) {
-            if (sc < cwid) gpart[(int64_t)sm.rslot[r] * C + c0 + sc] = sm.acc[r][sc];
+
+        // D element i of block cb: region row rp + 32w + 8(i/4) + 4h + i%4, channel c0 + 32cb + cl
+        if (wave_rows) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int lr = wave * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+                if (rp + lr >= KR) continue;
+                float* dst = gpart + (int64_t)sm.rslot[lr] * C + c0 + cl;
+#pragma unroll
+                for (int cb = 0; cb < 4; ++cb)
+                    if (c0 + 32 * cb + cl < C) dst[32 * cb] = acc[cb][i];
+            }
         }
     }
 }
@@ -868,7 +841,7 @@ struct FeatBufs {
     int* r_cells_sorted;
     int* r_pairs_sorted;
     int* r_gids;
-    int* rowmap;
+    int* table;
     int* roff;
     void* sort_ws;
     float* gpart;
@@ -882,14 +855,14 @@ static FeatBufs carve_feats(void* ws, const Grid& G, int n, int C, int64_t M, in
     FeatBufs b;
     b.fsp = c.take<__bf16>((int64_t)(n + 1) * feature_chunks(C) * 2 * kBtKc);
     b.partials = c.take<float>(m * kNumGrads);
-    b.wt = c.take<__bf16>(m * kWtRow);
+    b.wt = c.take<__bf16>((m + 1) * kWtRow);   // row M is zero (rows of absent pairs read it)
     b.r_cells = c.take<int>(mr);
     b.r_pairs = c.take<int>(mr);
     b.r_gauss = c.take<int>(mr);
     b.r_cells_sorted = c.take<int>(mr);
     b.r_pairs_sorted = c.take<int>(mr);
     b.r_gids = c.take<int>(mr);
-    b.rowmap = c.take<int>(m);
+    b.table = c.take<int>(mr * kBrSlots);
     b.roff = c.take<int>(RG.total + 1);
     b.sort_ws = c.take<char>(sort_workspace(MR, RG.total));
     b.gpart = c.take<float>(mr * (C > 0 ? C : 1));
@@ -945,14 +918,18 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
     if (MR > 0 && M > 0) {
         G2V_LAUNCH(k_region_gids, dim3((unsigned)ceil_div(MR, 256)), dim3(256), 0, s, (int)MR,
                    (const int*)b.r_pairs_sorted, (const int*)b.r_gauss, b.r_gids);
-        G2V_LAUNCH(k_region_rowmap, dim3((unsigned)ceil_div(M, 256)), dim3(256), 0, s, G, RG, (int)M, (int)MR,
-                   sorted_tiles, sorted_gauss, (const int*)b.roff, (const int*)b.r_gids, b.rowmap);
+        const int64_t tcount = MR * kBrSlots;
+        G2V_LAUNCH(k_fill_i32, dim3((unsigned)ceil_div(tcount, 256)), dim3(256), 0, s, tcount, (int)M, b.table);
+        G2V_LAUNCH(k_fill_i32, dim3(1), dim3(256), 0, s, (int64_t)(kWtRow / 2), 0,
+                   reinterpret_cast<int*>(b.wt + M * kWtRow));
+        G2V_LAUNCH(k_region_table, dim3((unsigned)ceil_div(M, 256)), dim3(256), 0, s, G, RG, (int)M, (int)MR,
+                   sorted_tiles, sorted_gauss, (const int*)b.roff, (const int*)b.r_gids, b.table);
         const int nchunk = (C + kBrCc - 1) / kBrCc;
         const int64_t items = (int64_t)RG.total * nchunk;
         const int blocks = (int)ceil_div(items, 8) * 8;
         G2V_LAUNCH(k_bwd_region, dim3(blocks), dim3(kBrThreads), 0, s, G, RG, C, nchunk, grad_feats, tile_offsets,
-                   (const int*)b.rowmap, (int)M, (const int*)b.roff, (const int*)b.r_pairs_sorted,
-                   (const int*)b.r_gids, (int)MR, (const __bf16*)b.wt, b.gpart);
+                   (int)M, (const int*)b.roff, (const int*)b.r_pairs_sorted, (const int*)b.table, (int)MR,
+                   (const __bf16*)b.wt, b.gpart);
     }
     G2V_LAUNCH(k_bwd_gauss, dim3(n), dim3(kBgThreads), 0, s, n, C, (int)M, (int)MR, g2t_offsets,
                (const float*)b.partials, (const int*)pb.g2r_offsets, (const float*)b.gpart, grad_means,
