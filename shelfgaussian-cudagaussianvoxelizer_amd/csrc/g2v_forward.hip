@@ -108,27 +108,39 @@ constexpr int kFwdThreads = 256;               // 4 waves
 constexpr int kFwdWaves = kFwdThreads / 64;
 constexpr int kFwdChanPerWave = 128;
 constexpr int kFwdChanPerPass = kFwdChanPerWave * kFwdWaves;
-constexpr int kFwdKMax = 256;                  // Gaussians held in LDS per K chunk (multiple of 32)
+constexpr int kFwdKMax = 224;                  // Gaussians held in LDS per K chunk (multiple of 32)
 constexpr int kFwdKSteps = kFwdKMax / 16;
-constexpr int kFwdPB = 64;                     // list entries whose parameters are staged at a time
 
 static_assert(kFwdChanPerWave == kPackedChannelAlign, "packed rows are padded to one wave's channels");
+
+// Gaussian parameters of one list entry as one 80-byte LDS record (five 16-byte reads).
+struct alignas(16) FwdParam {
+    float mu[3];
+    float o;
+    float A[9];
+    int lb[3];
+    int ub[3];
+    int pad;
+};
+static_assert(sizeof(FwdParam) == 80, "FwdParam is five 16-byte words");
 
 struct FwdSmem {
     bf16x8 whi[kFwdKSteps][2][64];   // A operand, hi part: [k step][voxel block][lane]
     bf16x8 wlo[kFwdKSteps][2][64];   // A operand, lo part
     alignas(16) uint32_t roff[kFwdKMax];   // byte offset of each K slot's packed row (zero row for padding)
-    ParamTile<kFwdPB> pt;            // parameters of the entries being turned into weights
+    FwdParam par[kFwdKMax];          // parameters of the K chunk's entries
     float dpart[kFwdWaves][64];      // per-wave partial densities
     alignas(16) float inv_den[64];   // 1 / max(D, eps)
     alignas(16) int vlin[64];        // linear voxel index, -1 outside the grid
 };
 
 // Builds the split W for K slots [kbeg, kbeg + 16*ksteps) of the tile list into LDS (slots past
-// klen get weight 0 and the zero row), kFwdPB entries at a time; wave w builds octets w, w+4, ...
-// of each batch for the lane's voxel.  Adds the raw density of the entries to dacc.
-__device__ __forceinline__ void fwd_build_w(FwdSmem& sm, const Grid& G, int j0, int kbeg, int klen,
-                                            int ksteps, bool add_density, float& dacc,
+// klen get weight 0 and the zero row).  The parameters of the chunk's entries are staged in LDS
+// as packed records in one round (one entry per thread; padding entries get an empty box); then
+// wave w builds octets w, w+4, ... for the lane's voxel, branch-free, from broadcast reads.
+// Adds the raw density of the entries to dacc.
+__device__ __forceinline__ void fwd_build_w(FwdSmem& sm, int j0, int kbeg, int klen, int ksteps,
+                                            bool add_density, float& dacc,
                                             const float* __restrict__ means,
                                             const float* __restrict__ opacity,
                                             const float* __restrict__ cov_inv,
@@ -138,38 +150,55 @@ __device__ __forceinline__ void fwd_build_w(FwdSmem& sm, const Grid& G, int j0, 
                                             float cy, float cz) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nslots = ksteps * 16;
-    for (int b0 = 0; b0 < nslots; b0 += kFwdPB) {
-        __syncthreads();   // the previous batch of parameters is consumed
-        stage_params(sm.pt, sorted_gauss + j0 + kbeg + b0, max(0, min(kFwdPB, klen - b0)), means, cov_inv,
-                     opacity, lb, ub);
-        __syncthreads();
-        for (int oc = wave; oc * 8 < min(kFwdPB, nslots - b0); oc += kFwdWaves) {
-            float wv[8];
-#pragma unroll 2
-            for (int i = 0; i < 8; ++i) {
-                const int k = oc * 8 + i;
-                const int g = sm.pt.gid[k];
-                float w = 0.0f;
-                if (g >= 0) {
-                    GaussParams p;
-                    read_params(sm.pt, k, p);
-                    if (in_box(p, x, y, z)) {
-                        float qx, qy, qz;
-                        w = p.o * eval_gauss(p, cx, cy, cz, qx, qy, qz);
-                    }
-                    if (add_density) dacc += w;
-                }
-                wv[i] = (w > 0.0f) ? w : 0.0f;   // feature gate of the reference (.cu:936)
-                if (lane == 0) sm.roff[b0 + k] = g >= 0 ? (uint32_t)g * row_bytes : zero_off;
+    for (int k = threadIdx.x; k < nslots; k += kFwdThreads) {
+        FwdParam r;
+        if (k < klen) {
+            const int g = sorted_gauss[j0 + kbeg + k];
+#pragma unroll
+            for (int a = 0; a < 3; ++a) {
+                r.mu[a] = means[g * 3 + a];
+                r.lb[a] = lb[g * 3 + a];
+                r.ub[a] = ub[g * 3 + a];
             }
-            bf16x8 h, l;
-            split8(wv, h, l);
-            const int o = (b0 >> 3) + oc;     // octet index within the chunk
-            const int s = o >> 1, mb = lane >> 5;
-            const int slot = (o & 1) * 32 + (lane & 31);
-            sm.whi[s][mb][slot] = h;
-            sm.wlo[s][mb][slot] = l;
+#pragma unroll
+            for (int a = 0; a < 9; ++a) r.A[a] = cov_inv[g * 9 + a];
+            r.o = opacity[g];
+            sm.roff[k] = (uint32_t)g * row_bytes;
+        } else {
+#pragma unroll
+            for (int a = 0; a < 3; ++a) { r.mu[a] = 0.0f; r.lb[a] = 1; r.ub[a] = 0; }   // empty box
+#pragma unroll
+            for (int a = 0; a < 9; ++a) r.A[a] = 0.0f;
+            r.o = 0.0f;
+            sm.roff[k] = zero_off;
         }
+        r.pad = 0;
+        sm.par[k] = r;
+    }
+    __syncthreads();
+    const int noct = ksteps * 2;
+    for (int o = wave; o < noct; o += kFwdWaves) {
+        float wv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const FwdParam r = sm.par[o * 8 + i];   // broadcast
+            const bool in = !(x < r.lb[0] || x > r.ub[0] || y < r.lb[1] || y > r.ub[1] || z < r.lb[2] ||
+                              z > r.ub[2]);
+            const float d0 = cx - r.mu[0], d1 = cy - r.mu[1], d2 = cz - r.mu[2];
+            const float qx = r.A[0] * d0 + r.A[1] * d1 + r.A[2] * d2;
+            const float qy = r.A[3] * d0 + r.A[4] * d1 + r.A[5] * d2;
+            const float qz = r.A[6] * d0 + r.A[7] * d1 + r.A[8] * d2;
+            const float m = d0 * qx + d1 * qy + d2 * qz;
+            const float w = in ? r.o * __expf(-0.5f * m) : 0.0f;   // the reference's weight (.cu:911-921)
+            if (add_density) dacc += w;
+            wv[i] = (w > 0.0f) ? w : 0.0f;   // feature gate of the reference (.cu:936)
+        }
+        bf16x8 h, l;
+        split8(wv, h, l);
+        const int s = o >> 1, mb = lane >> 5;
+        const int slot = (o & 1) * 32 + (lane & 31);
+        sm.whi[s][mb][slot] = h;
+        sm.wlo[s][mb][slot] = l;
     }
 }
 
@@ -215,8 +244,8 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
             const int ksteps = ((klen + 31) >> 5) * 2;   // even: the MFMA loop takes steps in pairs
             if (nkc > 1 || cbase == 0) {
                 __syncthreads();  // previous readers of W are done
-                fwd_build_w(sm, G, j0, kbeg, klen, ksteps, cbase == 0, dacc, means, opacity,
-                            cov_inv, lb, ub, sorted_gauss, row_bytes, zero_off, x, y, z, cx, cy, cz);
+                fwd_build_w(sm, j0, kbeg, klen, ksteps, cbase == 0, dacc, means, opacity, cov_inv, lb,
+                            ub, sorted_gauss, row_bytes, zero_off, x, y, z, cx, cy, cz);
                 __syncthreads();
             }
             if (has_ch) {
