@@ -3,8 +3,9 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3] [--no-cpu]
 
-One step = one forward + one backward of the G2V splat through the reference-compatible
-boundary (``_C.gaussian_voxelizer_forward`` then ``_C.gaussian_voxelizer_backward``) on the
+One step = one forward + one backward of the G2V splat through the reference's module
+(``PyCudaGaussianVoxelizer`` forward, then ``torch.autograd.backward`` with the upstream
+gradients; the module's autograd function calls the library through the ``_C`` functions) on the
 benchmark configuration (BASELINE config 3 by default: 18k Gaussians x 1024-D features into a
 200x200x16 grid, all-ones upstream gradients materialised before timing).  Inputs are resident
 in HBM before the timed region; synthetic data from tests/workloads.py.
@@ -150,15 +151,21 @@ def main():
     vs = torch.tensor(w.voxel_size, dtype=torch.float32, device=dev)
     vr = torch.tensor(w.voxel_range, dtype=torch.float32, device=dev)
 
+    # one step = the reference's module (PyCudaGaussianVoxelizer) forward + autograd backward
+    from CudaGaussianVoxelizer import PyCudaGaussianVoxelizer
+    vox = PyCudaGaussianVoxelizer(w.voxel_size, w.voxel_range)
+    leaves = [t.requires_grad_(True) for t in (md, od, cd) + (() if fd is None else (fd,))]
+    outs_grads = [gDd] if C == 0 else [gDd, gFd]
+
     def step():
-        out = _C.gaussian_voxelizer_forward(md, od, cd, vs, vr, fd)
-        g = _C.gaussian_voxelizer_backward(gDd, gFd, md, od, out[1], vs, vr, out[2], out[3], out[4],
-                                           out[6], out[7], out[0], out[5], fd)
-        return out, g
+        for t in leaves:
+            t.grad = None
+        density, grid_feats, stats = vox(md, od, cd, fd)
+        torch.autograd.backward([density] if C == 0 else [density, grid_feats], outs_grads)
+        return stats
 
     for _ in range(args.warmup):
-        out, g = step()
-        del out, g
+        step()
     torch.cuda.synchronize()
     _lib.profile_reset()
     _lib.profile_enable(True)
@@ -166,17 +173,18 @@ def main():
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        out, g = step()
-        fwd_s += out[8]
-        bwd_s += g[4]
-        last = (out, g)
-        del out, g
+        stats = step()
+        fwd_s += float(stats[0])
+        bwd_s += float(stats[1])
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     _lib.profile_enable(False)
     prof = _lib.profile_report()
     ms = (t1 - t0) * 1e3 / args.steps
-    out, g = last
+    # workload statistics (untimed): one more forward through the reference-compatible _C call
+    with torch.no_grad():
+        out = _C.gaussian_voxelizer_forward(md.detach(), od.detach(), cd.detach(), vs, vr,
+                                            None if fd is None else fd.detach())
     N = m.shape[0]
     V = X * Y * Z
     T = Tx * Ty * Tz
@@ -220,7 +228,7 @@ def main():
         host = (m.numpy(), o.numpy(), c.numpy(), None if f is None else f.numpy(), gD.numpy(),
                 None if C == 0 else gF.numpy())
         gpu_out = (out[0].cpu().numpy(), None if C == 0 else out[5].cpu().numpy())
-        del out, g, last
+        del out
         cpu = cpu_baseline(w, host, gpu_out, args.cpu_sample)
 
     flops = 2.0 * P * C + 4.0 * P * C    # forward W.F + backward (G.F^T and W^T.G) contractions

@@ -45,26 +45,34 @@ int g2v_grid_dims(const float voxel_size[3], const float voxel_range[6], int dim
  * Gaussian->Tile CSR is data dependent and the caller allocates g2t_tile_ids:
  *
  * g2v_forward_plan: per-Gaussian box, inverse covariance, voxel count and G->T row offsets
- * (reference .cu:1575-1631).  Synchronises the stream once to return M in *num_pairs. */
+ * (reference .cu:1575-1631).  Synchronises the stream once to return M in *num_pairs.  When
+ * bwd_plan_workspace is non-NULL (g2v_backward_plan_workspace(n) bytes) it also does the work of
+ * g2v_backward_plan into it and returns that pair count in *num_region_pairs on the same
+ * synchronisation, so that the backward needs no plan call of its own. */
 size_t g2v_forward_plan_workspace(int n);
 int g2v_forward_plan(int n, const float* means3D, const float* covariances,
                      const float voxel_size[3], const float voxel_range[6],
                      float* cov_inv, int* valid_voxel_lb, int* valid_voxel_ub,
                      int* num_voxels_per_gaussian, int* g2t_offsets,
-                     void* workspace, size_t workspace_bytes, long long* num_pairs, void* stream);
+                     void* workspace, size_t workspace_bytes, long long* num_pairs,
+                     void* bwd_plan_workspace, size_t bwd_plan_workspace_bytes,
+                     long long* num_region_pairs, void* stream);
 
 /* g2v_forward_splat: G->T fill, radix sort into the Tile->Gaussian CSR, per-tile splat of the
  * density and, when feat_dim > 0, of the density-weighted feature average (reference
  * .cu:1634-1904).  density (X,Y,Z) and grid_feats (X,Y,Z,feat_dim) are written completely;
- * features may be NULL when feat_dim == 0.  Asynchronous. */
+ * features may be NULL when feat_dim == 0.  When t2g_tiles, t2g_gauss (M each) and t2g_offsets
+ * (T+1) are all non-NULL the Tile->Gaussian CSR is built there (and can be handed to
+ * g2v_backward, which then skips rebuilding it); otherwise it lives in the workspace.
+ * Asynchronous. */
 size_t g2v_forward_splat_workspace(int n, int feat_dim, long long num_pairs, const float voxel_size[3],
                                    const float voxel_range[6]);
 int g2v_forward_splat(int n, int feat_dim, const float* means3D, const float* opacity,
                       const float* features, const float voxel_size[3], const float voxel_range[6],
                       const float* cov_inv, const int* valid_voxel_lb, const int* valid_voxel_ub,
                       const int* g2t_offsets, long long num_pairs, int* g2t_tile_ids,
-                      float* density, float* grid_feats,
-                      void* workspace, size_t workspace_bytes, void* stream);
+                      float* density, float* grid_feats, int* t2g_tiles, int* t2g_gauss,
+                      int* t2g_offsets, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- backward -----------------------------------------------------------------------------
  * Replaces cuda_gaussian_voxelizer_backward (src/cuda_gaussian_voxelizer.cu:1920-2057, bound at
@@ -80,8 +88,11 @@ int g2v_backward_plan(int n, int feat_dim, const float voxel_size[3], const floa
 
 /* g2v_backward: writes grad_means (N,3), grad_cov (N,9, symmetric), grad_opacity (N,) and, when
  * feat_dim > 0, grad_features (N,feat_dim).  grad_feats/grid_feats/features may be NULL when
- * feat_dim == 0.  plan_workspace is the one given to g2v_backward_plan.  Asynchronous;
- * atomic-free and deterministic. */
+ * feat_dim == 0.  plan_workspace is the one given to g2v_backward_plan.  t2g_tiles, t2g_gauss
+ * and t2g_offsets may carry the Tile->Gaussian CSR written by g2v_forward_splat for the same
+ * Gaussians (all three non-NULL); with NULL it is rebuilt from g2t_offsets/g2t_tile_ids, as the
+ * reference's backward signature provides only those.  Asynchronous; atomic-free and
+ * deterministic. */
 size_t g2v_backward_workspace(int n, int feat_dim, long long num_pairs, long long num_region_pairs,
                               const float voxel_size[3], const float voxel_range[6]);
 int g2v_backward(int n, int feat_dim, const float* grad_density, const float* grad_feats,
@@ -92,6 +103,7 @@ int g2v_backward(int n, int feat_dim, const float* grad_density, const float* gr
                  const int* g2t_tile_ids, long long num_pairs, long long num_region_pairs,
                  const float* density, const float* grid_feats, const float* features,
                  float* grad_means, float* grad_cov, float* grad_opacity, float* grad_features,
+                 const int* t2g_tiles, const int* t2g_gauss, const int* t2g_offsets,
                  const void* plan_workspace, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- Tile->Gaussian CSR (inspection) -------------------------------------------------------

@@ -83,6 +83,13 @@ def gaussian_voxelizer_forward(means3D, opacity, covariances, voxel_size, voxel_
         num_voxels_per_gaussian (N,) int32, grid_feats (X,Y,Z,C) (C = 0 without features),
         g2t_offsets (N+1,) int32, g2t_tile_ids (M,) int32, forward time in seconds.
     """
+    return _forward(means3D, opacity, covariances, voxel_size, voxel_range, features, keep_t2g=False)[0]
+
+
+def _forward(means3D, opacity, covariances, voxel_size, voxel_range, features, keep_t2g):
+    """The forward; with keep_t2g it also returns, beside the 9-tuple, what the backward would
+    otherwise recompute: the Tile->Gaussian CSR (sorted tiles, sorted Gaussians, tile offsets) and
+    the backward plan (region pair offsets and their count, counted on the plan's one sync)."""
     lib = _lib.load()
     means = _f32_input(means3D, "means3D")
     if means.dim() != 2 or means.shape[1] != 3:
@@ -120,24 +127,36 @@ def gaussian_voxelizer_forward(means3D, opacity, covariances, voxel_size, voxel_
         stop = torch.cuda.Event(enable_timing=True)
         start.record(cur)
         M = ctypes.c_longlong(0)
+        MR = ctypes.c_longlong(0)
+        # with keep_t2g the backward's plan (the (region, Gaussian) pair count) is done here too,
+        # on the same synchronisation
+        bplan = (torch.empty(max(1, lib.g2v_backward_plan_workspace(n)), dtype=torch.uint8, device=dev)
+                 if keep_t2g else None)
         _lib.check(lib.g2v_forward_plan(n, _ptr(means), _ptr(cov), vs, vr, _ptr(cov_inv), _ptr(lb),
                                         _ptr(ub), _ptr(nvox), _ptr(g2t_offsets), _ptr(ws),
-                                        ws.numel(), ctypes.byref(M), stream),
+                                        ws.numel(), ctypes.byref(M), _ptr(bplan),
+                                        0 if bplan is None else bplan.numel(), ctypes.byref(MR), stream),
                    "gaussian_voxelizer_forward (plan)")
         M = int(M.value)
         g2t_tile_ids = torch.empty(M, **i32)
         density = torch.empty(X, Y, Z, **f32)
         grid_feats = torch.empty(X, Y, Z, C, **f32)
         ws2 = torch.empty(lib.g2v_forward_splat_workspace(n, C, M, vs, vr), dtype=torch.uint8, device=dev)
+        t2g = None
+        if keep_t2g:
+            (_, (Tx, Ty, Tz)) = grid_dims(vs_h, vr_h)
+            t2g = dict(csr=(torch.empty(M, **i32), torch.empty(M, **i32), torch.empty(Tx * Ty * Tz + 1, **i32)),
+                       plan=bplan, num_region_pairs=int(MR.value))
         _lib.check(lib.g2v_forward_splat(n, C, _ptr(means), _ptr(op), _ptr(feats), vs, vr,
                                          _ptr(cov_inv), _ptr(lb), _ptr(ub), _ptr(g2t_offsets), M,
                                          _ptr(g2t_tile_ids), _ptr(density), _ptr(grid_feats),
+                                         *(_ptr(t) for t in (t2g["csr"] if t2g else (None, None, None))),
                                          _ptr(ws2), ws2.numel(), stream),
                    "gaussian_voxelizer_forward (splat)")
         stop.record(cur)
         stop.synchronize()
         fwd_sec = start.elapsed_time(stop) / 1000.0
-    return (density, cov_inv, lb, ub, nvox, grid_feats, g2t_offsets, g2t_tile_ids, fwd_sec)
+    return (density, cov_inv, lb, ub, nvox, grid_feats, g2t_offsets, g2t_tile_ids, fwd_sec), t2g
 
 
 def gaussian_voxelizer_backward(grad_output, grad_feats_output, means3D, opacity, cov_inv, voxel_size,
@@ -148,6 +167,15 @@ def gaussian_voxelizer_backward(grad_output, grad_feats_output, means3D, opacity
     Returns the reference's 5-tuple: grad_means (N,3), grad_cov (N,9), grad_opacity (N,),
     grad_feats (N,C) (N,0 without features), backward time in seconds.
     """
+    return _backward(grad_output, grad_feats_output, means3D, opacity, cov_inv, voxel_size, voxel_range,
+                     valid_voxel_lb, valid_voxel_ub, num_voxels_per_gaussian, g2t_offsets, g2t_tile_ids,
+                     density, grid_feats, features, t2g=None)
+
+
+def _backward(grad_output, grad_feats_output, means3D, opacity, cov_inv, voxel_size, voxel_range,
+              valid_voxel_lb, valid_voxel_ub, num_voxels_per_gaussian, g2t_offsets, g2t_tile_ids,
+              density, grid_feats, features, t2g):
+    """The backward; t2g is what _forward(keep_t2g=True) returned beside the 9-tuple, or None."""
     lib = _lib.load()
     if not isinstance(means3D, torch.Tensor) or means3D.device.type != "cuda":
         raise RuntimeError("means3D must be a GPU tensor")
@@ -189,22 +217,26 @@ def gaussian_voxelizer_backward(grad_output, grad_feats_output, means3D, opacity
         grad_cov = torch.empty(n, 9, dtype=f32, device=dev)
         grad_opacity = torch.empty(n, dtype=f32, device=dev)
         grad_feats = torch.empty(n, C, dtype=f32, device=dev)
-        plan_ws = torch.empty(max(1, lib.g2v_backward_plan_workspace(n)), dtype=torch.uint8, device=dev)
         start = torch.cuda.Event(enable_timing=True)
         stop = torch.cuda.Event(enable_timing=True)
         start.record(cur)
-        MR = ctypes.c_longlong(0)
-        _lib.check(lib.g2v_backward_plan(n, C, vs, vr, _ptr(valid_voxel_lb), _ptr(valid_voxel_ub), _ptr(plan_ws),
-                                         plan_ws.numel(), ctypes.byref(MR), stream),
-                   "gaussian_voxelizer_backward (plan)")
-        MR = int(MR.value)
+        if t2g is not None and C > 0:   # planned by the forward
+            plan_ws, MR = t2g["plan"], t2g["num_region_pairs"]
+        else:
+            plan_ws = torch.empty(max(1, lib.g2v_backward_plan_workspace(n)), dtype=torch.uint8, device=dev)
+            MR = ctypes.c_longlong(0)
+            _lib.check(lib.g2v_backward_plan(n, C, vs, vr, _ptr(valid_voxel_lb), _ptr(valid_voxel_ub),
+                                             _ptr(plan_ws), plan_ws.numel(), ctypes.byref(MR), stream),
+                       "gaussian_voxelizer_backward (plan)")
+            MR = int(MR.value)
         ws = torch.empty(max(1, lib.g2v_backward_workspace(n, C, M, MR, vs, vr)), dtype=torch.uint8, device=dev)
         _lib.check(lib.g2v_backward(n, C, _ptr(grad_output), _ptr(gF), _ptr(means3D), _ptr(opacity),
                                     _ptr(cov_inv), vs, vr, _ptr(valid_voxel_lb), _ptr(valid_voxel_ub),
                                     _ptr(num_voxels_per_gaussian), _ptr(g2t_offsets), _ptr(g2t_tile_ids),
                                     M, MR, _ptr(density), _ptr(grid_feats), _ptr(feats),
                                     _ptr(grad_means), _ptr(grad_cov), _ptr(grad_opacity),
-                                    _ptr(grad_feats), _ptr(plan_ws), _ptr(ws), ws.numel(), stream),
+                                    _ptr(grad_feats), *(_ptr(t) for t in (t2g["csr"] if t2g else (None, None, None))),
+                                    _ptr(plan_ws), _ptr(ws), ws.numel(), stream),
                    "gaussian_voxelizer_backward")
         stop.record(cur)
         stop.synchronize()

@@ -22,14 +22,18 @@ class _CudaGaussianVoxelizeFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, means3D, opacity, covariances, voxel_size, voxel_range, features):
+        # with features the backward reuses the forward's Tile->Gaussian CSR (kept beside the
+        # reference's saved tensors) instead of re-sorting the G->T pairs
+        keep = features is not None and features.shape[-1] > 0
         (density, cov_inv, valid_voxel_lb, valid_voxel_ub, num_valid_voxel, grid_feats, g2t_offsets,
-         g2t_tile_ids, fwd_sec) = gaussian_voxelizer_forward(means3D, opacity, covariances, voxel_size,
-                                                             voxel_range, features)
+         g2t_tile_ids, fwd_sec), t2g = _C._forward(means3D, opacity, covariances, voxel_size,
+                                                   voxel_range, features, keep_t2g=keep)
         stats = torch.zeros(2, dtype=torch.float32, device="cpu")
         stats[0] = fwd_sec
         ctx.save_for_backward(means3D, opacity, voxel_size, voxel_range, cov_inv, valid_voxel_lb,
                               valid_voxel_ub, num_valid_voxel, g2t_offsets, g2t_tile_ids, density,
                               grid_feats, features, stats)
+        ctx.t2g = t2g
         ctx.mark_non_differentiable(stats)
         ctx.opacity_shape = opacity.shape
         ctx.cov_shape = covariances.shape
@@ -44,9 +48,11 @@ class _CudaGaussianVoxelizeFunction(torch.autograd.Function):
         means32 = means32.detach().contiguous()
         op32 = op32.detach().reshape(-1).contiguous()
         feats = None if features is None else features.detach().contiguous()
-        grad_means3D, grad_cov, grad_opacity, grad_feats, bwd_sec = gaussian_voxelizer_backward(
+        grad_means3D, grad_cov, grad_opacity, grad_feats, bwd_sec = _C._backward(
             gout32, grad_feats_output, means32, op32, cov_inv, voxsz32, voxrg32, valid_voxel_lb,
-            valid_voxel_ub, num_valid_voxel, g2t_offsets, g2t_tile_ids, density, grid_feats, feats)
+            valid_voxel_ub, num_valid_voxel, g2t_offsets, g2t_tile_ids, density, grid_feats, feats,
+            t2g=ctx.t2g)
+        ctx.t2g = None
         stats[1] = bwd_sec
         # gradients take the shapes of the inputs ((N,) or (N,1) opacity, (N,9) or (N,3,3) cov)
         grad_opacity = grad_opacity.reshape(ctx.opacity_shape)

@@ -24,15 +24,16 @@ SIGNATURES = {
     "g2v_abi_version": (_i, []),
     "g2v_grid_dims": (_i, [_f3, _f3, _ip, _ip]),
     "g2v_forward_plan_workspace": (_sz, [_i]),
-    "g2v_forward_plan": (_i, [_i, _vp, _vp, _f3, _f3, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _llp, _vp]),
+    "g2v_forward_plan": (_i, [_i, _vp, _vp, _f3, _f3, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _llp, _vp, _sz, _llp,
+                              _vp]),
     "g2v_forward_splat_workspace": (_sz, [_i, _i, _ll, _f3, _f3]),
     "g2v_forward_splat": (_i, [_i, _i, _vp, _vp, _vp, _f3, _f3, _vp, _vp, _vp, _vp, _ll, _vp, _vp,
-                               _vp, _vp, _sz, _vp]),
+                               _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "g2v_backward_plan_workspace": (_sz, [_i]),
     "g2v_backward_plan": (_i, [_i, _i, _f3, _f3, _vp, _vp, _vp, _sz, _llp, _vp]),
     "g2v_backward_workspace": (_sz, [_i, _i, _ll, _ll, _f3, _f3]),
     "g2v_backward": (_i, [_i, _i, _vp, _vp, _vp, _vp, _vp, _f3, _f3, _vp, _vp, _vp, _vp, _vp, _ll, _ll,
-                          _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+                          _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "g2v_t2g_workspace": (_sz, [_i, _ll, _f3, _f3]),
     "g2v_build_t2g": (_i, [_i, _f3, _f3, _vp, _vp, _vp, _vp, _ll, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                            _vp, _sz, _vp]),

@@ -813,19 +813,23 @@ static PlanBufs carve_plan(void* ws, int n) {
 
 size_t backward_plan_workspace(int n) { return carve_plan(nullptr, n).bytes; }
 
-hipError_t backward_plan(const Grid& G, int n, const int* lb, const int* ub, void* plan_ws,
-                         long long* num_region_pairs, hipStream_t s) {
+hipError_t backward_plan_async(const Grid& G, int n, const int* lb, const int* ub, void* plan_ws,
+                               long long* mr_host, hipStream_t s) {
     const Regions RG = make_regions(G);
     const PlanBufs b = carve_plan(plan_ws, n);
+    *mr_host = 0;
     hipError_t e = launch_cell_count(n, lb, ub, RG.cell, b.g2r_offsets, s);
+    if (e != hipSuccess || n <= 0) return e;
+    e = scan_i32(b.g2r_offsets + 1, b.g2r_offsets + 1, n, true, b.total, b.scan_ws, s);
     if (e != hipSuccess) return e;
+    return hipMemcpyAsync(mr_host, b.total, sizeof(long long), hipMemcpyDeviceToHost, s);
+}
+
+hipError_t backward_plan(const Grid& G, int n, const int* lb, const int* ub, void* plan_ws,
+                         long long* num_region_pairs, hipStream_t s) {
     long long MR = 0;
-    if (n > 0) {
-        e = scan_i32(b.g2r_offsets + 1, b.g2r_offsets + 1, n, true, b.total, b.scan_ws, s);
-        if (e != hipSuccess) return e;
-        e = hipMemcpyAsync(&MR, b.total, sizeof(long long), hipMemcpyDeviceToHost, s);
-        if (e != hipSuccess) return e;
-    }
+    hipError_t e = backward_plan_async(G, n, lb, ub, plan_ws, &MR, s);
+    if (e != hipSuccess) return e;
     e = hipStreamSynchronize(s);
     *num_region_pairs = MR;
     return e;

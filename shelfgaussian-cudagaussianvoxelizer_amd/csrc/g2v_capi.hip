@@ -105,7 +105,7 @@ extern "C" {
 
 const char* g2v_last_error(void) { return g_err; }
 
-int g2v_abi_version(void) { return 1; }
+int g2v_abi_version(void) { return 2; }
 
 int g2v_grid_dims(const float voxel_size[3], const float voxel_range[6], int dims[3], int tiles[3]) {
     Grid G;
@@ -129,10 +129,16 @@ int g2v_forward_plan(int n, const float* means3D, const float* covariances,
                      const float voxel_size[3], const float voxel_range[6], float* cov_inv,
                      int* valid_voxel_lb, int* valid_voxel_ub, int* num_voxels_per_gaussian,
                      int* g2t_offsets, void* workspace, size_t workspace_bytes,
-                     long long* num_pairs, void* stream) {
+                     long long* num_pairs, void* bwd_plan_workspace, size_t bwd_plan_workspace_bytes,
+                     long long* num_region_pairs, void* stream) {
     g_err[0] = 0;
     if (n < 0) return fail(G2V_ERR_INVALID, "n = %d", n);
     if (!num_pairs || !g2t_offsets) return fail(G2V_ERR_INVALID, "num_pairs / g2t_offsets null");
+    if (bwd_plan_workspace && !num_region_pairs)
+        return fail(G2V_ERR_INVALID, "bwd_plan_workspace needs num_region_pairs");
+    if (bwd_plan_workspace && bwd_plan_workspace_bytes < backward_plan_workspace(n > 0 ? n : 0))
+        return fail(G2V_ERR_INVALID, "backward plan workspace too small: %zu < %zu bytes",
+                    bwd_plan_workspace_bytes, backward_plan_workspace(n > 0 ? n : 0));
     if (n > 0 && (!means3D || !covariances || !cov_inv || !valid_voxel_lb || !valid_voxel_ub ||
                   !num_voxels_per_gaussian))
         return fail(G2V_ERR_INVALID, "null input/output pointer");
@@ -148,15 +154,21 @@ int g2v_forward_plan(int n, const float* means3D, const float* covariances,
 
     G2V_HIP(launch_boxes(G, n, means3D, covariances, cov_inv, valid_voxel_lb, valid_voxel_ub,
                          num_voxels_per_gaussian, g2t_offsets, s));
-    long long M = 0;
+    long long M = 0, MR = 0;
     if (n > 0) {
         G2V_HIP(scan_i32(g2t_offsets + 1, g2t_offsets + 1, n, true, total, scan_ws, s));
         G2V_HIP(hipMemcpyAsync(&M, total, sizeof(long long), hipMemcpyDeviceToHost, s));
     }
+    // the backward's (region, Gaussian) pair count rides on the same synchronisation
+    if (bwd_plan_workspace)
+        G2V_HIP(backward_plan_async(G, n, valid_voxel_lb, valid_voxel_ub, bwd_plan_workspace, &MR, s));
     G2V_HIP(hipStreamSynchronize(s));
     if (M > 2147483647ll)
         return fail(G2V_ERR_LIMIT, "%lld Gaussian-tile pairs exceed the int32 CSR (limit 2^31-1)", M);
+    if (MR > 2147483647ll)
+        return fail(G2V_ERR_LIMIT, "%lld region-Gaussian pairs exceed the int32 CSR", MR);
     *num_pairs = M;
+    if (num_region_pairs) *num_region_pairs = bwd_plan_workspace ? MR : 0;
     return G2V_OK;
 }
 
@@ -171,8 +183,8 @@ int g2v_forward_splat(int n, int feat_dim, const float* means3D, const float* op
                       const float* features, const float voxel_size[3], const float voxel_range[6],
                       const float* cov_inv, const int* valid_voxel_lb, const int* valid_voxel_ub,
                       const int* g2t_offsets, long long num_pairs, int* g2t_tile_ids,
-                      float* density, float* grid_feats, void* workspace, size_t workspace_bytes,
-                      void* stream) {
+                      float* density, float* grid_feats, int* t2g_tiles, int* t2g_gauss,
+                      int* t2g_offsets, void* workspace, size_t workspace_bytes, void* stream) {
     g_err[0] = 0;
     if (n < 0 || feat_dim < 0 || num_pairs < 0)
         return fail(G2V_ERR_INVALID, "n = %d, feat_dim = %d, num_pairs = %lld", n, feat_dim, num_pairs);
@@ -193,7 +205,12 @@ int g2v_forward_splat(int n, int feat_dim, const float* means3D, const float* op
     const SplatBufs need = carve_splat(nullptr, n, num_pairs, G, feat_dim);
     rc = check_ws(workspace, workspace_bytes, need.bytes, "splat");
     if (rc != G2V_OK) return rc;
-    const SplatBufs b = carve_splat(workspace, n, num_pairs, G, feat_dim);
+    SplatBufs b = carve_splat(workspace, n, num_pairs, G, feat_dim);
+    if (t2g_tiles && t2g_gauss && t2g_offsets) {   // the caller keeps the Tile->Gaussian CSR
+        b.sorted_tiles = t2g_tiles;
+        b.sorted_gauss = t2g_gauss;
+        b.tile_offsets = t2g_offsets;
+    }
     hipStream_t s = static_cast<hipStream_t>(stream);
     rc = build_t2g(G, n, valid_voxel_lb, valid_voxel_ub, g2t_offsets, g2t_tile_ids, nullptr,
                    num_pairs, b, s);
@@ -251,7 +268,8 @@ int g2v_backward(int n, int feat_dim, const float* grad_density, const float* gr
                  const int* g2t_offsets, const int* g2t_tile_ids, long long num_pairs,
                  long long num_region_pairs, const float* density, const float* grid_feats,
                  const float* features, float* grad_means, float* grad_cov, float* grad_opacity,
-                 float* grad_features, const void* plan_workspace, void* workspace,
+                 float* grad_features, const int* t2g_tiles, const int* t2g_gauss,
+                 const int* t2g_offsets, const void* plan_workspace, void* workspace,
                  size_t workspace_bytes, void* stream) {
     g_err[0] = 0;
     (void)num_voxels_per_gaussian;
@@ -285,10 +303,16 @@ int g2v_backward(int n, int feat_dim, const float* grad_density, const float* gr
     Carver c(workspace, workspace_bytes);
     void* splat_ws = c.take<char>(carve_splat(nullptr, n, num_pairs, G).bytes);
     void* feats_ws = c.take<char>(backward_feats_workspace(G, n, feat_dim, num_pairs, num_region_pairs));
-    const SplatBufs b = carve_splat(splat_ws, n, num_pairs, G);
-    rc = build_t2g(G, n, valid_voxel_lb, valid_voxel_ub, g2t_offsets, nullptr, g2t_tile_ids,
-                   num_pairs, b, s);
-    if (rc != G2V_OK) return rc;
+    SplatBufs b = carve_splat(splat_ws, n, num_pairs, G);
+    if (t2g_tiles && t2g_gauss && t2g_offsets) {   // the forward's Tile->Gaussian CSR
+        b.sorted_tiles = const_cast<int*>(t2g_tiles);
+        b.sorted_gauss = const_cast<int*>(t2g_gauss);
+        b.tile_offsets = const_cast<int*>(t2g_offsets);
+    } else {
+        rc = build_t2g(G, n, valid_voxel_lb, valid_voxel_ub, g2t_offsets, nullptr, g2t_tile_ids,
+                       num_pairs, b, s);
+        if (rc != G2V_OK) return rc;
+    }
     G2V_HIP(launch_backward_feats(G, n, feat_dim, grad_density, grad_feats, means3D, opacity, cov_inv,
                                   valid_voxel_lb, valid_voxel_ub, g2t_offsets, num_pairs,
                                   b.tile_offsets, b.sorted_tiles, b.sorted_gauss, density, grid_feats, features,

@@ -90,6 +90,9 @@ size_t backward_plan_workspace(int n);
 // Counts the (region, Gaussian) pairs of the feature-gradient phase; synchronises the stream.
 hipError_t backward_plan(const Grid& G, int n, const int* lb, const int* ub, void* plan_ws,
                          long long* num_region_pairs, hipStream_t s);
+// The same without the synchronisation: the count lands in *mr_host once the stream reaches it.
+hipError_t backward_plan_async(const Grid& G, int n, const int* lb, const int* ub, void* plan_ws,
+                               long long* mr_host, hipStream_t s);
 size_t backward_feats_workspace(const Grid& G, int n, int C, int64_t M, int64_t MR);
 hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_density,
                                  const float* grad_feats, const float* means, const float* opacity,

@@ -31,7 +31,7 @@ def test_header_symbols_exported():
 
 
 def test_abi_version():
-    assert _lib().load().g2v_abi_version() == 1
+    assert _lib().load().g2v_abi_version() == 2
 
 
 @pytest.mark.parametrize("vs,vr", [
@@ -62,21 +62,21 @@ def test_invalid_arguments_fail_before_any_launch():
     M = ctypes.c_longlong(0)
     # negative N
     rc = lib.g2v_forward_plan(-1, None, None, vs, vr, None, None, None, None, None, None, 0,
-                              ctypes.byref(M), None)
+                              ctypes.byref(M), None, 0, None, None)
     assert rc == 1 and b"n = -1" in lib.g2v_last_error()
     # too many pairs for the int32 CSR
     rc = lib.g2v_forward_splat(1, 0, None, None, None, vs, vr, None, None, None, None, 1 << 31,
-                               None, None, None, None, 0, None)
+                               None, None, None, None, None, None, None, 0, None)
     assert rc == 3
     # missing workspace
     rc = lib.g2v_forward_splat(0, 0, None, None, None, vs, vr, None, None, None, None, 0, None,
-                               ctypes.c_void_p(16), None, None, 0, None)
+                               ctypes.c_void_p(16), None, None, None, None, None, 0, None)
     assert rc == 1 and b"workspace" in lib.g2v_last_error()
     # features requested without tensors
     rc = lib.g2v_backward(4, 8, ctypes.c_void_p(16), None, ctypes.c_void_p(16), ctypes.c_void_p(16),
                           ctypes.c_void_p(16), vs, vr, ctypes.c_void_p(16), ctypes.c_void_p(16), None,
                           None, None, 0, 0, None, None, None, ctypes.c_void_p(16), ctypes.c_void_p(16),
-                          ctypes.c_void_p(16), None, None, None, 0, None)
+                          ctypes.c_void_p(16), None, None, None, None, None, None, 0, None)
     assert rc == 1 and b"feat_dim" in lib.g2v_last_error()
 
 

@@ -274,6 +274,31 @@ def test_autograd_module_end_to_end():
     d3.sum().backward()
 
 
+def test_module_reuse_of_forward_csr_matches_rebuild():
+    """The module hands the forward's Tile->Gaussian CSR and backward plan to the backward; the
+    reference-signature backward rebuilds both.  Same kernels, same order: identical bits."""
+    from CudaGaussianVoxelizer import PyCudaGaussianVoxelizer
+    dev = torch.device("cuda")
+    w = W.Workload("reuse", 2500, 40, voxel_range=W.RANGE_SMALL, num_outside=30)
+    m, o, c, f = _scene(w, seed=11)
+    say("[reuse] module vs _C backward")
+    vox = PyCudaGaussianVoxelizer(voxel_size=list(w.voxel_size), voxel_range=list(w.voxel_range))
+    leaves = [t.to(dev).requires_grad_() for t in (m, o, c, f)]
+    density, grid_feats, _ = vox(*leaves)
+    gD = torch.randn(*density.shape, device=dev)
+    gF = torch.randn(*grid_feats.shape, device=dev)
+    torch.autograd.backward([density, grid_feats], [gD, gF])
+    a = _gpu_forward(w, m, o, c, f)
+    assert torch.equal(a[0], density.detach()) and torch.equal(a[5], grid_feats.detach())
+    vs, vr = torch.tensor(w.voxel_size, device=dev), torch.tensor(w.voxel_range, device=dev)
+    g = _C().gaussian_voxelizer_backward(gD, gF, m.to(dev), o.to(dev), a[1], vs, vr, a[2], a[3], a[4], a[6],
+                                         a[7], a[0], a[5], f.to(dev))
+    assert torch.equal(g[0], leaves[0].grad)
+    assert torch.equal(g[1], leaves[2].grad.reshape(-1, 9))
+    assert torch.equal(g[2], leaves[1].grad)
+    assert torch.equal(g[3], leaves[3].grad)
+
+
 def test_input_errors_raise():
     dev = torch.device("cuda")
     C = _C()
