@@ -20,6 +20,7 @@
 //                    of its region partial rows.
 // Without features, k_bwd_density walks each Gaussian's box with one wave.
 #include "g2v_internal.h"
+#include <type_traits>
 
 namespace g2v {
 
@@ -544,59 +545,246 @@ __global__ void __launch_bounds__(256) k_region_table(Grid G, Regions RG, int M,
 // ------------------------------------------------------------------------------------------
 // Phase B: per-region partial feature gradients, accumulated in registers.
 //
-// Work item = (region, 128-channel chunk); 8 waves.  Wave w owns 32 rows of the region's
-// Gaussian list (rows 256p + 32w .. +31 in pass p) and 128 channels: 4 accumulator blocks of
-// 32 x 32.  For every tile of the region the tile's gF chunk (64 voxels x 128 channels) is staged
-// in LDS, split hi/lo in the MFMA B layout, and each wave adds
-//     (its 32 rows x 64 voxels of split pair weights) . (64 voxels x 128 channels)
-// where a row whose Gaussian does not touch the tile reads the zero row of the weights.  Every
-// row is owned by one lane set and summed over the tiles in a fixed order: no atomics, no LDS
-// accumulators.  Software pipeline one tile ahead: while tile k is multiplied, the weights of
-// tile k+1 are loaded into the other register set, the gF values of tile k+1 are written to the
-// other LDS buffer, and the gF values of tile k+2 are loaded into registers.
+// Work item = (region, 128-channel chunk); 8 waves.  A pass covers up to 384 rows of the region's
+// Gaussian list in 16-row blocks; block b of the pass belongs to wave b % 8, so a wave owns
+// RB = ceil(blocks / 8) or one fewer blocks (RB <= 3) and every wave's work follows the row
+// count, not a fixed 256-row step.  For every tile of the region the tile's gF chunk (64 voxels x
+// 128 channels) is staged in LDS, split hi/lo in the MFMA B layout, and each wave adds
+//     (its rows x 64 voxels of split pair weights) . (64 voxels x 128 channels)
+// with 16 x 16 x 32 MFMAs, where a row whose Gaussian does not touch the tile reads the zero row
+// of the weights.  Every row is owned by one lane set and summed over the tiles in a fixed order:
+// no atomics, no LDS accumulators.  Software pipeline one tile ahead: while tile k is
+// multiplied, the weights of tile k+1 are loaded into the other register set, the gF values of
+// tile k+1 are written to the other LDS buffer, and the gF values of tile k+2 are loaded into
+// registers.
 // ------------------------------------------------------------------------------------------
 constexpr int kBrThreads = 512;   // 8 waves
 constexpr int kBrWaves = kBrThreads / 64;
 constexpr int kBrCc = 128;        // channels per work item
-constexpr int kBrPass = kBrWaves * 32;   // region rows per pass
-static_assert(kBrPass * kBrSlots % kBrThreads == 0 && kBrPass <= kBrThreads, "row-table staging shape");
+constexpr int kBrCb = kBrCc / 16; // 16-channel MFMA column blocks
+constexpr int kBrRbMax = 3;       // 16-row blocks per wave and pass
+constexpr int kBrPass = kBrWaves * kBrRbMax * 16;   // region rows per pass
+static_assert(kBrPass * kBrSlots % kBrThreads == 0 && kBrPass <= 2 * kBrThreads, "row-table staging shape");
 
 struct BrSmem {
-    bf16x8 bhi[2][4][4][64];   // B operand (gF chunk): [buffer][k step of 16 voxels][channel block][lane]
-    bf16x8 blo[2][4][4][64];
+    bf16x8 bhi[2][2][kBrCb][64];   // B operand (gF chunk): [buffer][k step of 32 voxels][channel block][lane]
+    bf16x8 blo[2][2][kBrCb][64];
     int tab[kBrPass][kBrSlots];           // row table of this pass's rows (M: absent pair)
     int rslot[kBrPass];                   // G->R slot of each row of the pass
     int tl_t[kBrSlots], tl_s[kBrSlots];   // tiles of the region (inside the grid) and their slots
     int ntl;
 };
 
-// gF of one tile for the staging thread (channel c of the chunk, voxel octets o0 and o0 + 4).
-// The loads are unconditional (indices clamped into the grid); bit i + 8k of the returned mask
-// marks value v[k][i] as real.
-__device__ __forceinline__ unsigned br_load_tile(const Grid& G, int C, int c0, int t, int c, int o0,
+// gF chunk of one tile for the staging thread: channel sc of the chunk, voxel octets so and
+// so + 4 (tile-local x = 2k + so/2, y = 2(so&1) + i/4, z = i%4 for value v[k][i]).  Buffer loads
+// from the tile origin: a per-thread offset for each (x, y) pair and a uniform offset for each z.
+// Coordinates are clamped into the grid, so every load stays inside gF (the descriptor's range
+// ends at gF's end as well); bit i + 8k of the returned mask marks the values that are real.
+// Offsets need 16 * Y * Z * C < 2^32 (checked on the host).
+__device__ __forceinline__ unsigned br_load_tile(const Grid& G, int C, int c0, int t, int sc, int so,
                                                  const float* __restrict__ gF, float (&v)[2][8]) {
     const int tyz = G.tiles[1] * G.tiles[2];
     const int tx = t / tyz, ty = (t - tx * tyz) / G.tiles[2], tz = t % G.tiles[2];
-    const int64_t Y = G.dims[1], Z = G.dims[2];
-    const bool cok = c0 + c < C;
-    const float* p = gF + min(c0 + c, C - 1);
-    unsigned mask = 0;
+    const int x0 = tx * kTile, y0 = ty * kTile, z0 = tz * kTile;
+    const int X = G.dims[0], Y = G.dims[1], Z = G.dims[2];
+    const int64_t origin = ((int64_t)(x0 * Y + y0) * Z + z0) * C + c0;
+    const int64_t left = ((int64_t)X * Y * Z * C - origin) * 4;
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(gF + origin), (short)0, (int)min(left, (int64_t)0x7fffffff), 0x00020000);
+    const bool cok = c0 + sc < C;
+    const unsigned cc = (unsigned)(min(c0 + sc, C - 1) - c0);
+    unsigned voff[2][2];
+    bool xok[2], yok[2];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-        const int o = o0 + 4 * k;
-        const int x = tx * kTile + (o >> 1);
-        const int y0 = ty * kTile + ((o & 1) << 1);
-        const int z0 = tz * kTile;
-        const int64_t xc = min(x, G.dims[0] - 1);
+        const int x = x0 + 2 * k + (so >> 1);
+        xok[k] = x < X;
+        const unsigned xl = (unsigned)(min(x, X - 1) - x0);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int y = y0 + (i >> 2), z = z0 + (i & 3);
-            const int64_t yc = min(y, G.dims[1] - 1), zc = min(z, G.dims[2] - 1);
-            v[k][i] = p[((xc * Y + yc) * Z + zc) * C];
-            mask |= (cok && x < G.dims[0] && y < G.dims[1] && z < G.dims[2]) ? (1u << (i + 8 * k)) : 0u;
+        for (int h = 0; h < 2; ++h) {
+            const int y = y0 + 2 * (so & 1) + h;
+            if (k == 0) yok[h] = y < Y;
+            const unsigned yl = (unsigned)(min(y, Y - 1) - y0);
+            voff[k][h] = ((xl * Y + yl) * Z * C + cc) * 4u;
         }
     }
+    int soff[4];
+    bool zok[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        zok[i] = z0 + i < Z;
+        soff[i] = (min(z0 + i, Z - 1) - z0) * C * 4;
+    }
+    unsigned mask = 0;
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            v[k][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff[k][i >> 2], soff[i & 3], 0));
+            mask |= (cok && xok[k] && yok[i >> 2] && zok[i & 3]) ? (1u << (i + 8 * k)) : 0u;
+        }
     return mask;
+}
+
+// Tile loop of one phase-B pass for a wave that owns NB row blocks (pass blocks wave + 8b,
+// b < NB; NB may be 0).  Every wave runs the same staging work and the same sequence of
+// barriers, whatever its NB, so waves of one workgroup may run different instantiations.  The
+// weights of a tile (A operand) are held once per wave: those of k step s for tile k+1 are
+// loaded as soon as the MFMAs of k step s of tile k are issued.  LDS hand-offs use lds_barrier,
+// so loads stay in flight across the barrier and the compiler waits for each where its registers
+// are used.
+template <int NB>
+__device__ __forceinline__ void br_tiles(BrSmem& sm, const Grid& G, int C, int c0, int ntl, int prow,
+                                         const float* __restrict__ gF, const __bf16* __restrict__ wt,
+                                         float* __restrict__ gpart) {
+    constexpr int NR = NB > 0 ? NB : 1;   // register arrays (unused when NB == 0)
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sc = threadIdx.x & (kBrCc - 1), so = threadIdx.x >> 7;   // staging: channel, octets so, so+4
+    const int q = lane >> 4, cl = lane & 15;
+
+    float pre[2][8];
+    unsigned pmask = 0;
+    auto stage = [&](int buf) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            float u[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) u[i] = (pmask >> (i + 8 * k)) & 1u ? pre[k][i] : 0.0f;
+            bf16x8 hh, ll;
+            split8(u, hh, ll);
+            // voxel octet so + 4k: k step k, lane group so
+            sm.bhi[buf][k][sc >> 4][so * 16 + (sc & 15)] = hh;
+            sm.blo[buf][k][sc >> 4][so * 16 + (sc & 15)] = ll;
+        }
+    };
+    // A operand of row block b for k step s of a tile: row 16 (wave + 8b) + l%16, voxels
+    // 32s + 8(l/16) + i; wj[b] is the pair's weight row (M: absent pair, the zero row).
+    bf16x8 wh[NR][2], wl[NR][2];
+    int wj[NR];
+    auto rows_of = [&](int k) {
+        const int slot = sm.tl_s[k];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) wj[b] = sm.tab[16 * (wave + kBrWaves * b) + cl][slot];
+    };
+    auto load_w = [&](int s) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const __bf16* wrow = wt + (int64_t)wj[b] * kWtRow + 8 * q + 32 * s;
+            wh[b][s] = *reinterpret_cast<const bf16x8*>(wrow);
+            wl[b][s] = *reinterpret_cast<const bf16x8*>(wrow + 64);
+        }
+    };
+    f32x4 acc[NR][kBrCb];
+#pragma unroll
+    for (int b = 0; b < NR; ++b)
+#pragma unroll
+        for (int cb = 0; cb < kBrCb; ++cb) acc[b][cb] = f32x4{};
+    // k step s of the tile in LDS buffer buf.  B fragments are read one channel block ahead of
+    // their MFMAs; the scheduling barriers keep the compiler from hoisting every LDS read of the
+    // step into registers.
+    auto half = [&](int buf, int s) {
+        if constexpr (NB > 0) {
+            bf16x8 bh[2], bl[2];
+            bh[0] = sm.bhi[buf][s][0][lane];
+            bl[0] = sm.blo[buf][s][0][lane];
+#pragma unroll
+            for (int cb = 0; cb < kBrCb; ++cb) {
+                if (cb + 1 < kBrCb) {
+                    bh[(cb + 1) & 1] = sm.bhi[buf][s][cb + 1][lane];
+                    bl[(cb + 1) & 1] = sm.blo[buf][s][cb + 1][lane];
+                }
+#pragma unroll
+                for (int b = 0; b < NB; ++b)
+                    acc[b][cb] = mfma3_16x16x32(wh[b][s], wl[b][s], bh[cb & 1], bl[cb & 1], acc[b][cb]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    const int klast = ntl - 1;
+    // prologue: tile 0 staged, gF of tile 1 and the weights of tile 0 in flight (in the order
+    // the loop issues them, so that the compiler's waits at the loop head stay exact)
+    pmask = br_load_tile(G, C, c0, uniform(sm.tl_t[0]), sc, so, gF, pre);
+    stage(0);
+    pmask = br_load_tile(G, C, c0, uniform(sm.tl_t[min(1, klast)]), sc, so, gF, pre);
+    rows_of(0);
+    load_w(0);
+    load_w(1);
+    lds_barrier();
+    for (int k = 0; k < ntl; ++k) {
+        const int kn = min(k + 1, klast);
+        stage((k + 1) & 1);
+        pmask = br_load_tile(G, C, c0, uniform(sm.tl_t[min(k + 2, klast)]), sc, so, gF, pre);
+        rows_of(kn);
+        __builtin_amdgcn_sched_barrier(0);
+        half(k & 1, 0);
+        load_w(0);
+        __builtin_amdgcn_sched_barrier(0);
+        half(k & 1, 1);
+        load_w(1);
+        lds_barrier();
+    }
+
+    // D element i of (b, cb): pass row 16 (wave + 8b) + 4 (l/16) + i, channel c0 + 16 cb + l%16
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int lr = 16 * (wave + kBrWaves * b) + 4 * q + i;
+            if (lr >= prow) continue;
+            float* dst = gpart + (int64_t)sm.rslot[lr] * C + c0 + cl;
+#pragma unroll
+            for (int cb = 0; cb < kBrCb; ++cb)
+                if (c0 + 16 * cb + cl < C) dst[16 * cb] = acc[b][cb][i];
+        }
+    }
+}
+
+// One pass of phase B over rows rp .. rp + prow - 1 of the region (prow <= 384): stages the
+// pass's row table and G->R slots, then runs the tile loop with this wave's block count.
+__device__ __forceinline__ void br_pass(BrSmem& sm, const Grid& G, int C, int c0, int ntl, int rp,
+                                        int KR, int M, int jr0, const float* __restrict__ gF,
+                                        const int* __restrict__ r_pairs, const int* __restrict__ table,
+                                        const __bf16* __restrict__ wt, float* __restrict__ gpart) {
+    const int wave = threadIdx.x >> 6;
+    const int prow = min(KR - rp, kBrPass);
+    const int nblk = (prow + 15) >> 4;
+    const int nb = uniform((nblk - wave + kBrWaves - 1) / kBrWaves);   // row blocks of this wave
+    __syncthreads();   // the previous pass is done with both buffers and the row tables
+    {
+        // all loads first, then the LDS stores (rows past the pass read the region's last row)
+        constexpr int kPer = kBrPass * kBrSlots / kBrThreads;
+        int tv[kPer];
+#pragma unroll
+        for (int e0 = 0; e0 < kPer; ++e0) {
+            const int e = threadIdx.x + e0 * kBrThreads;
+            const int r = min(rp + e / kBrSlots, KR - 1);
+            tv[e0] = table[(int64_t)(jr0 + r) * kBrSlots + e % kBrSlots];
+        }
+        int rs[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int r = threadIdx.x + h * kBrThreads;
+            rs[h] = r < kBrPass ? r_pairs[jr0 + min(rp + r, KR - 1)] : 0;
+        }
+#pragma unroll
+        for (int e0 = 0; e0 < kPer; ++e0) {
+            const int e = threadIdx.x + e0 * kBrThreads;
+            sm.tab[e / kBrSlots][e % kBrSlots] = e / kBrSlots < prow ? tv[e0] : M;
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int r = threadIdx.x + h * kBrThreads;
+            if (r < kBrPass) sm.rslot[r] = rs[h];
+        }
+    }
+    __syncthreads();
+    static_assert(kBrRbMax == 3, "block-count dispatch");
+    if (nb >= 3) br_tiles<3>(sm, G, C, c0, ntl, prow, gF, wt, gpart);
+    else if (nb == 2) br_tiles<2>(sm, G, C, c0, ntl, prow, gF, wt, gpart);
+    else if (nb == 1) br_tiles<1>(sm, G, C, c0, ntl, prow, gF, wt, gpart);
+    else br_tiles<0>(sm, G, C, c0, ntl, prow, gF, wt, gpart);
 }
 
 __global__ void __launch_bounds__(kBrThreads, 1) k_bwd_region(
@@ -610,7 +798,6 @@ __global__ void __launch_bounds__(kBrThreads, 1) k_bwd_region(
     const int chunk = uniform(idx - R * nchunk);
     if (R >= RG.total) return;
     const int c0 = chunk * kBrCc;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int jr0 = uniform(min(max(roff[R], 0), MR));
     const int KR = uniform(min(max(roff[R + 1], jr0), MR)) - jr0;
     if (KR <= 0) return;
@@ -637,103 +824,8 @@ __global__ void __launch_bounds__(kBrThreads, 1) k_bwd_region(
     const int ntl = uniform(sm.ntl);
     if (ntl == 0) return;   // every row stays zero: phase C reads no partial row of this region
 
-    const int sc = threadIdx.x & (kBrCc - 1), so = threadIdx.x >> 7;   // staging: channel, octets so, so+4
-    const int h = lane >> 5, cl = lane & 31;
-    float pre[2][8];
-    unsigned pmask = 0;
-    auto stage = [&](int buf) {
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            float u[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) u[i] = (pmask >> (i + 8 * k)) & 1u ? pre[k][i] : 0.0f;
-            bf16x8 hh, ll;
-            split8(u, hh, ll);
-            const int o = so + 4 * k;   // voxel octet: k step o/2, k group o&1
-            sm.bhi[buf][o >> 1][sc >> 5][(o & 1) * 32 + (sc & 31)] = hh;
-            sm.blo[buf][o >> 1][sc >> 5][(o & 1) * 32 + (sc & 31)] = ll;
-        }
-    };
-
-    for (int rp = 0; rp < KR; rp += kBrPass) {
-        const int lrow = wave * 32 + cl;                  // this lane's row of the pass (A operand row)
-        const bool wave_rows = rp + wave * 32 < KR;       // wave-uniform
-        auto load_w = [&](int k, bf16x8 (&wh)[4], bf16x8 (&wl)[4]) {
-            const int j = sm.tab[lrow][sm.tl_s[k]];
-            const __bf16* wrow = wt + (int64_t)j * kWtRow + h * 8;
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                wh[s] = *reinterpret_cast<const bf16x8*>(wrow + s * 16);
-                wl[s] = *reinterpret_cast<const bf16x8*>(wrow + 64 + s * 16);
-            }
-        };
-        f32x16 acc[4];
-#pragma unroll
-        for (int cb = 0; cb < 4; ++cb) acc[cb] = f32x16{};
-        auto compute = [&](int buf, const bf16x8 (&wh)[4], const bf16x8 (&wl)[4]) {
-            if (!wave_rows) return;
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-                for (int cb = 0; cb < 4; ++cb)
-                    acc[cb] = mfma3_32x32x16(wh[s], wl[s], sm.bhi[buf][s][cb][lane], sm.blo[buf][s][cb][lane], acc[cb]);
-        };
-
-        // prologue: tile 0 staged and its weights loaded; gF of tile 1 in registers
-        const int klast = ntl - 1;
-        bf16x8 ah[4], al[4], bh[4], bl[4];
-        __syncthreads();   // the previous pass is done with both buffers and the row tables
-        {
-            // all loads first, then the LDS stores (rows past the region read its last row)
-            constexpr int kPer = kBrPass * kBrSlots / kBrThreads;
-            int tv[kPer];
-#pragma unroll
-            for (int q = 0; q < kPer; ++q) {
-                const int e = threadIdx.x + q * kBrThreads;
-                const int r = min(rp + e / kBrSlots, KR - 1);
-                tv[q] = table[(int64_t)(jr0 + r) * kBrSlots + e % kBrSlots];
-            }
-            const int rs = r_pairs[jr0 + min(rp + (int)(threadIdx.x % kBrPass), KR - 1)];
-#pragma unroll
-            for (int q = 0; q < kPer; ++q) {
-                const int e = threadIdx.x + q * kBrThreads;
-                sm.tab[e / kBrSlots][e % kBrSlots] = rp + e / kBrSlots < KR ? tv[q] : M;
-            }
-            if (threadIdx.x < kBrPass) sm.rslot[threadIdx.x] = rs;
-        }
-        __syncthreads();
-        pmask = br_load_tile(G, C, c0, sm.tl_t[0], sc, so, gF, pre);
-        load_w(0, ah, al);
-        stage(0);
-        pmask = br_load_tile(G, C, c0, sm.tl_t[min(1, klast)], sc, so, gF, pre);
-        __syncthreads();
-        auto step = [&](int k, const bf16x8 (&wh)[4], const bf16x8 (&wl)[4], bf16x8 (&nh)[4], bf16x8 (&nl)[4]) {
-            load_w(min(k + 1, klast), nh, nl);
-            stage((k + 1) & 1);
-            pmask = br_load_tile(G, C, c0, sm.tl_t[min(k + 2, klast)], sc, so, gF, pre);
-            compute(k & 1, wh, wl);
-            __syncthreads();
-        };
-        for (int k = 0;; k += 2) {
-            step(k, ah, al, bh, bl);
-            if (k + 1 >= ntl) break;
-            step(k + 1, bh, bl, ah, al);
-            if (k + 2 >= ntl) break;
-        }
-
-        // D element i of block cb: region row rp + 32w + 8(i/4) + 4h + i%4, channel c0 + 32cb + cl
-        if (wave_rows) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int lr = wave * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-                if (rp + lr >= KR) continue;
-                float* dst = gpart + (int64_t)sm.rslot[lr] * C + c0 + cl;
-#pragma unroll
-                for (int cb = 0; cb < 4; ++cb)
-                    if (c0 + 32 * cb + cl < C) dst[32 * cb] = acc[cb][i];
-            }
-        }
-    }
+    for (int rp = 0; rp < KR; rp += kBrPass)
+        br_pass(sm, G, C, c0, ntl, rp, KR, M, jr0, gF, r_pairs, table, wt, gpart);
 }
 
 // ------------------------------------------------------------------------------------------

@@ -290,6 +290,9 @@ int g2v_backward(int n, int feat_dim, const float* grad_density, const float* gr
     Grid G;
     int rc = make_grid(voxel_size, voxel_range, G);
     if (rc != G2V_OK) return rc;
+    if (feat_dim > 0 && !region_offsets_fit(G, feat_dim))
+        return fail(G2V_ERR_LIMIT, "Y x Z x feat_dim = %d x %d x %d exceeds the 32-bit tile offsets of the "
+                    "feature backward (16 Y Z C < 2^31)", G.dims[1], G.dims[2], feat_dim);
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (feat_dim == 0) {
         G2V_HIP(launch_backward_density(G, n, grad_density, means3D, opacity, cov_inv, valid_voxel_lb,

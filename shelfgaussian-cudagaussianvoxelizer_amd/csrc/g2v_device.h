@@ -160,6 +160,16 @@ __device__ __forceinline__ f32x16 mfma3_32x32x16(const bf16x8& ah, const bf16x8&
     return acc;
 }
 
+// Same three-term product on the 16 x 16 x 32 shape.  Operand lanes: A row l%16, k 8(l/16)+i;
+// B column l%16, k 8(l/16)+i; D element i at row 4(l/16)+i, column l%16.
+__device__ __forceinline__ f32x4 mfma3_16x16x32(const bf16x8& ah, const bf16x8& al, const bf16x8& bh,
+                                               const bf16x8& bl, f32x4 acc) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
+    return acc;
+}
+
 // Wave64 sum (every lane gets the total).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -70,6 +70,11 @@ inline int packed_channels(int C) { return (C + kPackedChannelAlign - 1) & ~(kPa
 inline bool packed_fits(int n, int C) { return (int64_t)(n + 1) * packed_channels(C) * 4 <= (int64_t)UINT32_MAX; }
 // The split feature rows of the backward (32-channel chunks, 4 bytes per channel) likewise.
 inline bool split_rows_fit(int n, int C) { return (int64_t)(n + 1) * ((C + 31) / 32) * 128 <= (int64_t)UINT32_MAX; }
+// The feature backward reads grad_feats per tile through 32-bit byte offsets from the tile's
+// origin; they span at most 4 x-slices of the grid.
+inline bool region_offsets_fit(const Grid& G, int C) {
+    return (int64_t)16 * G.dims[1] * G.dims[2] * C < ((int64_t)1 << 31);
+}
 
 hipError_t launch_forward_density(const Grid& G, const float* means, const float* opacity,
                                   const float* cov_inv, const int* lb, const int* ub,
