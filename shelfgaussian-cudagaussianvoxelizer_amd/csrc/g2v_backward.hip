@@ -175,9 +175,7 @@ struct BtSmem {
         unsigned char frow[kBtStages][kBtPass * kBtRowBytes];
         float xch[2][kBtPass][kNumGrads];   // epilogue exchange, used after the K loop has drained
     } u;
-    float graw[kBtStages][64][kBtKc];   // G chunks as loaded (fp32, voxel-major)
-    bf16x8 ahi[2][2][2][64];   // A operand (G chunk), hi: [buffer][k step][voxel block][lane]
-    bf16x8 alo[2][2][2][64];
+    float graw[kBtStages][64][kBtKc];   // G chunks as loaded (fp32, voxel-major, 16-byte pieces swizzled)
     int vlin[64];
     float gD[64], inv[64], tv[64], D[64];
     ParamTile<kBtPass> pt;     // parameters of this pass's list entries
@@ -222,8 +220,8 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
     const int j0 = uniform(min(max(toff[tile], 0), M));
     const int Ng = uniform(min(max(toff[tile + 1], j0), M)) - j0;
     if (Ng <= 0) return;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int mb = wave & 1, ngrp = wave >> 1;
+    const int lane = threadIdx.x & 63, wave = uniform(threadIdx.x >> 6);
+    const int mb = wave >> 2, ngrp = wave & 3;   // voxel block (epilogues) / k half (K loop), N group
     const int tyz = G.tiles[1] * G.tiles[2];
     const int tx = tile / tyz, ty = (tile - tx * tyz) / G.tiles[2], tz = tile % G.tiles[2];
 
@@ -257,51 +255,37 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
     }
 
     // G staging: direct-to-LDS loads of the raw chunk (voxel rows clamped to a valid row, channels
-    // clamped into the row), then thread (voxel sv, channel quad sq) masks, splits and writes its
-    // four channels into the A operand.  VEC: one 16-byte load per lane, lane = (voxel, quad);
-    // otherwise four 4-byte loads per lane, each covering two voxel rows.
+    // clamped into the row).  Row v of a stage keeps its 16-byte piece p (channels 4p..4p+3) at
+    // slot p ^ (v & 7), so that the A-operand reads (8 consecutive rows per LDS cycle) are free of
+    // bank conflicts.  VEC: one 16-byte load per lane, lane = (row, slot); otherwise four 4-byte
+    // loads per lane, each covering two rows.
     constexpr int kNG = VEC ? 1 : 4;   // G loads per wave per chunk
-    const int sv = threadIdx.x >> 3, sq = threadIdx.x & 7;
-    const int grow = sm.vlin[sv];
     const float* gsrc[kNG];
+    int gcoff[kNG];   // channel of this lane's load within a chunk
 #pragma unroll
     for (int k = 0; k < kNG; ++k) {
-        const int v = VEC ? sv : wave * 8 + 2 * k + (lane >> 5);
+        const int v = VEC ? wave * 8 + (lane >> 3) : wave * 8 + 2 * k + (lane >> 5);
         gsrc[k] = gF + (int64_t)max(sm.vlin[v], 0) * C;
+        gcoff[k] = VEC ? 4 * ((lane & 7) ^ (v & 7)) : 4 * (((lane & 31) >> 2) ^ (v & 7)) + (lane & 3);
     }
     auto dma_g = [&](int chunk, int stage) {
 #pragma unroll
         for (int k = 0; k < kNG; ++k) {
-            if (VEC) {
-                const int c = min(chunk * kBtKc + 4 * sq, C - 4);
-                dma16(gsrc[k] + c, uniform(lds_addr(&sm.graw[stage][wave * 8][0])));
-            } else {
-                const int c = min(chunk * kBtKc + (lane & 31), C - 1);
-                dma4(gsrc[k] + c, uniform(lds_addr(&sm.graw[stage][wave * 8 + 2 * k][0])));
-            }
+            if (VEC)
+                dma16(gsrc[k] + min(chunk * kBtKc + gcoff[k], C - 4), uniform(lds_addr(&sm.graw[stage][wave * 8][0])));
+            else
+                dma4(gsrc[k] + min(chunk * kBtKc + gcoff[k], C - 1),
+                     uniform(lds_addr(&sm.graw[stage][wave * 8 + 2 * k][0])));
         }
-    };
-    auto write_g = [&](int chunk, int stage, int buf) {
-        const int c = chunk * kBtKc + 4 * sq;
-        const float4 v4 = *reinterpret_cast<const float4*>(&sm.graw[stage][sv][4 * sq]);
-        const float v[4] = {v4.x, v4.y, v4.z, v4.w};
-        typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-        bf16x4 hv, lv;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            __bf16 hh, ll;
-            split_bf16((grow >= 0 && c + e < C) ? v[e] : 0.0f, hh, ll);
-            hv[e] = hh;
-            lv[e] = ll;
-        }
-        // channels 4sq..4sq+3 of the chunk: K step sq/4, k group (sq/2)&1, half sq&1 of the slot
-        const int s = sq >> 2, L = ((sq >> 1) & 1) * 32 + (sv & 31);
-        *reinterpret_cast<bf16x4*>(reinterpret_cast<char*>(&sm.ahi[buf][s][sv >> 5][L]) + (sq & 1) * 8) = hv;
-        *reinterpret_cast<bf16x4*>(reinterpret_cast<char*>(&sm.alo[buf][s][sv >> 5][L]) + (sq & 1) * 8) = lv;
     };
 
     const uint32_t fstride = (uint32_t)nchk * kBtRowBytes;   // bytes of one Gaussian's split row
     const char* fbase = reinterpret_cast<const char*>(fsp);
+    const int ks = mb;                // k half of every chunk this wave multiplies (channels 16ks..16ks+15)
+    const int h = lane >> 5;
+    bool vok[2];                      // A-operand rows 32m + lane%32 lie in the grid
+#pragma unroll
+    for (int m = 0; m < 2; ++m) vok[m] = sm.vlin[32 * m + (lane & 31)] >= 0;
 
     for (int pbase = 0; pbase < Ng; pbase += kBtPass) {
         const int pcount = min(kBtPass, Ng - pbase);
@@ -313,7 +297,7 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
         // loaded by this wave; lane = (row rg*8 + lane/8, slot lane%8) and slot p carries the
         // 16-byte piece p ^ (row&7) of the row's chunk.  Rows past the list read the zero
         // row; a group wholly past it reads one 16-byte piece of the zero row in every lane.
-        // Every wave issues exactly kBtDma loads per chunk, so the wait counts below are exact.
+        // Every wave issues exactly kBtDma + kNG loads per chunk, so the wait counts below are exact.
         uint32_t doff[kBtDma];
 #pragma unroll
         for (int i = 0; i < kBtDma; ++i) {
@@ -323,18 +307,23 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             const int piece = (lane & 7) ^ (r & 7);
             doff[i] = (rg * 8 < pcount) ? (uint32_t)g * fstride + (uint32_t)piece * 16u : (uint32_t)n * fstride;
         }
-        auto dma_f = [&](int chunk, int buf) {
+        auto dma_f = [&](int chunk, int buf, int i0, int i1) {
 #pragma unroll
             for (int i = 0; i < kBtDma; ++i) {
+                if (i < i0 || i >= i1) continue;
                 const int rg = wave + kBtWaves * i;
                 dma16(fbase + (doff[i] + (uint32_t)chunk * kBtRowBytes),
                       uniform(lds_addr(&sm.u.frow[buf][rg * 8 * kBtRowBytes])));
             }
         };
 
-        f32x16 acc[kBtNbw];
+        // wave (ks, ngrp) accumulates k half ks of every chunk for both voxel blocks m and its N
+        // blocks ngrp + 4j; the halves are added after the K loop
+        f32x16 acc2[2][kBtNbw];
 #pragma unroll
-        for (int j = 0; j < kBtNbw; ++j) acc[j] = f32x16{};
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+            for (int j = 0; j < kBtNbw; ++j) acc2[m][j] = f32x16{};
         int nact = 0;
         int gcol[kBtNbw];
 #pragma unroll
@@ -343,61 +332,119 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             gcol[j] = sm.pt.gid[(ngrp + kBtGroups * j) * 32 + (lane & 31)];
         }
         nact = uniform(nact);
-        const int h = lane >> 5;
-        auto compute = [&](int buf, int abuf) {
+        // A operand of chunk ch (stage st): raw G of rows 32m + lane%32, channels 16ks + 8h + i,
+        // masked (rows outside the grid, channels past C) and split in registers
+        auto load_a = [&](int ch, int st, bf16x8 (&ah)[2], bf16x8 (&al)[2]) {
+            const int cv = min(max(C - (ch * kBtKc + 16 * ks + 8 * h), 0), 8);
 #pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                const bf16x8 ah = sm.ahi[abuf][s][mb][lane];
-                const bf16x8 al = sm.alo[abuf][s][mb][lane];
+            for (int m = 0; m < 2; ++m) {
+                const float* rowp = &sm.graw[st][32 * m + (lane & 31)][0];
+                const float4 x0 = *reinterpret_cast<const float4*>(rowp + 4 * ((4 * ks + 2 * h) ^ (lane & 7)));
+                const float4 x1 = *reinterpret_cast<const float4*>(rowp + 4 * ((4 * ks + 2 * h + 1) ^ (lane & 7)));
+                float u[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                const int lim = vok[m] ? cv : 0;
 #pragma unroll
-                for (int j = 0; j < kBtNbw; ++j) {
-                    if (j < nact) {
-                        const int r = (ngrp + kBtGroups * j) * 32 + (lane & 31);
-                        const int sw = r & 7;
-                        const unsigned char* rowp = &sm.u.frow[buf][r * kBtRowBytes];
-                        const bf16x8 bh = *reinterpret_cast<const bf16x8*>(rowp + (((2 * s + h) ^ sw) << 4));
-                        const bf16x8 bl = *reinterpret_cast<const bf16x8*>(rowp + (((4 + 2 * s + h) ^ sw) << 4));
-                        acc[j] = mfma3_32x32x16(ah, al, bh, bl, acc[j]);
-                    }
-                }
+                for (int i = 0; i < 8; ++i) u[i] = i < lim ? u[i] : 0.0f;
+                split8(u, ah[m], al[m]);
+            }
+        };
+        // N block j of chunk ch (stage st) against both voxel blocks
+        auto mult = [&](int j, int st, const bf16x8 (&ah)[2], const bf16x8 (&al)[2]) {
+            if (j < nact) {
+                const int r = (ngrp + kBtGroups * j) * 32 + (lane & 31);
+                const unsigned char* rowp = &sm.u.frow[st][r * kBtRowBytes];
+                const bf16x8 bh = *reinterpret_cast<const bf16x8*>(rowp + (((2 * ks + h) ^ (lane & 7)) << 4));
+                const bf16x8 bl = *reinterpret_cast<const bf16x8*>(rowp + (((4 + 2 * ks + h) ^ (lane & 7)) << 4));
+#pragma unroll
+                for (int m = 0; m < 2; ++m) acc2[m][j] = mfma3_32x32x16(ah[m], al[m], bh, bl, acc2[m][j]);
             }
         };
 
-        // Pipeline over chunks (every load is direct-to-LDS).  Step ch starts with the A operand
-        // and the F rows of chunk ch in LDS and the raw G values of chunk ch+1 complete; it loads
-        // the F rows of chunk ch+2 and the G values of chunk ch+3, multiplies chunk ch, writes the
-        // A operand of chunk ch+1, and waits until only its own loads are outstanding.
+        // Pipeline over chunks (every load is direct-to-LDS, two chunks ahead).  Step ch starts
+        // with the F rows and G values of chunk ch in LDS; it multiplies chunk ch and issues the
+        // loads of chunk ch+2 between its MFMAs (which run on while the loads issue), then waits
+        // until only those loads are outstanding.
         const int clast = nchk - 1;
+        dma_f(0, 0, 0, kBtDma);
         dma_g(0, 0);
-        dma_f(0, 0);
+        dma_f(min(1, clast), 1, 0, kBtDma);
         dma_g(min(1, clast), 1);
-        dma_f(min(1, clast), 1);
-        dma_g(min(2, clast), 2);
-        wait_vm<kBtDma + kNG>();      // G(0), F(0), G(1) complete
-        lds_barrier();
-        write_g(0, 0, 0);
+        wait_vm<kBtDma + kNG>();      // F(0), G(0) complete
         lds_barrier();
         for (int ch = 0; ch < nchk; ++ch) {
-            dma_f(min(ch + 2, clast), (ch + 2) % kBtStages);
-            dma_g(min(ch + 3, clast), (ch + 3) % kBtStages);
-            compute(ch % kBtStages, ch & 1);
-            write_g(ch + 1, (ch + 1) % kBtStages, (ch + 1) & 1);
-            wait_vm<kBtDma + kNG>();  // F(ch+1) and G(ch+2) complete
+            const int st = ch % kBtStages, nx = (ch + 2) % kBtStages, cn = min(ch + 2, clast);
+            bf16x8 ah[2], al[2];
+            load_a(ch, st, ah, al);
+            mult(0, st, ah, al);
+            __builtin_amdgcn_sched_barrier(0);
+            dma_f(cn, nx, 0, kBtDma / 2);
+            __builtin_amdgcn_sched_barrier(0);
+            mult(1, st, ah, al);
+            __builtin_amdgcn_sched_barrier(0);
+            dma_f(cn, nx, kBtDma / 2, kBtDma);
+            dma_g(cn, nx);
+            wait_vm<kBtDma + kNG>();  // F(ch+1) and G(ch+1) complete
             lds_barrier();
         }
         // drain the surplus loads of the last steps before the F buffers are reused
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         __syncthreads();
 
-        // ---- epilogue 1: split weights w / max(D, eps) of every pair; t_v from U (single pass)
+        // Sum the two k halves: wave (ks, ngrp) keeps voxel block mb = ks and hands the other
+        // block to its partner through LDS.  Both partners add (half 0) + (half 1).
+        f32x16 acc[kBtNbw];
+        {
+            // [ngrp][m][j][i][lane]: block m of N group ngrp, written by the wave that does not keep it
+            float* xb = reinterpret_cast<float*>(&sm.u.frow[0][0]) + ngrp * (2 * kBtNbw * 16 * 64) + lane;
+            constexpr int kXm = kBtNbw * 16 * 64;
+            if (ks == 0) {
+#pragma unroll
+                for (int j = 0; j < kBtNbw; ++j)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) xb[kXm + (j * 16 + i) * 64] = acc2[1][j][i];
+            } else {
+#pragma unroll
+                for (int j = 0; j < kBtNbw; ++j)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) xb[(j * 16 + i) * 64] = acc2[0][j][i];
+            }
+            __syncthreads();
+            if (ks == 0) {
+#pragma unroll
+                for (int j = 0; j < kBtNbw; ++j)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) acc[j][i] = acc2[0][j][i] + xb[(j * 16 + i) * 64];
+            } else {
+#pragma unroll
+                for (int j = 0; j < kBtNbw; ++j)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) acc[j][i] = xb[kXm + (j * 16 + i) * 64] + acc2[1][j][i];
+            }
+            __syncthreads();   // the exchange area is reused by the epilogues
+        }
+
+        // ---- epilogue 1: split weights w / max(D, eps) of every pair; t_v from U (single pass).
+        // Lane = Gaussian column lane%32 of N block j; element i is the tile's voxel row
+        // r = 32 mb + 8 (i/4) + 4 (lane/32) + i%4.  Branch-free: an element outside the grid, the
+        // Gaussian's box or the list gets e = 0 (and so w = 0).  e and the validity bits are kept
+        // for epilogue 2, which then evaluates no exponential.
+        unsigned rowok = 0;   // bit i: row r of element i lies in the grid
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            rowok |= (sm.vlin[mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3)] >= 0) ? (1u << i) : 0u;
         float rowt[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) rowt[i] = 0.0f;
+        float ek[kBtNbw][16];
+        unsigned okm[kBtNbw];
 #pragma unroll
         for (int j = 0; j < kBtNbw; ++j) {
+            okm[j] = 0;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) ek[j][i] = 0.0f;
+            if (j >= nact) continue;   // wave-uniform
             const int slot = (ngrp + kBtGroups * j) * 32 + (lane & 31);
-            const int g = (j < nact) ? gcol[j] : -1;
-            if (g < 0) continue;
+            const bool gok = gcol[j] >= 0;
             GaussParams p;
             read_params(sm.pt, slot, p);
             __bf16* wrow = wt + (int64_t)(j0 + pbase + slot) * kWtRow;
@@ -407,25 +454,27 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
 #pragma unroll
                 for (int ii = 0; ii < 4; ++ii) {
                     const int i = q4 * 4 + ii;
-                    const int r = mb * 32 + 8 * q4 + 4 * (lane >> 5) + ii;
-                    float w = 0.0f;
-                    if (sm.vlin[r] >= 0) {
-                        const int x = tx * kTile + (r >> 4), y = ty * kTile + ((r >> 2) & 3), z = tz * kTile + (r & 3);
-                        if (in_box(p, x, y, z)) {
-                            float qx, qy, qz;
-                            w = p.o * eval_gauss(p, centre(G, 0, x), centre(G, 1, y), centre(G, 2, z), qx, qy, qz);
-                        }
-                    }
+                    const int r = mb * 32 + 8 * q4 + 4 * h + ii;
+                    const int x = tx * kTile + (r >> 4), y = ty * kTile + ((r >> 2) & 3), z = tz * kTile + ii;
+                    const bool ok = gok && ((rowok >> i) & 1u) && in_box(p, x, y, z);
+                    float qx, qy, qz;
+                    const float e = ok ? eval_gauss(p, centre(G, 0, x), centre(G, 1, y), centre(G, 2, z), qx, qy, qz)
+                                       : 0.0f;
+                    ek[j][i] = e;
+                    okm[j] |= ok ? (1u << i) : 0u;
+                    const float w = p.o * e;
                     const float wtil = w * sm.inv[r];
                     split_bf16(wtil, hs[ii], ls[ii]);
                     rowt[i] += (w > 0.0f ? wtil : 0.0f) * acc[j][i];
                 }
-                const int r0 = mb * 32 + 8 * q4 + 4 * (lane >> 5);
-                typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-                bf16x4 hv = {hs[0], hs[1], hs[2], hs[3]};
-                bf16x4 lv = {ls[0], ls[1], ls[2], ls[3]};
-                *reinterpret_cast<bf16x4*>(wrow + r0) = hv;
-                *reinterpret_cast<bf16x4*>(wrow + 64 + r0) = lv;
+                if (gok) {
+                    const int r0 = mb * 32 + 8 * q4 + 4 * h;
+                    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+                    bf16x4 hv = {hs[0], hs[1], hs[2], hs[3]};
+                    bf16x4 lv = {ls[0], ls[1], ls[2], ls[3]};
+                    *reinterpret_cast<bf16x4*>(wrow + r0) = hv;
+                    *reinterpret_cast<bf16x4*>(wrow + 64 + r0) = lv;
+                }
             }
         }
         if (!multi) {
@@ -440,7 +489,7 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             if ((lane & 31) == 0) {
 #pragma unroll
                 for (int i = 0; i < 16; ++i)
-                    sm.tpart[ngrp][mb * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3)] = rowt[i];
+                    sm.tpart[ngrp][mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3)] = rowt[i];
             }
             __syncthreads();
             if (threadIdx.x < 64) {
@@ -452,25 +501,23 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             __syncthreads();
         }
 
-        // ---- epilogue 2: gw and the geometric partials of each pair
+        // ---- epilogue 2: gw and the geometric partials of each pair (e from epilogue 1; an
+        // invalid element adds exact zeros)
 #pragma unroll
         for (int j = 0; j < kBtNbw; ++j) {
             const int slot = (ngrp + kBtGroups * j) * 32 + (lane & 31);
-            const int g = (j < nact) ? gcol[j] : -1;
             float gr[kNumGrads] = {};
-            if (g >= 0) {
+            if (j < nact) {   // wave-uniform
                 GaussParams p;
                 read_params(sm.pt, slot, p);
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
-                    const int r = mb * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-                    if (sm.vlin[r] < 0) continue;
-                    const int x = tx * kTile + (r >> 4), y = ty * kTile + ((r >> 2) & 3), z = tz * kTile + (r & 3);
-                    if (!in_box(p, x, y, z)) continue;
+                    const int r = mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+                    const int x = tx * kTile + (r >> 4), y = ty * kTile + ((r >> 2) & 3), z = tz * kTile + (i & 3);
                     float qx, qy, qz;
-                    const float e = eval_gauss(p, centre(G, 0, x), centre(G, 1, y), centre(G, 2, z), qx, qy, qz);
+                    gauss_q(p, centre(G, 0, x), centre(G, 1, y), centre(G, 2, z), qx, qy, qz);
                     const float gw = sm.gD[r] + (acc[j][i] - sm.tv[r]) * sm.inv[r];
-                    accumulate_grads(gr, gw, e, p.o, qx, qy, qz);
+                    accumulate_grads(gr, ((okm[j] >> i) & 1u) ? gw : 0.0f, ek[j][i], p.o, qx, qy, qz);
                 }
             }
 #pragma unroll
@@ -993,7 +1040,7 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
                b.fsp);
     if (M > 0 && T > 0) {
         const int blocks = (int)ceil_div(T, 8) * 8;
-        if ((C & 3) == 0)
+        if ((C & 3) == 0 && ((uintptr_t)grad_feats & 15) == 0)   // 16-byte G loads
             G2V_LAUNCH(k_bwd_tile<true>, dim3(blocks), dim3(kBtThreads), 0, s, G, n, C, nchk, grad_density,
                        grad_feats, means, opacity, cov_inv, lb, ub, g2t_offsets, tile_offsets, sorted_gauss,
                        (int)M, density, grid_feats, (const __bf16*)b.fsp, b.partials, b.wt);

@@ -132,6 +132,15 @@ __device__ __forceinline__ float eval_gauss(const GaussParams& p, float cx, floa
     return __expf(-0.5f * m);
 }
 
+// q = A dx alone, with the same operations as eval_gauss (so the same values).
+__device__ __forceinline__ void gauss_q(const GaussParams& p, float cx, float cy, float cz, float& qx,
+                                        float& qy, float& qz) {
+    const float d0 = cx - p.mu[0], d1 = cy - p.mu[1], d2 = cz - p.mu[2];
+    qx = p.A[0] * d0 + p.A[1] * d1 + p.A[2] * d2;
+    qy = p.A[3] * d0 + p.A[4] * d1 + p.A[5] * d2;
+    qz = p.A[6] * d0 + p.A[7] * d1 + p.A[8] * d2;
+}
+
 __device__ __forceinline__ float centre(const Grid& G, int a, int i) {
     return fmaf((float)i + 0.5f, G.s[a], G.r0[a]);
 }
@@ -142,12 +151,19 @@ __device__ __forceinline__ void split_bf16(float x, __bf16& hi, __bf16& lo) {
     lo = (__bf16)(x - (float)hi);
 }
 
+// Eight values at once, converted in pairs (one packed conversion per pair for hi and for lo).
 __device__ __forceinline__ void split8(const float (&v)[8], bf16x8& hi, bf16x8& lo) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        __bf16 h = (__bf16)v[i];
-        hi[i] = h;
-        lo[i] = (__bf16)(v[i] - (float)h);
+    for (int p = 0; p < 4; ++p) {
+        const f32x2 x = {v[2 * p], v[2 * p + 1]};
+        const bf16x2 h = __builtin_convertvector(x, bf16x2);
+        const bf16x2 l = __builtin_convertvector(x - __builtin_convertvector(h, f32x2), bf16x2);
+        hi[2 * p] = h[0];
+        hi[2 * p + 1] = h[1];
+        lo[2 * p] = l[0];
+        lo[2 * p + 1] = l[1];
     }
 }
 
