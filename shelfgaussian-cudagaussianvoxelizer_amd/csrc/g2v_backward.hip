@@ -152,6 +152,12 @@ constexpr int kWtRow = 128;                            // bf16 per pair: 64 hi t
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
+// Slot swizzle of 128-byte LDS rows of 16-byte pieces: piece q of row r sits at slot q ^ swz(r).
+// Any 8 consecutive rows get distinct swz values, and any 16 consecutive rows give distinct
+// (row parity, swz) pairs, so reading one piece from each of 8 (32 banks) or 16 (64 banks)
+// consecutive rows per LDS cycle is free of bank conflicts.
+__device__ __forceinline__ int swz(int r) { return (r ^ (r >> 3)) & 7; }
+
 // Direct-to-LDS loads: lane l writes its 16 (or 4) bytes from gptr at LDS address lds + 16*l
 // (4*l).  Issued as inline assembly so that the compiler does not attach conservative waits to
 // later LDS reads; every consumer waits explicitly (wait_vm) and meets the other waves at a
@@ -170,12 +176,15 @@ __device__ __forceinline__ void dma4(const void* gptr, uint32_t lds) {
 
 struct BtSmem {
     union {
-        // F chunk rows of the pass's Gaussians; the 16-byte slot q of row r sits at q ^ (r&7), so the
-        // 8 lanes of one LDS cycle (8 consecutive rows) hit 8 different 16-byte bank groups
+        // F chunk rows of the pass's Gaussians; the 16-byte piece q of row r sits at slot
+        // q ^ swz(r), so that the lanes of one LDS cycle (8 or 16 consecutive rows) hit distinct
+        // 16-byte bank groups
         unsigned char frow[kBtStages][kBtPass * kBtRowBytes];
         float xch[2][kBtPass][kNumGrads];   // epilogue exchange, used after the K loop has drained
     } u;
-    float graw[kBtStages][64][kBtKc];   // G chunks as loaded (fp32, voxel-major, 16-byte pieces swizzled)
+    float graw[kBtStages][64][kBtKc];   // G chunks as loaded (fp32, voxel-major, pieces at q ^ swz(v))
+    bf16x8 ahi[2][2][2][64];   // A operand (G chunk), hi: [buffer][k half][voxel block][lane]
+    bf16x8 alo[2][2][2][64];
     int vlin[64];
     float gD[64], inv[64], tv[64], D[64];
     ParamTile<kBtPass> pt;     // parameters of this pass's list entries
@@ -256,8 +265,8 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
 
     // G staging: direct-to-LDS loads of the raw chunk (voxel rows clamped to a valid row, channels
     // clamped into the row).  Row v of a stage keeps its 16-byte piece p (channels 4p..4p+3) at
-    // slot p ^ (v & 7), so that the A-operand reads (8 consecutive rows per LDS cycle) are free of
-    // bank conflicts.  VEC: one 16-byte load per lane, lane = (row, slot); otherwise four 4-byte
+    // slot p ^ swz(v), so that the A-operand reads (8 or 16 consecutive rows per LDS cycle) are
+    // free of bank conflicts.  VEC: one 16-byte load per lane, lane = (row, slot); otherwise four 4-byte
     // loads per lane, each covering two rows.
     constexpr int kNG = VEC ? 1 : 4;   // G loads per wave per chunk
     const float* gsrc[kNG];
@@ -266,7 +275,7 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
     for (int k = 0; k < kNG; ++k) {
         const int v = VEC ? wave * 8 + (lane >> 3) : wave * 8 + 2 * k + (lane >> 5);
         gsrc[k] = gF + (int64_t)max(sm.vlin[v], 0) * C;
-        gcoff[k] = VEC ? 4 * ((lane & 7) ^ (v & 7)) : 4 * (((lane & 31) >> 2) ^ (v & 7)) + (lane & 3);
+        gcoff[k] = VEC ? 4 * ((lane & 7) ^ swz(v)) : 4 * (((lane & 31) >> 2) ^ swz(v)) + (lane & 3);
     }
     auto dma_g = [&](int chunk, int stage) {
 #pragma unroll
@@ -283,9 +292,6 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
     const char* fbase = reinterpret_cast<const char*>(fsp);
     const int ks = mb;                // k half of every chunk this wave multiplies (channels 16ks..16ks+15)
     const int h = lane >> 5;
-    bool vok[2];                      // A-operand rows 32m + lane%32 lie in the grid
-#pragma unroll
-    for (int m = 0; m < 2; ++m) vok[m] = sm.vlin[32 * m + (lane & 31)] >= 0;
 
     for (int pbase = 0; pbase < Ng; pbase += kBtPass) {
         const int pcount = min(kBtPass, Ng - pbase);
@@ -295,7 +301,7 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
 
         // F rows by direct-to-LDS loads: row group rg = wave + kBtWaves*i (8 rows, 1 KB) is
         // loaded by this wave; lane = (row rg*8 + lane/8, slot lane%8) and slot p carries the
-        // 16-byte piece p ^ (row&7) of the row's chunk.  Rows past the list read the zero
+        // 16-byte piece p ^ swz(row) of the row's chunk.  Rows past the list read the zero
         // row; a group wholly past it reads one 16-byte piece of the zero row in every lane.
         // Every wave issues exactly kBtDma + kNG loads per chunk, so the wait counts below are exact.
         uint32_t doff[kBtDma];
@@ -304,7 +310,7 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             const int rg = wave + kBtWaves * i;
             const int r = rg * 8 + (lane >> 3);
             const int g = r < pcount ? sm.pt.gid[r] : n;
-            const int piece = (lane & 7) ^ (r & 7);
+            const int piece = (lane & 7) ^ swz(r);
             doff[i] = (rg * 8 < pcount) ? (uint32_t)g * fstride + (uint32_t)piece * 16u : (uint32_t)n * fstride;
         }
         auto dma_f = [&](int chunk, int buf, int i0, int i1) {
@@ -332,58 +338,74 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             gcol[j] = sm.pt.gid[(ngrp + kBtGroups * j) * 32 + (lane & 31)];
         }
         nact = uniform(nact);
-        // A operand of chunk ch (stage st): raw G of rows 32m + lane%32, channels 16ks + 8h + i,
-        // masked (rows outside the grid, channels past C) and split in registers
-        auto load_a = [&](int ch, int st, bf16x8 (&ah)[2], bf16x8 (&al)[2]) {
-            const int cv = min(max(C - (ch * kBtKc + 16 * ks + 8 * h), 0), 8);
-#pragma unroll
-            for (int m = 0; m < 2; ++m) {
-                const float* rowp = &sm.graw[st][32 * m + (lane & 31)][0];
-                const float4 x0 = *reinterpret_cast<const float4*>(rowp + 4 * ((4 * ks + 2 * h) ^ (lane & 7)));
-                const float4 x1 = *reinterpret_cast<const float4*>(rowp + 4 * ((4 * ks + 2 * h + 1) ^ (lane & 7)));
-                float u[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-                const int lim = vok[m] ? cv : 0;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) u[i] = i < lim ? u[i] : 0.0f;
-                split8(u, ah[m], al[m]);
-            }
+        // A operand of chunk ch, split once per value: thread (voxel sv, channel quad sq) reads its
+        // four raw G values (stage gs), masks them (row outside the grid, channels past C),
+        // splits them and writes hi and lo into A buffer ab: channels 4sq.. of the chunk are k
+        // half sq/4, lane group (sq/2)&1, half sq&1 of the lane's 16-byte fragment.
+        const int sv = threadIdx.x >> 3, sq = threadIdx.x & 7;
+        const bool svok = sm.vlin[sv] >= 0;
+        auto write_a = [&](int ch, int gs, int ab) {
+            const float4 x = *reinterpret_cast<const float4*>(&sm.graw[gs][sv][4 * (sq ^ swz(sv))]);
+            const int lim = svok ? min(max(C - (ch * kBtKc + 4 * sq), 0), 4) : 0;
+            typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+            typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+            typedef float f32x2 __attribute__((ext_vector_type(2)));
+            const f32x2 x01 = {0 < lim ? x.x : 0.0f, 1 < lim ? x.y : 0.0f};
+            const f32x2 x23 = {2 < lim ? x.z : 0.0f, 3 < lim ? x.w : 0.0f};
+            const bf16x2 h01 = __builtin_convertvector(x01, bf16x2), h23 = __builtin_convertvector(x23, bf16x2);
+            const bf16x2 l01 = __builtin_convertvector(x01 - __builtin_convertvector(h01, f32x2), bf16x2);
+            const bf16x2 l23 = __builtin_convertvector(x23 - __builtin_convertvector(h23, f32x2), bf16x2);
+            const bf16x4 hv = {h01[0], h01[1], h23[0], h23[1]}, lv = {l01[0], l01[1], l23[0], l23[1]};
+            const int L = ((sq >> 1) & 1) * 32 + (sv & 31);
+            *reinterpret_cast<bf16x4*>(reinterpret_cast<char*>(&sm.ahi[ab][sq >> 2][sv >> 5][L]) + (sq & 1) * 8) = hv;
+            *reinterpret_cast<bf16x4*>(reinterpret_cast<char*>(&sm.alo[ab][sq >> 2][sv >> 5][L]) + (sq & 1) * 8) = lv;
         };
-        // N block j of chunk ch (stage st) against both voxel blocks
-        auto mult = [&](int j, int st, const bf16x8 (&ah)[2], const bf16x8 (&al)[2]) {
+        // N block j of chunk ch (F stage st, A buffer ab) against both voxel blocks
+        auto mult = [&](int j, int st, int ab) {
             if (j < nact) {
-                const int r = (ngrp + kBtGroups * j) * 32 + (lane & 31);
+                bf16x8 ah[2], al[2];
+#pragma unroll
+                for (int m = 0; m < 2; ++m) {
+                    ah[m] = sm.ahi[ab][ks][m][lane];
+                    al[m] = sm.alo[ab][ks][m][lane];
+                }
+                const int r = (ngrp + kBtGroups * j) * 32 + (lane & 31), sr = swz(r);
                 const unsigned char* rowp = &sm.u.frow[st][r * kBtRowBytes];
-                const bf16x8 bh = *reinterpret_cast<const bf16x8*>(rowp + (((2 * ks + h) ^ (lane & 7)) << 4));
-                const bf16x8 bl = *reinterpret_cast<const bf16x8*>(rowp + (((4 + 2 * ks + h) ^ (lane & 7)) << 4));
+                const bf16x8 bh = *reinterpret_cast<const bf16x8*>(rowp + (((2 * ks + h) ^ sr) << 4));
+                const bf16x8 bl = *reinterpret_cast<const bf16x8*>(rowp + (((4 + 2 * ks + h) ^ sr) << 4));
 #pragma unroll
                 for (int m = 0; m < 2; ++m) acc2[m][j] = mfma3_32x32x16(ah[m], al[m], bh, bl, acc2[m][j]);
             }
         };
 
-        // Pipeline over chunks (every load is direct-to-LDS, two chunks ahead).  Step ch starts
-        // with the F rows and G values of chunk ch in LDS; it multiplies chunk ch and issues the
-        // loads of chunk ch+2 between its MFMAs (which run on while the loads issue), then waits
-        // until only those loads are outstanding.
+        // Pipeline over chunks (every load is direct-to-LDS; F two chunks ahead, G three).  Step
+        // ch starts with the A operand of chunk ch (A buffer ch&1), the F rows of chunk ch and the
+        // G values of chunk ch+1 in LDS.  Between its MFMAs (which run on in the matrix unit) it
+        // writes the A operand of chunk ch+1 and issues the loads of F(ch+2) and G(ch+3); then it
+        // waits until only those loads are outstanding.  G(ch+3) goes to the stage of G(ch), whose
+        // A operand was written in the previous step.
         const int clast = nchk - 1;
-        dma_f(0, 0, 0, kBtDma);
         dma_g(0, 0);
-        dma_f(min(1, clast), 1, 0, kBtDma);
+        dma_f(0, 0, 0, kBtDma);
         dma_g(min(1, clast), 1);
-        wait_vm<kBtDma + kNG>();      // F(0), G(0) complete
+        dma_f(min(1, clast), 1, 0, kBtDma);
+        dma_g(min(2, clast), 2);
+        wait_vm<kBtDma + kNG>();      // G(0), F(0), G(1) complete
+        lds_barrier();
+        write_a(0, 0, 0);
         lds_barrier();
         for (int ch = 0; ch < nchk; ++ch) {
-            const int st = ch % kBtStages, nx = (ch + 2) % kBtStages, cn = min(ch + 2, clast);
-            bf16x8 ah[2], al[2];
-            load_a(ch, st, ah, al);
-            mult(0, st, ah, al);
+            const int st = ch % kBtStages, ab = ch & 1;
+            mult(0, st, ab);
             __builtin_amdgcn_sched_barrier(0);
-            dma_f(cn, nx, 0, kBtDma / 2);
+            write_a(ch + 1, (ch + 1) % kBtStages, ab ^ 1);
+            dma_f(min(ch + 2, clast), (ch + 2) % kBtStages, 0, kBtDma / 2);
             __builtin_amdgcn_sched_barrier(0);
-            mult(1, st, ah, al);
+            mult(1, st, ab);
             __builtin_amdgcn_sched_barrier(0);
-            dma_f(cn, nx, kBtDma / 2, kBtDma);
-            dma_g(cn, nx);
-            wait_vm<kBtDma + kNG>();  // F(ch+1) and G(ch+1) complete
+            dma_f(min(ch + 2, clast), (ch + 2) % kBtStages, kBtDma / 2, kBtDma);
+            dma_g(min(ch + 3, clast), st);
+            wait_vm<kBtDma + kNG>();  // F(ch+1) and G(ch+2) complete
             lds_barrier();
         }
         // drain the surplus loads of the last steps before the F buffers are reused
@@ -616,7 +638,7 @@ static_assert(kBrPass * kBrSlots % kBrThreads == 0 && kBrPass <= 2 * kBrThreads,
 struct BrSmem {
     bf16x8 bhi[2][2][kBrCb][64];   // B operand (gF chunk): [buffer][k step of 32 voxels][channel block][lane]
     bf16x8 blo[2][2][kBrCb][64];
-    int tab[kBrPass][kBrSlots];           // row table of this pass's rows (M: absent pair)
+    int tab[kBrPass][kBrSlots + 1];       // row table of this pass's rows (M: absent pair); padded row
     int rslot[kBrPass];                   // G->R slot of each row of the pass
     int tl_t[kBrSlots], tl_s[kBrSlots];   // tiles of the region (inside the grid) and their slots
     int ntl;
