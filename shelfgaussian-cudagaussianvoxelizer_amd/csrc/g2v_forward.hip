@@ -178,18 +178,29 @@ __device__ __forceinline__ void fwd_build_w(FwdSmem& sm, int j0, int kbeg, int k
     __syncthreads();
     const int noct = ksteps * 2;
     for (int o = wave; o < noct; o += kFwdWaves) {
+        // Straight-line evaluation (bitwise box test, exponential always computed, then
+        // selected): with no branches the compiler can issue the record reads of all eight
+        // entries ahead of their arithmetic.
         float wv[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const FwdParam r = sm.par[o * 8 + i];   // broadcast
-            const bool in = !(x < r.lb[0] || x > r.ub[0] || y < r.lb[1] || y > r.ub[1] || z < r.lb[2] ||
-                              z > r.ub[2]);
-            const float d0 = cx - r.mu[0], d1 = cy - r.mu[1], d2 = cz - r.mu[2];
-            const float qx = r.A[0] * d0 + r.A[1] * d1 + r.A[2] * d2;
-            const float qy = r.A[3] * d0 + r.A[4] * d1 + r.A[5] * d2;
-            const float qz = r.A[6] * d0 + r.A[7] * d1 + r.A[8] * d2;
+            const uint4* rp = reinterpret_cast<const uint4*>(&sm.par[o * 8 + i]);   // broadcast
+            const uint4 q0 = rp[0], q1 = rp[1], q2 = rp[2], q3 = rp[3], q4 = rp[4];
+            const float mu0 = __uint_as_float(q0.x), mu1 = __uint_as_float(q0.y), mu2 = __uint_as_float(q0.z);
+            const float ro = __uint_as_float(q0.w);
+            const float A0 = __uint_as_float(q1.x), A1 = __uint_as_float(q1.y), A2 = __uint_as_float(q1.z);
+            const float A3 = __uint_as_float(q1.w), A4 = __uint_as_float(q2.x), A5 = __uint_as_float(q2.y);
+            const float A6 = __uint_as_float(q2.z), A7 = __uint_as_float(q2.w), A8 = __uint_as_float(q3.x);
+            const int lb0 = (int)q3.y, lb1 = (int)q3.z, lb2 = (int)q3.w;
+            const int ub0 = (int)q4.x, ub1 = (int)q4.y, ub2 = (int)q4.z;
+            const bool in = (x >= lb0) & (x <= ub0) & (y >= lb1) & (y <= ub1) & (z >= lb2) & (z <= ub2);
+            const float d0 = cx - mu0, d1 = cy - mu1, d2 = cz - mu2;
+            const float qx = A0 * d0 + A1 * d1 + A2 * d2;
+            const float qy = A3 * d0 + A4 * d1 + A5 * d2;
+            const float qz = A6 * d0 + A7 * d1 + A8 * d2;
             const float m = d0 * qx + d1 * qy + d2 * qz;
-            const float w = in ? r.o * __expf(-0.5f * m) : 0.0f;   // the reference's weight (.cu:911-921)
+            const float e = __expf(-0.5f * m);
+            const float w = in ? ro * e : 0.0f;   // the reference's weight (.cu:911-921)
             if (add_density) dacc += w;
             wv[i] = (w > 0.0f) ? w : 0.0f;   // feature gate of the reference (.cu:936)
         }
