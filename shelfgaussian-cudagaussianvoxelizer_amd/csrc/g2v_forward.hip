@@ -339,7 +339,11 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
                         if (vs[ii] < 0) continue;
                         float* dst = grid_feats + (int64_t)vs[ii] * C + c0;
                         if ((C & 3) == 0) {
-                            if (c0 < C) *reinterpret_cast<float4*>(dst) = v;
+                            // written once and not read again by the forward: streaming store
+                            if (c0 < C) {
+                                const f32x4 nv = {v.x, v.y, v.z, v.w};
+                                __builtin_nontemporal_store(nv, reinterpret_cast<f32x4*>(dst));
+                            }
                         } else {
                             if (c0 + 0 < C) dst[0] = v.x;
                             if (c0 + 1 < C) dst[1] = v.y;
