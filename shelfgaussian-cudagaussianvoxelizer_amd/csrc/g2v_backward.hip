@@ -173,6 +173,16 @@ __device__ __forceinline__ void dma4(const void* gptr, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
                  :: "v"(gptr), "s"(lds) : "memory", "m0");
 }
+// Streaming variants (non-temporal): for data read once, so that it does not evict the feature
+// rows that many tiles re-read.
+__device__ __forceinline__ void dma16_nt(const void* gptr, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
+                 :: "v"(gptr), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4_nt(const void* gptr, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off nt"
+                 :: "v"(gptr), "s"(lds) : "memory", "m0");
+}
 
 struct BtSmem {
     union {
@@ -281,9 +291,9 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
 #pragma unroll
         for (int k = 0; k < kNG; ++k) {
             if (VEC)
-                dma16(gsrc[k] + min(chunk * kBtKc + gcoff[k], C - 4), uniform(lds_addr(&sm.graw[stage][wave * 8][0])));
+                dma16_nt(gsrc[k] + min(chunk * kBtKc + gcoff[k], C - 4), uniform(lds_addr(&sm.graw[stage][wave * 8][0])));
             else
-                dma4(gsrc[k] + min(chunk * kBtKc + gcoff[k], C - 1),
+                dma4_nt(gsrc[k] + min(chunk * kBtKc + gcoff[k], C - 1),
                      uniform(lds_addr(&sm.graw[stage][wave * 8 + 2 * k][0])));
         }
     };
@@ -689,7 +699,8 @@ __device__ __forceinline__ unsigned br_load_tile(const Grid& G, int C, int c0, i
     for (int k = 0; k < 2; ++k)
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            v[k][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff[k][i >> 2], soff[i & 3], 0));
+            // aux 2: non-temporal (grad_feats is streamed once per region)
+            v[k][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff[k][i >> 2], soff[i & 3], 2));
             mask |= (cok && xok[k] && yok[i >> 2] && zok[i & 3]) ? (1u << (i + 8 * k)) : 0u;
         }
     return mask;
@@ -939,7 +950,8 @@ __global__ void __launch_bounds__(kBgThreads) k_bwd_gauss(
                 const float4 v = *reinterpret_cast<const float4*>(gpart + (int64_t)r * C + c);
                 s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
             }
-            *reinterpret_cast<float4*>(out + c) = s;
+            const f32x4 nv = {s.x, s.y, s.z, s.w};
+            __builtin_nontemporal_store(nv, reinterpret_cast<f32x4*>(out + c));
         }
     } else {
         for (int c = threadIdx.x; c < C; c += kBgThreads) {
