@@ -212,6 +212,7 @@ __device__ __forceinline__ void wait_vm() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
+
 // Workgroup barrier for LDS hand-offs only: waits for this wave's LDS operations and meets the
 // other waves, without the release fence of __syncthreads (that fence would also wait for every
 // outstanding global load, including the direct-to-LDS loads kept in flight on purpose).  The
@@ -311,9 +312,10 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
 
         // F rows by direct-to-LDS loads: row group rg = wave + kBtWaves*i (8 rows, 1 KB) is
         // loaded by this wave; lane = (row rg*8 + lane/8, slot lane%8) and slot p carries the
-        // 16-byte piece p ^ swz(row) of the row's chunk.  Rows past the list read the zero
-        // row; a group wholly past it reads one 16-byte piece of the zero row in every lane.
-        // Every wave issues exactly kBtDma + kNG loads per chunk, so the wait counts below are exact.
+        // 16-byte piece p ^ swz(row) of the row's chunk.  Rows past the list read the zero row;
+        // groups wholly past it are not loaded (no wave reads them).  A wave issues exactly
+        // nld = (its groups within the list) + kNG loads per chunk, so the wait counts below are
+        // exact.
         uint32_t doff[kBtDma];
 #pragma unroll
         for (int i = 0; i < kBtDma; ++i) {
@@ -323,6 +325,11 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             const int piece = (lane & 7) ^ swz(r);
             doff[i] = (rg * 8 < pcount) ? (uint32_t)g * fstride + (uint32_t)piece * 16u : (uint32_t)n * fstride;
         }
+        // the wave's groups within the list are its first nf (rg grows with i)
+        int nf = 0;
+#pragma unroll
+        for (int i = 0; i < kBtDma; ++i) nf += ((wave + kBtWaves * i) * 8 < pcount) ? 1 : 0;
+        nf = uniform(nf);
         auto dma_f = [&](int chunk, int buf, int i0, int i1) {
 #pragma unroll
             for (int i = 0; i < kBtDma; ++i) {
@@ -394,29 +401,43 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
         // writes the A operand of chunk ch+1 and issues the loads of F(ch+2) and G(ch+3); then it
         // waits until only those loads are outstanding.  G(ch+3) goes to the stage of G(ch), whose
         // A operand was written in the previous step.
+        // The chunk loop, instantiated for the wave's group count NF (exact wait immediates;
+        // waves of one workgroup may run different instantiations, with the same barriers).
         const int clast = nchk - 1;
-        dma_g(0, 0);
-        dma_f(0, 0, 0, kBtDma);
-        dma_g(min(1, clast), 1);
-        dma_f(min(1, clast), 1, 0, kBtDma);
-        dma_g(min(2, clast), 2);
-        wait_vm<kBtDma + kNG>();      // G(0), F(0), G(1) complete
-        lds_barrier();
-        write_a(0, 0, 0);
-        lds_barrier();
-        for (int ch = 0; ch < nchk; ++ch) {
-            const int st = ch % kBtStages, ab = ch & 1;
-            mult(0, st, ab);
-            __builtin_amdgcn_sched_barrier(0);
-            write_a(ch + 1, (ch + 1) % kBtStages, ab ^ 1);
-            dma_f(min(ch + 2, clast), (ch + 2) % kBtStages, 0, kBtDma / 2);
-            __builtin_amdgcn_sched_barrier(0);
-            mult(1, st, ab);
-            __builtin_amdgcn_sched_barrier(0);
-            dma_f(min(ch + 2, clast), (ch + 2) % kBtStages, kBtDma / 2, kBtDma);
-            dma_g(min(ch + 3, clast), st);
-            wait_vm<kBtDma + kNG>();  // F(ch+1) and G(ch+2) complete
+        auto chunk_loop = [&](auto nfc) {
+            constexpr int NF = decltype(nfc)::value;
+            constexpr int kLd = NF + kNG;   // loads per wave per chunk
+            dma_g(0, 0);
+            dma_f(0, 0, 0, NF);
+            dma_g(min(1, clast), 1);
+            dma_f(min(1, clast), 1, 0, NF);
+            dma_g(min(2, clast), 2);
+            wait_vm<kLd>();               // G(0), F(0), G(1) complete
             lds_barrier();
+            write_a(0, 0, 0);
+            lds_barrier();
+            for (int ch = 0; ch < nchk; ++ch) {
+                const int st = ch % kBtStages, ab = ch & 1;
+                mult(0, st, ab);
+                __builtin_amdgcn_sched_barrier(0);
+                write_a(ch + 1, (ch + 1) % kBtStages, ab ^ 1);
+                dma_f(min(ch + 2, clast), (ch + 2) % kBtStages, 0, min(NF, kBtDma / 2));
+                __builtin_amdgcn_sched_barrier(0);
+                mult(1, st, ab);
+                __builtin_amdgcn_sched_barrier(0);
+                dma_f(min(ch + 2, clast), (ch + 2) % kBtStages, kBtDma / 2, NF);
+                dma_g(min(ch + 3, clast), st);
+                wait_vm<kLd>();           // F(ch+1) and G(ch+2) complete
+                lds_barrier();
+            }
+        };
+        static_assert(kBtDma == 4, "group-count dispatch");
+        switch (nf) {
+            case 4: chunk_loop(std::integral_constant<int, 4>{}); break;
+            case 3: chunk_loop(std::integral_constant<int, 3>{}); break;
+            case 2: chunk_loop(std::integral_constant<int, 2>{}); break;
+            case 1: chunk_loop(std::integral_constant<int, 1>{}); break;
+            default: chunk_loop(std::integral_constant<int, 0>{}); break;
         }
         // drain the surplus loads of the last steps before the F buffers are reused
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
@@ -497,7 +518,9 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
                     const float w = p.o * e;
                     const float wtil = w * sm.inv[r];
                     split_bf16(wtil, hs[ii], ls[ii]);
-                    rowt[i] += (w > 0.0f ? wtil : 0.0f) * acc[j][i];
+                    // a select, not a product with 0: columns past the list hold whatever
+                    // the unloaded F rows left in LDS
+                    rowt[i] += (w > 0.0f) ? wtil * acc[j][i] : 0.0f;
                 }
                 if (gok) {
                     const int r0 = mb * 32 + 8 * q4 + 4 * h;
