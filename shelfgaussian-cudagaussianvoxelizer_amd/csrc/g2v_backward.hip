@@ -125,17 +125,28 @@ constexpr int kBtRowBytes = kBtKc * 4;     // bytes of one row's chunk (hi and l
 
 __global__ void __launch_bounds__(256) k_split_chunks(const float* __restrict__ src, int n, int C, int nchk,
                                                       __bf16* __restrict__ dst) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;   // (row, channel), channels fastest
-    const int Cq = nchk * kBtKc;
-    if (i >= (int64_t)(n + 1) * Cq) return;
-    const int64_t r = i / Cq;
-    const int c = (int)(i - r * Cq);
-    const float v = (r < n && c < C) ? src[r * C + c] : 0.0f;
-    __bf16 h, l;
-    split_bf16(v, h, l);
+    // one thread per 8 channels of a row (an octet of a chunk): 16-byte hi and lo stores
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int noct = nchk * (kBtKc / 8);
+    if (i >= (int64_t)(n + 1) * noct) return;
+    const int64_t r = i / noct;
+    const int oc = (int)(i - r * noct);
+    const int c = oc * 8;
+    float v[8];
+    if (r < n && c + 8 <= C && ((uintptr_t)(src + r * C + c) & 15) == 0) {
+        const float4 a = *reinterpret_cast<const float4*>(src + r * C + c);
+        const float4 b = *reinterpret_cast<const float4*>(src + r * C + c + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (r < n && c + e < C) ? src[r * C + c + e] : 0.0f;
+    }
+    bf16x8 h, l;
+    split8(v, h, l);
     __bf16* row = dst + (r * nchk + c / kBtKc) * (2 * kBtKc);
-    row[c % kBtKc] = h;
-    row[kBtKc + c % kBtKc] = l;
+    *reinterpret_cast<bf16x8*>(row + c % kBtKc) = h;
+    *reinterpret_cast<bf16x8*>(row + kBtKc + c % kBtKc) = l;
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1092,7 +1103,7 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
     hipError_t e;
 
     // features as 32-channel chunks of bf16 hi/lo (B operand of phase A), plus a zero row
-    const int64_t fcount = (int64_t)(n + 1) * nchk * kBtKc;
+    const int64_t fcount = (int64_t)(n + 1) * nchk * (kBtKc / 8);   // one thread per 8 channels
     G2V_LAUNCH(k_split_chunks, dim3((unsigned)ceil_div(fcount, 256)), dim3(256), 0, s, features, n, C, nchk,
                b.fsp);
     if (M > 0 && T > 0) {

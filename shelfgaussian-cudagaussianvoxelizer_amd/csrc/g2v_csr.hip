@@ -179,12 +179,79 @@ __global__ void __launch_bounds__(kScanThreads) k_scan_apply(const int* in, int*
     }
 }
 
+// Single-workgroup scan for inputs up to kScanSingleMax.  Tiles of 1024 x 32 values: coalesced
+// loads into LDS (row of 32 values per thread, padded to 33 words), a sequential scan of each
+// thread's row, a workgroup scan of the row totals, and coalesced stores back from LDS; a
+// running carry joins the tiles.  In-place safe (a tile is read completely before it is written).
+constexpr int kScan1Threads = 1024;
+constexpr int kScan1Items = 32;
+constexpr int kScan1Row = kScan1Items + 1;
+constexpr int64_t kScanSingleMax = int64_t(1) << 20;
+
+__global__ void __launch_bounds__(kScan1Threads) k_scan_single(const int* in, int* out, int n, int inclusive,
+                                                               long long* __restrict__ total_dev) {
+    __shared__ int buf[kScan1Threads * kScan1Row];
+    __shared__ long long wsum[kScan1Threads / 64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int kTile = kScan1Threads * kScan1Items;
+    long long carry = 0;
+    for (int base = 0; base < n; base += kTile) {
+        // coalesced load: value e of the tile -> row e / 32, column e % 32
+#pragma unroll
+        for (int k = 0; k < kScan1Items; ++k) {
+            const int e = k * kScan1Threads + threadIdx.x;
+            buf[(e / kScan1Items) * kScan1Row + e % kScan1Items] = (base + e < n) ? in[base + e] : 0;
+        }
+        __syncthreads();
+        int* row = &buf[threadIdx.x * kScan1Row];
+        long long local = 0;
+#pragma unroll
+        for (int r = 0; r < kScan1Items; ++r) local += row[r];
+        long long x = local;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const long long t = __shfl_up(x, off, 64);
+            if (lane >= off) x += t;
+        }
+        if (lane == 63) wsum[wave] = x;
+        __syncthreads();
+        long long wcarry = 0, tot = 0;
+#pragma unroll
+        for (int w = 0; w < kScan1Threads / 64; ++w) {
+            const long long sw = wsum[w];
+            wcarry += (w < wave) ? sw : 0;
+            tot += sw;
+        }
+        long long run = carry + wcarry + x - local;
+#pragma unroll
+        for (int r = 0; r < kScan1Items; ++r) {
+            const long long nxt = run + row[r];
+            row[r] = (int)(inclusive ? nxt : run);
+            run = nxt;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < kScan1Items; ++k) {
+            const int e = k * kScan1Threads + threadIdx.x;
+            if (base + e < n) out[base + e] = buf[(e / kScan1Items) * kScan1Row + e % kScan1Items];
+        }
+        __syncthreads();   // buf and wsum are rewritten by the next tile
+        carry += tot;
+    }
+    if (threadIdx.x == 0 && total_dev) *total_dev = carry;
+}
+
 size_t scan_workspace(int64_t n) {
     return (size_t)(ceil_div(n > 0 ? n : 1, kScanTile) + 1) * sizeof(long long) + 256;
 }
 
 hipError_t scan_i32(const int* in, int* out, int64_t n, bool inclusive, long long* total_dev,
                     void* ws, hipStream_t s) {
+    if (n <= kScanSingleMax) {
+        G2V_LAUNCH(k_scan_single, dim3(1), dim3(kScan1Threads), 0, s, in, out, (int)n, inclusive ? 1 : 0,
+                   total_dev);
+        return hipGetLastError();
+    }
     const int64_t nb = ceil_div(n > 0 ? n : 1, kScanTile);
     long long* partials = static_cast<long long*>(ws);
     G2V_LAUNCH(k_scan_reduce, dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, n, partials);

@@ -70,16 +70,29 @@ hipError_t launch_forward_density(const Grid& G, const float* means, const float
 __global__ void __launch_bounds__(256) k_split_pack(const float* __restrict__ src, int n, int C, int Cp,
                                                     uint32_t* __restrict__ dst) {
     // (n + 1) x Cp packed pairs: row n and columns >= C are zero, so padded K slots and channels
-    // can be gathered without bounds checks
+    // can be gathered without bounds checks.  One thread per 4 channels (16-byte store).
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= (int64_t)(n + 1) * Cp) return;
-    const int64_t r = i / Cp;
-    const int c = (int)(i - r * Cp);
-    const float v = (r < n && c < C) ? src[r * C + c] : 0.0f;
-    __bf16 h, l;
-    split_bf16(v, h, l);
-    dst[i] = (uint32_t)__builtin_bit_cast(unsigned short, h) |
-             ((uint32_t)__builtin_bit_cast(unsigned short, l) << 16);
+    const int nq = Cp / 4;
+    if (i >= (int64_t)(n + 1) * nq) return;
+    const int64_t r = i / nq;
+    const int c = (int)(i - r * nq) * 4;
+    float v[4];
+    if (r < n && c + 4 <= C && ((uintptr_t)(src + r * C + c) & 15) == 0) {
+        const float4 a = *reinterpret_cast<const float4*>(src + r * C + c);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (r < n && c + e < C) ? src[r * C + c + e] : 0.0f;
+    }
+    uint4 o;
+    uint32_t* op = reinterpret_cast<uint32_t*>(&o);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        __bf16 h, l;
+        split_bf16(v[e], h, l);
+        op[e] = (uint32_t)__builtin_bit_cast(unsigned short, h) | ((uint32_t)__builtin_bit_cast(unsigned short, l) << 16);
+    }
+    *reinterpret_cast<uint4*>(dst + r * Cp + c) = o;
 }
 
 // B fragment (hi and lo) from 8 packed pairs: element i of the fragment is pair u[i].
@@ -370,7 +383,7 @@ hipError_t launch_forward_feats(const Grid& G, int C, const float* means, const 
     const int Cp = packed_channels(C);
     const int64_t count = (int64_t)(n + 1) * Cp;
     if (count * 4 > (int64_t)UINT32_MAX) return hipErrorInvalidValue;   // byte offsets are 32-bit
-    G2V_LAUNCH(k_split_pack, dim3((unsigned)ceil_div(count, 256)), dim3(256), 0, s, features, n, C, Cp, fpk);
+    G2V_LAUNCH(k_split_pack, dim3((unsigned)ceil_div(count / 4, 256)), dim3(256), 0, s, features, n, C, Cp, fpk);
     const int blocks = (int)ceil_div(T, 8) * 8;
     G2V_LAUNCH(k_fwd_feats, dim3(blocks), dim3(kFwdThreads), 0, s, G, C, means, opacity,
                        cov_inv, lb, ub, tile_offsets, sorted_gauss, M, n, Cp, (const uint32_t*)fpk, density,
