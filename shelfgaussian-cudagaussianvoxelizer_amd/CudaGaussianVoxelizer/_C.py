@@ -154,6 +154,12 @@ def _forward(means3D, opacity, covariances, voxel_size, voxel_range, features, k
                                          _ptr(ws2), ws2.numel(), stream),
                    "gaussian_voxelizer_forward (splat)")
         stop.record(cur)
+        if keep_t2g:
+            # the backward's outputs and workspace, allocated while the forward kernels run
+            t2g["grads"] = (torch.empty(n, 3, **f32), torch.empty(n, 9, **f32), torch.empty(n, **f32),
+                            torch.empty(n, C, **f32))
+            t2g["ws"] = torch.empty(max(1, lib.g2v_backward_workspace(n, C, M, t2g["num_region_pairs"], vs, vr)),
+                                    dtype=torch.uint8, device=dev)
         stop.synchronize()
         fwd_sec = start.elapsed_time(stop) / 1000.0
     return (density, cov_inv, lb, ub, nvox, grid_feats, g2t_offsets, g2t_tile_ids, fwd_sec), t2g
@@ -213,10 +219,13 @@ def _backward(grad_output, grad_feats_output, means3D, opacity, cov_inv, voxel_s
     with torch.cuda.device(dev):
         stream = _stream(dev)
         cur = torch.cuda.current_stream(dev)
-        grad_means = torch.empty(n, 3, dtype=f32, device=dev)
-        grad_cov = torch.empty(n, 9, dtype=f32, device=dev)
-        grad_opacity = torch.empty(n, dtype=f32, device=dev)
-        grad_feats = torch.empty(n, C, dtype=f32, device=dev)
+        if t2g is not None and "grads" in t2g:   # allocated by the forward
+            grad_means, grad_cov, grad_opacity, grad_feats = t2g["grads"]
+        else:
+            grad_means = torch.empty(n, 3, dtype=f32, device=dev)
+            grad_cov = torch.empty(n, 9, dtype=f32, device=dev)
+            grad_opacity = torch.empty(n, dtype=f32, device=dev)
+            grad_feats = torch.empty(n, C, dtype=f32, device=dev)
         start = torch.cuda.Event(enable_timing=True)
         stop = torch.cuda.Event(enable_timing=True)
         start.record(cur)
@@ -229,7 +238,10 @@ def _backward(grad_output, grad_feats_output, means3D, opacity, cov_inv, voxel_s
                                              _ptr(plan_ws), plan_ws.numel(), ctypes.byref(MR), stream),
                        "gaussian_voxelizer_backward (plan)")
             MR = int(MR.value)
-        ws = torch.empty(max(1, lib.g2v_backward_workspace(n, C, M, MR, vs, vr)), dtype=torch.uint8, device=dev)
+        if t2g is not None and "ws" in t2g and C > 0:
+            ws = t2g["ws"]
+        else:
+            ws = torch.empty(max(1, lib.g2v_backward_workspace(n, C, M, MR, vs, vr)), dtype=torch.uint8, device=dev)
         _lib.check(lib.g2v_backward(n, C, _ptr(grad_output), _ptr(gF), _ptr(means3D), _ptr(opacity),
                                     _ptr(cov_inv), vs, vr, _ptr(valid_voxel_lb), _ptr(valid_voxel_ub),
                                     _ptr(num_voxels_per_gaussian), _ptr(g2t_offsets), _ptr(g2t_tile_ids),

@@ -155,13 +155,12 @@ int g2v_forward_plan(int n, const float* means3D, const float* covariances,
     G2V_HIP(launch_boxes(G, n, means3D, covariances, cov_inv, valid_voxel_lb, valid_voxel_ub,
                          num_voxels_per_gaussian, g2t_offsets, s));
     long long M = 0, MR = 0;
-    if (n > 0) {
-        G2V_HIP(scan_i32(g2t_offsets + 1, g2t_offsets + 1, n, true, total, scan_ws, s));
-        G2V_HIP(hipMemcpyAsync(&M, total, sizeof(long long), hipMemcpyDeviceToHost, s));
-    }
-    // the backward's (region, Gaussian) pair count rides on the same synchronisation
+    if (n > 0) G2V_HIP(scan_i32(g2t_offsets + 1, g2t_offsets + 1, n, true, total, scan_ws, s));
+    // the backward's (region, Gaussian) pair count rides on the same synchronisation; the copies
+    // to (pageable) host memory come after every launch, so the host waits only once
     if (bwd_plan_workspace)
         G2V_HIP(backward_plan_async(G, n, valid_voxel_lb, valid_voxel_ub, bwd_plan_workspace, &MR, s));
+    if (n > 0) G2V_HIP(hipMemcpyAsync(&M, total, sizeof(long long), hipMemcpyDeviceToHost, s));
     G2V_HIP(hipStreamSynchronize(s));
     if (M > 2147483647ll)
         return fail(G2V_ERR_LIMIT, "%lld Gaussian-tile pairs exceed the int32 CSR (limit 2^31-1)", M);

@@ -97,6 +97,8 @@ CSR_CASES = {
                             var_range=(0.01, 0.2)),
     "one_tile_grid": W.Workload("one_tile", 50, 4, voxel_range=(0.0, 0.0, 0.0, 1.2, 1.2, 1.2), voxel_size=(0.4, 0.4, 0.4),
                                 var_range=(0.01, 0.3)),
+    # more than 2^20 Gaussians: the offsets scan takes the multi-workgroup path
+    "many_small_n1100000": W.Workload("many_small", 1_100_000, None, var_range=(0.01, 0.05)),
 }
 
 
