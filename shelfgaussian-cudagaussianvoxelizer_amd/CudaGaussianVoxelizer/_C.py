@@ -71,6 +71,37 @@ def _stream(device):
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
+_EVENTS = {}
+
+
+def _timing_events(device):
+    """A (start, stop) pair of timing events per device and thread, reused by every call (each call
+    records and synchronises both before it returns)."""
+    import threading
+    key = (device.index, threading.get_ident())
+    ev = _EVENTS.get(key)
+    if ev is None:
+        ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        _EVENTS[key] = ev
+    return ev
+
+
+class _OnDevice:
+    """torch.cuda.device(dev) only when dev is not already the current device."""
+
+    def __init__(self, dev):
+        self.ctx = None if dev.index == torch.cuda.current_device() else torch.cuda.device(dev)
+
+    def __enter__(self):
+        if self.ctx is not None:
+            self.ctx.__enter__()
+
+    def __exit__(self, *exc):
+        if self.ctx is not None:
+            self.ctx.__exit__(*exc)
+        return False
+
+
 def gaussian_voxelizer_forward(means3D, opacity, covariances, voxel_size, voxel_range, features=None):
     """Gaussian voxelization forward pass.
 
@@ -110,11 +141,11 @@ def _forward(means3D, opacity, covariances, voxel_size, voxel_range, features, k
     vs_h = _host_values(voxel_size, 3, "voxel_size")
     vr_h = _host_values(voxel_range, 6, "voxel_range")
     vs, vr = _lib.floats(vs_h), _lib.floats(vr_h)
-    (X, Y, Z), _ = grid_dims(vs_h, vr_h)
+    (X, Y, Z), (Tx, Ty, Tz) = grid_dims(vs_h, vr_h)
 
-    with torch.cuda.device(dev):
-        stream = _stream(dev)
+    with _OnDevice(dev):
         cur = torch.cuda.current_stream(dev)
+        stream = ctypes.c_void_p(cur.cuda_stream)
         i32 = dict(dtype=torch.int32, device=dev)
         f32 = dict(dtype=torch.float32, device=dev)
         cov_inv = torch.empty(n, 9, **f32)
@@ -123,8 +154,11 @@ def _forward(means3D, opacity, covariances, voxel_size, voxel_range, features, k
         nvox = torch.empty(n, **i32)
         g2t_offsets = torch.empty(n + 1, **i32)
         ws = torch.empty(lib.g2v_forward_plan_workspace(n), dtype=torch.uint8, device=dev)
-        start = torch.cuda.Event(enable_timing=True)
-        stop = torch.cuda.Event(enable_timing=True)
+        # outputs whose size does not depend on the plan's count, allocated before its host wait
+        density = torch.empty(X, Y, Z, **f32)
+        grid_feats = torch.empty(X, Y, Z, C, **f32)
+        t2g_toff = torch.empty(Tx * Ty * Tz + 1, **i32) if keep_t2g else None
+        start, stop = _timing_events(dev)
         start.record(cur)
         M = ctypes.c_longlong(0)
         MR = ctypes.c_longlong(0)
@@ -139,18 +173,16 @@ def _forward(means3D, opacity, covariances, voxel_size, voxel_range, features, k
                    "gaussian_voxelizer_forward (plan)")
         M = int(M.value)
         g2t_tile_ids = torch.empty(M, **i32)
-        density = torch.empty(X, Y, Z, **f32)
-        grid_feats = torch.empty(X, Y, Z, C, **f32)
         ws2 = torch.empty(lib.g2v_forward_splat_workspace(n, C, M, vs, vr), dtype=torch.uint8, device=dev)
         t2g = None
+        csr = (None, None, None)
         if keep_t2g:
-            (_, (Tx, Ty, Tz)) = grid_dims(vs_h, vr_h)
-            t2g = dict(csr=(torch.empty(M, **i32), torch.empty(M, **i32), torch.empty(Tx * Ty * Tz + 1, **i32)),
-                       plan=bplan, num_region_pairs=int(MR.value))
+            csr = (torch.empty(M, **i32), torch.empty(M, **i32), t2g_toff)
+            t2g = dict(csr=csr, plan=bplan, num_region_pairs=int(MR.value), vs=vs, vr=vr, dims=(X, Y, Z))
         _lib.check(lib.g2v_forward_splat(n, C, _ptr(means), _ptr(op), _ptr(feats), vs, vr,
                                          _ptr(cov_inv), _ptr(lb), _ptr(ub), _ptr(g2t_offsets), M,
                                          _ptr(g2t_tile_ids), _ptr(density), _ptr(grid_feats),
-                                         *(_ptr(t) for t in (t2g["csr"] if t2g else (None, None, None))),
+                                         _ptr(csr[0]), _ptr(csr[1]), _ptr(csr[2]),
                                          _ptr(ws2), ws2.numel(), stream),
                    "gaussian_voxelizer_forward (splat)")
         stop.record(cur)
@@ -181,32 +213,42 @@ def gaussian_voxelizer_backward(grad_output, grad_feats_output, means3D, opacity
 def _backward(grad_output, grad_feats_output, means3D, opacity, cov_inv, voxel_size, voxel_range,
               valid_voxel_lb, valid_voxel_ub, num_voxels_per_gaussian, g2t_offsets, g2t_tile_ids,
               density, grid_feats, features, t2g):
-    """The backward; t2g is what _forward(keep_t2g=True) returned beside the 9-tuple, or None."""
+    """The backward; t2g is what _forward(keep_t2g=True) returned beside the 9-tuple, or None.
+    With t2g the saved tensors are the forward's own outputs (already checked there), and the
+    grid, plan, outputs and workspace come from the forward: only the upstream gradients are
+    checked here."""
     lib = _lib.load()
     if not isinstance(means3D, torch.Tensor) or means3D.device.type != "cuda":
         raise RuntimeError("means3D must be a GPU tensor")
     dev = means3D.device
     f32, i32 = torch.float32, torch.int32
-    for t, name in ((grad_output, "grad_output"), (means3D, "means3D"), (opacity, "opacity"),
-                    (cov_inv, "cov_inv"), (density, "density"), (grid_feats, "grid_feats")):
-        _check_saved(t, name, f32, dev)
-    for t, name in ((valid_voxel_lb, "valid_voxel_lb"), (valid_voxel_ub, "valid_voxel_ub"),
-                    (num_voxels_per_gaussian, "num_voxels_per_gaussian"), (g2t_offsets, "g2t_offsets"),
-                    (g2t_tile_ids, "g2t_tile_ids")):
-        _check_saved(t, name, i32, dev)
+    trusted = t2g is not None and "grads" in t2g
+    if trusted:
+        vs, vr = t2g["vs"], t2g["vr"]
+        X, Y, Z = t2g["dims"]
+        _check_saved(grad_output, "grad_output", f32, dev)
+    else:
+        for t, name in ((grad_output, "grad_output"), (means3D, "means3D"), (opacity, "opacity"),
+                        (cov_inv, "cov_inv"), (density, "density"), (grid_feats, "grid_feats")):
+            _check_saved(t, name, f32, dev)
+        for t, name in ((valid_voxel_lb, "valid_voxel_lb"), (valid_voxel_ub, "valid_voxel_ub"),
+                        (num_voxels_per_gaussian, "num_voxels_per_gaussian"), (g2t_offsets, "g2t_offsets"),
+                        (g2t_tile_ids, "g2t_tile_ids")):
+            _check_saved(t, name, i32, dev)
+        vs_h = _host_values(voxel_size, 3, "voxel_size")
+        vr_h = _host_values(voxel_range, 6, "voxel_range")
+        vs, vr = _lib.floats(vs_h), _lib.floats(vr_h)
+        (X, Y, Z), _ = grid_dims(vs_h, vr_h)
     n = means3D.shape[0]
     if g2t_offsets.numel() != n + 1:
         raise RuntimeError(f"g2t_offsets must have N+1 = {n + 1} elements, got {g2t_offsets.numel()}")
-    vs_h = _host_values(voxel_size, 3, "voxel_size")
-    vr_h = _host_values(voxel_range, 6, "voxel_range")
-    vs, vr = _lib.floats(vs_h), _lib.floats(vr_h)
-    (X, Y, Z), _ = grid_dims(vs_h, vr_h)
     if tuple(grad_output.shape) != (X, Y, Z):
         raise RuntimeError(f"grad_output must be {(X, Y, Z)}, got {tuple(grad_output.shape)}")
     C = 0
     feats = gF = None
     if features is not None:
-        _check_saved(features, "features", f32, dev)
+        if not trusted:
+            _check_saved(features, "features", f32, dev)
         C = features.shape[1]
         if C > 0:
             feats = features
@@ -216,18 +258,17 @@ def _backward(grad_output, grad_feats_output, means3D, opacity, cov_inv, voxel_s
             gF = grad_feats_output
     M = g2t_tile_ids.numel()
 
-    with torch.cuda.device(dev):
-        stream = _stream(dev)
+    with _OnDevice(dev):
         cur = torch.cuda.current_stream(dev)
-        if t2g is not None and "grads" in t2g:   # allocated by the forward
+        stream = ctypes.c_void_p(cur.cuda_stream)
+        if trusted:   # allocated by the forward
             grad_means, grad_cov, grad_opacity, grad_feats = t2g["grads"]
         else:
             grad_means = torch.empty(n, 3, dtype=f32, device=dev)
             grad_cov = torch.empty(n, 9, dtype=f32, device=dev)
             grad_opacity = torch.empty(n, dtype=f32, device=dev)
             grad_feats = torch.empty(n, C, dtype=f32, device=dev)
-        start = torch.cuda.Event(enable_timing=True)
-        stop = torch.cuda.Event(enable_timing=True)
+        start, stop = _timing_events(dev)
         start.record(cur)
         if t2g is not None and C > 0:   # planned by the forward
             plan_ws, MR = t2g["plan"], t2g["num_region_pairs"]
@@ -238,16 +279,17 @@ def _backward(grad_output, grad_feats_output, means3D, opacity, cov_inv, voxel_s
                                              _ptr(plan_ws), plan_ws.numel(), ctypes.byref(MR), stream),
                        "gaussian_voxelizer_backward (plan)")
             MR = int(MR.value)
-        if t2g is not None and "ws" in t2g and C > 0:
+        if trusted and C > 0:
             ws = t2g["ws"]
         else:
             ws = torch.empty(max(1, lib.g2v_backward_workspace(n, C, M, MR, vs, vr)), dtype=torch.uint8, device=dev)
+        csr = t2g["csr"] if t2g else (None, None, None)
         _lib.check(lib.g2v_backward(n, C, _ptr(grad_output), _ptr(gF), _ptr(means3D), _ptr(opacity),
                                     _ptr(cov_inv), vs, vr, _ptr(valid_voxel_lb), _ptr(valid_voxel_ub),
                                     _ptr(num_voxels_per_gaussian), _ptr(g2t_offsets), _ptr(g2t_tile_ids),
                                     M, MR, _ptr(density), _ptr(grid_feats), _ptr(feats),
                                     _ptr(grad_means), _ptr(grad_cov), _ptr(grad_opacity),
-                                    _ptr(grad_feats), *(_ptr(t) for t in (t2g["csr"] if t2g else (None, None, None))),
+                                    _ptr(grad_feats), _ptr(csr[0]), _ptr(csr[1]), _ptr(csr[2]),
                                     _ptr(plan_ws), _ptr(ws), ws.numel(), stream),
                    "gaussian_voxelizer_backward")
         stop.record(cur)
