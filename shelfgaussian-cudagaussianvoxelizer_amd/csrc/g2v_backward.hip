@@ -544,18 +544,12 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             }
         }
         if (!multi) {
-            // rows are shared by the 32 lanes of each half-wave: reduce over them
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                float v = rowt[i];
-#pragma unroll
-                for (int off = 1; off < 32; off <<= 1) v += __shfl_xor(v, off, 64);
-                rowt[i] = v;
-            }
-            if ((lane & 31) == 0) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    sm.tpart[ngrp][mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3)] = rowt[i];
+            // rows are shared by the 32 lanes of each half-wave: reduce over them (lanes 2i and
+            // 2i+1 of a half end up with the sum of element i)
+            const float rs = transpose_sum16(rowt, lane & 31);
+            if ((lane & 1) == 0) {
+                const int i = (lane >> 1) & 15;
+                sm.tpart[ngrp][mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3)] = rs;
             }
             __syncthreads();
             if (threadIdx.x < 64) {

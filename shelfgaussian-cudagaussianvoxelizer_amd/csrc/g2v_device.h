@@ -186,6 +186,38 @@ __device__ __forceinline__ f32x4 mfma3_16x16x32(const bf16x8& ah, const bf16x8& 
     return acc;
 }
 
+// v of lane l ^ m within each 32-lane half, for m in {1, 2, 4, 8, 16}: DPP quad permutes for 1
+// and 2, ds_swizzle (bit mode) for 4, 8 and 16; no LDS address is needed.
+template <int M>
+__device__ __forceinline__ float xor_shfl(float v) {
+    static_assert(M == 1 || M == 2 || M == 4 || M == 8 || M == 16, "xor mask");
+    const int iv = __float_as_int(v);
+    if constexpr (M == 1) return __int_as_float(__builtin_amdgcn_mov_dpp(iv, 0xB1, 0xF, 0xF, false));
+    else if constexpr (M == 2) return __int_as_float(__builtin_amdgcn_mov_dpp(iv, 0x4E, 0xF, 0xF, false));
+    else return __int_as_float(__builtin_amdgcn_ds_swizzle(iv, 0x1F | (M << 10)));
+}
+
+// Sums of 16 values per lane over the 32 lanes of each half-wave, transposed: afterwards lanes
+// 2k and 2k+1 (of each half) hold the sum of value k.  Each butterfly step hands half of the
+// remaining values to the partner lane: 8 + 4 + 2 + 1 + 1 exchanges instead of 16 x 5.
+__device__ __forceinline__ float transpose_sum16(const float (&v)[16], int l /* lane % 32 */) {
+    float w[8];
+    const bool b16 = l & 16, b8 = l & 8, b4 = l & 4, b2 = l & 2;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+        w[k] = (b16 ? v[k + 8] : v[k]) + xor_shfl<16>(b16 ? v[k] : v[k + 8]);
+    float u[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        u[k] = (b8 ? w[k + 4] : w[k]) + xor_shfl<8>(b8 ? w[k] : w[k + 4]);
+    float t[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+        t[k] = (b4 ? u[k + 2] : u[k]) + xor_shfl<4>(b4 ? u[k] : u[k + 2]);
+    const float q = (b2 ? t[1] : t[0]) + xor_shfl<2>(b2 ? t[0] : t[1]);
+    return q + xor_shfl<1>(q);
+}
+
 // Wave64 sum (every lane gets the total).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
