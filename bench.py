@@ -46,6 +46,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-sample", type=float, default=1.0,
                     help="fraction of tiles (forward) and Gaussians (backward) the CPU baseline runs")
+    ap.add_argument("--no-cosine", action="store_true",
+                    help="skip the feature cosine-loss leg (the consumer of grid_feats)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="also run a plain device copy of this size (PMC scale reference)")
     return ap.parse_args()
@@ -124,6 +126,43 @@ def cpu_baseline(w, host, gpu_out, frac):
                        f"(measured {t_csr + t_fwd + t_bwd:.1f} s)"),
             "fwd_ms": round(1e3 * (t_csr + t_fwd * T / done_tiles), 1),
             "bwd_ms": round(1e3 * t_bwd * n / ng, 1)}
+
+
+def cosine_leg(_C, grid_feats, steps, warmup):
+    """The voxel-wise feature cosine loss (the consumer of grid_feats, reference
+    src/cuda_feats_loss.cu) on this config's grid: grid_feats of the G2V forward against a
+    synthetic target, 80 % of voxels visible, labels 0..2.  Forward and backward times are the
+    library calls' own HIP event spans (the forward includes its one host wait for the count)."""
+    import torch
+    dev = grid_feats.device
+    X, Y, Z, C = grid_feats.shape
+    gen = torch.Generator().manual_seed(11)
+    label = torch.randint(0, 3, (X, Y, Z), generator=gen).to(torch.float32).to(dev)
+    mask = (torch.rand((X, Y, Z), generator=gen) < 0.8).to(dev)
+    target = torch.randn((X, Y, Z, C), generator=gen).to(dev)
+    gout = torch.ones((), device=dev)
+    for _ in range(warmup):
+        _, cnt, _ = _C.CudaFeatsCosinelossForward(label, mask, grid_feats, target)
+        _C.CudaFeatsCosinelossBackward(gout, label, mask, grid_feats, target, cnt)
+    fwd = bwd = 0.0
+    for _ in range(steps):
+        _, cnt, f_s = _C.CudaFeatsCosinelossForward(label, mask, grid_feats, target)
+        grad, b_s = _C.CudaFeatsCosinelossBackward(gout, label, mask, grid_feats, target, cnt)
+        fwd += f_s
+        bwd += b_s
+        del grad
+    V = X * Y * Z
+    fwd_ms, bwd_ms = fwd * 1e3 / steps, bwd * 1e3 / steps
+    # compulsory bytes: label + mask of every voxel, both rows of each valid voxel, and the
+    # gradient of every voxel (written)
+    fwd_b = 5 * V + 8 * cnt * C
+    bwd_b = 5 * V + 8 * cnt * C + 4 * V * C
+    gf, gb = fwd_b / (fwd_ms * 1e-3) / 1e9, bwd_b / (bwd_ms * 1e-3) / 1e9
+    return {"grid": [X, Y, Z], "feat_dim": C, "valid_voxels": cnt, "fwd_ms": round(fwd_ms, 4),
+            "bwd_ms": round(bwd_ms, 4), "fwd_bytes": fwd_b, "bwd_bytes": bwd_b,
+            "fwd_gbps": round(gf, 1), "bwd_gbps": round(gb, 1),
+            "fwd_frac": round(gf / HBM_PEAK_GBPS, 4), "bwd_frac": round(gb / HBM_PEAK_GBPS, 4),
+            "data": "grid_feats of the G2V forward vs randn target (seed 11), synthetic labels and mask"}
 
 
 def main():
@@ -233,6 +272,10 @@ def main():
                         "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4), "traffic": traffic,
                         "algorithmic_bytes": bytes_k, "avg_ms": round(avg_s * 1e3, 4)}
 
+    cosine = None
+    if C > 0 and not args.no_cosine:
+        cosine = cosine_leg(_C, out[5].detach(), args.steps, args.warmup)
+
     cpu = None
     if not args.no_cpu and args.gpus == 1:
         import numpy as np
@@ -260,6 +303,7 @@ def main():
         "kernels_note": ("per-kernel HIP event pairs over K further steps run right after the timed "
                          "region (instrumented_ms_per_step is their wall time per step)"),
         "cpu_baseline": cpu,
+        "feats_cosine_loss": cosine,
     }
     print(json.dumps(res), flush=True)
 

@@ -18,6 +18,9 @@ relative to the reference repository root):
                         test/test_reference.py:57-79
 * ``backward_f64``   -- closed-form gradients, float64
                         src/cuda_gaussian_voxelizer.cu:1226-1297, :1304-1362, :1376-1482, :1995-1996
+* ``cosine_loss_f64`` / ``cosine_loss_grad_f64`` -- the voxel-wise feature cosine loss (mean over
+                        valid voxels) and its gradient with respect to grid_feats, float64
+                        src/cuda_feats_loss.cu:45-231 (forward), :233-366 (backward)
 
 The box and CSR functions are exact float32/int32 restatements: the HIP kernels
 must match them bit for bit.  The splat and gradient functions are float64
@@ -321,6 +324,53 @@ def backward_f64(grad_density, grad_feats, means, opacity, cov, features, lb, ub
         g_cov[g] = 0.5 * np.einsum("k,ki,kj->ij", gwd, q, q)
         g_o[g] = gw @ e
     return (g_mu, g_cov.reshape(n, 9), g_o, g_f if has_f else None)
+
+
+def cosine_valid(voxel_label, occ_mask):
+    """Voxels that count: visible and labelled (src/cuda_feats_loss.cu:67-68, :255)."""
+    return np.asarray(occ_mask, dtype=bool) & (np.asarray(voxel_label, dtype=np.float32) > 0)
+
+
+def _cosine_terms(p, g):
+    p = np.asarray(p, dtype=np.float64)
+    g = np.asarray(g, dtype=np.float64)
+    return p, g, (p * g).sum(-1), (p * p).sum(-1), (g * g).sum(-1)
+
+
+def cosine_loss_f64(voxel_label, occ_mask, grid_feats, pseudo_gt):
+    """(mean loss, valid count) of src/cuda_feats_loss.cu:45-231.
+
+    Per valid voxel 1 - p.g / (sqrt(max(|p|^2, eps)) sqrt(max(|g|^2, eps)) + eps) (:94-99); the
+    loss is the sum over valid voxels divided by their number, 0 when there is none (:205-212).
+    """
+    valid = cosine_valid(voxel_label, occ_mask)
+    _, _, dot, pp, gg = _cosine_terms(grid_feats, pseudo_gt)
+    eps = float(EPS)
+    lv = 1.0 - dot / (np.sqrt(np.maximum(pp, eps)) * np.sqrt(np.maximum(gg, eps)) + eps)
+    cnt = int(valid.sum())
+    return (float(lv[valid].sum()) / cnt if cnt > 0 else 0.0), cnt
+
+
+def cosine_loss_grad_f64(grad_out, voxel_label, occ_mask, grid_feats, pseudo_gt, num_valid_voxel):
+    """d loss / d grid_feats of src/cuda_feats_loss.cu:233-366, float64.
+
+    grad_out / count * (c1 g + c2 p) with c1 = -1/D, D = a b + eps, c2 = p.g b / (a D^2) when
+    |p|^2 > eps (else 0), a, b the clamped norms (:278-291); zero on invalid voxels (:255-261);
+    1/count is 0 when count is 0 (:319).
+    """
+    valid = cosine_valid(voxel_label, occ_mask)
+    p, g, dot, pp, gg = _cosine_terms(grid_feats, pseudo_gt)
+    eps = float(EPS)
+    a = np.sqrt(np.maximum(pp, eps))
+    b = np.sqrt(np.maximum(gg, eps))
+    D = a * b + eps
+    c1 = -1.0 / D
+    c2 = np.where(pp > eps, dot * b / (a * D * D), 0.0)
+    inv = 1.0 / num_valid_voxel if num_valid_voxel > 0 else 0.0
+    scale = float(grad_out) * inv
+    grad = scale * (c1[..., None] * g + c2[..., None] * p)
+    grad[~valid] = 0.0
+    return grad
 
 
 def rel_err(a, b):

@@ -333,12 +333,85 @@ def build_t2g(voxel_size, voxel_range, valid_voxel_lb, valid_voxel_ub, g2t_offse
     return out
 
 
+def _cosine_inputs(voxel_label, occ_gt_mask_camera, grid_feats, pseudo_dino_gt):
+    """The reference's input checks (src/cuda_feats_loss.cu:158-161: dtype, contiguity, device; a
+    failure is a RuntimeError) plus the shape agreement its 3-D / 4-D accessors assume."""
+    for t, name, dt in ((voxel_label, "voxel_label", torch.float32),
+                        (occ_gt_mask_camera, "occ_gt_mask_camera", torch.bool),
+                        (grid_feats, "grid_feats", torch.float32),
+                        (pseudo_dino_gt, "pseudo_dino_gt", torch.float32)):
+        if not isinstance(t, torch.Tensor) or t.dtype != dt or not t.is_contiguous() or t.device.type != "cuda":
+            raise RuntimeError(f"{name} must be a contiguous {dt} GPU tensor")
+    if voxel_label.dim() != 3 or grid_feats.dim() != 4:
+        raise RuntimeError("voxel_label must be (X, Y, Z) and grid_feats (X, Y, Z, C)")
+    dims = tuple(voxel_label.shape)
+    if (tuple(occ_gt_mask_camera.shape) != dims or tuple(grid_feats.shape[:3]) != dims
+            or tuple(pseudo_dino_gt.shape) != tuple(grid_feats.shape)):
+        raise RuntimeError(f"shape mismatch: voxel_label {dims}, occ_gt_mask_camera "
+                           f"{tuple(occ_gt_mask_camera.shape)}, grid_feats {tuple(grid_feats.shape)}, "
+                           f"pseudo_dino_gt {tuple(pseudo_dino_gt.shape)}")
+    dev = grid_feats.device
+    for t, name in ((voxel_label, "voxel_label"), (occ_gt_mask_camera, "occ_gt_mask_camera"),
+                    (pseudo_dino_gt, "pseudo_dino_gt")):
+        if t.device != dev:
+            raise RuntimeError(f"{name} is on {t.device}, grid_feats on {dev}")
+    return voxel_label.numel(), grid_feats.shape[3], dev
+
+
 def CudaFeatsCosinelossForward(voxel_label, occ_gt_mask_camera, grid_feats, pseudo_dino_gt):
-    """Not part of the G2V splatting path (reference src/cuda_feats_loss.cu); not provided."""
-    raise NotImplementedError("CudaFeatsCosinelossForward is outside the G2V splatting path of this build")
+    """Voxel-wise cosine loss (reference src/cuda_feats_loss.cu:154-231, bound at src/bindings.cpp:67-83).
+
+    Args: voxel_label (X,Y,Z) float32, occ_gt_mask_camera (X,Y,Z) bool, grid_feats and
+    pseudo_dino_gt (X,Y,Z,C) float32, all contiguous on the GPU.
+    Returns the reference's 3-tuple: the mean over valid voxels (mask and label > 0) of
+    1 - cos(grid_feats, pseudo_dino_gt) as a 0-dim GPU tensor (0 without valid voxels), the number
+    of valid voxels (int) and the forward time in seconds.
+    """
+    lib = _lib.load()
+    V, C, dev = _cosine_inputs(voxel_label, occ_gt_mask_camera, grid_feats, pseudo_dino_gt)
+    with _OnDevice(dev):
+        cur = torch.cuda.current_stream(dev)
+        loss = torch.empty((), dtype=torch.float32, device=dev)
+        cnt_dev = torch.empty((), dtype=torch.int32, device=dev)
+        ws = torch.empty(lib.g2v_cosine_loss_workspace(V, C), dtype=torch.uint8, device=dev)
+        cnt = ctypes.c_int(0)
+        start, stop = _timing_events(dev)
+        start.record(cur)
+        _lib.check(lib.g2v_cosine_loss_forward(V, C, _ptr(voxel_label), _ptr(occ_gt_mask_camera),
+                                               _ptr(grid_feats), _ptr(pseudo_dino_gt), _ptr(loss),
+                                               _ptr(cnt_dev), ctypes.byref(cnt), _ptr(ws), ws.numel(),
+                                               ctypes.c_void_p(cur.cuda_stream)),
+                   "CudaFeatsCosinelossForward")
+        stop.record(cur)
+        stop.synchronize()
+        fwd_sec = start.elapsed_time(stop) / 1000.0
+    return loss, int(cnt.value), fwd_sec
 
 
 def CudaFeatsCosinelossBackward(grad_output, voxel_label, occ_gt_mask_camera, grid_feats, pseudo_dino_gt,
                                 num_valid_voxel):
-    """Not part of the G2V splatting path (reference src/cuda_feats_loss.cu); not provided."""
-    raise NotImplementedError("CudaFeatsCosinelossBackward is outside the G2V splatting path of this build")
+    """Gradient of the cosine loss with respect to grid_feats (reference src/cuda_feats_loss.cu:311-366,
+    bound at src/bindings.cpp:85-104).
+
+    grad_output is the upstream gradient of the scalar loss (one element); it is read on the GPU,
+    without the reference's host round trip.  Returns (grad_grid_feats (X,Y,Z,C), backward time in
+    seconds); the gradient is zero on invalid voxels.
+    """
+    lib = _lib.load()
+    V, C, dev = _cosine_inputs(voxel_label, occ_gt_mask_camera, grid_feats, pseudo_dino_gt)
+    if not isinstance(grad_output, torch.Tensor) or grad_output.numel() != 1:
+        raise RuntimeError("grad_output must be a one-element tensor")
+    with _OnDevice(dev):
+        cur = torch.cuda.current_stream(dev)
+        gout = grad_output.detach().to(device=dev, dtype=torch.float32).reshape(1).contiguous()
+        grad_p = torch.empty_like(grid_feats)
+        start, stop = _timing_events(dev)
+        start.record(cur)
+        _lib.check(lib.g2v_cosine_loss_backward(V, C, _ptr(gout), _ptr(voxel_label), _ptr(occ_gt_mask_camera),
+                                                _ptr(grid_feats), _ptr(pseudo_dino_gt), int(num_valid_voxel),
+                                                _ptr(grad_p), ctypes.c_void_p(cur.cuda_stream)),
+                   "CudaFeatsCosinelossBackward")
+        stop.record(cur)
+        stop.synchronize()
+        bwd_sec = start.elapsed_time(stop) / 1000.0
+    return grad_p, bwd_sec

@@ -14,7 +14,8 @@ from ._C import gaussian_voxelizer_forward, gaussian_voxelizer_backward
 from ._C import CudaFeatsCosinelossForward, CudaFeatsCosinelossBackward
 
 __all__ = ["PyCudaGaussianVoxelizer", "PyCudaFeatsCosineLoss", "_C",
-           "gaussian_voxelizer_forward", "gaussian_voxelizer_backward"]
+           "gaussian_voxelizer_forward", "gaussian_voxelizer_backward",
+           "CudaFeatsCosinelossForward", "CudaFeatsCosinelossBackward"]
 
 
 class _CudaGaussianVoxelizeFunction(torch.autograd.Function):
@@ -61,6 +62,30 @@ class _CudaGaussianVoxelizeFunction(torch.autograd.Function):
                 grad_feats if features is not None else None)
 
 
+class _CudaFeatsCosinelossFunction(torch.autograd.Function):
+    """Autograd wrapper of the cosine loss (reference CudaGaussianVoxelizer/__init__.py:49-67):
+    the gradient flows to d_grid_feats only."""
+
+    @staticmethod
+    def forward(ctx, voxel_label, occ_gt_mask_camera, d_grid_feats, pseudo_dino_gt):
+        loss, num_valid_voxel, fwd_sec = CudaFeatsCosinelossForward(voxel_label, occ_gt_mask_camera,
+                                                                    d_grid_feats, pseudo_dino_gt)
+        stats = torch.zeros(2, dtype=torch.float32, device="cpu")
+        stats[0] = fwd_sec
+        ctx.save_for_backward(voxel_label, occ_gt_mask_camera, d_grid_feats, pseudo_dino_gt, stats)
+        ctx.num_valid_voxel = num_valid_voxel
+        return loss, stats
+
+    @staticmethod
+    def backward(ctx, grad_output, grad_stats):
+        voxel_label, occ_gt_mask_camera, d_grid_feats, pseudo_dino_gt, stats = ctx.saved_tensors
+        gout32 = grad_output.to(torch.float32).contiguous()
+        grad_predict, bwd_sec = CudaFeatsCosinelossBackward(gout32, voxel_label, occ_gt_mask_camera,
+                                                            d_grid_feats, pseudo_dino_gt, ctx.num_valid_voxel)
+        stats[1] = bwd_sec
+        return None, None, grad_predict, None
+
+
 class PyCudaGaussianVoxelizer(nn.Module):
     """Splats Gaussians (and their features) into a dense voxel grid of 4x4x4 tiles.
 
@@ -81,8 +106,13 @@ class PyCudaGaussianVoxelizer(nn.Module):
 
 
 class PyCudaFeatsCosineLoss(nn.Module):
-    """Present for API compatibility only: the cosine loss (reference src/cuda_feats_loss.cu) is
-    outside the G2V splatting path of this build and raises ``NotImplementedError``."""
+    """Mean voxel-wise cosine loss between grid features and pseudo ground-truth features over the
+    voxels that are visible (occ_gt_mask_camera) and labelled (voxel_label > 0).
+
+    Reference CudaGaussianVoxelizer/__init__.py:84-96; returns ``(loss, stats)`` with ``stats`` the
+    CPU float32 tensor ``[fwd_sec, bwd_sec]``.  voxel_size and voxel_range are kept as the
+    reference keeps them (unused by the loss).
+    """
 
     def __init__(self, voxel_size=[0.4, 0.4, 0.4], voxel_range=[-40, -40, -1, 40, 40, 5.4]):
         super().__init__()
@@ -90,4 +120,4 @@ class PyCudaFeatsCosineLoss(nn.Module):
         self.voxel_range = torch.tensor(voxel_range, dtype=torch.float32, device="cuda")
 
     def forward(self, voxel_label, occ_gt_mask_camera, d_grid_feats, pseudo_dino_gt):
-        return CudaFeatsCosinelossForward(voxel_label, occ_gt_mask_camera, d_grid_feats, pseudo_dino_gt)
+        return _CudaFeatsCosinelossFunction.apply(voxel_label, occ_gt_mask_camera, d_grid_feats, pseudo_dino_gt)

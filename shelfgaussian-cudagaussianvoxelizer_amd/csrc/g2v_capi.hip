@@ -105,7 +105,7 @@ extern "C" {
 
 const char* g2v_last_error(void) { return g_err; }
 
-int g2v_abi_version(void) { return 2; }
+int g2v_abi_version(void) { return 3; }
 
 int g2v_grid_dims(const float voxel_size[3], const float voxel_range[6], int dims[3], int tiles[3]) {
     Grid G;
@@ -370,6 +370,53 @@ int g2v_build_t2g(int n, const float voxel_size[3], const float voxel_range[6],
     G2V_HIP(hipMemcpyAsync(tile_offsets, b.tile_offsets, (T + 1) * sizeof(int),
                            hipMemcpyDeviceToDevice, s));
     G2V_HIP(launch_rle(b.tile_offsets, T, unique_tiles, counts, runs_offsets, num_runs, rle_ws, s));
+    return G2V_OK;
+}
+
+size_t g2v_cosine_loss_workspace(long long num_voxels, int feat_dim) {
+    (void)feat_dim;
+    return cosine_workspace(num_voxels > 0 ? num_voxels : 0);
+}
+
+int g2v_cosine_loss_forward(long long num_voxels, int feat_dim, const float* voxel_label,
+                            const unsigned char* occ_mask, const float* grid_feats, const float* pseudo_gt,
+                            float* loss, int* num_valid, int* num_valid_host, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+    g_err[0] = 0;
+    if (num_voxels < 0 || feat_dim < 0)
+        return fail(G2V_ERR_INVALID, "num_voxels = %lld, feat_dim = %d", num_voxels, feat_dim);
+    if (num_voxels > 2147483647ll)
+        return fail(G2V_ERR_LIMIT, "num_voxels = %lld exceeds the int32 valid-voxel count", num_voxels);
+    if (!loss || !num_valid) return fail(G2V_ERR_INVALID, "loss / num_valid is null");
+    if (num_voxels > 0 && (!voxel_label || !occ_mask || (feat_dim > 0 && (!grid_feats || !pseudo_gt))))
+        return fail(G2V_ERR_INVALID, "null input pointer");
+    int rc = check_ws(workspace, workspace_bytes, g2v_cosine_loss_workspace(num_voxels, feat_dim), "cosine loss");
+    if (rc != G2V_OK) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    G2V_HIP(launch_cosine_forward(num_voxels, feat_dim, voxel_label, occ_mask, grid_feats, pseudo_gt, loss,
+                                  num_valid, workspace, s));
+    if (num_valid_host) {
+        int h = 0;
+        G2V_HIP(hipMemcpyAsync(&h, num_valid, sizeof(int), hipMemcpyDeviceToHost, s));
+        G2V_HIP(hipStreamSynchronize(s));
+        *num_valid_host = h;
+    }
+    return G2V_OK;
+}
+
+int g2v_cosine_loss_backward(long long num_voxels, int feat_dim, const float* grad_output,
+                             const float* voxel_label, const unsigned char* occ_mask, const float* grid_feats,
+                             const float* pseudo_gt, int num_valid_voxel, float* grad_grid_feats, void* stream) {
+    g_err[0] = 0;
+    if (num_voxels < 0 || feat_dim < 0)
+        return fail(G2V_ERR_INVALID, "num_voxels = %lld, feat_dim = %d", num_voxels, feat_dim);
+    if (num_voxels == 0 || feat_dim == 0) return G2V_OK;
+    if (!grad_output || !voxel_label || !occ_mask || !grid_feats || !pseudo_gt || !grad_grid_feats)
+        return fail(G2V_ERR_INVALID, "null input/output pointer");
+    // the reference's host-side scale (src/cuda_feats_loss.cu:319)
+    const float inv_count = num_valid_voxel > 0 ? 1.0f / (float)num_valid_voxel : 0.0f;
+    G2V_HIP(launch_cosine_backward(num_voxels, feat_dim, voxel_label, occ_mask, grid_feats, pseudo_gt,
+                                   grad_output, inv_count, grad_grid_feats, static_cast<hipStream_t>(stream)));
     return G2V_OK;
 }
 

@@ -108,6 +108,18 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
                                  const void* plan_ws, int64_t MR, float* grad_means, float* grad_cov,
                                  float* grad_opacity, float* grad_features, void* ws, hipStream_t s);
 
+// ---- feature cosine loss (g2v_cosine.hip) --------------------------------------------------
+size_t cosine_workspace(int64_t V);
+// 16-byte vector rows: C % 4 == 0 and every non-null pointer 16-byte aligned.
+bool cosine_vec_ok(int C, const void* a, const void* b, const void* c);
+// Mean loss over the valid voxels into *loss and their number into *count (device pointers).
+hipError_t launch_cosine_forward(int64_t V, int C, const float* label, const uint8_t* mask, const float* p,
+                                 const float* g, float* loss, int* count, void* ws, hipStream_t s);
+// dloss/dp into grad_p (V x C), grad_out a device scalar, inv_count = 1 / count (0 when count = 0).
+hipError_t launch_cosine_backward(int64_t V, int C, const float* label, const uint8_t* mask, const float* p,
+                                  const float* g, const float* grad_out, float inv_count, float* grad_p,
+                                  hipStream_t s);
+
 // Brackets one kernel launch with HIP events when profiling is enabled (g2v_profile.hip).
 class ProfMark {
   public:
