@@ -99,6 +99,8 @@ CSR_CASES = {
                                 var_range=(0.01, 0.3)),
     # more than 2^20 Gaussians: the offsets scan takes the multi-workgroup path
     "many_small_n1100000": W.Workload("many_small", 1_100_000, None, var_range=(0.01, 0.05)),
+    # the reference's recorded training batch (tests/golden/mmdet_debug_inputs.npz)
+    "recorded_batch": W.mmdet_workload(),
 }
 
 
@@ -163,6 +165,8 @@ FWD_CASES = {
     "density_only": W.Workload("dens", 5000, None, var_range=(0.1, 0.6)),
     "wide_long_lists": W.Workload("wide", 4000, 32, var_range=(2.0, 12.0), mean_pad=4.0),
     "wide_channels_300": W.Workload("c300", 1500, 300, voxel_range=W.RANGE_SMALL),
+    "recorded_batch_density": W.mmdet_workload(),
+    "recorded_batch_c64": W.mmdet_workload(64),
 }
 
 
@@ -214,6 +218,8 @@ BWD_CASES = {
     "wide_long_lists": W.Workload("wide", 3000, 32, var_range=(2.0, 12.0), mean_pad=4.0),
     "odd_channels_13": W.Workload("odd13", 800, 13, voxel_range=W.RANGE_SMALL),
     "channels_300": W.Workload("c300", 800, 300, voxel_range=W.RANGE_SMALL),
+    "recorded_batch_density": W.mmdet_workload(),
+    "recorded_batch_c64": W.mmdet_workload(64),
 }
 
 

@@ -5,12 +5,15 @@ Every oracle function is checked against something other than its own formula:
   gaussian_boxes  hand-computed boxes (inside, clipped, outside on every face, exact voxel
                   boundaries, zero and negative variance), invariants, the C restatement
   invert_3x3      numpy.linalg.inv and the determinant clamp
-  g2t_csr/t2g_csr the toy CSR of the reference README figure (img/g2v_method.png), brute-force
+  g2t_csr/t2g_csr the toy CSR of the reference README figure (img/g2v_method.png, transcribed in
+                  tests/golden/toy_csr_readme_figure.json), brute-force
                   enumeration of tile/box intersections, numpy.lexsort, the C restatement
   forward_f64     closed forms: single Gaussian, identical features, one-hot features, D < eps
   backward_f64    central finite differences of forward_f64 and torch autograd (float64);
                   a planted mistake shows the finite-difference check catches a wrong factor
 """
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -19,6 +22,7 @@ from oracle import g2v_oracle as O
 from oracle import g2v_oracle_c as OC
 from tests import workloads as W
 
+GOLDEN = W.GOLDEN
 VS = np.array([0.4, 0.4, 0.4], np.float32)
 VR_SMALL = np.array(W.RANGE_SMALL, np.float32)
 VR_PAPER = np.array(W.RANGE_PAPER, np.float32)
@@ -154,27 +158,63 @@ def test_boxes_numpy_equals_c_restatement():
 
 # ------------------------------------------------------------------------------ CSR
 def test_toy_csr_of_readme_figure():
-    """img/g2v_method.png: G1->{1,2,4}, G2->{2,5,6}, G3->{5,6,8,9} (0-based Gaussians 0..2)."""
-    rows = [[1, 2, 4], [2, 5, 6], [5, 6, 8, 9]]
+    """img/g2v_method.png: G1->{1,2,4}, G2->{2,5,6}, G3->{5,6,8,9} (0-based Gaussians 0..2);
+    the expected CSRs are the figure's, transcribed in tests/golden/toy_csr_readme_figure.json."""
+    import json
+    with open(os.path.join(GOLDEN, "toy_csr_readme_figure.json")) as fh:
+        kat = json.load(fh)
+    rows = kat["gaussian_tiles"]
+    T = kat["num_tiles"]
     tid = np.array(sum(rows, []), np.int32)
     gid = np.array(sum([[g] * len(r) for g, r in enumerate(rows)], []), np.int32)
     off = np.concatenate([[0], np.cumsum([len(r) for r in rows])])
-    assert off.tolist() == [0, 3, 6, 10]
-    t = O.t2g_csr(tid, gid, 10)
-    assert t["unique_tiles"].tolist() == [1, 2, 4, 5, 6, 8, 9]
-    assert t["runs_offsets"].tolist() == [0, 1, 3, 4, 6, 8, 9, 10]
+    assert off.tolist() == kat["g2t_offsets"]
+    t = O.t2g_csr(tid, gid, T)
+    assert t["unique_tiles"].tolist() == kat["unique_tiles"]
+    assert t["runs_offsets"].tolist() == kat["runs_offsets"]
     lists = [t["sorted_gauss"][a:b].tolist() for a, b in zip(t["runs_offsets"][:-1], t["runs_offsets"][1:])]
-    assert lists == [[0], [0, 1], [0], [1, 2], [1, 2], [2], [2]]
-    assert t["num_runs"] == 7
-    assert t["tile_offsets"].tolist() == [0, 0, 1, 3, 3, 4, 6, 8, 8, 9, 10]
+    assert lists == kat["tile_lists"]
+    assert t["num_runs"] == len(kat["unique_tiles"])
+    assert t["tile_offsets"].tolist() == kat["tile_offsets"]
     # the C restatement (counting sort) agrees
-    toff = np.zeros(11, np.int32)
-    sg = np.zeros(10, np.int32)
+    M = len(tid)
+    toff = np.zeros(T + 1, np.int32)
+    sg = np.zeros(M, np.int32)
     import ctypes
-    OC.lib().g2vo_t2g(ctypes.c_longlong(10), tid.ctypes.data_as(OC._ip), gid.ctypes.data_as(OC._ip), 10,
+    OC.lib().g2vo_t2g(ctypes.c_longlong(M), tid.ctypes.data_as(OC._ip), gid.ctypes.data_as(OC._ip), T,
                       toff.ctypes.data_as(OC._ip), sg.ctypes.data_as(OC._ip))
     np.testing.assert_array_equal(toff, t["tile_offsets"])
     np.testing.assert_array_equal(sg, t["sorted_gauss"])
+
+
+def test_recorded_batch_boxes_and_csr():
+    """The reference's recorded training batch (tests/golden/mmdet_debug_inputs.npz): box
+    invariants, boxes of the Gaussians centred outside the grid, numpy == C restatement."""
+    m, o, c, vs, vr = W.mmdet_fixture()
+    m, c = m.numpy(), c.numpy()
+    vs, vr = np.array(vs, np.float32), np.array(vr, np.float32)
+    b = O.gaussian_boxes(m, c, vs, vr)
+    dims = np.array(O.grid_dims(vs, vr)[0])
+    empty = b["nvox"] == 0
+    assert (b["lb"][empty] == 0).all() and (b["ub"][empty] == -1).all()
+    ne = ~empty
+    assert ne.sum() > 100 and empty.sum() > 0
+    assert ((b["lb"][ne] >= 0) & (b["lb"][ne] <= b["ub"][ne]) & (b["ub"][ne] < dims)).all()
+    np.testing.assert_array_equal(b["nvox"][ne], np.prod(b["ub"][ne] - b["lb"][ne] + 1, axis=1))
+    # centred outside the x/y range but reaching into it: clipped, not dropped
+    out = (np.abs(m[:, :2]) > 40).any(axis=1)
+    assert (out & ne).any()
+    bc = OC.boxes(m, c, vs, vr)
+    for k in ("lb", "ub", "nvox", "tile_lo", "tile_hi", "ntiles"):
+        np.testing.assert_array_equal(b[k], bc[k], err_msg=k)
+    np.testing.assert_array_equal(b["cov_inv"].view(np.int32), bc["cov_inv"].view(np.int32))
+    off, tid, gid = O.g2t_csr(b["tile_lo"], b["tile_hi"], b["tiles"])
+    coff, ctid, _, ctoff, csg = OC.csr(b["tile_lo"], b["tile_hi"], b["tiles"])
+    np.testing.assert_array_equal(coff, off)
+    np.testing.assert_array_equal(ctid, tid)
+    t = O.t2g_csr(tid, gid, int(np.prod(b["tiles"])))
+    np.testing.assert_array_equal(ctoff, t["tile_offsets"])
+    np.testing.assert_array_equal(csg, t["sorted_gauss"])
 
 
 def _brute_force_t2g(tile_lo, tile_hi, tiles):

@@ -6,6 +6,8 @@ to 9, features -- on the CPU generator, then moved to the device by the caller.
 """
 from __future__ import annotations
 
+import os
+
 from dataclasses import dataclass, field
 from typing import Optional, Tuple
 
@@ -44,6 +46,10 @@ CONFIGS = {
 def generate(w: Workload, seed: int = 0):
     """(means3D (N,3), opacity (N,), covariances (N,9), features (N,C) or None), float32 CPU."""
     g = torch.Generator().manual_seed(seed)
+    if w.extra.get("fixture") == "mmdet":   # the recorded batch, with seeded synthetic features
+        means, opacity, cov, _, _ = mmdet_fixture()
+        feats = None if w.feat_dim is None else torch.randn(means.shape[0], w.feat_dim, generator=g)
+        return means, opacity, cov, feats
     lo = torch.tensor(w.voxel_range[:3], dtype=torch.float32) - w.mean_pad
     hi = torch.tensor(w.voxel_range[3:], dtype=torch.float32) + w.mean_pad
     means = torch.rand(w.n, 3, generator=g) * (hi - lo) + lo
@@ -83,3 +89,26 @@ def upstream_grads(w: Workload, seed: int = 1):
         gD = torch.randn(X, Y, Z, generator=g)
         gF = None if C is None else torch.randn(X, Y, Z, C, generator=g)
     return gD, gF
+
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def mmdet_fixture():
+    """The reference's recorded ShelfGaussian batch (tests/golden/mmdet_debug_inputs.npz, written by
+    tests/golden/make_mmdet_fixture.py): 1,800 Gaussians, many centred far outside the grid, with
+    float16 covariances up to 31 m^2 on the diagonal.  Returns (means (N,3), opacity (N,),
+    covariances (N,9)) as float32 CPU tensors, the covariances widened from float16 as the
+    reference's test/test_data_from_mmdetection.py does, and the voxel size and range."""
+    import numpy as np
+    d = np.load(os.path.join(GOLDEN, "mmdet_debug_inputs.npz"))
+    m = torch.from_numpy(d["means3D"].astype(np.float32))
+    o = torch.from_numpy(d["opacity"].astype(np.float32))
+    c = torch.from_numpy(d["covariances_f16"].astype(np.float32))
+    return m, o, c, tuple(float(v) for v in d["voxel_size"]), tuple(float(v) for v in d["voxel_range"])
+
+
+def mmdet_workload(feat_dim=None, grads="randn"):
+    """Workload of the recorded batch (see mmdet_fixture) on its own grid."""
+    return Workload("mmdet_debug_batch" + ("" if feat_dim is None else f"_c{feat_dim}"), 1800, feat_dim,
+                    voxel_range=RANGE_PAPER, voxel_size=VOXEL, grads=grads, extra={"fixture": "mmdet"})
