@@ -106,6 +106,34 @@ int g2v_backward(int n, int feat_dim, const float* grad_density, const float* gr
                  const int* t2g_tiles, const int* t2g_gauss, const int* t2g_offsets,
                  const void* plan_workspace, void* workspace, size_t workspace_bytes, void* stream);
 
+/* g2v_backward_prepare: the part of g2v_backward that needs no upstream gradient, for the
+ * feature case (feat_dim > 0): the bf16 split of the features, the (region, Gaussian) CSR and the
+ * row table of the feature-gradient phase, written into workspace (g2v_backward_workspace bytes).
+ * It needs the forward's Tile->Gaussian CSR (t2g_tiles, t2g_gauss from g2v_forward_splat) and the
+ * backward plan.  No counterpart in the reference, whose backward starts with the upstream
+ * gradients: a caller that blocks between forward and backward (the reference's module waits for
+ * the forward to finish, to report its time) can queue this behind the forward so that it runs
+ * while the host hands over to the backward.  Asynchronous.
+ *
+ * g2v_backward_prepared: g2v_backward, for a workspace that g2v_backward_prepare has filled for the
+ * same Gaussians, features, CSR and plan (and that nothing has written since); it skips those
+ * kernels.  Requires the Tile->Gaussian CSR arguments. */
+int g2v_backward_prepare(int n, int feat_dim, const float voxel_size[3], const float voxel_range[6],
+                         const int* valid_voxel_lb, const int* valid_voxel_ub, const float* features,
+                         long long num_pairs, long long num_region_pairs, const int* t2g_tiles,
+                         const int* t2g_gauss, const void* plan_workspace, void* workspace,
+                         size_t workspace_bytes, void* stream);
+int g2v_backward_prepared(int n, int feat_dim, const float* grad_density, const float* grad_feats,
+                          const float* means3D, const float* opacity, const float* cov_inv,
+                          const float voxel_size[3], const float voxel_range[6],
+                          const int* valid_voxel_lb, const int* valid_voxel_ub,
+                          const int* num_voxels_per_gaussian, const int* g2t_offsets,
+                          const int* g2t_tile_ids, long long num_pairs, long long num_region_pairs,
+                          const float* density, const float* grid_feats, const float* features,
+                          float* grad_means, float* grad_cov, float* grad_opacity, float* grad_features,
+                          const int* t2g_tiles, const int* t2g_gauss, const int* t2g_offsets,
+                          const void* plan_workspace, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- Tile->Gaussian CSR (inspection) -------------------------------------------------------
  * The internal Tile->Gaussian CSR of the forward, for parity tests: the stable sort of the G->T
  * pairs by tile (sorted_tiles, sorted_gauss: M each; reference .cu:1673-1691), the list bounds of

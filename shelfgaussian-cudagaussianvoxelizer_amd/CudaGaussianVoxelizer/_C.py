@@ -192,6 +192,14 @@ def _forward(means3D, opacity, covariances, voxel_size, voxel_range, features, k
                             torch.empty(n, C, **f32))
             t2g["ws"] = torch.empty(max(1, lib.g2v_backward_workspace(n, C, M, t2g["num_region_pairs"], vs, vr)),
                                     dtype=torch.uint8, device=dev)
+            # the backward's gradient-independent kernels, queued behind the forward (after its
+            # stop event): they run while this thread waits and hands over to the backward
+            if C > 0:
+                _lib.check(lib.g2v_backward_prepare(n, C, vs, vr, _ptr(lb), _ptr(ub), _ptr(feats), M,
+                                                    t2g["num_region_pairs"], _ptr(csr[0]), _ptr(csr[1]),
+                                                    _ptr(bplan), _ptr(t2g["ws"]), t2g["ws"].numel(), stream),
+                           "gaussian_voxelizer_forward (backward preparation)")
+                t2g["prepared"] = True
         stop.synchronize()
         fwd_sec = start.elapsed_time(stop) / 1000.0
     return (density, cov_inv, lb, ub, nvox, grid_feats, g2t_offsets, g2t_tile_ids, fwd_sec), t2g
@@ -284,7 +292,9 @@ def _backward(grad_output, grad_feats_output, means3D, opacity, cov_inv, voxel_s
         else:
             ws = torch.empty(max(1, lib.g2v_backward_workspace(n, C, M, MR, vs, vr)), dtype=torch.uint8, device=dev)
         csr = t2g["csr"] if t2g else (None, None, None)
-        _lib.check(lib.g2v_backward(n, C, _ptr(grad_output), _ptr(gF), _ptr(means3D), _ptr(opacity),
+        # the forward queued the gradient-independent part into this workspace
+        entry = lib.g2v_backward_prepared if (trusted and C > 0 and t2g.get("prepared")) else lib.g2v_backward
+        _lib.check(entry(n, C, _ptr(grad_output), _ptr(gF), _ptr(means3D), _ptr(opacity),
                                     _ptr(cov_inv), vs, vr, _ptr(valid_voxel_lb), _ptr(valid_voxel_ub),
                                     _ptr(num_voxels_per_gaussian), _ptr(g2t_offsets), _ptr(g2t_tile_ids),
                                     M, MR, _ptr(density), _ptr(grid_feats), _ptr(feats),

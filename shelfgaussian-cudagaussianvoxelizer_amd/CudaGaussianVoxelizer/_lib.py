@@ -34,6 +34,9 @@ SIGNATURES = {
     "g2v_backward_workspace": (_sz, [_i, _i, _ll, _ll, _f3, _f3]),
     "g2v_backward": (_i, [_i, _i, _vp, _vp, _vp, _vp, _vp, _f3, _f3, _vp, _vp, _vp, _vp, _vp, _ll, _ll,
                           _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "g2v_backward_prepare": (_i, [_i, _i, _f3, _f3, _vp, _vp, _vp, _ll, _ll, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "g2v_backward_prepared": (_i, [_i, _i, _vp, _vp, _vp, _vp, _vp, _f3, _f3, _vp, _vp, _vp, _vp, _vp, _ll, _ll,
+                                   _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "g2v_t2g_workspace": (_sz, [_i, _ll, _f3, _f3]),
     "g2v_build_t2g": (_i, [_i, _f3, _f3, _vp, _vp, _vp, _vp, _ll, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                            _vp, _sz, _vp]),

@@ -1079,17 +1079,11 @@ size_t backward_feats_workspace(const Grid& G, int n, int C, int64_t M, int64_t 
     return carve_feats(nullptr, G, n, C, M, MR).bytes;
 }
 
-hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_density,
-                                 const float* grad_feats, const float* means, const float* opacity,
-                                 const float* cov_inv, const int* lb, const int* ub,
-                                 const int* g2t_offsets, int64_t M, const int* tile_offsets,
-                                 const int* sorted_tiles, const int* sorted_gauss, const float* density,
-                                 const float* grid_feats, const float* features,
-                                 const void* plan_ws, int64_t MR, float* grad_means, float* grad_cov,
-                                 float* grad_opacity, float* grad_features, void* ws, hipStream_t s) {
+hipError_t launch_backward_prepare(const Grid& G, int n, int C, const float* features, const int* lb,
+                                   const int* ub, int64_t M, const int* sorted_tiles, const int* sorted_gauss,
+                                   const void* plan_ws, int64_t MR, void* ws, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     const Regions RG = make_regions(G);
-    const int T = G.tiles[0] * G.tiles[1] * G.tiles[2];
     const int nchk = feature_chunks(C);
     if (!split_rows_fit(n, C)) return hipErrorInvalidValue;   // byte offsets of the split rows are 32-bit
     const FeatBufs b = carve_feats(ws, G, n, C, M, MR);
@@ -1100,18 +1094,8 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
     const int64_t fcount = (int64_t)(n + 1) * nchk * (kBtKc / 8);   // one thread per 8 channels
     G2V_LAUNCH(k_split_chunks, dim3((unsigned)ceil_div(fcount, 256)), dim3(256), 0, s, features, n, C, nchk,
                b.fsp);
-    if (M > 0 && T > 0) {
-        const int blocks = (int)ceil_div(T, 8) * 8;
-        if ((C & 3) == 0 && ((uintptr_t)grad_feats & 15) == 0)   // 16-byte G loads
-            G2V_LAUNCH(k_bwd_tile<true>, dim3(blocks), dim3(kBtThreads), 0, s, G, n, C, nchk, grad_density,
-                       grad_feats, means, opacity, cov_inv, lb, ub, g2t_offsets, tile_offsets, sorted_gauss,
-                       (int)M, density, grid_feats, (const __bf16*)b.fsp, b.partials, b.wt);
-        else
-            G2V_LAUNCH(k_bwd_tile<false>, dim3(blocks), dim3(kBtThreads), 0, s, G, n, C, nchk, grad_density,
-                       grad_feats, means, opacity, cov_inv, lb, ub, g2t_offsets, tile_offsets, sorted_gauss,
-                       (int)M, density, grid_feats, (const __bf16*)b.fsp, b.partials, b.wt);
-    }
-    // Region -> Gaussian CSR (pairs carry their G->R slot so partial rows land Gaussian-major)
+    // Region -> Gaussian CSR (pairs carry their G->R slot so partial rows land Gaussian-major) and
+    // the row table of phase B
     if (MR > 0) {
         e = launch_fill_cells(n, lb, ub, pb.g2r_offsets, RG.cell, RG.n, b.r_cells, b.r_pairs, b.r_gauss, s);
         if (e != hipSuccess) return e;
@@ -1129,6 +1113,43 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
                    reinterpret_cast<int*>(b.wt + M * kWtRow));
         G2V_LAUNCH(k_region_table, dim3((unsigned)ceil_div(M, 256)), dim3(256), 0, s, G, RG, (int)M, (int)MR,
                    sorted_tiles, sorted_gauss, (const int*)b.roff, (const int*)b.r_gids, b.table);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_density,
+                                 const float* grad_feats, const float* means, const float* opacity,
+                                 const float* cov_inv, const int* lb, const int* ub,
+                                 const int* g2t_offsets, int64_t M, const int* tile_offsets,
+                                 const int* sorted_tiles, const int* sorted_gauss, const float* density,
+                                 const float* grid_feats, const float* features,
+                                 const void* plan_ws, int64_t MR, float* grad_means, float* grad_cov,
+                                 float* grad_opacity, float* grad_features, void* ws, bool prepared,
+                                 hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    const Regions RG = make_regions(G);
+    const int T = G.tiles[0] * G.tiles[1] * G.tiles[2];
+    const int nchk = feature_chunks(C);
+    if (!split_rows_fit(n, C)) return hipErrorInvalidValue;   // byte offsets of the split rows are 32-bit
+    const FeatBufs b = carve_feats(ws, G, n, C, M, MR);
+    const PlanBufs pb = carve_plan(const_cast<void*>(plan_ws), n);
+    if (!prepared) {
+        const hipError_t e = launch_backward_prepare(G, n, C, features, lb, ub, M, sorted_tiles, sorted_gauss,
+                                                     plan_ws, MR, ws, s);
+        if (e != hipSuccess) return e;
+    }
+    if (M > 0 && T > 0) {
+        const int blocks = (int)ceil_div(T, 8) * 8;
+        if ((C & 3) == 0 && ((uintptr_t)grad_feats & 15) == 0)   // 16-byte G loads
+            G2V_LAUNCH(k_bwd_tile<true>, dim3(blocks), dim3(kBtThreads), 0, s, G, n, C, nchk, grad_density,
+                       grad_feats, means, opacity, cov_inv, lb, ub, g2t_offsets, tile_offsets, sorted_gauss,
+                       (int)M, density, grid_feats, (const __bf16*)b.fsp, b.partials, b.wt);
+        else
+            G2V_LAUNCH(k_bwd_tile<false>, dim3(blocks), dim3(kBtThreads), 0, s, G, n, C, nchk, grad_density,
+                       grad_feats, means, opacity, cov_inv, lb, ub, g2t_offsets, tile_offsets, sorted_gauss,
+                       (int)M, density, grid_feats, (const __bf16*)b.fsp, b.partials, b.wt);
+    }
+    if (MR > 0 && M > 0) {
         const int nchunk = (C + kBrCc - 1) / kBrCc;
         const int64_t items = (int64_t)RG.total * nchunk;
         const int blocks = (int)ceil_div(items, 8) * 8;

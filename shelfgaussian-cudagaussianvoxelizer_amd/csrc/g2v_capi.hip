@@ -105,7 +105,7 @@ extern "C" {
 
 const char* g2v_last_error(void) { return g_err; }
 
-int g2v_abi_version(void) { return 3; }
+int g2v_abi_version(void) { return 4; }
 
 int g2v_grid_dims(const float voxel_size[3], const float voxel_range[6], int dims[3], int tiles[3]) {
     Grid G;
@@ -260,16 +260,20 @@ size_t g2v_backward_workspace(int n, int feat_dim, long long num_pairs, long lon
     return c.off + 256;
 }
 
-int g2v_backward(int n, int feat_dim, const float* grad_density, const float* grad_feats,
-                 const float* means3D, const float* opacity, const float* cov_inv,
-                 const float voxel_size[3], const float voxel_range[6], const int* valid_voxel_lb,
-                 const int* valid_voxel_ub, const int* num_voxels_per_gaussian,
-                 const int* g2t_offsets, const int* g2t_tile_ids, long long num_pairs,
-                 long long num_region_pairs, const float* density, const float* grid_feats,
-                 const float* features, float* grad_means, float* grad_cov, float* grad_opacity,
-                 float* grad_features, const int* t2g_tiles, const int* t2g_gauss,
-                 const int* t2g_offsets, const void* plan_workspace, void* workspace,
-                 size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int backward_impl(int n, int feat_dim, const float* grad_density, const float* grad_feats,
+                  const float* means3D, const float* opacity, const float* cov_inv,
+                  const float voxel_size[3], const float voxel_range[6], const int* valid_voxel_lb,
+                  const int* valid_voxel_ub, const int* num_voxels_per_gaussian,
+                  const int* g2t_offsets, const int* g2t_tile_ids, long long num_pairs,
+                  long long num_region_pairs, const float* density, const float* grid_feats,
+                  const float* features, float* grad_means, float* grad_cov, float* grad_opacity,
+                  float* grad_features, const int* t2g_tiles, const int* t2g_gauss,
+                  const int* t2g_offsets, const void* plan_workspace, void* workspace,
+                  size_t workspace_bytes, bool prepared, void* stream) {
     g_err[0] = 0;
     (void)num_voxels_per_gaussian;
     if (n < 0 || feat_dim < 0 || num_pairs < 0 || num_region_pairs < 0)
@@ -319,8 +323,83 @@ int g2v_backward(int n, int feat_dim, const float* grad_density, const float* gr
                                   valid_voxel_lb, valid_voxel_ub, g2t_offsets, num_pairs,
                                   b.tile_offsets, b.sorted_tiles, b.sorted_gauss, density, grid_feats, features,
                                   plan_workspace, num_region_pairs, grad_means, grad_cov, grad_opacity,
-                                  grad_features, feats_ws, s));
+                                  grad_features, feats_ws, prepared, s));
     return G2V_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int g2v_backward(int n, int feat_dim, const float* grad_density, const float* grad_feats,
+                 const float* means3D, const float* opacity, const float* cov_inv,
+                 const float voxel_size[3], const float voxel_range[6], const int* valid_voxel_lb,
+                 const int* valid_voxel_ub, const int* num_voxels_per_gaussian,
+                 const int* g2t_offsets, const int* g2t_tile_ids, long long num_pairs,
+                 long long num_region_pairs, const float* density, const float* grid_feats,
+                 const float* features, float* grad_means, float* grad_cov, float* grad_opacity,
+                 float* grad_features, const int* t2g_tiles, const int* t2g_gauss,
+                 const int* t2g_offsets, const void* plan_workspace, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+    return backward_impl(n, feat_dim, grad_density, grad_feats, means3D, opacity, cov_inv, voxel_size,
+                         voxel_range, valid_voxel_lb, valid_voxel_ub, num_voxels_per_gaussian, g2t_offsets,
+                         g2t_tile_ids, num_pairs, num_region_pairs, density, grid_feats, features, grad_means,
+                         grad_cov, grad_opacity, grad_features, t2g_tiles, t2g_gauss, t2g_offsets,
+                         plan_workspace, workspace, workspace_bytes, false, stream);
+}
+
+int g2v_backward_prepare(int n, int feat_dim, const float voxel_size[3], const float voxel_range[6],
+                         const int* valid_voxel_lb, const int* valid_voxel_ub, const float* features,
+                         long long num_pairs, long long num_region_pairs, const int* t2g_tiles,
+                         const int* t2g_gauss, const void* plan_workspace, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+    g_err[0] = 0;
+    if (n < 0 || feat_dim < 0 || num_pairs < 0 || num_region_pairs < 0)
+        return fail(G2V_ERR_INVALID, "n = %d, feat_dim = %d, num_pairs = %lld, num_region_pairs = %lld", n,
+                    feat_dim, num_pairs, num_region_pairs);
+    if (num_pairs > 2147483647ll || num_region_pairs > 2147483647ll)
+        return fail(G2V_ERR_LIMIT, "pair counts exceed int32");
+    if (n == 0 || feat_dim == 0) return G2V_OK;
+    if (!valid_voxel_lb || !valid_voxel_ub || !features || !plan_workspace ||
+        (num_pairs > 0 && (!t2g_tiles || !t2g_gauss)))
+        return fail(G2V_ERR_INVALID, "null input pointer (the Tile->Gaussian CSR of the forward is required)");
+    if (!split_rows_fit(n, feat_dim))
+        return fail(G2V_ERR_LIMIT, "n = %d x feat_dim = %d exceeds the split feature rows (4 GiB)", n, feat_dim);
+    Grid G;
+    int rc = make_grid(voxel_size, voxel_range, G);
+    if (rc != G2V_OK) return rc;
+    rc = check_ws(workspace, workspace_bytes,
+                  g2v_backward_workspace(n, feat_dim, num_pairs, num_region_pairs, voxel_size, voxel_range),
+                  "backward");
+    if (rc != G2V_OK) return rc;
+    Carver c(workspace, workspace_bytes);
+    c.take<char>(carve_splat(nullptr, n, num_pairs, G).bytes);
+    void* feats_ws = c.take<char>(backward_feats_workspace(G, n, feat_dim, num_pairs, num_region_pairs));
+    G2V_HIP(launch_backward_prepare(G, n, feat_dim, features, valid_voxel_lb, valid_voxel_ub, num_pairs,
+                                    t2g_tiles, t2g_gauss, plan_workspace, num_region_pairs, feats_ws,
+                                    static_cast<hipStream_t>(stream)));
+    return G2V_OK;
+}
+
+int g2v_backward_prepared(int n, int feat_dim, const float* grad_density, const float* grad_feats,
+                          const float* means3D, const float* opacity, const float* cov_inv,
+                          const float voxel_size[3], const float voxel_range[6], const int* valid_voxel_lb,
+                          const int* valid_voxel_ub, const int* num_voxels_per_gaussian,
+                          const int* g2t_offsets, const int* g2t_tile_ids, long long num_pairs,
+                          long long num_region_pairs, const float* density, const float* grid_feats,
+                          const float* features, float* grad_means, float* grad_cov, float* grad_opacity,
+                          float* grad_features, const int* t2g_tiles, const int* t2g_gauss,
+                          const int* t2g_offsets, const void* plan_workspace, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+    if (feat_dim > 0 && n > 0 && num_pairs > 0 && !(t2g_tiles && t2g_gauss && t2g_offsets)) {
+        g_err[0] = 0;
+        return fail(G2V_ERR_INVALID, "g2v_backward_prepared needs the forward's Tile->Gaussian CSR");
+    }
+    return backward_impl(n, feat_dim, grad_density, grad_feats, means3D, opacity, cov_inv, voxel_size,
+                         voxel_range, valid_voxel_lb, valid_voxel_ub, num_voxels_per_gaussian, g2t_offsets,
+                         g2t_tile_ids, num_pairs, num_region_pairs, density, grid_feats, features, grad_means,
+                         grad_cov, grad_opacity, grad_features, t2g_tiles, t2g_gauss, t2g_offsets,
+                         plan_workspace, workspace, workspace_bytes, true, stream);
 }
 
 size_t g2v_t2g_workspace(int n, long long num_pairs, const float voxel_size[3],

@@ -126,12 +126,14 @@ __global__ void __launch_bounds__(kScanThreads) k_scan_reduce(const int* __restr
                                                               long long* __restrict__ partials) {
     __shared__ long long sh[4];
     const int64_t base = (int64_t)blockIdx.x * kScanTile;
+    // every load is issued (clamped into the array) before any is used: a load under its own
+    // bounds branch would be followed by a wait of its own
+    int v[kScanItems];
+#pragma unroll
+    for (int r = 0; r < kScanItems; ++r) v[r] = in[min(base + (int64_t)r * kScanThreads + threadIdx.x, n - 1)];
     long long sum = 0;
 #pragma unroll
-    for (int r = 0; r < kScanItems; ++r) {
-        const int64_t i = base + (int64_t)r * kScanThreads + threadIdx.x;
-        if (i < n) sum += in[i];
-    }
+    for (int r = 0; r < kScanItems; ++r) sum += (base + (int64_t)r * kScanThreads + threadIdx.x < n) ? v[r] : 0;
     long long total;
     block_incl_scan(sum, sh, total);
     if (threadIdx.x == 0) partials[blockIdx.x] = total;
@@ -162,9 +164,10 @@ __global__ void __launch_bounds__(kScanThreads) k_scan_apply(const int* in, int*
     int v[kScanItems];
     long long local = 0;
 #pragma unroll
+    for (int r = 0; r < kScanItems; ++r) v[r] = in[min(base + r, n - 1)];   // clamped: no per-load branch
+#pragma unroll
     for (int r = 0; r < kScanItems; ++r) {
-        const int64_t i = base + r;
-        v[r] = i < n ? in[i] : 0;
+        v[r] = base + r < n ? v[r] : 0;
         local += v[r];
     }
     long long total;
@@ -197,10 +200,15 @@ __global__ void __launch_bounds__(kScan1Threads) k_scan_single(const int* in, in
     long long carry = 0;
     for (int base = 0; base < n; base += kTile) {
         // coalesced load: value e of the tile -> row e / 32, column e % 32
+        // all loads issued first (indices clamped into the array), then the masked LDS stores:
+        // a load under its own bounds branch would be followed by a wait of its own
+        int ld[kScan1Items];
+#pragma unroll
+        for (int k = 0; k < kScan1Items; ++k) ld[k] = in[min(base + k * kScan1Threads + (int)threadIdx.x, n - 1)];
 #pragma unroll
         for (int k = 0; k < kScan1Items; ++k) {
             const int e = k * kScan1Threads + threadIdx.x;
-            buf[(e / kScan1Items) * kScan1Row + e % kScan1Items] = (base + e < n) ? in[base + e] : 0;
+            buf[(e / kScan1Items) * kScan1Row + e % kScan1Items] = (base + e < n) ? ld[k] : 0;
         }
         __syncthreads();
         int* row = &buf[threadIdx.x * kScan1Row];
@@ -369,11 +377,12 @@ __global__ void __launch_bounds__(kSortThreads) k_radix_hist(const int* __restri
     for (int d = threadIdx.x; d < radix; d += kSortThreads) h[d] = 0;
     __syncthreads();
     const int64_t base = (int64_t)blockIdx.x * kSortTile;
-#pragma unroll 4
-    for (int r = 0; r < kSortRounds; ++r) {
-        const int64_t i = base + (int64_t)r * kSortThreads + threadIdx.x;
-        if (i < M) atomicAdd(&h[(keys[i] >> shift) & (radix - 1)], 1);
-    }
+    int kv[kSortRounds];
+#pragma unroll
+    for (int r = 0; r < kSortRounds; ++r) kv[r] = keys[min(base + (int64_t)r * kSortThreads + threadIdx.x, M - 1)];
+#pragma unroll
+    for (int r = 0; r < kSortRounds; ++r)
+        if (base + (int64_t)r * kSortThreads + threadIdx.x < M) atomicAdd(&h[(kv[r] >> shift) & (radix - 1)], 1);
     __syncthreads();
     for (int d = threadIdx.x; d < radix; d += kSortThreads) ghist[(int64_t)d * nblk + blockIdx.x] = h[d];
 }

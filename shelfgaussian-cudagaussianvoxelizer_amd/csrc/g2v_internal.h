@@ -99,6 +99,12 @@ hipError_t backward_plan(const Grid& G, int n, const int* lb, const int* ub, voi
 hipError_t backward_plan_async(const Grid& G, int n, const int* lb, const int* ub, void* plan_ws,
                                long long* mr_host, hipStream_t s);
 size_t backward_feats_workspace(const Grid& G, int n, int C, int64_t M, int64_t MR);
+// The part of the feature backward that needs no upstream gradient: split features, the
+// Region -> Gaussian CSR and the row table of phase B (into ws).
+hipError_t launch_backward_prepare(const Grid& G, int n, int C, const float* features, const int* lb,
+                                   const int* ub, int64_t M, const int* sorted_tiles, const int* sorted_gauss,
+                                   const void* plan_ws, int64_t MR, void* ws, hipStream_t s);
+// prepared: launch_backward_prepare already ran on ws for the same Gaussians and CSR.
 hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_density,
                                  const float* grad_feats, const float* means, const float* opacity,
                                  const float* cov_inv, const int* lb, const int* ub,
@@ -106,7 +112,8 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
                                  const int* sorted_tiles, const int* sorted_gauss, const float* density,
                                  const float* grid_feats, const float* features,
                                  const void* plan_ws, int64_t MR, float* grad_means, float* grad_cov,
-                                 float* grad_opacity, float* grad_features, void* ws, hipStream_t s);
+                                 float* grad_opacity, float* grad_features, void* ws, bool prepared,
+                                 hipStream_t s);
 
 // ---- feature cosine loss (g2v_cosine.hip) --------------------------------------------------
 size_t cosine_workspace(int64_t V);

@@ -31,7 +31,7 @@ def test_header_symbols_exported():
 
 
 def test_abi_version():
-    assert _lib().load().g2v_abi_version() == 3
+    assert _lib().load().g2v_abi_version() == 4
 
 
 @pytest.mark.parametrize("vs,vr", [
@@ -78,6 +78,24 @@ def test_invalid_arguments_fail_before_any_launch():
                           None, None, 0, 0, None, None, None, ctypes.c_void_p(16), ctypes.c_void_p(16),
                           ctypes.c_void_p(16), None, None, None, None, None, None, 0, None)
     assert rc == 1 and b"feat_dim" in lib.g2v_last_error()
+
+
+def test_backward_prepare_arguments_fail_before_any_launch():
+    L = _lib()
+    lib = L.load()
+    vs, vr = L.floats([0.4] * 3), L.floats(W.RANGE_PAPER)
+    one = ctypes.c_void_p(16)
+    rc = lib.g2v_backward_prepare(-1, 8, vs, vr, one, one, one, 0, 0, one, one, one, one, 1 << 20, None)
+    assert rc == 1 and b"n = -1" in lib.g2v_last_error()
+    # the forward's Tile->Gaussian CSR is required
+    rc = lib.g2v_backward_prepare(10, 8, vs, vr, one, one, one, 100, 10, None, None, one, one, 1 << 30, None)
+    assert rc == 1 and b"Tile->Gaussian" in lib.g2v_last_error()
+    rc = lib.g2v_backward_prepare(10, 8, vs, vr, one, one, one, 100, 10, one, one, one, one, 16, None)
+    assert rc == 1 and b"workspace" in lib.g2v_last_error()
+    assert lib.g2v_backward_prepare(10, 0, vs, vr, None, None, None, 0, 0, None, None, None, None, 0, None) == 0
+    rc = lib.g2v_backward_prepared(4, 8, one, one, one, one, one, vs, vr, one, one, None, one, one, 10, 5,
+                                   one, one, one, one, one, one, one, None, None, None, one, one, 1 << 30, None)
+    assert rc == 1 and b"Tile->Gaussian" in lib.g2v_last_error()
 
 
 def test_cosine_invalid_arguments_fail_before_any_launch():

@@ -283,8 +283,10 @@ def test_autograd_module_end_to_end():
 
 
 def test_module_reuse_of_forward_csr_matches_rebuild():
-    """The module hands the forward's Tile->Gaussian CSR and backward plan to the backward; the
-    reference-signature backward rebuilds both.  Same kernels, same order: identical bits."""
+    """The module hands the forward's Tile->Gaussian CSR and backward plan to the backward and
+    queues the backward's gradient-independent kernels behind the forward (g2v_backward_prepare,
+    then g2v_backward_prepared); the reference-signature backward rebuilds and recomputes all of
+    it.  Same kernels on the same inputs: identical bits."""
     from CudaGaussianVoxelizer import PyCudaGaussianVoxelizer
     dev = torch.device("cuda")
     w = W.Workload("reuse", 2500, 40, voxel_range=W.RANGE_SMALL, num_outside=30)
