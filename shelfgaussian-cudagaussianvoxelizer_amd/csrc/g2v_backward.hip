@@ -1026,6 +1026,14 @@ hipError_t backward_plan_async(const Grid& G, int n, const int* lb, const int* u
     return hipMemcpyAsync(mr_host, b.total, sizeof(long long), hipMemcpyDeviceToHost, s);
 }
 
+int* backward_plan_cells(const Grid& G, void* plan_ws, int n, int cell[3], void** scan_ws) {
+    const Regions RG = make_regions(G);
+    const PlanBufs b = carve_plan(plan_ws, n);
+    for (int a = 0; a < 3; ++a) cell[a] = RG.cell[a];
+    *scan_ws = b.scan_ws;
+    return b.g2r_offsets;
+}
+
 hipError_t backward_plan(const Grid& G, int n, const int* lb, const int* ub, void* plan_ws,
                          long long* num_region_pairs, hipStream_t s) {
     long long MR = 0;

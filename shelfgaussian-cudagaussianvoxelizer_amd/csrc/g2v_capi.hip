@@ -93,6 +93,24 @@ int build_t2g(const Grid& G, int n, const int* lb, const int* ub, const int* g2t
     return G2V_OK;
 }
 
+// Two counts in pinned, device-mapped host memory, one buffer per host thread (allocated on first
+// use, kept until the process ends): the plan's kernels write its pair counts straight into it, so
+// that the host wait is followed by no copy.  Null when pinned memory cannot be had (the plan then
+// copies the counts from device memory).
+long long* pinned_counts() {
+    thread_local long long* p = nullptr;
+    thread_local bool tried = false;
+    if (!tried) {
+        tried = true;
+        void* q = nullptr;
+        if (hipHostMalloc(&q, 64, hipHostMallocPortable | hipHostMallocMapped | hipHostMallocCoherent) == hipSuccess)
+            p = static_cast<long long*>(q);
+        else
+            (void)hipGetLastError();
+    }
+    return p;
+}
+
 int check_ws(const void* ws, size_t have, size_t need, const char* what) {
     if (need > have) return fail(G2V_ERR_INVALID, "%s workspace too small: %zu < %zu bytes", what, have, need);
     if (!ws && need > 0) return fail(G2V_ERR_INVALID, "%s workspace is null", what);
@@ -120,7 +138,7 @@ int g2v_grid_dims(const float voxel_size[3], const float voxel_range[6], int dim
 
 size_t g2v_forward_plan_workspace(int n) {
     Carver c(nullptr, (size_t)-1);
-    c.take<long long>(1);
+    c.take<long long>(2);
     c.take<char>(scan_workspace(n > 0 ? n : 1));
     return c.off + 256;
 }
@@ -149,19 +167,36 @@ int g2v_forward_plan(int n, const float* means3D, const float* covariances,
     if (rc != G2V_OK) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
     Carver c(workspace, workspace_bytes);
-    long long* total = c.take<long long>(1);
+    long long* total = c.take<long long>(2);
     void* scan_ws = c.take<char>(scan_workspace(n > 0 ? n : 1));
+    // the backward's (region, Gaussian) pair count rides on the same launches and synchronisation:
+    // the box kernel also counts each box's region cells, and one launch scans both count arrays
+    int cell[3] = {1, 1, 1};
+    void* plan_scan_ws = nullptr;
+    int* cell_off = bwd_plan_workspace ? backward_plan_cells(G, bwd_plan_workspace, n, cell, &plan_scan_ws) : nullptr;
+    long long* hc = pinned_counts();
+    long long* dc = total;
+    if (hc) {
+        hc[0] = hc[1] = 0;
+        G2V_HIP(hipHostGetDevicePointer(reinterpret_cast<void**>(&dc), hc, 0));
+    }
 
     G2V_HIP(launch_boxes(G, n, means3D, covariances, cov_inv, valid_voxel_lb, valid_voxel_ub,
-                         num_voxels_per_gaussian, g2t_offsets, s));
+                         num_voxels_per_gaussian, g2t_offsets, cell_off ? cell : nullptr, cell_off, s));
     long long M = 0, MR = 0;
-    if (n > 0) G2V_HIP(scan_i32(g2t_offsets + 1, g2t_offsets + 1, n, true, total, scan_ws, s));
-    // the backward's (region, Gaussian) pair count rides on the same synchronisation; the copies
-    // to (pageable) host memory come after every launch, so the host waits only once
-    if (bwd_plan_workspace)
-        G2V_HIP(backward_plan_async(G, n, valid_voxel_lb, valid_voxel_ub, bwd_plan_workspace, &MR, s));
-    if (n > 0) G2V_HIP(hipMemcpyAsync(&M, total, sizeof(long long), hipMemcpyDeviceToHost, s));
+    if (n > 0) {
+        G2V_HIP(scan_i32_pair(g2t_offsets + 1, g2t_offsets + 1, n, dc, scan_ws, cell_off ? cell_off + 1 : nullptr,
+                              cell_off ? cell_off + 1 : nullptr, cell_off ? n : 0, dc + 1, plan_scan_ws, s));
+        if (!hc) {   // counts in device memory: copy them after every launch, one host wait
+            G2V_HIP(hipMemcpyAsync(&M, total, sizeof(long long), hipMemcpyDeviceToHost, s));
+            if (cell_off) G2V_HIP(hipMemcpyAsync(&MR, total + 1, sizeof(long long), hipMemcpyDeviceToHost, s));
+        }
+    }
     G2V_HIP(hipStreamSynchronize(s));
+    if (hc && n > 0) {
+        M = hc[0];
+        MR = cell_off ? hc[1] : 0;
+    }
     if (M > 2147483647ll)
         return fail(G2V_ERR_LIMIT, "%lld Gaussian-tile pairs exceed the int32 CSR (limit 2^31-1)", M);
     if (MR > 2147483647ll)

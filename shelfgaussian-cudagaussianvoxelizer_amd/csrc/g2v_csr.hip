@@ -26,14 +26,20 @@ __device__ __forceinline__ int cvt_sat(float f) {
     return (int)f;
 }
 
+// With cell_offsets, also the number of cells of cx x cy x cz voxels that the box meets, at
+// cell_offsets[g+1] (cell_offsets[0] = 0), as k_cell_count computes it from the box.
 __global__ void __launch_bounds__(256) k_boxes(Grid G, int n, const float* __restrict__ means,
                                                const float* __restrict__ cov,
                                                float* __restrict__ cov_inv, int* __restrict__ lb,
                                                int* __restrict__ ub, int* __restrict__ nvox,
-                                               int* __restrict__ g2t_offsets) {
+                                               int* __restrict__ g2t_offsets, int cx, int cy, int cz,
+                                               int* __restrict__ cell_offsets) {
 #pragma clang fp contract(off)
     const int g = blockIdx.x * 256 + threadIdx.x;
-    if (g == 0) g2t_offsets[0] = 0;
+    if (g == 0) {
+        g2t_offsets[0] = 0;
+        if (cell_offsets) cell_offsets[0] = 0;
+    }
     if (g >= n) return;
     int lo[3], hi[3];
     bool empty = false;
@@ -57,6 +63,7 @@ __global__ void __launch_bounds__(256) k_boxes(Grid G, int n, const float* __res
         for (int a = 0; a < 3; ++a) { lb[g * 3 + a] = 0; ub[g * 3 + a] = -1; }
         nvox[g] = 0;
         g2t_offsets[g + 1] = 0;
+        if (cell_offsets) cell_offsets[g + 1] = 0;
 #pragma unroll
         for (int k = 0; k < 9; ++k) cov_inv[g * 9 + k] = 0.0f;
         return;
@@ -73,6 +80,8 @@ __global__ void __launch_bounds__(256) k_boxes(Grid G, int n, const float* __res
     }
     nvox[g] = nv;
     g2t_offsets[g + 1] = nt;
+    if (cell_offsets)
+        cell_offsets[g + 1] = (hi[0] / cx - lo[0] / cx + 1) * (hi[1] / cy - lo[1] / cy + 1) * (hi[2] / cz - lo[2] / cz + 1);
 
     float A[9];
 #pragma unroll
@@ -94,10 +103,12 @@ __global__ void __launch_bounds__(256) k_boxes(Grid G, int n, const float* __res
 }
 
 hipError_t launch_boxes(const Grid& G, int n, const float* means, const float* cov, float* cov_inv,
-                        int* lb, int* ub, int* nvox, int* g2t_offsets, hipStream_t s) {
+                        int* lb, int* ub, int* nvox, int* g2t_offsets, const int* cell, int* cell_offsets,
+                        hipStream_t s) {
     const int blocks = (int)ceil_div(n > 0 ? n : 1, 256);
+    const int cx = cell ? cell[0] : 1, cy = cell ? cell[1] : 1, cz = cell ? cell[2] : 1;
     G2V_LAUNCH(k_boxes, dim3(blocks), dim3(256), 0, s, G, n, means, cov, cov_inv, lb, ub,
-                       nvox, g2t_offsets);
+                       nvox, g2t_offsets, cx, cy, cz, cell ? cell_offsets : nullptr);
     return hipGetLastError();
 }
 
@@ -191,8 +202,22 @@ constexpr int kScan1Items = 32;
 constexpr int kScan1Row = kScan1Items + 1;
 constexpr int64_t kScanSingleMax = int64_t(1) << 20;
 
-__global__ void __launch_bounds__(kScan1Threads) k_scan_single(const int* in, int* out, int n, int inclusive,
-                                                               long long* __restrict__ total_dev) {
+struct ScanJob {
+    const int* in;
+    int* out;
+    int n;
+    int inclusive;
+    long long* total;
+};
+
+// Workgroup j scans job j (one or two jobs per launch).
+__global__ void __launch_bounds__(kScan1Threads) k_scan_single(ScanJob j0, ScanJob j1) {
+    const ScanJob& job = blockIdx.x == 0 ? j0 : j1;
+    const int* in = job.in;
+    int* out = job.out;
+    const int n = job.n;
+    const int inclusive = job.inclusive;
+    long long* total_dev = job.total;
     __shared__ int buf[kScan1Threads * kScan1Row];
     __shared__ long long wsum[kScan1Threads / 64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -256,8 +281,8 @@ size_t scan_workspace(int64_t n) {
 hipError_t scan_i32(const int* in, int* out, int64_t n, bool inclusive, long long* total_dev,
                     void* ws, hipStream_t s) {
     if (n <= kScanSingleMax) {
-        G2V_LAUNCH(k_scan_single, dim3(1), dim3(kScan1Threads), 0, s, in, out, (int)n, inclusive ? 1 : 0,
-                   total_dev);
+        const ScanJob j{in, out, (int)n, inclusive ? 1 : 0, total_dev};
+        G2V_LAUNCH(k_scan_single, dim3(1), dim3(kScan1Threads), 0, s, j, j);
         return hipGetLastError();
     }
     const int64_t nb = ceil_div(n > 0 ? n : 1, kScanTile);
@@ -267,6 +292,22 @@ hipError_t scan_i32(const int* in, int* out, int64_t n, bool inclusive, long lon
     G2V_LAUNCH(k_scan_apply, dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, out, n,
                        (const long long*)partials, inclusive ? 1 : 0);
     return hipGetLastError();
+}
+
+hipError_t scan_i32_pair(const int* in_a, int* out_a, int64_t n_a, long long* total_a, void* ws_a,
+                         const int* in_b, int* out_b, int64_t n_b, long long* total_b, void* ws_b,
+                         hipStream_t s) {
+    if (n_a > 0 && n_b > 0 && n_a <= kScanSingleMax && n_b <= kScanSingleMax) {
+        const ScanJob a{in_a, out_a, (int)n_a, 1, total_a}, b{in_b, out_b, (int)n_b, 1, total_b};
+        G2V_LAUNCH(k_scan_single, dim3(2), dim3(kScan1Threads), 0, s, a, b);
+        return hipGetLastError();
+    }
+    if (n_a > 0) {
+        const hipError_t e = scan_i32(in_a, out_a, n_a, true, total_a, ws_a, s);
+        if (e != hipSuccess) return e;
+    }
+    if (n_b > 0) return scan_i32(in_b, out_b, n_b, true, total_b, ws_b, s);
+    return hipSuccess;
 }
 
 // ------------------------------------------------------------------------------------------

@@ -40,8 +40,17 @@ size_t scan_workspace(int64_t n);
 hipError_t scan_i32(const int* in, int* out, int64_t n, bool inclusive, long long* total_dev,
                     void* ws, hipStream_t s);
 
+// Inclusive scans of two arrays in one launch when both fit one workgroup (else one after the
+// other); the totals go to total_a / total_b (device-accessible pointers).
+hipError_t scan_i32_pair(const int* in_a, int* out_a, int64_t n_a, long long* total_a, void* ws_a,
+                         const int* in_b, int* out_b, int64_t n_b, long long* total_b, void* ws_b,
+                         hipStream_t s);
+
+// Boxes, inverse covariances and G->T row counts; with cell (non-null) also the cell counts of
+// the boxes into cell_offsets[1..n] (cell_offsets[0] = 0), as launch_cell_count writes them.
 hipError_t launch_boxes(const Grid& G, int n, const float* means, const float* cov, float* cov_inv,
-                        int* lb, int* ub, int* nvox, int* g2t_offsets, hipStream_t s);
+                        int* lb, int* ub, int* nvox, int* g2t_offsets, const int* cell, int* cell_offsets,
+                        hipStream_t s);
 hipError_t launch_fill_g2t(const Grid& G, int n, const int* lb, const int* ub,
                            const int* g2t_offsets, int* tile_ids, int* gauss_ids, hipStream_t s);
 
@@ -98,6 +107,9 @@ hipError_t backward_plan(const Grid& G, int n, const int* lb, const int* ub, voi
 // The same without the synchronisation: the count lands in *mr_host once the stream reaches it.
 hipError_t backward_plan_async(const Grid& G, int n, const int* lb, const int* ub, void* plan_ws,
                                long long* mr_host, hipStream_t s);
+// The plan's cell counts (n + 1 ints), its scan workspace and the region cell size, for a caller
+// that fills and scans them itself (the forward plan does, in its own launches).
+int* backward_plan_cells(const Grid& G, void* plan_ws, int n, int cell[3], void** scan_ws);
 size_t backward_feats_workspace(const Grid& G, int n, int C, int64_t M, int64_t MR);
 // The part of the feature backward that needs no upstream gradient: split features, the
 // Region -> Gaussian CSR and the row table of phase B (into ws).
