@@ -443,13 +443,23 @@ __global__ void __launch_bounds__(kSortThreads) k_radix_scatter(
     __syncthreads();
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     const int64_t base = (int64_t)blockIdx.x * kSortTile;
+    // the block's keys and values are all requested up front (indices clamped into the arrays):
+    // the rounds below then wait for their own load only the first time
+    int kr[kSortRounds], vr[kSortRounds];
+#pragma unroll
+    for (int r = 0; r < kSortRounds; ++r) {
+        const int64_t i = min(base + (int64_t)r * kSortThreads + threadIdx.x, M - 1);
+        kr[r] = keys_in[i];
+        vr[r] = vals_in[i];
+    }
+#pragma unroll
     for (int r = 0; r < kSortRounds; ++r) {
         const int64_t rbase = base + (int64_t)r * kSortThreads;
         if (rbase >= M) break;  // uniform across the block
         const int64_t i = rbase + threadIdx.x;
         const bool valid = i < M;
-        const int k = valid ? keys_in[i] : 0;
-        const int v = valid ? vals_in[i] : 0;
+        const int k = valid ? kr[r] : 0;
+        const int v = valid ? vr[r] : 0;
         const int d = (k >> shift) & (radix - 1);
         uint64_t peers = __ballot(valid);
         for (int b = 0; b < dbits; ++b) {
