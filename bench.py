@@ -165,6 +165,37 @@ def cosine_leg(_C, grid_feats, steps, warmup):
             "data": "grid_feats of the G2V forward vs randn target (seed 11), synthetic labels and mask"}
 
 
+def covariance_leg(_C, n, steps):
+    """Covariances from scales and rotations (reference test/gaussian_voxelizer.py:14-37) for the
+    config's Gaussian count, forward and backward: HIP event spans on the current stream, averaged
+    over `steps` calls (10 warm-up calls first)."""
+    import torch
+    dev = torch.device("cuda", 0)
+    g = torch.Generator().manual_seed(12)
+    s = (torch.rand(n, 3, generator=g) + 0.1).to(dev)
+    q = torch.randn(n, 4, generator=g).to(dev)
+    gc = torch.randn(n, 9, generator=g).to(dev)
+    for _ in range(10):
+        _C.covariance_from_scale_rotation(s, q)
+        _C.covariance_from_scale_rotation_backward(s, q, gc)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    cur = torch.cuda.current_stream(dev)
+    ev[0].record(cur)
+    for _ in range(steps):
+        _C.covariance_from_scale_rotation(s, q)
+    ev[1].record(cur)
+    for _ in range(steps):
+        _C.covariance_from_scale_rotation_backward(s, q, gc)
+    ev[2].record(cur)
+    ev[2].synchronize()
+    fwd_us = ev[0].elapsed_time(ev[1]) * 1e3 / steps
+    bwd_us = ev[1].elapsed_time(ev[2]) * 1e3 / steps
+    fwd_b, bwd_b = 64 * n, 92 * n   # scales + quaternion in, covariance out; plus grad_cov in, two grads out
+    return {"n_gaussians": n, "fwd_us": round(fwd_us, 2), "bwd_us": round(bwd_us, 2),
+            "fwd_bytes": fwd_b, "bwd_bytes": bwd_b,
+            "note": "back-to-back calls; at this size launch-latency bound, not HBM bound"}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -272,6 +303,7 @@ def main():
                         "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4), "traffic": traffic,
                         "algorithmic_bytes": bytes_k, "avg_ms": round(avg_s * 1e3, 4)}
 
+    covariance = covariance_leg(_C, N, max(args.steps, 10))
     cosine = None
     if C > 0 and not args.no_cosine:
         cosine = cosine_leg(_C, out[5].detach(), args.steps, args.warmup)
@@ -304,6 +336,7 @@ def main():
                          "region (instrumented_ms_per_step is their wall time per step)"),
         "cpu_baseline": cpu,
         "feats_cosine_loss": cosine,
+        "covariance_from_scale_rotation": covariance,
     }
     print(json.dumps(res), flush=True)
 

@@ -173,6 +173,19 @@ int g2v_cosine_loss_backward(long long num_voxels, int feat_dim, const float* gr
                              const float* voxel_label, const unsigned char* occ_mask, const float* grid_feats,
                              const float* pseudo_gt, int num_valid_voxel, float* grad_grid_feats, void* stream);
 
+/* ---- covariances from scales and rotations -------------------------------------------------
+ * The covariance construction that ShelfGaussian runs before the voxelizer (reference
+ * test/gaussian_voxelizer.py:14-37 quat_to_rotmat / get_covariance, called at :168-169), for
+ * callers that hold scales (N,3) and rotation quaternions (N,4, real part first, not necessarily
+ * normalised) instead of covariances: covariances (N,9) = R diag(s) (R diag(s))^T row-major, R the
+ * rotation of q/|q|.  The backward maps grad_covariances (N,9, e.g. g2v_backward's grad_cov) to
+ * grad_scales (N,3) and grad_rotations (N,4).  Asynchronous. */
+int g2v_covariance_from_scale_rotation(int n, const float* scales, const float* rotations, float* covariances,
+                                       void* stream);
+int g2v_covariance_from_scale_rotation_backward(int n, const float* scales, const float* rotations,
+                                                const float* grad_covariances, float* grad_scales,
+                                                float* grad_rotations, void* stream);
+
 /* ---- per-kernel timing (benchmarks) --------------------------------------------------------
  * No counterpart in the reference (which times the whole forward/backward with one CUDA event
  * pair, src/cuda_gaussian_voxelizer.cu:1549-1555, :1905-1913).  While enabled, every kernel launch

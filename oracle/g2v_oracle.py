@@ -18,6 +18,9 @@ relative to the reference repository root):
                         test/test_reference.py:57-79
 * ``backward_f64``   -- closed-form gradients, float64
                         src/cuda_gaussian_voxelizer.cu:1226-1297, :1304-1362, :1376-1482, :1995-1996
+* ``covariance_from_scale_rotation_f64`` / ``..._grad_f64`` -- covariances R diag(s) (R diag(s))^T
+                        from scales and rotation quaternions, and the chain rule back to them
+                        test/gaussian_voxelizer.py:14-37
 * ``cosine_loss_f64`` / ``cosine_loss_grad_f64`` -- the voxel-wise feature cosine loss (mean over
                         valid voxels) and its gradient with respect to grid_feats, float64
                         src/cuda_feats_loss.cu:45-231 (forward), :233-366 (backward)
@@ -324,6 +327,58 @@ def backward_f64(grad_density, grad_feats, means, opacity, cov, features, lb, ub
         g_cov[g] = 0.5 * np.einsum("k,ki,kj->ij", gwd, q, q)
         g_o[g] = gw @ e
     return (g_mu, g_cov.reshape(n, 9), g_o, g_f if has_f else None)
+
+
+def _rotmat_f64(q):
+    """Rotation matrices of the normalised quaternions q (N,4), real part first
+    (test/gaussian_voxelizer.py:14-28)."""
+    q = np.asarray(q, dtype=np.float64)
+    q = q / np.sqrt((q * q).sum(-1, keepdims=True))
+    r, x, y, z = q[:, 0], q[:, 1], q[:, 2], q[:, 3]
+    R = np.empty((q.shape[0], 3, 3))
+    R[:, 0, 0] = 1 - 2 * (y * y + z * z)
+    R[:, 0, 1] = 2 * (x * y - r * z)
+    R[:, 0, 2] = 2 * (x * z + r * y)
+    R[:, 1, 0] = 2 * (x * y + r * z)
+    R[:, 1, 1] = 1 - 2 * (x * x + z * z)
+    R[:, 1, 2] = 2 * (y * z - r * x)
+    R[:, 2, 0] = 2 * (x * z - r * y)
+    R[:, 2, 1] = 2 * (y * z + r * x)
+    R[:, 2, 2] = 1 - 2 * (x * x + y * y)
+    return R, q
+
+
+def covariance_from_scale_rotation_f64(scales, rotations):
+    """(N,9) covariances (R diag(s)) (R diag(s))^T, float64 (test/gaussian_voxelizer.py:30-37)."""
+    R, _ = _rotmat_f64(rotations)
+    M = R * np.asarray(scales, dtype=np.float64)[:, None, :]
+    return (M @ M.transpose(0, 2, 1)).reshape(-1, 9)
+
+
+def covariance_from_scale_rotation_grad_f64(scales, rotations, grad_cov):
+    """(grad_scales (N,3), grad_rotations (N,4)) for grad_cov (N,9) = dL/dSigma, float64: the
+    chain rule through Sigma = M M^T, M = R diag(s), R(q / |q|)."""
+    s = np.asarray(scales, dtype=np.float64)
+    q0 = np.asarray(rotations, dtype=np.float64)
+    R, q = _rotmat_f64(q0)
+    G = np.asarray(grad_cov, dtype=np.float64).reshape(-1, 3, 3)
+    M = R * s[:, None, :]
+    dM = (G + G.transpose(0, 2, 1)) @ M
+    ds = (dM * R).sum(1)
+    dR = dM * s[:, None, :]
+    r, x, y, z = q[:, 0], q[:, 1], q[:, 2], q[:, 3]
+    zero = np.zeros_like(r)
+    # dR/dq^ for each quaternion component, as (N,3,3) matrices
+    J = {
+        0: [[zero, -2 * z, 2 * y], [2 * z, zero, -2 * x], [-2 * y, 2 * x, zero]],
+        1: [[zero, 2 * y, 2 * z], [2 * y, -4 * x, -2 * r], [2 * z, 2 * r, -4 * x]],
+        2: [[-4 * y, 2 * x, 2 * r], [2 * x, zero, 2 * z], [-2 * r, 2 * z, -4 * y]],
+        3: [[-4 * z, -2 * r, 2 * x], [2 * r, -4 * z, 2 * y], [2 * x, 2 * y, zero]],
+    }
+    dqh = np.stack([(np.moveaxis(np.array(J[k]), 2, 0) * dR).sum((1, 2)) for k in range(4)], axis=1)
+    norm = np.sqrt((q0 * q0).sum(-1, keepdims=True))
+    dq = (dqh - q * (q * dqh).sum(-1, keepdims=True)) / norm
+    return ds, dq
 
 
 def cosine_valid(voxel_label, occ_mask):

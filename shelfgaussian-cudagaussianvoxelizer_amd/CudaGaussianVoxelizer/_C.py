@@ -13,7 +13,8 @@ import torch
 from . import _lib
 
 __all__ = ["gaussian_voxelizer_forward", "gaussian_voxelizer_backward",
-           "CudaFeatsCosinelossForward", "CudaFeatsCosinelossBackward", "build_t2g", "grid_dims"]
+           "CudaFeatsCosinelossForward", "CudaFeatsCosinelossBackward", "build_t2g", "grid_dims",
+           "covariance_from_scale_rotation", "covariance_from_scale_rotation_backward"]
 
 
 def _ptr(t):
@@ -425,3 +426,49 @@ def CudaFeatsCosinelossBackward(grad_output, voxel_label, occ_gt_mask_camera, gr
         stop.synchronize()
         bwd_sec = start.elapsed_time(stop) / 1000.0
     return grad_p, bwd_sec
+
+
+def _scale_rot_inputs(scales, rotations):
+    sc = _f32_input(scales, "scales")
+    if sc.dim() < 1 or sc.shape[-1] != 3:
+        raise RuntimeError(f"scales must be (N, 3), got {tuple(sc.shape)}")
+    n = sc.numel() // 3
+    rot = _f32_input(rotations, "rotations")
+    if tuple(rot.shape) != tuple(sc.shape[:-1]) + (4,):
+        raise RuntimeError(f"rotations must be (N, 4) matching scales {tuple(sc.shape)}, got {tuple(rot.shape)}")
+    if rot.device != sc.device:
+        raise RuntimeError(f"rotations are on {rot.device}, scales on {sc.device}")
+    return sc.reshape(-1, 3), rot.reshape(-1, 4), n
+
+
+def covariance_from_scale_rotation(scales, rotations):
+    """Covariances (N, 9) row-major from scales (N, 3) and rotation quaternions (N, 4, real part
+    first, normalised here): (R diag(s)) (R diag(s))^T, as ShelfGaussian builds them before the
+    voxelizer (reference test/gaussian_voxelizer.py:14-37)."""
+    lib = _lib.load()
+    sc, rot, n = _scale_rot_inputs(scales, rotations)
+    dev = sc.device
+    with _OnDevice(dev):
+        cov = torch.empty(n, 9, dtype=torch.float32, device=dev)
+        _lib.check(lib.g2v_covariance_from_scale_rotation(n, _ptr(sc), _ptr(rot), _ptr(cov), _stream(dev)),
+                   "covariance_from_scale_rotation")
+    return cov
+
+
+def covariance_from_scale_rotation_backward(scales, rotations, grad_cov):
+    """(grad_scales (N, 3), grad_rotations (N, 4)) for grad_cov (N, 9) = dL/dcovariances."""
+    lib = _lib.load()
+    sc, rot, n = _scale_rot_inputs(scales, rotations)
+    dev = sc.device
+    g = _f32_input(grad_cov, "grad_cov")
+    if g.numel() != 9 * n:
+        raise RuntimeError(f"grad_cov must have N x 9 = {9 * n} elements, got {g.numel()}")
+    if g.device != dev:
+        raise RuntimeError(f"grad_cov is on {g.device}, scales on {dev}")
+    with _OnDevice(dev):
+        gs = torch.empty(n, 3, dtype=torch.float32, device=dev)
+        gq = torch.empty(n, 4, dtype=torch.float32, device=dev)
+        _lib.check(lib.g2v_covariance_from_scale_rotation_backward(n, _ptr(sc), _ptr(rot), _ptr(g), _ptr(gs),
+                                                                   _ptr(gq), _stream(dev)),
+                   "covariance_from_scale_rotation_backward")
+    return gs, gq

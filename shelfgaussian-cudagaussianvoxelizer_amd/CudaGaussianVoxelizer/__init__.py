@@ -15,7 +15,7 @@ from ._C import CudaFeatsCosinelossForward, CudaFeatsCosinelossBackward
 
 __all__ = ["PyCudaGaussianVoxelizer", "PyCudaFeatsCosineLoss", "_C",
            "gaussian_voxelizer_forward", "gaussian_voxelizer_backward",
-           "CudaFeatsCosinelossForward", "CudaFeatsCosinelossBackward"]
+           "CudaFeatsCosinelossForward", "CudaFeatsCosinelossBackward", "covariance_from_scale_rotation"]
 
 
 class _CudaGaussianVoxelizeFunction(torch.autograd.Function):
@@ -86,6 +86,30 @@ class _CudaFeatsCosinelossFunction(torch.autograd.Function):
         return None, None, grad_predict, None
 
 
+class _CovarianceFromScaleRotation(torch.autograd.Function):
+    """Covariances from scales and rotations (reference test/gaussian_voxelizer.py:14-37), with
+    the chain rule back to both."""
+
+    @staticmethod
+    def forward(ctx, scales, rotations):
+        ctx.save_for_backward(scales, rotations)
+        ctx.shapes = (scales.shape, rotations.shape)
+        return _C.covariance_from_scale_rotation(scales, rotations)
+
+    @staticmethod
+    def backward(ctx, grad_cov):
+        scales, rotations = ctx.saved_tensors
+        gs, gq = _C.covariance_from_scale_rotation_backward(scales, rotations, grad_cov.to(torch.float32))
+        return gs.reshape(ctx.shapes[0]), gq.reshape(ctx.shapes[1])
+
+
+def covariance_from_scale_rotation(scales, rotations):
+    """(N, 9) covariances (R diag(s)) (R diag(s))^T of scales (N, 3) and quaternions (N, 4, real
+    part first; normalised here), differentiable in both (reference
+    test/gaussian_voxelizer.py:30-37 get_covariance of quat_to_rotmat)."""
+    return _CovarianceFromScaleRotation.apply(scales, rotations)
+
+
 class PyCudaGaussianVoxelizer(nn.Module):
     """Splats Gaussians (and their features) into a dense voxel grid of 4x4x4 tiles.
 
@@ -100,7 +124,14 @@ class PyCudaGaussianVoxelizer(nn.Module):
         _C._host_values(self.voxel_size, 3, "voxel_size")
         _C._host_values(self.voxel_range, 6, "voxel_range")
 
-    def forward(self, means3D, opacity, covariances, features=None):
+    def forward(self, means3D, opacity, covariances=None, features=None, *, scales=None, rotations=None):
+        """As the reference's forward; without covariances, they are built from ``scales`` (N, 3)
+        and ``rotations`` (N, 4) (as ShelfGaussian's voxelizer does, reference
+        test/gaussian_voxelizer.py:168-169) and the gradients flow to those two."""
+        if covariances is None:
+            if scales is None or rotations is None:
+                raise RuntimeError("give covariances, or scales and rotations")
+            covariances = covariance_from_scale_rotation(scales, rotations)
         return _CudaGaussianVoxelizeFunction.apply(means3D, opacity, covariances, self.voxel_size,
                                                    self.voxel_range, features)
 

@@ -15,7 +15,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "CudaGaussianVoxelizer", "libg2v_hip.so")
-SOURCES = ["g2v_csr.hip", "g2v_forward.hip", "g2v_backward.hip", "g2v_cosine.hip", "g2v_capi.hip", "g2v_profile.hip"]
+SOURCES = ["g2v_csr.hip", "g2v_forward.hip", "g2v_backward.hip", "g2v_cosine.hip", "g2v_covariance.hip", "g2v_capi.hip", "g2v_profile.hip"]
 ARCH = os.environ.get("G2V_OFFLOAD_ARCH", "gfx950")
 
 

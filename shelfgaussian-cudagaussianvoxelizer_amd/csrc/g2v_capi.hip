@@ -123,7 +123,7 @@ extern "C" {
 
 const char* g2v_last_error(void) { return g_err; }
 
-int g2v_abi_version(void) { return 4; }
+int g2v_abi_version(void) { return 5; }
 
 int g2v_grid_dims(const float voxel_size[3], const float voxel_range[6], int dims[3], int tiles[3]) {
     Grid G;
@@ -531,6 +531,29 @@ int g2v_cosine_loss_backward(long long num_voxels, int feat_dim, const float* gr
     const float inv_count = num_valid_voxel > 0 ? 1.0f / (float)num_valid_voxel : 0.0f;
     G2V_HIP(launch_cosine_backward(num_voxels, feat_dim, voxel_label, occ_mask, grid_feats, pseudo_gt,
                                    grad_output, inv_count, grad_grid_feats, static_cast<hipStream_t>(stream)));
+    return G2V_OK;
+}
+
+int g2v_covariance_from_scale_rotation(int n, const float* scales, const float* rotations, float* covariances,
+                                       void* stream) {
+    g_err[0] = 0;
+    if (n < 0) return fail(G2V_ERR_INVALID, "n = %d", n);
+    if (n > 0 && (!scales || !rotations || !covariances)) return fail(G2V_ERR_INVALID, "null pointer");
+    if ((int64_t)n * 9 > 2147483647ll) return fail(G2V_ERR_LIMIT, "n = %d exceeds the int32 covariance index", n);
+    G2V_HIP(launch_cov_from_scale_rot(n, scales, rotations, covariances, static_cast<hipStream_t>(stream)));
+    return G2V_OK;
+}
+
+int g2v_covariance_from_scale_rotation_backward(int n, const float* scales, const float* rotations,
+                                                const float* grad_covariances, float* grad_scales,
+                                                float* grad_rotations, void* stream) {
+    g_err[0] = 0;
+    if (n < 0) return fail(G2V_ERR_INVALID, "n = %d", n);
+    if (n > 0 && (!scales || !rotations || !grad_covariances || !grad_scales || !grad_rotations))
+        return fail(G2V_ERR_INVALID, "null pointer");
+    if ((int64_t)n * 9 > 2147483647ll) return fail(G2V_ERR_LIMIT, "n = %d exceeds the int32 covariance index", n);
+    G2V_HIP(launch_cov_from_scale_rot_bwd(n, scales, rotations, grad_covariances, grad_scales, grad_rotations,
+                                          static_cast<hipStream_t>(stream)));
     return G2V_OK;
 }
 

@@ -139,6 +139,11 @@ hipError_t launch_cosine_backward(int64_t V, int C, const float* label, const ui
                                   const float* g, const float* grad_out, float inv_count, float* grad_p,
                                   hipStream_t s);
 
+// ---- covariances from scales and rotations (g2v_covariance.hip) ----------------------------
+hipError_t launch_cov_from_scale_rot(int n, const float* scales, const float* rotations, float* cov, hipStream_t s);
+hipError_t launch_cov_from_scale_rot_bwd(int n, const float* scales, const float* rotations, const float* grad_cov,
+                                         float* grad_scales, float* grad_rotations, hipStream_t s);
+
 // Brackets one kernel launch with HIP events when profiling is enabled (g2v_profile.hip).
 class ProfMark {
   public:
