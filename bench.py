@@ -196,6 +196,46 @@ def covariance_leg(_C, n, steps):
             "note": "back-to-back calls; at this size launch-latency bound, not HBM bound"}
 
 
+def batched_leg(steps, warmup):
+    """B scenes per call against one call per scene, on the reference's recorded training batch
+    (tests/golden/mmdet_debug_inputs.npz: 6 groups of 300 Gaussians, 200x200x16 grid) with
+    synthetic 64-D features: fwd+bwd through the module, wall time per batch."""
+    import time
+    import torch
+    from CudaGaussianVoxelizer import PyCudaGaussianVoxelizer
+    from tests import workloads as W
+    dev = torch.device("cuda", 0)
+    m, o, c, vs, vr = W.mmdet_fixture()
+    B, n, C = 6, 300, 64
+    m, o, c = m.reshape(B, n, 3).to(dev), o.reshape(B, n).to(dev), c.reshape(B, n, 9).to(dev)
+    f = torch.randn(B, n, C, generator=torch.Generator().manual_seed(13)).to(dev)
+    vox = PyCudaGaussianVoxelizer(list(vs), list(vr))
+    leaves = [t.clone().requires_grad_() for t in (m, o, c, f)]
+
+    def batched():
+        d, g, _ = vox(*leaves)
+        torch.autograd.backward([d, g], [torch.ones_like(d), torch.ones_like(g)])
+
+    def looped():
+        for b in range(B):
+            d, g, _ = vox(*[t[b].detach().requires_grad_() for t in leaves])
+            torch.autograd.backward([d, g], [torch.ones_like(d), torch.ones_like(g)])
+
+    res = {}
+    for name, fn in (("batched", batched), ("per_scene", looped)):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        res[name + "_ms"] = round((time.perf_counter() - t0) * 1e3 / steps, 3)
+    res.update({"scenes": B, "gaussians_per_scene": n, "feat_dim": C, "grid": [200, 200, 16],
+                "data": "recorded batch inputs, randn features (seed 13), all-ones upstream grads"})
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -304,6 +344,7 @@ def main():
                         "algorithmic_bytes": bytes_k, "avg_ms": round(avg_s * 1e3, 4)}
 
     covariance = covariance_leg(_C, N, max(args.steps, 10))
+    batched = batched_leg(max(args.steps, 5), args.warmup)
     cosine = None
     if C > 0 and not args.no_cosine:
         cosine = cosine_leg(_C, out[5].detach(), args.steps, args.warmup)
@@ -337,6 +378,7 @@ def main():
         "cpu_baseline": cpu,
         "feats_cosine_loss": cosine,
         "covariance_from_scale_rotation": covariance,
+        "batched_scenes": batched,
     }
     print(json.dumps(res), flush=True)
 

@@ -58,6 +58,17 @@ int g2v_forward_plan(int n, const float* means3D, const float* covariances,
                      void* bwd_plan_workspace, size_t bwd_plan_workspace_bytes,
                      long long* num_region_pairs, void* stream);
 
+/* g2v_forward_plan_async: the same work without the synchronisation, for callers that plan
+ * several scenes and wait once: the pair counts land in counts[0] (M) and counts[1] (the
+ * (region, Gaussian) pair count when bwd_plan_workspace is given, else 0), a device-accessible
+ * pointer (device or pinned host memory), when the stream reaches them.  No counterpart in the
+ * reference, which handles one scene per call. */
+int g2v_forward_plan_async(int n, const float* means3D, const float* covariances, const float voxel_size[3],
+                           const float voxel_range[6], float* cov_inv, int* valid_voxel_lb, int* valid_voxel_ub,
+                           int* num_voxels_per_gaussian, int* g2t_offsets, void* workspace, size_t workspace_bytes,
+                           void* bwd_plan_workspace, size_t bwd_plan_workspace_bytes, long long* counts,
+                           void* stream);
+
 /* g2v_forward_splat: G->T fill, radix sort into the Tile->Gaussian CSR, per-tile splat of the
  * density and, when feat_dim > 0, of the density-weighted feature average (reference
  * .cu:1634-1904).  density (X,Y,Z) and grid_feats (X,Y,Z,feat_dim) are written completely;

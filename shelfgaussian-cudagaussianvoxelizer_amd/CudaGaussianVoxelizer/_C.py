@@ -12,7 +12,7 @@ import torch
 
 from . import _lib
 
-__all__ = ["gaussian_voxelizer_forward", "gaussian_voxelizer_backward",
+__all__ = ["gaussian_voxelizer_forward", "gaussian_voxelizer_backward", "gaussian_voxelizer_forward_batched",
            "CudaFeatsCosinelossForward", "CudaFeatsCosinelossBackward", "build_t2g", "grid_dims",
            "covariance_from_scale_rotation", "covariance_from_scale_rotation_backward"]
 
@@ -221,7 +221,7 @@ def gaussian_voxelizer_backward(grad_output, grad_feats_output, means3D, opacity
 
 def _backward(grad_output, grad_feats_output, means3D, opacity, cov_inv, voxel_size, voxel_range,
               valid_voxel_lb, valid_voxel_ub, num_voxels_per_gaussian, g2t_offsets, g2t_tile_ids,
-              density, grid_feats, features, t2g):
+              density, grid_feats, features, t2g, timed=True):
     """The backward; t2g is what _forward(keep_t2g=True) returned beside the 9-tuple, or None.
     With t2g the saved tensors are the forward's own outputs (already checked there), and the
     grid, plan, outputs and workspace come from the forward: only the upstream gradients are
@@ -277,8 +277,9 @@ def _backward(grad_output, grad_feats_output, means3D, opacity, cov_inv, voxel_s
             grad_cov = torch.empty(n, 9, dtype=f32, device=dev)
             grad_opacity = torch.empty(n, dtype=f32, device=dev)
             grad_feats = torch.empty(n, C, dtype=f32, device=dev)
-        start, stop = _timing_events(dev)
-        start.record(cur)
+        if timed:
+            start, stop = _timing_events(dev)
+            start.record(cur)
         if t2g is not None and C > 0:   # planned by the forward
             plan_ws, MR = t2g["plan"], t2g["num_region_pairs"]
         else:
@@ -303,10 +304,165 @@ def _backward(grad_output, grad_feats_output, means3D, opacity, cov_inv, voxel_s
                                     _ptr(grad_feats), _ptr(csr[0]), _ptr(csr[1]), _ptr(csr[2]),
                                     _ptr(plan_ws), _ptr(ws), ws.numel(), stream),
                    "gaussian_voxelizer_backward")
+        bwd_sec = 0.0
+        if timed:
+            stop.record(cur)
+            stop.synchronize()
+            bwd_sec = start.elapsed_time(stop) / 1000.0
+    return (grad_means, grad_cov, grad_opacity, grad_feats, bwd_sec)
+
+
+_COUNTS = {}
+
+
+def _pinned_counts(dev, B):
+    """A reusable pinned (B, 2) int64 host buffer per device and thread (count read-back)."""
+    import threading
+    key = (dev.index, threading.get_ident())
+    buf = _COUNTS.get(key)
+    if buf is None or buf.shape[0] < B:
+        buf = torch.empty(max(B, 8), 2, dtype=torch.int64, pin_memory=True)
+        _COUNTS[key] = buf
+    return buf[:B]
+
+
+def gaussian_voxelizer_forward_batched(means3D, opacity, covariances, voxel_size, voxel_range, features=None):
+    """Forward of B scenes on one grid in one call: means3D (B,N,3), opacity (B,N) or (B,N,1),
+    covariances (B,N,9) or (B,N,3,3), features (B,N,C) or None.
+
+    Every scene is planned before the host waits once for all their pair counts (one scene per
+    call would wait B times); then every scene is splatted.  Returns a list of B 9-tuples laid out
+    as gaussian_voxelizer_forward's; the density and grid_feats of scene b are the views [b] of one
+    (B,X,Y,Z) and one (B,X,Y,Z,C) tensor, and the time in every tuple is that of the whole batch.
+    """
+    return [r[0] for r in _forward_batched(means3D, opacity, covariances, voxel_size, voxel_range, features,
+                                           keep_t2g=False)[0]]
+
+
+def _forward_batched(means3D, opacity, covariances, voxel_size, voxel_range, features, keep_t2g):
+    """Batched forward.  Returns ([(9-tuple, t2g) per scene], density (B,X,Y,Z), grid_feats
+    (B,X,Y,Z,C)); t2g as _forward(keep_t2g=True) returns it, or None."""
+    lib = _lib.load()
+    means = _f32_input(means3D, "means3D")
+    if means.dim() != 3 or means.shape[2] != 3:
+        raise RuntimeError(f"batched means3D must be (B, N, 3), got {tuple(means.shape)}")
+    B, n = means.shape[0], means.shape[1]
+    dev = means.device
+    op = _f32_input(opacity, "opacity", (B, n))
+    cov = _f32_input(covariances, "covariances", (B, n, 9))
+    feats = None
+    C = 0
+    if features is not None:
+        feats = _f32_input(features, "features")
+        if feats.dim() != 3 or tuple(feats.shape[:2]) != (B, n):
+            raise RuntimeError(f"features must be (B, N, C) with B, N = {B}, {n}, got {tuple(feats.shape)}")
+        C = feats.shape[2]
+        if C == 0:
+            feats = None
+    vs_h = _host_values(voxel_size, 3, "voxel_size")
+    vr_h = _host_values(voxel_range, 6, "voxel_range")
+    vs, vr = _lib.floats(vs_h), _lib.floats(vr_h)
+    (X, Y, Z), (Tx, Ty, Tz) = grid_dims(vs_h, vr_h)
+    T = Tx * Ty * Tz
+
+    with _OnDevice(dev):
+        cur = torch.cuda.current_stream(dev)
+        stream = ctypes.c_void_p(cur.cuda_stream)
+        i32 = dict(dtype=torch.int32, device=dev)
+        f32 = dict(dtype=torch.float32, device=dev)
+        cov_inv = torch.empty(B, n, 9, **f32)
+        lb = torch.empty(B, n, 3, **i32)
+        ub = torch.empty(B, n, 3, **i32)
+        nvox = torch.empty(B, n, **i32)
+        g2t_offsets = torch.empty(B, n + 1, **i32)
+        pws = lib.g2v_forward_plan_workspace(n)
+        ws = torch.empty(B, (pws + 255) // 256 * 256, dtype=torch.uint8, device=dev)   # rows 256-byte aligned
+        bws = max(1, lib.g2v_backward_plan_workspace(n)) if keep_t2g else 0
+        bplan = torch.empty(B, (bws + 255) // 256 * 256, dtype=torch.uint8, device=dev) if keep_t2g else None
+        counts_dev = torch.empty(B, 2, dtype=torch.int64, device=dev)
+        density = torch.empty(B, X, Y, Z, **f32)
+        grid_feats = torch.empty(B, X, Y, Z, C, **f32)
+        start, stop = _timing_events(dev)
+        start.record(cur)
+        for b in range(B):
+            _lib.check(lib.g2v_forward_plan_async(n, _ptr(means[b]), _ptr(cov[b]), vs, vr, _ptr(cov_inv[b]),
+                                                  _ptr(lb[b]), _ptr(ub[b]), _ptr(nvox[b]), _ptr(g2t_offsets[b]),
+                                                  _ptr(ws[b]), pws, None if bplan is None else _ptr(bplan[b]),
+                                                  bws, _ptr(counts_dev[b]), stream),
+                       "gaussian_voxelizer_forward_batched (plan)")
+        counts = _pinned_counts(dev, B)
+        counts.copy_(counts_dev, non_blocking=True)
+        cur.synchronize()   # the one host wait of the batch
+        cnt = counts.tolist()
+        results = []
+        for b in range(B):
+            M, MR = int(cnt[b][0]), int(cnt[b][1])
+            if M > 2147483647 or MR > 2147483647:
+                raise RuntimeError(f"scene {b}: pair counts {M}, {MR} exceed the int32 CSR")
+            g2t_tile_ids = torch.empty(M, **i32)
+            ws2 = torch.empty(lib.g2v_forward_splat_workspace(n, C, M, vs, vr), dtype=torch.uint8, device=dev)
+            t2g = None
+            csr = (None, None, None)
+            if keep_t2g:
+                csr = (torch.empty(M, **i32), torch.empty(M, **i32), torch.empty(T + 1, **i32))
+                t2g = dict(csr=csr, plan=bplan[b], num_region_pairs=MR, vs=vs, vr=vr, dims=(X, Y, Z))
+            fb = None if feats is None else feats[b]
+            _lib.check(lib.g2v_forward_splat(n, C, _ptr(means[b]), _ptr(op[b]), _ptr(fb), vs, vr,
+                                             _ptr(cov_inv[b]), _ptr(lb[b]), _ptr(ub[b]), _ptr(g2t_offsets[b]), M,
+                                             _ptr(g2t_tile_ids), _ptr(density[b]), _ptr(grid_feats[b]),
+                                             _ptr(csr[0]), _ptr(csr[1]), _ptr(csr[2]), _ptr(ws2), ws2.numel(),
+                                             stream),
+                       "gaussian_voxelizer_forward_batched (splat)")
+            results.append([[density[b], cov_inv[b], lb[b], ub[b], nvox[b], grid_feats[b], g2t_offsets[b],
+                             g2t_tile_ids, 0.0], t2g])
+        stop.record(cur)
+        if keep_t2g:
+            for b, (r, t2g) in enumerate(results):
+                M = r[7].numel()
+                t2g["grads"] = (torch.empty(n, 3, **f32), torch.empty(n, 9, **f32), torch.empty(n, **f32),
+                                torch.empty(n, C, **f32))
+                t2g["ws"] = torch.empty(max(1, lib.g2v_backward_workspace(n, C, M, t2g["num_region_pairs"], vs, vr)),
+                                        dtype=torch.uint8, device=dev)
+                if C > 0:
+                    _lib.check(lib.g2v_backward_prepare(n, C, vs, vr, _ptr(lb[b]), _ptr(ub[b]), _ptr(feats[b]), M,
+                                                        t2g["num_region_pairs"], _ptr(t2g["csr"][0]),
+                                                        _ptr(t2g["csr"][1]), _ptr(t2g["plan"]), _ptr(t2g["ws"]),
+                                                        t2g["ws"].numel(), stream),
+                               "gaussian_voxelizer_forward_batched (backward preparation)")
+                    t2g["prepared"] = True
+        stop.synchronize()
+        fwd_sec = start.elapsed_time(stop) / 1000.0
+    out = []
+    for r, t2g in results:
+        r[8] = fwd_sec
+        out.append((tuple(r), t2g))
+    return out, density, grid_feats
+
+
+def _backward_batched(grad_density, grad_feats, means, opacity, features, scenes):
+    """Backward of _forward_batched(keep_t2g=True): grad_density (B,X,Y,Z), grad_feats (B,X,Y,Z,C);
+    scenes = its per-scene (9-tuple, t2g) list.  Returns stacked gradients (B,N,3), (B,N,9),
+    (B,N), (B,N,C) and the time of the whole batch."""
+    dev = means.device
+    B = len(scenes)
+    with _OnDevice(dev):
+        cur = torch.cuda.current_stream(dev)
+        start, stop = _timing_events(dev)
+        start.record(cur)
+        grads = []
+        for b, (r, t2g) in enumerate(scenes):
+            (density, cov_inv, lb, ub, nvox, gfeat, g2t_offsets, g2t_tile_ids, _) = r
+            fb = None if features is None else features[b]
+            gF = grad_feats[b] if grad_feats is not None and grad_feats.shape[-1] > 0 else gfeat.new_zeros(gfeat.shape)
+            grads.append(_backward(grad_density[b], gF, means[b], opacity[b], cov_inv, None, None, lb, ub, nvox,
+                                   g2t_offsets, g2t_tile_ids, density, gfeat, fb, t2g=t2g, timed=False))
         stop.record(cur)
         stop.synchronize()
         bwd_sec = start.elapsed_time(stop) / 1000.0
-    return (grad_means, grad_cov, grad_opacity, grad_feats, bwd_sec)
+    return (torch.stack([g[0] for g in grads]) if B else means.new_zeros(0, 0, 3),
+            torch.stack([g[1] for g in grads]) if B else means.new_zeros(0, 0, 9),
+            torch.stack([g[2] for g in grads]) if B else means.new_zeros(0, 0),
+            torch.stack([g[3] for g in grads]) if B else means.new_zeros(0, 0, 0), bwd_sec)
 
 
 def build_t2g(voxel_size, voxel_range, valid_voxel_lb, valid_voxel_ub, g2t_offsets, g2t_tile_ids):

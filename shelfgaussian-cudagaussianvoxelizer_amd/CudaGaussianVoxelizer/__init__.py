@@ -11,10 +11,10 @@ import torch.nn as nn
 
 from . import _C
 from ._C import gaussian_voxelizer_forward, gaussian_voxelizer_backward
-from ._C import CudaFeatsCosinelossForward, CudaFeatsCosinelossBackward
+from ._C import CudaFeatsCosinelossForward, CudaFeatsCosinelossBackward, gaussian_voxelizer_forward_batched
 
 __all__ = ["PyCudaGaussianVoxelizer", "PyCudaFeatsCosineLoss", "_C",
-           "gaussian_voxelizer_forward", "gaussian_voxelizer_backward",
+           "gaussian_voxelizer_forward", "gaussian_voxelizer_backward", "gaussian_voxelizer_forward_batched",
            "CudaFeatsCosinelossForward", "CudaFeatsCosinelossBackward", "covariance_from_scale_rotation"]
 
 
@@ -86,6 +86,38 @@ class _CudaFeatsCosinelossFunction(torch.autograd.Function):
         return None, None, grad_predict, None
 
 
+class _CudaGaussianVoxelizeBatchedFunction(torch.autograd.Function):
+    """Autograd wrapper of B scenes on one grid (means3D (B,N,3)): one host wait for the whole
+    batch's plan, per-scene CSR; returns density (B,X,Y,Z), grid_feats (B,X,Y,Z,C) and stats."""
+
+    @staticmethod
+    def forward(ctx, means3D, opacity, covariances, voxel_size, voxel_range, features):
+        scenes, density, grid_feats = _C._forward_batched(means3D, opacity, covariances, voxel_size, voxel_range,
+                                                          features, keep_t2g=True)
+        stats = torch.zeros(2, dtype=torch.float32, device="cpu")
+        stats[0] = scenes[0][0][8] if scenes else 0.0
+        ctx.scenes = scenes
+        ctx.save_for_backward(means3D, opacity, features, stats)
+        ctx.mark_non_differentiable(stats)
+        ctx.shapes = (means3D.shape, opacity.shape, covariances.shape)
+        return density, grid_feats, stats
+
+    @staticmethod
+    def backward(ctx, grad_density_output, grad_feats_output, grad_stats):
+        means3D, opacity, features, stats = ctx.saved_tensors
+        B, n = means3D.shape[0], means3D.shape[1]
+        gD = grad_density_output.to(torch.float32).contiguous()
+        gF = grad_feats_output.to(torch.float32).contiguous()
+        m32 = means3D.detach().contiguous()
+        o32 = opacity.detach().reshape(B, n).contiguous()
+        feats = None if features is None else features.detach().contiguous()
+        gm, gc, go, gf, bwd_sec = _C._backward_batched(gD, gF, m32, o32, feats, ctx.scenes)
+        ctx.scenes = None
+        stats[1] = bwd_sec
+        return (gm.reshape(ctx.shapes[0]), go.reshape(ctx.shapes[1]), gc.reshape(ctx.shapes[2]), None, None,
+                gf if features is not None else None)
+
+
 class _CovarianceFromScaleRotation(torch.autograd.Function):
     """Covariances from scales and rotations (reference test/gaussian_voxelizer.py:14-37), with
     the chain rule back to both."""
@@ -127,11 +159,16 @@ class PyCudaGaussianVoxelizer(nn.Module):
     def forward(self, means3D, opacity, covariances=None, features=None, *, scales=None, rotations=None):
         """As the reference's forward; without covariances, they are built from ``scales`` (N, 3)
         and ``rotations`` (N, 4) (as ShelfGaussian's voxelizer does, reference
-        test/gaussian_voxelizer.py:168-169) and the gradients flow to those two."""
+        test/gaussian_voxelizer.py:168-169) and the gradients flow to those two.  With means3D of
+        shape (B, N, 3) (opacity (B, N[, 1]), covariances (B, N, 9), features (B, N, C)) the B
+        scenes are voxelized in one call: density (B, X, Y, Z), grid_feats (B, X, Y, Z, C)."""
         if covariances is None:
             if scales is None or rotations is None:
                 raise RuntimeError("give covariances, or scales and rotations")
             covariances = covariance_from_scale_rotation(scales, rotations)
+        if means3D.dim() == 3:   # B scenes on this grid: (B,N,3) means, outputs gain a leading B
+            return _CudaGaussianVoxelizeBatchedFunction.apply(means3D, opacity, covariances, self.voxel_size,
+                                                              self.voxel_range, features)
         return _CudaGaussianVoxelizeFunction.apply(means3D, opacity, covariances, self.voxel_size,
                                                    self.voxel_range, features)
 

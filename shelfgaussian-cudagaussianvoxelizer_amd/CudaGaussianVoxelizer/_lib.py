@@ -26,6 +26,7 @@ SIGNATURES = {
     "g2v_forward_plan_workspace": (_sz, [_i]),
     "g2v_forward_plan": (_i, [_i, _vp, _vp, _f3, _f3, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _llp, _vp, _sz, _llp,
                               _vp]),
+    "g2v_forward_plan_async": (_i, [_i, _vp, _vp, _f3, _f3, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _sz, _vp, _vp]),
     "g2v_forward_splat_workspace": (_sz, [_i, _i, _ll, _f3, _f3]),
     "g2v_forward_splat": (_i, [_i, _i, _vp, _vp, _vp, _f3, _f3, _vp, _vp, _vp, _vp, _ll, _vp, _vp,
                                _vp, _vp, _vp, _vp, _vp, _sz, _vp]),

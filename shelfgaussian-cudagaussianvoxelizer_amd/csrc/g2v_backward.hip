@@ -620,6 +620,12 @@ __global__ void __launch_bounds__(256) k_fill_i32(int64_t n, int v, int* __restr
     if (i < n) dst[i] = v;
 }
 
+hipError_t launch_fill_i32(int64_t n, int v, int* dst, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    G2V_LAUNCH(k_fill_i32, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, s, n, v, dst);
+    return hipGetLastError();
+}
+
 // Row table of phase B: for region row r (its position in the region's ascending Gaussian list,
 // at G->R slot roff[R] + r) and tile slot s, table[(roff[R] + r) * kBrSlots + s] is the
 // Tile->Gaussian index of the pair (tile, Gaussian), or M (the zero row of the split weights)

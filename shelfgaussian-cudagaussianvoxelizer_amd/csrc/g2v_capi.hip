@@ -123,7 +123,7 @@ extern "C" {
 
 const char* g2v_last_error(void) { return g_err; }
 
-int g2v_abi_version(void) { return 5; }
+int g2v_abi_version(void) { return 6; }
 
 int g2v_grid_dims(const float voxel_size[3], const float voxel_range[6], int dims[3], int tiles[3]) {
     Grid G;
@@ -143,6 +143,65 @@ size_t g2v_forward_plan_workspace(int n) {
     return c.off + 256;
 }
 
+}  // extern "C"
+
+namespace {
+
+// Argument checks shared by the synchronous and the asynchronous plan.
+int plan_checks(int n, const float* means3D, const float* covariances, const float* voxel_size,
+                const float* voxel_range, float* cov_inv, int* lb, int* ub, int* nvox, int* g2t_offsets,
+                void* workspace, size_t workspace_bytes, void* bwd_plan_workspace, size_t bwd_plan_workspace_bytes,
+                Grid& G) {
+    if (n < 0) return fail(G2V_ERR_INVALID, "n = %d", n);
+    if (!g2t_offsets) return fail(G2V_ERR_INVALID, "g2t_offsets is null");
+    if (bwd_plan_workspace && bwd_plan_workspace_bytes < backward_plan_workspace(n > 0 ? n : 0))
+        return fail(G2V_ERR_INVALID, "backward plan workspace too small: %zu < %zu bytes",
+                    bwd_plan_workspace_bytes, backward_plan_workspace(n > 0 ? n : 0));
+    if (n > 0 && (!means3D || !covariances || !cov_inv || !lb || !ub || !nvox))
+        return fail(G2V_ERR_INVALID, "null input/output pointer");
+    int rc = make_grid(voxel_size, voxel_range, G);
+    if (rc != G2V_OK) return rc;
+    return check_ws(workspace, workspace_bytes, g2v_forward_plan_workspace(n), "plan");
+}
+
+// Boxes, inverse covariances and G->T row offsets, plus the backward plan's region cell offsets
+// when bwd_plan_workspace is given; the pair counts land in counts[0] (M) and counts[1] (MR, or
+// 0), a device-accessible pointer, when the stream reaches them.  The backward's (region,
+// Gaussian) pair count rides on the same launches: the box kernel also counts each box's region
+// cells, and one launch scans both count arrays.
+int plan_launch(const Grid& G, int n, const float* means3D, const float* covariances, float* cov_inv, int* lb,
+                int* ub, int* nvox, int* g2t_offsets, void* workspace, size_t workspace_bytes,
+                void* bwd_plan_workspace, long long* counts, hipStream_t s) {
+    Carver c(workspace, workspace_bytes);
+    c.take<long long>(2);
+    void* scan_ws = c.take<char>(scan_workspace(n > 0 ? n : 1));
+    int cell[3] = {1, 1, 1};
+    void* plan_scan_ws = nullptr;
+    int* cell_off = bwd_plan_workspace ? backward_plan_cells(G, bwd_plan_workspace, n, cell, &plan_scan_ws) : nullptr;
+    G2V_HIP(launch_boxes(G, n, means3D, covariances, cov_inv, lb, ub, nvox, g2t_offsets, cell_off ? cell : nullptr,
+                         cell_off, s));
+    if (n > 0) {
+        G2V_HIP(scan_i32_pair(g2t_offsets + 1, g2t_offsets + 1, n, counts, scan_ws, cell_off ? cell_off + 1 : nullptr,
+                              cell_off ? cell_off + 1 : nullptr, cell_off ? n : 0, counts + 1, plan_scan_ws, s));
+        if (!cell_off) G2V_HIP(launch_fill_i32(2, 0, reinterpret_cast<int*>(counts + 1), s));
+    } else {
+        G2V_HIP(launch_fill_i32(4, 0, reinterpret_cast<int*>(counts), s));
+    }
+    return G2V_OK;
+}
+
+int check_counts(long long M, long long MR) {
+    if (M > 2147483647ll)
+        return fail(G2V_ERR_LIMIT, "%lld Gaussian-tile pairs exceed the int32 CSR (limit 2^31-1)", M);
+    if (MR > 2147483647ll)
+        return fail(G2V_ERR_LIMIT, "%lld region-Gaussian pairs exceed the int32 CSR", MR);
+    return G2V_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
 int g2v_forward_plan(int n, const float* means3D, const float* covariances,
                      const float voxel_size[3], const float voxel_range[6], float* cov_inv,
                      int* valid_voxel_lb, int* valid_voxel_ub, int* num_voxels_per_gaussian,
@@ -150,60 +209,52 @@ int g2v_forward_plan(int n, const float* means3D, const float* covariances,
                      long long* num_pairs, void* bwd_plan_workspace, size_t bwd_plan_workspace_bytes,
                      long long* num_region_pairs, void* stream) {
     g_err[0] = 0;
-    if (n < 0) return fail(G2V_ERR_INVALID, "n = %d", n);
-    if (!num_pairs || !g2t_offsets) return fail(G2V_ERR_INVALID, "num_pairs / g2t_offsets null");
+    if (!num_pairs) return fail(G2V_ERR_INVALID, "num_pairs is null");
     if (bwd_plan_workspace && !num_region_pairs)
         return fail(G2V_ERR_INVALID, "bwd_plan_workspace needs num_region_pairs");
-    if (bwd_plan_workspace && bwd_plan_workspace_bytes < backward_plan_workspace(n > 0 ? n : 0))
-        return fail(G2V_ERR_INVALID, "backward plan workspace too small: %zu < %zu bytes",
-                    bwd_plan_workspace_bytes, backward_plan_workspace(n > 0 ? n : 0));
-    if (n > 0 && (!means3D || !covariances || !cov_inv || !valid_voxel_lb || !valid_voxel_ub ||
-                  !num_voxels_per_gaussian))
-        return fail(G2V_ERR_INVALID, "null input/output pointer");
     Grid G;
-    int rc = make_grid(voxel_size, voxel_range, G);
-    if (rc != G2V_OK) return rc;
-    rc = check_ws(workspace, workspace_bytes, g2v_forward_plan_workspace(n), "plan");
+    int rc = plan_checks(n, means3D, covariances, voxel_size, voxel_range, cov_inv, valid_voxel_lb, valid_voxel_ub,
+                         num_voxels_per_gaussian, g2t_offsets, workspace, workspace_bytes, bwd_plan_workspace,
+                         bwd_plan_workspace_bytes, G);
     if (rc != G2V_OK) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    Carver c(workspace, workspace_bytes);
-    long long* total = c.take<long long>(2);
-    void* scan_ws = c.take<char>(scan_workspace(n > 0 ? n : 1));
-    // the backward's (region, Gaussian) pair count rides on the same launches and synchronisation:
-    // the box kernel also counts each box's region cells, and one launch scans both count arrays
-    int cell[3] = {1, 1, 1};
-    void* plan_scan_ws = nullptr;
-    int* cell_off = bwd_plan_workspace ? backward_plan_cells(G, bwd_plan_workspace, n, cell, &plan_scan_ws) : nullptr;
+    // the counts go straight into pinned host memory when there is some (no copy before the host
+    // wait), else into the workspace and are copied
     long long* hc = pinned_counts();
-    long long* dc = total;
-    if (hc) {
-        hc[0] = hc[1] = 0;
-        G2V_HIP(hipHostGetDevicePointer(reinterpret_cast<void**>(&dc), hc, 0));
-    }
-
-    G2V_HIP(launch_boxes(G, n, means3D, covariances, cov_inv, valid_voxel_lb, valid_voxel_ub,
-                         num_voxels_per_gaussian, g2t_offsets, cell_off ? cell : nullptr, cell_off, s));
-    long long M = 0, MR = 0;
-    if (n > 0) {
-        G2V_HIP(scan_i32_pair(g2t_offsets + 1, g2t_offsets + 1, n, dc, scan_ws, cell_off ? cell_off + 1 : nullptr,
-                              cell_off ? cell_off + 1 : nullptr, cell_off ? n : 0, dc + 1, plan_scan_ws, s));
-        if (!hc) {   // counts in device memory: copy them after every launch, one host wait
-            G2V_HIP(hipMemcpyAsync(&M, total, sizeof(long long), hipMemcpyDeviceToHost, s));
-            if (cell_off) G2V_HIP(hipMemcpyAsync(&MR, total + 1, sizeof(long long), hipMemcpyDeviceToHost, s));
-        }
-    }
+    long long* dc = reinterpret_cast<long long*>(Carver(workspace, workspace_bytes).take<long long>(2));
+    if (hc) G2V_HIP(hipHostGetDevicePointer(reinterpret_cast<void**>(&dc), hc, 0));
+    rc = plan_launch(G, n, means3D, covariances, cov_inv, valid_voxel_lb, valid_voxel_ub, num_voxels_per_gaussian,
+                     g2t_offsets, workspace, workspace_bytes, bwd_plan_workspace, dc, s);
+    if (rc != G2V_OK) return rc;
+    long long cnt[2] = {0, 0};
+    if (!hc) G2V_HIP(hipMemcpyAsync(cnt, dc, sizeof(cnt), hipMemcpyDeviceToHost, s));
     G2V_HIP(hipStreamSynchronize(s));
-    if (hc && n > 0) {
-        M = hc[0];
-        MR = cell_off ? hc[1] : 0;
+    if (hc) {
+        cnt[0] = hc[0];
+        cnt[1] = hc[1];
     }
-    if (M > 2147483647ll)
-        return fail(G2V_ERR_LIMIT, "%lld Gaussian-tile pairs exceed the int32 CSR (limit 2^31-1)", M);
-    if (MR > 2147483647ll)
-        return fail(G2V_ERR_LIMIT, "%lld region-Gaussian pairs exceed the int32 CSR", MR);
-    *num_pairs = M;
-    if (num_region_pairs) *num_region_pairs = bwd_plan_workspace ? MR : 0;
+    rc = check_counts(cnt[0], cnt[1]);
+    if (rc != G2V_OK) return rc;
+    *num_pairs = cnt[0];
+    if (num_region_pairs) *num_region_pairs = bwd_plan_workspace ? cnt[1] : 0;
     return G2V_OK;
+}
+
+int g2v_forward_plan_async(int n, const float* means3D, const float* covariances, const float voxel_size[3],
+                           const float voxel_range[6], float* cov_inv, int* valid_voxel_lb, int* valid_voxel_ub,
+                           int* num_voxels_per_gaussian, int* g2t_offsets, void* workspace, size_t workspace_bytes,
+                           void* bwd_plan_workspace, size_t bwd_plan_workspace_bytes, long long* counts,
+                           void* stream) {
+    g_err[0] = 0;
+    if (!counts) return fail(G2V_ERR_INVALID, "counts is null");
+    Grid G;
+    int rc = plan_checks(n, means3D, covariances, voxel_size, voxel_range, cov_inv, valid_voxel_lb, valid_voxel_ub,
+                         num_voxels_per_gaussian, g2t_offsets, workspace, workspace_bytes, bwd_plan_workspace,
+                         bwd_plan_workspace_bytes, G);
+    if (rc != G2V_OK) return rc;
+    return plan_launch(G, n, means3D, covariances, cov_inv, valid_voxel_lb, valid_voxel_ub, num_voxels_per_gaussian,
+                       g2t_offsets, workspace, workspace_bytes, bwd_plan_workspace, counts,
+                       static_cast<hipStream_t>(stream));
 }
 
 size_t g2v_forward_splat_workspace(int n, int feat_dim, long long num_pairs, const float voxel_size[3],

@@ -71,6 +71,9 @@ hipError_t launch_tile_offsets(const int* sorted_keys, int64_t M, int T, int* ti
 hipError_t launch_rle(const int* tile_offsets, int T, int* unique_tiles, int* counts,
                       int* runs_offsets, int* num_runs, void* ws, hipStream_t s);
 
+// n ints of value v (a kernel, not a memset node: safe where a stream may be captured).
+hipError_t launch_fill_i32(int64_t n, int v, int* dst, hipStream_t s);
+
 // ---- forward (g2v_forward.hip) ------------------------------------------------------------
 // Channels of the packed feature rows of the forward (a multiple of one wave's 128 channels).
 constexpr int kPackedChannelAlign = 128;
