@@ -48,6 +48,8 @@ def parse():
                     help="fraction of tiles (forward) and Gaussians (backward) the CPU baseline runs")
     ap.add_argument("--no-cosine", action="store_true",
                     help="skip the feature cosine-loss leg (the consumer of grid_feats)")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the covariance-construction and batched-scenes legs")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="also run a plain device copy of this size (PMC scale reference)")
     return ap.parse_args()
@@ -343,8 +345,10 @@ def main():
                         "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4), "traffic": traffic,
                         "algorithmic_bytes": bytes_k, "avg_ms": round(avg_s * 1e3, 4)}
 
-    covariance = covariance_leg(_C, N, max(args.steps, 10))
-    batched = batched_leg(max(args.steps, 5), args.warmup)
+    covariance = batched = None
+    if not args.no_extra:
+        covariance = covariance_leg(_C, N, max(args.steps, 10))
+        batched = batched_leg(max(args.steps, 5), args.warmup)
     cosine = None
     if C > 0 and not args.no_cosine:
         cosine = cosine_leg(_C, out[5].detach(), args.steps, args.warmup)
