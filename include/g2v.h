@@ -29,6 +29,12 @@ extern "C" {
 #define G2V_ERR_HIP 2       /* a HIP runtime call failed */
 #define G2V_ERR_LIMIT 3     /* problem exceeds a 32-bit index (pairs, grid cells) */
 
+/* Element type of the feature tensors (features, grid_feats, grad_features): float32, or
+ * bfloat16 (grid_feats and grad_features are then rounded to nearest even from float32 sums).
+ * Everything else (means, opacity, covariances, density, upstream gradients) is float32. */
+#define G2V_DTYPE_F32 0
+#define G2V_DTYPE_BF16 1
+
 /* Message of the last failed call on this thread ("" if none). */
 const char* g2v_last_error(void);
 
@@ -79,10 +85,10 @@ int g2v_forward_plan_async(int n, const float* means3D, const float* covariances
 size_t g2v_forward_splat_workspace(int n, int feat_dim, long long num_pairs, const float voxel_size[3],
                                    const float voxel_range[6]);
 int g2v_forward_splat(int n, int feat_dim, const float* means3D, const float* opacity,
-                      const float* features, const float voxel_size[3], const float voxel_range[6],
-                      const float* cov_inv, const int* valid_voxel_lb, const int* valid_voxel_ub,
-                      const int* g2t_offsets, long long num_pairs, int* g2t_tile_ids,
-                      float* density, float* grid_feats, int* t2g_tiles, int* t2g_gauss,
+                      const void* features, int feat_dtype, const float voxel_size[3],
+                      const float voxel_range[6], const float* cov_inv, const int* valid_voxel_lb,
+                      const int* valid_voxel_ub, const int* g2t_offsets, long long num_pairs,
+                      int* g2t_tile_ids, float* density, void* grid_feats, int* t2g_tiles, int* t2g_gauss,
                       int* t2g_offsets, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- backward -----------------------------------------------------------------------------
@@ -112,8 +118,8 @@ int g2v_backward(int n, int feat_dim, const float* grad_density, const float* gr
                  const int* valid_voxel_lb, const int* valid_voxel_ub,
                  const int* num_voxels_per_gaussian, const int* g2t_offsets,
                  const int* g2t_tile_ids, long long num_pairs, long long num_region_pairs,
-                 const float* density, const float* grid_feats, const float* features,
-                 float* grad_means, float* grad_cov, float* grad_opacity, float* grad_features,
+                 const float* density, const void* grid_feats, const void* features, int feat_dtype,
+                 float* grad_means, float* grad_cov, float* grad_opacity, void* grad_features,
                  const int* t2g_tiles, const int* t2g_gauss, const int* t2g_offsets,
                  const void* plan_workspace, void* workspace, size_t workspace_bytes, void* stream);
 
@@ -130,8 +136,8 @@ int g2v_backward(int n, int feat_dim, const float* grad_density, const float* gr
  * same Gaussians, features, CSR and plan (and that nothing has written since); it skips those
  * kernels.  Requires the Tile->Gaussian CSR arguments. */
 int g2v_backward_prepare(int n, int feat_dim, const float voxel_size[3], const float voxel_range[6],
-                         const int* valid_voxel_lb, const int* valid_voxel_ub, const float* features,
-                         long long num_pairs, long long num_region_pairs, const int* t2g_tiles,
+                         const int* valid_voxel_lb, const int* valid_voxel_ub, const void* features,
+                         int feat_dtype, long long num_pairs, long long num_region_pairs, const int* t2g_tiles,
                          const int* t2g_gauss, const void* plan_workspace, void* workspace,
                          size_t workspace_bytes, void* stream);
 int g2v_backward_prepared(int n, int feat_dim, const float* grad_density, const float* grad_feats,
@@ -140,8 +146,8 @@ int g2v_backward_prepared(int n, int feat_dim, const float* grad_density, const 
                           const int* valid_voxel_lb, const int* valid_voxel_ub,
                           const int* num_voxels_per_gaussian, const int* g2t_offsets,
                           const int* g2t_tile_ids, long long num_pairs, long long num_region_pairs,
-                          const float* density, const float* grid_feats, const float* features,
-                          float* grad_means, float* grad_cov, float* grad_opacity, float* grad_features,
+                          const float* density, const void* grid_feats, const void* features, int feat_dtype,
+                          float* grad_means, float* grad_cov, float* grad_opacity, void* grad_features,
                           const int* t2g_tiles, const int* t2g_gauss, const int* t2g_offsets,
                           const void* plan_workspace, void* workspace, size_t workspace_bytes, void* stream);
 

@@ -63,6 +63,21 @@ def _f32_input(t, name, shape=None):
     return t.detach().contiguous()
 
 
+_FEAT_DTYPES = {torch.float32: _lib.G2V_DTYPE_F32, torch.bfloat16: _lib.G2V_DTYPE_BF16}
+
+
+def _feat_input(t, name):
+    """Features: float32 or bfloat16 on the GPU (grid_feats and the feature gradient take the
+    same type)."""
+    if not isinstance(t, torch.Tensor):
+        raise RuntimeError(f"{name} must be a tensor")
+    if t.device.type != "cuda":
+        raise RuntimeError(f"{name} must be a GPU tensor, got {t.device}")
+    if t.dtype not in _FEAT_DTYPES:
+        raise RuntimeError(f"expected scalar type Float or BFloat16 for {name} but found {t.dtype}")
+    return t.detach().contiguous()
+
+
 def _check_saved(t, name, dtype, device):
     if not isinstance(t, torch.Tensor) or t.dtype != dtype or not t.is_contiguous() or t.device != device:
         raise RuntimeError(f"{name} must be a contiguous {dtype} tensor on {device}")
@@ -133,7 +148,7 @@ def _forward(means3D, opacity, covariances, voxel_size, voxel_range, features, k
     feats = None
     C = 0
     if features is not None:
-        feats = _f32_input(features, "features")
+        feats = _feat_input(features, "features")
         if feats.dim() != 2 or feats.shape[0] != n:
             raise RuntimeError(f"features must be (N, C) with N = {n}, got {tuple(feats.shape)}")
         C = feats.shape[1]
@@ -157,7 +172,9 @@ def _forward(means3D, opacity, covariances, voxel_size, voxel_range, features, k
         ws = torch.empty(lib.g2v_forward_plan_workspace(n), dtype=torch.uint8, device=dev)
         # outputs whose size does not depend on the plan's count, allocated before its host wait
         density = torch.empty(X, Y, Z, **f32)
-        grid_feats = torch.empty(X, Y, Z, C, **f32)
+        fdtype = torch.float32 if feats is None else feats.dtype
+        fdt = _FEAT_DTYPES[fdtype]
+        grid_feats = torch.empty(X, Y, Z, C, dtype=fdtype, device=dev)
         t2g_toff = torch.empty(Tx * Ty * Tz + 1, **i32) if keep_t2g else None
         start, stop = _timing_events(dev)
         start.record(cur)
@@ -180,7 +197,7 @@ def _forward(means3D, opacity, covariances, voxel_size, voxel_range, features, k
         if keep_t2g:
             csr = (torch.empty(M, **i32), torch.empty(M, **i32), t2g_toff)
             t2g = dict(csr=csr, plan=bplan, num_region_pairs=int(MR.value), vs=vs, vr=vr, dims=(X, Y, Z))
-        _lib.check(lib.g2v_forward_splat(n, C, _ptr(means), _ptr(op), _ptr(feats), vs, vr,
+        _lib.check(lib.g2v_forward_splat(n, C, _ptr(means), _ptr(op), _ptr(feats), fdt, vs, vr,
                                          _ptr(cov_inv), _ptr(lb), _ptr(ub), _ptr(g2t_offsets), M,
                                          _ptr(g2t_tile_ids), _ptr(density), _ptr(grid_feats),
                                          _ptr(csr[0]), _ptr(csr[1]), _ptr(csr[2]),
@@ -190,13 +207,13 @@ def _forward(means3D, opacity, covariances, voxel_size, voxel_range, features, k
         if keep_t2g:
             # the backward's outputs and workspace, allocated while the forward kernels run
             t2g["grads"] = (torch.empty(n, 3, **f32), torch.empty(n, 9, **f32), torch.empty(n, **f32),
-                            torch.empty(n, C, **f32))
+                            torch.empty(n, C, dtype=fdtype, device=dev))
             t2g["ws"] = torch.empty(max(1, lib.g2v_backward_workspace(n, C, M, t2g["num_region_pairs"], vs, vr)),
                                     dtype=torch.uint8, device=dev)
             # the backward's gradient-independent kernels, queued behind the forward (after its
             # stop event): they run while this thread waits and hands over to the backward
             if C > 0:
-                _lib.check(lib.g2v_backward_prepare(n, C, vs, vr, _ptr(lb), _ptr(ub), _ptr(feats), M,
+                _lib.check(lib.g2v_backward_prepare(n, C, vs, vr, _ptr(lb), _ptr(ub), _ptr(feats), fdt, M,
                                                     t2g["num_region_pairs"], _ptr(csr[0]), _ptr(csr[1]),
                                                     _ptr(bplan), _ptr(t2g["ws"]), t2g["ws"].numel(), stream),
                            "gaussian_voxelizer_forward (backward preparation)")
@@ -238,8 +255,9 @@ def _backward(grad_output, grad_feats_output, means3D, opacity, cov_inv, voxel_s
         _check_saved(grad_output, "grad_output", f32, dev)
     else:
         for t, name in ((grad_output, "grad_output"), (means3D, "means3D"), (opacity, "opacity"),
-                        (cov_inv, "cov_inv"), (density, "density"), (grid_feats, "grid_feats")):
+                        (cov_inv, "cov_inv"), (density, "density")):
             _check_saved(t, name, f32, dev)
+        _check_saved(grid_feats, "grid_feats", grid_feats.dtype if grid_feats.dtype in _FEAT_DTYPES else f32, dev)
         for t, name in ((valid_voxel_lb, "valid_voxel_lb"), (valid_voxel_ub, "valid_voxel_ub"),
                         (num_voxels_per_gaussian, "num_voxels_per_gaussian"), (g2t_offsets, "g2t_offsets"),
                         (g2t_tile_ids, "g2t_tile_ids")):
@@ -255,16 +273,21 @@ def _backward(grad_output, grad_feats_output, means3D, opacity, cov_inv, voxel_s
         raise RuntimeError(f"grad_output must be {(X, Y, Z)}, got {tuple(grad_output.shape)}")
     C = 0
     feats = gF = None
+    fdtype = f32
     if features is not None:
         if not trusted:
-            _check_saved(features, "features", f32, dev)
+            _check_saved(features, "features", features.dtype if features.dtype in _FEAT_DTYPES else f32, dev)
         C = features.shape[1]
+        fdtype = features.dtype
         if C > 0:
             feats = features
+            if grid_feats.dtype != fdtype:
+                raise RuntimeError(f"grid_feats ({grid_feats.dtype}) and features ({fdtype}) differ in type")
             _check_saved(grad_feats_output, "grad_feats_output", f32, dev)
             if tuple(grad_feats_output.shape) != (X, Y, Z, C) or tuple(grid_feats.shape) != (X, Y, Z, C):
                 raise RuntimeError("grad_feats_output and grid_feats must be (X, Y, Z, C)")
             gF = grad_feats_output
+    fdt = _FEAT_DTYPES[fdtype]
     M = g2t_tile_ids.numel()
 
     with _OnDevice(dev):
@@ -276,7 +299,7 @@ def _backward(grad_output, grad_feats_output, means3D, opacity, cov_inv, voxel_s
             grad_means = torch.empty(n, 3, dtype=f32, device=dev)
             grad_cov = torch.empty(n, 9, dtype=f32, device=dev)
             grad_opacity = torch.empty(n, dtype=f32, device=dev)
-            grad_feats = torch.empty(n, C, dtype=f32, device=dev)
+            grad_feats = torch.empty(n, C, dtype=fdtype, device=dev)
         if timed:
             start, stop = _timing_events(dev)
             start.record(cur)
@@ -299,7 +322,7 @@ def _backward(grad_output, grad_feats_output, means3D, opacity, cov_inv, voxel_s
         _lib.check(entry(n, C, _ptr(grad_output), _ptr(gF), _ptr(means3D), _ptr(opacity),
                                     _ptr(cov_inv), vs, vr, _ptr(valid_voxel_lb), _ptr(valid_voxel_ub),
                                     _ptr(num_voxels_per_gaussian), _ptr(g2t_offsets), _ptr(g2t_tile_ids),
-                                    M, MR, _ptr(density), _ptr(grid_feats), _ptr(feats),
+                                    M, MR, _ptr(density), _ptr(grid_feats), _ptr(feats), fdt,
                                     _ptr(grad_means), _ptr(grad_cov), _ptr(grad_opacity),
                                     _ptr(grad_feats), _ptr(csr[0]), _ptr(csr[1]), _ptr(csr[2]),
                                     _ptr(plan_ws), _ptr(ws), ws.numel(), stream),
@@ -353,7 +376,7 @@ def _forward_batched(means3D, opacity, covariances, voxel_size, voxel_range, fea
     feats = None
     C = 0
     if features is not None:
-        feats = _f32_input(features, "features")
+        feats = _feat_input(features, "features")
         if feats.dim() != 3 or tuple(feats.shape[:2]) != (B, n):
             raise RuntimeError(f"features must be (B, N, C) with B, N = {B}, {n}, got {tuple(feats.shape)}")
         C = feats.shape[2]
@@ -381,7 +404,9 @@ def _forward_batched(means3D, opacity, covariances, voxel_size, voxel_range, fea
         bplan = torch.empty(B, (bws + 255) // 256 * 256, dtype=torch.uint8, device=dev) if keep_t2g else None
         counts_dev = torch.empty(B, 2, dtype=torch.int64, device=dev)
         density = torch.empty(B, X, Y, Z, **f32)
-        grid_feats = torch.empty(B, X, Y, Z, C, **f32)
+        fdtype = torch.float32 if feats is None else feats.dtype
+        fdt = _FEAT_DTYPES[fdtype]
+        grid_feats = torch.empty(B, X, Y, Z, C, dtype=fdtype, device=dev)
         start, stop = _timing_events(dev)
         start.record(cur)
         for b in range(B):
@@ -407,7 +432,7 @@ def _forward_batched(means3D, opacity, covariances, voxel_size, voxel_range, fea
                 csr = (torch.empty(M, **i32), torch.empty(M, **i32), torch.empty(T + 1, **i32))
                 t2g = dict(csr=csr, plan=bplan[b], num_region_pairs=MR, vs=vs, vr=vr, dims=(X, Y, Z))
             fb = None if feats is None else feats[b]
-            _lib.check(lib.g2v_forward_splat(n, C, _ptr(means[b]), _ptr(op[b]), _ptr(fb), vs, vr,
+            _lib.check(lib.g2v_forward_splat(n, C, _ptr(means[b]), _ptr(op[b]), _ptr(fb), fdt, vs, vr,
                                              _ptr(cov_inv[b]), _ptr(lb[b]), _ptr(ub[b]), _ptr(g2t_offsets[b]), M,
                                              _ptr(g2t_tile_ids), _ptr(density[b]), _ptr(grid_feats[b]),
                                              _ptr(csr[0]), _ptr(csr[1]), _ptr(csr[2]), _ptr(ws2), ws2.numel(),
@@ -420,11 +445,11 @@ def _forward_batched(means3D, opacity, covariances, voxel_size, voxel_range, fea
             for b, (r, t2g) in enumerate(results):
                 M = r[7].numel()
                 t2g["grads"] = (torch.empty(n, 3, **f32), torch.empty(n, 9, **f32), torch.empty(n, **f32),
-                                torch.empty(n, C, **f32))
+                                torch.empty(n, C, dtype=fdtype, device=dev))
                 t2g["ws"] = torch.empty(max(1, lib.g2v_backward_workspace(n, C, M, t2g["num_region_pairs"], vs, vr)),
                                         dtype=torch.uint8, device=dev)
                 if C > 0:
-                    _lib.check(lib.g2v_backward_prepare(n, C, vs, vr, _ptr(lb[b]), _ptr(ub[b]), _ptr(feats[b]), M,
+                    _lib.check(lib.g2v_backward_prepare(n, C, vs, vr, _ptr(lb[b]), _ptr(ub[b]), _ptr(feats[b]), fdt, M,
                                                         t2g["num_region_pairs"], _ptr(t2g["csr"][0]),
                                                         _ptr(t2g["csr"][1]), _ptr(t2g["plan"]), _ptr(t2g["ws"]),
                                                         t2g["ws"].numel(), stream),

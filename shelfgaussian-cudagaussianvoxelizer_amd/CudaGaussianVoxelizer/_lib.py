@@ -12,6 +12,8 @@ LIB_NAME = "libg2v_hip.so"
 LIB_PATH = os.path.join(_HERE, LIB_NAME)
 
 G2V_OK = 0
+G2V_DTYPE_F32 = 0
+G2V_DTYPE_BF16 = 1
 _ERRORS = {1: "invalid argument", 2: "HIP runtime error", 3: "size limit exceeded"}
 
 # (name, restype, argtypes) of every exported entry point of include/g2v.h
@@ -28,16 +30,16 @@ SIGNATURES = {
                               _vp]),
     "g2v_forward_plan_async": (_i, [_i, _vp, _vp, _f3, _f3, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _sz, _vp, _vp]),
     "g2v_forward_splat_workspace": (_sz, [_i, _i, _ll, _f3, _f3]),
-    "g2v_forward_splat": (_i, [_i, _i, _vp, _vp, _vp, _f3, _f3, _vp, _vp, _vp, _vp, _ll, _vp, _vp,
+    "g2v_forward_splat": (_i, [_i, _i, _vp, _vp, _vp, _i, _f3, _f3, _vp, _vp, _vp, _vp, _ll, _vp, _vp,
                                _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "g2v_backward_plan_workspace": (_sz, [_i]),
     "g2v_backward_plan": (_i, [_i, _i, _f3, _f3, _vp, _vp, _vp, _sz, _llp, _vp]),
     "g2v_backward_workspace": (_sz, [_i, _i, _ll, _ll, _f3, _f3]),
     "g2v_backward": (_i, [_i, _i, _vp, _vp, _vp, _vp, _vp, _f3, _f3, _vp, _vp, _vp, _vp, _vp, _ll, _ll,
-                          _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
-    "g2v_backward_prepare": (_i, [_i, _i, _f3, _f3, _vp, _vp, _vp, _ll, _ll, _vp, _vp, _vp, _vp, _sz, _vp]),
+                          _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "g2v_backward_prepare": (_i, [_i, _i, _f3, _f3, _vp, _vp, _vp, _i, _ll, _ll, _vp, _vp, _vp, _vp, _sz, _vp]),
     "g2v_backward_prepared": (_i, [_i, _i, _vp, _vp, _vp, _vp, _vp, _f3, _f3, _vp, _vp, _vp, _vp, _vp, _ll, _ll,
-                                   _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+                                   _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "g2v_t2g_workspace": (_sz, [_i, _ll, _f3, _f3]),
     "g2v_build_t2g": (_i, [_i, _f3, _f3, _vp, _vp, _vp, _vp, _ll, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                            _vp, _sz, _vp]),

@@ -123,7 +123,8 @@ hipError_t launch_backward_density(const Grid& G, int n, const float* grad_densi
 constexpr int kBtKc = 32;                  // channels per chunk
 constexpr int kBtRowBytes = kBtKc * 4;     // bytes of one row's chunk (hi and lo)
 
-__global__ void __launch_bounds__(256) k_split_chunks(const float* __restrict__ src, int n, int C, int nchk,
+template <typename T>
+__global__ void __launch_bounds__(256) k_split_chunks(const T* __restrict__ src, int n, int C, int nchk,
                                                       __bf16* __restrict__ dst) {
     // one thread per 8 channels of a row (an octet of a chunk): 16-byte hi and lo stores
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -133,14 +134,14 @@ __global__ void __launch_bounds__(256) k_split_chunks(const float* __restrict__ 
     const int oc = (int)(i - r * noct);
     const int c = oc * 8;
     float v[8];
-    if (r < n && c + 8 <= C && ((uintptr_t)(src + r * C + c) & 15) == 0) {
+    if (sizeof(T) == 4 && r < n && c + 8 <= C && ((uintptr_t)(src + r * C + c) & 15) == 0) {
         const float4 a = *reinterpret_cast<const float4*>(src + r * C + c);
         const float4 b = *reinterpret_cast<const float4*>(src + r * C + c + 4);
         v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
         v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
     } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = (r < n && c + e < C) ? src[r * C + c + e] : 0.0f;
+        for (int e = 0; e < 8; ++e) v[e] = (r < n && c + e < C) ? feat_at(src, r * C + c + e) : 0.0f;
     }
     bf16x8 h, l;
     split8(v, h, l);
@@ -242,7 +243,7 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
     const float* __restrict__ cov_inv, const int* __restrict__ lb, const int* __restrict__ ub,
     const int* __restrict__ g2t_offsets, const int* __restrict__ toff,
     const int* __restrict__ sorted_gauss, int M, const float* __restrict__ density,
-    const float* __restrict__ grid_feats, const __bf16* __restrict__ fsp,
+    const void* __restrict__ grid_feats, int gdt, const __bf16* __restrict__ fsp,
     float* __restrict__ pair_partials, __bf16* __restrict__ wt) {
     __shared__ BtSmem sm;
     const int T = G.tiles[0] * G.tiles[1] * G.tiles[2];
@@ -277,9 +278,14 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             const int v = sm.vlin[r];
             if (v < 0) continue;
             const float* a = gF + (int64_t)v * C;
-            const float* b = grid_feats + (int64_t)v * C;
             float s = 0.0f;
-            for (int c = lane; c < C; c += 64) s += a[c] * b[c];
+            if (gdt == kDtBF16) {
+                const __bf16* b = static_cast<const __bf16*>(grid_feats) + (int64_t)v * C;
+                for (int c = lane; c < C; c += 64) s += a[c] * (float)b[c];
+            } else {
+                const float* b = static_cast<const float*>(grid_feats) + (int64_t)v * C;
+                for (int c = lane; c < C; c += 64) s += a[c] * b[c];
+            }
             s = wave_sum(s);
             if (lane == 0) sm.tv[r] = sm.D[r] >= kEps ? s : 0.0f;
         }
@@ -947,11 +953,13 @@ __global__ void __launch_bounds__(kBrThreads, 1) k_bwd_region(
 // ------------------------------------------------------------------------------------------
 constexpr int kBgThreads = 256;
 
+// OBF16: grad_features is stored as bfloat16 (rounded to nearest even), else float.
+template <bool OBF16>
 __global__ void __launch_bounds__(kBgThreads) k_bwd_gauss(
     int n, int C, int M, int MR, const int* __restrict__ g2t_offsets,
     const float* __restrict__ pair_partials, const int* __restrict__ g2r_offsets,
     const float* __restrict__ gpart, float* __restrict__ grad_means, float* __restrict__ grad_cov,
-    float* __restrict__ grad_opacity, float* __restrict__ grad_features) {
+    float* __restrict__ grad_opacity, void* __restrict__ grad_features_out) {
     __shared__ float red[4][kNumGrads];
     const int g = blockIdx.x;
     if (g >= n) return;
@@ -976,7 +984,16 @@ __global__ void __launch_bounds__(kBgThreads) k_bwd_gauss(
         write_grads(tot, g, grad_means, grad_cov, grad_opacity);
     }
     const int r0 = min(max(g2r_offsets[g], 0), MR), r1 = min(max(g2r_offsets[g + 1], r0), MR);
-    float* out = grad_features + (int64_t)g * C;
+    if constexpr (OBF16) {
+        __bf16* out = static_cast<__bf16*>(grad_features_out) + (int64_t)g * C;
+        for (int c = threadIdx.x; c < C; c += kBgThreads) {
+            float s = 0.0f;
+            for (int r = r0; r < r1; ++r) s += gpart[(int64_t)r * C + c];
+            out[c] = (__bf16)s;
+        }
+        return;
+    }
+    float* out = static_cast<float*>(grad_features_out) + (int64_t)g * C;
     if ((C & 3) == 0) {
         for (int c = threadIdx.x * 4; c < C; c += kBgThreads * 4) {
             float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1093,7 +1110,7 @@ size_t backward_feats_workspace(const Grid& G, int n, int C, int64_t M, int64_t 
     return carve_feats(nullptr, G, n, C, M, MR).bytes;
 }
 
-hipError_t launch_backward_prepare(const Grid& G, int n, int C, const float* features, const int* lb,
+hipError_t launch_backward_prepare(const Grid& G, int n, int C, const void* features, int fdt, const int* lb,
                                    const int* ub, int64_t M, const int* sorted_tiles, const int* sorted_gauss,
                                    const void* plan_ws, int64_t MR, void* ws, hipStream_t s) {
     if (n <= 0) return hipSuccess;
@@ -1106,8 +1123,12 @@ hipError_t launch_backward_prepare(const Grid& G, int n, int C, const float* fea
 
     // features as 32-channel chunks of bf16 hi/lo (B operand of phase A), plus a zero row
     const int64_t fcount = (int64_t)(n + 1) * nchk * (kBtKc / 8);   // one thread per 8 channels
-    G2V_LAUNCH(k_split_chunks, dim3((unsigned)ceil_div(fcount, 256)), dim3(256), 0, s, features, n, C, nchk,
-               b.fsp);
+    if (fdt == kDtBF16)
+        G2V_LAUNCH(k_split_chunks<__bf16>, dim3((unsigned)ceil_div(fcount, 256)), dim3(256), 0, s,
+                   static_cast<const __bf16*>(features), n, C, nchk, b.fsp);
+    else
+        G2V_LAUNCH(k_split_chunks<float>, dim3((unsigned)ceil_div(fcount, 256)), dim3(256), 0, s,
+                   static_cast<const float*>(features), n, C, nchk, b.fsp);
     // Region -> Gaussian CSR (pairs carry their G->R slot so partial rows land Gaussian-major) and
     // the row table of phase B
     if (MR > 0) {
@@ -1136,9 +1157,9 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
                                  const float* cov_inv, const int* lb, const int* ub,
                                  const int* g2t_offsets, int64_t M, const int* tile_offsets,
                                  const int* sorted_tiles, const int* sorted_gauss, const float* density,
-                                 const float* grid_feats, const float* features,
+                                 const void* grid_feats, const void* features, int fdt,
                                  const void* plan_ws, int64_t MR, float* grad_means, float* grad_cov,
-                                 float* grad_opacity, float* grad_features, void* ws, bool prepared,
+                                 float* grad_opacity, void* grad_features, void* ws, bool prepared,
                                  hipStream_t s) {
     if (n <= 0) return hipSuccess;
     const Regions RG = make_regions(G);
@@ -1148,8 +1169,8 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
     const FeatBufs b = carve_feats(ws, G, n, C, M, MR);
     const PlanBufs pb = carve_plan(const_cast<void*>(plan_ws), n);
     if (!prepared) {
-        const hipError_t e = launch_backward_prepare(G, n, C, features, lb, ub, M, sorted_tiles, sorted_gauss,
-                                                     plan_ws, MR, ws, s);
+        const hipError_t e = launch_backward_prepare(G, n, C, features, fdt, lb, ub, M, sorted_tiles,
+                                                     sorted_gauss, plan_ws, MR, ws, s);
         if (e != hipSuccess) return e;
     }
     if (M > 0 && T > 0) {
@@ -1157,11 +1178,11 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
         if ((C & 3) == 0 && ((uintptr_t)grad_feats & 15) == 0)   // 16-byte G loads
             G2V_LAUNCH(k_bwd_tile<true>, dim3(blocks), dim3(kBtThreads), 0, s, G, n, C, nchk, grad_density,
                        grad_feats, means, opacity, cov_inv, lb, ub, g2t_offsets, tile_offsets, sorted_gauss,
-                       (int)M, density, grid_feats, (const __bf16*)b.fsp, b.partials, b.wt);
+                       (int)M, density, grid_feats, fdt, (const __bf16*)b.fsp, b.partials, b.wt);
         else
             G2V_LAUNCH(k_bwd_tile<false>, dim3(blocks), dim3(kBtThreads), 0, s, G, n, C, nchk, grad_density,
                        grad_feats, means, opacity, cov_inv, lb, ub, g2t_offsets, tile_offsets, sorted_gauss,
-                       (int)M, density, grid_feats, (const __bf16*)b.fsp, b.partials, b.wt);
+                       (int)M, density, grid_feats, fdt, (const __bf16*)b.fsp, b.partials, b.wt);
     }
     if (MR > 0 && M > 0) {
         const int nchunk = (C + kBrCc - 1) / kBrCc;
@@ -1171,9 +1192,14 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
                    (int)M, (const int*)b.roff, (const int*)b.r_pairs_sorted, (const int*)b.table, (int)MR,
                    (const __bf16*)b.wt, b.gpart);
     }
-    G2V_LAUNCH(k_bwd_gauss, dim3(n), dim3(kBgThreads), 0, s, n, C, (int)M, (int)MR, g2t_offsets,
-               (const float*)b.partials, (const int*)pb.g2r_offsets, (const float*)b.gpart, grad_means,
-               grad_cov, grad_opacity, grad_features);
+    if (fdt == kDtBF16)
+        G2V_LAUNCH(k_bwd_gauss<true>, dim3(n), dim3(kBgThreads), 0, s, n, C, (int)M, (int)MR, g2t_offsets,
+                   (const float*)b.partials, (const int*)pb.g2r_offsets, (const float*)b.gpart, grad_means,
+                   grad_cov, grad_opacity, grad_features);
+    else
+        G2V_LAUNCH(k_bwd_gauss<false>, dim3(n), dim3(kBgThreads), 0, s, n, C, (int)M, (int)MR, g2t_offsets,
+                   (const float*)b.partials, (const int*)pb.g2r_offsets, (const float*)b.gpart, grad_means,
+                   grad_cov, grad_opacity, grad_features);
     return hipGetLastError();
 }
 

@@ -123,7 +123,7 @@ extern "C" {
 
 const char* g2v_last_error(void) { return g_err; }
 
-int g2v_abi_version(void) { return 6; }
+int g2v_abi_version(void) { return 7; }
 
 int g2v_grid_dims(const float voxel_size[3], const float voxel_range[6], int dims[3], int tiles[3]) {
     Grid G;
@@ -265,12 +265,14 @@ size_t g2v_forward_splat_workspace(int n, int feat_dim, long long num_pairs, con
 }
 
 int g2v_forward_splat(int n, int feat_dim, const float* means3D, const float* opacity,
-                      const float* features, const float voxel_size[3], const float voxel_range[6],
-                      const float* cov_inv, const int* valid_voxel_lb, const int* valid_voxel_ub,
-                      const int* g2t_offsets, long long num_pairs, int* g2t_tile_ids,
-                      float* density, float* grid_feats, int* t2g_tiles, int* t2g_gauss,
+                      const void* features, int feat_dtype, const float voxel_size[3],
+                      const float voxel_range[6], const float* cov_inv, const int* valid_voxel_lb,
+                      const int* valid_voxel_ub, const int* g2t_offsets, long long num_pairs,
+                      int* g2t_tile_ids, float* density, void* grid_feats, int* t2g_tiles, int* t2g_gauss,
                       int* t2g_offsets, void* workspace, size_t workspace_bytes, void* stream) {
     g_err[0] = 0;
+    if (feat_dtype != G2V_DTYPE_F32 && feat_dtype != G2V_DTYPE_BF16)
+        return fail(G2V_ERR_INVALID, "feat_dtype = %d (G2V_DTYPE_F32 or G2V_DTYPE_BF16)", feat_dtype);
     if (n < 0 || feat_dim < 0 || num_pairs < 0)
         return fail(G2V_ERR_INVALID, "n = %d, feat_dim = %d, num_pairs = %lld", n, feat_dim, num_pairs);
     if (num_pairs > 2147483647ll) return fail(G2V_ERR_LIMIT, "num_pairs = %lld exceeds int32", num_pairs);
@@ -303,7 +305,7 @@ int g2v_forward_splat(int n, int feat_dim, const float* means3D, const float* op
     if (feat_dim > 0)
         G2V_HIP(launch_forward_feats(G, feat_dim, means3D, opacity, cov_inv, valid_voxel_lb,
                                      valid_voxel_ub, b.tile_offsets, b.sorted_gauss, (int)num_pairs, n,
-                                     features, b.fpk, density, grid_feats, s));
+                                     features, feat_dtype, b.fpk, density, grid_feats, s));
     else
         G2V_HIP(launch_forward_density(G, means3D, opacity, cov_inv, valid_voxel_lb, valid_voxel_ub,
                                        b.tile_offsets, b.sorted_gauss, (int)num_pairs, density, s));
@@ -355,12 +357,14 @@ int backward_impl(int n, int feat_dim, const float* grad_density, const float* g
                   const float voxel_size[3], const float voxel_range[6], const int* valid_voxel_lb,
                   const int* valid_voxel_ub, const int* num_voxels_per_gaussian,
                   const int* g2t_offsets, const int* g2t_tile_ids, long long num_pairs,
-                  long long num_region_pairs, const float* density, const float* grid_feats,
-                  const float* features, float* grad_means, float* grad_cov, float* grad_opacity,
-                  float* grad_features, const int* t2g_tiles, const int* t2g_gauss,
+                  long long num_region_pairs, const float* density, const void* grid_feats,
+                  const void* features, int feat_dtype, float* grad_means, float* grad_cov, float* grad_opacity,
+                  void* grad_features, const int* t2g_tiles, const int* t2g_gauss,
                   const int* t2g_offsets, const void* plan_workspace, void* workspace,
                   size_t workspace_bytes, bool prepared, void* stream) {
     g_err[0] = 0;
+    if (feat_dtype != G2V_DTYPE_F32 && feat_dtype != G2V_DTYPE_BF16)
+        return fail(G2V_ERR_INVALID, "feat_dtype = %d (G2V_DTYPE_F32 or G2V_DTYPE_BF16)", feat_dtype);
     (void)num_voxels_per_gaussian;
     if (n < 0 || feat_dim < 0 || num_pairs < 0 || num_region_pairs < 0)
         return fail(G2V_ERR_INVALID, "n = %d, feat_dim = %d, num_pairs = %lld, num_region_pairs = %lld", n,
@@ -408,7 +412,7 @@ int backward_impl(int n, int feat_dim, const float* grad_density, const float* g
     G2V_HIP(launch_backward_feats(G, n, feat_dim, grad_density, grad_feats, means3D, opacity, cov_inv,
                                   valid_voxel_lb, valid_voxel_ub, g2t_offsets, num_pairs,
                                   b.tile_offsets, b.sorted_tiles, b.sorted_gauss, density, grid_feats, features,
-                                  plan_workspace, num_region_pairs, grad_means, grad_cov, grad_opacity,
+                                  feat_dtype, plan_workspace, num_region_pairs, grad_means, grad_cov, grad_opacity,
                                   grad_features, feats_ws, prepared, s));
     return G2V_OK;
 }
@@ -422,24 +426,26 @@ int g2v_backward(int n, int feat_dim, const float* grad_density, const float* gr
                  const float voxel_size[3], const float voxel_range[6], const int* valid_voxel_lb,
                  const int* valid_voxel_ub, const int* num_voxels_per_gaussian,
                  const int* g2t_offsets, const int* g2t_tile_ids, long long num_pairs,
-                 long long num_region_pairs, const float* density, const float* grid_feats,
-                 const float* features, float* grad_means, float* grad_cov, float* grad_opacity,
-                 float* grad_features, const int* t2g_tiles, const int* t2g_gauss,
+                 long long num_region_pairs, const float* density, const void* grid_feats,
+                 const void* features, int feat_dtype, float* grad_means, float* grad_cov, float* grad_opacity,
+                 void* grad_features, const int* t2g_tiles, const int* t2g_gauss,
                  const int* t2g_offsets, const void* plan_workspace, void* workspace,
                  size_t workspace_bytes, void* stream) {
     return backward_impl(n, feat_dim, grad_density, grad_feats, means3D, opacity, cov_inv, voxel_size,
                          voxel_range, valid_voxel_lb, valid_voxel_ub, num_voxels_per_gaussian, g2t_offsets,
-                         g2t_tile_ids, num_pairs, num_region_pairs, density, grid_feats, features, grad_means,
-                         grad_cov, grad_opacity, grad_features, t2g_tiles, t2g_gauss, t2g_offsets,
+                         g2t_tile_ids, num_pairs, num_region_pairs, density, grid_feats, features, feat_dtype,
+                         grad_means, grad_cov, grad_opacity, grad_features, t2g_tiles, t2g_gauss, t2g_offsets,
                          plan_workspace, workspace, workspace_bytes, false, stream);
 }
 
 int g2v_backward_prepare(int n, int feat_dim, const float voxel_size[3], const float voxel_range[6],
-                         const int* valid_voxel_lb, const int* valid_voxel_ub, const float* features,
-                         long long num_pairs, long long num_region_pairs, const int* t2g_tiles,
+                         const int* valid_voxel_lb, const int* valid_voxel_ub, const void* features,
+                         int feat_dtype, long long num_pairs, long long num_region_pairs, const int* t2g_tiles,
                          const int* t2g_gauss, const void* plan_workspace, void* workspace,
                          size_t workspace_bytes, void* stream) {
     g_err[0] = 0;
+    if (feat_dtype != G2V_DTYPE_F32 && feat_dtype != G2V_DTYPE_BF16)
+        return fail(G2V_ERR_INVALID, "feat_dtype = %d (G2V_DTYPE_F32 or G2V_DTYPE_BF16)", feat_dtype);
     if (n < 0 || feat_dim < 0 || num_pairs < 0 || num_region_pairs < 0)
         return fail(G2V_ERR_INVALID, "n = %d, feat_dim = %d, num_pairs = %lld, num_region_pairs = %lld", n,
                     feat_dim, num_pairs, num_region_pairs);
@@ -461,7 +467,7 @@ int g2v_backward_prepare(int n, int feat_dim, const float voxel_size[3], const f
     Carver c(workspace, workspace_bytes);
     c.take<char>(carve_splat(nullptr, n, num_pairs, G).bytes);
     void* feats_ws = c.take<char>(backward_feats_workspace(G, n, feat_dim, num_pairs, num_region_pairs));
-    G2V_HIP(launch_backward_prepare(G, n, feat_dim, features, valid_voxel_lb, valid_voxel_ub, num_pairs,
+    G2V_HIP(launch_backward_prepare(G, n, feat_dim, features, feat_dtype, valid_voxel_lb, valid_voxel_ub, num_pairs,
                                     t2g_tiles, t2g_gauss, plan_workspace, num_region_pairs, feats_ws,
                                     static_cast<hipStream_t>(stream)));
     return G2V_OK;
@@ -472,9 +478,9 @@ int g2v_backward_prepared(int n, int feat_dim, const float* grad_density, const 
                           const float voxel_size[3], const float voxel_range[6], const int* valid_voxel_lb,
                           const int* valid_voxel_ub, const int* num_voxels_per_gaussian,
                           const int* g2t_offsets, const int* g2t_tile_ids, long long num_pairs,
-                          long long num_region_pairs, const float* density, const float* grid_feats,
-                          const float* features, float* grad_means, float* grad_cov, float* grad_opacity,
-                          float* grad_features, const int* t2g_tiles, const int* t2g_gauss,
+                          long long num_region_pairs, const float* density, const void* grid_feats,
+                          const void* features, int feat_dtype, float* grad_means, float* grad_cov,
+                          float* grad_opacity, void* grad_features, const int* t2g_tiles, const int* t2g_gauss,
                           const int* t2g_offsets, const void* plan_workspace, void* workspace,
                           size_t workspace_bytes, void* stream) {
     if (feat_dim > 0 && n > 0 && num_pairs > 0 && !(t2g_tiles && t2g_gauss && t2g_offsets)) {
@@ -483,8 +489,8 @@ int g2v_backward_prepared(int n, int feat_dim, const float* grad_density, const 
     }
     return backward_impl(n, feat_dim, grad_density, grad_feats, means3D, opacity, cov_inv, voxel_size,
                          voxel_range, valid_voxel_lb, valid_voxel_ub, num_voxels_per_gaussian, g2t_offsets,
-                         g2t_tile_ids, num_pairs, num_region_pairs, density, grid_feats, features, grad_means,
-                         grad_cov, grad_opacity, grad_features, t2g_tiles, t2g_gauss, t2g_offsets,
+                         g2t_tile_ids, num_pairs, num_region_pairs, density, grid_feats, features, feat_dtype,
+                         grad_means, grad_cov, grad_opacity, grad_features, t2g_tiles, t2g_gauss, t2g_offsets,
                          plan_workspace, workspace, workspace_bytes, true, stream);
 }
 

@@ -10,6 +10,11 @@ constexpr int kVoxPerTile = 64;          // one voxel per lane of a wave64
 constexpr float kEps = 1e-6f;            // density clamp (reference include/utils.cuh:80)
 constexpr int kWave = 64;
 
+// Element type of the feature tensors (features, grid_feats, grad_features): the G2V_DTYPE_*
+// codes of the C ABI.
+constexpr int kDtF32 = 0;
+constexpr int kDtBF16 = 1;
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -237,6 +242,14 @@ __device__ __forceinline__ void load8(const float* __restrict__ p, int valid, bo
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = (i < valid) ? p[i] : 0.0f;
     }
+}
+
+
+// Feature element e of a row of type T, as float.
+template <typename T>
+__device__ __forceinline__ float feat_at(const T* __restrict__ p, int64_t e) {
+    if constexpr (sizeof(T) == 2) return (float)p[e];
+    else return p[e];
 }
 
 }  // namespace g2v

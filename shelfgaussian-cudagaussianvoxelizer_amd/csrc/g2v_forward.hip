@@ -67,7 +67,9 @@ hipError_t launch_forward_density(const Grid& G, const float* means, const float
 // ------------------------------------------------------------------------------------------
 // Features as packed bf16 pairs: low half = hi part, high half = lo part of the 2-term split.
 // ------------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) k_split_pack(const float* __restrict__ src, int n, int C, int Cp,
+// T: float or __bf16 features (a bf16 value splits into itself and a zero low part).
+template <typename T>
+__global__ void __launch_bounds__(256) k_split_pack(const T* __restrict__ src, int n, int C, int Cp,
                                                     uint32_t* __restrict__ dst) {
     // (n + 1) x Cp packed pairs: row n and columns >= C are zero, so padded K slots and channels
     // can be gathered without bounds checks.  One thread per 4 channels (16-byte store).
@@ -77,12 +79,17 @@ __global__ void __launch_bounds__(256) k_split_pack(const float* __restrict__ sr
     const int64_t r = i / nq;
     const int c = (int)(i - r * nq) * 4;
     float v[4];
-    if (r < n && c + 4 <= C && ((uintptr_t)(src + r * C + c) & 15) == 0) {
-        const float4 a = *reinterpret_cast<const float4*>(src + r * C + c);
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    if constexpr (sizeof(T) == 4) {
+        if (r < n && c + 4 <= C && ((uintptr_t)(src + r * C + c) & 15) == 0) {
+            const float4 a = *reinterpret_cast<const float4*>(src + r * C + c);
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = (r < n && c + e < C) ? (float)src[r * C + c + e] : 0.0f;
+        }
     } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = (r < n && c + e < C) ? src[r * C + c + e] : 0.0f;
+        for (int e = 0; e < 4; ++e) v[e] = (r < n && c + e < C) ? feat_at(src, r * C + c + e) : 0.0f;
     }
     uint4 o;
     uint32_t* op = reinterpret_cast<uint32_t*>(&o);
@@ -226,12 +233,14 @@ __device__ __forceinline__ void fwd_build_w(FwdSmem& sm, int j0, int kbeg, int k
     }
 }
 
+// OBF16: grid_feats is stored as bfloat16 (rounded to nearest even), else float.
+template <bool OBF16>
 __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
     Grid G, int C, const float* __restrict__ means, const float* __restrict__ opacity,
     const float* __restrict__ cov_inv, const int* __restrict__ lb, const int* __restrict__ ub,
     const int* __restrict__ toff, const int* __restrict__ sorted_gauss, int M, int n, int Cp,
     const uint32_t* __restrict__ fpk, float* __restrict__ density,
-    float* __restrict__ grid_feats) {
+    void* __restrict__ grid_feats_out) {
     __shared__ FwdSmem sm;
     const int T = G.tiles[0] * G.tiles[1] * G.tiles[2];
     const int tile = uniform(xcd_remap(blockIdx.x, gridDim.x));
@@ -350,7 +359,23 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
                         const float4 v = make_float4(acc[vb][0][e] * is[ii], acc[vb][1][e] * is[ii],
                                                      acc[vb][2][e] * is[ii], acc[vb][3][e] * is[ii]);
                         if (vs[ii] < 0) continue;
-                        float* dst = grid_feats + (int64_t)vs[ii] * C + c0;
+                        if constexpr (OBF16) {
+                            __bf16* dst = static_cast<__bf16*>(grid_feats_out) + (int64_t)vs[ii] * C + c0;
+                            if ((C & 3) == 0) {
+                                if (c0 < C) {
+                                    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+                                    const bf16x4 hv = {(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
+                                    *reinterpret_cast<bf16x4*>(dst) = hv;
+                                }
+                            } else {
+                                if (c0 + 0 < C) dst[0] = (__bf16)v.x;
+                                if (c0 + 1 < C) dst[1] = (__bf16)v.y;
+                                if (c0 + 2 < C) dst[2] = (__bf16)v.z;
+                                if (c0 + 3 < C) dst[3] = (__bf16)v.w;
+                            }
+                            continue;
+                        }
+                        float* dst = static_cast<float*>(grid_feats_out) + (int64_t)vs[ii] * C + c0;
                         if ((C & 3) == 0) {
                             // written once and not read again by the forward: streaming store
                             if (c0 < C) {
@@ -373,8 +398,8 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
 hipError_t launch_forward_feats(const Grid& G, int C, const float* means, const float* opacity,
                                 const float* cov_inv, const int* lb, const int* ub,
                                 const int* tile_offsets, const int* sorted_gauss, int M, int n,
-                                const float* features, uint32_t* fpk, float* density,
-                                float* grid_feats, hipStream_t s) {
+                                const void* features, int fdt, uint32_t* fpk, float* density,
+                                void* grid_feats, hipStream_t s) {
     const int T = G.tiles[0] * G.tiles[1] * G.tiles[2];
     if (T <= 0) return hipSuccess;
     if (C <= 0)
@@ -383,11 +408,20 @@ hipError_t launch_forward_feats(const Grid& G, int C, const float* means, const 
     const int Cp = packed_channels(C);
     const int64_t count = (int64_t)(n + 1) * Cp;
     if (count * 4 > (int64_t)UINT32_MAX) return hipErrorInvalidValue;   // byte offsets are 32-bit
-    G2V_LAUNCH(k_split_pack, dim3((unsigned)ceil_div(count / 4, 256)), dim3(256), 0, s, features, n, C, Cp, fpk);
+    const unsigned pblocks = (unsigned)ceil_div(count / 4, 256);
+    if (fdt == kDtBF16)
+        G2V_LAUNCH(k_split_pack<__bf16>, dim3(pblocks), dim3(256), 0, s, static_cast<const __bf16*>(features), n, C,
+                   Cp, fpk);
+    else
+        G2V_LAUNCH(k_split_pack<float>, dim3(pblocks), dim3(256), 0, s, static_cast<const float*>(features), n, C,
+                   Cp, fpk);
     const int blocks = (int)ceil_div(T, 8) * 8;
-    G2V_LAUNCH(k_fwd_feats, dim3(blocks), dim3(kFwdThreads), 0, s, G, C, means, opacity,
-                       cov_inv, lb, ub, tile_offsets, sorted_gauss, M, n, Cp, (const uint32_t*)fpk, density,
-                       grid_feats);
+    if (fdt == kDtBF16)
+        G2V_LAUNCH(k_fwd_feats<true>, dim3(blocks), dim3(kFwdThreads), 0, s, G, C, means, opacity, cov_inv, lb, ub,
+                   tile_offsets, sorted_gauss, M, n, Cp, (const uint32_t*)fpk, density, grid_feats);
+    else
+        G2V_LAUNCH(k_fwd_feats<false>, dim3(blocks), dim3(kFwdThreads), 0, s, G, C, means, opacity, cov_inv, lb,
+                   ub, tile_offsets, sorted_gauss, M, n, Cp, (const uint32_t*)fpk, density, grid_feats);
     return hipGetLastError();
 }
 

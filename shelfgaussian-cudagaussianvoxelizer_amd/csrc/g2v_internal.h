@@ -95,8 +95,8 @@ hipError_t launch_forward_density(const Grid& G, const float* means, const float
 hipError_t launch_forward_feats(const Grid& G, int C, const float* means, const float* opacity,
                                 const float* cov_inv, const int* lb, const int* ub,
                                 const int* tile_offsets, const int* sorted_gauss, int M, int n,
-                                const float* features, uint32_t* fpk, float* density,
-                                float* grid_feats, hipStream_t s);
+                                const void* features, int fdt, uint32_t* fpk, float* density,
+                                void* grid_feats, hipStream_t s);
 
 // ---- backward (g2v_backward.hip) ----------------------------------------------------------
 hipError_t launch_backward_density(const Grid& G, int n, const float* grad_density,
@@ -116,7 +116,7 @@ int* backward_plan_cells(const Grid& G, void* plan_ws, int n, int cell[3], void*
 size_t backward_feats_workspace(const Grid& G, int n, int C, int64_t M, int64_t MR);
 // The part of the feature backward that needs no upstream gradient: split features, the
 // Region -> Gaussian CSR and the row table of phase B (into ws).
-hipError_t launch_backward_prepare(const Grid& G, int n, int C, const float* features, const int* lb,
+hipError_t launch_backward_prepare(const Grid& G, int n, int C, const void* features, int fdt, const int* lb,
                                    const int* ub, int64_t M, const int* sorted_tiles, const int* sorted_gauss,
                                    const void* plan_ws, int64_t MR, void* ws, hipStream_t s);
 // prepared: launch_backward_prepare already ran on ws for the same Gaussians and CSR.
@@ -125,9 +125,9 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
                                  const float* cov_inv, const int* lb, const int* ub,
                                  const int* g2t_offsets, int64_t M, const int* tile_offsets,
                                  const int* sorted_tiles, const int* sorted_gauss, const float* density,
-                                 const float* grid_feats, const float* features,
+                                 const void* grid_feats, const void* features, int fdt,
                                  const void* plan_ws, int64_t MR, float* grad_means, float* grad_cov,
-                                 float* grad_opacity, float* grad_features, void* ws, bool prepared,
+                                 float* grad_opacity, void* grad_features, void* ws, bool prepared,
                                  hipStream_t s);
 
 // ---- feature cosine loss (g2v_cosine.hip) --------------------------------------------------

@@ -31,7 +31,7 @@ def test_header_symbols_exported():
 
 
 def test_abi_version():
-    assert _lib().load().g2v_abi_version() == 6
+    assert _lib().load().g2v_abi_version() == 7
 
 
 @pytest.mark.parametrize("vs,vr", [
@@ -65,17 +65,21 @@ def test_invalid_arguments_fail_before_any_launch():
                               ctypes.byref(M), None, 0, None, None)
     assert rc == 1 and b"n = -1" in lib.g2v_last_error()
     # too many pairs for the int32 CSR
-    rc = lib.g2v_forward_splat(1, 0, None, None, None, vs, vr, None, None, None, None, 1 << 31,
+    rc = lib.g2v_forward_splat(1, 0, None, None, None, 0, vs, vr, None, None, None, None, 1 << 31,
                                None, None, None, None, None, None, None, 0, None)
     assert rc == 3
+    # unknown feature type
+    rc = lib.g2v_forward_splat(1, 0, None, None, None, 7, vs, vr, None, None, None, None, 0,
+                               None, None, None, None, None, None, None, 0, None)
+    assert rc == 1 and b"feat_dtype" in lib.g2v_last_error()
     # missing workspace
-    rc = lib.g2v_forward_splat(0, 0, None, None, None, vs, vr, None, None, None, None, 0, None,
+    rc = lib.g2v_forward_splat(0, 0, None, None, None, 0, vs, vr, None, None, None, None, 0, None,
                                ctypes.c_void_p(16), None, None, None, None, None, 0, None)
     assert rc == 1 and b"workspace" in lib.g2v_last_error()
     # features requested without tensors
     rc = lib.g2v_backward(4, 8, ctypes.c_void_p(16), None, ctypes.c_void_p(16), ctypes.c_void_p(16),
                           ctypes.c_void_p(16), vs, vr, ctypes.c_void_p(16), ctypes.c_void_p(16), None,
-                          None, None, 0, 0, None, None, None, ctypes.c_void_p(16), ctypes.c_void_p(16),
+                          None, None, 0, 0, None, None, None, 0, ctypes.c_void_p(16), ctypes.c_void_p(16),
                           ctypes.c_void_p(16), None, None, None, None, None, None, 0, None)
     assert rc == 1 and b"feat_dim" in lib.g2v_last_error()
 
@@ -85,16 +89,16 @@ def test_backward_prepare_arguments_fail_before_any_launch():
     lib = L.load()
     vs, vr = L.floats([0.4] * 3), L.floats(W.RANGE_PAPER)
     one = ctypes.c_void_p(16)
-    rc = lib.g2v_backward_prepare(-1, 8, vs, vr, one, one, one, 0, 0, one, one, one, one, 1 << 20, None)
+    rc = lib.g2v_backward_prepare(-1, 8, vs, vr, one, one, one, 0, 0, 0, one, one, one, one, 1 << 20, None)
     assert rc == 1 and b"n = -1" in lib.g2v_last_error()
     # the forward's Tile->Gaussian CSR is required
-    rc = lib.g2v_backward_prepare(10, 8, vs, vr, one, one, one, 100, 10, None, None, one, one, 1 << 30, None)
+    rc = lib.g2v_backward_prepare(10, 8, vs, vr, one, one, one, 0, 100, 10, None, None, one, one, 1 << 30, None)
     assert rc == 1 and b"Tile->Gaussian" in lib.g2v_last_error()
-    rc = lib.g2v_backward_prepare(10, 8, vs, vr, one, one, one, 100, 10, one, one, one, one, 16, None)
+    rc = lib.g2v_backward_prepare(10, 8, vs, vr, one, one, one, 0, 100, 10, one, one, one, one, 16, None)
     assert rc == 1 and b"workspace" in lib.g2v_last_error()
-    assert lib.g2v_backward_prepare(10, 0, vs, vr, None, None, None, 0, 0, None, None, None, None, 0, None) == 0
+    assert lib.g2v_backward_prepare(10, 0, vs, vr, None, None, None, 0, 0, 0, None, None, None, None, 0, None) == 0
     rc = lib.g2v_backward_prepared(4, 8, one, one, one, one, one, vs, vr, one, one, None, one, one, 10, 5,
-                                   one, one, one, one, one, one, one, None, None, None, one, one, 1 << 30, None)
+                                   one, one, one, 0, one, one, one, one, None, None, None, one, one, 1 << 30, None)
     assert rc == 1 and b"Tile->Gaussian" in lib.g2v_last_error()
 
 
