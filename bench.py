@@ -238,6 +238,38 @@ def batched_leg(steps, warmup):
     return res
 
 
+def bf16_leg(md, od, cd, fd, gDd, gFd, vox, steps, warmup):
+    """The benchmark step with bfloat16 features (grid_feats and the feature gradient in bfloat16,
+    the all-ones upstream gradient of grid_feats in bfloat16 as autograd hands it over; the
+    module widens it to float32 as the reference's backward does)."""
+    import time
+    import torch
+    fb = fd.detach().to(torch.bfloat16).requires_grad_(True)
+    gFb = gFd.to(torch.bfloat16)
+    leaves = [t for t in (md, od, cd)] + [fb]
+
+    def step():
+        for t in leaves:
+            t.grad = None
+        density, grid_feats, stats = vox(md, od, cd, fb)
+        torch.autograd.backward([density, grid_feats], [gDd, gFb])
+        return stats
+
+    for _ in range(warmup):
+        step()
+    fwd = bwd = 0.0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        st = step()
+        fwd += float(st[0])
+        bwd += float(st[1])
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    return {"ms_per_step": round(ms, 4), "fwd_ms": round(fwd * 1e3 / steps, 4), "bwd_ms": round(bwd * 1e3 / steps, 4),
+            "note": "same workload with features, grid_feats and grad_features in bfloat16"}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -345,7 +377,9 @@ def main():
                         "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4), "traffic": traffic,
                         "algorithmic_bytes": bytes_k, "avg_ms": round(avg_s * 1e3, 4)}
 
-    covariance = batched = None
+    covariance = batched = bf16 = None
+    if not args.no_extra and C > 0:
+        bf16 = bf16_leg(md, od, cd, fd, gDd, gFd, vox, args.steps, args.warmup)
     if not args.no_extra:
         covariance = covariance_leg(_C, N, max(args.steps, 10))
         batched = batched_leg(max(args.steps, 5), args.warmup)
@@ -383,6 +417,7 @@ def main():
         "feats_cosine_loss": cosine,
         "covariance_from_scale_rotation": covariance,
         "batched_scenes": batched,
+        "bf16_features": bf16,
     }
     print(json.dumps(res), flush=True)
 

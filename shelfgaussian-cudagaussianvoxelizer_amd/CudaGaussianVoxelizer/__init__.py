@@ -159,13 +159,19 @@ class PyCudaGaussianVoxelizer(nn.Module):
     def forward(self, means3D, opacity, covariances=None, features=None, *, scales=None, rotations=None):
         """As the reference's forward; without covariances, they are built from ``scales`` (N, 3)
         and ``rotations`` (N, 4) (as ShelfGaussian's voxelizer does, reference
-        test/gaussian_voxelizer.py:168-169) and the gradients flow to those two.  With means3D of
+        test/gaussian_voxelizer.py:168-169) and the gradients flow to those two.  Covariances may
+        be float16 or bfloat16 and features bfloat16 (grid_feats and the feature gradient then
+        are bfloat16 too).  With means3D of
         shape (B, N, 3) (opacity (B, N[, 1]), covariances (B, N, 9), features (B, N, C)) the B
         scenes are voxelized in one call: density (B, X, Y, Z), grid_feats (B, X, Y, Z, C)."""
         if covariances is None:
             if scales is None or rotations is None:
                 raise RuntimeError("give covariances, or scales and rotations")
             covariances = covariance_from_scale_rotation(scales, rotations)
+        if covariances.dtype in (torch.float16, torch.bfloat16):
+            # reduced-precision covariances (ShelfGaussian records them in float16): widened on the
+            # device, the gradient flows back in their type
+            covariances = covariances.float()
         if means3D.dim() == 3:   # B scenes on this grid: (B,N,3) means, outputs gain a leading B
             return _CudaGaussianVoxelizeBatchedFunction.apply(means3D, opacity, covariances, self.voxel_size,
                                                               self.voxel_range, features)

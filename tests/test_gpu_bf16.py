@@ -156,3 +156,21 @@ def test_unsupported_feature_type_raises():
     md, od, cd, vs, vr = _args(w, m, o, c)
     with pytest.raises(RuntimeError):
         _C().gaussian_voxelizer_forward(md, od, cd, vs, vr, f.to(torch.float16).to(dev))
+
+
+def test_half_covariances_of_the_recorded_batch():
+    """The recorded batch keeps float16 covariances: the module widens them on the device, so the
+    outputs equal those of float32 covariances with the same values, and the covariance gradient
+    comes back in float16."""
+    from CudaGaussianVoxelizer import PyCudaGaussianVoxelizer
+    dev = torch.device("cuda")
+    m, o, c, vs, vr = W.mmdet_fixture()
+    c16 = c.to(torch.float16)   # exact: the fixture's covariances are float16 values
+    vox = PyCudaGaussianVoxelizer(voxel_size=list(vs), voxel_range=list(vr))
+    say("[bf16] float16 covariances")
+    ch = c16.to(dev).requires_grad_()
+    d16, _, _ = vox(m.to(dev), o.to(dev), ch)
+    d32, _, _ = vox(m.to(dev), o.to(dev), c.to(dev))
+    assert torch.equal(d16, d32)
+    d16.sum().backward()
+    assert ch.grad.dtype == torch.float16 and torch.isfinite(ch.grad.float()).all()
