@@ -395,20 +395,31 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             *reinterpret_cast<bf16x4*>(reinterpret_cast<char*>(&sm.alo[ab][sq >> 2][sv >> 5][L]) + (sq & 1) * 8) = lv;
         };
         // N block j of chunk ch (F stage st, A buffer ab) against both voxel blocks
-        auto mult = [&](int j, int st, int ab) {
-            if (j < nact) {
-                bf16x8 ah[2], al[2];
+        // Operands of one chunk step, A (both voxel blocks) and B (both N blocks), read from LDS
+        // together at the step's start, so that one LDS latency precedes the step's MFMAs (the B
+        // rows of an N block past the list hold stale values and are not multiplied).
+        struct StepOps {
+            bf16x8 ah[2], al[2], bh[kBtNbw], bl[kBtNbw];
+        };
+        auto load_ops = [&](int st, int ab, StepOps& o) {
 #pragma unroll
-                for (int m = 0; m < 2; ++m) {
-                    ah[m] = sm.ahi[ab][ks][m][lane];
-                    al[m] = sm.alo[ab][ks][m][lane];
-                }
+            for (int m = 0; m < 2; ++m) {
+                o.ah[m] = sm.ahi[ab][ks][m][lane];
+                o.al[m] = sm.alo[ab][ks][m][lane];
+            }
+#pragma unroll
+            for (int j = 0; j < kBtNbw; ++j) {
                 const int r = (ngrp + kBtGroups * j) * 32 + (lane & 31), sr = swz(r);
                 const unsigned char* rowp = &sm.u.frow[st][r * kBtRowBytes];
-                const bf16x8 bh = *reinterpret_cast<const bf16x8*>(rowp + (((2 * ks + h) ^ sr) << 4));
-                const bf16x8 bl = *reinterpret_cast<const bf16x8*>(rowp + (((4 + 2 * ks + h) ^ sr) << 4));
+                o.bh[j] = *reinterpret_cast<const bf16x8*>(rowp + (((2 * ks + h) ^ sr) << 4));
+                o.bl[j] = *reinterpret_cast<const bf16x8*>(rowp + (((4 + 2 * ks + h) ^ sr) << 4));
+            }
+        };
+        // N block j of the step against both voxel blocks
+        auto mult = [&](int j, const StepOps& o) {
+            if (j < nact) {
 #pragma unroll
-                for (int m = 0; m < 2; ++m) acc2[m][j] = mfma3_32x32x16(ah[m], al[m], bh, bl, acc2[m][j]);
+                for (int m = 0; m < 2; ++m) acc2[m][j] = mfma3_32x32x16(o.ah[m], o.al[m], o.bh[j], o.bl[j], acc2[m][j]);
             }
         };
 
@@ -435,12 +446,14 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             lds_barrier();
             for (int ch = 0; ch < nchk; ++ch) {
                 const int st = ch % kBtStages, ab = ch & 1;
-                mult(0, st, ab);
+                StepOps ops;
+                load_ops(st, ab, ops);
+                mult(0, ops);
                 __builtin_amdgcn_sched_barrier(0);
                 write_a(ch + 1, (ch + 1) % kBtStages, ab ^ 1);
                 dma_f(min(ch + 2, clast), (ch + 2) % kBtStages, 0, min(NF, kBtDma / 2));
                 __builtin_amdgcn_sched_barrier(0);
-                mult(1, st, ab);
+                mult(1, ops);
                 __builtin_amdgcn_sched_barrier(0);
                 dma_f(min(ch + 2, clast), (ch + 2) % kBtStages, kBtDma / 2, NF);
                 dma_g(min(ch + 3, clast), st);
