@@ -379,13 +379,17 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
         const int sv = threadIdx.x >> 3, sq = threadIdx.x & 7;
         const bool svok = sm.vlin[sv] >= 0;
         auto write_a = [&](int ch, int gs, int ab) {
-            const float4 x = *reinterpret_cast<const float4*>(&sm.graw[gs][sv][4 * (sq ^ swz(sv))]);
+            // one 16-byte LDS read, then the values past the row or the grid are cleared with bit
+            // masks (a select per value would let the compiler split the read into guarded parts)
+            const uint4 xr = *reinterpret_cast<const uint4*>(&sm.graw[gs][sv][4 * (sq ^ swz(sv))]);
             const int lim = svok ? min(max(C - (ch * kBtKc + 4 * sq), 0), 4) : 0;
             typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
             typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
             typedef float f32x2 __attribute__((ext_vector_type(2)));
-            const f32x2 x01 = {0 < lim ? x.x : 0.0f, 1 < lim ? x.y : 0.0f};
-            const f32x2 x23 = {2 < lim ? x.z : 0.0f, 3 < lim ? x.w : 0.0f};
+            const f32x2 x01 = {__uint_as_float(xr.x & (0u - (unsigned)(0 < lim))),
+                               __uint_as_float(xr.y & (0u - (unsigned)(1 < lim)))};
+            const f32x2 x23 = {__uint_as_float(xr.z & (0u - (unsigned)(2 < lim))),
+                               __uint_as_float(xr.w & (0u - (unsigned)(3 < lim)))};
             const bf16x2 h01 = __builtin_convertvector(x01, bf16x2), h23 = __builtin_convertvector(x23, bf16x2);
             const bf16x2 l01 = __builtin_convertvector(x01 - __builtin_convertvector(h01, f32x2), bf16x2);
             const bf16x2 l23 = __builtin_convertvector(x23 - __builtin_convertvector(h23, f32x2), bf16x2);
