@@ -881,7 +881,7 @@ __device__ __forceinline__ void br_tiles(BrSmem& sm, const Grid& G, int C, int c
 // One pass of phase B over rows rp .. rp + prow - 1 of the region (prow <= 384): stages the
 // pass's row table and G->R slots, then runs the tile loop with this wave's block count.
 __device__ __forceinline__ void br_pass(BrSmem& sm, const Grid& G, int C, int c0, int ntl, int rp,
-                                        int KR, int M, int jr0, const float* __restrict__ gF,
+                                        int KR, int M, int MR, int jr0, const float* __restrict__ gF,
                                         const int* __restrict__ r_pairs, const int* __restrict__ table,
                                         const __bf16* __restrict__ wt, float* __restrict__ gpart) {
     const int wave = threadIdx.x >> 6;
@@ -897,13 +897,15 @@ __device__ __forceinline__ void br_pass(BrSmem& sm, const Grid& G, int C, int c0
         for (int e0 = 0; e0 < kPer; ++e0) {
             const int e = threadIdx.x + e0 * kBrThreads;
             const int r = min(rp + e / kBrSlots, KR - 1);
-            tv[e0] = table[(int64_t)(jr0 + r) * kBrSlots + e % kBrSlots];
+            // clamped: a row table or slot list from a workspace that was not prepared for these
+            // Gaussians cannot send a load or a store outside the weights or the partial rows
+            tv[e0] = min(max(table[(int64_t)(jr0 + r) * kBrSlots + e % kBrSlots], 0), M);
         }
         int rs[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int r = threadIdx.x + h * kBrThreads;
-            rs[h] = r < kBrPass ? r_pairs[jr0 + min(rp + r, KR - 1)] : 0;
+            rs[h] = r < kBrPass ? min(max(r_pairs[jr0 + min(rp + r, KR - 1)], 0), MR - 1) : 0;
         }
 #pragma unroll
         for (int e0 = 0; e0 < kPer; ++e0) {
@@ -962,7 +964,7 @@ __global__ void __launch_bounds__(kBrThreads, 1) k_bwd_region(
     if (ntl == 0) return;   // every row stays zero: phase C reads no partial row of this region
 
     for (int rp = 0; rp < KR; rp += kBrPass)
-        br_pass(sm, G, C, c0, ntl, rp, KR, M, jr0, gF, r_pairs, table, wt, gpart);
+        br_pass(sm, G, C, c0, ntl, rp, KR, M, MR, jr0, gF, r_pairs, table, wt, gpart);
 }
 
 // ------------------------------------------------------------------------------------------
