@@ -236,7 +236,8 @@ __device__ __forceinline__ void lds_barrier() {
     __asm__ __volatile__("" ::: "memory");
 }
 
-template <bool VEC>
+// FEX: the features are bfloat16 values (the B operand's low part is zero).
+template <bool VEC, bool FEX>
 __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
     Grid G, int n, int C, int nchk, const float* __restrict__ gD, const float* __restrict__ gF,
     const float* __restrict__ means, const float* __restrict__ opacity,
@@ -423,7 +424,8 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
         auto mult = [&](int j, const StepOps& o) {
             if (j < nact) {
 #pragma unroll
-                for (int m = 0; m < 2; ++m) acc2[m][j] = mfma3_32x32x16(o.ah[m], o.al[m], o.bh[j], o.bl[j], acc2[m][j]);
+                for (int m = 0; m < 2; ++m)
+                    acc2[m][j] = mfma_split_32x32x16<false, FEX>(o.ah[m], o.al[m], o.bh[j], o.bl[j], acc2[m][j]);
             }
         };
 
@@ -1194,14 +1196,19 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
     }
     if (M > 0 && T > 0) {
         const int blocks = (int)ceil_div(T, 8) * 8;
-        if ((C & 3) == 0 && ((uintptr_t)grad_feats & 15) == 0)   // 16-byte G loads
-            G2V_LAUNCH(k_bwd_tile<true>, dim3(blocks), dim3(kBtThreads), 0, s, G, n, C, nchk, grad_density,
-                       grad_feats, means, opacity, cov_inv, lb, ub, g2t_offsets, tile_offsets, sorted_gauss,
-                       (int)M, density, grid_feats, fdt, (const __bf16*)b.fsp, b.partials, b.wt);
-        else
-            G2V_LAUNCH(k_bwd_tile<false>, dim3(blocks), dim3(kBtThreads), 0, s, G, n, C, nchk, grad_density,
-                       grad_feats, means, opacity, cov_inv, lb, ub, g2t_offsets, tile_offsets, sorted_gauss,
-                       (int)M, density, grid_feats, fdt, (const __bf16*)b.fsp, b.partials, b.wt);
+        const bool vec = (C & 3) == 0 && ((uintptr_t)grad_feats & 15) == 0;   // 16-byte G loads
+#define G2V_BT(V, F)                                                                                          \
+    G2V_LAUNCH((k_bwd_tile<V, F>), dim3(blocks), dim3(kBtThreads), 0, s, G, n, C, nchk, grad_density, grad_feats, \
+               means, opacity, cov_inv, lb, ub, g2t_offsets, tile_offsets, sorted_gauss, (int)M, density,        \
+               grid_feats, fdt, (const __bf16*)b.fsp, b.partials, b.wt)
+        if (fdt == kDtBF16) {
+            if (vec) G2V_BT(true, true);
+            else G2V_BT(false, true);
+        } else {
+            if (vec) G2V_BT(true, false);
+            else G2V_BT(false, false);
+        }
+#undef G2V_BT
     }
     if (MR > 0 && M > 0) {
         const int nchunk = (C + kBrCc - 1) / kBrCc;

@@ -181,6 +181,18 @@ __device__ __forceinline__ f32x16 mfma3_32x32x16(const bf16x8& ah, const bf16x8&
     return acc;
 }
 
+// The product with terms known to be zero left out: BEX, B's low part is zero (B holds
+// bfloat16 values exactly); AEX, A's low part is zero.  The remaining terms are added in the same
+// order, so the result equals the three-term product's (an exact zero term changes nothing but
+// the sign of a zero sum).
+template <bool AEX, bool BEX>
+__device__ __forceinline__ f32x16 mfma_split_32x32x16(const bf16x8& ah, const bf16x8& al, const bf16x8& bh,
+                                                      const bf16x8& bl, f32x16 acc) {
+    if constexpr (!AEX) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh, acc, 0, 0, 0);
+    if constexpr (!BEX) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl, acc, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh, acc, 0, 0, 0);
+}
+
 // Same three-term product on the 16 x 16 x 32 shape.  Operand lanes: A row l%16, k 8(l/16)+i;
 // B column l%16, k 8(l/16)+i; D element i at row 4(l/16)+i, column l%16.
 __device__ __forceinline__ f32x4 mfma3_16x16x32(const bf16x8& ah, const bf16x8& al, const bf16x8& bh,
@@ -189,6 +201,14 @@ __device__ __forceinline__ f32x4 mfma3_16x16x32(const bf16x8& ah, const bf16x8& 
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
     return acc;
+}
+
+template <bool AEX, bool BEX>
+__device__ __forceinline__ f32x4 mfma_split_16x16x32(const bf16x8& ah, const bf16x8& al, const bf16x8& bh,
+                                                    const bf16x8& bl, f32x4 acc) {
+    if constexpr (!AEX) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
+    if constexpr (!BEX) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
 }
 
 // v of lane l ^ m within each 32-lane half, for m in {1, 2, 4, 8, 16}: DPP quad permutes for 1

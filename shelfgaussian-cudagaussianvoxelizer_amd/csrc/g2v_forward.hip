@@ -302,8 +302,9 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
                         for (int i = 0; i < 8; ++i) q[i] = u[i][cb];
                         bf16x8 bh, bl;
                         unpack8(q, bh, bl);
-                        acc[0][cb] = mfma3_32x32x16(ah0, al0, bh, bl, acc[0][cb]);
-                        acc[1][cb] = mfma3_32x32x16(ah1, al1, bh, bl, acc[1][cb]);
+                        // bfloat16 features split into themselves and a zero low part
+                        acc[0][cb] = mfma_split_32x32x16<false, OBF16>(ah0, al0, bh, bl, acc[0][cb]);
+                        acc[1][cb] = mfma_split_32x32x16<false, OBF16>(ah1, al1, bh, bl, acc[1][cb]);
                     }
                 };
                 // loads and steps are unconditional (ksteps is even, the prefetch index is

@@ -92,11 +92,14 @@ int g2v_profile_collect(void) {
     for (auto& p : g_pending) {
         float ms = 0.0f;
         if (hipEventSynchronize(p.b) != hipSuccess || hipEventElapsedTime(&ms, p.a, p.b) != hipSuccess) ms = 0.0f;
+        // a template kernel is named in parentheses at its launch: "(k<a, b>)" -> "k<a, b>"
+        std::string nm(p.name);
+        if (nm.size() >= 2 && nm.front() == '(' && nm.back() == ')') nm = nm.substr(1, nm.size() - 2);
         Total* t = nullptr;
         for (auto& x : g_totals)
-            if (x.name == p.name) { t = &x; break; }
+            if (x.name == nm) { t = &x; break; }
         if (!t) {
-            g_totals.push_back(Total{p.name});
+            g_totals.push_back(Total{nm});
             t = &g_totals.back();
         }
         t->launches += 1;
