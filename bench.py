@@ -240,8 +240,8 @@ def batched_leg(steps, warmup):
 
 def bf16_leg(md, od, cd, fd, gDd, gFd, vox, steps, warmup):
     """The benchmark step with bfloat16 features (grid_feats and the feature gradient in bfloat16,
-    the all-ones upstream gradient of grid_feats in bfloat16 as autograd hands it over; the
-    module widens it to float32 as the reference's backward does)."""
+    the all-ones upstream gradient of grid_feats in bfloat16 as autograd hands it over and as the
+    backward multiplies it)."""
     import time
     import torch
     fb = fd.detach().to(torch.bfloat16).requires_grad_(True)

@@ -104,7 +104,9 @@ int g2v_backward_plan(int n, int feat_dim, const float voxel_size[3], const floa
                       size_t plan_workspace_bytes, long long* num_region_pairs, void* stream);
 
 /* g2v_backward: writes grad_means (N,3), grad_cov (N,9, symmetric), grad_opacity (N,) and, when
- * feat_dim > 0, grad_features (N,feat_dim).  grad_feats/grid_feats/features may be NULL when
+ * feat_dim > 0, grad_features (N,feat_dim).  grad_feats (X,Y,Z,feat_dim), grid_feats, features
+ * and grad_features are all of feat_dtype (float32 or bfloat16; a bfloat16 grad_feats is
+ * multiplied as it is, with float32 accumulation).  grad_feats/grid_feats/features may be NULL when
  * feat_dim == 0.  plan_workspace is the one given to g2v_backward_plan.  t2g_tiles, t2g_gauss
  * and t2g_offsets may carry the Tile->Gaussian CSR written by g2v_forward_splat for the same
  * Gaussians (all three non-NULL); with NULL it is rebuilt from g2t_offsets/g2t_tile_ids, as the
@@ -112,7 +114,7 @@ int g2v_backward_plan(int n, int feat_dim, const float voxel_size[3], const floa
  * deterministic. */
 size_t g2v_backward_workspace(int n, int feat_dim, long long num_pairs, long long num_region_pairs,
                               const float voxel_size[3], const float voxel_range[6]);
-int g2v_backward(int n, int feat_dim, const float* grad_density, const float* grad_feats,
+int g2v_backward(int n, int feat_dim, const float* grad_density, const void* grad_feats,
                  const float* means3D, const float* opacity, const float* cov_inv,
                  const float voxel_size[3], const float voxel_range[6],
                  const int* valid_voxel_lb, const int* valid_voxel_ub,
@@ -140,7 +142,7 @@ int g2v_backward_prepare(int n, int feat_dim, const float voxel_size[3], const f
                          int feat_dtype, long long num_pairs, long long num_region_pairs, const int* t2g_tiles,
                          const int* t2g_gauss, const void* plan_workspace, void* workspace,
                          size_t workspace_bytes, void* stream);
-int g2v_backward_prepared(int n, int feat_dim, const float* grad_density, const float* grad_feats,
+int g2v_backward_prepared(int n, int feat_dim, const float* grad_density, const void* grad_feats,
                           const float* means3D, const float* opacity, const float* cov_inv,
                           const float voxel_size[3], const float voxel_range[6],
                           const int* valid_voxel_lb, const int* valid_voxel_ub,

@@ -283,7 +283,12 @@ def _backward(grad_output, grad_feats_output, means3D, opacity, cov_inv, voxel_s
             feats = features
             if grid_feats.dtype != fdtype:
                 raise RuntimeError(f"grid_feats ({grid_feats.dtype}) and features ({fdtype}) differ in type")
-            _check_saved(grad_feats_output, "grad_feats_output", f32, dev)
+            # the upstream feature gradient is taken in the features' type (a float32 gradient of
+            # bfloat16 features is rounded to bfloat16, a bfloat16 one of float32 features widened)
+            if isinstance(grad_feats_output, torch.Tensor) and grad_feats_output.dtype != fdtype \
+                    and grad_feats_output.dtype in _FEAT_DTYPES:
+                grad_feats_output = grad_feats_output.to(fdtype).contiguous()
+            _check_saved(grad_feats_output, "grad_feats_output", fdtype, dev)
             if tuple(grad_feats_output.shape) != (X, Y, Z, C) or tuple(grid_feats.shape) != (X, Y, Z, C):
                 raise RuntimeError("grad_feats_output and grid_feats must be (X, Y, Z, C)")
             gF = grad_feats_output

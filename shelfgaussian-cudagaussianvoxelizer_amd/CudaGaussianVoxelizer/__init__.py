@@ -45,7 +45,7 @@ class _CudaGaussianVoxelizeFunction(torch.autograd.Function):
         (means32, op32, voxsz32, voxrg32, cov_inv, valid_voxel_lb, valid_voxel_ub, num_valid_voxel,
          g2t_offsets, g2t_tile_ids, density, grid_feats, features, stats) = ctx.saved_tensors
         gout32 = grad_density_output.to(torch.float32).contiguous()
-        grad_feats_output = grad_feats_output.to(torch.float32).contiguous()
+        grad_feats_output = grad_feats_output.to(grid_feats.dtype).contiguous()   # the features' type
         means32 = means32.detach().contiguous()
         op32 = op32.detach().reshape(-1).contiguous()
         feats = None if features is None else features.detach().contiguous()
@@ -107,7 +107,7 @@ class _CudaGaussianVoxelizeBatchedFunction(torch.autograd.Function):
         means3D, opacity, features, stats = ctx.saved_tensors
         B, n = means3D.shape[0], means3D.shape[1]
         gD = grad_density_output.to(torch.float32).contiguous()
-        gF = grad_feats_output.to(torch.float32).contiguous()
+        gF = grad_feats_output.to(torch.float32 if features is None else features.dtype).contiguous()
         m32 = means3D.detach().contiguous()
         o32 = opacity.detach().reshape(B, n).contiguous()
         feats = None if features is None else features.detach().contiguous()

@@ -236,10 +236,11 @@ __device__ __forceinline__ void lds_barrier() {
     __asm__ __volatile__("" ::: "memory");
 }
 
-// FEX: the features are bfloat16 values (the B operand's low part is zero).
-template <bool VEC, bool FEX>
+// BF: features and grad_feats are bfloat16 (the A and B operands' low parts are zero, and the
+// chunks of grad_feats are staged as bfloat16).
+template <bool VEC, bool BF>
 __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
-    Grid G, int n, int C, int nchk, const float* __restrict__ gD, const float* __restrict__ gF,
+    Grid G, int n, int C, int nchk, const float* __restrict__ gD, const void* __restrict__ gF_,
     const float* __restrict__ means, const float* __restrict__ opacity,
     const float* __restrict__ cov_inv, const int* __restrict__ lb, const int* __restrict__ ub,
     const int* __restrict__ g2t_offsets, const int* __restrict__ toff,
@@ -271,6 +272,8 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
     }
     __syncthreads();
 
+    typedef typename std::conditional<BF, __bf16, float>::type GT;   // element of grad_feats
+    const GT* gF = static_cast<const GT*>(gF_);
     // Lists longer than one pass: t_v = sum_c gF_vc F_vc straight from grid_feats.
     const bool multi = Ng > kBtPass;
     if (multi) {
@@ -278,14 +281,14 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             const int r = wave * 8 + k;
             const int v = sm.vlin[r];
             if (v < 0) continue;
-            const float* a = gF + (int64_t)v * C;
+            const GT* a = gF + (int64_t)v * C;
             float s = 0.0f;
             if (gdt == kDtBF16) {
                 const __bf16* b = static_cast<const __bf16*>(grid_feats) + (int64_t)v * C;
-                for (int c = lane; c < C; c += 64) s += a[c] * (float)b[c];
+                for (int c = lane; c < C; c += 64) s += (float)a[c] * (float)b[c];
             } else {
                 const float* b = static_cast<const float*>(grid_feats) + (int64_t)v * C;
-                for (int c = lane; c < C; c += 64) s += a[c] * b[c];
+                for (int c = lane; c < C; c += 64) s += (float)a[c] * b[c];
             }
             s = wave_sum(s);
             if (lane == 0) sm.tv[r] = sm.D[r] >= kEps ? s : 0.0f;
@@ -297,23 +300,34 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
     // slot p ^ swz(v), so that the A-operand reads (8 or 16 consecutive rows per LDS cycle) are
     // free of bank conflicts.  VEC: one 16-byte load per lane, lane = (row, slot); otherwise four 4-byte
     // loads per lane, each covering two rows.
-    constexpr int kNG = VEC ? 1 : 4;   // G loads per wave per chunk
-    const float* gsrc[kNG];
-    int gcoff[kNG];   // channel of this lane's load within a chunk
+    // BF: a chunk row is 64 bytes of bfloat16; with VEC (C % 8 == 0, 16-byte aligned rows) lanes
+    // 0..31 of a wave load its 8 rows as 16-byte pieces at slot = piece (stage rows of 64 bytes,
+    // read whole by write_a); without VEC the A operand is loaded by write_a itself (no staging).
+    constexpr int kNG = BF ? (VEC ? 1 : 0) : (VEC ? 1 : 4);   // G loads per wave per chunk
+    constexpr int kNGs = kNG > 0 ? kNG : 1;
+    const GT* gsrc[kNGs];
+    int gcoff[kNGs];   // channel of this lane's load within a chunk
 #pragma unroll
     for (int k = 0; k < kNG; ++k) {
-        const int v = VEC ? wave * 8 + (lane >> 3) : wave * 8 + 2 * k + (lane >> 5);
+        const int v = BF ? wave * 8 + ((lane & 31) >> 2)
+                         : (VEC ? wave * 8 + (lane >> 3) : wave * 8 + 2 * k + (lane >> 5));
         gsrc[k] = gF + (int64_t)max(sm.vlin[v], 0) * C;
-        gcoff[k] = VEC ? 4 * ((lane & 7) ^ swz(v)) : 4 * (((lane & 31) >> 2) ^ swz(v)) + (lane & 3);
+        gcoff[k] = BF ? 8 * (lane & 3)
+                      : (VEC ? 4 * ((lane & 7) ^ swz(v)) : 4 * (((lane & 31) >> 2) ^ swz(v)) + (lane & 3));
     }
     auto dma_g = [&](int chunk, int stage) {
 #pragma unroll
         for (int k = 0; k < kNG; ++k) {
-            if (VEC)
+            if constexpr (BF) {
+                if (lane < 32)
+                    dma16_nt(gsrc[k] + min(chunk * kBtKc + gcoff[k], C - 8),
+                             uniform(lds_addr(reinterpret_cast<char*>(&sm.graw[stage][0][0]) + wave * 8 * 64)));
+            } else if (VEC) {
                 dma16_nt(gsrc[k] + min(chunk * kBtKc + gcoff[k], C - 4), uniform(lds_addr(&sm.graw[stage][wave * 8][0])));
-            else
+            } else {
                 dma4_nt(gsrc[k] + min(chunk * kBtKc + gcoff[k], C - 1),
                      uniform(lds_addr(&sm.graw[stage][wave * 8 + 2 * k][0])));
+            }
         }
     };
 
@@ -380,13 +394,38 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
         const int sv = threadIdx.x >> 3, sq = threadIdx.x & 7;
         const bool svok = sm.vlin[sv] >= 0;
         auto write_a = [&](int ch, int gs, int ab) {
-            // one 16-byte LDS read, then the values past the row or the grid are cleared with bit
-            // masks (a select per value would let the compiler split the read into guarded parts)
-            const uint4 xr = *reinterpret_cast<const uint4*>(&sm.graw[gs][sv][4 * (sq ^ swz(sv))]);
             const int lim = svok ? min(max(C - (ch * kBtKc + 4 * sq), 0), 4) : 0;
             typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
             typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
             typedef float f32x2 __attribute__((ext_vector_type(2)));
+            const int L = ((sq >> 1) & 1) * 32 + (sv & 31);
+            if constexpr (BF) {
+                // bfloat16 values: the high part is the value itself, the low part zero (not stored:
+                // the MFMAs leave that term out)
+                unsigned short e[4];
+                if constexpr (VEC) {
+                    const uint2 xr = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(&sm.graw[gs][0][0]) +
+                                                                     sv * 64 + sq * 8);
+                    e[0] = (unsigned short)(xr.x & 0xffffu);
+                    e[1] = (unsigned short)(xr.x >> 16);
+                    e[2] = (unsigned short)(xr.y & 0xffffu);
+                    e[3] = (unsigned short)(xr.y >> 16);
+                } else {
+                    const unsigned short* row =
+                        reinterpret_cast<const unsigned short*>(gF + (int64_t)max(sm.vlin[sv], 0) * C);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) e[i] = row[min(ch * kBtKc + 4 * sq + i, C - 1)];
+                }
+                bf16x4 hv;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    hv[i] = __builtin_bit_cast(__bf16, (unsigned short)(e[i] & (0u - (unsigned)(i < lim))));
+                *reinterpret_cast<bf16x4*>(reinterpret_cast<char*>(&sm.ahi[ab][sq >> 2][sv >> 5][L]) + (sq & 1) * 8) = hv;
+                return;
+            }
+            // one 16-byte LDS read, then the values past the row or the grid are cleared with bit
+            // masks (a select per value would let the compiler split the read into guarded parts)
+            const uint4 xr = *reinterpret_cast<const uint4*>(&sm.graw[gs][sv][4 * (sq ^ swz(sv))]);
             const f32x2 x01 = {__uint_as_float(xr.x & (0u - (unsigned)(0 < lim))),
                                __uint_as_float(xr.y & (0u - (unsigned)(1 < lim)))};
             const f32x2 x23 = {__uint_as_float(xr.z & (0u - (unsigned)(2 < lim))),
@@ -395,7 +434,6 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             const bf16x2 l01 = __builtin_convertvector(x01 - __builtin_convertvector(h01, f32x2), bf16x2);
             const bf16x2 l23 = __builtin_convertvector(x23 - __builtin_convertvector(h23, f32x2), bf16x2);
             const bf16x4 hv = {h01[0], h01[1], h23[0], h23[1]}, lv = {l01[0], l01[1], l23[0], l23[1]};
-            const int L = ((sq >> 1) & 1) * 32 + (sv & 31);
             *reinterpret_cast<bf16x4*>(reinterpret_cast<char*>(&sm.ahi[ab][sq >> 2][sv >> 5][L]) + (sq & 1) * 8) = hv;
             *reinterpret_cast<bf16x4*>(reinterpret_cast<char*>(&sm.alo[ab][sq >> 2][sv >> 5][L]) + (sq & 1) * 8) = lv;
         };
@@ -425,7 +463,7 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             if (j < nact) {
 #pragma unroll
                 for (int m = 0; m < 2; ++m)
-                    acc2[m][j] = mfma_split_32x32x16<false, FEX>(o.ah[m], o.al[m], o.bh[j], o.bl[j], acc2[m][j]);
+                    acc2[m][j] = mfma_split_32x32x16<BF, BF>(o.ah[m], o.al[m], o.bh[j], o.bl[j], acc2[m][j]);
             }
         };
 
@@ -719,16 +757,20 @@ struct BrSmem {
 // Coordinates are clamped into the grid, so every load stays inside gF (the descriptor's range
 // ends at gF's end as well); bit i + 8k of the returned mask marks the values that are real.
 // Offsets need 16 * Y * Z * C < 2^32 (checked on the host).
+// GB: gF holds bfloat16 values (2-byte loads, widened exactly).
+template <bool GB>
 __device__ __forceinline__ unsigned br_load_tile(const Grid& G, int C, int c0, int t, int sc, int so,
-                                                 const float* __restrict__ gF, float (&v)[2][8]) {
+                                                 const void* __restrict__ gF, float (&v)[2][8]) {
+    constexpr int kEs = GB ? 2 : 4;   // bytes per element
     const int tyz = G.tiles[1] * G.tiles[2];
     const int tx = t / tyz, ty = (t - tx * tyz) / G.tiles[2], tz = t % G.tiles[2];
     const int x0 = tx * kTile, y0 = ty * kTile, z0 = tz * kTile;
     const int X = G.dims[0], Y = G.dims[1], Z = G.dims[2];
     const int64_t origin = ((int64_t)(x0 * Y + y0) * Z + z0) * C + c0;
-    const int64_t left = ((int64_t)X * Y * Z * C - origin) * 4;
+    const int64_t left = ((int64_t)X * Y * Z * C - origin) * kEs;
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(gF + origin), (short)0, (int)min(left, (int64_t)0x7fffffff), 0x00020000);
+        const_cast<char*>(static_cast<const char*>(gF) + origin * kEs), (short)0, (int)min(left, (int64_t)0x7fffffff),
+        0x00020000);
     const bool cok = c0 + sc < C;
     const unsigned cc = (unsigned)(min(c0 + sc, C - 1) - c0);
     unsigned voff[2][2];
@@ -743,7 +785,7 @@ __device__ __forceinline__ unsigned br_load_tile(const Grid& G, int C, int c0, i
             const int y = y0 + 2 * (so & 1) + h;
             if (k == 0) yok[h] = y < Y;
             const unsigned yl = (unsigned)(min(y, Y - 1) - y0);
-            voff[k][h] = ((xl * Y + yl) * Z * C + cc) * 4u;
+            voff[k][h] = ((xl * Y + yl) * Z * C + cc) * (unsigned)kEs;
         }
     }
     int soff[4];
@@ -751,7 +793,7 @@ __device__ __forceinline__ unsigned br_load_tile(const Grid& G, int C, int c0, i
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         zok[i] = z0 + i < Z;
-        soff[i] = (min(z0 + i, Z - 1) - z0) * C * 4;
+        soff[i] = (min(z0 + i, Z - 1) - z0) * C * kEs;
     }
     unsigned mask = 0;
 #pragma unroll
@@ -759,7 +801,11 @@ __device__ __forceinline__ unsigned br_load_tile(const Grid& G, int C, int c0, i
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             // aux 2: non-temporal (grad_feats is streamed once per region)
-            v[k][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff[k][i >> 2], soff[i & 3], 2));
+            if constexpr (GB)
+                v[k][i] = __uint_as_float((unsigned)__builtin_amdgcn_raw_buffer_load_b16(rsrc, voff[k][i >> 2], soff[i & 3], 2)
+                                          << 16);
+            else
+                v[k][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff[k][i >> 2], soff[i & 3], 2));
             mask |= (cok && xok[k] && yok[i >> 2] && zok[i & 3]) ? (1u << (i + 8 * k)) : 0u;
         }
     return mask;
@@ -772,9 +818,9 @@ __device__ __forceinline__ unsigned br_load_tile(const Grid& G, int C, int c0, i
 // loaded as soon as the MFMAs of k step s of tile k are issued.  LDS hand-offs use lds_barrier,
 // so loads stay in flight across the barrier and the compiler waits for each where its registers
 // are used.
-template <int NB>
+template <int NB, bool GB>
 __device__ __forceinline__ void br_tiles(BrSmem& sm, const Grid& G, int C, int c0, int ntl, int prow,
-                                         const float* __restrict__ gF, const __bf16* __restrict__ wt,
+                                         const void* __restrict__ gF, const __bf16* __restrict__ wt,
                                          float* __restrict__ gpart) {
     constexpr int NR = NB > 0 ? NB : 1;   // register arrays (unused when NB == 0)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -793,7 +839,7 @@ __device__ __forceinline__ void br_tiles(BrSmem& sm, const Grid& G, int C, int c
             split8(u, hh, ll);
             // voxel octet so + 4k: k step k, lane group so
             sm.bhi[buf][k][sc >> 4][so * 16 + (sc & 15)] = hh;
-            sm.blo[buf][k][sc >> 4][so * 16 + (sc & 15)] = ll;
+            if constexpr (!GB) sm.blo[buf][k][sc >> 4][so * 16 + (sc & 15)] = ll;   // zero for bfloat16
         }
     };
     // A operand of row block b for k step s of a tile: row 16 (wave + 8b) + l%16, voxels
@@ -834,7 +880,7 @@ __device__ __forceinline__ void br_tiles(BrSmem& sm, const Grid& G, int C, int c
                 }
 #pragma unroll
                 for (int b = 0; b < NB; ++b)
-                    acc[b][cb] = mfma3_16x16x32(wh[b][s], wl[b][s], bh[cb & 1], bl[cb & 1], acc[b][cb]);
+                    acc[b][cb] = mfma_split_16x16x32<false, GB>(wh[b][s], wl[b][s], bh[cb & 1], bl[cb & 1], acc[b][cb]);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -844,9 +890,9 @@ __device__ __forceinline__ void br_tiles(BrSmem& sm, const Grid& G, int C, int c
     const int klast = ntl - 1;
     // prologue: tile 0 staged, gF of tile 1 and the weights of tile 0 in flight (in the order
     // the loop issues them, so that the compiler's waits at the loop head stay exact)
-    pmask = br_load_tile(G, C, c0, uniform(sm.tl_t[0]), sc, so, gF, pre);
+    pmask = br_load_tile<GB>(G, C, c0, uniform(sm.tl_t[0]), sc, so, gF, pre);
     stage(0);
-    pmask = br_load_tile(G, C, c0, uniform(sm.tl_t[min(1, klast)]), sc, so, gF, pre);
+    pmask = br_load_tile<GB>(G, C, c0, uniform(sm.tl_t[min(1, klast)]), sc, so, gF, pre);
     rows_of(0);
     load_w(0);
     load_w(1);
@@ -854,7 +900,7 @@ __device__ __forceinline__ void br_tiles(BrSmem& sm, const Grid& G, int C, int c
     for (int k = 0; k < ntl; ++k) {
         const int kn = min(k + 1, klast);
         stage((k + 1) & 1);
-        pmask = br_load_tile(G, C, c0, uniform(sm.tl_t[min(k + 2, klast)]), sc, so, gF, pre);
+        pmask = br_load_tile<GB>(G, C, c0, uniform(sm.tl_t[min(k + 2, klast)]), sc, so, gF, pre);
         rows_of(kn);
         __builtin_amdgcn_sched_barrier(0);
         half(k & 1, 0);
@@ -882,8 +928,9 @@ __device__ __forceinline__ void br_tiles(BrSmem& sm, const Grid& G, int C, int c
 
 // One pass of phase B over rows rp .. rp + prow - 1 of the region (prow <= 384): stages the
 // pass's row table and G->R slots, then runs the tile loop with this wave's block count.
+template <bool GB>
 __device__ __forceinline__ void br_pass(BrSmem& sm, const Grid& G, int C, int c0, int ntl, int rp,
-                                        int KR, int M, int MR, int jr0, const float* __restrict__ gF,
+                                        int KR, int M, int MR, int jr0, const void* __restrict__ gF,
                                         const int* __restrict__ r_pairs, const int* __restrict__ table,
                                         const __bf16* __restrict__ wt, float* __restrict__ gpart) {
     const int wave = threadIdx.x >> 6;
@@ -922,14 +969,15 @@ __device__ __forceinline__ void br_pass(BrSmem& sm, const Grid& G, int C, int c0
     }
     __syncthreads();
     static_assert(kBrRbMax == 3, "block-count dispatch");
-    if (nb >= 3) br_tiles<3>(sm, G, C, c0, ntl, prow, gF, wt, gpart);
-    else if (nb == 2) br_tiles<2>(sm, G, C, c0, ntl, prow, gF, wt, gpart);
-    else if (nb == 1) br_tiles<1>(sm, G, C, c0, ntl, prow, gF, wt, gpart);
-    else br_tiles<0>(sm, G, C, c0, ntl, prow, gF, wt, gpart);
+    if (nb >= 3) br_tiles<3, GB>(sm, G, C, c0, ntl, prow, gF, wt, gpart);
+    else if (nb == 2) br_tiles<2, GB>(sm, G, C, c0, ntl, prow, gF, wt, gpart);
+    else if (nb == 1) br_tiles<1, GB>(sm, G, C, c0, ntl, prow, gF, wt, gpart);
+    else br_tiles<0, GB>(sm, G, C, c0, ntl, prow, gF, wt, gpart);
 }
 
+template <bool GB>
 __global__ void __launch_bounds__(kBrThreads, 1) k_bwd_region(
-    Grid G, Regions RG, int C, int nchunk, const float* __restrict__ gF,
+    Grid G, Regions RG, int C, int nchunk, const void* __restrict__ gF,
     const int* __restrict__ toff, int M, const int* __restrict__ roff,
     const int* __restrict__ r_pairs, const int* __restrict__ table, int MR,
     const __bf16* __restrict__ wt, float* __restrict__ gpart) {
@@ -966,7 +1014,7 @@ __global__ void __launch_bounds__(kBrThreads, 1) k_bwd_region(
     if (ntl == 0) return;   // every row stays zero: phase C reads no partial row of this region
 
     for (int rp = 0; rp < KR; rp += kBrPass)
-        br_pass(sm, G, C, c0, ntl, rp, KR, M, MR, jr0, gF, r_pairs, table, wt, gpart);
+        br_pass<GB>(sm, G, C, c0, ntl, rp, KR, M, MR, jr0, gF, r_pairs, table, wt, gpart);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1174,7 +1222,7 @@ hipError_t launch_backward_prepare(const Grid& G, int n, int C, const void* feat
 }
 
 hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_density,
-                                 const float* grad_feats, const float* means, const float* opacity,
+                                 const void* grad_feats, const float* means, const float* opacity,
                                  const float* cov_inv, const int* lb, const int* ub,
                                  const int* g2t_offsets, int64_t M, const int* tile_offsets,
                                  const int* sorted_tiles, const int* sorted_gauss, const float* density,
@@ -1196,10 +1244,11 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
     }
     if (M > 0 && T > 0) {
         const int blocks = (int)ceil_div(T, 8) * 8;
-        const bool vec = (C & 3) == 0 && ((uintptr_t)grad_feats & 15) == 0;   // 16-byte G loads
+        // 16-byte G loads: 4 float or 8 bfloat16 channels per load, rows 16-byte aligned
+        const bool vec = (C & (fdt == kDtBF16 ? 7 : 3)) == 0 && ((uintptr_t)grad_feats & 15) == 0;
 #define G2V_BT(V, F)                                                                                          \
-    G2V_LAUNCH((k_bwd_tile<V, F>), dim3(blocks), dim3(kBtThreads), 0, s, G, n, C, nchk, grad_density, grad_feats, \
-               means, opacity, cov_inv, lb, ub, g2t_offsets, tile_offsets, sorted_gauss, (int)M, density,        \
+    G2V_LAUNCH((k_bwd_tile<V, F>), dim3(blocks), dim3(kBtThreads), 0, s, G, n, C, nchk, grad_density,              \
+               grad_feats, means, opacity, cov_inv, lb, ub, g2t_offsets, tile_offsets, sorted_gauss, (int)M, density,        \
                grid_feats, fdt, (const __bf16*)b.fsp, b.partials, b.wt)
         if (fdt == kDtBF16) {
             if (vec) G2V_BT(true, true);
@@ -1214,9 +1263,14 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
         const int nchunk = (C + kBrCc - 1) / kBrCc;
         const int64_t items = (int64_t)RG.total * nchunk;
         const int blocks = (int)ceil_div(items, 8) * 8;
-        G2V_LAUNCH(k_bwd_region, dim3(blocks), dim3(kBrThreads), 0, s, G, RG, C, nchunk, grad_feats, tile_offsets,
-                   (int)M, (const int*)b.roff, (const int*)b.r_pairs_sorted, (const int*)b.table, (int)MR,
-                   (const __bf16*)b.wt, b.gpart);
+        if (fdt == kDtBF16)
+            G2V_LAUNCH(k_bwd_region<true>, dim3(blocks), dim3(kBrThreads), 0, s, G, RG, C, nchunk,
+                       (const void*)grad_feats, tile_offsets, (int)M, (const int*)b.roff,
+                       (const int*)b.r_pairs_sorted, (const int*)b.table, (int)MR, (const __bf16*)b.wt, b.gpart);
+        else
+            G2V_LAUNCH(k_bwd_region<false>, dim3(blocks), dim3(kBrThreads), 0, s, G, RG, C, nchunk,
+                       (const void*)grad_feats, tile_offsets, (int)M, (const int*)b.roff,
+                       (const int*)b.r_pairs_sorted, (const int*)b.table, (int)MR, (const __bf16*)b.wt, b.gpart);
     }
     if (fdt == kDtBF16)
         G2V_LAUNCH(k_bwd_gauss<true>, dim3(n), dim3(kBgThreads), 0, s, n, C, (int)M, (int)MR, g2t_offsets,

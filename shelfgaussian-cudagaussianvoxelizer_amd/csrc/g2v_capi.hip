@@ -123,7 +123,7 @@ extern "C" {
 
 const char* g2v_last_error(void) { return g_err; }
 
-int g2v_abi_version(void) { return 7; }
+int g2v_abi_version(void) { return 8; }
 
 int g2v_grid_dims(const float voxel_size[3], const float voxel_range[6], int dims[3], int tiles[3]) {
     Grid G;
@@ -352,7 +352,7 @@ size_t g2v_backward_workspace(int n, int feat_dim, long long num_pairs, long lon
 
 namespace {
 
-int backward_impl(int n, int feat_dim, const float* grad_density, const float* grad_feats,
+int backward_impl(int n, int feat_dim, const float* grad_density, const void* grad_feats,
                   const float* means3D, const float* opacity, const float* cov_inv,
                   const float voxel_size[3], const float voxel_range[6], const int* valid_voxel_lb,
                   const int* valid_voxel_ub, const int* num_voxels_per_gaussian,
@@ -421,7 +421,7 @@ int backward_impl(int n, int feat_dim, const float* grad_density, const float* g
 
 extern "C" {
 
-int g2v_backward(int n, int feat_dim, const float* grad_density, const float* grad_feats,
+int g2v_backward(int n, int feat_dim, const float* grad_density, const void* grad_feats,
                  const float* means3D, const float* opacity, const float* cov_inv,
                  const float voxel_size[3], const float voxel_range[6], const int* valid_voxel_lb,
                  const int* valid_voxel_ub, const int* num_voxels_per_gaussian,
@@ -473,7 +473,7 @@ int g2v_backward_prepare(int n, int feat_dim, const float voxel_size[3], const f
     return G2V_OK;
 }
 
-int g2v_backward_prepared(int n, int feat_dim, const float* grad_density, const float* grad_feats,
+int g2v_backward_prepared(int n, int feat_dim, const float* grad_density, const void* grad_feats,
                           const float* means3D, const float* opacity, const float* cov_inv,
                           const float voxel_size[3], const float voxel_range[6], const int* valid_voxel_lb,
                           const int* valid_voxel_ub, const int* num_voxels_per_gaussian,

@@ -121,7 +121,7 @@ hipError_t launch_backward_prepare(const Grid& G, int n, int C, const void* feat
                                    const void* plan_ws, int64_t MR, void* ws, hipStream_t s);
 // prepared: launch_backward_prepare already ran on ws for the same Gaussians and CSR.
 hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_density,
-                                 const float* grad_feats, const float* means, const float* opacity,
+                                 const void* grad_feats, const float* means, const float* opacity,
                                  const float* cov_inv, const int* lb, const int* ub,
                                  const int* g2t_offsets, int64_t M, const int* tile_offsets,
                                  const int* sorted_tiles, const int* sorted_gauss, const float* density,

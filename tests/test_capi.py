@@ -31,7 +31,7 @@ def test_header_symbols_exported():
 
 
 def test_abi_version():
-    assert _lib().load().g2v_abi_version() == 7
+    assert _lib().load().g2v_abi_version() == 8
 
 
 @pytest.mark.parametrize("vs,vr", [

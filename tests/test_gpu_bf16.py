@@ -6,9 +6,10 @@ float32 path fed with the same values (features.bfloat16().float()) multiplies e
 operands.  Bars:
   * density: identical to the float32 path on the same values;
   * grid_feats: the float32 path's grid_feats rounded to bfloat16 (nearest even), bit for bit;
-  * gradients of means, covariances, opacity: identical to the float32 path when no tile list
-    needs a second pass (the only place grid_feats itself is read back); the feature gradient is
-    the float32 path's rounded to bfloat16, bit for bit;
+  * gradients of means, covariances, opacity: identical to the float32 path (fed the upstream
+    feature gradient rounded to bfloat16, as the bfloat16 path takes it) when no tile list needs a
+    second pass (the only place grid_feats itself is read back); the feature gradient is the
+    float32 path's rounded to bfloat16, bit for bit;
   * against the float64 oracle on the rounded features: density rel < 1e-4, grid_feats and the
     feature gradient rel < 1e-2 (bfloat16 output rounding, 2^-9 relative per element).
 """
@@ -47,6 +48,8 @@ CASES = {
     "small_grid_c64": W.Workload("bf_c64", 700, 64, voxel_range=W.RANGE_SMALL, var_range=(0.2, 1.5)),
     "odd_channels_13": W.Workload("bf_c13", 500, 13, voxel_range=W.RANGE_SMALL, var_range=(0.2, 1.5)),
     "c256": W.Workload("bf_c256", 600, 256, voxel_range=W.RANGE_SMALL, var_range=(0.2, 1.5)),
+    # 16-byte grad_feats loads need 8 bfloat16 channels per piece: C = 20 takes the element loads
+    "c20_element_loads": W.Workload("bf_c20", 600, 20, voxel_range=W.RANGE_SMALL, var_range=(0.2, 1.5)),
 }
 
 
@@ -81,9 +84,9 @@ def test_bf16_features_match_float32_path(name):
     assert int(torch.diff(_C().build_t2g(vs, vr, ob[2], ob[3], ob[6], ob[7])["tile_offsets"]).max()) <= 256
     g = torch.Generator().manual_seed(4)
     gD = torch.randn(*ob[0].shape, generator=g).to(dev)
-    gF = torch.randn(*ob[5].shape, generator=g).to(dev)
-    gb = _C().gaussian_voxelizer_backward(gD, gF, md, od, ob[1], vs, vr, ob[2], ob[3], ob[4], ob[6], ob[7],
-                                          ob[0], ob[5], fb.to(dev))
+    gF = torch.randn(*ob[5].shape, generator=g).bfloat16().float().to(dev)   # bfloat16 values
+    gb = _C().gaussian_voxelizer_backward(gD, gF.bfloat16(), md, od, ob[1], vs, vr, ob[2], ob[3], ob[4], ob[6],
+                                          ob[7], ob[0], ob[5], fb.to(dev))
     gf = _C().gaussian_voxelizer_backward(gD, gF, md, od, of[1], vs, vr, of[2], of[3], of[4], of[6], of[7],
                                           of[0], of[5], fb.float().to(dev))
     assert gb[3].dtype == torch.bfloat16
@@ -109,7 +112,8 @@ def test_bf16_long_lists_against_oracle():
     assert int(torch.diff(_C().build_t2g(vs, vr, ob[2], ob[3], ob[6], ob[7])["tile_offsets"]).max()) > 256
     g = torch.Generator().manual_seed(5)
     gD = torch.randn(*ob[0].shape, generator=g).to(dev)
-    gF = torch.randn(*ob[5].shape, generator=g).to(dev)
+    gF = torch.randn(*ob[5].shape, generator=g).bfloat16().float().to(dev)   # bfloat16 values
+    # a float32 upstream gradient of bfloat16 features is rounded to bfloat16 (exact here)
     gb = _C().gaussian_voxelizer_backward(gD, gF, md, od, ob[1], vs, vr, ob[2], ob[3], ob[4], ob[6], ob[7],
                                           ob[0], ob[5], fb.to(dev))
     vsn, vrn = np.array(w.voxel_size, np.float32), np.array(w.voxel_range, np.float32)
