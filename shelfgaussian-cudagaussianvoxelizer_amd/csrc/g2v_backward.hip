@@ -236,6 +236,51 @@ __device__ __forceinline__ void lds_barrier() {
     __asm__ __volatile__("" ::: "memory");
 }
 
+// Geometry of one lane's 16 epilogue elements against its Gaussian.  The elements of a lane are
+// the 2 x 2 x 4 voxel block x = x0 + a, y = y0 + 2b, z = z0 + c of the tile (a, b < 2, c < 4), so
+// dx = centre - mu splits by axis and q = A dx is the sum of one column product per axis:
+// q = A[:,0] dx_a + A[:,1] dy_b + A[:,2] dz_c.  The box test splits by axis as well (bit masks).
+struct LaneGeom {
+    float dx[2], dy[2], dz[4];
+    float qa[2][3], qb[2][3], qc[4][3];   // column products, by axis and offset
+    unsigned inx, iny, inz;               // bit a / b / c: the offset lies in the Gaussian's box
+};
+
+__device__ __forceinline__ void lane_geom(const Grid& G, const GaussParams& p, int x0, int y0, int z0,
+                                          LaneGeom& L) {
+    L.inx = L.iny = L.inz = 0;
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+        const int x = x0 + a, y = y0 + 2 * a;
+        L.dx[a] = centre(G, 0, x) - p.mu[0];
+        L.dy[a] = centre(G, 1, y) - p.mu[1];
+        L.inx |= (x >= p.lb[0] && x <= p.ub[0]) ? (1u << a) : 0u;
+        L.iny |= (y >= p.lb[1] && y <= p.ub[1]) ? (1u << a) : 0u;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            L.qa[a][k] = p.A[3 * k] * L.dx[a];
+            L.qb[a][k] = p.A[3 * k + 1] * L.dy[a];
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int z = z0 + c;
+        L.dz[c] = centre(G, 2, z) - p.mu[2];
+        L.inz |= (z >= p.lb[2] && z <= p.ub[2]) ? (1u << c) : 0u;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) L.qc[c][k] = p.A[3 * k + 2] * L.dz[c];
+    }
+}
+
+// q and the Mahalanobis term m = dx . q of element (a, b, c).
+__device__ __forceinline__ float lane_q(const LaneGeom& L, int a, int b, int c, float& qx, float& qy,
+                                        float& qz) {
+    qx = (L.qa[a][0] + L.qb[b][0]) + L.qc[c][0];
+    qy = (L.qa[a][1] + L.qb[b][1]) + L.qc[c][1];
+    qz = (L.qa[a][2] + L.qb[b][2]) + L.qc[c][2];
+    return L.dx[a] * qx + L.dy[b] * qy + L.dz[c] * qz;
+}
+
 // BF: features and grad_feats are bfloat16 (the A and B operands' low parts are zero, and the
 // chunks of grad_feats are staged as bfloat16).
 template <bool VEC, bool BF>
@@ -574,19 +619,23 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             const bool gok = gcol[j] >= 0;
             GaussParams p;
             read_params(sm.pt, slot, p);
+            LaneGeom L;
+            lane_geom(G, p, tx * kTile + 2 * mb, ty * kTile + h, tz * kTile, L);
             __bf16* wrow = wt + (int64_t)(j0 + pbase + slot) * kWtRow;
 #pragma unroll
             for (int q4 = 0; q4 < 4; ++q4) {
                 __bf16 hs[4], ls[4];
+                const int a = q4 >> 1, b = q4 & 1;
 #pragma unroll
                 for (int ii = 0; ii < 4; ++ii) {
+                    // element i: voxel row r = mb*32 + 8 q4 + 4h + ii, at x = x0 + a, y = y0 + 2b,
+                    // z = z0 + ii; the exponential is always evaluated, then selected
                     const int i = q4 * 4 + ii;
                     const int r = mb * 32 + 8 * q4 + 4 * h + ii;
-                    const int x = tx * kTile + (r >> 4), y = ty * kTile + ((r >> 2) & 3), z = tz * kTile + ii;
-                    const bool ok = gok && ((rowok >> i) & 1u) && in_box(p, x, y, z);
+                    const bool ok = gok & (((rowok >> i) & (L.inx >> a) & (L.iny >> b) & (L.inz >> ii) & 1u) != 0u);
                     float qx, qy, qz;
-                    const float e = ok ? eval_gauss(p, centre(G, 0, x), centre(G, 1, y), centre(G, 2, z), qx, qy, qz)
-                                       : 0.0f;
+                    const float m = lane_q(L, a, b, ii, qx, qy, qz);
+                    const float e = ok ? __expf(-0.5f * m) : 0.0f;
                     ek[j][i] = e;
                     okm[j] |= ok ? (1u << i) : 0u;
                     const float w = p.o * e;
@@ -633,12 +682,13 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             if (j < nact) {   // wave-uniform
                 GaussParams p;
                 read_params(sm.pt, slot, p);
+                LaneGeom L;
+                lane_geom(G, p, tx * kTile + 2 * mb, ty * kTile + h, tz * kTile, L);
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const int r = mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-                    const int x = tx * kTile + (r >> 4), y = ty * kTile + ((r >> 2) & 3), z = tz * kTile + (i & 3);
                     float qx, qy, qz;
-                    gauss_q(p, centre(G, 0, x), centre(G, 1, y), centre(G, 2, z), qx, qy, qz);
+                    lane_q(L, i >> 3, (i >> 2) & 1, i & 3, qx, qy, qz);
                     const float gw = sm.gD[r] + (acc[j][i] - sm.tv[r]) * sm.inv[r];
                     accumulate_grads(gr, ((okm[j] >> i) & 1u) ? gw : 0.0f, ek[j][i], p.o, qx, qy, qz);
                 }
