@@ -93,13 +93,30 @@ __global__ void __launch_bounds__(256) k_bwd_density(Grid G, int n, const float*
     const int nv = (ex > 0 && ey > 0 && ez > 0) ? ex * ey * ez : 0;
     const int eyz = ey * ez;
     float gr[kNumGrads] = {};
+    // Voxel i of the box (z fastest) sits at (ix, iy, iz) = the digits of i in radix (ey, ez).  A
+    // lane visits i = lane, lane + 64, ...: its position is stepped by the digits (sx, sy, sz) of
+    // 64, with at most one carry per digit, instead of divided out at every voxel.
+    int ix = 0, iy = 0, iz = 0, sx = 0, sy = 0, sz = 0;
+    if (nv > 0) {
+        ix = lane / eyz;
+        iy = (lane - ix * eyz) / ez;
+        iz = lane - ix * eyz - iy * ez;
+        sx = 64 / eyz;
+        sy = (64 - sx * eyz) / ez;
+        sz = 64 - sx * eyz - sy * ez;
+    }
     for (int i = lane; i < nv; i += 64) {
-        const int ix = i / eyz, r = i - ix * eyz;
-        const int iy = r / ez, iz = r - iy * ez;
         const int x = p.lb[0] + ix, y = p.lb[1] + iy, z = p.lb[2] + iz;
         float qx, qy, qz;
         const float e = eval_gauss(p, centre(G, 0, x), centre(G, 1, y), centre(G, 2, z), qx, qy, qz);
         accumulate_grads(gr, gD[voxel_index(G, x, y, z)], e, p.o, qx, qy, qz);
+        iz += sz;
+        const int cz = iz >= ez ? 1 : 0;
+        iz -= cz * ez;
+        iy += sy + cz;
+        const int cy = iy >= ey ? 1 : 0;
+        iy -= cy * ey;
+        ix += sx + cy;
     }
 #pragma unroll
     for (int k = 0; k < kNumGrads; ++k) gr[k] = wave_sum(gr[k]);

@@ -19,52 +19,6 @@
 namespace g2v {
 
 // ------------------------------------------------------------------------------------------
-// Density only: one wave per tile, one voxel per lane, Gaussian parameters wave-uniform.
-// ------------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) k_fwd_density(Grid G, const float* __restrict__ means,
-                                                     const float* __restrict__ opacity,
-                                                     const float* __restrict__ cov_inv,
-                                                     const int* __restrict__ lb,
-                                                     const int* __restrict__ ub,
-                                                     const int* __restrict__ toff,
-                                                     const int* __restrict__ sorted_gauss,
-                                                     int M, float* __restrict__ density) {
-    const int T = G.tiles[0] * G.tiles[1] * G.tiles[2];
-    const int nblocks = gridDim.x;
-    const int tile = uniform(xcd_remap(blockIdx.x, nblocks) * 4 + (threadIdx.x >> 6));
-    if (tile >= T) return;
-    const int lane = threadIdx.x & 63;
-    int x, y, z;
-    tile_voxel(G, tile, lane, x, y, z);
-    const float cx = centre(G, 0, x), cy = centre(G, 1, y), cz = centre(G, 2, z);
-    const int j0 = uniform(min(max(toff[tile], 0), M));
-    const int j1 = uniform(min(max(toff[tile + 1], j0), M));
-    float acc = 0.0f;
-    for (int j = j0; j < j1; ++j) {
-        const int g = uniform(sorted_gauss[j]);
-        GaussParams p;
-        load_params(p, g, means, cov_inv, opacity, lb, ub);
-        if (!in_box(p, x, y, z)) continue;
-        float qx, qy, qz;
-        acc += p.o * eval_gauss(p, cx, cy, cz, qx, qy, qz);
-    }
-    if (in_grid(G, x, y, z)) density[voxel_index(G, x, y, z)] = acc;
-}
-
-hipError_t launch_forward_density(const Grid& G, const float* means, const float* opacity,
-                                  const float* cov_inv, const int* lb, const int* ub,
-                                  const int* tile_offsets, const int* sorted_gauss, int M,
-                                  float* density, hipStream_t s) {
-    const int T = G.tiles[0] * G.tiles[1] * G.tiles[2];
-    if (T <= 0) return hipSuccess;
-    const int groups = (int)ceil_div(T, 4);
-    const int blocks = (int)ceil_div(groups, 8) * 8;
-    G2V_LAUNCH(k_fwd_density, dim3(blocks), dim3(256), 0, s, G, means, opacity, cov_inv, lb,
-                       ub, tile_offsets, sorted_gauss, M, density);
-    return hipGetLastError();
-}
-
-// ------------------------------------------------------------------------------------------
 // Features as packed bf16 pairs: low half = hi part, high half = lo part of the 2-term split.
 // ------------------------------------------------------------------------------------------
 // T: float or __bf16 features (a bf16 value splits into itself and a zero low part).
@@ -143,6 +97,109 @@ struct alignas(16) FwdParam {
     int pad;
 };
 static_assert(sizeof(FwdParam) == 80, "FwdParam is five 16-byte words");
+
+// ------------------------------------------------------------------------------------------
+// Density only: one wave per tile, one voxel per lane.  The wave walks its tile's list in
+// ascending order, 64 entries at a time: lane k gathers entry k's parameters (those of the next
+// 64 entries are gathered into registers while the current ones are evaluated) and writes them
+// as one record into the wave's LDS slab; every lane then evaluates the 64 records branch-free
+// from broadcast reads and adds o e where the voxel lies in the entry's box (the sum of the
+// reference's kernel, .cu:7-136, in the same order).
+// ------------------------------------------------------------------------------------------
+constexpr int kDenWaves = 4;
+
+// LDS hand-off between the lanes of one wave: waits for the wave's LDS operations; the compiler
+// barriers keep the slab's reads and writes on their side of it.
+__device__ __forceinline__ void wave_lds_sync() {
+    __asm__ __volatile__("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((15 << 0) | (7 << 4) | (0 << 8) | (3 << 14));   // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+    __asm__ __volatile__("" ::: "memory");
+}
+
+__global__ void __launch_bounds__(kDenWaves * 64) k_fwd_density(Grid G, const float* __restrict__ means,
+                                                               const float* __restrict__ opacity,
+                                                               const float* __restrict__ cov_inv,
+                                                               const int* __restrict__ lb,
+                                                               const int* __restrict__ ub,
+                                                               const int* __restrict__ toff,
+                                                               const int* __restrict__ sorted_gauss,
+                                                               int M, float* __restrict__ density) {
+    __shared__ FwdParam slab[kDenWaves][64];
+    const int T = G.tiles[0] * G.tiles[1] * G.tiles[2];
+    const int tile = uniform(xcd_remap(blockIdx.x, gridDim.x) * kDenWaves + (threadIdx.x >> 6));
+    if (tile >= T) return;   // whole waves; the kernel has no workgroup barrier
+    const int lane = threadIdx.x & 63;
+    FwdParam* sl = slab[threadIdx.x >> 6];
+    int x, y, z;
+    tile_voxel(G, tile, lane, x, y, z);
+    const float cx = centre(G, 0, x), cy = centre(G, 1, y), cz = centre(G, 2, z);
+    const int j0 = uniform(min(max(toff[tile], 0), M));
+    const int j1 = uniform(min(max(toff[tile + 1], j0), M));
+    // parameters of list entry j (an empty box past the list)
+    auto fetch = [&](int j, FwdParam& r) {
+        if (j < j1) {
+            const int g = sorted_gauss[j];
+#pragma unroll
+            for (int a = 0; a < 3; ++a) {
+                r.mu[a] = means[g * 3 + a];
+                r.lb[a] = lb[g * 3 + a];
+                r.ub[a] = ub[g * 3 + a];
+            }
+#pragma unroll
+            for (int a = 0; a < 9; ++a) r.A[a] = cov_inv[g * 9 + a];
+            r.o = opacity[g];
+        } else {
+#pragma unroll
+            for (int a = 0; a < 3; ++a) { r.mu[a] = 0.0f; r.lb[a] = 1; r.ub[a] = 0; }
+#pragma unroll
+            for (int a = 0; a < 9; ++a) r.A[a] = 0.0f;
+            r.o = 0.0f;
+        }
+        r.pad = 0;
+    };
+    float acc = 0.0f;
+    FwdParam nxt;
+    fetch(j0 + lane, nxt);
+    for (int jb = j0; jb < j1; jb += 64) {
+        wave_lds_sync();   // the previous records are read
+        sl[lane] = nxt;
+        wave_lds_sync();
+        fetch(jb + 64 + lane, nxt);
+        const int cnt = uniform(min(64, j1 - jb));
+#pragma unroll 2
+        for (int k = 0; k < cnt; ++k) {
+            GaussParams p;
+            const FwdParam& r = sl[k];   // broadcast
+#pragma unroll
+            for (int a = 0; a < 3; ++a) {
+                p.mu[a] = r.mu[a];
+                p.lb[a] = r.lb[a];
+                p.ub[a] = r.ub[a];
+            }
+#pragma unroll
+            for (int a = 0; a < 9; ++a) p.A[a] = r.A[a];
+            p.o = r.o;
+            float qx, qy, qz;
+            const float e = eval_gauss(p, cx, cy, cz, qx, qy, qz);
+            acc += in_box(p, x, y, z) ? p.o * e : 0.0f;
+        }
+    }
+    if (in_grid(G, x, y, z)) density[voxel_index(G, x, y, z)] = acc;
+}
+
+hipError_t launch_forward_density(const Grid& G, const float* means, const float* opacity,
+                                  const float* cov_inv, const int* lb, const int* ub,
+                                  const int* tile_offsets, const int* sorted_gauss, int M,
+                                  float* density, hipStream_t s) {
+    const int T = G.tiles[0] * G.tiles[1] * G.tiles[2];
+    if (T <= 0) return hipSuccess;
+    const int groups = (int)ceil_div(T, kDenWaves);
+    const int blocks = (int)ceil_div(groups, 8) * 8;
+    G2V_LAUNCH(k_fwd_density, dim3(blocks), dim3(kDenWaves * 64), 0, s, G, means, opacity, cov_inv, lb,
+               ub, tile_offsets, sorted_gauss, M, density);
+    return hipGetLastError();
+}
 
 struct FwdSmem {
     bf16x8 whi[kFwdKSteps][2][64];   // A operand, hi part: [k step][voxel block][lane]
