@@ -193,14 +193,16 @@ __global__ void __launch_bounds__(kScanThreads) k_scan_apply(const int* in, int*
     }
 }
 
-// Single-workgroup scan for inputs up to kScanSingleMax.  Tiles of 1024 x 32 values: coalesced
+// Single-workgroup scan for inputs up to kScanSingleMax (two tiles: beyond that the three-kernel
+// scan, whose reduce and apply kernels spread over the whole chip, is faster; a tile takes one
+// workgroup about 5 us).  Tiles of 1024 x 32 values: coalesced
 // loads into LDS (row of 32 values per thread, padded to 33 words), a sequential scan of each
 // thread's row, a workgroup scan of the row totals, and coalesced stores back from LDS; a
 // running carry joins the tiles.  In-place safe (a tile is read completely before it is written).
 constexpr int kScan1Threads = 1024;
 constexpr int kScan1Items = 32;
 constexpr int kScan1Row = kScan1Items + 1;
-constexpr int64_t kScanSingleMax = int64_t(1) << 20;
+constexpr int64_t kScanSingleMax = int64_t(2) * kScan1Threads * kScan1Items;
 
 struct ScanJob {
     const int* in;

@@ -97,8 +97,11 @@ CSR_CASES = {
                             var_range=(0.01, 0.2)),
     "one_tile_grid": W.Workload("one_tile", 50, 4, voxel_range=(0.0, 0.0, 0.0, 1.2, 1.2, 1.2), voxel_size=(0.4, 0.4, 0.4),
                                 var_range=(0.01, 0.3)),
-    # more than 2^20 Gaussians: the offsets scan takes the multi-workgroup path
+    # more than 2^20 Gaussians (the offsets scan, and the sort's histogram scans, take the
+    # multi-workgroup path above 65,536 values)
     "many_small_n1100000": W.Workload("many_small", 1_100_000, None, var_range=(0.01, 0.05)),
+    # 70,000 Gaussians: the offsets scan (over more than 65,536 values) takes the multi-workgroup path
+    "small_n70000": W.Workload("small_n70000", 70_000, None, var_range=(0.1, 0.6)),
     # the reference's recorded training batch (tests/golden/mmdet_debug_inputs.npz)
     "recorded_batch": W.mmdet_workload(),
 }
