@@ -316,13 +316,19 @@ hipError_t scan_i32_pair(const int* in_a, int* out_a, int64_t n_a, long long* to
 // G->T fill: one wave per Gaussian enumerates its tile box row-major (x slowest, z fastest).
 // tile_ids may be null (only the Gaussian id of every pair is regenerated).
 // ------------------------------------------------------------------------------------------
+// 16 lanes per Gaussian (16 Gaussians per workgroup): a Gaussian touches about 25 to 360 tiles.
+// Entry i of a row is tile box position (lx, ly, lz) = the digits of i in radix (dy, dz); a lane
+// visits i = l, l + 16, ... and steps its position by the digits of 16 (at most one carry per
+// digit) instead of dividing at every entry.
+constexpr int kFillLanes = 16;
+
 __global__ void __launch_bounds__(256) k_fill_g2t(Grid G, int n, const int* __restrict__ lb,
                                                   const int* __restrict__ ub,
                                                   const int* __restrict__ g2t_offsets,
                                                   int* __restrict__ tile_ids,
                                                   int* __restrict__ gauss_ids) {
-    const int lane = threadIdx.x & 63;
-    const int g = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int l = threadIdx.x & (kFillLanes - 1);
+    const int g = blockIdx.x * (256 / kFillLanes) + threadIdx.x / kFillLanes;
     if (g >= n) return;
     const int base = g2t_offsets[g];
     const int cnt = g2t_offsets[g + 1] - base;
@@ -331,19 +337,30 @@ __global__ void __launch_bounds__(256) k_fill_g2t(Grid G, int n, const int* __re
     const int dy = ub[g * 3 + 1] / kTile - ty0 + 1;
     const int dz = ub[g * 3 + 2] / kTile - tz0 + 1;
     const int dyz = dy * dz;
-    for (int i = lane; i < cnt; i += 64) {
-        const int lx = i / dyz, r = i - lx * dyz;
-        const int ly = r / dz, lz = r - ly * dz;
+    int lx = l / dyz;
+    int ly = (l - lx * dyz) / dz;
+    int lz = l - lx * dyz - ly * dz;
+    const int sx = kFillLanes / dyz;
+    const int sy = (kFillLanes - sx * dyz) / dz;
+    const int sz = kFillLanes - sx * dyz - sy * dz;
+    for (int i = l; i < cnt; i += kFillLanes) {
         if (tile_ids) tile_ids[base + i] = ((tx0 + lx) * G.tiles[1] + (ty0 + ly)) * G.tiles[2] + (tz0 + lz);
         gauss_ids[base + i] = g;
+        lz += sz;
+        const int cz = lz >= dz ? 1 : 0;
+        lz -= cz * dz;
+        ly += sy + cz;
+        const int cy = ly >= dy ? 1 : 0;
+        ly -= cy * dy;
+        lx += sx + cy;
     }
 }
 
 hipError_t launch_fill_g2t(const Grid& G, int n, const int* lb, const int* ub,
                            const int* g2t_offsets, int* tile_ids, int* gauss_ids, hipStream_t s) {
     if (n <= 0) return hipSuccess;
-    G2V_LAUNCH(k_fill_g2t, dim3((unsigned)ceil_div(n, 4)), dim3(256), 0, s, G, n, lb, ub,
-                       g2t_offsets, tile_ids, gauss_ids);
+    G2V_LAUNCH(k_fill_g2t, dim3((unsigned)ceil_div(n, 256 / kFillLanes)), dim3(256), 0, s, G, n, lb, ub,
+               g2t_offsets, tile_ids, gauss_ids);
     return hipGetLastError();
 }
 
