@@ -140,12 +140,17 @@ hipError_t launch_backward_density(const Grid& G, int n, const float* grad_densi
 constexpr int kBtKc = 32;                  // channels per chunk
 constexpr int kBtRowBytes = kBtKc * 4;     // bytes of one row's chunk (hi and lo)
 
+// bfloat16 features need no split: their chunks are kBtKcBf = 64 channels of the row itself, 128
+// bytes (the same bytes per chunk row as a float chunk's hi and lo).
+constexpr int kBtKcBf = 2 * kBtKc;
+
 template <typename T>
 __global__ void __launch_bounds__(256) k_split_chunks(const T* __restrict__ src, int n, int C, int nchk,
                                                       __bf16* __restrict__ dst) {
     // one thread per 8 channels of a row (an octet of a chunk): 16-byte hi and lo stores
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int noct = nchk * (kBtKc / 8);
+    constexpr bool kBf = sizeof(T) == 2;
+    const int noct = nchk * ((kBf ? kBtKcBf : kBtKc) / 8);
     if (i >= (int64_t)(n + 1) * noct) return;
     const int64_t r = i / noct;
     const int oc = (int)(i - r * noct);
@@ -162,6 +167,10 @@ __global__ void __launch_bounds__(256) k_split_chunks(const T* __restrict__ src,
     }
     bf16x8 h, l;
     split8(v, h, l);
+    if constexpr (kBf) {   // the row padded to nchk * 64 channels (l is zero)
+        *reinterpret_cast<bf16x8*>(dst + r * nchk * kBtKcBf + c) = h;
+        return;
+    }
     __bf16* row = dst + (r * nchk + c / kBtKc) * (2 * kBtKc);
     *reinterpret_cast<bf16x8*>(row + c % kBtKc) = h;
     *reinterpret_cast<bf16x8*>(row + kBtKc + c % kBtKc) = l;
@@ -298,8 +307,10 @@ __device__ __forceinline__ float lane_q(const LaneGeom& L, int a, int b, int c, 
     return L.dx[a] * qx + L.dy[b] * qy + L.dz[c] * qz;
 }
 
-// BF: features and grad_feats are bfloat16 (the A and B operands' low parts are zero, and the
-// chunks of grad_feats are staged as bfloat16).
+// BF: features and grad_feats are bfloat16.  A chunk is then 64 channels (the split rows hold the
+// values themselves, 128 bytes per chunk row, as k_split_chunks<__bf16> writes them; the grad_feats
+// chunk rows are 128 bytes of bfloat16), and each k half of 32 channels is two 16-channel slices:
+// the A and B "hi" operands carry slice 0 and the "lo" operands slice 1, with one MFMA each.
 template <bool VEC, bool BF>
 __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
     Grid G, int n, int C, int nchk, const float* __restrict__ gD, const void* __restrict__ gF_,
@@ -336,6 +347,7 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
 
     typedef typename std::conditional<BF, __bf16, float>::type GT;   // element of grad_feats
     const GT* gF = static_cast<const GT*>(gF_);
+    constexpr int kKc = BF ? kBtKcBf : kBtKc;   // channels per chunk
     // Lists longer than one pass: t_v = sum_c gF_vc F_vc straight from grid_feats.
     const bool multi = Ng > kBtPass;
     if (multi) {
@@ -362,28 +374,26 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
     // slot p ^ swz(v), so that the A-operand reads (8 or 16 consecutive rows per LDS cycle) are
     // free of bank conflicts.  VEC: one 16-byte load per lane, lane = (row, slot); otherwise four 4-byte
     // loads per lane, each covering two rows.
-    // BF: a chunk row is 64 bytes of bfloat16; with VEC (C % 8 == 0, 16-byte aligned rows) lanes
-    // 0..31 of a wave load its 8 rows as 16-byte pieces at slot = piece (stage rows of 64 bytes,
-    // read whole by write_a); without VEC the A operand is loaded by write_a itself (no staging).
+    // BF: a chunk row is 128 bytes of bfloat16; with VEC (C % 8 == 0, 16-byte aligned rows) lane l
+    // loads 16-byte piece l % 8 of row l / 8 of the wave's 8 rows (stage rows of 128 bytes, pieces
+    // in order, read whole by write_a); without VEC write_a loads the A operand itself.
     constexpr int kNG = BF ? (VEC ? 1 : 0) : (VEC ? 1 : 4);   // G loads per wave per chunk
     constexpr int kNGs = kNG > 0 ? kNG : 1;
     const GT* gsrc[kNGs];
     int gcoff[kNGs];   // channel of this lane's load within a chunk
 #pragma unroll
     for (int k = 0; k < kNG; ++k) {
-        const int v = BF ? wave * 8 + ((lane & 31) >> 2)
-                         : (VEC ? wave * 8 + (lane >> 3) : wave * 8 + 2 * k + (lane >> 5));
+        const int v = (BF || VEC) ? wave * 8 + (lane >> 3) : wave * 8 + 2 * k + (lane >> 5);
         gsrc[k] = gF + (int64_t)max(sm.vlin[v], 0) * C;
-        gcoff[k] = BF ? 8 * (lane & 3)
+        gcoff[k] = BF ? 8 * (lane & 7)
                       : (VEC ? 4 * ((lane & 7) ^ swz(v)) : 4 * (((lane & 31) >> 2) ^ swz(v)) + (lane & 3));
     }
     auto dma_g = [&](int chunk, int stage) {
 #pragma unroll
         for (int k = 0; k < kNG; ++k) {
             if constexpr (BF) {
-                if (lane < 32)
-                    dma16_nt(gsrc[k] + min(chunk * kBtKc + gcoff[k], C - 8),
-                             uniform(lds_addr(reinterpret_cast<char*>(&sm.graw[stage][0][0]) + wave * 8 * 64)));
+                dma16_nt(gsrc[k] + min(chunk * kKc + gcoff[k], C - 8),
+                         uniform(lds_addr(reinterpret_cast<char*>(&sm.graw[stage][0][0]) + wave * 8 * 128)));
             } else if (VEC) {
                 dma16_nt(gsrc[k] + min(chunk * kBtKc + gcoff[k], C - 4), uniform(lds_addr(&sm.graw[stage][wave * 8][0])));
             } else {
@@ -456,33 +466,38 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
         const int sv = threadIdx.x >> 3, sq = threadIdx.x & 7;
         const bool svok = sm.vlin[sv] >= 0;
         auto write_a = [&](int ch, int gs, int ab) {
-            const int lim = svok ? min(max(C - (ch * kBtKc + 4 * sq), 0), 4) : 0;
+            const int lim = svok ? min(max(C - (ch * kKc + 4 * sq), 0), 4) : 0;
             typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
             typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
             typedef float f32x2 __attribute__((ext_vector_type(2)));
             const int L = ((sq >> 1) & 1) * 32 + (sv & 31);
             if constexpr (BF) {
-                // bfloat16 values: the high part is the value itself, the low part zero (not stored:
-                // the MFMAs leave that term out)
-                unsigned short e[4];
+                // bfloat16: thread (sv, sq) takes channels 8sq..8sq+7 of the 64-channel chunk, i.e.
+                // k half sq/4, slice (sq/2)&1 (A buffer ahi for slice 0, alo for slice 1), lane
+                // group sq&1 of the voxel's fragment; values past the row or the grid are cleared
+                const int lim8 = svok ? min(max(C - (ch * kKc + 8 * sq), 0), 8) : 0;
+                uint4 xr;
                 if constexpr (VEC) {
-                    const uint2 xr = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(&sm.graw[gs][0][0]) +
-                                                                     sv * 64 + sq * 8);
-                    e[0] = (unsigned short)(xr.x & 0xffffu);
-                    e[1] = (unsigned short)(xr.x >> 16);
-                    e[2] = (unsigned short)(xr.y & 0xffffu);
-                    e[3] = (unsigned short)(xr.y >> 16);
+                    xr = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(&sm.graw[gs][0][0]) +
+                                                         sv * 128 + sq * 16);
                 } else {
                     const unsigned short* row =
                         reinterpret_cast<const unsigned short*>(gF + (int64_t)max(sm.vlin[sv], 0) * C);
+                    unsigned e[8];
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) e[i] = row[min(ch * kBtKc + 4 * sq + i, C - 1)];
+                    for (int i = 0; i < 8; ++i) e[i] = row[min(ch * kKc + 8 * sq + i, C - 1)];
+                    xr = make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
                 }
-                bf16x4 hv;
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    hv[i] = __builtin_bit_cast(__bf16, (unsigned short)(e[i] & (0u - (unsigned)(i < lim))));
-                *reinterpret_cast<bf16x4*>(reinterpret_cast<char*>(&sm.ahi[ab][sq >> 2][sv >> 5][L]) + (sq & 1) * 8) = hv;
+                auto keep = [&](int w) {   // mask of word w (elements 2w and 2w + 1)
+                    return (2 * w < lim8 ? 0x0000ffffu : 0u) | (2 * w + 1 < lim8 ? 0xffff0000u : 0u);
+                };
+                xr.x &= keep(0);
+                xr.y &= keep(1);
+                xr.z &= keep(2);
+                xr.w &= keep(3);
+                const int Lb = (sq & 1) * 32 + (sv & 31);
+                bf16x8* dst = ((sq >> 1) & 1) ? &sm.alo[ab][sq >> 2][sv >> 5][Lb] : &sm.ahi[ab][sq >> 2][sv >> 5][Lb];
+                *reinterpret_cast<uint4*>(dst) = xr;
                 return;
             }
             // one 16-byte LDS read, then the values past the row or the grid are cleared with bit
@@ -514,18 +529,27 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             }
 #pragma unroll
             for (int j = 0; j < kBtNbw; ++j) {
+                // float: pieces 2ks+h (hi) and 4+2ks+h (lo); bfloat16: pieces 4ks+h (slice 0) and
+                // 4ks+2+h (slice 1)
                 const int r = (ngrp + kBtGroups * j) * 32 + (lane & 31), sr = swz(r);
+                const int qh = BF ? 4 * ks + h : 2 * ks + h, ql = BF ? 4 * ks + 2 + h : 4 + 2 * ks + h;
                 const unsigned char* rowp = &sm.u.frow[st][r * kBtRowBytes];
-                o.bh[j] = *reinterpret_cast<const bf16x8*>(rowp + (((2 * ks + h) ^ sr) << 4));
-                o.bl[j] = *reinterpret_cast<const bf16x8*>(rowp + (((4 + 2 * ks + h) ^ sr) << 4));
+                o.bh[j] = *reinterpret_cast<const bf16x8*>(rowp + ((qh ^ sr) << 4));
+                o.bl[j] = *reinterpret_cast<const bf16x8*>(rowp + ((ql ^ sr) << 4));
             }
         };
         // N block j of the step against both voxel blocks
         auto mult = [&](int j, const StepOps& o) {
             if (j < nact) {
 #pragma unroll
-                for (int m = 0; m < 2; ++m)
-                    acc2[m][j] = mfma_split_32x32x16<BF, BF>(o.ah[m], o.al[m], o.bh[j], o.bl[j], acc2[m][j]);
+                for (int m = 0; m < 2; ++m) {
+                    if constexpr (BF) {   // slices 0 and 1
+                        acc2[m][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(o.ah[m], o.bh[j], acc2[m][j], 0, 0, 0);
+                        acc2[m][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(o.al[m], o.bl[j], acc2[m][j], 0, 0, 0);
+                    } else {
+                        acc2[m][j] = mfma_split_32x32x16<false, false>(o.ah[m], o.al[m], o.bh[j], o.bl[j], acc2[m][j]);
+                    }
+                }
             }
         };
 
@@ -1120,16 +1144,10 @@ __global__ void __launch_bounds__(kBgThreads) k_bwd_gauss(
         write_grads(tot, g, grad_means, grad_cov, grad_opacity);
     }
     const int r0 = min(max(g2r_offsets[g], 0), MR), r1 = min(max(g2r_offsets[g + 1], r0), MR);
-    if constexpr (OBF16) {
-        __bf16* out = static_cast<__bf16*>(grad_features_out) + (int64_t)g * C;
-        for (int c = threadIdx.x; c < C; c += kBgThreads) {
-            float s = 0.0f;
-            for (int r = r0; r < r1; ++r) s += gpart[(int64_t)r * C + c];
-            out[c] = (__bf16)s;
-        }
-        return;
-    }
-    float* out = static_cast<float*>(grad_features_out) + (int64_t)g * C;
+    // region rows summed in ascending order per channel; a bfloat16 output is the float sum rounded
+    // to nearest even
+    typedef typename std::conditional<OBF16, __bf16, float>::type OT;
+    OT* out = static_cast<OT*>(grad_features_out) + (int64_t)g * C;
     if ((C & 3) == 0) {
         for (int c = threadIdx.x * 4; c < C; c += kBgThreads * 4) {
             float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1138,13 +1156,18 @@ __global__ void __launch_bounds__(kBgThreads) k_bwd_gauss(
                 s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
             }
             const f32x4 nv = {s.x, s.y, s.z, s.w};
-            __builtin_nontemporal_store(nv, reinterpret_cast<f32x4*>(out + c));
+            if constexpr (OBF16) {
+                typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+                *reinterpret_cast<bf16x4*>(out + c) = __builtin_convertvector(nv, bf16x4);
+            } else {
+                __builtin_nontemporal_store(nv, reinterpret_cast<f32x4*>(out + c));
+            }
         }
     } else {
         for (int c = threadIdx.x; c < C; c += kBgThreads) {
             float s = 0.0f;
             for (int r = r0; r < r1; ++r) s += gpart[(int64_t)r * C + c];
-            out[c] = s;
+            out[c] = (OT)s;
         }
     }
 }
@@ -1153,6 +1176,8 @@ __global__ void __launch_bounds__(kBgThreads) k_bwd_gauss(
 // Host side
 // ------------------------------------------------------------------------------------------
 static int feature_chunks(int C) { return (C + kBtKc - 1) / kBtKc; }
+// Chunks of phase A for the feature type: 32 channels (float, split hi/lo) or 64 (bfloat16).
+static int feature_chunks(int C, int fdt) { return fdt == kDtBF16 ? (C + kBtKcBf - 1) / kBtKcBf : feature_chunks(C); }
 
 struct PlanBufs {
     int* g2r_offsets;
@@ -1251,14 +1276,15 @@ hipError_t launch_backward_prepare(const Grid& G, int n, int C, const void* feat
                                    const void* plan_ws, int64_t MR, void* ws, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     const Regions RG = make_regions(G);
-    const int nchk = feature_chunks(C);
+    const int nchk = feature_chunks(C, fdt);
     if (!split_rows_fit(n, C)) return hipErrorInvalidValue;   // byte offsets of the split rows are 32-bit
     const FeatBufs b = carve_feats(ws, G, n, C, M, MR);
     const PlanBufs pb = carve_plan(const_cast<void*>(plan_ws), n);
     hipError_t e;
 
-    // features as 32-channel chunks of bf16 hi/lo (B operand of phase A), plus a zero row
-    const int64_t fcount = (int64_t)(n + 1) * nchk * (kBtKc / 8);   // one thread per 8 channels
+    // features as 32-channel chunks of bf16 hi/lo (64-channel chunks of the values for bfloat16
+    // features): the B operand of phase A, plus a zero row
+    const int64_t fcount = (int64_t)(n + 1) * nchk * ((fdt == kDtBF16 ? kBtKcBf : kBtKc) / 8);   // one thread per 8 channels
     if (fdt == kDtBF16)
         G2V_LAUNCH(k_split_chunks<__bf16>, dim3((unsigned)ceil_div(fcount, 256)), dim3(256), 0, s,
                    static_cast<const __bf16*>(features), n, C, nchk, b.fsp);
@@ -1300,7 +1326,7 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
     if (n <= 0) return hipSuccess;
     const Regions RG = make_regions(G);
     const int T = G.tiles[0] * G.tiles[1] * G.tiles[2];
-    const int nchk = feature_chunks(C);
+    const int nchk = feature_chunks(C, fdt);
     if (!split_rows_fit(n, C)) return hipErrorInvalidValue;   // byte offsets of the split rows are 32-bit
     const FeatBufs b = carve_feats(ws, G, n, C, M, MR);
     const PlanBufs pb = carve_plan(const_cast<void*>(plan_ws), n);

@@ -6,10 +6,13 @@ float32 path fed with the same values (features.bfloat16().float()) multiplies e
 operands.  Bars:
   * density: identical to the float32 path on the same values;
   * grid_feats: the float32 path's grid_feats rounded to bfloat16 (nearest even), bit for bit;
-  * gradients of means, covariances, opacity: identical to the float32 path (fed the upstream
+  * gradients of means, covariances, opacity: within rel 1e-5 of the float32 path (fed the upstream
     feature gradient rounded to bfloat16, as the bfloat16 path takes it) when no tile list needs a
-    second pass (the only place grid_feats itself is read back); the feature gradient is the
-    float32 path's rounded to bfloat16, bit for bit;
+    second pass (the only place grid_feats itself is read back).  They are not bit-equal: the
+    bfloat16 path sums u = gF . f over 64-channel chunks, the float32 path over 32-channel ones,
+    so the float32 partial sums are grouped differently;
+  * the feature gradient is the float32 path's rounded to bfloat16, bit for bit (its products do
+    not depend on that grouping);
   * against the float64 oracle on the rounded features: density rel < 1e-4, grid_feats and the
     feature gradient rel < 1e-2 (bfloat16 output rounding, 2^-9 relative per element).
 """
@@ -91,7 +94,7 @@ def test_bf16_features_match_float32_path(name):
                                           of[0], of[5], fb.float().to(dev))
     assert gb[3].dtype == torch.bfloat16
     for k in range(3):
-        assert torch.equal(gb[k], gf[k]), k
+        assert O.rel_err(gb[k].cpu().numpy(), gf[k].cpu().numpy()) < 1e-5, k
     assert torch.equal(gb[3], gf[3].to(torch.bfloat16))
     ref = O.backward_f64(gD.cpu().numpy(), gF.cpu().numpy(), m.numpy(), o.numpy(), c.numpy(), fb.float().numpy(),
                          b["lb"], b["ub"], np.array(w.voxel_size, np.float32), np.array(w.voxel_range, np.float32),
