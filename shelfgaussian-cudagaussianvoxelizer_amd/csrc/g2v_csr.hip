@@ -581,27 +581,30 @@ hipError_t radix_sort_pairs(const int* keys_in, const int* vals_in, int* keys_ou
 }
 
 // ------------------------------------------------------------------------------------------
-// Tile offsets for every tile from the sorted keys: toff[t] = first sorted index with key >= t.
+// Tile offsets for every tile from the sorted keys: toff[t] = first sorted index with key >= t,
+// toff[T] = M.  One lower-bound search per tile (about log2 M dependent loads), so the time does
+// not depend on how the keys are spread: long runs of empty tiles cost nothing extra.  Every
+// entry lies in [0, M] whatever the keys hold.
 // ------------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) k_tile_offsets(const int* __restrict__ keys, int64_t M, int T,
                                                       int* __restrict__ toff) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i > M) return;
-    // keys are clamped to [0, T-1] so that a malformed CSR cannot write outside toff
-    if (i < M) {
-        const int k = min(max(keys[i], 0), T - 1);
-        const int prev = (i == 0) ? -1 : min(max(keys[i - 1], 0), T - 1);
-        for (int t = prev + 1; t <= k; ++t) toff[t] = (int)i;
-    } else {
-        const int last = (M == 0) ? -1 : min(max(keys[M - 1], 0), T - 1);
-        for (int t = last + 1; t <= T; ++t) toff[t] = (int)M;
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    if (t > T) return;
+    int64_t lo = 0, hi = M;
+    if (t == T) lo = M;
+    while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (keys[mid] < t) lo = mid + 1;
+        else hi = mid;
     }
+    toff[t] = (int)lo;
 }
 
 hipError_t launch_tile_offsets(const int* sorted_keys, int64_t M, int T, int* tile_offsets,
                                hipStream_t s) {
-    G2V_LAUNCH(k_tile_offsets, dim3((unsigned)ceil_div(M + 1, 256)), dim3(256), 0, s,
-                       sorted_keys, M, T, tile_offsets);
+    if (T < 0) return hipErrorInvalidValue;
+    G2V_LAUNCH(k_tile_offsets, dim3((unsigned)ceil_div((int64_t)T + 1, 256)), dim3(256), 0, s,
+               sorted_keys, M, T, tile_offsets);
     return hipGetLastError();
 }
 
