@@ -343,6 +343,30 @@ def _backward(grad_output, grad_feats_output, means3D, opacity, cov_inv, voxel_s
 _COUNTS = {}
 
 
+_SIDE_STREAMS = {}
+
+
+def _side_streams(dev, k):
+    """k side streams of the device (created once, default priority) for the scenes of a batch."""
+    lst = _SIDE_STREAMS.setdefault(dev.index, [])
+    while len(lst) < k:
+        lst.append(torch.cuda.Stream(device=dev))
+    return lst[:k]
+
+
+# scenes of one batch run on up to this many streams at once (their CSR kernels and their sparse
+# phases leave most of the chip idle)
+_BATCH_STREAMS = 4
+
+
+def _join(cur, streams):
+    """Makes cur wait for all the work queued so far on streams."""
+    for st in streams:
+        e = torch.cuda.Event()
+        e.record(st)
+        cur.wait_event(e)
+
+
 def _pinned_counts(dev, B):
     """A reusable pinned (B, 2) int64 host buffer per device and thread (count read-back)."""
     import threading
@@ -425,7 +449,18 @@ def _forward_batched(means3D, opacity, covariances, voxel_size, voxel_range, fea
         cur.synchronize()   # the one host wait of the batch
         cnt = counts.tolist()
         results = []
+        # scene b's splat (and backward preparation) runs on side stream b % K, after the plan; every
+        # tensor allocated here on cur and used there is recorded on that stream, and cur waits for
+        # all of them before the stop event
+        sides = _side_streams(dev, min(B, _BATCH_STREAMS)) if B > 1 else [cur]
+        ready = torch.cuda.Event()
+        ready.record(cur)
+        for st in sides:
+            if st is not cur:
+                st.wait_event(ready)
         for b in range(B):
+            side = sides[b % len(sides)]
+            sstream = ctypes.c_void_p(side.cuda_stream)
             M, MR = int(cnt[b][0]), int(cnt[b][1])
             if M > 2147483647 or MR > 2147483647:
                 raise RuntimeError(f"scene {b}: pair counts {M}, {MR} exceed the int32 CSR")
@@ -441,25 +476,38 @@ def _forward_batched(means3D, opacity, covariances, voxel_size, voxel_range, fea
                                              _ptr(cov_inv[b]), _ptr(lb[b]), _ptr(ub[b]), _ptr(g2t_offsets[b]), M,
                                              _ptr(g2t_tile_ids), _ptr(density[b]), _ptr(grid_feats[b]),
                                              _ptr(csr[0]), _ptr(csr[1]), _ptr(csr[2]), _ptr(ws2), ws2.numel(),
-                                             stream),
+                                             sstream),
                        "gaussian_voxelizer_forward_batched (splat)")
+            if side is not cur:
+                for t in (g2t_tile_ids, ws2) + tuple(t for t in csr if t is not None):
+                    t.record_stream(side)
+            if t2g is not None:
+                t2g["stream"] = side
             results.append([[density[b], cov_inv[b], lb[b], ub[b], nvox[b], grid_feats[b], g2t_offsets[b],
                              g2t_tile_ids, 0.0], t2g])
+        _join(cur, [st for st in sides if st is not cur])
         stop.record(cur)
         if keep_t2g:
             for b, (r, t2g) in enumerate(results):
                 M = r[7].numel()
+                side = t2g["stream"]
                 t2g["grads"] = (torch.empty(n, 3, **f32), torch.empty(n, 9, **f32), torch.empty(n, **f32),
                                 torch.empty(n, C, dtype=fdtype, device=dev))
                 t2g["ws"] = torch.empty(max(1, lib.g2v_backward_workspace(n, C, M, t2g["num_region_pairs"], vs, vr)),
                                         dtype=torch.uint8, device=dev)
+                if side is not cur:
+                    for t in t2g["grads"] + (t2g["ws"],):
+                        t.record_stream(side)
                 if C > 0:
                     _lib.check(lib.g2v_backward_prepare(n, C, vs, vr, _ptr(lb[b]), _ptr(ub[b]), _ptr(feats[b]), fdt, M,
                                                         t2g["num_region_pairs"], _ptr(t2g["csr"][0]),
                                                         _ptr(t2g["csr"][1]), _ptr(t2g["plan"]), _ptr(t2g["ws"]),
-                                                        t2g["ws"].numel(), stream),
+                                                        t2g["ws"].numel(), ctypes.c_void_p(side.cuda_stream)),
                                "gaussian_voxelizer_forward_batched (backward preparation)")
                     t2g["prepared"] = True
+                # the backward of this scene starts after its preparation
+                t2g["ready"] = torch.cuda.Event()
+                t2g["ready"].record(side)
         stop.synchronize()
         fwd_sec = start.elapsed_time(stop) / 1000.0
     out = []
@@ -480,12 +528,28 @@ def _backward_batched(grad_density, grad_feats, means, opacity, features, scenes
         start, stop = _timing_events(dev)
         start.record(cur)
         grads = []
+        keep = []   # tensors made here on cur and used on a side stream, alive until the join
+        # scene b runs on the side stream of its forward, after the upstream gradients (cur) and its
+        # backward preparation
+        ready = torch.cuda.Event()
+        ready.record(cur)
+        used = []
         for b, (r, t2g) in enumerate(scenes):
             (density, cov_inv, lb, ub, nvox, gfeat, g2t_offsets, g2t_tile_ids, _) = r
             fb = None if features is None else features[b]
             gF = grad_feats[b] if grad_feats is not None and grad_feats.shape[-1] > 0 else gfeat.new_zeros(gfeat.shape)
-            grads.append(_backward(grad_density[b], gF, means[b], opacity[b], cov_inv, None, None, lb, ub, nvox,
-                                   g2t_offsets, g2t_tile_ids, density, gfeat, fb, t2g=t2g, timed=False))
+            keep.append(gF)
+            side = (t2g or {}).get("stream", cur)
+            if side is not cur:
+                side.wait_event(ready)
+                if t2g.get("ready") is not None:
+                    side.wait_event(t2g["ready"])
+                if side not in used:
+                    used.append(side)
+            with torch.cuda.stream(side):
+                grads.append(_backward(grad_density[b], gF, means[b], opacity[b], cov_inv, None, None, lb, ub, nvox,
+                                       g2t_offsets, g2t_tile_ids, density, gfeat, fb, t2g=t2g, timed=False))
+        _join(cur, used)
         stop.record(cur)
         stop.synchronize()
         bwd_sec = start.elapsed_time(stop) / 1000.0
