@@ -77,22 +77,31 @@ def test_batched_forward_equals_single_scene_calls(C):
     assert O.rel_err(outs[b][0].cpu().numpy(), D) < 1e-4
 
 
-@pytest.mark.parametrize("C", [None, 16])
-def test_batched_module_gradients_equal_single_scene_module(C):
+# B = 6 puts two scenes on each of the first two of the four side streams; the batch runs twice in
+# a row (the second call reuses the streams and the memory of the first)
+@pytest.mark.parametrize("B,C", [(3, None), (3, 16), (6, 16)])
+def test_batched_module_gradients_equal_single_scene_module(B, C):
     from CudaGaussianVoxelizer import PyCudaGaussianVoxelizer
     dev = torch.device("cuda")
-    m, o, c, f = _batch(3, 500, C, seed=40)
+    m, o, c, f = _batch(B, 500, C, seed=40)
     vox = PyCudaGaussianVoxelizer(voxel_size=list(W.VOXEL), voxel_range=list(W.RANGE_SMALL))
-    say(f"[batched] module B=3 C={C}")
-    leaves = [t.to(dev).requires_grad_() for t in (m, o, c)] + ([] if f is None else [f.to(dev).requires_grad_()])
-    density, grid_feats, stats = vox(leaves[0], leaves[1], leaves[2], None if f is None else leaves[3])
-    assert density.shape[0] == 3 and grid_feats.shape[0] == 3 and stats[0] > 0
+    say(f"[batched] module B={B} C={C}")
     g = torch.Generator().manual_seed(3)
-    gD = torch.randn(*density.shape, generator=g).to(dev)
-    gF = torch.randn(*grid_feats.shape, generator=g).to(dev)
-    torch.autograd.backward([density] if f is None else [density, grid_feats], [gD] if f is None else [gD, gF])
-    assert stats[1] > 0
-    for b in range(3):
+    gD = gF = None
+    for rep in range(2):
+        leaves = [t.to(dev).requires_grad_() for t in (m, o, c)] + ([] if f is None else [f.to(dev).requires_grad_()])
+        density, grid_feats, stats = vox(leaves[0], leaves[1], leaves[2], None if f is None else leaves[3])
+        assert density.shape[0] == B and grid_feats.shape[0] == B and stats[0] > 0
+        if gD is None:
+            gD = torch.randn(*density.shape, generator=g).to(dev)
+            gF = torch.randn(*grid_feats.shape, generator=g).to(dev)
+        torch.autograd.backward([density] if f is None else [density, grid_feats], [gD] if f is None else [gD, gF])
+        assert stats[1] > 0
+        if rep == 0:
+            first = [t.grad.clone() for t in leaves]
+    for a, t in zip(first, leaves):
+        assert torch.equal(a, t.grad)
+    for b in range(B):
         lb_ = [t[b].detach().clone().requires_grad_() for t in (leaves[0], leaves[1], leaves[2])]
         fb = None if f is None else leaves[3][b].detach().clone().requires_grad_()
         d1, f1, _ = vox(lb_[0], lb_[1], lb_[2], fb)
