@@ -274,7 +274,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
-              "(the G2V path runs on a single MI355X; see DESIGN.md for how it would shard)",
+              "(the G2V path runs on a single MI355X; sharding it across GPUs is not built)",
               file=sys.stderr)
         sys.exit(2)
     import torch
