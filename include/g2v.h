@@ -171,7 +171,9 @@ int g2v_build_t2g(int n, const float voxel_size[3], const float voxel_range[6],
  * Replaces CudaFeatsCosinelossForward / CudaFeatsCosinelossBackward (src/cuda_feats_loss.cu:154-231
  * and :311-366, bound at src/bindings.cpp:67-104).  Over num_voxels = X*Y*Z voxels with
  * voxel_label (X,Y,Z) float32, occ_mask (X,Y,Z) bool (one byte, 0 or 1), grid_feats and pseudo_gt
- * (X,Y,Z,feat_dim) float32, a voxel is valid when occ_mask != 0 and voxel_label > 0, and
+ * (X,Y,Z,feat_dim) of feat_dtype (G2V_DTYPE_F32, as the reference, or G2V_DTYPE_BF16: both tensors,
+ * and grad_grid_feats, then hold bfloat16; the sums are float32), a voxel is valid when
+ * occ_mask != 0 and voxel_label > 0, and
  *     loss = mean over valid voxels of 1 - p.g / (sqrt(max(|p|^2,1e-6)) sqrt(max(|g|^2,1e-6)) + 1e-6)
  * (0 when no voxel is valid).
  *
@@ -181,16 +183,17 @@ int g2v_build_t2g(int n, const float voxel_size[3], const float voxel_range[6],
  * The workspace (g2v_cosine_loss_workspace bytes) holds per-block partial sums. */
 size_t g2v_cosine_loss_workspace(long long num_voxels, int feat_dim);
 int g2v_cosine_loss_forward(long long num_voxels, int feat_dim, const float* voxel_label,
-                            const unsigned char* occ_mask, const float* grid_feats, const float* pseudo_gt,
-                            float* loss, int* num_valid, int* num_valid_host, void* workspace,
+                            const unsigned char* occ_mask, const void* grid_feats, const void* pseudo_gt,
+                            int feat_dtype, float* loss, int* num_valid, int* num_valid_host, void* workspace,
                             size_t workspace_bytes, void* stream);
 
 /* g2v_cosine_loss_backward writes d loss / d grid_feats (X,Y,Z,feat_dim) for the upstream scalar
  * gradient grad_output (a device float: no host read, where the reference calls .item()) and the
  * forward's valid-voxel count; zero on invalid voxels.  Asynchronous, needs no workspace. */
 int g2v_cosine_loss_backward(long long num_voxels, int feat_dim, const float* grad_output,
-                             const float* voxel_label, const unsigned char* occ_mask, const float* grid_feats,
-                             const float* pseudo_gt, int num_valid_voxel, float* grad_grid_feats, void* stream);
+                             const float* voxel_label, const unsigned char* occ_mask, const void* grid_feats,
+                             const void* pseudo_gt, int feat_dtype, int num_valid_voxel, void* grad_grid_feats,
+                             void* stream);
 
 /* ---- covariances from scales and rotations -------------------------------------------------
  * The covariance construction that ShelfGaussian runs before the voxelizer (reference

@@ -596,11 +596,15 @@ def build_t2g(voxel_size, voxel_range, valid_voxel_lb, valid_voxel_ub, g2t_offse
 
 def _cosine_inputs(voxel_label, occ_gt_mask_camera, grid_feats, pseudo_dino_gt):
     """The reference's input checks (src/cuda_feats_loss.cu:158-161: dtype, contiguity, device; a
-    failure is a RuntimeError) plus the shape agreement its 3-D / 4-D accessors assume."""
+    failure is a RuntimeError) plus the shape agreement its 3-D / 4-D accessors assume.  grid_feats
+    may also be bfloat16 (as the voxelizer returns it for bfloat16 features); pseudo_dino_gt then
+    has to be bfloat16 too."""
+    fdtype = grid_feats.dtype if isinstance(grid_feats, torch.Tensor) and grid_feats.dtype in _FEAT_DTYPES \
+        else torch.float32
     for t, name, dt in ((voxel_label, "voxel_label", torch.float32),
                         (occ_gt_mask_camera, "occ_gt_mask_camera", torch.bool),
-                        (grid_feats, "grid_feats", torch.float32),
-                        (pseudo_dino_gt, "pseudo_dino_gt", torch.float32)):
+                        (grid_feats, "grid_feats", fdtype),
+                        (pseudo_dino_gt, "pseudo_dino_gt", fdtype)):
         if not isinstance(t, torch.Tensor) or t.dtype != dt or not t.is_contiguous() or t.device.type != "cuda":
             raise RuntimeError(f"{name} must be a contiguous {dt} GPU tensor")
     if voxel_label.dim() != 3 or grid_feats.dim() != 4:
@@ -616,20 +620,20 @@ def _cosine_inputs(voxel_label, occ_gt_mask_camera, grid_feats, pseudo_dino_gt):
                     (pseudo_dino_gt, "pseudo_dino_gt")):
         if t.device != dev:
             raise RuntimeError(f"{name} is on {t.device}, grid_feats on {dev}")
-    return voxel_label.numel(), grid_feats.shape[3], dev
+    return voxel_label.numel(), grid_feats.shape[3], dev, _FEAT_DTYPES[fdtype]
 
 
 def CudaFeatsCosinelossForward(voxel_label, occ_gt_mask_camera, grid_feats, pseudo_dino_gt):
     """Voxel-wise cosine loss (reference src/cuda_feats_loss.cu:154-231, bound at src/bindings.cpp:67-83).
 
     Args: voxel_label (X,Y,Z) float32, occ_gt_mask_camera (X,Y,Z) bool, grid_feats and
-    pseudo_dino_gt (X,Y,Z,C) float32, all contiguous on the GPU.
+    pseudo_dino_gt (X,Y,Z,C) float32 (or both bfloat16), all contiguous on the GPU.
     Returns the reference's 3-tuple: the mean over valid voxels (mask and label > 0) of
     1 - cos(grid_feats, pseudo_dino_gt) as a 0-dim GPU tensor (0 without valid voxels), the number
     of valid voxels (int) and the forward time in seconds.
     """
     lib = _lib.load()
-    V, C, dev = _cosine_inputs(voxel_label, occ_gt_mask_camera, grid_feats, pseudo_dino_gt)
+    V, C, dev, fdt = _cosine_inputs(voxel_label, occ_gt_mask_camera, grid_feats, pseudo_dino_gt)
     with _OnDevice(dev):
         cur = torch.cuda.current_stream(dev)
         loss = torch.empty((), dtype=torch.float32, device=dev)
@@ -639,7 +643,7 @@ def CudaFeatsCosinelossForward(voxel_label, occ_gt_mask_camera, grid_feats, pseu
         start, stop = _timing_events(dev)
         start.record(cur)
         _lib.check(lib.g2v_cosine_loss_forward(V, C, _ptr(voxel_label), _ptr(occ_gt_mask_camera),
-                                               _ptr(grid_feats), _ptr(pseudo_dino_gt), _ptr(loss),
+                                               _ptr(grid_feats), _ptr(pseudo_dino_gt), fdt, _ptr(loss),
                                                _ptr(cnt_dev), ctypes.byref(cnt), _ptr(ws), ws.numel(),
                                                ctypes.c_void_p(cur.cuda_stream)),
                    "CudaFeatsCosinelossForward")
@@ -656,10 +660,11 @@ def CudaFeatsCosinelossBackward(grad_output, voxel_label, occ_gt_mask_camera, gr
 
     grad_output is the upstream gradient of the scalar loss (one element); it is read on the GPU,
     without the reference's host round trip.  Returns (grad_grid_feats (X,Y,Z,C), backward time in
-    seconds); the gradient is zero on invalid voxels.
+    seconds); the gradient is zero on invalid voxels and has grid_feats' type (a bfloat16 gradient is
+    the float value rounded to nearest even).
     """
     lib = _lib.load()
-    V, C, dev = _cosine_inputs(voxel_label, occ_gt_mask_camera, grid_feats, pseudo_dino_gt)
+    V, C, dev, fdt = _cosine_inputs(voxel_label, occ_gt_mask_camera, grid_feats, pseudo_dino_gt)
     if not isinstance(grad_output, torch.Tensor) or grad_output.numel() != 1:
         raise RuntimeError("grad_output must be a one-element tensor")
     with _OnDevice(dev):
@@ -669,7 +674,7 @@ def CudaFeatsCosinelossBackward(grad_output, voxel_label, occ_gt_mask_camera, gr
         start, stop = _timing_events(dev)
         start.record(cur)
         _lib.check(lib.g2v_cosine_loss_backward(V, C, _ptr(gout), _ptr(voxel_label), _ptr(occ_gt_mask_camera),
-                                                _ptr(grid_feats), _ptr(pseudo_dino_gt), int(num_valid_voxel),
+                                                _ptr(grid_feats), _ptr(pseudo_dino_gt), fdt, int(num_valid_voxel),
                                                 _ptr(grad_p), ctypes.c_void_p(cur.cuda_stream)),
                    "CudaFeatsCosinelossBackward")
         stop.record(cur)

@@ -44,8 +44,8 @@ SIGNATURES = {
     "g2v_build_t2g": (_i, [_i, _f3, _f3, _vp, _vp, _vp, _vp, _ll, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                            _vp, _sz, _vp]),
     "g2v_cosine_loss_workspace": (_sz, [_ll, _i]),
-    "g2v_cosine_loss_forward": (_i, [_ll, _i, _vp, _vp, _vp, _vp, _vp, _vp, _ip, _vp, _sz, _vp]),
-    "g2v_cosine_loss_backward": (_i, [_ll, _i, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp]),
+    "g2v_cosine_loss_forward": (_i, [_ll, _i, _vp, _vp, _vp, _vp, _i, _vp, _vp, _ip, _vp, _sz, _vp]),
+    "g2v_cosine_loss_backward": (_i, [_ll, _i, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp]),
     "g2v_covariance_from_scale_rotation": (_i, [_i, _vp, _vp, _vp, _vp]),
     "g2v_covariance_from_scale_rotation_backward": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _vp]),
     "g2v_profile_enable": (_i, [_i]),

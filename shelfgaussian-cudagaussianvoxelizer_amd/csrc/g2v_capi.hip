@@ -123,7 +123,7 @@ extern "C" {
 
 const char* g2v_last_error(void) { return g_err; }
 
-int g2v_abi_version(void) { return 8; }
+int g2v_abi_version(void) { return 9; }
 
 int g2v_grid_dims(const float voxel_size[3], const float voxel_range[6], int dims[3], int tiles[3]) {
     Grid G;
@@ -550,10 +550,12 @@ size_t g2v_cosine_loss_workspace(long long num_voxels, int feat_dim) {
 }
 
 int g2v_cosine_loss_forward(long long num_voxels, int feat_dim, const float* voxel_label,
-                            const unsigned char* occ_mask, const float* grid_feats, const float* pseudo_gt,
-                            float* loss, int* num_valid, int* num_valid_host, void* workspace,
+                            const unsigned char* occ_mask, const void* grid_feats, const void* pseudo_gt,
+                            int feat_dtype, float* loss, int* num_valid, int* num_valid_host, void* workspace,
                             size_t workspace_bytes, void* stream) {
     g_err[0] = 0;
+    if (feat_dtype != G2V_DTYPE_F32 && feat_dtype != G2V_DTYPE_BF16)
+        return fail(G2V_ERR_INVALID, "feat_dtype = %d (G2V_DTYPE_F32 or G2V_DTYPE_BF16)", feat_dtype);
     if (num_voxels < 0 || feat_dim < 0)
         return fail(G2V_ERR_INVALID, "num_voxels = %lld, feat_dim = %d", num_voxels, feat_dim);
     if (num_voxels > 2147483647ll)
@@ -564,8 +566,8 @@ int g2v_cosine_loss_forward(long long num_voxels, int feat_dim, const float* vox
     int rc = check_ws(workspace, workspace_bytes, g2v_cosine_loss_workspace(num_voxels, feat_dim), "cosine loss");
     if (rc != G2V_OK) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    G2V_HIP(launch_cosine_forward(num_voxels, feat_dim, voxel_label, occ_mask, grid_feats, pseudo_gt, loss,
-                                  num_valid, workspace, s));
+    G2V_HIP(launch_cosine_forward(num_voxels, feat_dim, voxel_label, occ_mask, grid_feats, pseudo_gt, feat_dtype,
+                                  loss, num_valid, workspace, s));
     if (num_valid_host) {
         int h = 0;
         G2V_HIP(hipMemcpyAsync(&h, num_valid, sizeof(int), hipMemcpyDeviceToHost, s));
@@ -576,9 +578,12 @@ int g2v_cosine_loss_forward(long long num_voxels, int feat_dim, const float* vox
 }
 
 int g2v_cosine_loss_backward(long long num_voxels, int feat_dim, const float* grad_output,
-                             const float* voxel_label, const unsigned char* occ_mask, const float* grid_feats,
-                             const float* pseudo_gt, int num_valid_voxel, float* grad_grid_feats, void* stream) {
+                             const float* voxel_label, const unsigned char* occ_mask, const void* grid_feats,
+                             const void* pseudo_gt, int feat_dtype, int num_valid_voxel, void* grad_grid_feats,
+                             void* stream) {
     g_err[0] = 0;
+    if (feat_dtype != G2V_DTYPE_F32 && feat_dtype != G2V_DTYPE_BF16)
+        return fail(G2V_ERR_INVALID, "feat_dtype = %d (G2V_DTYPE_F32 or G2V_DTYPE_BF16)", feat_dtype);
     if (num_voxels < 0 || feat_dim < 0)
         return fail(G2V_ERR_INVALID, "num_voxels = %lld, feat_dim = %d", num_voxels, feat_dim);
     if (num_voxels == 0 || feat_dim == 0) return G2V_OK;
@@ -586,7 +591,7 @@ int g2v_cosine_loss_backward(long long num_voxels, int feat_dim, const float* gr
         return fail(G2V_ERR_INVALID, "null input/output pointer");
     // the reference's host-side scale (src/cuda_feats_loss.cu:319)
     const float inv_count = num_valid_voxel > 0 ? 1.0f / (float)num_valid_voxel : 0.0f;
-    G2V_HIP(launch_cosine_backward(num_voxels, feat_dim, voxel_label, occ_mask, grid_feats, pseudo_gt,
+    G2V_HIP(launch_cosine_backward(num_voxels, feat_dim, voxel_label, occ_mask, grid_feats, pseudo_gt, feat_dtype,
                                    grad_output, inv_count, grad_grid_feats, static_cast<hipStream_t>(stream)));
     return G2V_OK;
 }

@@ -17,6 +17,9 @@
 // reference sums with float atomics).  Everything is a single streaming pass over HBM: the
 // forward reads p and g once (8 C bytes per valid voxel), the backward reads them once more and
 // writes the gradient with non-temporal stores (12 C bytes per valid voxel, 4 C per other voxel).
+// grid_feats, pseudo_gt and the gradient share one element type T, float or bfloat16 (half the
+// bytes); the arithmetic is float, and a bfloat16 gradient is the float value rounded to nearest
+// even.
 #include "../../include/g2v.h"
 #include "g2v_internal.h"
 
@@ -43,6 +46,20 @@ __device__ __forceinline__ float group_sum(float x) {
     return x;
 }
 
+// Four consecutive elements 4q..4q+3 as floats (one 16-byte or 8-byte non-temporal load), and the
+// matching store; single elements for the unaligned path.
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+template <typename T>
+__device__ __forceinline__ f32x4 load4(const T* __restrict__ p, int64_t q) {
+    if constexpr (std::is_same<T, float>::value) return __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p) + q);
+    else return __builtin_convertvector(__builtin_nontemporal_load(reinterpret_cast<const bf16x4_t*>(p) + q), f32x4);
+}
+template <typename T>
+__device__ __forceinline__ void store4(T* __restrict__ p, int64_t q, f32x4 v) {
+    if constexpr (std::is_same<T, float>::value) __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p) + q);
+    else __builtin_nontemporal_store(__builtin_convertvector(v, bf16x4_t), reinterpret_cast<bf16x4_t*>(p) + q);
+}
+
 __device__ __forceinline__ float cos_loss(float dot, float pp, float gg) {
     const float pn = sqrtf(fmaxf(pp, kEps));
     const float gn = sqrtf(fmaxf(gg, kEps));
@@ -61,18 +78,16 @@ __device__ __forceinline__ void cos_coefs(float dot, float pp, float gg, float s
 }
 
 // Row sums dot(p,g), |p|^2, |g|^2 of one voxel by a group of L lanes (lane gl of the group).
-template <int L, bool VEC>
-__device__ __forceinline__ void row_sums(const float* __restrict__ p, const float* __restrict__ g, int C,
+template <int L, bool VEC, typename T>
+__device__ __forceinline__ void row_sums(const T* __restrict__ p, const T* __restrict__ g, int C,
                                          int gl, float& dot, float& pp, float& gg) {
     float d = 0.0f, a = 0.0f, b = 0.0f;
     if constexpr (VEC) {
-        const f32x4* p4 = reinterpret_cast<const f32x4*>(p);
-        const f32x4* g4 = reinterpret_cast<const f32x4*>(g);
         const int C4 = C >> 2;
 #pragma unroll 4
         for (int c = gl; c < C4; c += L) {
-            const f32x4 x = __builtin_nontemporal_load(p4 + c);
-            const f32x4 y = __builtin_nontemporal_load(g4 + c);
+            const f32x4 x = load4(p, c);
+            const f32x4 y = load4(g, c);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 d += x[i] * y[i];
@@ -83,7 +98,7 @@ __device__ __forceinline__ void row_sums(const float* __restrict__ p, const floa
     } else {
 #pragma unroll 4
         for (int c = gl; c < C; c += L) {
-            const float x = p[c], y = g[c];
+            const float x = (float)p[c], y = (float)g[c];
             d += x * y;
             a += x * x;
             b += y * y;
@@ -95,12 +110,12 @@ __device__ __forceinline__ void row_sums(const float* __restrict__ p, const floa
 }
 
 // Forward: block b sums the losses and counts the valid voxels of voxels [b vpb, (b+1) vpb).
-template <int L, bool VEC>
+template <int L, bool VEC, typename T>
 __global__ void __launch_bounds__(kCosThreads) k_cos_fwd(int64_t V, int C, int vpb,
                                                           const float* __restrict__ label,
                                                           const uint8_t* __restrict__ mask,
-                                                          const float* __restrict__ p,
-                                                          const float* __restrict__ g,
+                                                          const T* __restrict__ p,
+                                                          const T* __restrict__ g,
                                                           float* __restrict__ part_loss,
                                                           int* __restrict__ part_cnt) {
     constexpr int G = kCosThreads / L;
@@ -114,7 +129,7 @@ __global__ void __launch_bounds__(kCosThreads) k_cos_fwd(int64_t V, int C, int v
     for (int64_t v = v0 + grp; v < v1; v += G) {
         if (!cos_valid(label, mask, v)) continue;
         float dot, pp, gg;
-        row_sums<L, VEC>(p + v * C, g + v * C, C, gl, dot, pp, gg);
+        row_sums<L, VEC, T>(p + v * C, g + v * C, C, gl, dot, pp, gg);
         lsum += cos_loss(dot, pp, gg);
         ++cnt;
     }
@@ -167,14 +182,14 @@ __global__ void __launch_bounds__(kCosFinalThreads) k_cos_final(int nparts, cons
 
 // Backward, rows held in registers (C <= 4 L NV, 16-byte aligned rows): one voxel per group and
 // iteration over the block's voxel range.
-template <int L, int NV>
+template <int L, int NV, typename T>
 __global__ void __launch_bounds__(kCosThreads) k_cos_bwd(int64_t V, int C, int vpb,
                                                           const float* __restrict__ label,
                                                           const uint8_t* __restrict__ mask,
-                                                          const float* __restrict__ p,
-                                                          const float* __restrict__ g,
+                                                          const T* __restrict__ p,
+                                                          const T* __restrict__ g,
                                                           const float* __restrict__ grad_out, float inv_count,
-                                                          float* __restrict__ grad_p) {
+                                                          T* __restrict__ grad_p) {
     constexpr int G = kCosThreads / L;
     const int grp = threadIdx.x / L, gl = threadIdx.x % L;
     const int C4 = C >> 2;
@@ -182,23 +197,23 @@ __global__ void __launch_bounds__(kCosThreads) k_cos_bwd(int64_t V, int C, int v
     const int64_t v0 = (int64_t)blockIdx.x * vpb;
     const int64_t v1 = min(v0 + vpb, V);
     for (int64_t v = v0 + grp; v < v1; v += G) {
-        f32x4* out = reinterpret_cast<f32x4*>(grad_p + v * C);
+        T* out = grad_p + v * C;
         if (!cos_valid(label, mask, v)) {
 #pragma unroll
             for (int j = 0; j < NV; ++j) {
                 const int c = gl + L * j;
-                if (c < C4) __builtin_nontemporal_store(f32x4{}, out + c);
+                if (c < C4) store4(out, c, f32x4{});
             }
             continue;
         }
-        const f32x4* p4 = reinterpret_cast<const f32x4*>(p + v * C);
-        const f32x4* g4 = reinterpret_cast<const f32x4*>(g + v * C);
+        const T* pr = p + v * C;
+        const T* gr = g + v * C;
         f32x4 x[NV], y[NV];
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             const int c = gl + L * j;
-            x[j] = c < C4 ? __builtin_nontemporal_load(p4 + c) : f32x4{};
-            y[j] = c < C4 ? __builtin_nontemporal_load(g4 + c) : f32x4{};
+            x[j] = c < C4 ? load4(pr, c) : f32x4{};
+            y[j] = c < C4 ? load4(gr, c) : f32x4{};
         }
         float d = 0.0f, a = 0.0f, b = 0.0f;
 #pragma unroll
@@ -214,38 +229,38 @@ __global__ void __launch_bounds__(kCosThreads) k_cos_bwd(int64_t V, int C, int v
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             const int c = gl + L * j;
-            if (c < C4) __builtin_nontemporal_store(k1 * y[j] + k2 * x[j], out + c);
+            if (c < C4) store4(out, c, k1 * y[j] + k2 * x[j]);
         }
     }
 }
 
 // Backward for any C and alignment: row sums first, then a second pass over the row (re-read).
-template <int L>
+template <int L, typename T>
 __global__ void __launch_bounds__(kCosThreads) k_cos_bwd_any(int64_t V, int C, int vpb,
                                                               const float* __restrict__ label,
                                                               const uint8_t* __restrict__ mask,
-                                                              const float* __restrict__ p,
-                                                              const float* __restrict__ g,
+                                                              const T* __restrict__ p,
+                                                              const T* __restrict__ g,
                                                               const float* __restrict__ grad_out,
-                                                              float inv_count, float* __restrict__ grad_p) {
+                                                              float inv_count, T* __restrict__ grad_p) {
     constexpr int G = kCosThreads / L;
     const int grp = threadIdx.x / L, gl = threadIdx.x % L;
     const float scale = grad_out[0] * inv_count;
     const int64_t v0 = (int64_t)blockIdx.x * vpb;
     const int64_t v1 = min(v0 + vpb, V);
     for (int64_t v = v0 + grp; v < v1; v += G) {
-        float* out = grad_p + v * C;
+        T* out = grad_p + v * C;
         if (!cos_valid(label, mask, v)) {
-            for (int c = gl; c < C; c += L) out[c] = 0.0f;
+            for (int c = gl; c < C; c += L) out[c] = (T)0.0f;
             continue;
         }
-        const float* pr = p + v * C;
-        const float* gr = g + v * C;
+        const T* pr = p + v * C;
+        const T* gr = g + v * C;
         float dot, pp, gg;
-        row_sums<L, false>(pr, gr, C, gl, dot, pp, gg);
+        row_sums<L, false, T>(pr, gr, C, gl, dot, pp, gg);
         float k1, k2;
         cos_coefs(dot, pp, gg, scale, k1, k2);
-        for (int c = gl; c < C; c += L) out[c] = k1 * gr[c] + k2 * pr[c];
+        for (int c = gl; c < C; c += L) out[c] = (T)(k1 * (float)gr[c] + k2 * (float)pr[c]);
     }
 }
 
@@ -274,13 +289,20 @@ hipError_t dispatch_lanes(int L, F&& f) {
     }
 }
 
-template <int L, int NV>
+template <int L, int NV, typename T>
 hipError_t launch_bwd_nv(int64_t V, int C, int vpb, unsigned blocks, const float* label, const uint8_t* mask,
-                         const float* p, const float* g, const float* grad_out, float inv_count, float* grad_p,
+                         const T* p, const T* g, const float* grad_out, float inv_count, T* grad_p,
                          hipStream_t s) {
-    G2V_LAUNCH((k_cos_bwd<L, NV>), dim3(blocks), dim3(kCosThreads), 0, s, V, C, vpb, label, mask, p, g,
+    G2V_LAUNCH((k_cos_bwd<L, NV, T>), dim3(blocks), dim3(kCosThreads), 0, s, V, C, vpb, label, mask, p, g,
                grad_out, inv_count, grad_p);
     return hipGetLastError();
+}
+
+// f on the element type of fdt (float or bfloat16).
+template <typename F>
+hipError_t dispatch_type(int fdt, F&& f) {
+    if (fdt == kDtBF16) return f(__bf16{});
+    return f(float{});
 }
 
 }  // namespace
@@ -290,30 +312,38 @@ size_t cosine_workspace(int64_t V) {
     return (size_t)kCosMaxBlocks * (sizeof(float) + sizeof(int)) + 512;
 }
 
-bool cosine_vec_ok(int C, const void* a, const void* b, const void* c) {
-    const auto al = [](const void* q) { return q == nullptr || (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+bool cosine_vec_ok(int C, int esize, const void* a, const void* b, const void* c) {
+    // 4-element vectors: 16-byte (float) or 8-byte (bfloat16) aligned rows
+    const uintptr_t m = (uintptr_t)(4 * esize - 1);
+    const auto al = [m](const void* q) { return q == nullptr || (reinterpret_cast<uintptr_t>(q) & m) == 0; };
     return (C & 3) == 0 && al(a) && al(b) && al(c);
 }
 
-hipError_t launch_cosine_forward(int64_t V, int C, const float* label, const uint8_t* mask, const float* p,
-                                 const float* g, float* loss, int* count, void* ws, hipStream_t s) {
+hipError_t launch_cosine_forward(int64_t V, int C, const float* label, const uint8_t* mask, const void* p_,
+                                 const void* g_, int fdt, float* loss, int* count, void* ws, hipStream_t s) {
     Carver c(ws, (size_t)-1);
     float* part_loss = c.take<float>(kCosMaxBlocks);
     int* part_cnt = c.take<int>(kCosMaxBlocks);
-    const bool vec = cosine_vec_ok(C, p, g, nullptr);
+    const int esize = fdt == kDtBF16 ? 2 : 4;
+    const bool vec = cosine_vec_ok(C, esize, p_, g_, nullptr);
     const int L = lanes_for(vec ? C / 4 : C);
     const int vpb = voxels_per_block(V, L);
     const int blocks = V > 0 ? (int)ceil_div(V, vpb) : 0;
     if (blocks > 0) {
-        const hipError_t e = dispatch_lanes(L, [&](auto Lc) -> hipError_t {
-            constexpr int LL = decltype(Lc)::value;
-            if (vec)
-                G2V_LAUNCH((k_cos_fwd<LL, true>), dim3(blocks), dim3(kCosThreads), 0, s, V, C, vpb, label, mask,
-                           p, g, part_loss, part_cnt);
-            else
-                G2V_LAUNCH((k_cos_fwd<LL, false>), dim3(blocks), dim3(kCosThreads), 0, s, V, C, vpb, label, mask,
-                           p, g, part_loss, part_cnt);
-            return hipGetLastError();
+        const hipError_t e = dispatch_type(fdt, [&](auto tv) -> hipError_t {
+            using T = decltype(tv);
+            const T* p = static_cast<const T*>(p_);
+            const T* g = static_cast<const T*>(g_);
+            return dispatch_lanes(L, [&](auto Lc) -> hipError_t {
+                constexpr int LL = decltype(Lc)::value;
+                if (vec)
+                    G2V_LAUNCH((k_cos_fwd<LL, true, T>), dim3(blocks), dim3(kCosThreads), 0, s, V, C, vpb, label,
+                               mask, p, g, part_loss, part_cnt);
+                else
+                    G2V_LAUNCH((k_cos_fwd<LL, false, T>), dim3(blocks), dim3(kCosThreads), 0, s, V, C, vpb, label,
+                               mask, p, g, part_loss, part_cnt);
+                return hipGetLastError();
+            });
         });
         if (e != hipSuccess) return e;
     }
@@ -322,40 +352,47 @@ hipError_t launch_cosine_forward(int64_t V, int C, const float* label, const uin
     return hipGetLastError();
 }
 
-hipError_t launch_cosine_backward(int64_t V, int C, const float* label, const uint8_t* mask, const float* p,
-                                  const float* g, const float* grad_out, float inv_count, float* grad_p,
+hipError_t launch_cosine_backward(int64_t V, int C, const float* label, const uint8_t* mask, const void* p_,
+                                  const void* g_, int fdt, const float* grad_out, float inv_count, void* grad_p_,
                                   hipStream_t s) {
     if (V == 0 || C == 0) return hipSuccess;
-    const bool vec = cosine_vec_ok(C, p, g, grad_p);
+    const int esize = fdt == kDtBF16 ? 2 : 4;
+    const bool vec = cosine_vec_ok(C, esize, p_, g_, grad_p_);
     const int L = lanes_for(vec ? C / 4 : C);
     const int NV = vec ? (int)ceil_div(C / 4, L) : 0;
     const int vpb = voxels_per_block(V, L);
     const unsigned blocks = (unsigned)ceil_div(V, vpb);
-    if (vec && NV <= kCosMaxNv) {
+    return dispatch_type(fdt, [&](auto tv) -> hipError_t {
+        using T = decltype(tv);
+        const T* p = static_cast<const T*>(p_);
+        const T* g = static_cast<const T*>(g_);
+        T* grad_p = static_cast<T*>(grad_p_);
+        if (vec && NV <= kCosMaxNv) {
+            return dispatch_lanes(L, [&](auto Lc) -> hipError_t {
+                constexpr int LL = decltype(Lc)::value;
+                if constexpr (LL < 64) {
+                    // small rows: one vector per lane
+                    return launch_bwd_nv<LL, 1, T>(V, C, vpb, blocks, label, mask, p, g, grad_out, inv_count, grad_p, s);
+                } else {
+                    switch (NV) {
+                        case 1: return launch_bwd_nv<64, 1, T>(V, C, vpb, blocks, label, mask, p, g, grad_out, inv_count, grad_p, s);
+                        case 2: return launch_bwd_nv<64, 2, T>(V, C, vpb, blocks, label, mask, p, g, grad_out, inv_count, grad_p, s);
+                        case 3: return launch_bwd_nv<64, 3, T>(V, C, vpb, blocks, label, mask, p, g, grad_out, inv_count, grad_p, s);
+                        case 4: return launch_bwd_nv<64, 4, T>(V, C, vpb, blocks, label, mask, p, g, grad_out, inv_count, grad_p, s);
+                        case 5: return launch_bwd_nv<64, 5, T>(V, C, vpb, blocks, label, mask, p, g, grad_out, inv_count, grad_p, s);
+                        case 6: return launch_bwd_nv<64, 6, T>(V, C, vpb, blocks, label, mask, p, g, grad_out, inv_count, grad_p, s);
+                        case 7: return launch_bwd_nv<64, 7, T>(V, C, vpb, blocks, label, mask, p, g, grad_out, inv_count, grad_p, s);
+                        default: return launch_bwd_nv<64, 8, T>(V, C, vpb, blocks, label, mask, p, g, grad_out, inv_count, grad_p, s);
+                    }
+                }
+            });
+        }
         return dispatch_lanes(L, [&](auto Lc) -> hipError_t {
             constexpr int LL = decltype(Lc)::value;
-            if constexpr (LL < 64) {
-                // small rows: one vector per lane
-                return launch_bwd_nv<LL, 1>(V, C, vpb, blocks, label, mask, p, g, grad_out, inv_count, grad_p, s);
-            } else {
-                switch (NV) {
-                    case 1: return launch_bwd_nv<64, 1>(V, C, vpb, blocks, label, mask, p, g, grad_out, inv_count, grad_p, s);
-                    case 2: return launch_bwd_nv<64, 2>(V, C, vpb, blocks, label, mask, p, g, grad_out, inv_count, grad_p, s);
-                    case 3: return launch_bwd_nv<64, 3>(V, C, vpb, blocks, label, mask, p, g, grad_out, inv_count, grad_p, s);
-                    case 4: return launch_bwd_nv<64, 4>(V, C, vpb, blocks, label, mask, p, g, grad_out, inv_count, grad_p, s);
-                    case 5: return launch_bwd_nv<64, 5>(V, C, vpb, blocks, label, mask, p, g, grad_out, inv_count, grad_p, s);
-                    case 6: return launch_bwd_nv<64, 6>(V, C, vpb, blocks, label, mask, p, g, grad_out, inv_count, grad_p, s);
-                    case 7: return launch_bwd_nv<64, 7>(V, C, vpb, blocks, label, mask, p, g, grad_out, inv_count, grad_p, s);
-                    default: return launch_bwd_nv<64, 8>(V, C, vpb, blocks, label, mask, p, g, grad_out, inv_count, grad_p, s);
-                }
-            }
+            G2V_LAUNCH((k_cos_bwd_any<LL, T>), dim3(blocks), dim3(kCosThreads), 0, s, V, C, vpb, label, mask, p, g,
+                       grad_out, inv_count, grad_p);
+            return hipGetLastError();
         });
-    }
-    return dispatch_lanes(L, [&](auto Lc) -> hipError_t {
-        constexpr int LL = decltype(Lc)::value;
-        G2V_LAUNCH((k_cos_bwd_any<LL>), dim3(blocks), dim3(kCosThreads), 0, s, V, C, vpb, label, mask, p, g,
-                   grad_out, inv_count, grad_p);
-        return hipGetLastError();
     });
 }
 

@@ -132,14 +132,16 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
 
 // ---- feature cosine loss (g2v_cosine.hip) --------------------------------------------------
 size_t cosine_workspace(int64_t V);
-// 16-byte vector rows: C % 4 == 0 and every non-null pointer 16-byte aligned.
-bool cosine_vec_ok(int C, const void* a, const void* b, const void* c);
-// Mean loss over the valid voxels into *loss and their number into *count (device pointers).
-hipError_t launch_cosine_forward(int64_t V, int C, const float* label, const uint8_t* mask, const float* p,
-                                 const float* g, float* loss, int* count, void* ws, hipStream_t s);
-// dloss/dp into grad_p (V x C), grad_out a device scalar, inv_count = 1 / count (0 when count = 0).
-hipError_t launch_cosine_backward(int64_t V, int C, const float* label, const uint8_t* mask, const float* p,
-                                  const float* g, const float* grad_out, float inv_count, float* grad_p,
+// 4-element vector rows: C % 4 == 0 and every non-null pointer aligned to 4 elements of esize bytes.
+bool cosine_vec_ok(int C, int esize, const void* a, const void* b, const void* c);
+// Mean loss over the valid voxels into *loss and their number into *count (device pointers); p and g
+// hold elements of type fdt (kDtF32 or kDtBF16).
+hipError_t launch_cosine_forward(int64_t V, int C, const float* label, const uint8_t* mask, const void* p,
+                                 const void* g, int fdt, float* loss, int* count, void* ws, hipStream_t s);
+// dloss/dp into grad_p (V x C, type fdt), grad_out a device scalar, inv_count = 1 / count (0 when
+// count = 0).
+hipError_t launch_cosine_backward(int64_t V, int C, const float* label, const uint8_t* mask, const void* p,
+                                  const void* g, int fdt, const float* grad_out, float inv_count, void* grad_p,
                                   hipStream_t s);
 
 // ---- covariances from scales and rotations (g2v_covariance.hip) ----------------------------

@@ -31,7 +31,7 @@ def test_header_symbols_exported():
 
 
 def test_abi_version():
-    assert _lib().load().g2v_abi_version() == 8
+    assert _lib().load().g2v_abi_version() == 9
 
 
 @pytest.mark.parametrize("vs,vr", [
@@ -107,18 +107,22 @@ def test_cosine_invalid_arguments_fail_before_any_launch():
     lib = L.load()
     cnt = ctypes.c_int(0)
     one = ctypes.c_void_p(16)
-    rc = lib.g2v_cosine_loss_forward(-1, 8, None, None, None, None, one, one, None, None, 0, None)
+    rc = lib.g2v_cosine_loss_forward(-1, 8, None, None, None, None, 0, one, one, None, None, 0, None)
     assert rc == 1 and b"num_voxels = -1" in lib.g2v_last_error()
-    rc = lib.g2v_cosine_loss_forward(1 << 31, 8, one, one, one, one, one, one, None, one, 1 << 20, None)
+    rc = lib.g2v_cosine_loss_forward(1 << 31, 8, one, one, one, one, 0, one, one, None, one, 1 << 20, None)
     assert rc == 3
-    rc = lib.g2v_cosine_loss_forward(64, 8, one, one, one, one, None, one, ctypes.byref(cnt), one, 1 << 20, None)
+    rc = lib.g2v_cosine_loss_forward(64, 8, one, one, one, one, 0, None, one, ctypes.byref(cnt), one, 1 << 20, None)
     assert rc == 1 and b"null" in lib.g2v_last_error()
-    rc = lib.g2v_cosine_loss_forward(64, 8, one, one, one, one, one, one, None, one, 16, None)
+    rc = lib.g2v_cosine_loss_forward(64, 8, one, one, one, one, 0, one, one, None, one, 16, None)
     assert rc == 1 and b"workspace" in lib.g2v_last_error()
-    rc = lib.g2v_cosine_loss_backward(64, 8, None, one, one, one, one, 3, one, None)
+    rc = lib.g2v_cosine_loss_forward(64, 8, one, one, one, one, 2, one, one, None, one, 1 << 20, None)
+    assert rc == 1 and b"feat_dtype" in lib.g2v_last_error()
+    rc = lib.g2v_cosine_loss_backward(64, 8, None, one, one, one, one, 0, 3, one, None)
     assert rc == 1 and b"null" in lib.g2v_last_error()
+    rc = lib.g2v_cosine_loss_backward(64, 8, one, one, one, one, one, 7, 3, one, None)
+    assert rc == 1 and b"feat_dtype" in lib.g2v_last_error()
     # nothing to do: no launch, success
-    assert lib.g2v_cosine_loss_backward(0, 8, None, None, None, None, None, 0, None, None) == 0
+    assert lib.g2v_cosine_loss_backward(0, 8, None, None, None, None, None, 0, 0, None, None) == 0
     assert lib.g2v_cosine_loss_workspace(640_000, 1024) > 0
 
 

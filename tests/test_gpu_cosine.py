@@ -214,3 +214,77 @@ def test_cosine_behind_the_voxelizer():
     ref = _C.gaussian_voxelizer_backward(gD, gF, m, o, out[1], vox.voxel_size, vox.voxel_range, out[2], out[3],
                                          out[4], out[6], out[7], out[0], out[5], f)
     assert O.rel_err(fr.grad.cpu().numpy(), ref[3].cpu().numpy()) < 1e-6
+
+
+# bfloat16 grid_feats and target: the kernels widen the values exactly and sum in float32 in the
+# same order as the float32 path, so on the same values the loss and count are identical and the
+# gradient is the float32 gradient rounded to bfloat16 (nearest even), bit for bit.  Cases: rows
+# held in registers (C = 1024), rows too long for them (C = 2304), small rows sharing a wave
+# (C = 16), scalar rows (C = 13) and rows not aligned to 8 bytes (2-byte offset).
+@pytest.mark.parametrize("shape,C,misalign", [((24, 24, 8), 1024, False), ((8, 8, 4), 2304, False),
+                                              ((32, 32, 8), 16, False), ((16, 16, 8), 13, False),
+                                              ((16, 16, 8), 64, True)])
+def test_cosine_bf16_equals_float32_path_on_the_same_values(shape, C, misalign):
+    label, mask, p, q, ld, md, pd, qd = _inputs(shape, C, 21)
+    dev = torch.device("cuda")
+    if misalign:
+        def shifted(t):
+            buf = torch.empty(t.numel() + 1, dtype=torch.bfloat16, device=dev)
+            v = buf[1:].view(t.shape)
+            v.copy_(t.to(dev))
+            return v
+        pb, qb = shifted(pd.bfloat16()), shifted(qd.bfloat16())
+    else:
+        pb, qb = pd.bfloat16().contiguous(), qd.bfloat16().contiguous()
+    say(f"[cosine bf16] shape={shape} C={C} misalign={misalign}")
+    lb_, cb, _ = _C().CudaFeatsCosinelossForward(ld, md, pb, qb)
+    lf, cf, _ = _C().CudaFeatsCosinelossForward(ld, md, pb.float().contiguous(), qb.float().contiguous())
+    assert cb == cf and torch.equal(lb_, lf)
+    go = torch.tensor(2.0, device=dev)
+    gb, _ = _C().CudaFeatsCosinelossBackward(go, ld, md, pb, qb, cb)
+    gf, _ = _C().CudaFeatsCosinelossBackward(go, ld, md, pb.float().contiguous(), qb.float().contiguous(), cf)
+    assert gb.dtype == torch.bfloat16 and torch.equal(gb, gf.to(torch.bfloat16))
+    # and against the float64 oracle on the rounded values
+    exp_loss, exp_cnt = O.cosine_loss_f64(label.numpy(), mask.numpy(), pb.float().cpu().numpy(),
+                                          qb.float().cpu().numpy())
+    assert cb == exp_cnt and abs(lb_.item() - exp_loss) <= TOL * max(abs(exp_loss), 1e-12)
+
+
+def test_cosine_bf16_mixed_types_raise():
+    dev = torch.device("cuda")
+    ld = torch.ones(4, 4, 4, device=dev)
+    md = torch.ones(4, 4, 4, dtype=torch.bool, device=dev)
+    pd = torch.randn(4, 4, 4, 8, device=dev)
+    with pytest.raises(RuntimeError):
+        _C().CudaFeatsCosinelossForward(ld, md, pd.bfloat16(), pd)    # target must match grid_feats
+    with pytest.raises(RuntimeError):
+        _C().CudaFeatsCosinelossForward(ld, md, pd.half(), pd.half())  # float16 is not supported
+
+
+def test_cosine_bf16_behind_the_bf16_voxelizer():
+    """bfloat16 features -> bfloat16 grid_feats -> cosine loss -> backward through both modules, with
+    no float32 copy of grid_feats: the cosine gradient arrives in bfloat16 and the feature gradient
+    comes back in bfloat16."""
+    from CudaGaussianVoxelizer import PyCudaFeatsCosineLoss, PyCudaGaussianVoxelizer
+    from tests import workloads as W
+    w = W.CONFIGS[1]
+    m, o, c, f = W.generate(w, seed=0)
+    dev = torch.device("cuda")
+    m, o, c = (t.to(dev) for t in (m, o, c))
+    vox = PyCudaGaussianVoxelizer(w.voxel_size, w.voxel_range)
+    cos = PyCudaFeatsCosineLoss(w.voxel_size, w.voxel_range)
+    fr = f.to(dev).bfloat16().requires_grad_(True)
+    density, grid_feats, _ = vox(m, o, c, fr)
+    assert grid_feats.dtype == torch.bfloat16
+    g = torch.Generator().manual_seed(5)
+    label = torch.randint(0, 3, density.shape, generator=g).float().to(dev)
+    mask = (torch.rand(density.shape, generator=g) < 0.7).to(dev)
+    target = torch.randn(grid_feats.shape, generator=g).to(dev).bfloat16()
+    say("[cosine bf16] behind the bf16 voxelizer")
+    loss, _ = cos(label, mask, grid_feats, target)
+    loss.backward()
+    assert fr.grad.dtype == torch.bfloat16 and torch.isfinite(fr.grad.float()).all()
+    # the same chain on float32 copies of the same values: the loss is identical
+    gf = grid_feats.detach().float()
+    lf, _, _ = _C().CudaFeatsCosinelossForward(label, mask, gf, target.float())
+    assert torch.equal(loss.detach(), lf)
