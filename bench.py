@@ -143,28 +143,38 @@ def cosine_leg(_C, grid_feats, steps, warmup):
     mask = (torch.rand((X, Y, Z), generator=gen) < 0.8).to(dev)
     target = torch.randn((X, Y, Z, C), generator=gen).to(dev)
     gout = torch.ones((), device=dev)
-    for _ in range(warmup):
-        _, cnt, _ = _C.CudaFeatsCosinelossForward(label, mask, grid_feats, target)
-        _C.CudaFeatsCosinelossBackward(gout, label, mask, grid_feats, target, cnt)
-    fwd = bwd = 0.0
-    for _ in range(steps):
-        _, cnt, f_s = _C.CudaFeatsCosinelossForward(label, mask, grid_feats, target)
-        grad, b_s = _C.CudaFeatsCosinelossBackward(gout, label, mask, grid_feats, target, cnt)
-        fwd += f_s
-        bwd += b_s
-        del grad
-    V = X * Y * Z
-    fwd_ms, bwd_ms = fwd * 1e3 / steps, bwd * 1e3 / steps
-    # compulsory bytes: label + mask of every voxel, both rows of each valid voxel, and the
-    # gradient of every voxel (written)
-    fwd_b = 5 * V + 8 * cnt * C
-    bwd_b = 5 * V + 8 * cnt * C + 4 * V * C
-    gf, gb = fwd_b / (fwd_ms * 1e-3) / 1e9, bwd_b / (bwd_ms * 1e-3) / 1e9
-    return {"grid": [X, Y, Z], "feat_dim": C, "valid_voxels": cnt, "fwd_ms": round(fwd_ms, 4),
-            "bwd_ms": round(bwd_ms, 4), "fwd_bytes": fwd_b, "bwd_bytes": bwd_b,
-            "fwd_gbps": round(gf, 1), "bwd_gbps": round(gb, 1),
-            "fwd_frac": round(gf / HBM_PEAK_GBPS, 4), "bwd_frac": round(gb / HBM_PEAK_GBPS, 4),
-            "data": "grid_feats of the G2V forward vs randn target (seed 11), synthetic labels and mask"}
+
+    def run(p, t, esize):
+        for _ in range(warmup):
+            _, cnt, _ = _C.CudaFeatsCosinelossForward(label, mask, p, t)
+            _C.CudaFeatsCosinelossBackward(gout, label, mask, p, t, cnt)
+        fwd = bwd = 0.0
+        for _ in range(steps):
+            _, cnt, f_s = _C.CudaFeatsCosinelossForward(label, mask, p, t)
+            grad, b_s = _C.CudaFeatsCosinelossBackward(gout, label, mask, p, t, cnt)
+            fwd += f_s
+            bwd += b_s
+            del grad
+        V = X * Y * Z
+        fwd_ms, bwd_ms = fwd * 1e3 / steps, bwd * 1e3 / steps
+        # compulsory bytes: label + mask of every voxel, both rows of each valid voxel, and the
+        # gradient of every voxel (written)
+        fwd_b = 5 * V + 2 * esize * cnt * C
+        bwd_b = 5 * V + 2 * esize * cnt * C + esize * V * C
+        gf, gb = fwd_b / (fwd_ms * 1e-3) / 1e9, bwd_b / (bwd_ms * 1e-3) / 1e9
+        return cnt, {"fwd_ms": round(fwd_ms, 4), "bwd_ms": round(bwd_ms, 4), "fwd_bytes": fwd_b,
+                     "bwd_bytes": bwd_b, "fwd_gbps": round(gf, 1), "bwd_gbps": round(gb, 1),
+                     "fwd_frac": round(gf / HBM_PEAK_GBPS, 4), "bwd_frac": round(gb / HBM_PEAK_GBPS, 4)}
+
+    cnt, res = run(grid_feats, target, 4)
+    out = {"grid": [X, Y, Z], "feat_dim": C, "valid_voxels": cnt}
+    out.update(res)
+    # the same loss on bfloat16 copies of grid_feats and the target (half the row bytes)
+    pb, tb = grid_feats.to(torch.bfloat16), target.to(torch.bfloat16)
+    _, out["bf16"] = run(pb, tb, 2)
+    del pb, tb
+    out["data"] = "grid_feats of the G2V forward vs randn target (seed 11), synthetic labels and mask"
+    return out
 
 
 def covariance_leg(_C, n, steps):
