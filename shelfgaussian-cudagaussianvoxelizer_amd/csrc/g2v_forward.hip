@@ -21,7 +21,8 @@ namespace g2v {
 // ------------------------------------------------------------------------------------------
 // Features as packed bf16 pairs: low half = hi part, high half = lo part of the 2-term split.
 // ------------------------------------------------------------------------------------------
-// T: float or __bf16 features (a bf16 value splits into itself and a zero low part).
+// T: float features, packed as (hi, lo) bf16 pairs, 4 bytes per channel; or __bf16 features,
+// packed as they are, 2 bytes per channel.
 template <typename T>
 __global__ void __launch_bounds__(256) k_split_pack(const T* __restrict__ src, int n, int C, int Cp,
                                                     uint32_t* __restrict__ dst) {
@@ -42,8 +43,14 @@ __global__ void __launch_bounds__(256) k_split_pack(const T* __restrict__ src, i
             for (int e = 0; e < 4; ++e) v[e] = (r < n && c + e < C) ? (float)src[r * C + c + e] : 0.0f;
         }
     } else {
+        // bfloat16 features are packed as they are: 2 bytes per channel (rows of Cp values)
+        unsigned short h[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = (r < n && c + e < C) ? feat_at(src, r * C + c + e) : 0.0f;
+        for (int e = 0; e < 4; ++e)
+            h[e] = (r < n && c + e < C) ? __builtin_bit_cast(unsigned short, src[r * C + c + e]) : (unsigned short)0;
+        *reinterpret_cast<uint2*>(reinterpret_cast<unsigned short*>(dst) + r * Cp + c) =
+            make_uint2(h[0] | ((unsigned)h[1] << 16), h[2] | ((unsigned)h[3] << 16));
+        return;
     }
     uint4 o;
     uint32_t* op = reinterpret_cast<uint32_t*>(&o);
@@ -313,7 +320,8 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
     const int j0 = uniform(min(max(toff[tile], 0), M));
     const int Ng = uniform(min(max(toff[tile + 1], j0), M)) - j0;
     const int nkc = (Ng + kFwdKMax - 1) / kFwdKMax;
-    const uint32_t row_bytes = (uint32_t)Cp * 4u;
+    constexpr uint32_t kCh = OBF16 ? 2u : 4u;   // packed bytes per channel
+    const uint32_t row_bytes = (uint32_t)Cp * kCh;
     const uint32_t zero_off = (uint32_t)n * row_bytes;
     const char* fbase = reinterpret_cast<const char*>(fpk);
     float dacc = 0.0f;
@@ -321,7 +329,7 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
     for (int cbase = 0; cbase < C; cbase += kFwdChanPerPass) {
         const int cw0 = cbase + wave * kFwdChanPerWave;          // first channel of this wave
         const bool has_ch = cw0 < C;                               // wave-uniform
-        const uint32_t lane_off = (uint32_t)(cw0 + 4 * jl) * 4u;  // byte offset of the lane's quad
+        const uint32_t lane_off = (uint32_t)(cw0 + 4 * jl) * kCh;  // byte offset of the lane's quad
         f32x16 acc[2][4];
 #pragma unroll
         for (int vb = 0; vb < 2; ++vb)
@@ -340,25 +348,40 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
             }
             if (has_ch) {
                 // packed quads of K step ks: rows of slots ks*16 + 8*kh + i, channels cw0+4jl..+3
-                auto gather = [&](int ks, uint4 (&u)[8]) {
+                typedef typename std::conditional<OBF16, uint2, uint4>::type Quad;   // 4 packed channels
+                auto gather = [&](int ks, Quad (&u)[8]) {
                     const uint32_t* rp = &sm.roff[ks * 16 + kh * 8];
                     const uint4 ra = *reinterpret_cast<const uint4*>(rp);
                     const uint4 rb = *reinterpret_cast<const uint4*>(rp + 4);
                     const uint32_t rs[8] = {ra.x, ra.y, ra.z, ra.w, rb.x, rb.y, rb.z, rb.w};
 #pragma unroll
                     for (int i = 0; i < 8; ++i)
-                        u[i] = *reinterpret_cast<const uint4*>(fbase + (size_t)(rs[i] + lane_off));
+                        u[i] = *reinterpret_cast<const Quad*>(fbase + (size_t)(rs[i] + lane_off));
                 };
-                auto step = [&](int ks, const uint4 (&u)[8]) {
+                auto step = [&](int ks, const Quad (&u)[8]) {
                     const bf16x8 ah0 = sm.whi[ks][0][lane], al0 = sm.wlo[ks][0][lane];
                     const bf16x8 ah1 = sm.whi[ks][1][lane], al1 = sm.wlo[ks][1][lane];
 #pragma unroll
                     for (int cb = 0; cb < 4; ++cb) {
-                        uint32_t q[8];
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) q[i] = u[i][cb];
                         bf16x8 bh, bl;
-                        unpack8(q, bh, bl);
+                        if constexpr (OBF16) {
+                            // channel cb of rows 2j and 2j+1: half cb&1 of word cb/2 of each row
+                            typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+                            u32x4 hv;
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) {
+                                const uint32_t w0 = cb < 2 ? u[2 * j].x : u[2 * j].y;
+                                const uint32_t w1 = cb < 2 ? u[2 * j + 1].x : u[2 * j + 1].y;
+                                hv[j] = __builtin_amdgcn_perm(w1, w0, (cb & 1) ? 0x07060302u : 0x05040100u);
+                            }
+                            bh = __builtin_bit_cast(bf16x8, hv);
+                            bl = bf16x8{};   // zero low part: its MFMA term is left out
+                        } else {
+                            uint32_t q[8];
+#pragma unroll
+                            for (int i = 0; i < 8; ++i) q[i] = u[i][cb];
+                            unpack8(q, bh, bl);
+                        }
                         // bfloat16 features split into themselves and a zero low part
                         acc[0][cb] = mfma_split_32x32x16<false, OBF16>(ah0, al0, bh, bl, acc[0][cb]);
                         acc[1][cb] = mfma_split_32x32x16<false, OBF16>(ah1, al1, bh, bl, acc[1][cb]);
@@ -367,7 +390,7 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
                 // loads and steps are unconditional (ksteps is even, the prefetch index is
                 // clamped) so the next step's gather stays in flight across this step's MFMAs;
                 // the scheduling barriers keep the compiler from sinking the gathers to their use
-                uint4 ua[8], ub[8];
+                Quad ua[8], ub[8];
                 const int klast = ksteps - 1;
                 if (ksteps > 0) {
                     gather(0, ua);
