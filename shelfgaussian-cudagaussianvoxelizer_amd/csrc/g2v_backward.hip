@@ -902,6 +902,65 @@ __device__ __forceinline__ unsigned br_load_tile(const Grid& G, int C, int c0, i
     return mask;
 }
 
+// Paired form of br_load_tile for even C (rows aligned to two channels): the staging thread takes
+// channels cp2 and cp2 + 1 of the chunk (cp2 = 2 cp) for the 8 voxels of octet o (tile-local
+// x = o/2, y = 2(o&1) + i/4, z = i%4 for value v[h][i] of channel cp2 + h), with one 2-channel load
+// per voxel: half the load instructions of the one-channel form.  Bit i + 8h of the mask marks the
+// values that are real.
+template <bool GB>
+__device__ __forceinline__ unsigned br_load_tile2(const Grid& G, int C, int c0, int t, int cp2, int o,
+                                                  const void* __restrict__ gF, float (&v)[2][8]) {
+    constexpr int kEs = GB ? 2 : 4;   // bytes per element
+    const int tyz = G.tiles[1] * G.tiles[2];
+    const int tx = t / tyz, ty = (t - tx * tyz) / G.tiles[2], tz = t % G.tiles[2];
+    const int x0 = tx * kTile, y0 = ty * kTile, z0 = tz * kTile;
+    const int X = G.dims[0], Y = G.dims[1], Z = G.dims[2];
+    const int64_t origin = ((int64_t)(x0 * Y + y0) * Z + z0) * C + c0;
+    const int64_t left = ((int64_t)X * Y * Z * C - origin) * kEs;
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(static_cast<const char*>(gF) + origin * kEs), (short)0, (int)min(left, (int64_t)0x7fffffff),
+        0x00020000);
+    const bool cok = c0 + cp2 < C;   // C even: both channels of the pair or neither
+    const unsigned cc = (unsigned)(min(c0 + cp2, C - 2) - c0);
+    const int x = x0 + (o >> 1);
+    const bool xok = x < X;
+    const unsigned xl = (unsigned)(min(x, X - 1) - x0);
+    unsigned voff[2];
+    bool yok[2];
+#pragma unroll
+    for (int hy = 0; hy < 2; ++hy) {
+        const int y = y0 + 2 * (o & 1) + hy;
+        yok[hy] = y < Y;
+        const unsigned yl = (unsigned)(min(y, Y - 1) - y0);
+        voff[hy] = ((xl * Y + yl) * Z * C + cc) * (unsigned)kEs;
+    }
+    int soff[4];
+    bool zok[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        zok[i] = z0 + i < Z;
+        soff[i] = (min(z0 + i, Z - 1) - z0) * C * kEs;
+    }
+    unsigned mask = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        // aux 2: non-temporal (grad_feats is streamed once per region)
+        if constexpr (GB) {
+            const unsigned w = (unsigned)__builtin_amdgcn_raw_buffer_load_b32(rsrc, voff[i >> 2], soff[i & 3], 2);
+            v[0][i] = __uint_as_float(w << 16);
+            v[1][i] = __uint_as_float(w & 0xffff0000u);
+        } else {
+            typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+            const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rsrc, voff[i >> 2], soff[i & 3], 2));
+            v[0][i] = __uint_as_float(w[0]);
+            v[1][i] = __uint_as_float(w[1]);
+        }
+        const unsigned ok = (cok && xok && yok[i >> 2] && zok[i & 3]) ? 1u : 0u;
+        mask |= (ok << i) | (ok << (i + 8));
+    }
+    return mask;
+}
+
 // Tile loop of one phase-B pass for a wave that owns NB row blocks (pass blocks wave + 8b,
 // b < NB; NB may be 0).  Every wave runs the same staging work and the same sequence of
 // barriers, whatever its NB, so waves of one workgroup may run different instantiations.  The
@@ -909,13 +968,15 @@ __device__ __forceinline__ unsigned br_load_tile(const Grid& G, int C, int c0, i
 // loaded as soon as the MFMAs of k step s of tile k are issued.  LDS hand-offs use lds_barrier,
 // so loads stay in flight across the barrier and the compiler waits for each where its registers
 // are used.
-template <int NB, bool GB>
+template <int NB, bool GB, bool P2>
 __device__ __forceinline__ void br_tiles(BrSmem& sm, const Grid& G, int C, int c0, int ntl, int prow,
                                          const void* __restrict__ gF, const __bf16* __restrict__ wt,
                                          float* __restrict__ gpart) {
     constexpr int NR = NB > 0 ? NB : 1;   // register arrays (unused when NB == 0)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int sc = threadIdx.x & (kBrCc - 1), so = threadIdx.x >> 7;   // staging: channel, octets so, so+4
+    // staging: channel sc, octets so and so + 4; or (P2) channels 2 cp and 2 cp + 1, octet ot
+    const int sc = threadIdx.x & (kBrCc - 1), so = threadIdx.x >> 7;
+    const int cp2 = 2 * (threadIdx.x & (kBrCc / 2 - 1)), ot = threadIdx.x / (kBrCc / 2);
     const int q = lane >> 4, cl = lane & 15;
 
     float pre[2][8];
@@ -928,9 +989,11 @@ __device__ __forceinline__ void br_tiles(BrSmem& sm, const Grid& G, int C, int c
             for (int i = 0; i < 8; ++i) u[i] = (pmask >> (i + 8 * k)) & 1u ? pre[k][i] : 0.0f;
             bf16x8 hh, ll;
             split8(u, hh, ll);
-            // voxel octet so + 4k: k step k, lane group so
-            sm.bhi[buf][k][sc >> 4][so * 16 + (sc & 15)] = hh;
-            if constexpr (!GB) sm.blo[buf][k][sc >> 4][so * 16 + (sc & 15)] = ll;   // zero for bfloat16
+            // P2: channel cp2 + k of octet ot (k step ot / 4, lane group ot % 4); else voxel octet
+            // so + 4k (k step k, lane group so) of channel sc
+            const int ch = P2 ? cp2 + k : sc, ks = P2 ? (ot >> 2) : k, lg = P2 ? (ot & 3) : so;
+            sm.bhi[buf][ks][ch >> 4][lg * 16 + (ch & 15)] = hh;
+            if constexpr (!GB) sm.blo[buf][ks][ch >> 4][lg * 16 + (ch & 15)] = ll;   // zero for bfloat16
         }
     };
     // A operand of row block b for k step s of a tile: row 16 (wave + 8b) + l%16, voxels
@@ -981,9 +1044,13 @@ __device__ __forceinline__ void br_tiles(BrSmem& sm, const Grid& G, int C, int c
     const int klast = ntl - 1;
     // prologue: tile 0 staged, gF of tile 1 and the weights of tile 0 in flight (in the order
     // the loop issues them, so that the compiler's waits at the loop head stay exact)
-    pmask = br_load_tile<GB>(G, C, c0, uniform(sm.tl_t[0]), sc, so, gF, pre);
+    auto load_tile = [&](int t) {
+        if constexpr (P2) return br_load_tile2<GB>(G, C, c0, t, cp2, ot, gF, pre);
+        else return br_load_tile<GB>(G, C, c0, t, sc, so, gF, pre);
+    };
+    pmask = load_tile(uniform(sm.tl_t[0]));
     stage(0);
-    pmask = br_load_tile<GB>(G, C, c0, uniform(sm.tl_t[min(1, klast)]), sc, so, gF, pre);
+    pmask = load_tile(uniform(sm.tl_t[min(1, klast)]));
     rows_of(0);
     load_w(0);
     load_w(1);
@@ -991,7 +1058,7 @@ __device__ __forceinline__ void br_tiles(BrSmem& sm, const Grid& G, int C, int c
     for (int k = 0; k < ntl; ++k) {
         const int kn = min(k + 1, klast);
         stage((k + 1) & 1);
-        pmask = br_load_tile<GB>(G, C, c0, uniform(sm.tl_t[min(k + 2, klast)]), sc, so, gF, pre);
+        pmask = load_tile(uniform(sm.tl_t[min(k + 2, klast)]));
         rows_of(kn);
         __builtin_amdgcn_sched_barrier(0);
         half(k & 1, 0);
@@ -1019,7 +1086,7 @@ __device__ __forceinline__ void br_tiles(BrSmem& sm, const Grid& G, int C, int c
 
 // One pass of phase B over rows rp .. rp + prow - 1 of the region (prow <= 384): stages the
 // pass's row table and G->R slots, then runs the tile loop with this wave's block count.
-template <bool GB>
+template <bool GB, bool P2>
 __device__ __forceinline__ void br_pass(BrSmem& sm, const Grid& G, int C, int c0, int ntl, int rp,
                                         int KR, int M, int MR, int jr0, const void* __restrict__ gF,
                                         const int* __restrict__ r_pairs, const int* __restrict__ table,
@@ -1060,13 +1127,14 @@ __device__ __forceinline__ void br_pass(BrSmem& sm, const Grid& G, int C, int c0
     }
     __syncthreads();
     static_assert(kBrRbMax == 3, "block-count dispatch");
-    if (nb >= 3) br_tiles<3, GB>(sm, G, C, c0, ntl, prow, gF, wt, gpart);
-    else if (nb == 2) br_tiles<2, GB>(sm, G, C, c0, ntl, prow, gF, wt, gpart);
-    else if (nb == 1) br_tiles<1, GB>(sm, G, C, c0, ntl, prow, gF, wt, gpart);
-    else br_tiles<0, GB>(sm, G, C, c0, ntl, prow, gF, wt, gpart);
+    if (nb >= 3) br_tiles<3, GB, P2>(sm, G, C, c0, ntl, prow, gF, wt, gpart);
+    else if (nb == 2) br_tiles<2, GB, P2>(sm, G, C, c0, ntl, prow, gF, wt, gpart);
+    else if (nb == 1) br_tiles<1, GB, P2>(sm, G, C, c0, ntl, prow, gF, wt, gpart);
+    else br_tiles<0, GB, P2>(sm, G, C, c0, ntl, prow, gF, wt, gpart);
 }
 
-template <bool GB>
+// P2: even C with rows aligned to two channels, so the gF staging loads take two channels at once.
+template <bool GB, bool P2>
 __global__ void __launch_bounds__(kBrThreads, 1) k_bwd_region(
     Grid G, Regions RG, int C, int nchunk, const void* __restrict__ gF,
     const int* __restrict__ toff, int M, const int* __restrict__ roff,
@@ -1105,7 +1173,7 @@ __global__ void __launch_bounds__(kBrThreads, 1) k_bwd_region(
     if (ntl == 0) return;   // every row stays zero: phase C reads no partial row of this region
 
     for (int rp = 0; rp < KR; rp += kBrPass)
-        br_pass<GB>(sm, G, C, c0, ntl, rp, KR, M, MR, jr0, gF, r_pairs, table, wt, gpart);
+        br_pass<GB, P2>(sm, G, C, c0, ntl, rp, KR, M, MR, jr0, gF, r_pairs, table, wt, gpart);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1356,14 +1424,20 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
         const int nchunk = (C + kBrCc - 1) / kBrCc;
         const int64_t items = (int64_t)RG.total * nchunk;
         const int blocks = (int)ceil_div(items, 8) * 8;
-        if (fdt == kDtBF16)
-            G2V_LAUNCH(k_bwd_region<true>, dim3(blocks), dim3(kBrThreads), 0, s, G, RG, C, nchunk,
-                       (const void*)grad_feats, tile_offsets, (int)M, (const int*)b.roff,
-                       (const int*)b.r_pairs_sorted, (const int*)b.table, (int)MR, (const __bf16*)b.wt, b.gpart);
-        else
-            G2V_LAUNCH(k_bwd_region<false>, dim3(blocks), dim3(kBrThreads), 0, s, G, RG, C, nchunk,
-                       (const void*)grad_feats, tile_offsets, (int)M, (const int*)b.roff,
-                       (const int*)b.r_pairs_sorted, (const int*)b.table, (int)MR, (const __bf16*)b.wt, b.gpart);
+        // two-channel staging loads: even C and a grad_feats base aligned to two elements
+        const bool pair = (C & 1) == 0 && ((uintptr_t)grad_feats & (fdt == kDtBF16 ? 3 : 7)) == 0;
+#define G2V_BR(GBV, P2V)                                                                                      \
+    G2V_LAUNCH((k_bwd_region<GBV, P2V>), dim3(blocks), dim3(kBrThreads), 0, s, G, RG, C, nchunk, grad_feats,       \
+               tile_offsets, (int)M, (const int*)b.roff, (const int*)b.r_pairs_sorted, (const int*)b.table, (int)MR, \
+               (const __bf16*)b.wt, b.gpart)
+        if (fdt == kDtBF16) {
+            if (pair) G2V_BR(true, true);
+            else G2V_BR(true, false);
+        } else {
+            if (pair) G2V_BR(false, true);
+            else G2V_BR(false, false);
+        }
+#undef G2V_BR
     }
     if (fdt == kDtBF16)
         G2V_LAUNCH(k_bwd_gauss<true>, dim3(n), dim3(kBgThreads), 0, s, n, C, (int)M, (int)MR, g2t_offsets,
