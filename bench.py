@@ -40,7 +40,7 @@ PUBLISHED_FWD_BWD_MS = 3200.0   # README Table 13, 1x L40S, 18k Gaussians x 1024
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=3, help="BASELINE config (1-5)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
