@@ -64,6 +64,16 @@ def algorithmic_bytes(N, C, V, M, T, MR):
     fwd = 4 * (13 * N + N * C + V + V * C + (N + 1) + M + 16 * N)
     bwd = 4 * (2 * V + V * C + N * C + 4 * N + 16 * N + (N + 1) + M + 13 * N + N * C)
     params = 4 * 19 * N                      # means, opacity, cov_inv, lb, ub
+    # each compulsory byte of the step attributed to the first kernel that moves it (the kernels'
+    # own intermediates and second reads count for nothing here)
+    compulsory = {
+        "k_fwd_feats": 4 * (N * C + V + V * C) + params,
+        "k_fwd_density": 4 * V + params,
+        "k_bwd_tile": 4 * (V * C + 2 * V + N * C + (N + 1) + M) + params,
+        "k_bwd_region": 0,
+        "k_bwd_gauss": 4 * (13 * N + N * C),
+        "k_bwd_density": 4 * (V + 13 * N) + params,
+    }
     per_kernel = {
         "k_fwd_feats": 4 * (N * C + (T + 1) + M + V + V * C) + params,
         "k_fwd_density": 4 * ((T + 1) + M + V) + params,
@@ -72,7 +82,7 @@ def algorithmic_bytes(N, C, V, M, T, MR):
         "k_bwd_gauss": 4 * (10 * M + MR * C + 2 * (N + 1) + 13 * N + N * C),
         "k_bwd_density": 4 * (V + 13 * N) + params,
     }
-    return fwd, bwd, per_kernel
+    return fwd, bwd, per_kernel, compulsory
 
 
 def region_pairs(lb, ub, tiles_z):
@@ -324,6 +334,8 @@ def main():
     # timed region: K steps of the product path, no instrumentation
     fwd_s = bwd_s = 0.0
     torch.cuda.synchronize()
+    resident = torch.cuda.memory_allocated(dev)     # inputs and upstream gradients
+    torch.cuda.reset_peak_memory_stats(dev)
     t0 = time.perf_counter()
     for _ in range(args.steps):
         stats = step()
@@ -332,6 +344,14 @@ def main():
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms = (t1 - t0) * 1e3 / args.steps
+    peak = torch.cuda.max_memory_allocated(dev)
+    memory = {"peak_allocated_gb": round(peak / 1e9, 3), "resident_inputs_gb": round(resident / 1e9, 3),
+              "step_peak_gb": round((peak - resident) / 1e9, 3),
+              "reference_gb": 4.9 if args.config == 3 else (3.7 if args.config == 2 else None),
+              "note": ("torch caching-allocator peak over the timed steps (all device memory the step "
+                       "holds: inputs, upstream gradients, outputs and the library's workspaces); "
+                       "step_peak_gb leaves out the inputs and upstream gradients resident before the "
+                       "step; reference_gb: README.md:98, 1x L40S")}
     # per-kernel times: K more steps with a HIP event pair around every launch of the library,
     # recorded on the stream each kernel runs on (the events add host work, so these steps are
     # timed separately and reported as instrumented_ms_per_step)
@@ -356,7 +376,7 @@ def main():
     M = int(out[7].numel())
     P = int(out[4].to(torch.int64).sum().item())         # in-box (Gaussian, voxel) pairs
     MR = region_pairs(out[2].cpu().numpy(), out[3].cpu().numpy(), Tz) if C else 0
-    fwd_b, bwd_b, per_kernel = algorithmic_bytes(N, C, V, M, T, MR)
+    fwd_b, bwd_b, per_kernel, compulsory = algorithmic_bytes(N, C, V, M, T, MR)
     gbps = (fwd_b + bwd_b) / (ms * 1e-3) / 1e9
 
     if args.copy_probe_mib > 0:   # a plain copy of known size, the scale of the PMC byte counters
@@ -383,9 +403,14 @@ def main():
                 traffic = tr.get("bytes_per_launch")
         if bytes_k is not None:
             ach = bytes_k / avg_s / 1e9
+            comp = compulsory.get(dom.split("<")[0])
             roofline = {"kernel": dom, "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
                         "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                        "algorithmic_bytes": bytes_k, "avg_ms": round(avg_s * 1e3, 4)}
+                        "algorithmic_bytes": bytes_k, "avg_ms": round(avg_s * 1e3, 4),
+                        # the same launch credited with its share of the step's compulsory bytes only
+                        # (no intermediates of the design, no second reads)
+                        "compulsory_bytes": comp,
+                        "compulsory_frac": None if comp is None else round(comp / avg_s / 1e9 / HBM_PEAK_GBPS, 4)}
 
     covariance = batched = bf16 = None
     if not args.no_extra and C > 0:
@@ -420,7 +445,7 @@ def main():
         "hbm_gbps": round(gbps, 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
         "compulsory_bytes": fwd_b + bwd_b,
         "fp32_equiv_tflops": round(flops / (ms * 1e-3) / 1e12, 2),
-        "roofline": roofline, "kernels": kernels, "instrumented_ms_per_step": round(ms_instr, 4),
+        "roofline": roofline, "memory": memory, "kernels": kernels, "instrumented_ms_per_step": round(ms_instr, 4),
         "kernels_note": ("per-kernel HIP event pairs over K further steps run right after the timed "
                          "region (instrumented_ms_per_step is their wall time per step)"),
         "cpu_baseline": cpu,

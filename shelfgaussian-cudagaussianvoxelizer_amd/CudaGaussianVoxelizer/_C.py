@@ -496,7 +496,11 @@ def _forward_batched(means3D, opacity, covariances, voxel_size, voxel_range, fea
                 t2g["ws"] = torch.empty(max(1, lib.g2v_backward_workspace(n, C, M, t2g["num_region_pairs"], vs, vr)),
                                         dtype=torch.uint8, device=dev)
                 if side is not cur:
-                    for t in t2g["grads"] + (t2g["ws"],):
+                    # everything the preparation below reads or writes on the side stream: it is
+                    # queued after the join, so nothing on cur waits for it, and lb/ub/bplan/feats
+                    # (feats possibly a temporary copy) may be freed on cur before it runs
+                    used_by_prep = t2g["grads"] + (t2g["ws"], lb, ub, bplan) + (() if feats is None else (feats,))
+                    for t in used_by_prep:
                         t.record_stream(side)
                 if C > 0:
                     _lib.check(lib.g2v_backward_prepare(n, C, vs, vr, _ptr(lb[b]), _ptr(ub[b]), _ptr(feats[b]), fdt, M,
@@ -517,10 +521,11 @@ def _forward_batched(means3D, opacity, covariances, voxel_size, voxel_range, fea
     return out, density, grid_feats
 
 
-def _backward_batched(grad_density, grad_feats, means, opacity, features, scenes):
-    """Backward of _forward_batched(keep_t2g=True): grad_density (B,X,Y,Z), grad_feats (B,X,Y,Z,C);
-    scenes = its per-scene (9-tuple, t2g) list.  Returns stacked gradients (B,N,3), (B,N,9),
-    (B,N), (B,N,C) and the time of the whole batch."""
+def _backward_batched(grad_density, grad_feats, means, opacity, features, scenes, voxel_size=None, voxel_range=None):
+    """Backward of _forward_batched: grad_density (B,X,Y,Z), grad_feats (B,X,Y,Z,C); scenes = its
+    per-scene (9-tuple, t2g) list (t2g None when the forward kept nothing: each scene's backward
+    then rebuilds its CSR and plan, on the grid of voxel_size and voxel_range).  Returns stacked
+    gradients (B,N,3), (B,N,9), (B,N), (B,N,C) and the time of the whole batch."""
     dev = means.device
     B = len(scenes)
     with _OnDevice(dev):
@@ -547,8 +552,8 @@ def _backward_batched(grad_density, grad_feats, means, opacity, features, scenes
                 if side not in used:
                     used.append(side)
             with torch.cuda.stream(side):
-                grads.append(_backward(grad_density[b], gF, means[b], opacity[b], cov_inv, None, None, lb, ub, nvox,
-                                       g2t_offsets, g2t_tile_ids, density, gfeat, fb, t2g=t2g, timed=False))
+                grads.append(_backward(grad_density[b], gF, means[b], opacity[b], cov_inv, voxel_size, voxel_range, lb,
+                                       ub, nvox, g2t_offsets, g2t_tile_ids, density, gfeat, fb, t2g=t2g, timed=False))
         _join(cur, used)
         stop.record(cur)
         stop.synchronize()

@@ -18,14 +18,31 @@ __all__ = ["PyCudaGaussianVoxelizer", "PyCudaFeatsCosineLoss", "_C",
            "CudaFeatsCosinelossForward", "CudaFeatsCosinelossBackward", "covariance_from_scale_rotation"]
 
 
+def _wants_backward(ctx, need_backward):
+    """Whether the forward should keep and prepare what the backward reuses.  Inside
+    Function.forward grad mode is always off, so the caller's grad mode arrives as need_backward
+    (the module passes it); without it, whether any input requires grad decides."""
+    if need_backward is not None:
+        return bool(need_backward)
+    return any(ctx.needs_input_grad)
+
+
+def _grad_possible(*tensors):
+    """A backward can follow this forward: grad mode is on and an input requires grad."""
+    return torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad for t in tensors)
+
+
 class _CudaGaussianVoxelizeFunction(torch.autograd.Function):
     """Autograd wrapper (reference CudaGaussianVoxelizer/__init__.py:10-47)."""
 
     @staticmethod
-    def forward(ctx, means3D, opacity, covariances, voxel_size, voxel_range, features):
+    def forward(ctx, means3D, opacity, covariances, voxel_size, voxel_range, features, need_backward=None):
         # with features the backward reuses the forward's Tile->Gaussian CSR (kept beside the
-        # reference's saved tensors) instead of re-sorting the G->T pairs
-        keep = features is not None and features.shape[-1] > 0
+        # reference's saved tensors) instead of re-sorting the G->T pairs, and its workspace is
+        # prepared behind the forward; both only when a backward can follow (need_backward, or
+        # when not given, whether an input requires grad), so that an inference forward
+        # allocates and launches nothing for a backward that never runs
+        keep = features is not None and features.shape[-1] > 0 and _wants_backward(ctx, need_backward)
         (density, cov_inv, valid_voxel_lb, valid_voxel_ub, num_valid_voxel, grid_feats, g2t_offsets,
          g2t_tile_ids, fwd_sec), t2g = _C._forward(means3D, opacity, covariances, voxel_size,
                                                    voxel_range, features, keep_t2g=keep)
@@ -59,7 +76,7 @@ class _CudaGaussianVoxelizeFunction(torch.autograd.Function):
         grad_opacity = grad_opacity.reshape(ctx.opacity_shape)
         grad_cov = grad_cov.reshape(ctx.cov_shape)
         return (grad_means3D, grad_opacity, grad_cov, None, None,
-                grad_feats if features is not None else None)
+                grad_feats if features is not None else None, None)
 
 
 class _CudaFeatsCosinelossFunction(torch.autograd.Function):
@@ -91,12 +108,13 @@ class _CudaGaussianVoxelizeBatchedFunction(torch.autograd.Function):
     batch's plan, per-scene CSR; returns density (B,X,Y,Z), grid_feats (B,X,Y,Z,C) and stats."""
 
     @staticmethod
-    def forward(ctx, means3D, opacity, covariances, voxel_size, voxel_range, features):
+    def forward(ctx, means3D, opacity, covariances, voxel_size, voxel_range, features, need_backward=None):
         scenes, density, grid_feats = _C._forward_batched(means3D, opacity, covariances, voxel_size, voxel_range,
-                                                          features, keep_t2g=True)
+                                                          features, keep_t2g=_wants_backward(ctx, need_backward))
         stats = torch.zeros(2, dtype=torch.float32, device="cpu")
         stats[0] = scenes[0][0][8] if scenes else 0.0
         ctx.scenes = scenes
+        ctx.grid = (voxel_size, voxel_range)
         ctx.save_for_backward(means3D, opacity, features, stats)
         ctx.mark_non_differentiable(stats)
         ctx.shapes = (means3D.shape, opacity.shape, covariances.shape)
@@ -111,11 +129,11 @@ class _CudaGaussianVoxelizeBatchedFunction(torch.autograd.Function):
         m32 = means3D.detach().contiguous()
         o32 = opacity.detach().reshape(B, n).contiguous()
         feats = None if features is None else features.detach().contiguous()
-        gm, gc, go, gf, bwd_sec = _C._backward_batched(gD, gF, m32, o32, feats, ctx.scenes)
+        gm, gc, go, gf, bwd_sec = _C._backward_batched(gD, gF, m32, o32, feats, ctx.scenes, *ctx.grid)
         ctx.scenes = None
         stats[1] = bwd_sec
         return (gm.reshape(ctx.shapes[0]), go.reshape(ctx.shapes[1]), gc.reshape(ctx.shapes[2]), None, None,
-                gf if features is not None else None)
+                gf if features is not None else None, None)
 
 
 class _CovarianceFromScaleRotation(torch.autograd.Function):
@@ -172,11 +190,12 @@ class PyCudaGaussianVoxelizer(nn.Module):
             # reduced-precision covariances (ShelfGaussian records them in float16): widened on the
             # device, the gradient flows back in their type
             covariances = covariances.float()
+        need = _grad_possible(means3D, opacity, covariances, features)
         if means3D.dim() == 3:   # B scenes on this grid: (B,N,3) means, outputs gain a leading B
             return _CudaGaussianVoxelizeBatchedFunction.apply(means3D, opacity, covariances, self.voxel_size,
-                                                              self.voxel_range, features)
+                                                              self.voxel_range, features, need)
         return _CudaGaussianVoxelizeFunction.apply(means3D, opacity, covariances, self.voxel_size,
-                                                   self.voxel_range, features)
+                                                   self.voxel_range, features, need)
 
 
 class PyCudaFeatsCosineLoss(nn.Module):

@@ -12,6 +12,8 @@ LIB_NAME = "libg2v_hip.so"
 LIB_PATH = os.path.join(_HERE, LIB_NAME)
 
 G2V_OK = 0
+# the ABI that SIGNATURES describes (g2v_abi_version() of a matching build)
+ABI_VERSION = 9
 G2V_DTYPE_F32 = 0
 G2V_DTYPE_BF16 = 1
 _ERRORS = {1: "invalid argument", 2: "HIP runtime error", 3: "size limit exceeded"}
@@ -67,6 +69,14 @@ def load():
             f"{LIB_PATH} is missing: build the HIP library first "
             "(python shelfgaussian-cudagaussianvoxelizer_amd/build.py); there is no CPU fallback")
     lib = ctypes.CDLL(LIB_PATH)
+    # a library built from other sources would be called with mismatched argument lists: refuse it
+    # before any entry point runs
+    lib.g2v_abi_version.restype = ctypes.c_int
+    lib.g2v_abi_version.argtypes = []
+    got = lib.g2v_abi_version()
+    if got != ABI_VERSION:
+        raise ImportError(f"{LIB_PATH} has ABI {got}, this package expects {ABI_VERSION}: rebuild it "
+                          "(python shelfgaussian-cudagaussianvoxelizer_amd/build.py)")
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.restype = res

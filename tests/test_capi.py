@@ -31,7 +31,16 @@ def test_header_symbols_exported():
 
 
 def test_abi_version():
-    assert _lib().load().g2v_abi_version() == 9
+    assert _lib().load().g2v_abi_version() == _lib().ABI_VERSION == 9
+
+
+def test_loader_refuses_other_abi(monkeypatch):
+    """A library whose ABI differs from the one SIGNATURES describes is refused at load time."""
+    L = _lib()
+    monkeypatch.setattr(L, "ABI_VERSION", L.ABI_VERSION + 1)
+    monkeypatch.setattr(L, "_lib", None)
+    with pytest.raises(ImportError, match="rebuild"):
+        L.load()
 
 
 @pytest.mark.parametrize("vs,vr", [
