@@ -10,14 +10,16 @@
 // twice instead of once per overlapping Gaussian (the reference re-reads it per pair):
 //   A  k_bwd_tile    one workgroup per 4x4x4 tile: U^T = G_tile (64 x C) . F_list^T on the matrix
 //                    cores (3-term bf16 split, fp32 accumulate); t_v from U (sum_g [w>0] w u / D is
-//                    sum_c gF F); gw; the ten geometric partial sums of each (tile, Gaussian) pair,
-//                    stored at the pair's G->T CSR slot; the split weights w/max(D,eps) of the pair.
+//                    sum_c gF F); gw; ten moments of r = gw e over the pair's voxels (sum r d,
+//                    sum r d d^T, sum r with d = centre - mu), stored at the pair's G->T CSR
+//                    slot; the split weights w/max(D,eps) of the pair.
 //   B  k_bwd_region  one workgroup per (region of 2x2xRZ tiles, 128-channel chunk): for every
 //                    tile of the region, (region rows x 64 voxels) . (64 voxels x 128 channels) on
 //                    the matrix cores, accumulated in registers (a wave owns 32 region rows);
 //                    writes one partial d f row per (region, Gaussian) pair at its G->R CSR slot.
-//   C  k_bwd_gauss   one workgroup per Gaussian: fixed-order sums of its geometric partials and
-//                    of its region partial rows.
+//   C  k_bwd_gauss   one workgroup per Gaussian: fixed-order sums of its pair moments, turned
+//                    into d mu, d Sigma and d o by its inverse covariance, and of its region
+//                    partial rows.
 // Without features, k_bwd_density walks each Gaussian's box with one wave.
 #include "g2v_internal.h"
 #include <type_traits>
@@ -187,6 +189,7 @@ constexpr int kBtPass = kBtGroups * kBtNbw * 32;       // 256 Gaussians per pass
 constexpr int kBtStages = 3;                           // F chunks resident in LDS (loaded 2 ahead)
 constexpr int kBtDma = kBtPass / 8 / kBtWaves;         // 1 KB direct-to-LDS loads per wave per chunk
 constexpr int kWtRow = 128;                            // bf16 per pair: 64 hi then 64 lo
+constexpr float kq = -0.72134752044448170f;            // exp(-m/2) = exp2(kq m)
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
@@ -264,11 +267,9 @@ __device__ __forceinline__ void lds_barrier() {
 
 // Geometry of one lane's 16 epilogue elements against its Gaussian.  The elements of a lane are
 // the 2 x 2 x 4 voxel block x = x0 + a, y = y0 + 2b, z = z0 + c of the tile (a, b < 2, c < 4), so
-// dx = centre - mu splits by axis and q = A dx is the sum of one column product per axis:
-// q = A[:,0] dx_a + A[:,1] dy_b + A[:,2] dz_c.  The box test splits by axis as well (bit masks).
+// dx = centre - mu and the box test (bit masks) split by axis.
 struct LaneGeom {
     float dx[2], dy[2], dz[4];
-    float qa[2][3], qb[2][3], qc[4][3];   // column products, by axis and offset
     unsigned inx, iny, inz;               // bit a / b / c: the offset lies in the Gaussian's box
 };
 
@@ -282,29 +283,37 @@ __device__ __forceinline__ void lane_geom(const Grid& G, const GaussParams& p, i
         L.dy[a] = centre(G, 1, y) - p.mu[1];
         L.inx |= (x >= p.lb[0] && x <= p.ub[0]) ? (1u << a) : 0u;
         L.iny |= (y >= p.lb[1] && y <= p.ub[1]) ? (1u << a) : 0u;
-#pragma unroll
-        for (int k = 0; k < 3; ++k) {
-            L.qa[a][k] = p.A[3 * k] * L.dx[a];
-            L.qb[a][k] = p.A[3 * k + 1] * L.dy[a];
-        }
     }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         const int z = z0 + c;
         L.dz[c] = centre(G, 2, z) - p.mu[2];
         L.inz |= (z >= p.lb[2] && z <= p.ub[2]) ? (1u << c) : 0u;
-#pragma unroll
-        for (int k = 0; k < 3; ++k) L.qc[c][k] = p.A[3 * k + 2] * L.dz[c];
     }
 }
 
-// q and the Mahalanobis term m = dx . q of element (a, b, c).
-__device__ __forceinline__ float lane_q(const LaneGeom& L, int a, int b, int c, float& qx, float& qy,
-                                        float& qz) {
-    qx = (L.qa[a][0] + L.qb[b][0]) + L.qc[c][0];
-    qy = (L.qa[a][1] + L.qb[b][1]) + L.qc[c][1];
-    qz = (L.qa[a][2] + L.qb[b][2]) + L.qc[c][2];
-    return L.dx[a] * qx + L.dy[b] * qy + L.dz[c] * qz;
+// The exponent -m/2 of a lane's element (a, b, c), split by axis and scaled by kq so that
+// e = exp2(Fxy[a][b] + Fz[c] + Gxy[a][b] dz[c]) (m = d^T A d summed in this order).
+struct LaneExp {
+    float Fxy[2][2], Gxy[2][2], Fz[4];
+};
+
+__device__ __forceinline__ void lane_exp(const GaussParams& p, const LaneGeom& L, LaneExp& E) {
+    const float sxy = p.A[1] + p.A[3], sxz = p.A[2] + p.A[6], syz = p.A[5] + p.A[7];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const float dx = L.dx[a], dy = L.dy[b];
+            E.Fxy[a][b] = kq * fmaf(fmaf(p.A[0], dx, sxy * dy), dx, p.A[4] * dy * dy);
+            E.Gxy[a][b] = kq * fmaf(sxz, dx, syz * dy);
+        }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) E.Fz[c] = kq * (p.A[8] * L.dz[c] * L.dz[c]);
+}
+
+__device__ __forceinline__ float lane_e(const LaneExp& E, const LaneGeom& L, int a, int b, int c) {
+    return __builtin_amdgcn_exp2f(fmaf(E.Gxy[a][b], L.dz[c], E.Fxy[a][b] + E.Fz[c]));
 }
 
 // BF: features and grad_feats are bfloat16.  A chunk is then 64 channels (the split rows hold the
@@ -639,8 +648,9 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
         // ---- epilogue 1: split weights w / max(D, eps) of every pair; t_v from U (single pass).
         // Lane = Gaussian column lane%32 of N block j; element i is the tile's voxel row
         // r = 32 mb + 8 (i/4) + 4 (lane/32) + i%4.  Branch-free: an element outside the grid, the
-        // Gaussian's box or the list gets e = 0 (and so w = 0).  e and the validity bits are kept
-        // for epilogue 2, which then evaluates no exponential.
+        // Gaussian's box or the list gets e = 0 (and so w = 0).  The validity bits are kept for
+        // epilogue 2, which evaluates e again (cheaper than keeping 32 values per lane live across
+        // the t_v exchange).
         unsigned rowok = 0;   // bit i: row r of element i lies in the grid
 #pragma unroll
         for (int i = 0; i < 16; ++i)
@@ -648,13 +658,10 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
         float rowt[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) rowt[i] = 0.0f;
-        float ek[kBtNbw][16];
         unsigned okm[kBtNbw];
 #pragma unroll
         for (int j = 0; j < kBtNbw; ++j) {
             okm[j] = 0;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) ek[j][i] = 0.0f;
             if (j >= nact) continue;   // wave-uniform
             const int slot = (ngrp + kBtGroups * j) * 32 + (lane & 31);
             const bool gok = gcol[j] >= 0;
@@ -662,6 +669,8 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             read_params(sm.pt, slot, p);
             LaneGeom L;
             lane_geom(G, p, tx * kTile + 2 * mb, ty * kTile + h, tz * kTile, L);
+            LaneExp E;
+            lane_exp(p, L, E);
             __bf16* wrow = wt + (int64_t)(j0 + pbase + slot) * kWtRow;
 #pragma unroll
             for (int q4 = 0; q4 < 4; ++q4) {
@@ -674,10 +683,7 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
                     const int i = q4 * 4 + ii;
                     const int r = mb * 32 + 8 * q4 + 4 * h + ii;
                     const bool ok = gok & (((rowok >> i) & (L.inx >> a) & (L.iny >> b) & (L.inz >> ii) & 1u) != 0u);
-                    float qx, qy, qz;
-                    const float m = lane_q(L, a, b, ii, qx, qy, qz);
-                    const float e = ok ? __expf(-0.5f * m) : 0.0f;
-                    ek[j][i] = e;
+                    const float e = ok ? lane_e(E, L, a, b, ii) : 0.0f;
                     okm[j] |= ok ? (1u << i) : 0u;
                     const float w = p.o * e;
                     const float wtil = w * sm.inv[r];
@@ -714,8 +720,11 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             __syncthreads();
         }
 
-        // ---- epilogue 2: gw and the geometric partials of each pair (e from epilogue 1; an
-        // invalid element adds exact zeros)
+        // ---- epilogue 2: r = gw e of every element (e from epilogue 1; an invalid element
+        // adds exact zeros) and its moments over the lane's 2 x 2 x 4 voxels relative to the
+        // mean (d = centre - mu): sum r d, sum r d d^T (times o) and sum r.  Phase C turns them
+        // into d mu = A (o sum r d), d Sigma = A (o sum r d d^T) A^T / 2 and d o = sum r, since
+        // q = A d, sum gw w q = o A sum r d and sum gw w q q^T = o A (sum r d d^T) A^T.
 #pragma unroll
         for (int j = 0; j < kBtNbw; ++j) {
             const int slot = (ngrp + kBtGroups * j) * 32 + (lane & 31);
@@ -725,14 +734,47 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
                 read_params(sm.pt, slot, p);
                 LaneGeom L;
                 lane_geom(G, p, tx * kTile + 2 * mb, ty * kTile + h, tz * kTile, L);
+                LaneExp E;   // e is evaluated again rather than kept across the t_v exchange
+                lane_exp(p, L, E);
+                float m0 = 0.f, mx = 0.f, my = 0.f, mz = 0.f, mxx = 0.f, myy = 0.f, mzz = 0.f, mxy = 0.f,
+                      mxz = 0.f, myz = 0.f;
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int r = mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-                    float qx, qy, qz;
-                    lane_q(L, i >> 3, (i >> 2) & 1, i & 3, qx, qy, qz);
-                    const float gw = sm.gD[r] + (acc[j][i] - sm.tv[r]) * sm.inv[r];
-                    accumulate_grads(gr, ((okm[j] >> i) & 1u) ? gw : 0.0f, ek[j][i], p.o, qx, qy, qz);
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    const int a = q4 >> 1, b = q4 & 1;
+                    float s0 = 0.f, sz = 0.f, szz = 0.f;
+#pragma unroll
+                    for (int ii = 0; ii < 4; ++ii) {
+                        const int i = q4 * 4 + ii;
+                        const int r = mb * 32 + 8 * q4 + 4 * h + ii;
+                        const float gw = sm.gD[r] + (acc[j][i] - sm.tv[r]) * sm.inv[r];
+                        const float rr = ((okm[j] >> i) & 1u) ? gw * lane_e(E, L, a, b, ii) : 0.0f;
+                        s0 += rr;
+                        const float rz = rr * L.dz[ii];
+                        sz += rz;
+                        szz = fmaf(rz, L.dz[ii], szz);
+                    }
+                    const float dx = L.dx[a], dy = L.dy[b];
+                    m0 += s0;
+                    mx = fmaf(dx, s0, mx);
+                    my = fmaf(dy, s0, my);
+                    mz += sz;
+                    mxx = fmaf(dx * dx, s0, mxx);
+                    myy = fmaf(dy * dy, s0, myy);
+                    mzz += szz;
+                    mxy = fmaf(dx * dy, s0, mxy);
+                    mxz = fmaf(dx, sz, mxz);
+                    myz = fmaf(dy, sz, myz);
                 }
+                gr[0] = p.o * mx;
+                gr[1] = p.o * my;
+                gr[2] = p.o * mz;
+                gr[3] = p.o * mxx;
+                gr[4] = p.o * myy;
+                gr[5] = p.o * mzz;
+                gr[6] = p.o * mxy;
+                gr[7] = p.o * mxz;
+                gr[8] = p.o * myz;
+                gr[9] = m0;
             }
 #pragma unroll
             for (int k = 0; k < kNumGrads; ++k) gr[k] += __shfl_xor(gr[k], 32, 64);
@@ -1184,7 +1226,7 @@ constexpr int kBgThreads = 256;
 // OBF16: grad_features is stored as bfloat16 (rounded to nearest even), else float.
 template <bool OBF16>
 __global__ void __launch_bounds__(kBgThreads) k_bwd_gauss(
-    int n, int C, int M, int MR, const int* __restrict__ g2t_offsets,
+    int n, int C, int M, int MR, const int* __restrict__ g2t_offsets, const float* __restrict__ cov_inv,
     const float* __restrict__ pair_partials, const int* __restrict__ g2r_offsets,
     const float* __restrict__ gpart, float* __restrict__ grad_means, float* __restrict__ grad_cov,
     float* __restrict__ grad_opacity, void* __restrict__ grad_features_out) {
@@ -1206,10 +1248,36 @@ __global__ void __launch_bounds__(kBgThreads) k_bwd_gauss(
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        float tot[kNumGrads];
+        // the pair values are o sum r d (3), o sum r d d^T (xx yy zz xy xz yz) and sum r, with
+        // r = gw e and d = centre - mu: d mu = A (o sum r d), d Sigma = A (o sum r d d^T) A^T / 2,
+        // d o = sum r (A = cov_inv, row-major)
+        float t[kNumGrads];
 #pragma unroll
-        for (int k = 0; k < kNumGrads; ++k) tot[k] = ((red[0][k] + red[1][k]) + red[2][k]) + red[3][k];
-        write_grads(tot, g, grad_means, grad_cov, grad_opacity);
+        for (int k = 0; k < kNumGrads; ++k) t[k] = ((red[0][k] + red[1][k]) + red[2][k]) + red[3][k];
+        float A[9];
+#pragma unroll
+        for (int k = 0; k < 9; ++k) A[k] = cov_inv[g * 9 + k];
+        const float P[9] = {t[3], t[6], t[7], t[6], t[4], t[8], t[7], t[8], t[5]};
+        float B[9];   // A P
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+#pragma unroll
+            for (int k = 0; k < 3; ++k)
+                B[i * 3 + k] = fmaf(A[i * 3], P[k], fmaf(A[i * 3 + 1], P[3 + k], A[i * 3 + 2] * P[6 + k]));
+        auto bat = [&](int i, int l) {   // (A P A^T)_il / 2
+            return 0.5f * fmaf(B[i * 3], A[l * 3], fmaf(B[i * 3 + 1], A[l * 3 + 1], B[i * 3 + 2] * A[l * 3 + 2]));
+        };
+        float gr[kNumGrads];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) gr[i] = fmaf(A[i * 3], t[0], fmaf(A[i * 3 + 1], t[1], A[i * 3 + 2] * t[2]));
+        gr[3] = bat(0, 0);
+        gr[4] = bat(1, 1);
+        gr[5] = bat(2, 2);
+        gr[6] = bat(0, 1);
+        gr[7] = bat(0, 2);
+        gr[8] = bat(1, 2);
+        gr[9] = t[9];
+        write_grads(gr, g, grad_means, grad_cov, grad_opacity);
     }
     const int r0 = min(max(g2r_offsets[g], 0), MR), r1 = min(max(g2r_offsets[g + 1], r0), MR);
     // region rows summed in ascending order per channel; a bfloat16 output is the float sum rounded
@@ -1441,11 +1509,11 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
     }
     if (fdt == kDtBF16)
         G2V_LAUNCH(k_bwd_gauss<true>, dim3(n), dim3(kBgThreads), 0, s, n, C, (int)M, (int)MR, g2t_offsets,
-                   (const float*)b.partials, (const int*)pb.g2r_offsets, (const float*)b.gpart, grad_means,
+                   cov_inv, (const float*)b.partials, (const int*)pb.g2r_offsets, (const float*)b.gpart, grad_means,
                    grad_cov, grad_opacity, grad_features);
     else
         G2V_LAUNCH(k_bwd_gauss<false>, dim3(n), dim3(kBgThreads), 0, s, n, C, (int)M, (int)MR, g2t_offsets,
-                   (const float*)b.partials, (const int*)pb.g2r_offsets, (const float*)b.gpart, grad_means,
+                   cov_inv, (const float*)b.partials, (const int*)pb.g2r_offsets, (const float*)b.gpart, grad_means,
                    grad_cov, grad_opacity, grad_features);
     return hipGetLastError();
 }
