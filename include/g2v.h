@@ -187,6 +187,17 @@ int g2v_cosine_loss_forward(long long num_voxels, int feat_dim, const float* vox
                             int feat_dtype, float* loss, int* num_valid, int* num_valid_host, void* workspace,
                             size_t workspace_bytes, void* stream);
 
+/* g2v_cosine_loss_forward_noalloc: g2v_cosine_loss_forward without a workspace and without the
+ * host count, for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation).  No counterpart in the reference.  The block
+ * partial sums live in a 32 KiB device array of the library (one per GPU, held until the process
+ * ends), which fits the partials of any num_voxels up to INT32_MAX (larger counts are rejected with
+ * G2V_ERR_LIMIT); calls that overlap on one GPU share it and race.  Same kernels, so the same
+ * results, bit for bit.  Asynchronous; allocates nothing. */
+int g2v_cosine_loss_forward_noalloc(long long num_voxels, int feat_dim, const float* voxel_label,
+                                    const unsigned char* occ_mask, const void* grid_feats, const void* pseudo_gt,
+                                    int feat_dtype, float* loss, int* num_valid, void* stream);
+
 /* g2v_cosine_loss_backward writes d loss / d grid_feats (X,Y,Z,feat_dim) for the upstream scalar
  * gradient grad_output (a device float: no host read, where the reference calls .item()) and the
  * forward's valid-voxel count; zero on invalid voxels.  Asynchronous, needs no workspace. */

@@ -47,6 +47,7 @@ SIGNATURES = {
                            _vp, _sz, _vp]),
     "g2v_cosine_loss_workspace": (_sz, [_ll, _i]),
     "g2v_cosine_loss_forward": (_i, [_ll, _i, _vp, _vp, _vp, _vp, _i, _vp, _vp, _ip, _vp, _sz, _vp]),
+    "g2v_cosine_loss_forward_noalloc": (_i, [_ll, _i, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp]),
     "g2v_cosine_loss_backward": (_i, [_ll, _i, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp]),
     "g2v_covariance_from_scale_rotation": (_i, [_i, _vp, _vp, _vp, _vp]),
     "g2v_covariance_from_scale_rotation_backward": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _vp]),

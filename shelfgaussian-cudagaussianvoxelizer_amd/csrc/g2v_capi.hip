@@ -577,6 +577,29 @@ int g2v_cosine_loss_forward(long long num_voxels, int feat_dim, const float* vox
     return G2V_OK;
 }
 
+int g2v_cosine_loss_forward_noalloc(long long num_voxels, int feat_dim, const float* voxel_label,
+                                    const unsigned char* occ_mask, const void* grid_feats, const void* pseudo_gt,
+                                    int feat_dtype, float* loss, int* num_valid, void* stream) {
+    g_err[0] = 0;
+    if (feat_dtype != G2V_DTYPE_F32 && feat_dtype != G2V_DTYPE_BF16)
+        return fail(G2V_ERR_INVALID, "feat_dtype = %d (G2V_DTYPE_F32 or G2V_DTYPE_BF16)", feat_dtype);
+    if (num_voxels < 0 || feat_dim < 0)
+        return fail(G2V_ERR_INVALID, "num_voxels = %lld, feat_dim = %d", num_voxels, feat_dim);
+    if (num_voxels > 2147483647ll)
+        return fail(G2V_ERR_LIMIT, "num_voxels = %lld exceeds the int32 valid-voxel count", num_voxels);
+    if (!loss || !num_valid) return fail(G2V_ERR_INVALID, "loss / num_valid is null");
+    if (num_voxels > 0 && (!voxel_label || !occ_mask || (feat_dim > 0 && (!grid_feats || !pseudo_gt))))
+        return fail(G2V_ERR_INVALID, "null input pointer");
+    const hipError_t e = launch_cosine_forward_noalloc(num_voxels, feat_dim, voxel_label, occ_mask, grid_feats,
+                                                       pseudo_gt, feat_dtype, loss, num_valid,
+                                                       static_cast<hipStream_t>(stream));
+    if (e == hipErrorInvalidValue)
+        return fail(G2V_ERR_LIMIT, "num_voxels = %lld needs more block partials than the %zu-byte scratch holds",
+                    num_voxels, cosine_scratch_bytes());
+    if (e != hipSuccess) return hip_fail(e, "launch_cosine_forward_noalloc");
+    return G2V_OK;
+}
+
 int g2v_cosine_loss_backward(long long num_voxels, int feat_dim, const float* grad_output,
                              const float* voxel_label, const unsigned char* occ_mask, const void* grid_feats,
                              const void* pseudo_gt, int feat_dtype, int num_valid_voxel, void* grad_grid_feats,

@@ -23,6 +23,7 @@
 #include "../../include/g2v.h"
 #include "g2v_internal.h"
 
+#include <mutex>
 #include <type_traits>
 
 namespace g2v {
@@ -394,6 +395,53 @@ hipError_t launch_cosine_backward(int64_t V, int C, const float* label, const ui
             return hipGetLastError();
         });
     });
+}
+
+// ---- forward without allocation ------------------------------------------------------------
+// The per-block partial sums of a forward live in this file-scope array instead of a caller's
+// workspace: one copy per GPU, held until the process ends.  A forward launches at most
+// kCosMaxBlocks blocks whatever the voxel count (voxels_per_block grows with it), and every block
+// writes its own partial, so a call never reads what an earlier call left.  Calls that overlap on
+// one GPU share the array and race.
+constexpr size_t kCosPartBytes = (size_t)kCosMaxBlocks * sizeof(float);
+constexpr size_t kCosScratchBytes = 2 * ((kCosPartBytes + 255) & ~size_t(255));
+static __device__ __align__(256) unsigned char scratch[kCosScratchBytes];
+
+size_t cosine_scratch_bytes() { return kCosScratchBytes; }
+
+// Device address of `scratch` on the current device, looked up once per device with that device
+// current (in host code the array's name is not a device address).
+static hipError_t scratch_address(void** out) {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static void* addr[kMaxDevices] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        addr[dev] = p;
+    }
+    *out = addr[dev];
+    return hipSuccess;
+}
+
+hipError_t launch_cosine_forward_noalloc(int64_t V, int C, const float* label, const uint8_t* mask, const void* p,
+                                         const void* g, int fdt, float* loss, int* count, hipStream_t s) {
+    // the partials of the largest grid a forward can see fit the array (checked, not assumed)
+    const int esize = fdt == kDtBF16 ? 2 : 4;
+    const bool vec = cosine_vec_ok(C, esize, p, g, nullptr);
+    const int L = lanes_for(vec ? C / 4 : C);
+    const int64_t blocks = V > 0 ? ceil_div(V, voxels_per_block(V, L)) : 0;
+    if (blocks > kCosMaxBlocks) return hipErrorInvalidValue;
+    void* ws = nullptr;
+    const hipError_t e = scratch_address(&ws);
+    if (e != hipSuccess) return e;
+    return launch_cosine_forward(V, C, label, mask, p, g, fdt, loss, count, ws, s);
 }
 
 }  // namespace g2v

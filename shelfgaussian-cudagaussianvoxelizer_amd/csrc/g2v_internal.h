@@ -138,6 +138,11 @@ bool cosine_vec_ok(int C, int esize, const void* a, const void* b, const void* c
 // hold elements of type fdt (kDtF32 or kDtBF16).
 hipError_t launch_cosine_forward(int64_t V, int C, const float* label, const uint8_t* mask, const void* p,
                                  const void* g, int fdt, float* loss, int* count, void* ws, hipStream_t s);
+// The same forward with the block partials in a file-scope device array of
+// cosine_scratch_bytes() bytes (per GPU) instead of a workspace: allocates nothing.
+size_t cosine_scratch_bytes();
+hipError_t launch_cosine_forward_noalloc(int64_t V, int C, const float* label, const uint8_t* mask, const void* p,
+                                         const void* g, int fdt, float* loss, int* count, hipStream_t s);
 // dloss/dp into grad_p (V x C, type fdt), grad_out a device scalar, inv_count = 1 / count (0 when
 // count = 0).
 hipError_t launch_cosine_backward(int64_t V, int C, const float* label, const uint8_t* mask, const void* p,
