@@ -189,7 +189,6 @@ constexpr int kBtPass = kBtGroups * kBtNbw * 32;       // 256 Gaussians per pass
 constexpr int kBtStages = 3;                           // F chunks resident in LDS (loaded 2 ahead)
 constexpr int kBtDma = kBtPass / 8 / kBtWaves;         // 1 KB direct-to-LDS loads per wave per chunk
 constexpr int kWtRow = 128;                            // bf16 per pair: 64 hi then 64 lo
-constexpr float kq = -0.72134752044448170f;            // exp(-m/2) = exp2(kq m)
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 

@@ -146,6 +146,8 @@ __device__ __forceinline__ void gauss_q(const GaussParams& p, float cx, float cy
     qz = p.A[6] * d0 + p.A[7] * d1 + p.A[8] * d2;
 }
 
+constexpr float kq = -0.72134752044448170f;   // -log2(e)/2: exp(-m/2) = exp2(kq m)
+
 __device__ __forceinline__ float centre(const Grid& G, int a, int i) {
     return fmaf((float)i + 0.5f, G.s[a], G.r0[a]);
 }

@@ -208,92 +208,141 @@ hipError_t launch_forward_density(const Grid& G, const float* means, const float
     return hipGetLastError();
 }
 
+// One list entry as the W build reads it, relative to the tile's first voxel (x0, y0, z0): the
+// exponent of exp2 at voxel (x0+a, y0+b, z0+c) is
+//     F(a,b) + Gxy(a,b) dz_c + fz_c,
+//     F = a00 dx^2 + a01 dx dy + a11 dy^2,  Gxy = a02 dx + a12 dy,  fz_c = kq A22 dz_c^2,
+// with dx, dy the offsets of the voxel centre from the mean, a00 = kq A00, a01 = kq (A01 + A10),
+// a11 = kq A11, a02 = kq (A02 + A20), a12 = kq (A12 + A21), kq = -log2(e)/2, so that
+// exp2(...) = exp(-dx^T A dx / 2) (reference .cu:911-921).  A voxel outside the box in z has
+// fz_c = -inf; one outside it in x or y (bit 4a+b of xymask clear) gets F = -inf; either way the
+// weight is exactly 0, as the reference's box test makes it.
+struct alignas(16) FwdRec {
+    float mux, muy, o, a12;
+    float a00, a01, a11, a02;
+    float dz[4];
+    float fz[4];
+    uint32_t xymask;
+    uint32_t pad[3];
+};
+static_assert(sizeof(FwdRec) == 80, "FwdRec is five 16-byte words");
+
 struct FwdSmem {
     bf16x8 whi[kFwdKSteps][2][64];   // A operand, hi part: [k step][voxel block][lane]
     bf16x8 wlo[kFwdKSteps][2][64];   // A operand, lo part
     alignas(16) uint32_t roff[kFwdKMax];   // byte offset of each K slot's packed row (zero row for padding)
-    FwdParam par[kFwdKMax];          // parameters of the K chunk's entries
-    float dpart[kFwdWaves][64];      // per-wave partial densities
+    FwdRec rec[kFwdKMax];            // the K chunk's entries
+    alignas(16) float dpart[kFwdWaves][64];   // per-wave partial densities
     alignas(16) float inv_den[64];   // 1 / max(D, eps)
     alignas(16) int vlin[64];        // linear voxel index, -1 outside the grid
 };
 
 // Builds the split W for K slots [kbeg, kbeg + 16*ksteps) of the tile list into LDS (slots past
-// klen get weight 0 and the zero row).  The parameters of the chunk's entries are staged in LDS
-// as packed records in one round (one entry per thread; padding entries get an empty box); then
-// wave w builds octets w, w+4, ... for the lane's voxel, branch-free, from broadcast reads.
-// Adds the raw density of the entries to dacc.
+// klen get weight 0 and the zero row).  First each thread turns one entry into its tile-relative
+// record.  Then thread t owns the voxel column (x0 + a, y0 + b), col = 4a + b = t % 16, and the
+// octets t/16, t/16 + 16, ...: for each of the octet's eight entries it forms F and Gxy once and
+// the four weights of its column from them, and writes the column's four voxels as finished A
+// fragments (8 entries x 1 voxel each).  Adds the raw weights of the column's voxels to dacc
+// (a build repeated for a later channel pass adds them again; only the first pass reads dacc).
 __device__ __forceinline__ void fwd_build_w(FwdSmem& sm, int j0, int kbeg, int klen, int ksteps,
-                                            bool add_density, float& dacc,
+                                            float (&dacc)[4],
                                             const float* __restrict__ means,
                                             const float* __restrict__ opacity,
                                             const float* __restrict__ cov_inv,
                                             const int* __restrict__ lb, const int* __restrict__ ub,
                                             const int* __restrict__ sorted_gauss, uint32_t row_bytes,
-                                            uint32_t zero_off, int x, int y, int z, float cx,
-                                            float cy, float cz) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+                                            uint32_t zero_off, int x0, int y0, int z0,
+                                            const float (&cz)[4], float cxl, float cyl) {
     const int nslots = ksteps * 16;
     for (int k = threadIdx.x; k < nslots; k += kFwdThreads) {
-        FwdParam r;
+        FwdRec r;
         if (k < klen) {
             const int g = sorted_gauss[j0 + kbeg + k];
+            float A[9];
 #pragma unroll
-            for (int a = 0; a < 3; ++a) {
-                r.mu[a] = means[g * 3 + a];
-                r.lb[a] = lb[g * 3 + a];
-                r.ub[a] = ub[g * 3 + a];
+            for (int i = 0; i < 9; ++i) A[i] = cov_inv[g * 9 + i];
+            const float mu2 = means[g * 3 + 2];
+            int l[3], u[3];
+#pragma unroll
+            for (int i = 0; i < 3; ++i) {
+                l[i] = lb[g * 3 + i];
+                u[i] = ub[g * 3 + i];
             }
-#pragma unroll
-            for (int a = 0; a < 9; ++a) r.A[a] = cov_inv[g * 9 + a];
+            r.mux = means[g * 3 + 0];
+            r.muy = means[g * 3 + 1];
             r.o = opacity[g];
+            r.a00 = kq * A[0];
+            r.a01 = kq * (A[1] + A[3]);
+            r.a11 = kq * A[4];
+            r.a02 = kq * (A[2] + A[6]);
+            r.a12 = kq * (A[5] + A[7]);
+            const float a22 = kq * A[8];
+            uint32_t xm = 0, ym = 0;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const float dz = cz[c] - mu2;
+                r.dz[c] = dz;
+                r.fz[c] = (z0 + c >= l[2] && z0 + c <= u[2]) ? a22 * dz * dz : -__builtin_inff();
+                xm |= (x0 + c >= l[0] && x0 + c <= u[0]) ? (1u << c) : 0u;
+                ym |= (y0 + c >= l[1] && y0 + c <= u[1]) ? (1u << c) : 0u;
+            }
+            uint32_t m = 0;
+#pragma unroll
+            for (int a = 0; a < 4; ++a) m |= (xm >> a) & 1u ? ym << (4 * a) : 0u;
+            r.xymask = m;
             sm.roff[k] = (uint32_t)g * row_bytes;
         } else {
+            r.mux = r.muy = r.o = r.a12 = 0.0f;
+            r.a00 = r.a01 = r.a11 = r.a02 = 0.0f;
 #pragma unroll
-            for (int a = 0; a < 3; ++a) { r.mu[a] = 0.0f; r.lb[a] = 1; r.ub[a] = 0; }   // empty box
-#pragma unroll
-            for (int a = 0; a < 9; ++a) r.A[a] = 0.0f;
-            r.o = 0.0f;
+            for (int c = 0; c < 4; ++c) {
+                r.dz[c] = 0.0f;
+                r.fz[c] = -__builtin_inff();
+            }
+            r.xymask = 0;
             sm.roff[k] = zero_off;
         }
-        r.pad = 0;
-        sm.par[k] = r;
+        r.pad[0] = r.pad[1] = r.pad[2] = 0;
+        sm.rec[k] = r;
     }
     __syncthreads();
+    const int col = threadIdx.x & 15;
     const int noct = ksteps * 2;
-    for (int o = wave; o < noct; o += kFwdWaves) {
-        // Straight-line evaluation (bitwise box test, exponential always computed, then
-        // selected): with no branches the compiler can issue the record reads of all eight
-        // entries ahead of their arithmetic.
-        float wv[8];
+    for (int o = threadIdx.x >> 4; o < noct; o += kFwdThreads / 16) {
+        float wv[4][8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const uint4* rp = reinterpret_cast<const uint4*>(&sm.par[o * 8 + i]);   // broadcast
-            const uint4 q0 = rp[0], q1 = rp[1], q2 = rp[2], q3 = rp[3], q4 = rp[4];
-            const float mu0 = __uint_as_float(q0.x), mu1 = __uint_as_float(q0.y), mu2 = __uint_as_float(q0.z);
-            const float ro = __uint_as_float(q0.w);
-            const float A0 = __uint_as_float(q1.x), A1 = __uint_as_float(q1.y), A2 = __uint_as_float(q1.z);
-            const float A3 = __uint_as_float(q1.w), A4 = __uint_as_float(q2.x), A5 = __uint_as_float(q2.y);
-            const float A6 = __uint_as_float(q2.z), A7 = __uint_as_float(q2.w), A8 = __uint_as_float(q3.x);
-            const int lb0 = (int)q3.y, lb1 = (int)q3.z, lb2 = (int)q3.w;
-            const int ub0 = (int)q4.x, ub1 = (int)q4.y, ub2 = (int)q4.z;
-            const bool in = (x >= lb0) & (x <= ub0) & (y >= lb1) & (y <= ub1) & (z >= lb2) & (z <= ub2);
-            const float d0 = cx - mu0, d1 = cy - mu1, d2 = cz - mu2;
-            const float qx = A0 * d0 + A1 * d1 + A2 * d2;
-            const float qy = A3 * d0 + A4 * d1 + A5 * d2;
-            const float qz = A6 * d0 + A7 * d1 + A8 * d2;
-            const float m = d0 * qx + d1 * qy + d2 * qz;
-            const float e = __expf(-0.5f * m);
-            const float w = in ? ro * e : 0.0f;   // the reference's weight (.cu:911-921)
-            if (add_density) dacc += w;
-            wv[i] = (w > 0.0f) ? w : 0.0f;   // feature gate of the reference (.cu:936)
+            const uint4* rp = reinterpret_cast<const uint4*>(&sm.rec[o * 8 + i]);   // 16 lanes each
+            const uint4 q0 = rp[0], q1 = rp[1], q2 = rp[2], q3 = rp[3];
+            const uint32_t m = sm.rec[o * 8 + i].xymask;
+            const float dx = cxl - __uint_as_float(q0.x), dy = cyl - __uint_as_float(q0.y);
+            const float ro = __uint_as_float(q0.z), a12 = __uint_as_float(q0.w);
+            const float a00 = __uint_as_float(q1.x), a01 = __uint_as_float(q1.y);
+            const float a11 = __uint_as_float(q1.z), a02 = __uint_as_float(q1.w);
+            const float dz[4] = {__uint_as_float(q2.x), __uint_as_float(q2.y), __uint_as_float(q2.z),
+                                 __uint_as_float(q2.w)};
+            const float fz[4] = {__uint_as_float(q3.x), __uint_as_float(q3.y), __uint_as_float(q3.z),
+                                 __uint_as_float(q3.w)};
+            float F = fmaf(fmaf(a00, dx, a01 * dy), dx, a11 * dy * dy);
+            F = ((m >> col) & 1u) ? F : -__builtin_inff();
+            const float Gxy = fmaf(a02, dx, a12 * dy);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const float w = ro * __builtin_amdgcn_exp2f(fmaf(Gxy, dz[c], F) + fz[c]);
+                dacc[c] += w;
+                wv[c][i] = fmaxf(w, 0.0f);   // feature gate of the reference (.cu:936)
+            }
         }
-        bf16x8 h, l;
-        split8(wv, h, l);
-        const int s = o >> 1, mb = lane >> 5;
-        const int slot = (o & 1) * 32 + (lane & 31);
-        sm.whi[s][mb][slot] = h;
-        sm.wlo[s][mb][slot] = l;
+        // voxel (a, b, c) of the tile is row 16a + 4b + c of W: block a/2, row 16(a%2) + 4b + c
+        const int s = o >> 1, mb = col >> 3;
+        const int slot = (o & 1) * 32 + (col & 7) * 4;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            bf16x8 h, l;
+            split8(wv[c], h, l);
+            sm.whi[s][mb][slot + c] = h;
+            sm.wlo[s][mb][slot + c] = l;
+        }
     }
 }
 
@@ -314,8 +363,13 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
 
     int x, y, z;
     tile_voxel(G, tile, lane, x, y, z);
-    const float cx = centre(G, 0, x), cy = centre(G, 1, y), cz = centre(G, 2, z);
     if (wave == 0) sm.vlin[lane] = in_grid(G, x, y, z) ? (int)voxel_index(G, x, y, z) : -1;
+    // the tile's first voxel, the z centres of its four layers and the centre of this thread's
+    // W-build column (x0 + col/4, y0 + col%4)
+    const int x0 = x & ~(kTile - 1), y0 = y & ~(kTile - 1), z0 = z & ~(kTile - 1);
+    const float cz[4] = {centre(G, 2, z0), centre(G, 2, z0 + 1), centre(G, 2, z0 + 2), centre(G, 2, z0 + 3)};
+    const int col = threadIdx.x & 15;
+    const float cxl = centre(G, 0, x0 + (col >> 2)), cyl = centre(G, 1, y0 + (col & 3));
 
     const int j0 = uniform(min(max(toff[tile], 0), M));
     const int Ng = uniform(min(max(toff[tile + 1], j0), M)) - j0;
@@ -324,7 +378,7 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
     const uint32_t row_bytes = (uint32_t)Cp * kCh;
     const uint32_t zero_off = (uint32_t)n * row_bytes;
     const char* fbase = reinterpret_cast<const char*>(fpk);
-    float dacc = 0.0f;
+    float dacc[4] = {0.0f, 0.0f, 0.0f, 0.0f};   // density of the column's voxels, this thread's octets
 
     for (int cbase = 0; cbase < C; cbase += kFwdChanPerPass) {
         const int cw0 = cbase + wave * kFwdChanPerWave;          // first channel of this wave
@@ -342,8 +396,8 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
             const int ksteps = ((klen + 31) >> 5) * 2;   // even: the MFMA loop takes steps in pairs
             if (nkc > 1 || cbase == 0) {
                 __syncthreads();  // previous readers of W are done
-                fwd_build_w(sm, j0, kbeg, klen, ksteps, cbase == 0, dacc, means, opacity, cov_inv, lb,
-                            ub, sorted_gauss, row_bytes, zero_off, x, y, z, cx, cy, cz);
+                fwd_build_w(sm, j0, kbeg, klen, ksteps, dacc, means, opacity, cov_inv, lb,
+                            ub, sorted_gauss, row_bytes, zero_off, x0, y0, z0, cz, cxl, cyl);
                 __syncthreads();
             }
             if (has_ch) {
@@ -409,7 +463,14 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
         }
 
         if (cbase == 0) {
-            sm.dpart[wave][lane] = dacc;
+            // the 16 threads of a column: four per wave (lanes col, col + 16, col + 32, col + 48)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                dacc[c] += __shfl_xor(dacc[c], 16);
+                dacc[c] += __shfl_xor(dacc[c], 32);
+            }
+            if (lane < 16)
+                *reinterpret_cast<float4*>(&sm.dpart[wave][4 * lane]) = make_float4(dacc[0], dacc[1], dacc[2], dacc[3]);
             __syncthreads();
             if (wave == 0) {
                 float D = 0.0f;
