@@ -187,6 +187,67 @@ def cosine_leg(_C, grid_feats, steps, warmup):
     return out
 
 
+def cosine_fused_leg(w, md, od, cd, fd, gDd, steps, warmup):
+    """Voxelizer + feature cosine loss, fwd+bwd of density.gD + loss: chained (the two modules and
+    autograd: the loss's backward writes the (X,Y,Z,C) gradient of grid_feats, the voxelizer's
+    reads it back) against PyCudaGaussianVoxelizerCosineLoss (that gradient formed inside the
+    feature-gradient kernels).  ms per step on the current stream's HIP events (host waits
+    included), and the step's peak allocation."""
+    import torch
+    from CudaGaussianVoxelizer import (PyCudaFeatsCosineLoss, PyCudaGaussianVoxelizer,
+                                       PyCudaGaussianVoxelizerCosineLoss)
+    dev = md.device
+    X, Y, Z = _grid(w)
+    C = fd.shape[1]
+    gen = torch.Generator().manual_seed(11)
+    label = torch.randint(0, 3, (X, Y, Z), generator=gen).to(torch.float32).to(dev)
+    mask = (torch.rand((X, Y, Z), generator=gen) < 0.8).to(dev)
+    target = torch.randn((X, Y, Z, C), generator=gen).to(dev)
+    one = torch.ones((), device=dev)
+    vox = PyCudaGaussianVoxelizer(w.voxel_size, w.voxel_range)
+    cos = PyCudaFeatsCosineLoss(w.voxel_size, w.voxel_range)
+    fused = PyCudaGaussianVoxelizerCosineLoss(w.voxel_size, w.voxel_range)
+    leaves = [t.detach().requires_grad_(True) for t in (md, od, cd, fd)]
+
+    def chained():
+        density, grid_feats, _ = vox(*leaves)
+        loss, _ = cos(label, mask, grid_feats, target)
+        torch.autograd.backward([density, loss], [gDd, one])
+
+    def fused_step():
+        density, loss, _, _ = fused(leaves[0], leaves[1], leaves[2], leaves[3], label, mask, target)
+        torch.autograd.backward([density, loss], [gDd, one])
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        base = torch.cuda.memory_allocated()
+        torch.cuda.reset_peak_memory_stats()
+        cur = torch.cuda.current_stream()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(cur)
+        for _ in range(steps):
+            for t in leaves:
+                t.grad = None
+            fn()
+        b.record(cur)
+        b.synchronize()
+        return round(a.elapsed_time(b) / steps, 4), round((torch.cuda.max_memory_allocated() - base) / 1e9, 3)
+
+    ch_ms, ch_gb = timed(chained)
+    fu_ms, fu_gb = timed(fused_step)
+    return {"grid": [X, Y, Z], "feat_dim": C, "chained_ms": ch_ms, "fused_ms": fu_ms,
+            "speedup": round(ch_ms / fu_ms, 3), "chained_step_peak_gb": ch_gb, "fused_step_peak_gb": fu_gb,
+            "data": "the G2V workload with a randn target (seed 11), 80 % of voxels visible, labels 0..2; "
+                    "objective density.gD + loss"}
+
+
+def _grid(w):
+    from CudaGaussianVoxelizer import _C
+    return _C.grid_dims(w.voxel_size, w.voxel_range)[0]
+
+
 def covariance_leg(_C, n, steps):
     """Covariances from scales and rotations (reference test/gaussian_voxelizer.py:14-37) for the
     config's Gaussian count, forward and backward: HIP event spans on the current stream, averaged
@@ -421,6 +482,7 @@ def main():
     cosine = None
     if C > 0 and not args.no_cosine:
         cosine = cosine_leg(_C, out[5].detach(), args.steps, args.warmup)
+        cosine["fused_backward"] = cosine_fused_leg(w, md, od, cd, fd, gDd, min(args.steps, 10), args.warmup)
 
     cpu = None
     if not args.no_cpu and args.gpus == 1:

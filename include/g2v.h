@@ -153,6 +153,32 @@ int g2v_backward_prepared(int n, int feat_dim, const float* grad_density, const 
                           const int* t2g_tiles, const int* t2g_gauss, const int* t2g_offsets,
                           const void* plan_workspace, void* workspace, size_t workspace_bytes, void* stream);
 
+/* g2v_backward_cosine: g2v_backward when the upstream gradient of grid_feats is that of the
+ * feature cosine loss (g2v_cosine_loss_forward_coef on this grid_feats and pseudo_gt), fused into
+ * the feature backward.  The reference chains the two through autograd (CudaGaussianVoxelizer/
+ * __init__.py:36-67): src/cuda_feats_loss.cu:233-366 writes the gradient of grid_feats and
+ * src/cuda_gaussian_voxelizer.cu:1920-2057 reads it.  Instead of reading an (X,Y,Z,feat_dim)
+ * grad_feats, the kernels form it per voxel on chip as
+ *     k1 pseudo_gt + k2 grid_feats,  (k1, k2) = coef[2v .. 2v+1] * grad_loss[0] / num_valid_voxel
+ * (0 when num_valid_voxel == 0), the expression of g2v_cosine_loss_backward, so the gradient is
+ * never written to or read from memory.  grad_loss is the device float upstream gradient of the
+ * loss.  float32 features (feat_dtype G2V_DTYPE_F32) with feat_dim % 4 == 0; pseudo_gt and
+ * grid_feats 16-byte aligned.  prepared != 0: the workspace was filled by g2v_backward_prepare
+ * (as for g2v_backward_prepared; the Tile->Gaussian CSR arguments are then required).  The other
+ * arguments are g2v_backward's.  Asynchronous. */
+int g2v_backward_cosine(int n, int feat_dim, const float* grad_density, const float* grad_loss,
+                        const void* pseudo_gt, const float* coef, int num_valid_voxel,
+                        const float* means3D, const float* opacity, const float* cov_inv,
+                        const float voxel_size[3], const float voxel_range[6],
+                        const int* valid_voxel_lb, const int* valid_voxel_ub,
+                        const int* num_voxels_per_gaussian, const int* g2t_offsets,
+                        const int* g2t_tile_ids, long long num_pairs, long long num_region_pairs,
+                        const float* density, const void* grid_feats, const void* features, int feat_dtype,
+                        float* grad_means, float* grad_cov, float* grad_opacity, void* grad_features,
+                        const int* t2g_tiles, const int* t2g_gauss, const int* t2g_offsets,
+                        const void* plan_workspace, void* workspace, size_t workspace_bytes, int prepared,
+                        void* stream);
+
 /* ---- Tile->Gaussian CSR (inspection) -------------------------------------------------------
  * The internal Tile->Gaussian CSR of the forward, for parity tests: the stable sort of the G->T
  * pairs by tile (sorted_tiles, sorted_gauss: M each; reference .cu:1673-1691), the list bounds of
@@ -186,6 +212,15 @@ int g2v_cosine_loss_forward(long long num_voxels, int feat_dim, const float* vox
                             const unsigned char* occ_mask, const void* grid_feats, const void* pseudo_gt,
                             int feat_dtype, float* loss, int* num_valid, int* num_valid_host, void* workspace,
                             size_t workspace_bytes, void* stream);
+
+/* g2v_cosine_loss_forward_coef: g2v_cosine_loss_forward that also writes, for g2v_backward_cosine,
+ * the unscaled gradient coefficients of every voxel into coef (num_voxels x 2 floats, 8-byte
+ * aligned): (c1, c2) with d loss / d grid_feats = (c1 pseudo_gt + c2 grid_feats) grad / count on a
+ * valid voxel (reference src/cuda_feats_loss.cu:278-291), (0, 0) on the others. */
+int g2v_cosine_loss_forward_coef(long long num_voxels, int feat_dim, const float* voxel_label,
+                                 const unsigned char* occ_mask, const void* grid_feats, const void* pseudo_gt,
+                                 int feat_dtype, float* loss, int* num_valid, int* num_valid_host, float* coef,
+                                 void* workspace, size_t workspace_bytes, void* stream);
 
 /* g2v_cosine_loss_forward_noalloc: g2v_cosine_loss_forward without a workspace and without the
  * host count, for callers that cannot allocate device memory (code under HIP graph capture, tight

@@ -236,13 +236,32 @@ def gaussian_voxelizer_backward(grad_output, grad_feats_output, means3D, opacity
                      density, grid_feats, features, t2g=None)
 
 
+def gaussian_voxelizer_backward_cosine(grad_output, grad_loss, pseudo_dino_gt, coef, num_valid_voxel, means3D,
+                                       opacity, cov_inv, voxel_size, voxel_range, valid_voxel_lb, valid_voxel_ub,
+                                       num_voxels_per_gaussian, g2t_offsets, g2t_tile_ids, density, grid_feats,
+                                       features):
+    """gaussian_voxelizer_backward with the feature cosine loss's gradient as the upstream gradient
+    of grid_feats, fused (g2v_backward_cosine): the (X,Y,Z,C) gradient that the reference's
+    CudaFeatsCosinelossBackward writes and its voxelizer backward reads (src/cuda_feats_loss.cu:
+    311-366, src/cuda_gaussian_voxelizer.cu:1920-2057) is formed per voxel inside the kernels.
+    grad_loss: the upstream gradient of the loss (one-element GPU tensor); coef and num_valid_voxel
+    as _cosine_forward(..., want_coef=True) returned them for this grid_feats and pseudo_dino_gt
+    (float32, C % 4 == 0).  Returns gaussian_voxelizer_backward's 5-tuple."""
+    gl = grad_loss.detach().to(device=means3D.device, dtype=torch.float32).reshape(1).contiguous()
+    return _backward(grad_output, None, means3D, opacity, cov_inv, voxel_size, voxel_range, valid_voxel_lb,
+                     valid_voxel_ub, num_voxels_per_gaussian, g2t_offsets, g2t_tile_ids, density, grid_feats,
+                     features, t2g=None, cosine=(gl, pseudo_dino_gt, coef, num_valid_voxel))
+
+
 def _backward(grad_output, grad_feats_output, means3D, opacity, cov_inv, voxel_size, voxel_range,
               valid_voxel_lb, valid_voxel_ub, num_voxels_per_gaussian, g2t_offsets, g2t_tile_ids,
-              density, grid_feats, features, t2g, timed=True):
+              density, grid_feats, features, t2g, timed=True, cosine=None):
     """The backward; t2g is what _forward(keep_t2g=True) returned beside the 9-tuple, or None.
     With t2g the saved tensors are the forward's own outputs (already checked there), and the
     grid, plan, outputs and workspace come from the forward: only the upstream gradients are
-    checked here."""
+    checked here.  cosine = (grad_loss, pseudo_dino_gt, coef, num_valid_voxel): the upstream
+    gradient of grid_feats is the cosine loss's, formed inside the kernels (grad_feats_output is
+    ignored)."""
     lib = _lib.load()
     if not isinstance(means3D, torch.Tensor) or means3D.device.type != "cuda":
         raise RuntimeError("means3D must be a GPU tensor")
@@ -283,12 +302,23 @@ def _backward(grad_output, grad_feats_output, means3D, opacity, cov_inv, voxel_s
             feats = features
             if grid_feats.dtype != fdtype:
                 raise RuntimeError(f"grid_feats ({grid_feats.dtype}) and features ({fdtype}) differ in type")
-            # the upstream feature gradient is taken in the features' type (a float32 gradient of
-            # bfloat16 features is rounded to bfloat16, a bfloat16 one of float32 features widened)
-            if isinstance(grad_feats_output, torch.Tensor) and grad_feats_output.dtype != fdtype \
-                    and grad_feats_output.dtype in _FEAT_DTYPES:
-                grad_feats_output = grad_feats_output.to(fdtype).contiguous()
-            _check_saved(grad_feats_output, "grad_feats_output", fdtype, dev)
+            if cosine is not None:
+                grad_feats_output = cosine[1]   # checked as the stand-in upstream tensor
+                coef, gl = cosine[2], cosine[0]
+                _check_saved(coef, "coef", f32, dev)
+                _check_saved(gl, "grad_loss", f32, dev)
+                if tuple(coef.shape) != (X * Y * Z, 2) or gl.numel() != 1:
+                    raise RuntimeError(f"coef must be ({X * Y * Z}, 2) and grad_loss one element")
+                if fdtype != f32 or C % 4 != 0:
+                    raise RuntimeError("the fused cosine gradient takes float32 features with C % 4 == 0")
+            else:
+                # the upstream feature gradient is taken in the features' type (a float32 gradient of
+                # bfloat16 features is rounded to bfloat16, a bfloat16 one of float32 features widened)
+                if isinstance(grad_feats_output, torch.Tensor) and grad_feats_output.dtype != fdtype \
+                        and grad_feats_output.dtype in _FEAT_DTYPES:
+                    grad_feats_output = grad_feats_output.to(fdtype).contiguous()
+            _check_saved(grad_feats_output, "pseudo_dino_gt" if cosine is not None else "grad_feats_output",
+                         fdtype, dev)
             if tuple(grad_feats_output.shape) != (X, Y, Z, C) or tuple(grid_feats.shape) != (X, Y, Z, C):
                 raise RuntimeError("grad_feats_output and grid_feats must be (X, Y, Z, C)")
             gF = grad_feats_output
@@ -323,15 +353,29 @@ def _backward(grad_output, grad_feats_output, means3D, opacity, cov_inv, voxel_s
             ws = torch.empty(max(1, lib.g2v_backward_workspace(n, C, M, MR, vs, vr)), dtype=torch.uint8, device=dev)
         csr = t2g["csr"] if t2g else (None, None, None)
         # the forward queued the gradient-independent part into this workspace
-        entry = lib.g2v_backward_prepared if (trusted and C > 0 and t2g.get("prepared")) else lib.g2v_backward
-        _lib.check(entry(n, C, _ptr(grad_output), _ptr(gF), _ptr(means3D), _ptr(opacity),
-                                    _ptr(cov_inv), vs, vr, _ptr(valid_voxel_lb), _ptr(valid_voxel_ub),
-                                    _ptr(num_voxels_per_gaussian), _ptr(g2t_offsets), _ptr(g2t_tile_ids),
-                                    M, MR, _ptr(density), _ptr(grid_feats), _ptr(feats), fdt,
-                                    _ptr(grad_means), _ptr(grad_cov), _ptr(grad_opacity),
-                                    _ptr(grad_feats), _ptr(csr[0]), _ptr(csr[1]), _ptr(csr[2]),
-                                    _ptr(plan_ws), _ptr(ws), ws.numel(), stream),
-                   "gaussian_voxelizer_backward")
+        prepared = bool(trusted and C > 0 and t2g.get("prepared"))
+        if cosine is not None and C > 0:
+            grad_loss, _, coef, num_valid = cosine
+            _lib.check(lib.g2v_backward_cosine(n, C, _ptr(grad_output), _ptr(grad_loss), _ptr(gF), _ptr(coef),
+                                               int(num_valid), _ptr(means3D), _ptr(opacity), _ptr(cov_inv), vs, vr,
+                                               _ptr(valid_voxel_lb), _ptr(valid_voxel_ub),
+                                               _ptr(num_voxels_per_gaussian), _ptr(g2t_offsets),
+                                               _ptr(g2t_tile_ids), M, MR, _ptr(density), _ptr(grid_feats),
+                                               _ptr(feats), fdt, _ptr(grad_means), _ptr(grad_cov),
+                                               _ptr(grad_opacity), _ptr(grad_feats), _ptr(csr[0]), _ptr(csr[1]),
+                                               _ptr(csr[2]), _ptr(plan_ws), _ptr(ws), ws.numel(), int(prepared),
+                                               stream),
+                       "gaussian_voxelizer_backward_cosine")
+        else:
+            entry = lib.g2v_backward_prepared if prepared else lib.g2v_backward
+            _lib.check(entry(n, C, _ptr(grad_output), _ptr(gF), _ptr(means3D), _ptr(opacity),
+                             _ptr(cov_inv), vs, vr, _ptr(valid_voxel_lb), _ptr(valid_voxel_ub),
+                             _ptr(num_voxels_per_gaussian), _ptr(g2t_offsets), _ptr(g2t_tile_ids),
+                             M, MR, _ptr(density), _ptr(grid_feats), _ptr(feats), fdt,
+                             _ptr(grad_means), _ptr(grad_cov), _ptr(grad_opacity),
+                             _ptr(grad_feats), _ptr(csr[0]), _ptr(csr[1]), _ptr(csr[2]),
+                             _ptr(plan_ws), _ptr(ws), ws.numel(), stream),
+                       "gaussian_voxelizer_backward")
         bwd_sec = 0.0
         if timed:
             stop.record(cur)
@@ -637,6 +681,13 @@ def CudaFeatsCosinelossForward(voxel_label, occ_gt_mask_camera, grid_feats, pseu
     1 - cos(grid_feats, pseudo_dino_gt) as a 0-dim GPU tensor (0 without valid voxels), the number
     of valid voxels (int) and the forward time in seconds.
     """
+    loss, cnt, fwd_sec, _ = _cosine_forward(voxel_label, occ_gt_mask_camera, grid_feats, pseudo_dino_gt, False)
+    return loss, cnt, fwd_sec
+
+
+def _cosine_forward(voxel_label, occ_gt_mask_camera, grid_feats, pseudo_dino_gt, want_coef):
+    """CudaFeatsCosinelossForward; want_coef also returns the (X*Y*Z, 2) float32 tensor of the
+    voxels' unscaled gradient coefficients (g2v_cosine_loss_forward_coef), else None."""
     lib = _lib.load()
     V, C, dev, fdt = _cosine_inputs(voxel_label, occ_gt_mask_camera, grid_feats, pseudo_dino_gt)
     with _OnDevice(dev):
@@ -644,18 +695,21 @@ def CudaFeatsCosinelossForward(voxel_label, occ_gt_mask_camera, grid_feats, pseu
         loss = torch.empty((), dtype=torch.float32, device=dev)
         cnt_dev = torch.empty((), dtype=torch.int32, device=dev)
         ws = torch.empty(lib.g2v_cosine_loss_workspace(V, C), dtype=torch.uint8, device=dev)
+        coef = torch.empty(V, 2, dtype=torch.float32, device=dev) if want_coef else None
         cnt = ctypes.c_int(0)
         start, stop = _timing_events(dev)
         start.record(cur)
-        _lib.check(lib.g2v_cosine_loss_forward(V, C, _ptr(voxel_label), _ptr(occ_gt_mask_camera),
-                                               _ptr(grid_feats), _ptr(pseudo_dino_gt), fdt, _ptr(loss),
-                                               _ptr(cnt_dev), ctypes.byref(cnt), _ptr(ws), ws.numel(),
-                                               ctypes.c_void_p(cur.cuda_stream)),
-                   "CudaFeatsCosinelossForward")
+        args = (V, C, _ptr(voxel_label), _ptr(occ_gt_mask_camera), _ptr(grid_feats), _ptr(pseudo_dino_gt), fdt,
+                _ptr(loss), _ptr(cnt_dev), ctypes.byref(cnt))
+        tail = (_ptr(ws), ws.numel(), ctypes.c_void_p(cur.cuda_stream))
+        if want_coef:
+            _lib.check(lib.g2v_cosine_loss_forward_coef(*args, _ptr(coef), *tail), "CudaFeatsCosinelossForward")
+        else:
+            _lib.check(lib.g2v_cosine_loss_forward(*args, *tail), "CudaFeatsCosinelossForward")
         stop.record(cur)
         stop.synchronize()
         fwd_sec = start.elapsed_time(stop) / 1000.0
-    return loss, int(cnt.value), fwd_sec
+    return loss, int(cnt.value), fwd_sec, coef
 
 
 def CudaFeatsCosinelossBackward(grad_output, voxel_label, occ_gt_mask_camera, grid_feats, pseudo_dino_gt,

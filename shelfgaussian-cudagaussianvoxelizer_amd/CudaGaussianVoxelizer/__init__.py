@@ -13,7 +13,7 @@ from . import _C
 from ._C import gaussian_voxelizer_forward, gaussian_voxelizer_backward
 from ._C import CudaFeatsCosinelossForward, CudaFeatsCosinelossBackward, gaussian_voxelizer_forward_batched
 
-__all__ = ["PyCudaGaussianVoxelizer", "PyCudaFeatsCosineLoss", "_C",
+__all__ = ["PyCudaGaussianVoxelizer", "PyCudaFeatsCosineLoss", "PyCudaGaussianVoxelizerCosineLoss", "_C",
            "gaussian_voxelizer_forward", "gaussian_voxelizer_backward", "gaussian_voxelizer_forward_batched",
            "CudaFeatsCosinelossForward", "CudaFeatsCosinelossBackward", "covariance_from_scale_rotation"]
 
@@ -101,6 +101,79 @@ class _CudaFeatsCosinelossFunction(torch.autograd.Function):
                                                             d_grid_feats, pseudo_dino_gt, ctx.num_valid_voxel)
         stats[1] = bwd_sec
         return None, None, grad_predict, None
+
+
+def _fusable(grid_feats, pseudo_dino_gt):
+    """The fused cosine gradient applies: float32 rows of a multiple of 4 channels, 16-byte aligned."""
+    return (grid_feats.dtype == torch.float32 and pseudo_dino_gt.dtype == torch.float32
+            and grid_feats.shape[-1] > 0 and grid_feats.shape[-1] % 4 == 0
+            and grid_feats.data_ptr() % 16 == 0 and pseudo_dino_gt.data_ptr() % 16 == 0)
+
+
+class _CudaGaussianVoxelizeCosineLossFunction(torch.autograd.Function):
+    """The voxelizer (reference CudaGaussianVoxelizer/__init__.py:10-47) followed by the feature
+    cosine loss on its grid_feats (:49-67), with the loss's gradient fused into the voxelizer's
+    backward: the (X,Y,Z,C) gradient of grid_feats that the reference writes between the two
+    backwards is formed per voxel inside the feature-gradient kernels (_C.gaussian_voxelizer_
+    backward_cosine).  grid_feats is returned without a gradient path of its own.  float32 inputs
+    with C % 4 == 0 take the fused kernels; other feature types chain the two backwards."""
+
+    @staticmethod
+    def forward(ctx, means3D, opacity, covariances, voxel_size, voxel_range, features, voxel_label,
+                occ_gt_mask_camera, pseudo_dino_gt, need_backward=None):
+        if features is None or features.shape[-1] == 0:
+            raise RuntimeError("the cosine loss needs features")
+        keep = _wants_backward(ctx, need_backward)
+        (density, cov_inv, valid_voxel_lb, valid_voxel_ub, num_valid_voxel, grid_feats, g2t_offsets,
+         g2t_tile_ids, fwd_sec), t2g = _C._forward(means3D, opacity, covariances, voxel_size,
+                                                   voxel_range, features, keep_t2g=keep)
+        fused = keep and _fusable(grid_feats, pseudo_dino_gt)
+        loss, count, cos_sec, coef = _C._cosine_forward(voxel_label, occ_gt_mask_camera, grid_feats,
+                                                        pseudo_dino_gt, fused)
+        stats = torch.zeros(2, dtype=torch.float32, device="cpu")
+        stats[0] = fwd_sec + cos_sec
+        ctx.save_for_backward(means3D, opacity, voxel_size, voxel_range, cov_inv, valid_voxel_lb,
+                              valid_voxel_ub, num_valid_voxel, g2t_offsets, g2t_tile_ids, density,
+                              grid_feats, features, voxel_label, occ_gt_mask_camera, pseudo_dino_gt, coef,
+                              stats)
+        ctx.t2g = t2g
+        ctx.count = count
+        ctx.fused = fused
+        ctx.mark_non_differentiable(grid_feats, stats)
+        # no zero-filled (X,Y,Z,C) gradient for grid_feats: unused outputs arrive as None
+        ctx.set_materialize_grads(False)
+        ctx.opacity_shape = opacity.shape
+        ctx.cov_shape = covariances.shape
+        return density, loss, grid_feats, stats
+
+    @staticmethod
+    def backward(ctx, grad_density_output, grad_loss, grad_grid_feats, grad_stats):
+        (means32, op32, voxsz32, voxrg32, cov_inv, valid_voxel_lb, valid_voxel_ub, num_valid_voxel,
+         g2t_offsets, g2t_tile_ids, density, grid_feats, features, voxel_label, occ_gt_mask_camera,
+         pseudo_dino_gt, coef, stats) = ctx.saved_tensors
+        gout32 = torch.zeros_like(density) if grad_density_output is None else \
+            grad_density_output.to(torch.float32).contiguous()
+        gl32 = torch.zeros(1, dtype=torch.float32, device=density.device) if grad_loss is None else \
+            grad_loss.detach().to(torch.float32).reshape(1).contiguous()
+        means32 = means32.detach().contiguous()
+        op32 = op32.detach().reshape(-1).contiguous()
+        feats = features.detach().contiguous()
+        saved = (means32, op32, cov_inv, voxsz32, voxrg32, valid_voxel_lb, valid_voxel_ub, num_valid_voxel,
+                 g2t_offsets, g2t_tile_ids, density, grid_feats, feats)
+        if ctx.fused:
+            res = _C._backward(gout32, None, *saved, t2g=ctx.t2g,
+                               cosine=(gl32, pseudo_dino_gt, coef, ctx.count))
+            bwd_sec = res[4]
+        else:   # chained: the loss's gradient of grid_feats, then the voxelizer's backward
+            grad_grid, cos_sec = _C.CudaFeatsCosinelossBackward(gl32, voxel_label, occ_gt_mask_camera, grid_feats,
+                                                                pseudo_dino_gt, ctx.count)
+            res = _C._backward(gout32, grad_grid, *saved, t2g=ctx.t2g)
+            bwd_sec = res[4] + cos_sec
+        grad_means3D, grad_cov, grad_opacity, grad_feats, _ = res
+        ctx.t2g = None
+        stats[1] = bwd_sec
+        return (grad_means3D, grad_opacity.reshape(ctx.opacity_shape), grad_cov.reshape(ctx.cov_shape), None,
+                None, grad_feats, None, None, None, None)
 
 
 class _CudaGaussianVoxelizeBatchedFunction(torch.autograd.Function):
@@ -196,6 +269,28 @@ class PyCudaGaussianVoxelizer(nn.Module):
                                                               self.voxel_range, features, need)
         return _CudaGaussianVoxelizeFunction.apply(means3D, opacity, covariances, self.voxel_size,
                                                    self.voxel_range, features, need)
+
+
+class PyCudaGaussianVoxelizerCosineLoss(PyCudaGaussianVoxelizer):
+    """PyCudaGaussianVoxelizer followed by PyCudaFeatsCosineLoss on its grid_feats, as one op whose
+    backward forms the loss's gradient of grid_feats inside the voxelizer's feature-gradient kernels
+    instead of writing and re-reading it (2.6 GB at 200 x 200 x 16 x 1024 float32).
+
+    ``forward(means3D, opacity, covariances, features, voxel_label, occ_gt_mask_camera,
+    pseudo_dino_gt)`` returns ``(density, loss, grid_feats, stats)``: density and loss carry
+    gradients (to means3D, opacity, covariances and features), grid_feats does not, stats is the CPU
+    float32 tensor ``[fwd_sec, bwd_sec]`` of both ops together.  One scene (means3D (N, 3)).
+    """
+
+    def forward(self, means3D, opacity, covariances, features, voxel_label, occ_gt_mask_camera, pseudo_dino_gt):
+        if means3D.dim() != 2:
+            raise RuntimeError("PyCudaGaussianVoxelizerCosineLoss takes one scene: means3D (N, 3)")
+        if covariances.dtype in (torch.float16, torch.bfloat16):
+            covariances = covariances.float()
+        need = _grad_possible(means3D, opacity, covariances, features)
+        return _CudaGaussianVoxelizeCosineLossFunction.apply(means3D, opacity, covariances, self.voxel_size,
+                                                             self.voxel_range, features, voxel_label,
+                                                             occ_gt_mask_camera, pseudo_dino_gt, need)
 
 
 class PyCudaFeatsCosineLoss(nn.Module):

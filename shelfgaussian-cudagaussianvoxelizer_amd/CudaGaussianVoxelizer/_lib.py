@@ -13,7 +13,7 @@ LIB_PATH = os.path.join(_HERE, LIB_NAME)
 
 G2V_OK = 0
 # the ABI that SIGNATURES describes (g2v_abi_version() of a matching build)
-ABI_VERSION = 9
+ABI_VERSION = 10
 G2V_DTYPE_F32 = 0
 G2V_DTYPE_BF16 = 1
 _ERRORS = {1: "invalid argument", 2: "HIP runtime error", 3: "size limit exceeded"}
@@ -42,11 +42,15 @@ SIGNATURES = {
     "g2v_backward_prepare": (_i, [_i, _i, _f3, _f3, _vp, _vp, _vp, _i, _ll, _ll, _vp, _vp, _vp, _vp, _sz, _vp]),
     "g2v_backward_prepared": (_i, [_i, _i, _vp, _vp, _vp, _vp, _vp, _f3, _f3, _vp, _vp, _vp, _vp, _vp, _ll, _ll,
                                    _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "g2v_backward_cosine": (_i, [_i, _i, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _f3, _f3, _vp, _vp, _vp, _vp, _vp,
+                                 _ll, _ll, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
+                                 _i, _vp]),
     "g2v_t2g_workspace": (_sz, [_i, _ll, _f3, _f3]),
     "g2v_build_t2g": (_i, [_i, _f3, _f3, _vp, _vp, _vp, _vp, _ll, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                            _vp, _sz, _vp]),
     "g2v_cosine_loss_workspace": (_sz, [_ll, _i]),
     "g2v_cosine_loss_forward": (_i, [_ll, _i, _vp, _vp, _vp, _vp, _i, _vp, _vp, _ip, _vp, _sz, _vp]),
+    "g2v_cosine_loss_forward_coef": (_i, [_ll, _i, _vp, _vp, _vp, _vp, _i, _vp, _vp, _ip, _vp, _vp, _sz, _vp]),
     "g2v_cosine_loss_forward_noalloc": (_i, [_ll, _i, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp]),
     "g2v_cosine_loss_backward": (_i, [_ll, _i, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp]),
     "g2v_covariance_from_scale_rotation": (_i, [_i, _vp, _vp, _vp, _vp]),

@@ -224,22 +224,33 @@ __device__ __forceinline__ void dma4_nt(const void* gptr, uint32_t lds) {
                  :: "v"(gptr), "s"(lds) : "memory", "m0");
 }
 
+// FU: the upstream feature gradient is the cosine loss's, G = k1 target + k2 grid_feats per voxel,
+// formed on chip from two raw chunks (target and grid_feats) per stage; the F rows then use two
+// buffers (loaded one chunk ahead) so that the second raw chunk fits.
+template <bool FU>
 struct BtSmem {
+    static constexpr int kFStages = FU ? 2 : kBtStages;   // F chunk buffers
+    static constexpr int kSrc = FU ? 2 : 1;               // raw G sources per stage
     union {
         // F chunk rows of the pass's Gaussians; the 16-byte piece q of row r sits at slot
         // q ^ swz(r), so that the lanes of one LDS cycle (8 or 16 consecutive rows) hit distinct
         // 16-byte bank groups
-        unsigned char frow[kBtStages][kBtPass * kBtRowBytes];
+        unsigned char frow[kFStages][kBtPass * kBtRowBytes];
         float xch[2][kBtPass][kNumGrads];   // epilogue exchange, used after the K loop has drained
     } u;
-    float graw[kBtStages][64][kBtKc];   // G chunks as loaded (fp32, voxel-major, pieces at q ^ swz(v))
+    // G chunks as loaded (fp32, voxel-major, pieces at q ^ swz(v)); FU: [0] target, [1] grid_feats
+    float graw[kBtStages][kSrc][64][kBtKc];
     bf16x8 ahi[2][2][2][64];   // A operand (G chunk), hi: [buffer][k half][voxel block][lane]
     bf16x8 alo[2][2][2][64];
     int vlin[64];
     float gD[64], inv[64], tv[64], D[64];
+    float kc[2][FU ? 64 : 1];  // FU: the voxel's k1, k2 (scaled by the loss's upstream gradient)
     ParamTile<kBtPass> pt;     // parameters of this pass's list entries
     float tpart[kBtGroups][64];
 };
+static_assert(sizeof(float) * 2 * kBtNbw * 16 * 64 * kBtGroups <= BtSmem<true>::kFStages * kBtPass * kBtRowBytes,
+              "the k-half exchange fits in the F buffers");
+
 
 // s_waitcnt immediate that waits for vmcnt <= n and leaves the other counters alone.
 __device__ constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
@@ -319,7 +330,8 @@ __device__ __forceinline__ float lane_e(const LaneExp& E, const LaneGeom& L, int
 // values themselves, 128 bytes per chunk row, as k_split_chunks<__bf16> writes them; the grad_feats
 // chunk rows are 128 bytes of bfloat16), and each k half of 32 channels is two 16-channel slices:
 // the A and B "hi" operands carry slice 0 and the "lo" operands slice 1, with one MFMA each.
-template <bool VEC, bool BF>
+// FU (with VEC, float32): the upstream feature gradient is the cosine loss's (cg), gF_ is unused.
+template <bool VEC, bool BF, bool FU>
 __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
     Grid G, int n, int C, int nchk, const float* __restrict__ gD, const void* __restrict__ gF_,
     const float* __restrict__ means, const float* __restrict__ opacity,
@@ -327,8 +339,9 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
     const int* __restrict__ g2t_offsets, const int* __restrict__ toff,
     const int* __restrict__ sorted_gauss, int M, const float* __restrict__ density,
     const void* __restrict__ grid_feats, int gdt, const __bf16* __restrict__ fsp,
-    float* __restrict__ pair_partials, __bf16* __restrict__ wt) {
-    __shared__ BtSmem sm;
+    float* __restrict__ pair_partials, __bf16* __restrict__ wt, CosG cg) {
+    static_assert(!FU || (VEC && !BF), "the fused cosine gradient takes 16-byte float32 rows");
+    __shared__ BtSmem<FU> sm;
     const int T = G.tiles[0] * G.tiles[1] * G.tiles[2];
     const int tile = uniform(xcd_remap(blockIdx.x, gridDim.x));
     if (tile >= T) return;
@@ -350,6 +363,11 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
         sm.D[threadIdx.x] = ok ? density[v] : 0.0f;
         sm.inv[threadIdx.x] = ok ? 1.0f / fmaxf(density[v], kEps) : 0.0f;
         sm.tv[threadIdx.x] = 0.0f;
+        if constexpr (FU) {
+            const float scale = cg.grad_loss[0] * cg.inv_count;   // as the loss's own backward forms it
+            sm.kc[0][threadIdx.x] = ok ? cg.coef[2 * v] * scale : 0.0f;
+            sm.kc[1][threadIdx.x] = ok ? cg.coef[2 * v + 1] * scale : 0.0f;
+        }
     }
     __syncthreads();
 
@@ -365,7 +383,16 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             if (v < 0) continue;
             const GT* a = gF + (int64_t)v * C;
             float s = 0.0f;
-            if (gdt == kDtBF16) {
+            if constexpr (FU) {
+                // G = k1 target + k2 grid_feats, as the loss's backward rounds it to float
+                const float k1 = sm.kc[0][r], k2 = sm.kc[1][r];
+                const float* tg = cg.tgt + (int64_t)v * C;
+                const float* b = static_cast<const float*>(grid_feats) + (int64_t)v * C;
+                for (int c = lane; c < C; c += 64) {
+                    const float gv = k1 * tg[c] + k2 * b[c];
+                    s += gv * b[c];
+                }
+            } else if (gdt == kDtBF16) {
                 const __bf16* b = static_cast<const __bf16*>(grid_feats) + (int64_t)v * C;
                 for (int c = lane; c < C; c += 64) s += (float)a[c] * (float)b[c];
             } else {
@@ -385,30 +412,41 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
     // BF: a chunk row is 128 bytes of bfloat16; with VEC (C % 8 == 0, 16-byte aligned rows) lane l
     // loads 16-byte piece l % 8 of row l / 8 of the wave's 8 rows (stage rows of 128 bytes, pieces
     // in order, read whole by write_a); without VEC write_a loads the A operand itself.
-    constexpr int kNG = BF ? (VEC ? 1 : 0) : (VEC ? 1 : 4);   // G loads per wave per chunk
+    // FU: the target and grid_feats chunks of the same rows, into sources 0 and 1 of the stage.
+    constexpr int kNG = BF ? (VEC ? 1 : 0) : (VEC ? 1 : 4);   // G loads per wave per chunk and source
     constexpr int kNGs = kNG > 0 ? kNG : 1;
-    const GT* gsrc[kNGs];
+    constexpr int kSrc = FU ? 2 : 1;
+    const GT* gsrc[kSrc][kNGs];
     int gcoff[kNGs];   // channel of this lane's load within a chunk
 #pragma unroll
     for (int k = 0; k < kNG; ++k) {
         const int v = (BF || VEC) ? wave * 8 + (lane >> 3) : wave * 8 + 2 * k + (lane >> 5);
-        gsrc[k] = gF + (int64_t)max(sm.vlin[v], 0) * C;
+        const int64_t row = (int64_t)max(sm.vlin[v], 0) * C;
+        if constexpr (FU) {
+            gsrc[0][k] = reinterpret_cast<const GT*>(cg.tgt) + row;
+            gsrc[kSrc - 1][k] = static_cast<const GT*>(grid_feats) + row;
+        } else {
+            gsrc[0][k] = gF + row;
+        }
         gcoff[k] = BF ? 8 * (lane & 7)
                       : (VEC ? 4 * ((lane & 7) ^ swz(v)) : 4 * (((lane & 31) >> 2) ^ swz(v)) + (lane & 3));
     }
     auto dma_g = [&](int chunk, int stage) {
 #pragma unroll
-        for (int k = 0; k < kNG; ++k) {
-            if constexpr (BF) {
-                dma16_nt(gsrc[k] + min(chunk * kKc + gcoff[k], C - 8),
-                         uniform(lds_addr(reinterpret_cast<char*>(&sm.graw[stage][0][0]) + wave * 8 * 128)));
-            } else if (VEC) {
-                dma16_nt(gsrc[k] + min(chunk * kBtKc + gcoff[k], C - 4), uniform(lds_addr(&sm.graw[stage][wave * 8][0])));
-            } else {
-                dma4_nt(gsrc[k] + min(chunk * kBtKc + gcoff[k], C - 1),
-                     uniform(lds_addr(&sm.graw[stage][wave * 8 + 2 * k][0])));
+        for (int sr = 0; sr < kSrc; ++sr)
+#pragma unroll
+            for (int k = 0; k < kNG; ++k) {
+                if constexpr (BF) {
+                    dma16_nt(gsrc[sr][k] + min(chunk * kKc + gcoff[k], C - 8),
+                             uniform(lds_addr(reinterpret_cast<char*>(&sm.graw[stage][sr][0][0]) + wave * 8 * 128)));
+                } else if (VEC) {
+                    dma16_nt(gsrc[sr][k] + min(chunk * kBtKc + gcoff[k], C - 4),
+                             uniform(lds_addr(&sm.graw[stage][sr][wave * 8][0])));
+                } else {
+                    dma4_nt(gsrc[sr][k] + min(chunk * kBtKc + gcoff[k], C - 1),
+                            uniform(lds_addr(&sm.graw[stage][sr][wave * 8 + 2 * k][0])));
+                }
             }
-        }
     };
 
     const uint32_t fstride = (uint32_t)nchk * kBtRowBytes;   // bytes of one Gaussian's split row
@@ -486,7 +524,7 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
                 const int lim8 = svok ? min(max(C - (ch * kKc + 8 * sq), 0), 8) : 0;
                 uint4 xr;
                 if constexpr (VEC) {
-                    xr = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(&sm.graw[gs][0][0]) +
+                    xr = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(&sm.graw[gs][0][0][0]) +
                                                          sv * 128 + sq * 16);
                 } else {
                     const unsigned short* row =
@@ -510,7 +548,16 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             }
             // one 16-byte LDS read, then the values past the row or the grid are cleared with bit
             // masks (a select per value would let the compiler split the read into guarded parts)
-            const uint4 xr = *reinterpret_cast<const uint4*>(&sm.graw[gs][sv][4 * (sq ^ swz(sv))]);
+            uint4 xr = *reinterpret_cast<const uint4*>(&sm.graw[gs][0][sv][4 * (sq ^ swz(sv))]);
+            if constexpr (FU) {
+                // G = k1 target + k2 grid_feats (the expression of the loss's own backward)
+                const uint4 xf = *reinterpret_cast<const uint4*>(&sm.graw[gs][kSrc - 1][sv][4 * (sq ^ swz(sv))]);
+                const float k1 = sm.kc[0][sv], k2 = sm.kc[1][sv];
+                xr.x = __float_as_uint(k1 * __uint_as_float(xr.x) + k2 * __uint_as_float(xf.x));
+                xr.y = __float_as_uint(k1 * __uint_as_float(xr.y) + k2 * __uint_as_float(xf.y));
+                xr.z = __float_as_uint(k1 * __uint_as_float(xr.z) + k2 * __uint_as_float(xf.z));
+                xr.w = __float_as_uint(k1 * __uint_as_float(xr.w) + k2 * __uint_as_float(xf.w));
+            }
             const f32x2 x01 = {__uint_as_float(xr.x & (0u - (unsigned)(0 < lim))),
                                __uint_as_float(xr.y & (0u - (unsigned)(1 < lim)))};
             const f32x2 x23 = {__uint_as_float(xr.z & (0u - (unsigned)(2 < lim))),
@@ -599,13 +646,46 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
                 lds_barrier();
             }
         };
+        // FU: two F buffers, so F(ch+1) is loaded at the start of step ch into the buffer that step
+        // ch-1 read, and waited for at its end; G (two sources) is still three chunks ahead.
+        auto chunk_loop_fu = [&](auto nfc) {
+            constexpr int NF = decltype(nfc)::value;
+            constexpr int kLg = kSrc * kNG;   // G loads per wave per chunk
+            dma_g(0, 0);
+            dma_f(0, 0, 0, NF);
+            dma_g(min(1, clast), 1);
+            dma_g(min(2, clast), 2);
+            wait_vm<kLg>();               // G(0), F(0), G(1) complete
+            lds_barrier();
+            write_a(0, 0, 0);
+            lds_barrier();
+            for (int ch = 0; ch < nchk; ++ch) {
+                const int st = ch % kBtStages, fb = ch & 1, ab = ch & 1;
+                dma_f(min(ch + 1, clast), fb ^ 1, 0, NF);
+                StepOps ops;
+                load_ops(fb, ab, ops);
+                mult(0, ops);
+                __builtin_amdgcn_sched_barrier(0);
+                write_a(ch + 1, (ch + 1) % kBtStages, ab ^ 1);
+                __builtin_amdgcn_sched_barrier(0);
+                mult(1, ops);
+                __builtin_amdgcn_sched_barrier(0);
+                dma_g(min(ch + 3, clast), st);
+                wait_vm<kLg>();           // F(ch+1) and G(ch+2) complete
+                lds_barrier();
+            }
+        };
         static_assert(kBtDma == 4, "group-count dispatch");
+        auto run = [&](auto nfc) {
+            if constexpr (FU) chunk_loop_fu(nfc);
+            else chunk_loop(nfc);
+        };
         switch (nf) {
-            case 4: chunk_loop(std::integral_constant<int, 4>{}); break;
-            case 3: chunk_loop(std::integral_constant<int, 3>{}); break;
-            case 2: chunk_loop(std::integral_constant<int, 2>{}); break;
-            case 1: chunk_loop(std::integral_constant<int, 1>{}); break;
-            default: chunk_loop(std::integral_constant<int, 0>{}); break;
+            case 4: run(std::integral_constant<int, 4>{}); break;
+            case 3: run(std::integral_constant<int, 3>{}); break;
+            case 2: run(std::integral_constant<int, 2>{}); break;
+            case 1: run(std::integral_constant<int, 1>{}); break;
+            default: run(std::integral_constant<int, 0>{}); break;
         }
         // drain the surplus loads of the last steps before the F buffers are reused
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
@@ -874,6 +954,9 @@ constexpr int kBrRbMax = 3;       // 16-row blocks per wave and pass
 constexpr int kBrPass = kBrWaves * kBrRbMax * 16;   // region rows per pass
 static_assert(kBrPass * kBrSlots % kBrThreads == 0 && kBrPass <= 2 * kBrThreads, "row-table staging shape");
 
+// FU: the upstream feature gradient is the cosine loss's (k1 target + k2 grid_feats per voxel);
+// kc holds (k1, k2) of the voxels of the region's tiles, in the order of tl_t.
+template <bool FU>
 struct BrSmem {
     bf16x8 bhi[2][2][kBrCb][64];   // B operand (gF chunk): [buffer][k step of 32 voxels][channel block][lane]
     bf16x8 blo[2][2][kBrCb][64];
@@ -881,6 +964,7 @@ struct BrSmem {
     int rslot[kBrPass];                   // G->R slot of each row of the pass
     int tl_t[kBrSlots], tl_s[kBrSlots];   // tiles of the region (inside the grid) and their slots
     int ntl;
+    float2 kc[FU ? kBrSlots : 1][FU ? 64 : 1];
 };
 
 // gF chunk of one tile for the staging thread: channel sc of the chunk, voxel octets so and
@@ -1009,10 +1093,11 @@ __device__ __forceinline__ unsigned br_load_tile2(const Grid& G, int C, int c0, 
 // loaded as soon as the MFMAs of k step s of tile k are issued.  LDS hand-offs use lds_barrier,
 // so loads stay in flight across the barrier and the compiler waits for each where its registers
 // are used.
-template <int NB, bool GB, bool P2>
-__device__ __forceinline__ void br_tiles(BrSmem& sm, const Grid& G, int C, int c0, int ntl, int prow,
-                                         const void* __restrict__ gF, const __bf16* __restrict__ wt,
-                                         float* __restrict__ gpart) {
+// FU: gF is the target and gF2 grid_feats; a staged value is k1 target + k2 grid_feats.
+template <int NB, bool GB, bool P2, bool FU>
+__device__ __forceinline__ void br_tiles(BrSmem<FU>& sm, const Grid& G, int C, int c0, int ntl, int prow,
+                                         const void* __restrict__ gF, const void* __restrict__ gF2,
+                                         const __bf16* __restrict__ wt, float* __restrict__ gpart) {
     constexpr int NR = NB > 0 ? NB : 1;   // register arrays (unused when NB == 0)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     // staging: channel sc, octets so and so + 4; or (P2) channels 2 cp and 2 cp + 1, octet ot
@@ -1021,13 +1106,26 @@ __device__ __forceinline__ void br_tiles(BrSmem& sm, const Grid& G, int C, int c
     const int q = lane >> 4, cl = lane & 15;
 
     float pre[2][8];
+    float pre2[FU ? 2 : 1][FU ? 8 : 1];   // FU: grid_feats values of the same voxels and channels
     unsigned pmask = 0;
-    auto stage = [&](int buf) {
+    // tpos: the tile's position in tl_t (FU: its row of kc)
+    auto stage = [&](int buf, int tpos) {
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
             float u[8];
+            if constexpr (FU) {
+                // tile-local voxel of value i: 8 ot + i (P2) or 32 k + 8 so + i
+                const float2* kr = &sm.kc[tpos][P2 ? 8 * ot : 32 * k + 8 * so];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) u[i] = (pmask >> (i + 8 * k)) & 1u ? pre[k][i] : 0.0f;
+                for (int i = 0; i < 8; ++i) {
+                    const float2 kk = kr[i];
+                    const float gv = kk.x * pre[k][i] + kk.y * pre2[k][i];
+                    u[i] = (pmask >> (i + 8 * k)) & 1u ? gv : 0.0f;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) u[i] = (pmask >> (i + 8 * k)) & 1u ? pre[k][i] : 0.0f;
+            }
             bf16x8 hh, ll;
             split8(u, hh, ll);
             // P2: channel cp2 + k of octet ot (k step ot / 4, lane group ot % 4); else voxel octet
@@ -1086,11 +1184,15 @@ __device__ __forceinline__ void br_tiles(BrSmem& sm, const Grid& G, int C, int c
     // prologue: tile 0 staged, gF of tile 1 and the weights of tile 0 in flight (in the order
     // the loop issues them, so that the compiler's waits at the loop head stay exact)
     auto load_tile = [&](int t) {
+        if constexpr (FU) {   // same voxels and channels, so the same mask
+            if constexpr (P2) br_load_tile2<GB>(G, C, c0, t, cp2, ot, gF2, pre2);
+            else br_load_tile<GB>(G, C, c0, t, sc, so, gF2, pre2);
+        }
         if constexpr (P2) return br_load_tile2<GB>(G, C, c0, t, cp2, ot, gF, pre);
         else return br_load_tile<GB>(G, C, c0, t, sc, so, gF, pre);
     };
     pmask = load_tile(uniform(sm.tl_t[0]));
-    stage(0);
+    stage(0, 0);
     pmask = load_tile(uniform(sm.tl_t[min(1, klast)]));
     rows_of(0);
     load_w(0);
@@ -1098,7 +1200,7 @@ __device__ __forceinline__ void br_tiles(BrSmem& sm, const Grid& G, int C, int c
     lds_barrier();
     for (int k = 0; k < ntl; ++k) {
         const int kn = min(k + 1, klast);
-        stage((k + 1) & 1);
+        stage((k + 1) & 1, kn);
         pmask = load_tile(uniform(sm.tl_t[min(k + 2, klast)]));
         rows_of(kn);
         __builtin_amdgcn_sched_barrier(0);
@@ -1127,11 +1229,12 @@ __device__ __forceinline__ void br_tiles(BrSmem& sm, const Grid& G, int C, int c
 
 // One pass of phase B over rows rp .. rp + prow - 1 of the region (prow <= 384): stages the
 // pass's row table and G->R slots, then runs the tile loop with this wave's block count.
-template <bool GB, bool P2>
-__device__ __forceinline__ void br_pass(BrSmem& sm, const Grid& G, int C, int c0, int ntl, int rp,
+template <bool GB, bool P2, bool FU>
+__device__ __forceinline__ void br_pass(BrSmem<FU>& sm, const Grid& G, int C, int c0, int ntl, int rp,
                                         int KR, int M, int MR, int jr0, const void* __restrict__ gF,
-                                        const int* __restrict__ r_pairs, const int* __restrict__ table,
-                                        const __bf16* __restrict__ wt, float* __restrict__ gpart) {
+                                        const void* __restrict__ gF2, const int* __restrict__ r_pairs,
+                                        const int* __restrict__ table, const __bf16* __restrict__ wt,
+                                        float* __restrict__ gpart) {
     const int wave = threadIdx.x >> 6;
     const int prow = min(KR - rp, kBrPass);
     const int nblk = (prow + 15) >> 4;
@@ -1168,20 +1271,23 @@ __device__ __forceinline__ void br_pass(BrSmem& sm, const Grid& G, int C, int c0
     }
     __syncthreads();
     static_assert(kBrRbMax == 3, "block-count dispatch");
-    if (nb >= 3) br_tiles<3, GB, P2>(sm, G, C, c0, ntl, prow, gF, wt, gpart);
-    else if (nb == 2) br_tiles<2, GB, P2>(sm, G, C, c0, ntl, prow, gF, wt, gpart);
-    else if (nb == 1) br_tiles<1, GB, P2>(sm, G, C, c0, ntl, prow, gF, wt, gpart);
-    else br_tiles<0, GB, P2>(sm, G, C, c0, ntl, prow, gF, wt, gpart);
+    if (nb >= 3) br_tiles<3, GB, P2, FU>(sm, G, C, c0, ntl, prow, gF, gF2, wt, gpart);
+    else if (nb == 2) br_tiles<2, GB, P2, FU>(sm, G, C, c0, ntl, prow, gF, gF2, wt, gpart);
+    else if (nb == 1) br_tiles<1, GB, P2, FU>(sm, G, C, c0, ntl, prow, gF, gF2, wt, gpart);
+    else br_tiles<0, GB, P2, FU>(sm, G, C, c0, ntl, prow, gF, gF2, wt, gpart);
 }
 
 // P2: even C with rows aligned to two channels, so the gF staging loads take two channels at once.
-template <bool GB, bool P2>
+// FU (float32): the upstream feature gradient is the cosine loss's (cg; gF unused), formed per
+// value from the target and grid_feats.
+template <bool GB, bool P2, bool FU>
 __global__ void __launch_bounds__(kBrThreads, 1) k_bwd_region(
     Grid G, Regions RG, int C, int nchunk, const void* __restrict__ gF,
     const int* __restrict__ toff, int M, const int* __restrict__ roff,
     const int* __restrict__ r_pairs, const int* __restrict__ table, int MR,
-    const __bf16* __restrict__ wt, float* __restrict__ gpart) {
-    __shared__ BrSmem sm;
+    const __bf16* __restrict__ wt, float* __restrict__ gpart, const void* __restrict__ grid_feats, CosG cg) {
+    static_assert(!FU || !GB, "the fused cosine gradient takes float32 rows");
+    __shared__ BrSmem<FU> sm;
     const int idx = xcd_remap(blockIdx.x, gridDim.x);
     const int R = uniform(idx / nchunk);
     const int chunk = uniform(idx - R * nchunk);
@@ -1212,9 +1318,25 @@ __global__ void __launch_bounds__(kBrThreads, 1) k_bwd_region(
     __syncthreads();
     const int ntl = uniform(sm.ntl);
     if (ntl == 0) return;   // every row stays zero: phase C reads no partial row of this region
+    if constexpr (FU) {
+        // (k1, k2) of every voxel of the region's tiles (0 outside the grid; those values are
+        // masked anyway); the first pass's barrier orders these stores before their reads
+        const float scale = cg.grad_loss[0] * cg.inv_count;   // as the loss's own backward forms it
+        for (int e = threadIdx.x; e < ntl * 64; e += kBrThreads) {
+            int x, y, z;
+            tile_voxel(G, sm.tl_t[e >> 6], e & 63, x, y, z);
+            float2 kk = make_float2(0.0f, 0.0f);
+            if (in_grid(G, x, y, z)) {
+                const float2 c = *reinterpret_cast<const float2*>(cg.coef + 2 * voxel_index(G, x, y, z));
+                kk = make_float2(c.x * scale, c.y * scale);
+            }
+            sm.kc[e >> 6][e & 63] = kk;
+        }
+        gF = cg.tgt;
+    }
 
     for (int rp = 0; rp < KR; rp += kBrPass)
-        br_pass<GB, P2>(sm, G, C, c0, ntl, rp, KR, M, MR, jr0, gF, r_pairs, table, wt, gpart);
+        br_pass<GB, P2, FU>(sm, G, C, c0, ntl, rp, KR, M, MR, jr0, gF, grid_feats, r_pairs, table, wt, gpart);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1457,8 +1579,13 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
                                  const void* grid_feats, const void* features, int fdt,
                                  const void* plan_ws, int64_t MR, float* grad_means, float* grad_cov,
                                  float* grad_opacity, void* grad_features, void* ws, bool prepared,
-                                 hipStream_t s) {
+                                 hipStream_t s, const CosG* cos) {
     if (n <= 0) return hipSuccess;
+    // the fused cosine gradient: float32 rows of 16-byte multiples, 16-byte aligned
+    if (cos && (fdt != kDtF32 || (C & 3) != 0 || ((uintptr_t)cos->tgt & 15) != 0 || ((uintptr_t)grid_feats & 15) != 0 ||
+                !cos->tgt || !cos->coef || !cos->grad_loss))
+        return hipErrorInvalidValue;
+    const CosG cg = cos ? *cos : CosG{nullptr, nullptr, nullptr, 0.0f};
     const Regions RG = make_regions(G);
     const int T = G.tiles[0] * G.tiles[1] * G.tiles[2];
     const int nchk = feature_chunks(C, fdt);
@@ -1474,16 +1601,18 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
         const int blocks = (int)ceil_div(T, 8) * 8;
         // 16-byte G loads: 4 float or 8 bfloat16 channels per load, rows 16-byte aligned
         const bool vec = (C & (fdt == kDtBF16 ? 7 : 3)) == 0 && ((uintptr_t)grad_feats & 15) == 0;
-#define G2V_BT(V, F)                                                                                          \
-    G2V_LAUNCH((k_bwd_tile<V, F>), dim3(blocks), dim3(kBtThreads), 0, s, G, n, C, nchk, grad_density,              \
+#define G2V_BT(V, F, FU)                                                                                      \
+    G2V_LAUNCH((k_bwd_tile<V, F, FU>), dim3(blocks), dim3(kBtThreads), 0, s, G, n, C, nchk, grad_density,          \
                grad_feats, means, opacity, cov_inv, lb, ub, g2t_offsets, tile_offsets, sorted_gauss, (int)M, density,        \
-               grid_feats, fdt, (const __bf16*)b.fsp, b.partials, b.wt)
-        if (fdt == kDtBF16) {
-            if (vec) G2V_BT(true, true);
-            else G2V_BT(false, true);
+               grid_feats, fdt, (const __bf16*)b.fsp, b.partials, b.wt, cg)
+        if (cos) {
+            G2V_BT(true, false, true);
+        } else if (fdt == kDtBF16) {
+            if (vec) G2V_BT(true, true, false);
+            else G2V_BT(false, true, false);
         } else {
-            if (vec) G2V_BT(true, false);
-            else G2V_BT(false, false);
+            if (vec) G2V_BT(true, false, false);
+            else G2V_BT(false, false, false);
         }
 #undef G2V_BT
     }
@@ -1493,16 +1622,18 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
         const int blocks = (int)ceil_div(items, 8) * 8;
         // two-channel staging loads: even C and a grad_feats base aligned to two elements
         const bool pair = (C & 1) == 0 && ((uintptr_t)grad_feats & (fdt == kDtBF16 ? 3 : 7)) == 0;
-#define G2V_BR(GBV, P2V)                                                                                      \
-    G2V_LAUNCH((k_bwd_region<GBV, P2V>), dim3(blocks), dim3(kBrThreads), 0, s, G, RG, C, nchunk, grad_feats,       \
+#define G2V_BR(GBV, P2V, FU)                                                                                  \
+    G2V_LAUNCH((k_bwd_region<GBV, P2V, FU>), dim3(blocks), dim3(kBrThreads), 0, s, G, RG, C, nchunk, grad_feats,   \
                tile_offsets, (int)M, (const int*)b.roff, (const int*)b.r_pairs_sorted, (const int*)b.table, (int)MR, \
-               (const __bf16*)b.wt, b.gpart)
-        if (fdt == kDtBF16) {
-            if (pair) G2V_BR(true, true);
-            else G2V_BR(true, false);
+               (const __bf16*)b.wt, b.gpart, grid_feats, cg)
+        if (cos) {   // C % 4 == 0 and 16-byte aligned rows: the paired loads apply
+            G2V_BR(false, true, true);
+        } else if (fdt == kDtBF16) {
+            if (pair) G2V_BR(true, true, false);
+            else G2V_BR(true, false, false);
         } else {
-            if (pair) G2V_BR(false, true);
-            else G2V_BR(false, false);
+            if (pair) G2V_BR(false, true, false);
+            else G2V_BR(false, false, false);
         }
 #undef G2V_BR
     }

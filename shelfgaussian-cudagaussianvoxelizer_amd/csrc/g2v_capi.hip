@@ -123,7 +123,7 @@ extern "C" {
 
 const char* g2v_last_error(void) { return g_err; }
 
-int g2v_abi_version(void) { return 9; }
+int g2v_abi_version(void) { return 10; }
 
 int g2v_grid_dims(const float voxel_size[3], const float voxel_range[6], int dims[3], int tiles[3]) {
     Grid G;
@@ -361,7 +361,7 @@ int backward_impl(int n, int feat_dim, const float* grad_density, const void* gr
                   const void* features, int feat_dtype, float* grad_means, float* grad_cov, float* grad_opacity,
                   void* grad_features, const int* t2g_tiles, const int* t2g_gauss,
                   const int* t2g_offsets, const void* plan_workspace, void* workspace,
-                  size_t workspace_bytes, bool prepared, void* stream) {
+                  size_t workspace_bytes, bool prepared, void* stream, const CosG* cos = nullptr) {
     g_err[0] = 0;
     if (feat_dtype != G2V_DTYPE_F32 && feat_dtype != G2V_DTYPE_BF16)
         return fail(G2V_ERR_INVALID, "feat_dtype = %d (G2V_DTYPE_F32 or G2V_DTYPE_BF16)", feat_dtype);
@@ -375,7 +375,7 @@ int backward_impl(int n, int feat_dim, const float* grad_density, const void* gr
     if (!grad_density || !means3D || !opacity || !cov_inv || !valid_voxel_lb || !valid_voxel_ub ||
         !grad_means || !grad_cov || !grad_opacity)
         return fail(G2V_ERR_INVALID, "null input/output pointer");
-    if (feat_dim > 0 && (!grad_feats || !grid_feats || !features || !grad_features || !density ||
+    if (feat_dim > 0 && ((!grad_feats && !cos) || !grid_feats || !features || !grad_features || !density ||
                          !g2t_offsets || !plan_workspace || (num_pairs > 0 && !g2t_tile_ids)))
         return fail(G2V_ERR_INVALID, "feat_dim = %d needs the feature tensors, density, the CSR and the plan workspace", feat_dim);
     if (feat_dim > 0 && !split_rows_fit(n, feat_dim))
@@ -413,7 +413,7 @@ int backward_impl(int n, int feat_dim, const float* grad_density, const void* gr
                                   valid_voxel_lb, valid_voxel_ub, g2t_offsets, num_pairs,
                                   b.tile_offsets, b.sorted_tiles, b.sorted_gauss, density, grid_feats, features,
                                   feat_dtype, plan_workspace, num_region_pairs, grad_means, grad_cov, grad_opacity,
-                                  grad_features, feats_ws, prepared, s));
+                                  grad_features, feats_ws, prepared, s, cos));
     return G2V_OK;
 }
 
@@ -471,6 +471,37 @@ int g2v_backward_prepare(int n, int feat_dim, const float voxel_size[3], const f
                                     t2g_tiles, t2g_gauss, plan_workspace, num_region_pairs, feats_ws,
                                     static_cast<hipStream_t>(stream)));
     return G2V_OK;
+}
+
+int g2v_backward_cosine(int n, int feat_dim, const float* grad_density, const float* grad_loss,
+                        const void* pseudo_gt, const float* coef, int num_valid_voxel, const float* means3D,
+                        const float* opacity, const float* cov_inv, const float voxel_size[3],
+                        const float voxel_range[6], const int* valid_voxel_lb, const int* valid_voxel_ub,
+                        const int* num_voxels_per_gaussian, const int* g2t_offsets, const int* g2t_tile_ids,
+                        long long num_pairs, long long num_region_pairs, const float* density,
+                        const void* grid_feats, const void* features, int feat_dtype, float* grad_means,
+                        float* grad_cov, float* grad_opacity, void* grad_features, const int* t2g_tiles,
+                        const int* t2g_gauss, const int* t2g_offsets, const void* plan_workspace, void* workspace,
+                        size_t workspace_bytes, int prepared, void* stream) {
+    g_err[0] = 0;
+    if (feat_dtype != G2V_DTYPE_F32)
+        return fail(G2V_ERR_INVALID, "feat_dtype = %d: the fused cosine gradient takes float32 features", feat_dtype);
+    if (feat_dim <= 0 || (feat_dim & 3) != 0)
+        return fail(G2V_ERR_INVALID, "feat_dim = %d: the fused cosine gradient needs feat_dim %% 4 == 0", feat_dim);
+    if (n > 0 && (!grad_loss || !pseudo_gt || !coef))
+        return fail(G2V_ERR_INVALID, "grad_loss, pseudo_gt and coef are required");
+    if (((uintptr_t)pseudo_gt & 15) != 0 || ((uintptr_t)grid_feats & 15) != 0 || ((uintptr_t)coef & 7) != 0)
+        return fail(G2V_ERR_INVALID, "pseudo_gt and grid_feats must be 16-byte aligned, coef 8-byte aligned");
+    if (prepared && n > 0 && num_pairs > 0 && !(t2g_tiles && t2g_gauss && t2g_offsets))
+        return fail(G2V_ERR_INVALID, "a prepared backward needs the forward's Tile->Gaussian CSR");
+    // the scale of the loss's own backward (reference src/cuda_feats_loss.cu:319)
+    const CosG cos{static_cast<const float*>(pseudo_gt), coef, grad_loss,
+                   num_valid_voxel > 0 ? 1.0f / (float)num_valid_voxel : 0.0f};
+    return backward_impl(n, feat_dim, grad_density, nullptr, means3D, opacity, cov_inv, voxel_size, voxel_range,
+                         valid_voxel_lb, valid_voxel_ub, num_voxels_per_gaussian, g2t_offsets, g2t_tile_ids,
+                         num_pairs, num_region_pairs, density, grid_feats, features, feat_dtype, grad_means, grad_cov,
+                         grad_opacity, grad_features, t2g_tiles, t2g_gauss, t2g_offsets, plan_workspace, workspace,
+                         workspace_bytes, prepared != 0, stream, &cos);
 }
 
 int g2v_backward_prepared(int n, int feat_dim, const float* grad_density, const void* grad_feats,
@@ -549,11 +580,11 @@ size_t g2v_cosine_loss_workspace(long long num_voxels, int feat_dim) {
     return cosine_workspace(num_voxels > 0 ? num_voxels : 0);
 }
 
-int g2v_cosine_loss_forward(long long num_voxels, int feat_dim, const float* voxel_label,
-                            const unsigned char* occ_mask, const void* grid_feats, const void* pseudo_gt,
-                            int feat_dtype, float* loss, int* num_valid, int* num_valid_host, void* workspace,
-                            size_t workspace_bytes, void* stream) {
-    g_err[0] = 0;
+// The loss forward; coef (optional) receives the per-voxel gradient coefficients.
+static int cosine_forward_impl(long long num_voxels, int feat_dim, const float* voxel_label,
+                               const unsigned char* occ_mask, const void* grid_feats, const void* pseudo_gt,
+                               int feat_dtype, float* loss, int* num_valid, int* num_valid_host, float* coef,
+                               void* workspace, size_t workspace_bytes, void* stream) {
     if (feat_dtype != G2V_DTYPE_F32 && feat_dtype != G2V_DTYPE_BF16)
         return fail(G2V_ERR_INVALID, "feat_dtype = %d (G2V_DTYPE_F32 or G2V_DTYPE_BF16)", feat_dtype);
     if (num_voxels < 0 || feat_dim < 0)
@@ -567,7 +598,7 @@ int g2v_cosine_loss_forward(long long num_voxels, int feat_dim, const float* vox
     if (rc != G2V_OK) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
     G2V_HIP(launch_cosine_forward(num_voxels, feat_dim, voxel_label, occ_mask, grid_feats, pseudo_gt, feat_dtype,
-                                  loss, num_valid, workspace, s));
+                                  loss, num_valid, workspace, s, coef));
     if (num_valid_host) {
         int h = 0;
         G2V_HIP(hipMemcpyAsync(&h, num_valid, sizeof(int), hipMemcpyDeviceToHost, s));
@@ -575,6 +606,26 @@ int g2v_cosine_loss_forward(long long num_voxels, int feat_dim, const float* vox
         *num_valid_host = h;
     }
     return G2V_OK;
+}
+
+int g2v_cosine_loss_forward(long long num_voxels, int feat_dim, const float* voxel_label,
+                            const unsigned char* occ_mask, const void* grid_feats, const void* pseudo_gt,
+                            int feat_dtype, float* loss, int* num_valid, int* num_valid_host, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+    g_err[0] = 0;
+    return cosine_forward_impl(num_voxels, feat_dim, voxel_label, occ_mask, grid_feats, pseudo_gt, feat_dtype, loss,
+                               num_valid, num_valid_host, nullptr, workspace, workspace_bytes, stream);
+}
+
+int g2v_cosine_loss_forward_coef(long long num_voxels, int feat_dim, const float* voxel_label,
+                                 const unsigned char* occ_mask, const void* grid_feats, const void* pseudo_gt,
+                                 int feat_dtype, float* loss, int* num_valid, int* num_valid_host, float* coef,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+    g_err[0] = 0;
+    if (num_voxels > 0 && !coef) return fail(G2V_ERR_INVALID, "coef is null");
+    if (((uintptr_t)coef & 7) != 0) return fail(G2V_ERR_INVALID, "coef must be 8-byte aligned");
+    return cosine_forward_impl(num_voxels, feat_dim, voxel_label, occ_mask, grid_feats, pseudo_gt, feat_dtype, loss,
+                               num_valid, num_valid_host, coef, workspace, workspace_bytes, stream);
 }
 
 int g2v_cosine_loss_forward_noalloc(long long num_voxels, int feat_dim, const float* voxel_label,

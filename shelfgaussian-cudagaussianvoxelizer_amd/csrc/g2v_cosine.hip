@@ -111,6 +111,9 @@ __device__ __forceinline__ void row_sums(const T* __restrict__ p, const T* __res
 }
 
 // Forward: block b sums the losses and counts the valid voxels of voxels [b vpb, (b+1) vpb).
+// With coef, the unscaled gradient coefficients (c1, c2) of every voxel of the range are written
+// as well ((0, 0) for a voxel the loss does not count), for a backward that forms the gradient
+// c1 g + c2 p itself.
 template <int L, bool VEC, typename T>
 __global__ void __launch_bounds__(kCosThreads) k_cos_fwd(int64_t V, int C, int vpb,
                                                           const float* __restrict__ label,
@@ -118,7 +121,8 @@ __global__ void __launch_bounds__(kCosThreads) k_cos_fwd(int64_t V, int C, int v
                                                           const T* __restrict__ p,
                                                           const T* __restrict__ g,
                                                           float* __restrict__ part_loss,
-                                                          int* __restrict__ part_cnt) {
+                                                          int* __restrict__ part_cnt,
+                                                          float* __restrict__ coef) {
     constexpr int G = kCosThreads / L;
     __shared__ float s_loss[G];
     __shared__ int s_cnt[G];
@@ -128,11 +132,19 @@ __global__ void __launch_bounds__(kCosThreads) k_cos_fwd(int64_t V, int C, int v
     float lsum = 0.0f;
     int cnt = 0;
     for (int64_t v = v0 + grp; v < v1; v += G) {
-        if (!cos_valid(label, mask, v)) continue;
+        if (!cos_valid(label, mask, v)) {
+            if (coef && gl == 0) *reinterpret_cast<float2*>(coef + 2 * v) = make_float2(0.0f, 0.0f);
+            continue;
+        }
         float dot, pp, gg;
         row_sums<L, VEC, T>(p + v * C, g + v * C, C, gl, dot, pp, gg);
         lsum += cos_loss(dot, pp, gg);
         ++cnt;
+        if (coef && gl == 0) {
+            float c1, c2;
+            cos_coefs(dot, pp, gg, 1.0f, c1, c2);
+            *reinterpret_cast<float2*>(coef + 2 * v) = make_float2(c1, c2);
+        }
     }
     if (gl == 0) {
         s_loss[grp] = lsum;
@@ -321,7 +333,8 @@ bool cosine_vec_ok(int C, int esize, const void* a, const void* b, const void* c
 }
 
 hipError_t launch_cosine_forward(int64_t V, int C, const float* label, const uint8_t* mask, const void* p_,
-                                 const void* g_, int fdt, float* loss, int* count, void* ws, hipStream_t s) {
+                                 const void* g_, int fdt, float* loss, int* count, void* ws, hipStream_t s,
+                                 float* coef) {
     Carver c(ws, (size_t)-1);
     float* part_loss = c.take<float>(kCosMaxBlocks);
     int* part_cnt = c.take<int>(kCosMaxBlocks);
@@ -339,10 +352,10 @@ hipError_t launch_cosine_forward(int64_t V, int C, const float* label, const uin
                 constexpr int LL = decltype(Lc)::value;
                 if (vec)
                     G2V_LAUNCH((k_cos_fwd<LL, true, T>), dim3(blocks), dim3(kCosThreads), 0, s, V, C, vpb, label,
-                               mask, p, g, part_loss, part_cnt);
+                               mask, p, g, part_loss, part_cnt, coef);
                 else
                     G2V_LAUNCH((k_cos_fwd<LL, false, T>), dim3(blocks), dim3(kCosThreads), 0, s, V, C, vpb, label,
-                               mask, p, g, part_loss, part_cnt);
+                               mask, p, g, part_loss, part_cnt, coef);
                 return hipGetLastError();
             });
         });

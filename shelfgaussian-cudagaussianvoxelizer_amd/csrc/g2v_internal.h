@@ -119,7 +119,19 @@ size_t backward_feats_workspace(const Grid& G, int n, int C, int64_t M, int64_t 
 hipError_t launch_backward_prepare(const Grid& G, int n, int C, const void* features, int fdt, const int* lb,
                                    const int* ub, int64_t M, const int* sorted_tiles, const int* sorted_gauss,
                                    const void* plan_ws, int64_t MR, void* ws, hipStream_t s);
+// The cosine loss's gradient as the feature backward's upstream gradient, formed on chip per voxel
+// as k1 target + k2 grid_feats with (k1, k2) = coef[2v .. 2v+1] * grad_loss[0] * inv_count: coef
+// as launch_cosine_forward writes it, grad_loss a device scalar, inv_count = 1 / count (0 when
+// count = 0).  float32 target and grid_feats with C % 4 == 0 and 16-byte aligned rows.
+struct CosG {
+    const float* tgt;
+    const float* coef;
+    const float* grad_loss;
+    float inv_count;
+};
+
 // prepared: launch_backward_prepare already ran on ws for the same Gaussians and CSR.
+// cos (optional): the upstream feature gradient is the cosine loss's (grad_feats unused).
 hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_density,
                                  const void* grad_feats, const float* means, const float* opacity,
                                  const float* cov_inv, const int* lb, const int* ub,
@@ -128,16 +140,18 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
                                  const void* grid_feats, const void* features, int fdt,
                                  const void* plan_ws, int64_t MR, float* grad_means, float* grad_cov,
                                  float* grad_opacity, void* grad_features, void* ws, bool prepared,
-                                 hipStream_t s);
+                                 hipStream_t s, const CosG* cos = nullptr);
 
 // ---- feature cosine loss (g2v_cosine.hip) --------------------------------------------------
 size_t cosine_workspace(int64_t V);
 // 4-element vector rows: C % 4 == 0 and every non-null pointer aligned to 4 elements of esize bytes.
 bool cosine_vec_ok(int C, int esize, const void* a, const void* b, const void* c);
 // Mean loss over the valid voxels into *loss and their number into *count (device pointers); p and g
-// hold elements of type fdt (kDtF32 or kDtBF16).
+// hold elements of type fdt (kDtF32 or kDtBF16).  coef (V x 2 floats, optional): the unscaled gradient
+// coefficients (c1, c2) of every voxel, 0 where the loss does not count the voxel.
 hipError_t launch_cosine_forward(int64_t V, int C, const float* label, const uint8_t* mask, const void* p,
-                                 const void* g, int fdt, float* loss, int* count, void* ws, hipStream_t s);
+                                 const void* g, int fdt, float* loss, int* count, void* ws, hipStream_t s,
+                                 float* coef = nullptr);
 // The same forward with the block partials in a file-scope device array of
 // cosine_scratch_bytes() bytes (per GPU) instead of a workspace: allocates nothing.
 size_t cosine_scratch_bytes();

@@ -31,7 +31,7 @@ def test_header_symbols_exported():
 
 
 def test_abi_version():
-    assert _lib().load().g2v_abi_version() == _lib().ABI_VERSION == 9
+    assert _lib().load().g2v_abi_version() == _lib().ABI_VERSION == 10
 
 
 def test_loader_refuses_other_abi(monkeypatch):
