@@ -195,7 +195,7 @@ def cosine_fused_leg(w, md, od, cd, fd, gDd, steps, warmup):
     included), and the step's peak allocation."""
     import torch
     from CudaGaussianVoxelizer import (PyCudaFeatsCosineLoss, PyCudaGaussianVoxelizer,
-                                       PyCudaGaussianVoxelizerCosineLoss)
+                                       PyCudaGaussianVoxelizerCosineLoss, _lib)
     dev = md.device
     X, Y, Z = _grid(w)
     C = fd.shape[1]
@@ -233,12 +233,25 @@ def cosine_fused_leg(w, md, od, cd, fd, gDd, steps, warmup):
             fn()
         b.record(cur)
         b.synchronize()
-        return round(a.elapsed_time(b) / steps, 4), round((torch.cuda.max_memory_allocated() - base) / 1e9, 3)
+        ms = round(a.elapsed_time(b) / steps, 4)
+        peak = round((torch.cuda.max_memory_allocated() - base) / 1e9, 3)
+        # the library's own kernels over as many further steps (HIP event pairs per launch)
+        _lib.profile_reset()
+        _lib.profile_enable(True)
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        _lib.profile_enable(False)
+        prof = _lib.profile_report()
+        _lib.profile_reset()
+        top = sorted(prof.items(), key=lambda kv: -kv[1][1])[:6]
+        return ms, peak, {k: round(v[1] / steps, 4) for k, v in top}
 
-    ch_ms, ch_gb = timed(chained)
-    fu_ms, fu_gb = timed(fused_step)
+    ch_ms, ch_gb, ch_k = timed(chained)
+    fu_ms, fu_gb, fu_k = timed(fused_step)
     return {"grid": [X, Y, Z], "feat_dim": C, "chained_ms": ch_ms, "fused_ms": fu_ms,
             "speedup": round(ch_ms / fu_ms, 3), "chained_step_peak_gb": ch_gb, "fused_step_peak_gb": fu_gb,
+            "chained_kernels_ms": ch_k, "fused_kernels_ms": fu_k,
             "data": "the G2V workload with a randn target (seed 11), 80 % of voxels visible, labels 0..2; "
                     "objective density.gD + loss"}
 

@@ -965,6 +965,7 @@ struct BrSmem {
     int tl_t[kBrSlots], tl_s[kBrSlots];   // tiles of the region (inside the grid) and their slots
     int ntl;
     float2 kc[FU ? kBrSlots : 1][FU ? 64 : 1];
+    int tl_org[FU ? kBrSlots : 1][3];     // FU: first voxel (x, y, z) of each tile of tl_t
 };
 
 // gF chunk of one tile for the staging thread: channel sc of the chunk, voxel octets so and
@@ -1311,6 +1312,11 @@ __global__ void __launch_bounds__(kBrThreads, 1) k_bwd_region(
                     if (min(max(toff[t + 1], 0), M) <= min(max(toff[t], 0), M)) continue;   // empty list
                     sm.tl_t[k] = t;
                     sm.tl_s[k] = (a * 2 + b) * tpz + cz;
+                    if constexpr (FU) {
+                        sm.tl_org[k][0] = tx * kTile;
+                        sm.tl_org[k][1] = ty * kTile;
+                        sm.tl_org[k][2] = tz * kTile;
+                    }
                     ++k;
                 }
         sm.ntl = k;
@@ -1320,17 +1326,26 @@ __global__ void __launch_bounds__(kBrThreads, 1) k_bwd_region(
     if (ntl == 0) return;   // every row stays zero: phase C reads no partial row of this region
     if constexpr (FU) {
         // (k1, k2) of every voxel of the region's tiles (0 outside the grid; those values are
-        // masked anyway); the first pass's barrier orders these stores before their reads
+        // masked anyway); the first pass's barrier orders these stores before their reads.  Two
+        // guarded entries per thread (ntl * 64 <= 2 * kBrThreads) and the tile origins from
+        // tl_org: a loop with a per-thread trip count here would leave values that the tile loop
+        // shares with it divergent, and its buffer descriptors with them.
+        static_assert(kBrSlots * 64 <= 2 * kBrThreads, "two coefficient entries per thread");
         const float scale = cg.grad_loss[0] * cg.inv_count;   // as the loss's own backward forms it
-        for (int e = threadIdx.x; e < ntl * 64; e += kBrThreads) {
-            int x, y, z;
-            tile_voxel(G, sm.tl_t[e >> 6], e & 63, x, y, z);
-            float2 kk = make_float2(0.0f, 0.0f);
-            if (in_grid(G, x, y, z)) {
-                const float2 c = *reinterpret_cast<const float2*>(cg.coef + 2 * voxel_index(G, x, y, z));
-                kk = make_float2(c.x * scale, c.y * scale);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int e = threadIdx.x + h * kBrThreads;
+            if (e < ntl * 64) {
+                const int* org = sm.tl_org[e >> 6];
+                const int lv = e & 63;
+                const int x = org[0] + (lv >> 4), y = org[1] + ((lv >> 2) & 3), z = org[2] + (lv & 3);
+                float2 kk = make_float2(0.0f, 0.0f);
+                if (in_grid(G, x, y, z)) {
+                    const float2 c = *reinterpret_cast<const float2*>(cg.coef + 2 * voxel_index(G, x, y, z));
+                    kk = make_float2(c.x * scale, c.y * scale);
+                }
+                sm.kc[e >> 6][lv] = kk;
             }
-            sm.kc[e >> 6][e & 63] = kk;
         }
         gF = cg.tgt;
     }
