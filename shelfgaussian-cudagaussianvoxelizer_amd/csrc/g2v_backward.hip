@@ -955,20 +955,19 @@ constexpr int kBrPass = kBrWaves * kBrRbMax * 16;   // region rows per pass
 static_assert(kBrPass * kBrSlots % kBrThreads == 0 && kBrPass <= 2 * kBrThreads, "row-table staging shape");
 
 // FU: the upstream feature gradient is the cosine loss's (k1 target + k2 grid_feats per voxel);
-// kc holds (k1, k2) of the voxels of the region's tiles, in the order of tl_t.
+// kc holds (k1, k2) of the voxels of the region's tiles, in the order of tl_org.
 template <bool FU>
 struct BrSmem {
     bf16x8 bhi[2][2][kBrCb][64];   // B operand (gF chunk): [buffer][k step of 32 voxels][channel block][lane]
     bf16x8 blo[2][2][kBrCb][64];
     int tab[kBrPass][kBrSlots + 1];       // row table of this pass's rows (M: absent pair); padded row
     int rslot[kBrPass];                   // G->R slot of each row of the pass
-    int tl_t[kBrSlots], tl_s[kBrSlots];   // tiles of the region (inside the grid) and their slots
+    int tl_org[kBrSlots][3], tl_s[kBrSlots];   // tiles of the region (inside the grid): first voxel, slot
     int ntl;
     float2 kc[FU ? kBrSlots : 1][FU ? 64 : 1];
-    int tl_org[FU ? kBrSlots : 1][3];     // FU: first voxel (x, y, z) of each tile of tl_t
 };
 
-// gF chunk of one tile for the staging thread: channel sc of the chunk, voxel octets so and
+// gF chunk of the tile whose first voxel is (x0, y0, z0), for the staging thread: channel sc of the chunk, voxel octets so and
 // so + 4 (tile-local x = 2k + so/2, y = 2(so&1) + i/4, z = i%4 for value v[k][i]).  Buffer loads
 // from the tile origin: a per-thread offset for each (x, y) pair and a uniform offset for each z.
 // Coordinates are clamped into the grid, so every load stays inside gF (the descriptor's range
@@ -976,12 +975,9 @@ struct BrSmem {
 // Offsets need 16 * Y * Z * C < 2^32 (checked on the host).
 // GB: gF holds bfloat16 values (2-byte loads, widened exactly).
 template <bool GB>
-__device__ __forceinline__ unsigned br_load_tile(const Grid& G, int C, int c0, int t, int sc, int so,
+__device__ __forceinline__ unsigned br_load_tile(const Grid& G, int C, int c0, int x0, int y0, int z0, int sc, int so,
                                                  const void* __restrict__ gF, float (&v)[2][8]) {
     constexpr int kEs = GB ? 2 : 4;   // bytes per element
-    const int tyz = G.tiles[1] * G.tiles[2];
-    const int tx = t / tyz, ty = (t - tx * tyz) / G.tiles[2], tz = t % G.tiles[2];
-    const int x0 = tx * kTile, y0 = ty * kTile, z0 = tz * kTile;
     const int X = G.dims[0], Y = G.dims[1], Z = G.dims[2];
     const int64_t origin = ((int64_t)(x0 * Y + y0) * Z + z0) * C + c0;
     const int64_t left = ((int64_t)X * Y * Z * C - origin) * kEs;
@@ -1034,12 +1030,9 @@ __device__ __forceinline__ unsigned br_load_tile(const Grid& G, int C, int c0, i
 // per voxel: half the load instructions of the one-channel form.  Bit i + 8h of the mask marks the
 // values that are real.
 template <bool GB>
-__device__ __forceinline__ unsigned br_load_tile2(const Grid& G, int C, int c0, int t, int cp2, int o,
+__device__ __forceinline__ unsigned br_load_tile2(const Grid& G, int C, int c0, int x0, int y0, int z0, int cp2, int o,
                                                   const void* __restrict__ gF, float (&v)[2][8]) {
     constexpr int kEs = GB ? 2 : 4;   // bytes per element
-    const int tyz = G.tiles[1] * G.tiles[2];
-    const int tx = t / tyz, ty = (t - tx * tyz) / G.tiles[2], tz = t % G.tiles[2];
-    const int x0 = tx * kTile, y0 = ty * kTile, z0 = tz * kTile;
     const int X = G.dims[0], Y = G.dims[1], Z = G.dims[2];
     const int64_t origin = ((int64_t)(x0 * Y + y0) * Z + z0) * C + c0;
     const int64_t left = ((int64_t)X * Y * Z * C - origin) * kEs;
@@ -1109,7 +1102,7 @@ __device__ __forceinline__ void br_tiles(BrSmem<FU>& sm, const Grid& G, int C, i
     float pre[2][8];
     float pre2[FU ? 2 : 1][FU ? 8 : 1];   // FU: grid_feats values of the same voxels and channels
     unsigned pmask = 0;
-    // tpos: the tile's position in tl_t (FU: its row of kc)
+    // tpos: the tile's position in tl_org (FU: its row of kc)
     auto stage = [&](int buf, int tpos) {
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
@@ -1184,17 +1177,19 @@ __device__ __forceinline__ void br_tiles(BrSmem<FU>& sm, const Grid& G, int C, i
     const int klast = ntl - 1;
     // prologue: tile 0 staged, gF of tile 1 and the weights of tile 0 in flight (in the order
     // the loop issues them, so that the compiler's waits at the loop head stay exact)
-    auto load_tile = [&](int t) {
+    // the tile at position k of the region's list, from its first voxel (no tile-id divisions here)
+    auto load_tile = [&](int k) {
+        const int x0 = uniform(sm.tl_org[k][0]), y0 = uniform(sm.tl_org[k][1]), z0 = uniform(sm.tl_org[k][2]);
         if constexpr (FU) {   // same voxels and channels, so the same mask
-            if constexpr (P2) br_load_tile2<GB>(G, C, c0, t, cp2, ot, gF2, pre2);
-            else br_load_tile<GB>(G, C, c0, t, sc, so, gF2, pre2);
+            if constexpr (P2) br_load_tile2<GB>(G, C, c0, x0, y0, z0, cp2, ot, gF2, pre2);
+            else br_load_tile<GB>(G, C, c0, x0, y0, z0, sc, so, gF2, pre2);
         }
-        if constexpr (P2) return br_load_tile2<GB>(G, C, c0, t, cp2, ot, gF, pre);
-        else return br_load_tile<GB>(G, C, c0, t, sc, so, gF, pre);
+        if constexpr (P2) return br_load_tile2<GB>(G, C, c0, x0, y0, z0, cp2, ot, gF, pre);
+        else return br_load_tile<GB>(G, C, c0, x0, y0, z0, sc, so, gF, pre);
     };
-    pmask = load_tile(uniform(sm.tl_t[0]));
+    pmask = load_tile(0);
     stage(0, 0);
-    pmask = load_tile(uniform(sm.tl_t[min(1, klast)]));
+    pmask = load_tile(min(1, klast));
     rows_of(0);
     load_w(0);
     load_w(1);
@@ -1202,7 +1197,7 @@ __device__ __forceinline__ void br_tiles(BrSmem<FU>& sm, const Grid& G, int C, i
     for (int k = 0; k < ntl; ++k) {
         const int kn = min(k + 1, klast);
         stage((k + 1) & 1, kn);
-        pmask = load_tile(uniform(sm.tl_t[min(k + 2, klast)]));
+        pmask = load_tile(min(k + 2, klast));
         rows_of(kn);
         __builtin_amdgcn_sched_barrier(0);
         half(k & 1, 0);
@@ -1310,13 +1305,10 @@ __global__ void __launch_bounds__(kBrThreads, 1) k_bwd_region(
                     if (tx >= G.tiles[0] || ty >= G.tiles[1] || tz >= G.tiles[2]) continue;
                     const int t = (tx * G.tiles[1] + ty) * G.tiles[2] + tz;
                     if (min(max(toff[t + 1], 0), M) <= min(max(toff[t], 0), M)) continue;   // empty list
-                    sm.tl_t[k] = t;
                     sm.tl_s[k] = (a * 2 + b) * tpz + cz;
-                    if constexpr (FU) {
-                        sm.tl_org[k][0] = tx * kTile;
-                        sm.tl_org[k][1] = ty * kTile;
-                        sm.tl_org[k][2] = tz * kTile;
-                    }
+                    sm.tl_org[k][0] = tx * kTile;
+                    sm.tl_org[k][1] = ty * kTile;
+                    sm.tl_org[k][2] = tz * kTile;
                     ++k;
                 }
         sm.ntl = k;
