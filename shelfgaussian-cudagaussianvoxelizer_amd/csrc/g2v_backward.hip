@@ -633,6 +633,7 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
                 const int st = ch % kBtStages, ab = ch & 1;
                 StepOps ops;
                 load_ops(st, ab, ops);
+                asm volatile("" ::: "memory");   // every operand read issued before the first MFMA
                 mult(0, ops);
                 __builtin_amdgcn_sched_barrier(0);
                 write_a(ch + 1, (ch + 1) % kBtStages, ab ^ 1);
@@ -664,6 +665,7 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
                 dma_f(min(ch + 1, clast), fb ^ 1, 0, NF);
                 StepOps ops;
                 load_ops(fb, ab, ops);
+                asm volatile("" ::: "memory");   // every operand read issued before the first MFMA
                 mult(0, ops);
                 __builtin_amdgcn_sched_barrier(0);
                 write_a(ch + 1, (ch + 1) % kBtStages, ab ^ 1);

@@ -380,6 +380,22 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
     const char* fbase = reinterpret_cast<const char*>(fpk);
     float dacc[4] = {0.0f, 0.0f, 0.0f, 0.0f};   // density of the column's voxels, this thread's octets
 
+    // packed quads of K step ks: rows of slots ks*16 + 8*kh + i, channels (lane offset lo)..+3
+    typedef typename std::conditional<OBF16, uint2, uint4>::type Quad;   // 4 packed channels
+    auto gather = [&](int ks, uint32_t lo, Quad (&u)[8]) {
+        const uint32_t* rp = &sm.roff[ks * 16 + kh * 8];
+        const uint4 ra = *reinterpret_cast<const uint4*>(rp);
+        const uint4 rb = *reinterpret_cast<const uint4*>(rp + 4);
+        const uint32_t rs[8] = {ra.x, ra.y, ra.z, ra.w, rb.x, rb.y, rb.z, rb.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) u[i] = *reinterpret_cast<const Quad*>(fbase + (size_t)(rs[i] + lo));
+    };
+    // The first gather of a pass whose K chunk is already in LDS (one chunk: the weights stay for
+    // every pass) is issued before the previous pass's stores: loads and stores share one in-order
+    // counter, so a gather issued after the stores would wait for every store to complete.
+    Quad qa[8], qb[8];
+    bool qa_ready = false;
+
     for (int cbase = 0; cbase < C; cbase += kFwdChanPerPass) {
         const int cw0 = cbase + wave * kFwdChanPerWave;          // first channel of this wave
         const bool has_ch = cw0 < C;                               // wave-uniform
@@ -401,17 +417,6 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
                 __syncthreads();
             }
             if (has_ch) {
-                // packed quads of K step ks: rows of slots ks*16 + 8*kh + i, channels cw0+4jl..+3
-                typedef typename std::conditional<OBF16, uint2, uint4>::type Quad;   // 4 packed channels
-                auto gather = [&](int ks, Quad (&u)[8]) {
-                    const uint32_t* rp = &sm.roff[ks * 16 + kh * 8];
-                    const uint4 ra = *reinterpret_cast<const uint4*>(rp);
-                    const uint4 rb = *reinterpret_cast<const uint4*>(rp + 4);
-                    const uint32_t rs[8] = {ra.x, ra.y, ra.z, ra.w, rb.x, rb.y, rb.z, rb.w};
-#pragma unroll
-                    for (int i = 0; i < 8; ++i)
-                        u[i] = *reinterpret_cast<const Quad*>(fbase + (size_t)(rs[i] + lane_off));
-                };
                 auto step = [&](int ks, const Quad (&u)[8]) {
                     const bf16x8 ah0 = sm.whi[ks][0][lane], al0 = sm.wlo[ks][0][lane];
                     const bf16x8 ah1 = sm.whi[ks][1][lane], al1 = sm.wlo[ks][1][lane];
@@ -444,22 +449,22 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
                 // loads and steps are unconditional (ksteps is even, the prefetch index is
                 // clamped) so the next step's gather stays in flight across this step's MFMAs;
                 // the scheduling barriers keep the compiler from sinking the gathers to their use
-                Quad ua[8], ub[8];
                 const int klast = ksteps - 1;
                 if (ksteps > 0) {
-                    gather(0, ua);
+                    if (!qa_ready) gather(0, lane_off, qa);
                     for (int ks = 0; ks < ksteps; ks += 2) {
-                        gather(ks + 1, ub);
+                        gather(ks + 1, lane_off, qb);
                         __builtin_amdgcn_sched_barrier(0);
-                        step(ks, ua);
+                        step(ks, qa);
                         __builtin_amdgcn_sched_barrier(0);
-                        gather(min(ks + 2, klast), ua);
+                        gather(min(ks + 2, klast), lane_off, qa);
                         __builtin_amdgcn_sched_barrier(0);
-                        step(ks + 1, ub);
+                        step(ks + 1, qb);
                         __builtin_amdgcn_sched_barrier(0);
                     }
                 }
             }
+            qa_ready = false;
         }
 
         if (cbase == 0) {
@@ -482,6 +487,13 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
             __syncthreads();
         }
 
+        {
+            const int nb = cbase + kFwdChanPerPass;   // the next pass, when its weights stay in LDS
+            if (nkc == 1 && Ng > 0 && nb + wave * kFwdChanPerWave < C) {
+                gather(0, (uint32_t)(nb + wave * kFwdChanPerWave + 4 * jl) * kCh, qa);
+                qa_ready = true;
+            }
+        }
         // epilogue: D row of element i = 8*(i/4) + 4*kh + i%4 (voxel), column jl -> channels
         // cw0 + 4*jl + cb for channel block cb
         if (has_ch) {
