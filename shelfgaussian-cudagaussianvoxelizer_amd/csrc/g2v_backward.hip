@@ -213,6 +213,16 @@ __device__ __forceinline__ void dma4(const void* gptr, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
                  :: "v"(gptr), "s"(lds) : "memory", "m0");
 }
+// Scalar-base forms: the wave-uniform base in SGPRs and a 32-bit per-lane byte offset, so that a
+// chunk's advance is scalar work and the per-lane offsets stay fixed across the chunk loop.
+__device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :: "v"(voff), "s"(sbase), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void dma16s_nt(const void* sbase, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt"
+                 :: "v"(voff), "s"(sbase), "s"(lds) : "memory", "m0");
+}
 // Streaming variants (non-temporal): for data read once, so that it does not evict the feature
 // rows that many tiles re-read.
 __device__ __forceinline__ void dma16_nt(const void* gptr, uint32_t lds) {
@@ -352,6 +362,9 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
     const int mb = wave >> 2, ngrp = wave & 3;   // voxel block (epilogues) / k half (K loop), N group
     const int tyz = G.tiles[1] * G.tiles[2];
     const int tx = tile / tyz, ty = (tile - tx * tyz) / G.tiles[2], tz = tile % G.tiles[2];
+    // every voxel of the tile inside the grid (no row of the A operand is cleared)
+    const bool tile_in = (tx + 1) * kTile <= G.dims[0] && (ty + 1) * kTile <= G.dims[1] &&
+                         (tz + 1) * kTile <= G.dims[2];
 
     if (threadIdx.x < 64) {
         int x, y, z;
@@ -418,6 +431,13 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
     constexpr int kSrc = FU ? 2 : 1;
     const GT* gsrc[kSrc][kNGs];
     int gcoff[kNGs];   // channel of this lane's load within a chunk
+    // VEC float: chunks wholly inside the rows are loaded from a wave-uniform base (the source's
+    // start plus the chunk) and the lane's fixed 32-bit byte offset, when every row offset fits
+    const GT* gbase[kSrc];
+    uint32_t goff[kNGs];
+    gbase[0] = FU ? reinterpret_cast<const GT*>(cg.tgt) : gF;
+    gbase[kSrc - 1] = FU ? static_cast<const GT*>(grid_feats) : gF;
+    const bool g32 = (int64_t)G.dims[0] * G.dims[1] * G.dims[2] * C * (int64_t)sizeof(GT) <= 0xffffffffLL;
 #pragma unroll
     for (int k = 0; k < kNG; ++k) {
         const int v = (BF || VEC) ? wave * 8 + (lane >> 3) : wave * 8 + 2 * k + (lane >> 5);
@@ -430,6 +450,7 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
         }
         gcoff[k] = BF ? 8 * (lane & 7)
                       : (VEC ? 4 * ((lane & 7) ^ swz(v)) : 4 * (((lane & 31) >> 2) ^ swz(v)) + (lane & 3));
+        goff[k] = (uint32_t)((row + gcoff[k]) * (int64_t)sizeof(GT));
     }
     auto dma_g = [&](int chunk, int stage) {
 #pragma unroll
@@ -440,8 +461,11 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
                     dma16_nt(gsrc[sr][k] + min(chunk * kKc + gcoff[k], C - 8),
                              uniform(lds_addr(reinterpret_cast<char*>(&sm.graw[stage][sr][0][0]) + wave * 8 * 128)));
                 } else if (VEC) {
-                    dma16_nt(gsrc[sr][k] + min(chunk * kBtKc + gcoff[k], C - 4),
-                             uniform(lds_addr(&sm.graw[stage][sr][wave * 8][0])));
+                    const uint32_t lds = uniform(lds_addr(&sm.graw[stage][sr][wave * 8][0]));
+                    if (g32 && chunk * kBtKc + kBtKc <= C)   // wave-uniform
+                        dma16s_nt(gbase[sr] + chunk * kBtKc, goff[k], lds);
+                    else
+                        dma16_nt(gsrc[sr][k] + min(chunk * kBtKc + gcoff[k], C - 4), lds);
                 } else {
                     dma4_nt(gsrc[sr][k] + min(chunk * kBtKc + gcoff[k], C - 1),
                             uniform(lds_addr(&sm.graw[stage][sr][wave * 8 + 2 * k][0])));
@@ -485,8 +509,8 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             for (int i = 0; i < kBtDma; ++i) {
                 if (i < i0 || i >= i1) continue;
                 const int rg = wave + kBtWaves * i;
-                dma16(fbase + (doff[i] + (uint32_t)chunk * kBtRowBytes),
-                      uniform(lds_addr(&sm.u.frow[buf][rg * 8 * kBtRowBytes])));
+                dma16s(fbase + (size_t)chunk * kBtRowBytes, doff[i],
+                       uniform(lds_addr(&sm.u.frow[buf][rg * 8 * kBtRowBytes])));
             }
         };
 
@@ -558,10 +582,14 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
                 xr.z = __float_as_uint(k1 * __uint_as_float(xr.z) + k2 * __uint_as_float(xf.z));
                 xr.w = __float_as_uint(k1 * __uint_as_float(xr.w) + k2 * __uint_as_float(xf.w));
             }
-            const f32x2 x01 = {__uint_as_float(xr.x & (0u - (unsigned)(0 < lim))),
-                               __uint_as_float(xr.y & (0u - (unsigned)(1 < lim)))};
-            const f32x2 x23 = {__uint_as_float(xr.z & (0u - (unsigned)(2 < lim))),
-                               __uint_as_float(xr.w & (0u - (unsigned)(3 < lim)))};
+            if (!(tile_in && ch * kKc + kKc <= C)) {   // wave-uniform: rows or channels to clear
+                xr.x &= 0u - (unsigned)(0 < lim);
+                xr.y &= 0u - (unsigned)(1 < lim);
+                xr.z &= 0u - (unsigned)(2 < lim);
+                xr.w &= 0u - (unsigned)(3 < lim);
+            }
+            const f32x2 x01 = {__uint_as_float(xr.x), __uint_as_float(xr.y)};
+            const f32x2 x23 = {__uint_as_float(xr.z), __uint_as_float(xr.w)};
             const bf16x2 h01 = __builtin_convertvector(x01, bf16x2), h23 = __builtin_convertvector(x23, bf16x2);
             const bf16x2 l01 = __builtin_convertvector(x01 - __builtin_convertvector(h01, f32x2), bf16x2);
             const bf16x2 l23 = __builtin_convertvector(x23 - __builtin_convertvector(h23, f32x2), bf16x2);
@@ -975,8 +1003,9 @@ struct BrSmem {
 // Coordinates are clamped into the grid, so every load stays inside gF (the descriptor's range
 // ends at gF's end as well); bit i + 8k of the returned mask marks the values that are real.
 // Offsets need 16 * Y * Z * C < 2^32 (checked on the host).
-// GB: gF holds bfloat16 values (2-byte loads, widened exactly).
-template <bool GB>
+// GB: gF holds bfloat16 values (2-byte loads, widened exactly).  IN: the tile lies inside the grid
+// and the chunk inside the row (no clamps; every value is real).
+template <bool GB, bool IN>
 __device__ __forceinline__ unsigned br_load_tile(const Grid& G, int C, int c0, int x0, int y0, int z0, int sc, int so,
                                                  const void* __restrict__ gF, float (&v)[2][8]) {
     constexpr int kEs = GB ? 2 : 4;   // bytes per element
@@ -986,20 +1015,20 @@ __device__ __forceinline__ unsigned br_load_tile(const Grid& G, int C, int c0, i
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<char*>(static_cast<const char*>(gF) + origin * kEs), (short)0, (int)min(left, (int64_t)0x7fffffff),
         0x00020000);
-    const bool cok = c0 + sc < C;
-    const unsigned cc = (unsigned)(min(c0 + sc, C - 1) - c0);
+    const bool cok = IN || c0 + sc < C;
+    const unsigned cc = IN ? (unsigned)sc : (unsigned)(min(c0 + sc, C - 1) - c0);
     unsigned voff[2][2];
     bool xok[2], yok[2];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
         const int x = x0 + 2 * k + (so >> 1);
-        xok[k] = x < X;
-        const unsigned xl = (unsigned)(min(x, X - 1) - x0);
+        xok[k] = IN || x < X;
+        const unsigned xl = IN ? (unsigned)(2 * k + (so >> 1)) : (unsigned)(min(x, X - 1) - x0);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int y = y0 + 2 * (so & 1) + h;
-            if (k == 0) yok[h] = y < Y;
-            const unsigned yl = (unsigned)(min(y, Y - 1) - y0);
+            if (k == 0) yok[h] = IN || y < Y;
+            const unsigned yl = IN ? (unsigned)(2 * (so & 1) + h) : (unsigned)(min(y, Y - 1) - y0);
             voff[k][h] = ((xl * Y + yl) * Z * C + cc) * (unsigned)kEs;
         }
     }
@@ -1007,8 +1036,8 @@ __device__ __forceinline__ unsigned br_load_tile(const Grid& G, int C, int c0, i
     bool zok[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        zok[i] = z0 + i < Z;
-        soff[i] = (min(z0 + i, Z - 1) - z0) * C * kEs;
+        zok[i] = IN || z0 + i < Z;
+        soff[i] = (IN ? i : min(z0 + i, Z - 1) - z0) * C * kEs;
     }
     unsigned mask = 0;
 #pragma unroll
@@ -1023,15 +1052,15 @@ __device__ __forceinline__ unsigned br_load_tile(const Grid& G, int C, int c0, i
                 v[k][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff[k][i >> 2], soff[i & 3], 2));
             mask |= (cok && xok[k] && yok[i >> 2] && zok[i & 3]) ? (1u << (i + 8 * k)) : 0u;
         }
-    return mask;
+    return IN ? 0xffffu : mask;
 }
 
 // Paired form of br_load_tile for even C (rows aligned to two channels): the staging thread takes
 // channels cp2 and cp2 + 1 of the chunk (cp2 = 2 cp) for the 8 voxels of octet o (tile-local
 // x = o/2, y = 2(o&1) + i/4, z = i%4 for value v[h][i] of channel cp2 + h), with one 2-channel load
 // per voxel: half the load instructions of the one-channel form.  Bit i + 8h of the mask marks the
-// values that are real.
-template <bool GB>
+// values that are real.  IN as for br_load_tile.
+template <bool GB, bool IN>
 __device__ __forceinline__ unsigned br_load_tile2(const Grid& G, int C, int c0, int x0, int y0, int z0, int cp2, int o,
                                                   const void* __restrict__ gF, float (&v)[2][8]) {
     constexpr int kEs = GB ? 2 : 4;   // bytes per element
@@ -1041,26 +1070,26 @@ __device__ __forceinline__ unsigned br_load_tile2(const Grid& G, int C, int c0, 
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<char*>(static_cast<const char*>(gF) + origin * kEs), (short)0, (int)min(left, (int64_t)0x7fffffff),
         0x00020000);
-    const bool cok = c0 + cp2 < C;   // C even: both channels of the pair or neither
-    const unsigned cc = (unsigned)(min(c0 + cp2, C - 2) - c0);
+    const bool cok = IN || c0 + cp2 < C;   // C even: both channels of the pair or neither
+    const unsigned cc = IN ? (unsigned)cp2 : (unsigned)(min(c0 + cp2, C - 2) - c0);
     const int x = x0 + (o >> 1);
-    const bool xok = x < X;
-    const unsigned xl = (unsigned)(min(x, X - 1) - x0);
+    const bool xok = IN || x < X;
+    const unsigned xl = IN ? (unsigned)(o >> 1) : (unsigned)(min(x, X - 1) - x0);
     unsigned voff[2];
     bool yok[2];
 #pragma unroll
     for (int hy = 0; hy < 2; ++hy) {
         const int y = y0 + 2 * (o & 1) + hy;
-        yok[hy] = y < Y;
-        const unsigned yl = (unsigned)(min(y, Y - 1) - y0);
+        yok[hy] = IN || y < Y;
+        const unsigned yl = IN ? (unsigned)(2 * (o & 1) + hy) : (unsigned)(min(y, Y - 1) - y0);
         voff[hy] = ((xl * Y + yl) * Z * C + cc) * (unsigned)kEs;
     }
     int soff[4];
     bool zok[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        zok[i] = z0 + i < Z;
-        soff[i] = (min(z0 + i, Z - 1) - z0) * C * kEs;
+        zok[i] = IN || z0 + i < Z;
+        soff[i] = (IN ? i : min(z0 + i, Z - 1) - z0) * C * kEs;
     }
     unsigned mask = 0;
 #pragma unroll
@@ -1079,7 +1108,7 @@ __device__ __forceinline__ unsigned br_load_tile2(const Grid& G, int C, int c0, 
         const unsigned ok = (cok && xok && yok[i >> 2] && zok[i & 3]) ? 1u : 0u;
         mask |= (ok << i) | (ok << (i + 8));
     }
-    return mask;
+    return IN ? 0xffffu : mask;
 }
 
 // Tile loop of one phase-B pass for a wave that owns NB row blocks (pass blocks wave + 8b,
@@ -1090,7 +1119,7 @@ __device__ __forceinline__ unsigned br_load_tile2(const Grid& G, int C, int c0, 
 // so loads stay in flight across the barrier and the compiler waits for each where its registers
 // are used.
 // FU: gF is the target and gF2 grid_feats; a staged value is k1 target + k2 grid_feats.
-template <int NB, bool GB, bool P2, bool FU>
+template <int NB, bool GB, bool P2, bool FU, bool IN>
 __device__ __forceinline__ void br_tiles(BrSmem<FU>& sm, const Grid& G, int C, int c0, int ntl, int prow,
                                          const void* __restrict__ gF, const void* __restrict__ gF2,
                                          const __bf16* __restrict__ wt, float* __restrict__ gpart) {
@@ -1183,11 +1212,11 @@ __device__ __forceinline__ void br_tiles(BrSmem<FU>& sm, const Grid& G, int C, i
     auto load_tile = [&](int k) {
         const int x0 = uniform(sm.tl_org[k][0]), y0 = uniform(sm.tl_org[k][1]), z0 = uniform(sm.tl_org[k][2]);
         if constexpr (FU) {   // same voxels and channels, so the same mask
-            if constexpr (P2) br_load_tile2<GB>(G, C, c0, x0, y0, z0, cp2, ot, gF2, pre2);
-            else br_load_tile<GB>(G, C, c0, x0, y0, z0, sc, so, gF2, pre2);
+            if constexpr (P2) br_load_tile2<GB, IN>(G, C, c0, x0, y0, z0, cp2, ot, gF2, pre2);
+            else br_load_tile<GB, IN>(G, C, c0, x0, y0, z0, sc, so, gF2, pre2);
         }
-        if constexpr (P2) return br_load_tile2<GB>(G, C, c0, x0, y0, z0, cp2, ot, gF, pre);
-        else return br_load_tile<GB>(G, C, c0, x0, y0, z0, sc, so, gF, pre);
+        if constexpr (P2) return br_load_tile2<GB, IN>(G, C, c0, x0, y0, z0, cp2, ot, gF, pre);
+        else return br_load_tile<GB, IN>(G, C, c0, x0, y0, z0, sc, so, gF, pre);
     };
     pmask = load_tile(0);
     stage(0, 0);
@@ -1232,7 +1261,7 @@ __device__ __forceinline__ void br_pass(BrSmem<FU>& sm, const Grid& G, int C, in
                                         int KR, int M, int MR, int jr0, const void* __restrict__ gF,
                                         const void* __restrict__ gF2, const int* __restrict__ r_pairs,
                                         const int* __restrict__ table, const __bf16* __restrict__ wt,
-                                        float* __restrict__ gpart) {
+                                        float* __restrict__ gpart, bool interior) {
     const int wave = threadIdx.x >> 6;
     const int prow = min(KR - rp, kBrPass);
     const int nblk = (prow + 15) >> 4;
@@ -1269,10 +1298,15 @@ __device__ __forceinline__ void br_pass(BrSmem<FU>& sm, const Grid& G, int C, in
     }
     __syncthreads();
     static_assert(kBrRbMax == 3, "block-count dispatch");
-    if (nb >= 3) br_tiles<3, GB, P2, FU>(sm, G, C, c0, ntl, prow, gF, gF2, wt, gpart);
-    else if (nb == 2) br_tiles<2, GB, P2, FU>(sm, G, C, c0, ntl, prow, gF, gF2, wt, gpart);
-    else if (nb == 1) br_tiles<1, GB, P2, FU>(sm, G, C, c0, ntl, prow, gF, gF2, wt, gpart);
-    else br_tiles<0, GB, P2, FU>(sm, G, C, c0, ntl, prow, gF, gF2, wt, gpart);
+    auto run = [&](auto inc) {
+        constexpr bool IN = decltype(inc)::value;
+        if (nb >= 3) br_tiles<3, GB, P2, FU, IN>(sm, G, C, c0, ntl, prow, gF, gF2, wt, gpart);
+        else if (nb == 2) br_tiles<2, GB, P2, FU, IN>(sm, G, C, c0, ntl, prow, gF, gF2, wt, gpart);
+        else if (nb == 1) br_tiles<1, GB, P2, FU, IN>(sm, G, C, c0, ntl, prow, gF, gF2, wt, gpart);
+        else br_tiles<0, GB, P2, FU, IN>(sm, G, C, c0, ntl, prow, gF, gF2, wt, gpart);
+    };
+    if (interior) run(std::true_type{});
+    else run(std::false_type{});
 }
 
 // P2: even C with rows aligned to two channels, so the gF staging loads take two channels at once.
@@ -1344,8 +1378,18 @@ __global__ void __launch_bounds__(kBrThreads, 1) k_bwd_region(
         gF = cg.tgt;
     }
 
+    // every voxel of the region's tiles inside the grid and the whole chunk inside the rows: the
+    // staging loads need no clamps and every staged value is real
+    bool interior;
+    {
+        const int rnyz = RG.n[1] * RG.n[2];
+        const int rx = R / rnyz, ry = (R - rx * rnyz) / RG.n[2], rz = R % RG.n[2];
+        interior = uniform((rx + 1) * RG.cell[0] <= G.dims[0] && (ry + 1) * RG.cell[1] <= G.dims[1] &&
+                           (rz + 1) * RG.cell[2] <= G.dims[2] && c0 + kBrCc <= C) != 0;
+    }
     for (int rp = 0; rp < KR; rp += kBrPass)
-        br_pass<GB, P2, FU>(sm, G, C, c0, ntl, rp, KR, M, MR, jr0, gF, grid_feats, r_pairs, table, wt, gpart);
+        br_pass<GB, P2, FU>(sm, G, C, c0, ntl, rp, KR, M, MR, jr0, gF, grid_feats, r_pairs, table, wt, gpart,
+                            interior);
 }
 
 // ------------------------------------------------------------------------------------------
