@@ -295,6 +295,7 @@ struct LaneGeom {
 
 __device__ __forceinline__ void lane_geom(const Grid& G, const GaussParams& p, int x0, int y0, int z0,
                                           LaneGeom& L) {
+#pragma clang fp contract(off)
     L.inx = L.iny = L.inz = 0;
 #pragma unroll
     for (int a = 0; a < 2; ++a) {
@@ -318,7 +319,10 @@ struct LaneExp {
     float Fxy[2][2], Gxy[2][2], Fz[4];
 };
 
+// Contraction is off in these helpers, so that every phase A instantiation that inlines them
+// computes the same e (and so the same split weights) for the same pair, whatever the code around.
 __device__ __forceinline__ void lane_exp(const GaussParams& p, const LaneGeom& L, LaneExp& E) {
+#pragma clang fp contract(off)
     const float sxy = p.A[1] + p.A[3], sxz = p.A[2] + p.A[6], syz = p.A[5] + p.A[7];
 #pragma unroll
     for (int a = 0; a < 2; ++a)
@@ -333,6 +337,7 @@ __device__ __forceinline__ void lane_exp(const GaussParams& p, const LaneGeom& L
 }
 
 __device__ __forceinline__ float lane_e(const LaneExp& E, const LaneGeom& L, int a, int b, int c) {
+#pragma clang fp contract(off)
     return __builtin_amdgcn_exp2f(fmaf(E.Gxy[a][b], L.dz[c], E.Fxy[a][b] + E.Fz[c]));
 }
 
