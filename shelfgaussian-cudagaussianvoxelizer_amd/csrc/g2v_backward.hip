@@ -394,7 +394,30 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
     constexpr int kKc = BF ? kBtKcBf : kBtKc;   // channels per chunk
     // Lists longer than one pass: t_v = sum_c gF_vc F_vc straight from grid_feats.
     const bool multi = Ng > kBtPass;
-    if (multi) {
+    if (multi && VEC && !BF && !FU && gdt != kDtBF16 && ((uintptr_t)grid_feats & 15) == 0) {
+        // float rows of 16-byte multiples: the wave's 8 voxels at once, 8 lanes per row reading
+        // 16-byte pieces (many loads in flight), then a sum over the row's 8 lanes
+        const int r = wave * 8 + (lane >> 3), q = lane & 7;
+        const int v = sm.vlin[r];
+        float s = 0.0f;
+        if (v >= 0) {
+            const float4* a4 = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(gF) + (int64_t)v * C);
+            const float4* b4 = reinterpret_cast<const float4*>(static_cast<const float*>(grid_feats) + (int64_t)v * C);
+            const int n4 = C / 4;
+#pragma unroll 4
+            for (int c4 = q; c4 < n4; c4 += 8) {
+                const float4 x = a4[c4], y = b4[c4];
+                s = fmaf(x.x, y.x, s);
+                s = fmaf(x.y, y.y, s);
+                s = fmaf(x.z, y.z, s);
+                s = fmaf(x.w, y.w, s);
+            }
+        }
+        s += __shfl_xor(s, 1, 64);
+        s += __shfl_xor(s, 2, 64);
+        s += __shfl_xor(s, 4, 64);
+        if (q == 0 && v >= 0) sm.tv[r] = sm.D[r] >= kEps ? s : 0.0f;
+    } else if (multi) {
         for (int k = 0; k < 8; ++k) {
             const int r = wave * 8 + k;
             const int v = sm.vlin[r];
