@@ -394,19 +394,33 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
     constexpr int kKc = BF ? kBtKcBf : kBtKc;   // channels per chunk
     // Lists longer than one pass: t_v = sum_c gF_vc F_vc straight from grid_feats.
     const bool multi = Ng > kBtPass;
-    if (multi && VEC && !BF && !FU && gdt != kDtBF16 && ((uintptr_t)grid_feats & 15) == 0) {
+    if (multi && VEC && !BF && (FU || gdt != kDtBF16) && ((uintptr_t)grid_feats & 15) == 0) {
         // float rows of 16-byte multiples: the wave's 8 voxels at once, 8 lanes per row reading
-        // 16-byte pieces (many loads in flight), then a sum over the row's 8 lanes
+        // 16-byte pieces (many loads in flight), then a sum over the row's 8 lanes.  FU: G = k1
+        // target + k2 grid_feats formed per value, as the loss's own backward forms it.
         const int r = wave * 8 + (lane >> 3), q = lane & 7;
         const int v = sm.vlin[r];
         float s = 0.0f;
         if (v >= 0) {
-            const float4* a4 = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(gF) + (int64_t)v * C);
+            const float* arow = FU ? cg.tgt + (int64_t)v * C : reinterpret_cast<const float*>(gF) + (int64_t)v * C;
+            const float4* a4 = reinterpret_cast<const float4*>(arow);
             const float4* b4 = reinterpret_cast<const float4*>(static_cast<const float*>(grid_feats) + (int64_t)v * C);
             const int n4 = C / 4;
+            float k1 = 1.0f, k2 = 0.0f;
+            if constexpr (FU) {
+                k1 = sm.kc[0][r];
+                k2 = sm.kc[1][r];
+            }
 #pragma unroll 4
             for (int c4 = q; c4 < n4; c4 += 8) {
-                const float4 x = a4[c4], y = b4[c4];
+                float4 x = a4[c4];
+                const float4 y = b4[c4];
+                if constexpr (FU) {
+                    x.x = k1 * x.x + k2 * y.x;
+                    x.y = k1 * x.y + k2 * y.y;
+                    x.z = k1 * x.z + k2 * y.z;
+                    x.w = k1 * x.w + k2 * y.w;
+                }
                 s = fmaf(x.x, y.x, s);
                 s = fmaf(x.y, y.y, s);
                 s = fmaf(x.z, y.z, s);
