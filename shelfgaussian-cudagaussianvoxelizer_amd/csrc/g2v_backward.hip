@@ -1371,25 +1371,30 @@ __global__ void __launch_bounds__(kBrThreads, 1) k_bwd_region(
     const int KR = uniform(min(max(roff[R + 1], jr0), MR)) - jr0;
     if (KR <= 0) return;
 
-    if (threadIdx.x == 0) {
+    if (threadIdx.x < 64) {
+        // the region's tiles with a non-empty list, in slot order ((a, b) then z): lane s checks
+        // slot s (its list bounds loaded by all slots at once) and takes its place among the kept
+        // slots below it
         const int rnyz = RG.n[1] * RG.n[2];
         const int rx = R / rnyz, ry = (R - rx * rnyz) / RG.n[2], rz = R % RG.n[2];
         const int tpz = RG.cell[2] / kTile;
-        int k = 0;
-        for (int a = 0; a < 2; ++a)
-            for (int b = 0; b < 2; ++b)
-                for (int cz = 0; cz < tpz; ++cz) {
-                    const int tx = rx * 2 + a, ty = ry * 2 + b, tz = rz * tpz + cz;
-                    if (tx >= G.tiles[0] || ty >= G.tiles[1] || tz >= G.tiles[2]) continue;
-                    const int t = (tx * G.tiles[1] + ty) * G.tiles[2] + tz;
-                    if (min(max(toff[t + 1], 0), M) <= min(max(toff[t], 0), M)) continue;   // empty list
-                    sm.tl_s[k] = (a * 2 + b) * tpz + cz;
-                    sm.tl_org[k][0] = tx * kTile;
-                    sm.tl_org[k][1] = ty * kTile;
-                    sm.tl_org[k][2] = tz * kTile;
-                    ++k;
-                }
-        sm.ntl = k;
+        const int s = threadIdx.x;
+        const int ab = s / max(tpz, 1), cz = s - ab * tpz;
+        const int tx = rx * 2 + (ab >> 1), ty = ry * 2 + (ab & 1), tz = rz * tpz + cz;
+        bool keep = s < 4 * tpz && tx < G.tiles[0] && ty < G.tiles[1] && tz < G.tiles[2];
+        if (keep) {
+            const int t = (tx * G.tiles[1] + ty) * G.tiles[2] + tz;
+            keep = min(max(toff[t + 1], 0), M) > min(max(toff[t], 0), M);   // non-empty list
+        }
+        const unsigned long long kept = __ballot(keep);
+        if (keep) {
+            const int k = __popcll(kept & ((1ull << s) - 1ull));
+            sm.tl_s[k] = s;
+            sm.tl_org[k][0] = tx * kTile;
+            sm.tl_org[k][1] = ty * kTile;
+            sm.tl_org[k][2] = tz * kTile;
+        }
+        if (s == 0) sm.ntl = __popcll(kept);
     }
     __syncthreads();
     const int ntl = uniform(sm.ntl);
