@@ -474,13 +474,15 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
                 dacc[c] += __shfl_xor(dacc[c], 16);
                 dacc[c] += __shfl_xor(dacc[c], 32);
             }
-            if (lane < 16)
-                *reinterpret_cast<float4*>(&sm.dpart[wave][4 * lane]) = make_float4(dacc[0], dacc[1], dacc[2], dacc[3]);
+            int ln = lane;   // opaque, as in the epilogue below
+            asm volatile("" : "+v"(ln));
+            if (ln < 16)
+                *reinterpret_cast<float4*>(&sm.dpart[wave][4 * ln]) = make_float4(dacc[0], dacc[1], dacc[2], dacc[3]);
             __syncthreads();
             if (wave == 0) {
                 float D = 0.0f;
 #pragma unroll
-                for (int w = 0; w < kFwdWaves; ++w) D += sm.dpart[w][lane];
+                for (int w = 0; w < kFwdWaves; ++w) D += sm.dpart[w][ln];
                 sm.inv_den[lane] = 1.0f / fmaxf(D, kEps);
                 if (sm.vlin[lane] >= 0) density[sm.vlin[lane]] = D;
             }
@@ -498,11 +500,17 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
         // cw0 + 4*jl + cb for channel block cb
         if (has_ch) {
             const int c0 = cw0 + 4 * jl;
+            // the lane's row offset, opaque to the compiler: the LDS addresses below are then formed
+            // here, from one base and immediate offsets, instead of being hoisted out of the channel
+            // pass loop and kept in registers (which spilled, and each reload waited for every
+            // outstanding store)
+            int khr = 4 * kh;
+            asm volatile("" : "+v"(khr));
 #pragma unroll
             for (int vb = 0; vb < 2; ++vb) {
 #pragma unroll
                 for (int qd = 0; qd < 4; ++qd) {
-                    const int r0 = vb * 32 + 8 * qd + 4 * kh;
+                    const int r0 = vb * 32 + 8 * qd + khr;
                     const int4 vl = *reinterpret_cast<const int4*>(&sm.vlin[r0]);
                     const float4 iv = *reinterpret_cast<const float4*>(&sm.inv_den[r0]);
                     const int vs[4] = {vl.x, vl.y, vl.z, vl.w};
