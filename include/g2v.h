@@ -193,6 +193,62 @@ int g2v_build_t2g(int n, const float voxel_size[3], const float voxel_range[6],
                   int* runs_offsets, int* num_runs, void* workspace, size_t workspace_bytes,
                   void* stream);
 
+/* ---- batches of scenes on one grid -------------------------------------------------------------
+ * No counterpart in the reference, which takes one scene per call; ShelfGaussian batches B scenes
+ * (its recorded batch holds (1, 6, 300) Gaussians).  B scenes of n Gaussians each on one
+ * (voxel_size, voxel_range) grid run as one problem of B n Gaussians on B T tiles: one launch per
+ * kernel for the whole batch instead of one per scene.  Inputs are scene-major (B, n, ...) arrays,
+ * outputs (B, X, Y, Z) and (B, X, Y, Z, feat_dim); cov_inv, lb, ub and nvox are (B, n, ...) with the
+ * values of single-scene calls, and every per-scene output equals that of g2v_forward_plan /
+ * g2v_forward_splat / g2v_backward on the scene alone, bit for bit.
+ *
+ * g2v_batch_forward_plan: boxes, inverse covariances and the per-scene G->T row offsets
+ * g2t_offsets (B, n+1) of every scene, scene-local as g2v_forward_plan writes them; the batch's own
+ * offsets stay in plan_workspace (g2v_batch_plan_workspace bytes), which the caller keeps until the
+ * batch's backward.  counts (B + 1 long longs, device-accessible: device or pinned host memory)
+ * receives each scene's pair count M_b and, last, the batch's (region, Gaussian) pair count when
+ * want_backward != 0 (else 0).  Asynchronous: the caller waits once for the whole batch.
+ *
+ * g2v_batch_forward_splat: the splat of the batch, num_pairs = sum of M_b.  g2t_tile_ids (num_pairs,
+ * optional) receives the scene-local tile ids of scene 0's pairs, then scene 1's, ...; density and
+ * grid_feats are written completely; t2g_tiles, t2g_gauss (num_pairs) and t2g_offsets (B T + 1),
+ * when all non-NULL, receive the batch's Tile->Gaussian CSR (batch tile ids b T + t, batch
+ * Gaussian ids b n + g) for the backward.
+ *
+ * g2v_batch_backward_prepare / g2v_batch_backward: g2v_backward_prepare and g2v_backward
+ * (prepared != 0: as g2v_backward_prepared) for the batch, with num_pairs and num_region_pairs the
+ * batch's totals, plan_workspace the batch plan's (planned with want_backward != 0 when
+ * feat_dim > 0) and the batch's Tile->Gaussian CSR from g2v_batch_forward_splat (optional without
+ * prepared: rebuilt from the boxes).  Gradients are (B, n, ...).  Asynchronous. */
+size_t g2v_batch_plan_workspace(int num_scenes, int n);
+int g2v_batch_forward_plan(int num_scenes, int n, const float* means3D, const float* covariances,
+                           const float voxel_size[3], const float voxel_range[6], float* cov_inv, int* valid_voxel_lb,
+                           int* valid_voxel_ub, int* num_voxels_per_gaussian, int* g2t_offsets, void* plan_workspace,
+                           size_t plan_workspace_bytes, int want_backward, long long* counts, void* stream);
+size_t g2v_batch_forward_splat_workspace(int num_scenes, int n, int feat_dim, long long num_pairs,
+                                         const float voxel_size[3], const float voxel_range[6]);
+int g2v_batch_forward_splat(int num_scenes, int n, int feat_dim, const float* means3D, const float* opacity,
+                            const void* features, int feat_dtype, const float voxel_size[3],
+                            const float voxel_range[6], const float* cov_inv, const int* valid_voxel_lb,
+                            const int* valid_voxel_ub, const void* plan_workspace, size_t plan_workspace_bytes,
+                            long long num_pairs, int* g2t_tile_ids, float* density, void* grid_feats, int* t2g_tiles,
+                            int* t2g_gauss, int* t2g_offsets, void* workspace, size_t workspace_bytes, void* stream);
+size_t g2v_batch_backward_workspace(int num_scenes, int n, int feat_dim, long long num_pairs,
+                                    long long num_region_pairs, const float voxel_size[3], const float voxel_range[6]);
+int g2v_batch_backward_prepare(int num_scenes, int n, int feat_dim, const float voxel_size[3],
+                               const float voxel_range[6], const int* valid_voxel_lb, const int* valid_voxel_ub,
+                               const void* features, int feat_dtype, long long num_pairs, long long num_region_pairs,
+                               const int* t2g_tiles, const int* t2g_gauss, const void* plan_workspace,
+                               size_t plan_workspace_bytes, void* workspace, size_t workspace_bytes, void* stream);
+int g2v_batch_backward(int num_scenes, int n, int feat_dim, const float* grad_density, const void* grad_feats,
+                       const float* means3D, const float* opacity, const float* cov_inv, const float voxel_size[3],
+                       const float voxel_range[6], const int* valid_voxel_lb, const int* valid_voxel_ub,
+                       long long num_pairs, long long num_region_pairs, const float* density, const void* grid_feats,
+                       const void* features, int feat_dtype, float* grad_means, float* grad_cov, float* grad_opacity,
+                       void* grad_features, const int* t2g_tiles, const int* t2g_gauss, const int* t2g_offsets,
+                       const void* plan_workspace, size_t plan_workspace_bytes, void* workspace,
+                       size_t workspace_bytes, int prepared, void* stream);
+
 /* ---- feature cosine loss --------------------------------------------------------------------
  * Replaces CudaFeatsCosinelossForward / CudaFeatsCosinelossBackward (src/cuda_feats_loss.cu:154-231
  * and :311-366, bound at src/bindings.cpp:67-104).  Over num_voxels = X*Y*Z voxels with

@@ -387,57 +387,34 @@ def _backward(grad_output, grad_feats_output, means3D, opacity, cov_inv, voxel_s
 _COUNTS = {}
 
 
-_SIDE_STREAMS = {}
-
-
-def _side_streams(dev, k):
-    """k side streams of the device (created once, default priority) for the scenes of a batch."""
-    lst = _SIDE_STREAMS.setdefault(dev.index, [])
-    while len(lst) < k:
-        lst.append(torch.cuda.Stream(device=dev))
-    return lst[:k]
-
-
-# scenes of one batch run on up to this many streams at once (their CSR kernels and their sparse
-# phases leave most of the chip idle)
-_BATCH_STREAMS = 4
-
-
-def _join(cur, streams):
-    """Makes cur wait for all the work queued so far on streams."""
-    for st in streams:
-        e = torch.cuda.Event()
-        e.record(st)
-        cur.wait_event(e)
-
-
-def _pinned_counts(dev, B):
-    """A reusable pinned (B, 2) int64 host buffer per device and thread (count read-back)."""
+def _pinned_counts(dev, k):
+    """A reusable pinned (k,) int64 host buffer per device and thread (count read-back)."""
     import threading
     key = (dev.index, threading.get_ident())
     buf = _COUNTS.get(key)
-    if buf is None or buf.shape[0] < B:
-        buf = torch.empty(max(B, 8), 2, dtype=torch.int64, pin_memory=True)
+    if buf is None or buf.numel() < k:
+        buf = torch.empty(max(k, 16), dtype=torch.int64, pin_memory=True)
         _COUNTS[key] = buf
-    return buf[:B]
+    return buf[:k]
 
 
 def gaussian_voxelizer_forward_batched(means3D, opacity, covariances, voxel_size, voxel_range, features=None):
     """Forward of B scenes on one grid in one call: means3D (B,N,3), opacity (B,N) or (B,N,1),
     covariances (B,N,9) or (B,N,3,3), features (B,N,C) or None.
 
-    Every scene is planned before the host waits once for all their pair counts (one scene per
-    call would wait B times); then every scene is splatted.  Returns a list of B 9-tuples laid out
-    as gaussian_voxelizer_forward's; the density and grid_feats of scene b are the views [b] of one
-    (B,X,Y,Z) and one (B,X,Y,Z,C) tensor, and the time in every tuple is that of the whole batch.
+    The B scenes run as one problem of B N Gaussians (one launch per kernel for the whole batch,
+    one host wait for its pair counts).  Returns a list of B 9-tuples laid out as
+    gaussian_voxelizer_forward's, each equal to that of the scene alone; the density and
+    grid_feats of scene b are the views [b] of one (B,X,Y,Z) and one (B,X,Y,Z,C) tensor, and the
+    time in every tuple is that of the whole batch.
     """
-    return [r[0] for r in _forward_batched(means3D, opacity, covariances, voxel_size, voxel_range, features,
-                                           keep_t2g=False)[0]]
+    return _forward_batched(means3D, opacity, covariances, voxel_size, voxel_range, features, keep_t2g=False)[0]
 
 
 def _forward_batched(means3D, opacity, covariances, voxel_size, voxel_range, features, keep_t2g):
-    """Batched forward.  Returns ([(9-tuple, t2g) per scene], density (B,X,Y,Z), grid_feats
-    (B,X,Y,Z,C)); t2g as _forward(keep_t2g=True) returns it, or None."""
+    """Batched forward.  Returns ([9-tuple per scene], density (B,X,Y,Z), grid_feats (B,X,Y,Z,C),
+    batch) where batch holds what _backward_batched needs (the batch plan, the batch's
+    Tile->Gaussian CSR, the prepared backward workspace) with keep_t2g, else None."""
     lib = _lib.load()
     means = _f32_input(means3D, "means3D")
     if means.dim() != 3 or means.shape[2] != 3:
@@ -460,6 +437,10 @@ def _forward_batched(means3D, opacity, covariances, voxel_size, voxel_range, fea
     vs, vr = _lib.floats(vs_h), _lib.floats(vr_h)
     (X, Y, Z), (Tx, Ty, Tz) = grid_dims(vs_h, vr_h)
     T = Tx * Ty * Tz
+    if B == 0:
+        f32 = dict(dtype=torch.float32, device=dev)
+        return [], torch.empty(0, X, Y, Z, **f32), torch.empty(0, X, Y, Z, C, dtype=torch.float32 if feats is None
+                                                                 else feats.dtype, device=dev), None
 
     with _OnDevice(dev):
         cur = torch.cuda.current_stream(dev)
@@ -471,141 +452,101 @@ def _forward_batched(means3D, opacity, covariances, voxel_size, voxel_range, fea
         ub = torch.empty(B, n, 3, **i32)
         nvox = torch.empty(B, n, **i32)
         g2t_offsets = torch.empty(B, n + 1, **i32)
-        pws = lib.g2v_forward_plan_workspace(n)
-        ws = torch.empty(B, (pws + 255) // 256 * 256, dtype=torch.uint8, device=dev)   # rows 256-byte aligned
-        bws = max(1, lib.g2v_backward_plan_workspace(n)) if keep_t2g else 0
-        bplan = torch.empty(B, (bws + 255) // 256 * 256, dtype=torch.uint8, device=dev) if keep_t2g else None
-        counts_dev = torch.empty(B, 2, dtype=torch.int64, device=dev)
+        pws = lib.g2v_batch_plan_workspace(B, n)
+        if pws == 0:
+            raise RuntimeError(f"batch of {B} scenes x {n} Gaussians exceeds the int32 Gaussian index")
+        plan = torch.empty(pws, dtype=torch.uint8, device=dev)
+        counts_dev = torch.empty(B + 1, dtype=torch.int64, device=dev)
+        # outputs whose size does not depend on the plan's counts, allocated before its host wait
         density = torch.empty(B, X, Y, Z, **f32)
         fdtype = torch.float32 if feats is None else feats.dtype
         fdt = _FEAT_DTYPES[fdtype]
         grid_feats = torch.empty(B, X, Y, Z, C, dtype=fdtype, device=dev)
         start, stop = _timing_events(dev)
         start.record(cur)
-        for b in range(B):
-            _lib.check(lib.g2v_forward_plan_async(n, _ptr(means[b]), _ptr(cov[b]), vs, vr, _ptr(cov_inv[b]),
-                                                  _ptr(lb[b]), _ptr(ub[b]), _ptr(nvox[b]), _ptr(g2t_offsets[b]),
-                                                  _ptr(ws[b]), pws, None if bplan is None else _ptr(bplan[b]),
-                                                  bws, _ptr(counts_dev[b]), stream),
-                       "gaussian_voxelizer_forward_batched (plan)")
-        counts = _pinned_counts(dev, B)
+        # the (region, Gaussian) pair count of the backward rides on the same launches and wait
+        want_bwd = 1 if (keep_t2g and C > 0) else 0
+        _lib.check(lib.g2v_batch_forward_plan(B, n, _ptr(means), _ptr(cov), vs, vr, _ptr(cov_inv), _ptr(lb), _ptr(ub),
+                                              _ptr(nvox), _ptr(g2t_offsets), _ptr(plan), pws, want_bwd,
+                                              _ptr(counts_dev), stream),
+                   "gaussian_voxelizer_forward_batched (plan)")
+        counts = _pinned_counts(dev, B + 1)
         counts.copy_(counts_dev, non_blocking=True)
         cur.synchronize()   # the one host wait of the batch
         cnt = counts.tolist()
-        results = []
-        # scene b's splat (and backward preparation) runs on side stream b % K, after the plan; every
-        # tensor allocated here on cur and used there is recorded on that stream, and cur waits for
-        # all of them before the stop event
-        sides = _side_streams(dev, min(B, _BATCH_STREAMS)) if B > 1 else [cur]
-        ready = torch.cuda.Event()
-        ready.record(cur)
-        for st in sides:
-            if st is not cur:
-                st.wait_event(ready)
-        for b in range(B):
-            side = sides[b % len(sides)]
-            sstream = ctypes.c_void_p(side.cuda_stream)
-            M, MR = int(cnt[b][0]), int(cnt[b][1])
-            if M > 2147483647 or MR > 2147483647:
-                raise RuntimeError(f"scene {b}: pair counts {M}, {MR} exceed the int32 CSR")
-            g2t_tile_ids = torch.empty(M, **i32)
-            ws2 = torch.empty(lib.g2v_forward_splat_workspace(n, C, M, vs, vr), dtype=torch.uint8, device=dev)
-            t2g = None
-            csr = (None, None, None)
-            if keep_t2g:
-                csr = (torch.empty(M, **i32), torch.empty(M, **i32), torch.empty(T + 1, **i32))
-                t2g = dict(csr=csr, plan=bplan[b], num_region_pairs=MR, vs=vs, vr=vr, dims=(X, Y, Z))
-            fb = None if feats is None else feats[b]
-            _lib.check(lib.g2v_forward_splat(n, C, _ptr(means[b]), _ptr(op[b]), _ptr(fb), fdt, vs, vr,
-                                             _ptr(cov_inv[b]), _ptr(lb[b]), _ptr(ub[b]), _ptr(g2t_offsets[b]), M,
-                                             _ptr(g2t_tile_ids), _ptr(density[b]), _ptr(grid_feats[b]),
-                                             _ptr(csr[0]), _ptr(csr[1]), _ptr(csr[2]), _ptr(ws2), ws2.numel(),
-                                             sstream),
-                       "gaussian_voxelizer_forward_batched (splat)")
-            if side is not cur:
-                for t in (g2t_tile_ids, ws2) + tuple(t for t in csr if t is not None):
-                    t.record_stream(side)
-            if t2g is not None:
-                t2g["stream"] = side
-            results.append([[density[b], cov_inv[b], lb[b], ub[b], nvox[b], grid_feats[b], g2t_offsets[b],
-                             g2t_tile_ids, 0.0], t2g])
-        _join(cur, [st for st in sides if st is not cur])
+        Ms, MR = [int(v) for v in cnt[:B]], int(cnt[B])
+        M = sum(Ms)
+        if M > 2147483647 or MR > 2147483647:
+            raise RuntimeError(f"batch pair counts {M}, {MR} exceed the int32 CSR")
+        g2t_tile_ids = torch.empty(M, **i32)
+        ws = torch.empty(lib.g2v_batch_forward_splat_workspace(B, n, C, M, vs, vr), dtype=torch.uint8, device=dev)
+        csr = (torch.empty(M, **i32), torch.empty(M, **i32), torch.empty(B * T + 1, **i32)) if keep_t2g \
+            else (None, None, None)
+        _lib.check(lib.g2v_batch_forward_splat(B, n, C, _ptr(means), _ptr(op), _ptr(feats), fdt, vs, vr, _ptr(cov_inv),
+                                               _ptr(lb), _ptr(ub), _ptr(plan), pws, M, _ptr(g2t_tile_ids),
+                                               _ptr(density), _ptr(grid_feats), _ptr(csr[0]), _ptr(csr[1]),
+                                               _ptr(csr[2]), _ptr(ws), ws.numel(), stream),
+                   "gaussian_voxelizer_forward_batched (splat)")
         stop.record(cur)
+        batch = None
         if keep_t2g:
-            for b, (r, t2g) in enumerate(results):
-                M = r[7].numel()
-                side = t2g["stream"]
-                t2g["grads"] = (torch.empty(n, 3, **f32), torch.empty(n, 9, **f32), torch.empty(n, **f32),
-                                torch.empty(n, C, dtype=fdtype, device=dev))
-                t2g["ws"] = torch.empty(max(1, lib.g2v_backward_workspace(n, C, M, t2g["num_region_pairs"], vs, vr)),
-                                        dtype=torch.uint8, device=dev)
-                if side is not cur:
-                    # everything the preparation below reads or writes on the side stream: it is
-                    # queued after the join, so nothing on cur waits for it, and lb/ub/bplan/feats
-                    # (feats possibly a temporary copy) may be freed on cur before it runs
-                    used_by_prep = t2g["grads"] + (t2g["ws"], lb, ub, bplan) + (() if feats is None else (feats,))
-                    for t in used_by_prep:
-                        t.record_stream(side)
-                if C > 0:
-                    _lib.check(lib.g2v_backward_prepare(n, C, vs, vr, _ptr(lb[b]), _ptr(ub[b]), _ptr(feats[b]), fdt, M,
-                                                        t2g["num_region_pairs"], _ptr(t2g["csr"][0]),
-                                                        _ptr(t2g["csr"][1]), _ptr(t2g["plan"]), _ptr(t2g["ws"]),
-                                                        t2g["ws"].numel(), ctypes.c_void_p(side.cuda_stream)),
-                               "gaussian_voxelizer_forward_batched (backward preparation)")
-                    t2g["prepared"] = True
-                # the backward of this scene starts after its preparation
-                t2g["ready"] = torch.cuda.Event()
-                t2g["ready"].record(side)
+            # the backward's outputs and workspace, and its gradient-independent kernels queued
+            # behind the forward (after its stop event), as for one scene
+            batch = dict(B=B, n=n, C=C, fdt=fdt, M=M, MR=MR, vs=vs, vr=vr, plan=plan, csr=csr, cov_inv=cov_inv,
+                         lb=lb, ub=ub, density=density, grid_feats=grid_feats, prepared=False)
+            batch["grads"] = (torch.empty(B, n, 3, **f32), torch.empty(B, n, 9, **f32), torch.empty(B, n, **f32),
+                              torch.empty(B, n, C, dtype=fdtype, device=dev))
+            batch["ws"] = torch.empty(max(1, lib.g2v_batch_backward_workspace(B, n, C, M, MR, vs, vr)),
+                                      dtype=torch.uint8, device=dev)
+            if C > 0:
+                _lib.check(lib.g2v_batch_backward_prepare(B, n, C, vs, vr, _ptr(lb), _ptr(ub), _ptr(feats), fdt, M, MR,
+                                                          _ptr(csr[0]), _ptr(csr[1]), _ptr(plan), pws,
+                                                          _ptr(batch["ws"]), batch["ws"].numel(), stream),
+                           "gaussian_voxelizer_forward_batched (backward preparation)")
+                batch["prepared"] = True
         stop.synchronize()
         fwd_sec = start.elapsed_time(stop) / 1000.0
-    out = []
-    for r, t2g in results:
-        r[8] = fwd_sec
-        out.append((tuple(r), t2g))
-    return out, density, grid_feats
+    out, off = [], 0
+    for b in range(B):
+        out.append((density[b], cov_inv[b], lb[b], ub[b], nvox[b], grid_feats[b], g2t_offsets[b],
+                    g2t_tile_ids[off:off + Ms[b]], fwd_sec))
+        off += Ms[b]
+    return out, density, grid_feats, batch
 
 
-def _backward_batched(grad_density, grad_feats, means, opacity, features, scenes, voxel_size=None, voxel_range=None):
-    """Backward of _forward_batched: grad_density (B,X,Y,Z), grad_feats (B,X,Y,Z,C); scenes = its
-    per-scene (9-tuple, t2g) list (t2g None when the forward kept nothing: each scene's backward
-    then rebuilds its CSR and plan, on the grid of voxel_size and voxel_range).  Returns stacked
-    gradients (B,N,3), (B,N,9), (B,N), (B,N,C) and the time of the whole batch."""
+def _backward_batched(grad_density, grad_feats, means, opacity, features, batch):
+    """Backward of _forward_batched(keep_t2g=True): grad_density (B,X,Y,Z), grad_feats (B,X,Y,Z,C)
+    (or None: zero); batch = its fourth result.  One g2v_batch_backward call for the B scenes.
+    Returns the gradients (B,N,3), (B,N,9), (B,N), (B,N,C) and the time of the batch."""
+    lib = _lib.load()
     dev = means.device
-    B = len(scenes)
+    B, n, C, fdt = batch["B"], batch["n"], batch["C"], batch["fdt"]
+    gD = _f32_input(grad_density, "grad_density", tuple(batch["density"].shape))
+    gF = None
+    if C > 0:
+        gfeat = batch["grid_feats"]
+        gF = grad_feats if grad_feats is not None and grad_feats.shape[-1] > 0 else torch.zeros_like(gfeat)
+        if tuple(gF.shape) != tuple(gfeat.shape):
+            raise RuntimeError(f"grad_feats_output must be {tuple(gfeat.shape)}, got {tuple(gF.shape)}")
+        gF = gF.to(gfeat.dtype).contiguous()
+    gm, gc, go, gf = batch["grads"]
+    csr, plan = batch["csr"], batch["plan"]
     with _OnDevice(dev):
         cur = torch.cuda.current_stream(dev)
         start, stop = _timing_events(dev)
         start.record(cur)
-        grads = []
-        keep = []   # tensors made here on cur and used on a side stream, alive until the join
-        # scene b runs on the side stream of its forward, after the upstream gradients (cur) and its
-        # backward preparation
-        ready = torch.cuda.Event()
-        ready.record(cur)
-        used = []
-        for b, (r, t2g) in enumerate(scenes):
-            (density, cov_inv, lb, ub, nvox, gfeat, g2t_offsets, g2t_tile_ids, _) = r
-            fb = None if features is None else features[b]
-            gF = grad_feats[b] if grad_feats is not None and grad_feats.shape[-1] > 0 else gfeat.new_zeros(gfeat.shape)
-            keep.append(gF)
-            side = (t2g or {}).get("stream", cur)
-            if side is not cur:
-                side.wait_event(ready)
-                if t2g.get("ready") is not None:
-                    side.wait_event(t2g["ready"])
-                if side not in used:
-                    used.append(side)
-            with torch.cuda.stream(side):
-                grads.append(_backward(grad_density[b], gF, means[b], opacity[b], cov_inv, voxel_size, voxel_range, lb,
-                                       ub, nvox, g2t_offsets, g2t_tile_ids, density, gfeat, fb, t2g=t2g, timed=False))
-        _join(cur, used)
+        _lib.check(lib.g2v_batch_backward(B, n, C, _ptr(gD), _ptr(gF), _ptr(means), _ptr(opacity), _ptr(batch["cov_inv"]),
+                                          batch["vs"], batch["vr"], _ptr(batch["lb"]), _ptr(batch["ub"]), batch["M"],
+                                          batch["MR"], _ptr(batch["density"]), _ptr(batch["grid_feats"]),
+                                          _ptr(features), fdt, _ptr(gm), _ptr(gc), _ptr(go), _ptr(gf), _ptr(csr[0]),
+                                          _ptr(csr[1]), _ptr(csr[2]), _ptr(plan), plan.numel(), _ptr(batch["ws"]),
+                                          batch["ws"].numel(), 1 if batch["prepared"] else 0,
+                                          ctypes.c_void_p(cur.cuda_stream)),
+                   "gaussian_voxelizer_backward (batched)")
         stop.record(cur)
         stop.synchronize()
         bwd_sec = start.elapsed_time(stop) / 1000.0
-    return (torch.stack([g[0] for g in grads]) if B else means.new_zeros(0, 0, 3),
-            torch.stack([g[1] for g in grads]) if B else means.new_zeros(0, 0, 9),
-            torch.stack([g[2] for g in grads]) if B else means.new_zeros(0, 0),
-            torch.stack([g[3] for g in grads]) if B else means.new_zeros(0, 0, 0), bwd_sec)
+    return gm, gc, go, gf, bwd_sec
 
 
 def build_t2g(voxel_size, voxel_range, valid_voxel_lb, valid_voxel_ub, g2t_offsets, g2t_tile_ids):

@@ -177,33 +177,43 @@ class _CudaGaussianVoxelizeCosineLossFunction(torch.autograd.Function):
 
 
 class _CudaGaussianVoxelizeBatchedFunction(torch.autograd.Function):
-    """Autograd wrapper of B scenes on one grid (means3D (B,N,3)): one host wait for the whole
-    batch's plan, per-scene CSR; returns density (B,X,Y,Z), grid_feats (B,X,Y,Z,C) and stats."""
+    """Autograd wrapper of B scenes on one grid (means3D (B,N,3)), run as one problem of B N
+    Gaussians (one launch per kernel for the batch, one host wait for its plan); returns density
+    (B,X,Y,Z), grid_feats (B,X,Y,Z,C) and stats."""
 
     @staticmethod
     def forward(ctx, means3D, opacity, covariances, voxel_size, voxel_range, features, need_backward=None):
-        scenes, density, grid_feats = _C._forward_batched(means3D, opacity, covariances, voxel_size, voxel_range,
-                                                          features, keep_t2g=_wants_backward(ctx, need_backward))
+        scenes, density, grid_feats, batch = _C._forward_batched(means3D, opacity, covariances, voxel_size,
+                                                                 voxel_range, features,
+                                                                 keep_t2g=_wants_backward(ctx, need_backward))
         stats = torch.zeros(2, dtype=torch.float32, device="cpu")
-        stats[0] = scenes[0][0][8] if scenes else 0.0
-        ctx.scenes = scenes
+        stats[0] = scenes[0][8] if scenes else 0.0
+        ctx.batch = batch
         ctx.grid = (voxel_size, voxel_range)
-        ctx.save_for_backward(means3D, opacity, features, stats)
+        ctx.save_for_backward(means3D, opacity, covariances, features, stats)
         ctx.mark_non_differentiable(stats)
         ctx.shapes = (means3D.shape, opacity.shape, covariances.shape)
         return density, grid_feats, stats
 
     @staticmethod
     def backward(ctx, grad_density_output, grad_feats_output, grad_stats):
-        means3D, opacity, features, stats = ctx.saved_tensors
+        means3D, opacity, covariances, features, stats = ctx.saved_tensors
         B, n = means3D.shape[0], means3D.shape[1]
-        gD = grad_density_output.to(torch.float32).contiguous()
-        gF = grad_feats_output.to(torch.float32 if features is None else features.dtype).contiguous()
         m32 = means3D.detach().contiguous()
         o32 = opacity.detach().reshape(B, n).contiguous()
         feats = None if features is None else features.detach().contiguous()
-        gm, gc, go, gf, bwd_sec = _C._backward_batched(gD, gF, m32, o32, feats, ctx.scenes, *ctx.grid)
-        ctx.scenes = None
+        batch = ctx.batch
+        if batch is None:   # the forward kept nothing for a backward (need_backward=False): redo its plan
+            batch = _C._forward_batched(m32, o32, covariances.detach(), *ctx.grid, feats, keep_t2g=True)[3]
+        if B == 0:
+            gm, gc, go = m32.new_zeros(0, n, 3), m32.new_zeros(0, n, 9), m32.new_zeros(0, n)
+            gf = None if feats is None else feats.new_zeros(feats.shape)
+            bwd_sec = 0.0
+        else:
+            gD = grad_density_output.to(torch.float32).contiguous()
+            gF = grad_feats_output.to(torch.float32 if features is None else features.dtype).contiguous()
+            gm, gc, go, gf, bwd_sec = _C._backward_batched(gD, gF, m32, o32, feats, batch)
+        ctx.batch = None
         stats[1] = bwd_sec
         return (gm.reshape(ctx.shapes[0]), go.reshape(ctx.shapes[1]), gc.reshape(ctx.shapes[2]), None, None,
                 gf if features is not None else None, None)

@@ -13,7 +13,7 @@ LIB_PATH = os.path.join(_HERE, LIB_NAME)
 
 G2V_OK = 0
 # the ABI that SIGNATURES describes (g2v_abi_version() of a matching build)
-ABI_VERSION = 10
+ABI_VERSION = 11
 G2V_DTYPE_F32 = 0
 G2V_DTYPE_BF16 = 1
 _ERRORS = {1: "invalid argument", 2: "HIP runtime error", 3: "size limit exceeded"}
@@ -48,6 +48,16 @@ SIGNATURES = {
     "g2v_t2g_workspace": (_sz, [_i, _ll, _f3, _f3]),
     "g2v_build_t2g": (_i, [_i, _f3, _f3, _vp, _vp, _vp, _vp, _ll, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                            _vp, _sz, _vp]),
+    "g2v_batch_plan_workspace": (_sz, [_i, _i]),
+    "g2v_batch_forward_plan": (_i, [_i, _i, _vp, _vp, _f3, _f3, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _vp, _vp]),
+    "g2v_batch_forward_splat_workspace": (_sz, [_i, _i, _i, _ll, _f3, _f3]),
+    "g2v_batch_forward_splat": (_i, [_i, _i, _i, _vp, _vp, _vp, _i, _f3, _f3, _vp, _vp, _vp, _vp, _sz, _ll, _vp,
+                                     _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "g2v_batch_backward_workspace": (_sz, [_i, _i, _i, _ll, _ll, _f3, _f3]),
+    "g2v_batch_backward_prepare": (_i, [_i, _i, _i, _f3, _f3, _vp, _vp, _vp, _i, _ll, _ll, _vp, _vp, _vp, _sz, _vp,
+                                        _sz, _vp]),
+    "g2v_batch_backward": (_i, [_i, _i, _i, _vp, _vp, _vp, _vp, _vp, _f3, _f3, _vp, _vp, _ll, _ll, _vp, _vp, _vp,
+                                _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _sz, _i, _vp]),
     "g2v_cosine_loss_workspace": (_sz, [_ll, _i]),
     "g2v_cosine_loss_forward": (_i, [_ll, _i, _vp, _vp, _vp, _vp, _i, _vp, _vp, _ip, _vp, _sz, _vp]),
     "g2v_cosine_loss_forward_coef": (_i, [_ll, _i, _vp, _vp, _vp, _vp, _i, _vp, _vp, _ip, _vp, _vp, _sz, _vp]),

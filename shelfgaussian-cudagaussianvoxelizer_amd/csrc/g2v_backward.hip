@@ -89,6 +89,7 @@ __global__ void __launch_bounds__(256) k_bwd_density(Grid G, int n, const float*
     const int lane = threadIdx.x & 63;
     const int g = uniform(blockIdx.x * 4 + (threadIdx.x >> 6));
     if (g >= n) return;
+    gD += scene_of(G, g) * scene_voxels(G);   // the scene's voxels
     GaussParams p;
     load_params(p, g, means, cov_inv, opacity, lb, ub);
     const int ex = p.ub[0] - p.lb[0] + 1, ey = p.ub[1] - p.lb[1] + 1, ez = p.ub[2] - p.lb[2] + 1;
@@ -357,12 +358,25 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
     float* __restrict__ pair_partials, __bf16* __restrict__ wt, CosG cg) {
     static_assert(!FU || (VEC && !BF), "the fused cosine gradient takes 16-byte float32 rows");
     __shared__ BtSmem<FU> sm;
-    const int T = G.tiles[0] * G.tiles[1] * G.tiles[2];
-    const int tile = uniform(xcd_remap(blockIdx.x, gridDim.x));
-    if (tile >= T) return;
-    const int j0 = uniform(min(max(toff[tile], 0), M));
-    const int Ng = uniform(min(max(toff[tile + 1], j0), M)) - j0;
+    const int T = scene_tiles(G);
+    // tb: the batch's tile (its list), tile: the scene's
+    const int tb = uniform(xcd_remap(blockIdx.x, gridDim.x));
+    if (tb >= T * G.scenes) return;
+    const int j0 = uniform(min(max(toff[tb], 0), M));
+    const int Ng = uniform(min(max(toff[tb + 1], j0), M)) - j0;
     if (Ng <= 0) return;
+    const int scene = uniform(tb / T), tile = tb - scene * T;
+    if (scene > 0) {   // the scene's voxel rows
+        const int64_t vb = scene * scene_voxels(G);
+        gD += vb;
+        density += vb;
+        gF_ = static_cast<const char*>(gF_) + vb * C * (BF ? 2 : 4);
+        grid_feats = static_cast<const char*>(grid_feats) + vb * C * (gdt == kDtBF16 ? 2 : 4);
+        if constexpr (FU) {
+            cg.tgt += vb * C;
+            cg.coef += 2 * vb;
+        }
+    }
     const int lane = threadIdx.x & 63, wave = uniform(threadIdx.x >> 6);
     const int mb = wave >> 2, ngrp = wave & 3;   // voxel block (epilogues) / k half (K loop), N group
     const int tyz = G.tiles[1] * G.tiles[2];
@@ -985,11 +999,13 @@ __global__ void __launch_bounds__(256) k_region_table(Grid G, Regions RG, int M,
                                                       int* __restrict__ table) {
     const int j = blockIdx.x * 256 + threadIdx.x;
     if (j >= M) return;
-    const int t = sorted_tiles[j], g = sorted_gauss[j];
+    const int tb = sorted_tiles[j], g = sorted_gauss[j];   // the batch's tile
+    const int T = scene_tiles(G);
+    const int scene = tb / T, t = tb - scene * T;
     const int tyz = G.tiles[1] * G.tiles[2];
     const int tx = t / tyz, ty = (t - tx * tyz) / G.tiles[2], tz = t % G.tiles[2];
     const int tpz = RG.cell[2] / kTile;
-    const int R = ((tx >> 1) * RG.n[1] + (ty >> 1)) * RG.n[2] + tz / tpz;
+    const int R = scene * RG.total + ((tx >> 1) * RG.n[1] + (ty >> 1)) * RG.n[2] + tz / tpz;   // the batch's region
     const int slot = ((tx & 1) * 2 + (ty & 1)) * tpz + tz % tpz;
     const int a = min(max(roff[R], 0), MR);
     const int b = min(max(roff[R + 1], a), MR);
@@ -1363,13 +1379,24 @@ __global__ void __launch_bounds__(kBrThreads, 1) k_bwd_region(
     static_assert(!FU || !GB, "the fused cosine gradient takes float32 rows");
     __shared__ BrSmem<FU> sm;
     const int idx = xcd_remap(blockIdx.x, gridDim.x);
-    const int R = uniform(idx / nchunk);
-    const int chunk = uniform(idx - R * nchunk);
-    if (R >= RG.total) return;
+    const int Rb = uniform(idx / nchunk);   // the batch's region (its list)
+    const int chunk = uniform(idx - Rb * nchunk);
+    if (Rb >= RG.total * G.scenes) return;
     const int c0 = chunk * kBrCc;
-    const int jr0 = uniform(min(max(roff[R], 0), MR));
-    const int KR = uniform(min(max(roff[R + 1], jr0), MR)) - jr0;
+    const int jr0 = uniform(min(max(roff[Rb], 0), MR));
+    const int KR = uniform(min(max(roff[Rb + 1], jr0), MR)) - jr0;
     if (KR <= 0) return;
+    const int scene = uniform(Rb / RG.total), R = Rb - scene * RG.total;   // R: the scene's region
+    const int tbase = scene * scene_tiles(G);                               // its first tile in the batch
+    if (scene > 0) {   // the scene's voxel rows
+        const int64_t vb = scene * scene_voxels(G);
+        gF = static_cast<const char*>(gF) + vb * C * (GB ? 2 : 4);
+        if constexpr (FU) {
+            grid_feats = static_cast<const float*>(grid_feats) + vb * C;
+            cg.tgt += vb * C;
+            cg.coef += 2 * vb;
+        }
+    }
 
     if (threadIdx.x < 64) {
         // the region's tiles with a non-empty list, in slot order ((a, b) then z): lane s checks
@@ -1384,7 +1411,7 @@ __global__ void __launch_bounds__(kBrThreads, 1) k_bwd_region(
         bool keep = s < 4 * tpz && tx < G.tiles[0] && ty < G.tiles[1] && tz < G.tiles[2];
         if (keep) {
             const int t = (tx * G.tiles[1] + ty) * G.tiles[2] + tz;
-            keep = min(max(toff[t + 1], 0), M) > min(max(toff[t], 0), M);   // non-empty list
+            keep = min(max(toff[tbase + t + 1], 0), M) > min(max(toff[tbase + t], 0), M);   // non-empty list
         }
         const unsigned long long kept = __ballot(keep);
         if (keep) {
@@ -1617,8 +1644,9 @@ static FeatBufs carve_feats(void* ws, const Grid& G, int n, int C, int64_t M, in
     b.r_pairs_sorted = c.take<int>(mr);
     b.r_gids = c.take<int>(mr);
     b.table = c.take<int>(mr * kBrSlots);
-    b.roff = c.take<int>(RG.total + 1);
-    b.sort_ws = c.take<char>(sort_workspace(MR, RG.total));
+    const int nreg = RG.total * G.scenes;   // regions of the batch
+    b.roff = c.take<int>(nreg + 1);
+    b.sort_ws = c.take<char>(sort_workspace(MR, nreg));
     b.gpart = c.take<float>(mr * (C > 0 ? C : 1));
     b.bytes = c.off + 256;
     return b;
@@ -1650,13 +1678,15 @@ hipError_t launch_backward_prepare(const Grid& G, int n, int C, const void* feat
                    static_cast<const float*>(features), n, C, nchk, b.fsp);
     // Region -> Gaussian CSR (pairs carry their G->R slot so partial rows land Gaussian-major) and
     // the row table of phase B
+    const int nreg = RG.total * G.scenes;   // regions of the batch: scene b's region r is b R + r
     if (MR > 0) {
-        e = launch_fill_cells(n, lb, ub, pb.g2r_offsets, RG.cell, RG.n, b.r_cells, b.r_pairs, b.r_gauss, s);
+        e = launch_fill_cells(n, lb, ub, pb.g2r_offsets, RG.cell, RG.n, b.r_cells, b.r_pairs, b.r_gauss, s,
+                              G.scenes > 1 ? G.scene_n : 0, RG.total);
         if (e != hipSuccess) return e;
-        e = radix_sort_pairs(b.r_cells, b.r_pairs, b.r_cells_sorted, b.r_pairs_sorted, MR, RG.total, b.sort_ws, s);
+        e = radix_sort_pairs(b.r_cells, b.r_pairs, b.r_cells_sorted, b.r_pairs_sorted, MR, nreg, b.sort_ws, s);
         if (e != hipSuccess) return e;
     }
-    e = launch_tile_offsets(b.r_cells_sorted, MR, RG.total, b.roff, s);
+    e = launch_tile_offsets(b.r_cells_sorted, MR, nreg, b.roff, s);
     if (e != hipSuccess) return e;
     if (MR > 0 && M > 0) {
         G2V_LAUNCH(k_region_gids, dim3((unsigned)ceil_div(MR, 256)), dim3(256), 0, s, (int)MR,
@@ -1687,7 +1717,7 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
         return hipErrorInvalidValue;
     const CosG cg = cos ? *cos : CosG{nullptr, nullptr, nullptr, 0.0f};
     const Regions RG = make_regions(G);
-    const int T = G.tiles[0] * G.tiles[1] * G.tiles[2];
+    const int T = scene_tiles(G) * G.scenes;   // tiles of the batch
     const int nchk = feature_chunks(C, fdt);
     if (!split_rows_fit(n, C)) return hipErrorInvalidValue;   // byte offsets of the split rows are 32-bit
     const FeatBufs b = carve_feats(ws, G, n, C, M, MR);
@@ -1718,7 +1748,7 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
     }
     if (MR > 0 && M > 0) {
         const int nchunk = (C + kBrCc - 1) / kBrCc;
-        const int64_t items = (int64_t)RG.total * nchunk;
+        const int64_t items = (int64_t)RG.total * G.scenes * nchunk;
         const int blocks = (int)ceil_div(items, 8) * 8;
         // two-channel staging loads: even C and a grad_feats base aligned to two elements
         const bool pair = (C & 1) == 0 && ((uintptr_t)grad_feats & (fdt == kDtBF16 ? 3 : 7)) == 0;

@@ -36,6 +36,8 @@ int hip_fail(hipError_t e, const char* where) {
 // Grid of (voxel_size, voxel_range) in float32, truncated like the reference (.cu:1512-1519).
 int make_grid(const float* vs, const float* vr, Grid& G) {
     if (!vs || !vr) return fail(G2V_ERR_INVALID, "voxel_size / voxel_range must not be null");
+    G.scenes = 1;
+    G.scene_n = 0;
     for (int a = 0; a < 3; ++a) {
         const float q = (vr[a + 3] - vr[a]) / vs[a];
         if (!(q >= 1.0f) || !(q < 2147483648.0f))
@@ -52,9 +54,11 @@ int make_grid(const float* vs, const float* vr, Grid& G) {
     return G2V_OK;
 }
 
-int num_tiles(const Grid& G) { return G.tiles[0] * G.tiles[1] * G.tiles[2]; }
+// Tiles of the problem (of every scene of a batch).
+int num_tiles(const Grid& G) { return scene_tiles(G) * G.scenes; }
 
 struct SplatBufs {
+    int* keys;          // batches: the batch's tile id of every G->T entry (the sort key)
     int* gauss_ids;
     int* sorted_tiles;
     int* sorted_gauss;
@@ -69,6 +73,7 @@ SplatBufs carve_splat(void* ws, int n, int64_t M, const Grid& G, int feat_dim = 
     const int T = num_tiles(G);
     Carver c(ws, (size_t)-1);
     SplatBufs b;
+    b.keys = G.scenes > 1 ? c.take<int>(m) : nullptr;
     b.gauss_ids = c.take<int>(m);
     b.sorted_tiles = c.take<int>(m);
     b.sorted_gauss = c.take<int>(m);
@@ -79,14 +84,15 @@ SplatBufs carve_splat(void* ws, int n, int64_t M, const Grid& G, int feat_dim = 
     return b;
 }
 
-// G->T gauss ids, stable sort by tile, tile offsets: the Tile->Gaussian CSR.
+// G->T gauss ids, stable sort by tile, tile offsets: the Tile->Gaussian CSR.  A batch sorts by
+// the batch's tile ids (b.keys, written beside the scene-local g2t_tile_ids_out).
 int build_t2g(const Grid& G, int n, const int* lb, const int* ub, const int* g2t_offsets,
               int* g2t_tile_ids_out, const int* g2t_tile_ids_in, int64_t M, const SplatBufs& b,
               hipStream_t s) {
     const int T = num_tiles(G);
     if (M > 0) {
-        G2V_HIP(launch_fill_g2t(G, n, lb, ub, g2t_offsets, g2t_tile_ids_out, b.gauss_ids, s));
-        const int* keys = g2t_tile_ids_out ? g2t_tile_ids_out : g2t_tile_ids_in;
+        G2V_HIP(launch_fill_g2t(G, n, lb, ub, g2t_offsets, g2t_tile_ids_out, b.gauss_ids, s, b.keys));
+        const int* keys = b.keys ? b.keys : g2t_tile_ids_out ? g2t_tile_ids_out : g2t_tile_ids_in;
         G2V_HIP(radix_sort_pairs(keys, b.gauss_ids, b.sorted_tiles, b.sorted_gauss, M, T, b.sort_ws, s));
     }
     G2V_HIP(launch_tile_offsets(b.sorted_tiles, M, T, b.tile_offsets, s));
@@ -111,6 +117,15 @@ long long* pinned_counts() {
     return p;
 }
 
+// Workspace of the backward of n Gaussians (all scenes of a batch) on G.
+size_t backward_ws_bytes(const Grid& G, int n, int feat_dim, long long num_pairs, long long num_region_pairs) {
+    if (feat_dim <= 0) return 256;
+    Carver c(nullptr, (size_t)-1);
+    c.take<char>(carve_splat(nullptr, n, num_pairs, G).bytes);
+    c.take<char>(backward_feats_workspace(G, n, feat_dim, num_pairs, num_region_pairs));
+    return c.off + 256;
+}
+
 int check_ws(const void* ws, size_t have, size_t need, const char* what) {
     if (need > have) return fail(G2V_ERR_INVALID, "%s workspace too small: %zu < %zu bytes", what, have, need);
     if (!ws && need > 0) return fail(G2V_ERR_INVALID, "%s workspace is null", what);
@@ -123,7 +138,7 @@ extern "C" {
 
 const char* g2v_last_error(void) { return g_err; }
 
-int g2v_abi_version(void) { return 10; }
+int g2v_abi_version(void) { return 11; }
 
 int g2v_grid_dims(const float voxel_size[3], const float voxel_range[6], int dims[3], int tiles[3]) {
     Grid G;
@@ -264,13 +279,17 @@ size_t g2v_forward_splat_workspace(int n, int feat_dim, long long num_pairs, con
     return carve_splat(nullptr, n, num_pairs, G, feat_dim).bytes;
 }
 
-int g2v_forward_splat(int n, int feat_dim, const float* means3D, const float* opacity,
-                      const void* features, int feat_dtype, const float voxel_size[3],
-                      const float voxel_range[6], const float* cov_inv, const int* valid_voxel_lb,
-                      const int* valid_voxel_ub, const int* g2t_offsets, long long num_pairs,
-                      int* g2t_tile_ids, float* density, void* grid_feats, int* t2g_tiles, int* t2g_gauss,
-                      int* t2g_offsets, void* workspace, size_t workspace_bytes, void* stream) {
-    g_err[0] = 0;
+}  // extern "C"
+
+namespace {
+
+// The splat of n Gaussians (every scene of a batch) on G.  g2t_tile_ids (scene-local tile ids) may
+// be null for a batch, whose sort keys are the batch's tile ids.
+int splat_impl(const Grid& G, int n, int feat_dim, const float* means3D, const float* opacity,
+               const void* features, int feat_dtype, const float* cov_inv, const int* valid_voxel_lb,
+               const int* valid_voxel_ub, const int* g2t_offsets, long long num_pairs, int* g2t_tile_ids,
+               float* density, void* grid_feats, int* t2g_tiles, int* t2g_gauss, int* t2g_offsets, void* workspace,
+               size_t workspace_bytes, void* stream) {
     if (feat_dtype != G2V_DTYPE_F32 && feat_dtype != G2V_DTYPE_BF16)
         return fail(G2V_ERR_INVALID, "feat_dtype = %d (G2V_DTYPE_F32 or G2V_DTYPE_BF16)", feat_dtype);
     if (n < 0 || feat_dim < 0 || num_pairs < 0)
@@ -281,16 +300,13 @@ int g2v_forward_splat(int n, int feat_dim, const float* means3D, const float* op
         return fail(G2V_ERR_LIMIT, "n = %d x feat_dim = %d exceeds the packed feature rows (4 GiB)", n, feat_dim);
     if (feat_dim > 0 && (!grid_feats || (n > 0 && !features)))
         return fail(G2V_ERR_INVALID, "feat_dim = %d needs features and grid_feats", feat_dim);
-    if (num_pairs > 0 && (!g2t_tile_ids || !g2t_offsets || !means3D || !opacity || !cov_inv ||
+    if (num_pairs > 0 && ((!g2t_tile_ids && G.scenes == 1) || !g2t_offsets || !means3D || !opacity || !cov_inv ||
                           !valid_voxel_lb || !valid_voxel_ub))
         return fail(G2V_ERR_INVALID, "null input/output pointer");
-    Grid G;
-    int rc = make_grid(voxel_size, voxel_range, G);
-    if (rc != G2V_OK) return rc;
-    if ((double)G.dims[0] * G.dims[1] * G.dims[2] * (double)feat_dim >= 9.2e18)
+    if ((double)scene_voxels(G) * G.scenes * (double)feat_dim >= 9.2e18)
         return fail(G2V_ERR_LIMIT, "grid_feats too large");
     const SplatBufs need = carve_splat(nullptr, n, num_pairs, G, feat_dim);
-    rc = check_ws(workspace, workspace_bytes, need.bytes, "splat");
+    int rc = check_ws(workspace, workspace_bytes, need.bytes, "splat");
     if (rc != G2V_OK) return rc;
     SplatBufs b = carve_splat(workspace, n, num_pairs, G, feat_dim);
     if (t2g_tiles && t2g_gauss && t2g_offsets) {   // the caller keeps the Tile->Gaussian CSR
@@ -310,6 +326,25 @@ int g2v_forward_splat(int n, int feat_dim, const float* means3D, const float* op
         G2V_HIP(launch_forward_density(G, means3D, opacity, cov_inv, valid_voxel_lb, valid_voxel_ub,
                                        b.tile_offsets, b.sorted_gauss, (int)num_pairs, density, s));
     return G2V_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int g2v_forward_splat(int n, int feat_dim, const float* means3D, const float* opacity,
+                      const void* features, int feat_dtype, const float voxel_size[3],
+                      const float voxel_range[6], const float* cov_inv, const int* valid_voxel_lb,
+                      const int* valid_voxel_ub, const int* g2t_offsets, long long num_pairs,
+                      int* g2t_tile_ids, float* density, void* grid_feats, int* t2g_tiles, int* t2g_gauss,
+                      int* t2g_offsets, void* workspace, size_t workspace_bytes, void* stream) {
+    g_err[0] = 0;
+    Grid G;
+    const int rc = make_grid(voxel_size, voxel_range, G);
+    if (rc != G2V_OK) return rc;
+    return splat_impl(G, n, feat_dim, means3D, opacity, features, feat_dtype, cov_inv, valid_voxel_lb, valid_voxel_ub,
+                      g2t_offsets, num_pairs, g2t_tile_ids, density, grid_feats, t2g_tiles, t2g_gauss, t2g_offsets,
+                      workspace, workspace_bytes, stream);
 }
 
 size_t g2v_backward_plan_workspace(int n) { return backward_plan_workspace(n > 0 ? n : 0); }
@@ -341,11 +376,7 @@ size_t g2v_backward_workspace(int n, int feat_dim, long long num_pairs, long lon
                               const float voxel_size[3], const float voxel_range[6]) {
     Grid G;
     if (make_grid(voxel_size, voxel_range, G) != G2V_OK) return 0;
-    if (feat_dim <= 0) return 256;
-    Carver c(nullptr, (size_t)-1);
-    c.take<char>(carve_splat(nullptr, n, num_pairs, G).bytes);
-    c.take<char>(backward_feats_workspace(G, n, feat_dim, num_pairs, num_region_pairs));
-    return c.off + 256;
+    return backward_ws_bytes(G, n, feat_dim, num_pairs, num_region_pairs);
 }
 
 }  // extern "C"
@@ -361,7 +392,8 @@ int backward_impl(int n, int feat_dim, const float* grad_density, const void* gr
                   const void* features, int feat_dtype, float* grad_means, float* grad_cov, float* grad_opacity,
                   void* grad_features, const int* t2g_tiles, const int* t2g_gauss,
                   const int* t2g_offsets, const void* plan_workspace, void* workspace,
-                  size_t workspace_bytes, bool prepared, void* stream, const CosG* cos = nullptr) {
+                  size_t workspace_bytes, bool prepared, void* stream, const CosG* cos = nullptr,
+                  int scenes = 1) {
     g_err[0] = 0;
     if (feat_dtype != G2V_DTYPE_F32 && feat_dtype != G2V_DTYPE_BF16)
         return fail(G2V_ERR_INVALID, "feat_dtype = %d (G2V_DTYPE_F32 or G2V_DTYPE_BF16)", feat_dtype);
@@ -375,14 +407,20 @@ int backward_impl(int n, int feat_dim, const float* grad_density, const void* gr
     if (!grad_density || !means3D || !opacity || !cov_inv || !valid_voxel_lb || !valid_voxel_ub ||
         !grad_means || !grad_cov || !grad_opacity)
         return fail(G2V_ERR_INVALID, "null input/output pointer");
+    const bool have_t2g = t2g_tiles && t2g_gauss && t2g_offsets;
     if (feat_dim > 0 && ((!grad_feats && !cos) || !grid_feats || !features || !grad_features || !density ||
-                         !g2t_offsets || !plan_workspace || (num_pairs > 0 && !g2t_tile_ids)))
+                         !g2t_offsets || !plan_workspace ||
+                         (num_pairs > 0 && !g2t_tile_ids && !have_t2g && scenes == 1)))
         return fail(G2V_ERR_INVALID, "feat_dim = %d needs the feature tensors, density, the CSR and the plan workspace", feat_dim);
     if (feat_dim > 0 && !split_rows_fit(n, feat_dim))
         return fail(G2V_ERR_LIMIT, "n = %d x feat_dim = %d exceeds the split feature rows (4 GiB)", n, feat_dim);
     Grid G;
     int rc = make_grid(voxel_size, voxel_range, G);
     if (rc != G2V_OK) return rc;
+    if (scenes > 1) {   // n = scenes x scene_n Gaussians, scene-major
+        G.scenes = scenes;
+        G.scene_n = n / scenes;
+    }
     if (feat_dim > 0 && !region_offsets_fit(G, feat_dim))
         return fail(G2V_ERR_LIMIT, "Y x Z x feat_dim = %d x %d x %d exceeds the 32-bit tile offsets of the "
                     "feature backward (16 Y Z C < 2^31)", G.dims[1], G.dims[2], feat_dim);
@@ -392,8 +430,7 @@ int backward_impl(int n, int feat_dim, const float* grad_density, const void* gr
                                         valid_voxel_ub, grad_means, grad_cov, grad_opacity, s));
         return G2V_OK;
     }
-    rc = check_ws(workspace, workspace_bytes,
-                  g2v_backward_workspace(n, feat_dim, num_pairs, num_region_pairs, voxel_size, voxel_range),
+    rc = check_ws(workspace, workspace_bytes, backward_ws_bytes(G, n, feat_dim, num_pairs, num_region_pairs),
                   "backward");
     if (rc != G2V_OK) return rc;
     Carver c(workspace, workspace_bytes);
@@ -438,11 +475,14 @@ int g2v_backward(int n, int feat_dim, const float* grad_density, const void* gra
                          plan_workspace, workspace, workspace_bytes, false, stream);
 }
 
-int g2v_backward_prepare(int n, int feat_dim, const float voxel_size[3], const float voxel_range[6],
-                         const int* valid_voxel_lb, const int* valid_voxel_ub, const void* features,
-                         int feat_dtype, long long num_pairs, long long num_region_pairs, const int* t2g_tiles,
-                         const int* t2g_gauss, const void* plan_workspace, void* workspace,
-                         size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int prepare_impl(int n, int feat_dim, const float voxel_size[3], const float voxel_range[6],
+                 const int* valid_voxel_lb, const int* valid_voxel_ub, const void* features, int feat_dtype,
+                 long long num_pairs, long long num_region_pairs, const int* t2g_tiles, const int* t2g_gauss,
+                 const void* plan_workspace, void* workspace, size_t workspace_bytes, void* stream, int scenes) {
     g_err[0] = 0;
     if (feat_dtype != G2V_DTYPE_F32 && feat_dtype != G2V_DTYPE_BF16)
         return fail(G2V_ERR_INVALID, "feat_dtype = %d (G2V_DTYPE_F32 or G2V_DTYPE_BF16)", feat_dtype);
@@ -460,8 +500,11 @@ int g2v_backward_prepare(int n, int feat_dim, const float voxel_size[3], const f
     Grid G;
     int rc = make_grid(voxel_size, voxel_range, G);
     if (rc != G2V_OK) return rc;
-    rc = check_ws(workspace, workspace_bytes,
-                  g2v_backward_workspace(n, feat_dim, num_pairs, num_region_pairs, voxel_size, voxel_range),
+    if (scenes > 1) {   // n = scenes x scene_n Gaussians, scene-major
+        G.scenes = scenes;
+        G.scene_n = n / scenes;
+    }
+    rc = check_ws(workspace, workspace_bytes, backward_ws_bytes(G, n, feat_dim, num_pairs, num_region_pairs),
                   "backward");
     if (rc != G2V_OK) return rc;
     Carver c(workspace, workspace_bytes);
@@ -471,6 +514,20 @@ int g2v_backward_prepare(int n, int feat_dim, const float voxel_size[3], const f
                                     t2g_tiles, t2g_gauss, plan_workspace, num_region_pairs, feats_ws,
                                     static_cast<hipStream_t>(stream)));
     return G2V_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int g2v_backward_prepare(int n, int feat_dim, const float voxel_size[3], const float voxel_range[6],
+                         const int* valid_voxel_lb, const int* valid_voxel_ub, const void* features,
+                         int feat_dtype, long long num_pairs, long long num_region_pairs, const int* t2g_tiles,
+                         const int* t2g_gauss, const void* plan_workspace, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+    return prepare_impl(n, feat_dim, voxel_size, voxel_range, valid_voxel_lb, valid_voxel_ub, features, feat_dtype,
+                        num_pairs, num_region_pairs, t2g_tiles, t2g_gauss, plan_workspace, workspace, workspace_bytes,
+                        stream, 1);
 }
 
 int g2v_backward_cosine(int n, int feat_dim, const float* grad_density, const float* grad_loss,
@@ -691,6 +748,159 @@ int g2v_covariance_from_scale_rotation_backward(int n, const float* scales, cons
     G2V_HIP(launch_cov_from_scale_rot_bwd(n, scales, rotations, grad_covariances, grad_scales, grad_rotations,
                                           static_cast<hipStream_t>(stream)));
     return G2V_OK;
+}
+
+// ---- batches of scenes on one grid -------------------------------------------------------------
+//
+// B scenes of n Gaussians each, laid out scene-major ((B, n, ...) inputs, (B, X, Y, Z[, C]) outputs),
+// are planned, splatted and differentiated as one problem of B n Gaussians on B T tiles (see Grid).
+
+}  // extern "C"
+
+namespace {
+
+// The batch's plan workspace: the batch's G->T row offsets (B n + 1) and pair totals, the plan's own
+// workspace and the backward plan's region cell offsets, all for B n Gaussians.  The caller keeps it
+// from the plan to the batch's backward.
+struct BatchPlan {
+    int* goff;
+    long long* totals;   // pairs, region pairs of the batch
+    void* plan_ws;
+    size_t plan_bytes;
+    void* bwd_ws;
+    size_t bytes;
+};
+
+BatchPlan carve_batch_plan(void* ws, int B, int n) {
+    const int nt = B * n;
+    Carver c(ws, (size_t)-1);
+    BatchPlan p;
+    p.goff = c.take<int>((size_t)nt + 1);
+    p.totals = c.take<long long>(2);
+    p.plan_bytes = g2v_forward_plan_workspace(nt);
+    p.plan_ws = c.take<char>(p.plan_bytes);
+    p.bwd_ws = c.take<char>(backward_plan_workspace(nt));
+    p.bytes = c.off + 256;
+    return p;
+}
+
+bool batch_sizes_ok(int B, int n) { return B >= 1 && n >= 0 && (int64_t)B * n < 2147483647ll; }
+
+// Grid of a batch of B scenes (n Gaussians each) and its plan workspace, checked.
+int batch_setup(int B, int n, const float* vs, const float* vr, const void* plan_ws, size_t plan_bytes, Grid& G,
+                BatchPlan& p) {
+    if (!batch_sizes_ok(B, n)) return fail(G2V_ERR_INVALID, "num_scenes = %d, n = %d", B, n);
+    int rc = make_grid(vs, vr, G);
+    if (rc != G2V_OK) return rc;
+    if ((int64_t)scene_tiles(G) * B >= 2147483647ll)
+        return fail(G2V_ERR_LIMIT, "%d scenes x %d tiles exceed int32", B, scene_tiles(G));
+    G.scenes = B;
+    G.scene_n = n;
+    rc = check_ws(plan_ws, plan_bytes, carve_batch_plan(nullptr, B, n).bytes, "batch plan");
+    if (rc != G2V_OK) return rc;
+    p = carve_batch_plan(const_cast<void*>(plan_ws), B, n);
+    return G2V_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t g2v_batch_plan_workspace(int num_scenes, int n) {
+    if (!batch_sizes_ok(num_scenes, n)) return 0;
+    return carve_batch_plan(nullptr, num_scenes, n).bytes;
+}
+
+int g2v_batch_forward_plan(int num_scenes, int n, const float* means3D, const float* covariances,
+                           const float voxel_size[3], const float voxel_range[6], float* cov_inv, int* valid_voxel_lb,
+                           int* valid_voxel_ub, int* num_voxels_per_gaussian, int* g2t_offsets, void* plan_workspace,
+                           size_t plan_workspace_bytes, int want_backward, long long* counts, void* stream) {
+    g_err[0] = 0;
+    if (!counts || !g2t_offsets) return fail(G2V_ERR_INVALID, "counts / g2t_offsets is null");
+    Grid G;
+    BatchPlan p;
+    int rc = batch_setup(num_scenes, n, voxel_size, voxel_range, plan_workspace, plan_workspace_bytes, G, p);
+    if (rc != G2V_OK) return rc;
+    const int nt = num_scenes * n;
+    if (nt > 0 && (!means3D || !covariances || !cov_inv || !valid_voxel_lb || !valid_voxel_ub || !num_voxels_per_gaussian))
+        return fail(G2V_ERR_INVALID, "null input/output pointer");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    rc = plan_launch(G, nt, means3D, covariances, cov_inv, valid_voxel_lb, valid_voxel_ub, num_voxels_per_gaussian,
+                     p.goff, p.plan_ws, p.plan_bytes, want_backward ? p.bwd_ws : nullptr, p.totals, s);
+    if (rc != G2V_OK) return rc;
+    G2V_HIP(launch_scene_offsets(num_scenes, n, p.goff, want_backward ? p.totals + 1 : nullptr, g2t_offsets, counts, s));
+    return G2V_OK;
+}
+
+size_t g2v_batch_forward_splat_workspace(int num_scenes, int n, int feat_dim, long long num_pairs,
+                                         const float voxel_size[3], const float voxel_range[6]) {
+    Grid G;
+    if (!batch_sizes_ok(num_scenes, n) || make_grid(voxel_size, voxel_range, G) != G2V_OK) return 0;
+    G.scenes = num_scenes;
+    G.scene_n = n;
+    return carve_splat(nullptr, num_scenes * n, num_pairs, G, feat_dim).bytes;
+}
+
+int g2v_batch_forward_splat(int num_scenes, int n, int feat_dim, const float* means3D, const float* opacity,
+                            const void* features, int feat_dtype, const float voxel_size[3],
+                            const float voxel_range[6], const float* cov_inv, const int* valid_voxel_lb,
+                            const int* valid_voxel_ub, const void* plan_workspace, size_t plan_workspace_bytes,
+                            long long num_pairs, int* g2t_tile_ids, float* density, void* grid_feats, int* t2g_tiles,
+                            int* t2g_gauss, int* t2g_offsets, void* workspace, size_t workspace_bytes, void* stream) {
+    g_err[0] = 0;
+    Grid G;
+    BatchPlan p;
+    const int rc = batch_setup(num_scenes, n, voxel_size, voxel_range, plan_workspace, plan_workspace_bytes, G, p);
+    if (rc != G2V_OK) return rc;
+    return splat_impl(G, num_scenes * n, feat_dim, means3D, opacity, features, feat_dtype, cov_inv, valid_voxel_lb,
+                      valid_voxel_ub, p.goff, num_pairs, g2t_tile_ids, density, grid_feats, t2g_tiles, t2g_gauss,
+                      t2g_offsets, workspace, workspace_bytes, stream);
+}
+
+size_t g2v_batch_backward_workspace(int num_scenes, int n, int feat_dim, long long num_pairs,
+                                    long long num_region_pairs, const float voxel_size[3], const float voxel_range[6]) {
+    Grid G;
+    if (!batch_sizes_ok(num_scenes, n) || make_grid(voxel_size, voxel_range, G) != G2V_OK) return 0;
+    G.scenes = num_scenes;
+    G.scene_n = n;
+    return backward_ws_bytes(G, num_scenes * n, feat_dim, num_pairs, num_region_pairs);
+}
+
+int g2v_batch_backward_prepare(int num_scenes, int n, int feat_dim, const float voxel_size[3],
+                               const float voxel_range[6], const int* valid_voxel_lb, const int* valid_voxel_ub,
+                               const void* features, int feat_dtype, long long num_pairs, long long num_region_pairs,
+                               const int* t2g_tiles, const int* t2g_gauss, const void* plan_workspace,
+                               size_t plan_workspace_bytes, void* workspace, size_t workspace_bytes, void* stream) {
+    g_err[0] = 0;
+    Grid G;
+    BatchPlan p;
+    const int rc = batch_setup(num_scenes, n, voxel_size, voxel_range, plan_workspace, plan_workspace_bytes, G, p);
+    if (rc != G2V_OK) return rc;
+    return prepare_impl(num_scenes * n, feat_dim, voxel_size, voxel_range, valid_voxel_lb, valid_voxel_ub, features,
+                        feat_dtype, num_pairs, num_region_pairs, t2g_tiles, t2g_gauss, p.bwd_ws, workspace,
+                        workspace_bytes, stream, num_scenes);
+}
+
+int g2v_batch_backward(int num_scenes, int n, int feat_dim, const float* grad_density, const void* grad_feats,
+                       const float* means3D, const float* opacity, const float* cov_inv, const float voxel_size[3],
+                       const float voxel_range[6], const int* valid_voxel_lb, const int* valid_voxel_ub,
+                       long long num_pairs, long long num_region_pairs, const float* density, const void* grid_feats,
+                       const void* features, int feat_dtype, float* grad_means, float* grad_cov, float* grad_opacity,
+                       void* grad_features, const int* t2g_tiles, const int* t2g_gauss, const int* t2g_offsets,
+                       const void* plan_workspace, size_t plan_workspace_bytes, void* workspace,
+                       size_t workspace_bytes, int prepared, void* stream) {
+    g_err[0] = 0;
+    Grid G;
+    BatchPlan p;
+    const int rc = batch_setup(num_scenes, n, voxel_size, voxel_range, plan_workspace, plan_workspace_bytes, G, p);
+    if (rc != G2V_OK) return rc;
+    if (prepared && feat_dim > 0 && n > 0 && num_pairs > 0 && !(t2g_tiles && t2g_gauss && t2g_offsets))
+        return fail(G2V_ERR_INVALID, "a prepared backward needs the forward's Tile->Gaussian CSR");
+    return backward_impl(num_scenes * n, feat_dim, grad_density, grad_feats, means3D, opacity, cov_inv, voxel_size,
+                         voxel_range, valid_voxel_lb, valid_voxel_ub, nullptr, p.goff, nullptr, num_pairs,
+                         num_region_pairs, density, grid_feats, features, feat_dtype, grad_means, grad_cov, grad_opacity,
+                         grad_features, t2g_tiles, t2g_gauss, t2g_offsets, p.bwd_ws, workspace, workspace_bytes,
+                         prepared != 0, stream, nullptr, num_scenes);
 }
 
 }  // extern "C"

@@ -320,13 +320,16 @@ hipError_t scan_i32_pair(const int* in_a, int* out_a, int64_t n_a, long long* to
 // Entry i of a row is tile box position (lx, ly, lz) = the digits of i in radix (dy, dz); a lane
 // visits i = l, l + 16, ... and steps its position by the digits of 16 (at most one carry per
 // digit) instead of dividing at every entry.
+// keys (optional, batches): the batch's tile id of every entry (scene b T + tile), the sort key;
+// tile_ids keeps the scene-local ids.
 constexpr int kFillLanes = 16;
 
 __global__ void __launch_bounds__(256) k_fill_g2t(Grid G, int n, const int* __restrict__ lb,
                                                   const int* __restrict__ ub,
                                                   const int* __restrict__ g2t_offsets,
                                                   int* __restrict__ tile_ids,
-                                                  int* __restrict__ gauss_ids) {
+                                                  int* __restrict__ gauss_ids,
+                                                  int* __restrict__ keys) {
     const int l = threadIdx.x & (kFillLanes - 1);
     const int g = blockIdx.x * (256 / kFillLanes) + threadIdx.x / kFillLanes;
     if (g >= n) return;
@@ -343,8 +346,11 @@ __global__ void __launch_bounds__(256) k_fill_g2t(Grid G, int n, const int* __re
     const int sx = kFillLanes / dyz;
     const int sy = (kFillLanes - sx * dyz) / dz;
     const int sz = kFillLanes - sx * dyz - sy * dz;
+    const int kb = scene_of(G, g) * scene_tiles(G);
     for (int i = l; i < cnt; i += kFillLanes) {
-        if (tile_ids) tile_ids[base + i] = ((tx0 + lx) * G.tiles[1] + (ty0 + ly)) * G.tiles[2] + (tz0 + lz);
+        const int t = ((tx0 + lx) * G.tiles[1] + (ty0 + ly)) * G.tiles[2] + (tz0 + lz);
+        if (tile_ids) tile_ids[base + i] = t;
+        if (keys) keys[base + i] = kb + t;
         gauss_ids[base + i] = g;
         lz += sz;
         const int cz = lz >= dz ? 1 : 0;
@@ -357,10 +363,36 @@ __global__ void __launch_bounds__(256) k_fill_g2t(Grid G, int n, const int* __re
 }
 
 hipError_t launch_fill_g2t(const Grid& G, int n, const int* lb, const int* ub,
-                           const int* g2t_offsets, int* tile_ids, int* gauss_ids, hipStream_t s) {
+                           const int* g2t_offsets, int* tile_ids, int* gauss_ids, hipStream_t s, int* keys) {
     if (n <= 0) return hipSuccess;
     G2V_LAUNCH(k_fill_g2t, dim3((unsigned)ceil_div(n, 256 / kFillLanes)), dim3(256), 0, s, G, n, lb, ub,
-               g2t_offsets, tile_ids, gauss_ids);
+               g2t_offsets, tile_ids, gauss_ids, keys);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------------
+// Batches: the per-scene G->T row offsets and pair counts from the batch's offsets.
+// out[b (n + 1) + k] = goff[b n + k] - goff[b n] (k = 0..n); counts[b] = goff[(b + 1) n] - goff[b n]
+// for b < B and counts[B] = *mr_total (0 without it).
+// ------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) k_scene_offsets(int B, int n, const int* __restrict__ goff,
+                                                       const long long* __restrict__ mr_total,
+                                                       int* __restrict__ out, long long* __restrict__ counts) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t rows = (int64_t)B * (n + 1);
+    if (i < rows) {
+        const int64_t b = i / (n + 1), k = i - b * (n + 1);
+        out[i] = goff[b * n + k] - goff[b * n];
+    }
+    if (i < B) counts[i] = (long long)(goff[(i + 1) * n] - goff[i * n]);
+    if (i == B) counts[B] = mr_total ? *mr_total : 0;
+}
+
+hipError_t launch_scene_offsets(int B, int n, const int* goff, const long long* mr_total, int* out,
+                                long long* counts, hipStream_t s) {
+    const int64_t items = max((int64_t)B * (n + 1), (int64_t)B + 1);
+    G2V_LAUNCH(k_scene_offsets, dim3((unsigned)ceil_div(items, 256)), dim3(256), 0, s, B, n, goff, mr_total, out,
+               counts);
     return hipGetLastError();
 }
 
@@ -368,7 +400,8 @@ hipError_t launch_fill_g2t(const Grid& G, int n, const int* lb, const int* ub,
 // Cells: coarser boxes of `cell` voxels per axis (the backward's regions of 2x2xRZ tiles).
 // k_cell_count writes each Gaussian's cell count to offsets[g+1] (offsets[0] = 0);
 // k_fill_cells enumerates each Gaussian's cell box row-major like k_fill_g2t and also writes
-// the pair index of every entry (the value the sort carries).
+// the pair index of every entry (the value the sort carries).  In a batch (scene_n > 0) the cell
+// id of Gaussian g's entries is offset by (g / scene_n) scene_cells.
 // ------------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) k_cell_count(int n, const int* __restrict__ lb,
                                                     const int* __restrict__ ub, int cx, int cy, int cz,
@@ -388,7 +421,7 @@ __global__ void __launch_bounds__(256) k_fill_cells(int n, const int* __restrict
                                                     const int* __restrict__ offsets, int cx, int cy,
                                                     int cz, int ny, int nz, int* __restrict__ cell_ids,
                                                     int* __restrict__ pair_ids,
-                                                    int* __restrict__ gauss_ids) {
+                                                    int* __restrict__ gauss_ids, int scene_n, int scene_cells) {
     const int lane = threadIdx.x & 63;
     const int g = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (g >= n) return;
@@ -399,10 +432,11 @@ __global__ void __launch_bounds__(256) k_fill_cells(int n, const int* __restrict
     const int dy = ub[g * 3 + 1] / cy - y0 + 1;
     const int dz = ub[g * 3 + 2] / cz - z0 + 1;
     const int dyz = dy * dz;
+    const int kb = scene_n > 0 ? (g / scene_n) * scene_cells : 0;
     for (int i = lane; i < cnt; i += 64) {
         const int lx = i / dyz, r = i - lx * dyz;
         const int ly = r / dz, lz = r - ly * dz;
-        cell_ids[base + i] = ((x0 + lx) * ny + (y0 + ly)) * nz + (z0 + lz);
+        cell_ids[base + i] = kb + ((x0 + lx) * ny + (y0 + ly)) * nz + (z0 + lz);
         pair_ids[base + i] = base + i;
         gauss_ids[base + i] = g;
     }
@@ -417,10 +451,10 @@ hipError_t launch_cell_count(int n, const int* lb, const int* ub, const int cell
 
 hipError_t launch_fill_cells(int n, const int* lb, const int* ub, const int* offsets, const int cell[3],
                              const int ncells[3], int* cell_ids, int* pair_ids, int* gauss_ids,
-                             hipStream_t s) {
+                             hipStream_t s, int scene_n, int scene_cells) {
     if (n <= 0) return hipSuccess;
     G2V_LAUNCH(k_fill_cells, dim3((unsigned)ceil_div(n, 4)), dim3(256), 0, s, n, lb, ub, offsets, cell[0],
-               cell[1], cell[2], ncells[1], ncells[2], cell_ids, pair_ids, gauss_ids);
+               cell[1], cell[2], ncells[1], ncells[2], cell_ids, pair_ids, gauss_ids, scene_n, scene_cells);
     return hipGetLastError();
 }
 

@@ -20,13 +20,29 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // Grid geometry passed by value to every kernel.
+//
+// A batch of B scenes on the same grid is one problem with B x N Gaussians: Gaussian g belongs to
+// scene g / N, tile t of scene b is tile b T + t of the batch (T tiles per scene) and region r of
+// scene b is region b R + r, and the voxel rows of scene b start at row b X Y Z of the outputs.
+// dims and tiles stay those of one scene; every box, tile and voxel coordinate is scene-local.
 struct Grid {
     float r0[3];      // range lower corner
     float r1[3];      // range upper corner
     float s[3];       // voxel size
     int dims[3];      // X, Y, Z
     int tiles[3];     // Tx, Ty, Tz
+    int scenes;       // B (1: a single scene)
+    int scene_n;      // N, Gaussians per scene (used when scenes > 1)
 };
+
+__host__ __device__ __forceinline__ int scene_tiles(const Grid& G) { return G.tiles[0] * G.tiles[1] * G.tiles[2]; }
+__host__ __device__ __forceinline__ int64_t scene_voxels(const Grid& G) {
+    return (int64_t)G.dims[0] * G.dims[1] * G.dims[2];
+}
+// Scene of the batch's Gaussian g.
+__host__ __device__ __forceinline__ int scene_of(const Grid& G, int g) {
+    return G.scenes > 1 && G.scene_n > 0 ? g / G.scene_n : 0;
+}
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 

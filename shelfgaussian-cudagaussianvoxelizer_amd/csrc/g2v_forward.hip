@@ -133,16 +133,19 @@ __global__ void __launch_bounds__(kDenWaves * 64) k_fwd_density(Grid G, const fl
                                                                const int* __restrict__ sorted_gauss,
                                                                int M, float* __restrict__ density) {
     __shared__ FwdParam slab[kDenWaves][64];
-    const int T = G.tiles[0] * G.tiles[1] * G.tiles[2];
-    const int tile = uniform(xcd_remap(blockIdx.x, gridDim.x) * kDenWaves + (threadIdx.x >> 6));
-    if (tile >= T) return;   // whole waves; the kernel has no workgroup barrier
+    const int T = scene_tiles(G);
+    // tb: the batch's tile (its list), tile: the scene's
+    const int tb = uniform(xcd_remap(blockIdx.x, gridDim.x) * kDenWaves + (threadIdx.x >> 6));
+    if (tb >= T * G.scenes) return;   // whole waves; the kernel has no workgroup barrier
+    const int scene = uniform(tb / T), tile = tb - scene * T;
+    density += scene * scene_voxels(G);
     const int lane = threadIdx.x & 63;
     FwdParam* sl = slab[threadIdx.x >> 6];
     int x, y, z;
     tile_voxel(G, tile, lane, x, y, z);
     const float cx = centre(G, 0, x), cy = centre(G, 1, y), cz = centre(G, 2, z);
-    const int j0 = uniform(min(max(toff[tile], 0), M));
-    const int j1 = uniform(min(max(toff[tile + 1], j0), M));
+    const int j0 = uniform(min(max(toff[tb], 0), M));
+    const int j1 = uniform(min(max(toff[tb + 1], j0), M));
     // parameters of list entry j (an empty box past the list)
     auto fetch = [&](int j, FwdParam& r) {
         if (j < j1) {
@@ -199,7 +202,7 @@ hipError_t launch_forward_density(const Grid& G, const float* means, const float
                                   const float* cov_inv, const int* lb, const int* ub,
                                   const int* tile_offsets, const int* sorted_gauss, int M,
                                   float* density, hipStream_t s) {
-    const int T = G.tiles[0] * G.tiles[1] * G.tiles[2];
+    const int T = scene_tiles(G) * G.scenes;
     if (T <= 0) return hipSuccess;
     const int groups = (int)ceil_div(T, kDenWaves);
     const int blocks = (int)ceil_div(groups, 8) * 8;
@@ -355,9 +358,16 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
     const uint32_t* __restrict__ fpk, float* __restrict__ density,
     void* __restrict__ grid_feats_out) {
     __shared__ FwdSmem sm;
-    const int T = G.tiles[0] * G.tiles[1] * G.tiles[2];
-    const int tile = uniform(xcd_remap(blockIdx.x, gridDim.x));
-    if (tile >= T) return;
+    const int T = scene_tiles(G);
+    // tb: the batch's tile (its list), tile: the scene's
+    const int tb = uniform(xcd_remap(blockIdx.x, gridDim.x));
+    if (tb >= T * G.scenes) return;
+    const int scene = uniform(tb / T), tile = tb - scene * T;
+    {
+        const int64_t vb = scene * scene_voxels(G);
+        density += vb;
+        grid_feats_out = static_cast<char*>(grid_feats_out) + vb * C * (OBF16 ? 2 : 4);
+    }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int jl = lane & 31, kh = lane >> 5;
 
@@ -371,8 +381,8 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
     const int col = threadIdx.x & 15;
     const float cxl = centre(G, 0, x0 + (col >> 2)), cyl = centre(G, 1, y0 + (col & 3));
 
-    const int j0 = uniform(min(max(toff[tile], 0), M));
-    const int Ng = uniform(min(max(toff[tile + 1], j0), M)) - j0;
+    const int j0 = uniform(min(max(toff[tb], 0), M));
+    const int Ng = uniform(min(max(toff[tb + 1], j0), M)) - j0;
     const int nkc = (Ng + kFwdKMax - 1) / kFwdKMax;
     constexpr uint32_t kCh = OBF16 ? 2u : 4u;   // packed bytes per channel
     const uint32_t row_bytes = (uint32_t)Cp * kCh;
@@ -562,7 +572,7 @@ hipError_t launch_forward_feats(const Grid& G, int C, const float* means, const 
                                 const int* tile_offsets, const int* sorted_gauss, int M, int n,
                                 const void* features, int fdt, uint32_t* fpk, float* density,
                                 void* grid_feats, hipStream_t s) {
-    const int T = G.tiles[0] * G.tiles[1] * G.tiles[2];
+    const int T = scene_tiles(G) * G.scenes;
     if (T <= 0) return hipSuccess;
     if (C <= 0)
         return launch_forward_density(G, means, opacity, cov_inv, lb, ub, tile_offsets, sorted_gauss,

@@ -51,14 +51,22 @@ hipError_t scan_i32_pair(const int* in_a, int* out_a, int64_t n_a, long long* to
 hipError_t launch_boxes(const Grid& G, int n, const float* means, const float* cov, float* cov_inv,
                         int* lb, int* ub, int* nvox, int* g2t_offsets, const int* cell, int* cell_offsets,
                         hipStream_t s);
+// keys (optional): the batch's tile ids (sort keys) beside the scene-local tile_ids.
 hipError_t launch_fill_g2t(const Grid& G, int n, const int* lb, const int* ub,
-                           const int* g2t_offsets, int* tile_ids, int* gauss_ids, hipStream_t s);
+                           const int* g2t_offsets, int* tile_ids, int* gauss_ids, hipStream_t s,
+                           int* keys = nullptr);
 
+// A batch of B scenes of n Gaussians: the per-scene G->T row offsets out (B x (n + 1)) and pair
+// counts (counts[b], b < B; counts[B] = *mr_total, or 0 when mr_total is null) from the batch's
+// offsets goff (B n + 1).
+hipError_t launch_scene_offsets(int B, int n, const int* goff, const long long* mr_total, int* out,
+                                long long* counts, hipStream_t s);
 hipError_t launch_cell_count(int n, const int* lb, const int* ub, const int cell[3], int* offsets,
                              hipStream_t s);
+// scene_n > 0 (a batch): the cells of Gaussian g are numbered from (g / scene_n) scene_cells.
 hipError_t launch_fill_cells(int n, const int* lb, const int* ub, const int* offsets, const int cell[3],
                              const int ncells[3], int* cell_ids, int* pair_ids, int* gauss_ids,
-                             hipStream_t s);
+                             hipStream_t s, int scene_n = 0, int scene_cells = 0);
 
 int sort_key_bits(int num_tiles);
 size_t sort_workspace(int64_t M, int num_tiles);
@@ -188,11 +196,17 @@ class ProfMark {
         hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);     \
     } while (0)
 
-// XCD-aware block -> item mapping: consecutive items land on the same XCD (shared L2).
+// XCD-aware block -> item mapping.  Workgroups are dealt to the 8 XCDs round robin (block b to XCD
+// b % 8); here every run of 64 consecutive items goes to one XCD (neighbouring tiles share Gaussians,
+// hence their rows in that XCD's L2), and the runs are dealt round robin, so that a grid whose work
+// sits in a few places (a sparse scene) still spreads over all XCDs.  A last partial group of
+// 8 x 64 blocks keeps the identity order.  A bijection on [0, nblocks).
 __device__ __forceinline__ int xcd_remap(int b, int nblocks) {
-    constexpr int kXcd = 8;
-    const int per = (nblocks + kXcd - 1) / kXcd;
-    return (b % kXcd) * per + b / kXcd;
+    constexpr int kXcd = 8, kRun = 64, kGroup = kXcd * kRun;
+    const int g = b / kGroup;
+    if ((g + 1) * kGroup > nblocks) return b;
+    const int r = b - g * kGroup;
+    return g * kGroup + (r % kXcd) * kRun + r / kXcd;
 }
 
 }  // namespace g2v

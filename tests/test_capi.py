@@ -31,7 +31,7 @@ def test_header_symbols_exported():
 
 
 def test_abi_version():
-    assert _lib().load().g2v_abi_version() == _lib().ABI_VERSION == 10
+    assert _lib().load().g2v_abi_version() == _lib().ABI_VERSION == 11
 
 
 def test_loader_refuses_other_abi(monkeypatch):
@@ -148,6 +148,37 @@ def test_workspace_queries_grow_with_problem():
     assert lib.g2v_forward_plan_workspace(200_000) > lib.g2v_forward_plan_workspace(10)
 
 
+def test_batch_arguments_and_workspaces():
+    """The batch entry points check their sizes before any launch, and a batch of B scenes needs
+    the workspaces of one problem of B n Gaussians on B T tiles."""
+    L = _lib()
+    lib = L.load()
+    vs, vr = L.floats([0.4] * 3), L.floats(W.RANGE_PAPER)
+    one = ctypes.c_void_p(16)
+    assert lib.g2v_batch_plan_workspace(0, 300) == 0
+    assert lib.g2v_batch_plan_workspace(1 << 16, 1 << 16) == 0   # B n beyond int32
+    p1, p6 = lib.g2v_batch_plan_workspace(1, 300), lib.g2v_batch_plan_workspace(6, 300)
+    assert 0 < p1 < p6
+    s1 = lib.g2v_batch_forward_splat_workspace(1, 300, 64, 10_000, vs, vr)
+    s6 = lib.g2v_batch_forward_splat_workspace(6, 300, 64, 10_000, vs, vr)
+    # six scenes hold six tile-offset arrays and a sort key per pair
+    assert s6 > s1 >= lib.g2v_forward_splat_workspace(300, 64, 10_000, vs, vr)
+    assert (lib.g2v_batch_backward_workspace(6, 300, 64, 10_000, 2000, vs, vr) >
+            lib.g2v_batch_backward_workspace(1, 300, 64, 10_000, 2000, vs, vr))
+    cnt = (ctypes.c_longlong * 8)()
+    rc = lib.g2v_batch_forward_plan(0, 300, one, one, vs, vr, one, one, one, one, one, one, 1 << 20, 1, cnt, None)
+    assert rc == 1 and b"num_scenes = 0" in lib.g2v_last_error()
+    rc = lib.g2v_batch_forward_plan(2, 300, one, one, vs, vr, one, one, one, one, one, one, 16, 1, cnt, None)
+    assert rc == 1 and b"workspace" in lib.g2v_last_error()
+    rc = lib.g2v_batch_forward_plan(2, 300, one, one, vs, vr, one, one, one, one, None, one, 1 << 20, 1, cnt, None)
+    assert rc == 1 and b"null" in lib.g2v_last_error()
+    # the plan workspace of one scene is too small for two; a prepared backward needs the batch's CSR
+    rc = lib.g2v_batch_backward(2, 300, 8, one, one, one, one, one, vs, vr, one, one, 100, 10, one, one, one, 0, one,
+                                one, one, one, None, None, None, one, p1, one, 1 << 30, 1, None)
+    assert rc == 1 and b"batch plan workspace" in lib.g2v_last_error()
+    rc = lib.g2v_batch_backward(2, 300, 8, one, one, one, one, one, vs, vr, one, one, 100, 10, one, one, one, 0, one,
+                                one, one, one, None, None, None, one, p6, one, 1 << 30, 1, None)
+    assert rc == 1 and b"Tile->Gaussian" in lib.g2v_last_error()
 def test_product_path_does_not_reference_oracle():
     pkg = os.path.join(ROOT, "shelfgaussian-cudagaussianvoxelizer_amd")
     for dirpath, _, files in os.walk(pkg):
