@@ -355,7 +355,7 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
     const int* __restrict__ g2t_offsets, const int* __restrict__ toff,
     const int* __restrict__ sorted_gauss, int M, const float* __restrict__ density,
     const void* __restrict__ grid_feats, int gdt, const __bf16* __restrict__ fsp,
-    float* __restrict__ pair_partials, __bf16* __restrict__ wt, CosG cg) {
+    float* __restrict__ pair_partials, __bf16* __restrict__ wt, CosG cg, int skip_le) {
     static_assert(!FU || (VEC && !BF), "the fused cosine gradient takes 16-byte float32 rows");
     __shared__ BtSmem<FU> sm;
     const int T = scene_tiles(G);
@@ -364,7 +364,7 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
     if (tb >= T * G.scenes) return;
     const int j0 = uniform(min(max(toff[tb], 0), M));
     const int Ng = uniform(min(max(toff[tb + 1], j0), M)) - j0;
-    if (Ng <= 0) return;
+    if (Ng <= skip_le) return;   // empty, or a short list that k_bwd_tile_short takes
     const int scene = uniform(tb / T), tile = tb - scene * T;
     if (scene > 0) {   // the scene's voxel rows
         const int64_t vb = scene * scene_voxels(G);
@@ -958,6 +958,207 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             float* out = pair_partials + pair * kNumGrads;
 #pragma unroll
             for (int k = 0; k < kNumGrads; ++k) out[k] = sm.u.xch[0][slot][k] + sm.u.xch[1][slot][k];
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Phase A for short lists (1 .. kBsMax Gaussians).  k_bwd_tile holds one tile per CU (its LDS is
+// sized for 256-Gaussian passes), so a short list leaves that tile's chain of loads and barriers
+// bare; here a 4-wave workgroup with about 17 KB of LDS takes the tile and many run per CU.  The
+// per-pair results are those of k_bwd_tile up to float32 rounding: U = G F^T from float32 products
+// of gF and the split features' hi + lo (the matrix-core path leaves out lo x lo), t_v from U,
+// the same e (the same helper operations) and so the same split weights, and the moments summed
+// over the voxels in another order.  Which kernel takes a tile depends on its list length alone.
+// Thread = (voxel row lane, Gaussian slots 8 wave .. 8 wave + 7).
+// ------------------------------------------------------------------------------------------
+constexpr int kBsThreads = 256;
+constexpr int kBsMax = 32;     // longest list taken
+constexpr int kBsKc = 32;      // channels per staged chunk
+
+struct BsSmem {
+    float g[64][kBsKc + 1];    // gF chunk, voxel-major; rows padded so that lanes (voxels) hit distinct banks
+    float f[kBsKc][kBsMax];    // feature chunk, channel-major: a wave reads its 8 Gaussians of a channel at once
+    ParamTile<kBsMax> pt;
+    int vlin[64];
+    float gD[64], inv[64], D[64], tv[64];
+    float tpart[kBsThreads / 64][64];
+};
+
+// e of Gaussian p at voxel (x, y, z) with the operations of lane_geom / lane_exp / lane_e (so the
+// same value); in: the voxel lies in the Gaussian's box.
+__device__ __forceinline__ float voxel_e(const Grid& G, const GaussParams& p, int x, int y, int z, float& dx,
+                                         float& dy, float& dz, bool& in) {
+#pragma clang fp contract(off)
+    dx = centre(G, 0, x) - p.mu[0];
+    dy = centre(G, 1, y) - p.mu[1];
+    dz = centre(G, 2, z) - p.mu[2];
+    in = x >= p.lb[0] && x <= p.ub[0] && y >= p.lb[1] && y <= p.ub[1] && z >= p.lb[2] && z <= p.ub[2];
+    const float sxy = p.A[1] + p.A[3], sxz = p.A[2] + p.A[6], syz = p.A[5] + p.A[7];
+    const float fxy = kq * fmaf(fmaf(p.A[0], dx, sxy * dy), dx, p.A[4] * dy * dy);
+    const float gxy = kq * fmaf(sxz, dx, syz * dy);
+    const float fz = kq * (p.A[8] * dz * dz);
+    return __builtin_amdgcn_exp2f(fmaf(gxy, dz, fxy + fz));
+}
+
+// BF: grad_feats and the features are bfloat16 (the split rows then hold 64-channel chunks of the
+// values).
+template <bool BF>
+__global__ void __launch_bounds__(kBsThreads) k_bwd_tile_short(
+    Grid G, int n, int C, int nchk, const float* __restrict__ gD, const void* __restrict__ gF_,
+    const float* __restrict__ means, const float* __restrict__ opacity, const float* __restrict__ cov_inv,
+    const int* __restrict__ lb, const int* __restrict__ ub, const int* __restrict__ g2t_offsets,
+    const int* __restrict__ toff, const int* __restrict__ sorted_gauss, int M, const float* __restrict__ density,
+    const __bf16* __restrict__ fsp, float* __restrict__ pair_partials, __bf16* __restrict__ wt) {
+    __shared__ BsSmem sm;
+    const int T = scene_tiles(G);
+    const int tb = uniform(xcd_remap(blockIdx.x, gridDim.x));   // the batch's tile (its list)
+    if (tb >= T * G.scenes) return;
+    const int j0 = uniform(min(max(toff[tb], 0), M));
+    const int Ng = uniform(min(max(toff[tb + 1], j0), M)) - j0;
+    if (Ng <= 0 || Ng > kBsMax) return;
+    const int scene = uniform(tb / T), tile = tb - scene * T;
+    typedef typename std::conditional<BF, __bf16, float>::type GT;   // element of grad_feats
+    const GT* gF = static_cast<const GT*>(gF_);
+    if (scene > 0) {   // the scene's voxel rows
+        const int64_t vb = scene * scene_voxels(G);
+        gD += vb;
+        density += vb;
+        gF += vb * C;
+    }
+    const int lane = threadIdx.x & 63, wave = uniform(threadIdx.x >> 6);
+    int x, y, z;
+    tile_voxel(G, tile, lane, x, y, z);   // voxel row lane of the tile
+    if (threadIdx.x < 64) {
+        const bool ok = in_grid(G, x, y, z);
+        const int64_t v = ok ? voxel_index(G, x, y, z) : 0;
+        sm.vlin[lane] = ok ? (int)v : -1;
+        sm.gD[lane] = ok ? gD[v] : 0.0f;
+        sm.D[lane] = ok ? density[v] : 0.0f;
+        sm.inv[lane] = ok ? 1.0f / fmaxf(density[v], kEps) : 0.0f;
+    }
+    stage_params(sm.pt, sorted_gauss + j0, Ng, means, cov_inv, opacity, lb, ub);
+    __syncthreads();
+
+    // U: thread (voxel lane, slots 8 wave + i) over 32-channel chunks staged in LDS
+    const int rowlen = nchk * 2 * kBtKc;   // bf16 per split feature row
+    float u[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) u[i] = 0.0f;
+    for (int c0 = 0; c0 < C; c0 += kBsKc) {
+        {   // gF: voxel row r, channels c0 + 8q .. c0 + 8q + 7 (zero past the row or outside the grid)
+            const int r = threadIdx.x >> 2, q = threadIdx.x & 3;
+            const int vr = sm.vlin[r];
+            const GT* src = gF + (int64_t)max(vr, 0) * C;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int c = c0 + 8 * q + i;
+                sm.g[r][8 * q + i] = (vr >= 0 && c < C) ? (float)src[min(c, C - 1)] : 0.0f;
+            }
+        }
+        {   // features: slot s (the zero row past the list), channels c0 + 4o .. c0 + 4o + 3
+            const int sl = threadIdx.x >> 3, o = threadIdx.x & 7;
+            const int g = sl < Ng ? sm.pt.gid[sl] : n;
+            const __bf16* row = fsp + (int64_t)g * rowlen;
+            float fv[4];
+            if constexpr (BF) {   // the values themselves, 64-channel chunks: element c at offset c
+                const uint2 hv = *reinterpret_cast<const uint2*>(row + c0 + 4 * o);
+                fv[0] = __uint_as_float(hv.x << 16);
+                fv[1] = __uint_as_float(hv.x & 0xffff0000u);
+                fv[2] = __uint_as_float(hv.y << 16);
+                fv[3] = __uint_as_float(hv.y & 0xffff0000u);
+            } else {              // chunk c0 / 32: hi[32] then lo[32]
+                const __bf16* ck = row + (c0 / kBtKc) * (2 * kBtKc);
+                const uint2 hv = *reinterpret_cast<const uint2*>(ck + 4 * o);
+                const uint2 lv = *reinterpret_cast<const uint2*>(ck + kBtKc + 4 * o);
+                fv[0] = __uint_as_float(hv.x << 16) + __uint_as_float(lv.x << 16);
+                fv[1] = __uint_as_float(hv.x & 0xffff0000u) + __uint_as_float(lv.x & 0xffff0000u);
+                fv[2] = __uint_as_float(hv.y << 16) + __uint_as_float(lv.y << 16);
+                fv[3] = __uint_as_float(hv.y & 0xffff0000u) + __uint_as_float(lv.y & 0xffff0000u);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sm.f[4 * o + i][sl] = fv[i];
+        }
+        __syncthreads();
+#pragma unroll 4
+        for (int c = 0; c < kBsKc; ++c) {
+            const float a = sm.g[lane][c];
+            const float4 f0 = *reinterpret_cast<const float4*>(&sm.f[c][8 * wave]);
+            const float4 f1 = *reinterpret_cast<const float4*>(&sm.f[c][8 * wave + 4]);
+            u[0] = fmaf(a, f0.x, u[0]);
+            u[1] = fmaf(a, f0.y, u[1]);
+            u[2] = fmaf(a, f0.z, u[2]);
+            u[3] = fmaf(a, f0.w, u[3]);
+            u[4] = fmaf(a, f1.x, u[4]);
+            u[5] = fmaf(a, f1.y, u[5]);
+            u[6] = fmaf(a, f1.z, u[6]);
+            u[7] = fmaf(a, f1.w, u[7]);
+        }
+        __syncthreads();
+    }
+
+    // split weights of every pair (row lane of the pair's weight row) and t_v from U
+    const bool rowok = sm.vlin[lane] >= 0;
+    const float inv = sm.inv[lane];
+    float tsum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int slot = 8 * wave + i;
+        if (slot >= Ng) break;   // wave-uniform
+        GaussParams p;
+        read_params(sm.pt, slot, p);
+        float dx, dy, dz;
+        bool in;
+        const float e0 = voxel_e(G, p, x, y, z, dx, dy, dz, in);
+        const float e = (rowok && in) ? e0 : 0.0f;
+        const float w = p.o * e;
+        const float wtil = w * inv;
+        __bf16 hs, ls;
+        split_bf16(wtil, hs, ls);
+        __bf16* wrow = wt + (int64_t)(j0 + slot) * kWtRow;
+        wrow[lane] = hs;
+        wrow[64 + lane] = ls;
+        tsum += (w > 0.0f) ? wtil * u[i] : 0.0f;
+    }
+    sm.tpart[wave][lane] = tsum;
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        const float s = ((sm.tpart[0][lane] + sm.tpart[1][lane]) + sm.tpart[2][lane]) + sm.tpart[3][lane];
+        // sum_g [w>0] w u / max(D, eps) = sum_c gF F; zero where D < eps (reference .cu:1450)
+        sm.tv[lane] = (rowok && sm.D[lane] >= kEps) ? s : 0.0f;
+    }
+    __syncthreads();
+
+    // r = gw e and its moments over the tile's voxels (d = centre - mu), as k_bwd_tile stores them
+    const float tv = sm.tv[lane], gd = sm.gD[lane];
+    const int tyz = G.tiles[1] * G.tiles[2];
+    const int tx = tile / tyz, ty = (tile - tx * tyz) / G.tiles[2], tz = tile % G.tiles[2];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int slot = 8 * wave + i;
+        if (slot >= Ng) break;   // wave-uniform
+        GaussParams p;
+        read_params(sm.pt, slot, p);
+        float dx, dy, dz;
+        bool in;
+        const float e0 = voxel_e(G, p, x, y, z, dx, dy, dz, in);
+        const float gw = gd + (u[i] - tv) * inv;
+        const float r = (rowok && in) ? gw * e0 : 0.0f;
+        float m[kNumGrads] = {r * dx, r * dy, r * dz, r * dx * dx, r * dy * dy, r * dz * dz,
+                              r * dx * dy, r * dx * dz, r * dy * dz, r};
+#pragma unroll
+        for (int k = 0; k < kNumGrads; ++k) m[k] = wave_sum(m[k]);
+        if (lane == 0) {
+            const int g = sm.pt.gid[slot];
+            const int tx0 = p.lb[0] / kTile, ty0 = p.lb[1] / kTile, tz0 = p.lb[2] / kTile;
+            const int ey = p.ub[1] / kTile - ty0 + 1, ez = p.ub[2] / kTile - tz0 + 1;
+            const int64_t pair = (int64_t)g2t_offsets[g] + ((tx - tx0) * ey + (ty - ty0)) * ez + (tz - tz0);
+            if (pair >= 0 && pair < M) {   // malformed CSR: never write outside the buffer
+                float* out = pair_partials + pair * kNumGrads;
+#pragma unroll
+                for (int k = 0; k < kNumGrads - 1; ++k) out[k] = p.o * m[k];
+                out[kNumGrads - 1] = m[kNumGrads - 1];
+            }
         }
     }
 }
@@ -1731,10 +1932,23 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
         const int blocks = (int)ceil_div(T, 8) * 8;
         // 16-byte G loads: 4 float or 8 bfloat16 channels per load, rows 16-byte aligned
         const bool vec = (C & (fdt == kDtBF16 ? 7 : 3)) == 0 && ((uintptr_t)grad_feats & 15) == 0;
+        // lists of at most kBsMax Gaussians go to k_bwd_tile_short (not with the fused cosine
+        // gradient, whose tiles all take k_bwd_tile)
+        const int skip_le = cos ? 0 : kBsMax;
+        if (!cos) {
+            if (fdt == kDtBF16)
+                G2V_LAUNCH(k_bwd_tile_short<true>, dim3(blocks), dim3(kBsThreads), 0, s, G, n, C, nchk, grad_density,
+                           grad_feats, means, opacity, cov_inv, lb, ub, g2t_offsets, tile_offsets, sorted_gauss, (int)M,
+                           density, (const __bf16*)b.fsp, b.partials, b.wt);
+            else
+                G2V_LAUNCH(k_bwd_tile_short<false>, dim3(blocks), dim3(kBsThreads), 0, s, G, n, C, nchk, grad_density,
+                           grad_feats, means, opacity, cov_inv, lb, ub, g2t_offsets, tile_offsets, sorted_gauss, (int)M,
+                           density, (const __bf16*)b.fsp, b.partials, b.wt);
+        }
 #define G2V_BT(V, F, FU)                                                                                      \
     G2V_LAUNCH((k_bwd_tile<V, F, FU>), dim3(blocks), dim3(kBtThreads), 0, s, G, n, C, nchk, grad_density,          \
                grad_feats, means, opacity, cov_inv, lb, ub, g2t_offsets, tile_offsets, sorted_gauss, (int)M, density,        \
-               grid_feats, fdt, (const __bf16*)b.fsp, b.partials, b.wt, cg)
+               grid_feats, fdt, (const __bf16*)b.fsp, b.partials, b.wt, cg, skip_le)
         if (cos) {
             G2V_BT(true, false, true);
         } else if (fdt == kDtBF16) {

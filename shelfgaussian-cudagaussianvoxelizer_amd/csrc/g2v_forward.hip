@@ -349,6 +349,35 @@ __device__ __forceinline__ void fwd_build_w(FwdSmem& sm, int j0, int kbeg, int k
     }
 }
 
+// Density and features of a tile that no Gaussian touches: zero (the general path forms the same
+// zeros and stores them from one wave per 128 channels).  Every wave of the workgroup stores whole
+// columns (x, y): a column's voxel rows z0 .. z0 + nz - 1 are one contiguous run.
+template <bool OBF16>
+__device__ __forceinline__ void fwd_zero_tile(const Grid& G, int tile, int C, float* __restrict__ density,
+                                                        void* __restrict__ grid_feats_out) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int x, y, z;
+    tile_voxel(G, tile, lane, x, y, z);
+    if (threadIdx.x < 64 && in_grid(G, x, y, z)) density[voxel_index(G, x, y, z)] = 0.0f;
+    const int x0 = x & ~(kTile - 1), y0 = y & ~(kTile - 1), z0 = z & ~(kTile - 1);
+    constexpr int kEs = OBF16 ? 2 : 4;
+    const int64_t run = (int64_t)min(kTile, G.dims[2] - z0) * C * kEs;   // bytes of a column
+    for (int c = wave; c < kTile * kTile; c += kFwdWaves) {
+        const int xc = x0 + (c >> 2), yc = y0 + (c & 3);
+        if (xc >= G.dims[0] || yc >= G.dims[1]) continue;   // wave-uniform
+        char* dst = static_cast<char*>(grid_feats_out) + voxel_index(G, xc, yc, z0) * C * kEs;
+        if (((uintptr_t)dst & 15) == 0 && (run & 15) == 0) {
+            for (int64_t b = (int64_t)lane * 16; b < run; b += 64 * 16)
+                __builtin_nontemporal_store(f32x4{0.0f, 0.0f, 0.0f, 0.0f}, reinterpret_cast<f32x4*>(dst + b));
+        } else {
+            for (int64_t b = (int64_t)lane * kEs; b < run; b += 64 * kEs) {
+                if constexpr (OBF16) *reinterpret_cast<unsigned short*>(dst + b) = 0;
+                else *reinterpret_cast<float*>(dst + b) = 0.0f;
+            }
+        }
+    }
+}
+
 // OBF16: grid_feats is stored as bfloat16 (rounded to nearest even), else float.
 template <bool OBF16>
 __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
@@ -368,6 +397,12 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
         density += vb;
         grid_feats_out = static_cast<char*>(grid_feats_out) + vb * C * (OBF16 ? 2 : 4);
     }
+    const int j0 = uniform(min(max(toff[tb], 0), M));
+    const int Ng = uniform(min(max(toff[tb + 1], j0), M)) - j0;
+    if (Ng == 0) {   // no Gaussian touches the tile
+        fwd_zero_tile<OBF16>(G, tile, C, density, grid_feats_out);
+        return;
+    }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int jl = lane & 31, kh = lane >> 5;
 
@@ -381,8 +416,6 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
     const int col = threadIdx.x & 15;
     const float cxl = centre(G, 0, x0 + (col >> 2)), cyl = centre(G, 1, y0 + (col & 3));
 
-    const int j0 = uniform(min(max(toff[tb], 0), M));
-    const int Ng = uniform(min(max(toff[tb + 1], j0), M)) - j0;
     const int nkc = (Ng + kFwdKMax - 1) / kFwdKMax;
     constexpr uint32_t kCh = OBF16 ? 2u : 4u;   // packed bytes per channel
     const uint32_t row_bytes = (uint32_t)Cp * kCh;
