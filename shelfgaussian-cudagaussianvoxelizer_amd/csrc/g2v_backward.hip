@@ -1029,6 +1029,69 @@ __global__ void __launch_bounds__(kBsThreads) k_bwd_tile_short(
     const int lane = threadIdx.x & 63, wave = uniform(threadIdx.x >> 6);
     int x, y, z;
     tile_voxel(G, tile, lane, x, y, z);   // voxel row lane of the tile
+
+    // Staging roles.  gF: voxel row sr, channels 8 sq .. 8 sq + 7 of a chunk.  Features: slot fs
+    // (the zero row past the list), channels 4 fo .. 4 fo + 3.  A chunk's values are loaded into
+    // registers one chunk ahead (the first chunk's loads go out with the tile's own), stored to
+    // LDS at the chunk's start.
+    const int sr = threadIdx.x >> 2, sq = threadIdx.x & 3;
+    const int fs = threadIdx.x >> 3, fo = threadIdx.x & 7;
+    int rx, ry, rz;
+    tile_voxel(G, tile, sr, rx, ry, rz);
+    const bool srok = in_grid(G, rx, ry, rz);
+    const GT* gsrc = gF + (srok ? voxel_index(G, rx, ry, rz) : 0) * C;
+    const bool gvec = (C & 7) == 0 && ((uintptr_t)gF & 15) == 0;   // 16-byte row pieces
+    const int rowlen = nchk * 2 * kBtKc;                              // bf16 per split feature row
+    const __bf16* frow = fsp + (int64_t)(fs < Ng ? sorted_gauss[j0 + fs] : n) * rowlen;
+    float gv[8], fv[4];
+    auto load_g = [&](int c0) {
+        const int c = c0 + 8 * sq;
+        if (gvec) {   // whole octets: C % 8 == 0
+            if (c < C) {
+                if constexpr (BF) {
+                    const uint4 h = *reinterpret_cast<const uint4*>(gsrc + c);
+                    const unsigned w[4] = {h.x, h.y, h.z, h.w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        gv[2 * i] = __uint_as_float(w[i] << 16);
+                        gv[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+                    }
+                } else {
+                    const float4 q0 = *reinterpret_cast<const float4*>(gsrc + c);
+                    const float4 q1 = *reinterpret_cast<const float4*>(gsrc + c + 4);
+                    gv[0] = q0.x; gv[1] = q0.y; gv[2] = q0.z; gv[3] = q0.w;
+                    gv[4] = q1.x; gv[5] = q1.y; gv[6] = q1.z; gv[7] = q1.w;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) gv[i] = 0.0f;
+            }
+        } else {      // every element loaded (clamped into the row) before any is masked
+#pragma unroll
+            for (int i = 0; i < 8; ++i) gv[i] = (float)gsrc[min(c + i, C - 1)];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) gv[i] = c + i < C ? gv[i] : 0.0f;
+        }
+    };
+    auto load_f = [&](int c0) {
+        if constexpr (BF) {   // the values themselves, 64-channel chunks: element c at offset c
+            const uint2 hv = *reinterpret_cast<const uint2*>(frow + c0 + 4 * fo);
+            fv[0] = __uint_as_float(hv.x << 16);
+            fv[1] = __uint_as_float(hv.x & 0xffff0000u);
+            fv[2] = __uint_as_float(hv.y << 16);
+            fv[3] = __uint_as_float(hv.y & 0xffff0000u);
+        } else {              // chunk c0 / 32: hi[32] then lo[32]
+            const __bf16* ck = frow + (c0 / kBtKc) * (2 * kBtKc);
+            const uint2 hv = *reinterpret_cast<const uint2*>(ck + 4 * fo);
+            const uint2 lv = *reinterpret_cast<const uint2*>(ck + kBtKc + 4 * fo);
+            fv[0] = __uint_as_float(hv.x << 16) + __uint_as_float(lv.x << 16);
+            fv[1] = __uint_as_float(hv.x & 0xffff0000u) + __uint_as_float(lv.x & 0xffff0000u);
+            fv[2] = __uint_as_float(hv.y << 16) + __uint_as_float(lv.y << 16);
+            fv[3] = __uint_as_float(hv.y & 0xffff0000u) + __uint_as_float(lv.y & 0xffff0000u);
+        }
+    };
+    load_g(0);
+    load_f(0);
     if (threadIdx.x < 64) {
         const bool ok = in_grid(G, x, y, z);
         const int64_t v = ok ? voxel_index(G, x, y, z) : 0;
@@ -1038,48 +1101,21 @@ __global__ void __launch_bounds__(kBsThreads) k_bwd_tile_short(
         sm.inv[lane] = ok ? 1.0f / fmaxf(density[v], kEps) : 0.0f;
     }
     stage_params(sm.pt, sorted_gauss + j0, Ng, means, cov_inv, opacity, lb, ub);
-    __syncthreads();
 
     // U: thread (voxel lane, slots 8 wave + i) over 32-channel chunks staged in LDS
-    const int rowlen = nchk * 2 * kBtKc;   // bf16 per split feature row
     float u[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) u[i] = 0.0f;
     for (int c0 = 0; c0 < C; c0 += kBsKc) {
-        {   // gF: voxel row r, channels c0 + 8q .. c0 + 8q + 7 (zero past the row or outside the grid)
-            const int r = threadIdx.x >> 2, q = threadIdx.x & 3;
-            const int vr = sm.vlin[r];
-            const GT* src = gF + (int64_t)max(vr, 0) * C;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int c = c0 + 8 * q + i;
-                sm.g[r][8 * q + i] = (vr >= 0 && c < C) ? (float)src[min(c, C - 1)] : 0.0f;
-            }
-        }
-        {   // features: slot s (the zero row past the list), channels c0 + 4o .. c0 + 4o + 3
-            const int sl = threadIdx.x >> 3, o = threadIdx.x & 7;
-            const int g = sl < Ng ? sm.pt.gid[sl] : n;
-            const __bf16* row = fsp + (int64_t)g * rowlen;
-            float fv[4];
-            if constexpr (BF) {   // the values themselves, 64-channel chunks: element c at offset c
-                const uint2 hv = *reinterpret_cast<const uint2*>(row + c0 + 4 * o);
-                fv[0] = __uint_as_float(hv.x << 16);
-                fv[1] = __uint_as_float(hv.x & 0xffff0000u);
-                fv[2] = __uint_as_float(hv.y << 16);
-                fv[3] = __uint_as_float(hv.y & 0xffff0000u);
-            } else {              // chunk c0 / 32: hi[32] then lo[32]
-                const __bf16* ck = row + (c0 / kBtKc) * (2 * kBtKc);
-                const uint2 hv = *reinterpret_cast<const uint2*>(ck + 4 * o);
-                const uint2 lv = *reinterpret_cast<const uint2*>(ck + kBtKc + 4 * o);
-                fv[0] = __uint_as_float(hv.x << 16) + __uint_as_float(lv.x << 16);
-                fv[1] = __uint_as_float(hv.x & 0xffff0000u) + __uint_as_float(lv.x & 0xffff0000u);
-                fv[2] = __uint_as_float(hv.y << 16) + __uint_as_float(lv.y << 16);
-                fv[3] = __uint_as_float(hv.y & 0xffff0000u) + __uint_as_float(lv.y & 0xffff0000u);
-            }
+        for (int i = 0; i < 8; ++i) sm.g[sr][8 * sq + i] = srok ? gv[i] : 0.0f;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sm.f[4 * o + i][sl] = fv[i];
+        for (int i = 0; i < 4; ++i) sm.f[4 * fo + i][fs] = fv[i];
+        __syncthreads();   // also orders the tile's own values and parameters before their reads
+        if (c0 + kBsKc < C) {   // the next chunk's loads run under this chunk's products
+            load_g(c0 + kBsKc);
+            load_f(c0 + kBsKc);
         }
-        __syncthreads();
 #pragma unroll 4
         for (int c = 0; c < kBsKc; ++c) {
             const float a = sm.g[lane][c];
@@ -1144,21 +1180,20 @@ __global__ void __launch_bounds__(kBsThreads) k_bwd_tile_short(
         const float e0 = voxel_e(G, p, x, y, z, dx, dy, dz, in);
         const float gw = gd + (u[i] - tv) * inv;
         const float r = (rowok && in) ? gw * e0 : 0.0f;
-        float m[kNumGrads] = {r * dx, r * dy, r * dz, r * dx * dx, r * dy * dy, r * dz * dz,
-                              r * dx * dy, r * dx * dz, r * dy * dz, r};
-#pragma unroll
-        for (int k = 0; k < kNumGrads; ++k) m[k] = wave_sum(m[k]);
-        if (lane == 0) {
+        const float m[16] = {r * dx, r * dy, r * dz, r * dx * dx, r * dy * dy, r * dz * dz,
+                             r * dx * dy, r * dx * dz, r * dy * dz, r, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        // lanes 2k and 2k + 1 of each half-wave get the half's sum of m[k]; lane 2k adds the other
+        // half's and stores value k of the pair
+        float t = transpose_sum16(m, lane & 31);
+        t += __shfl_down(t, 32, 64);
+        const int k = lane >> 1;
+        if ((lane & 1) == 0 && k < kNumGrads) {
             const int g = sm.pt.gid[slot];
             const int tx0 = p.lb[0] / kTile, ty0 = p.lb[1] / kTile, tz0 = p.lb[2] / kTile;
             const int ey = p.ub[1] / kTile - ty0 + 1, ez = p.ub[2] / kTile - tz0 + 1;
             const int64_t pair = (int64_t)g2t_offsets[g] + ((tx - tx0) * ey + (ty - ty0)) * ez + (tz - tz0);
-            if (pair >= 0 && pair < M) {   // malformed CSR: never write outside the buffer
-                float* out = pair_partials + pair * kNumGrads;
-#pragma unroll
-                for (int k = 0; k < kNumGrads - 1; ++k) out[k] = p.o * m[k];
-                out[kNumGrads - 1] = m[kNumGrads - 1];
-            }
+            if (pair >= 0 && pair < M)   // malformed CSR: never write outside the buffer
+                pair_partials[pair * kNumGrads + k] = k < kNumGrads - 1 ? p.o * t : t;
         }
     }
 }

@@ -378,6 +378,141 @@ __device__ __forceinline__ void fwd_zero_tile(const Grid& G, int tile, int C, fl
     }
 }
 
+// ------------------------------------------------------------------------------------------
+// Tiles whose list holds at most kFsMax Gaussians, empty ones included.  k_fwd_feats keeps two
+// tiles per CU (its LDS holds a 224-Gaussian K chunk), so a short list leaves that tile's chain of
+// loads and barriers bare; here a 4-wave workgroup with about 10 KB of LDS takes the tile and many
+// run per CU.  The weights are those of fwd_build_w (the same operations), the density their sum
+// (in another order), the features float32 sums of max(w, 0) f over the list in its order, read
+// straight from the caller's features.  Which kernel takes a tile depends on its list length
+// alone.
+// ------------------------------------------------------------------------------------------
+constexpr int kFsThreads = 256;
+constexpr int kFsMax = 32;          // longest list taken
+constexpr int kFsStride = kFsMax + 4;   // weight row of a voxel: 16-byte aligned, few bank conflicts
+
+struct FsSmem {
+    alignas(16) float w[64][kFsStride];   // feature weights max(w, 0): [voxel row][slot]
+    float dpart[kFsThreads / 64][64];
+    float inv[64];
+    int vlin[64];
+    int gid[kFsMax];
+};
+
+template <bool OBF16>
+__global__ void __launch_bounds__(kFsThreads) k_fwd_short(
+    Grid G, int C, const float* __restrict__ means, const float* __restrict__ opacity,
+    const float* __restrict__ cov_inv, const int* __restrict__ lb, const int* __restrict__ ub,
+    const int* __restrict__ toff, const int* __restrict__ sorted_gauss, int M, const void* __restrict__ features,
+    float* __restrict__ density, void* __restrict__ grid_feats_out) {
+    __shared__ FsSmem sm;
+    const int T = scene_tiles(G);
+    const int tb = uniform(xcd_remap(blockIdx.x, gridDim.x));   // the batch's tile (its list)
+    if (tb >= T * G.scenes) return;
+    const int j0 = uniform(min(max(toff[tb], 0), M));
+    const int Ng = uniform(min(max(toff[tb + 1], j0), M)) - j0;
+    if (Ng > kFsMax) return;   // k_fwd_feats takes the tile
+    const int scene = uniform(tb / T), tile = tb - scene * T;
+    {
+        const int64_t vb = scene * scene_voxels(G);
+        density += vb;
+        grid_feats_out = static_cast<char*>(grid_feats_out) + vb * C * (OBF16 ? 2 : 4);
+    }
+    if (Ng == 0) {   // no Gaussian touches the tile
+        fwd_zero_tile<OBF16>(G, tile, C, density, grid_feats_out);
+        return;
+    }
+    typedef typename std::conditional<OBF16, __bf16, float>::type FT;   // element of the features
+    const FT* feats = static_cast<const FT*>(features);
+    const int lane = threadIdx.x & 63, wave = uniform(threadIdx.x >> 6);
+    int x, y, z;
+    tile_voxel(G, tile, lane, x, y, z);   // voxel row lane of the tile
+    const float cx = centre(G, 0, x), cy = centre(G, 1, y), cz = centre(G, 2, z);
+
+    // weights of voxel row lane against slots 8 wave .. 8 wave + 7 (fwd_build_w's operations)
+    float dsum = 0.0f;
+#pragma unroll 1
+    for (int i = 0; i < 8; ++i) {
+        const int slot = 8 * wave + i;
+        float wf = 0.0f;
+        if (slot < Ng) {   // wave-uniform
+            const int g = uniform(sorted_gauss[j0 + slot]);
+            float A[9];
+#pragma unroll
+            for (int k = 0; k < 9; ++k) A[k] = cov_inv[g * 9 + k];
+            const float a00 = kq * A[0], a01 = kq * (A[1] + A[3]), a11 = kq * A[4];
+            const float a02 = kq * (A[2] + A[6]), a12 = kq * (A[5] + A[7]), a22 = kq * A[8];
+            const bool inxy = x >= lb[g * 3] && x <= ub[g * 3] && y >= lb[g * 3 + 1] && y <= ub[g * 3 + 1];
+            const bool inz = z >= lb[g * 3 + 2] && z <= ub[g * 3 + 2];
+            const float dx = cx - means[g * 3], dy = cy - means[g * 3 + 1], dz = cz - means[g * 3 + 2];
+            const float fz = inz ? a22 * dz * dz : -__builtin_inff();
+            float F = fmaf(fmaf(a00, dx, a01 * dy), dx, a11 * dy * dy);
+            F = inxy ? F : -__builtin_inff();
+            const float Gxy = fmaf(a02, dx, a12 * dy);
+            const float w = opacity[g] * __builtin_amdgcn_exp2f(fmaf(Gxy, dz, F) + fz);
+            dsum += w;
+            wf = fmaxf(w, 0.0f);   // feature gate of the reference (.cu:936)
+            if (lane == 0) sm.gid[slot] = g;
+        }
+        sm.w[lane][slot] = wf;
+    }
+    sm.dpart[wave][lane] = dsum;
+    __syncthreads();
+    if (wave == 0) {
+        const float D = ((sm.dpart[0][lane] + sm.dpart[1][lane]) + sm.dpart[2][lane]) + sm.dpart[3][lane];
+        const bool ok = in_grid(G, x, y, z);
+        const int v = ok ? (int)voxel_index(G, x, y, z) : -1;
+        sm.inv[lane] = 1.0f / fmaxf(D, kEps);
+        sm.vlin[lane] = v;
+        if (ok) density[v] = D;
+    }
+    __syncthreads();
+
+    // features: wave w owns voxel rows 16 w .. 16 w + 15, lane = channel of a 64-channel block;
+    // the list is taken 8 slots at a time (slots past it have weight 0 and read as 0)
+    for (int cb = 0; cb < C; cb += 64) {
+        const int c = cb + lane;
+        const int cc = min(c, C - 1);
+        float acc[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+        for (int s0 = 0; s0 < Ng; s0 += 8) {
+            float f[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {   // every load issued before the first product
+                const int sl = s0 + k;
+                const int g = uniform(sm.gid[min(sl, Ng - 1)]);   // a uniform row base: one offset register for all
+                f[k] = sl < Ng ? (float)feats[(int64_t)g * C + cc] : 0.0f;
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float* wr = &sm.w[16 * wave + r][s0];
+                const float4 wa = *reinterpret_cast<const float4*>(wr);
+                const float4 wb = *reinterpret_cast<const float4*>(wr + 4);
+                acc[r] = fmaf(wa.x, f[0], acc[r]);
+                acc[r] = fmaf(wa.y, f[1], acc[r]);
+                acc[r] = fmaf(wa.z, f[2], acc[r]);
+                acc[r] = fmaf(wa.w, f[3], acc[r]);
+                acc[r] = fmaf(wb.x, f[4], acc[r]);
+                acc[r] = fmaf(wb.y, f[5], acc[r]);
+                acc[r] = fmaf(wb.z, f[6], acc[r]);
+                acc[r] = fmaf(wb.w, f[7], acc[r]);
+            }
+        }
+        if (c < C) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = 16 * wave + r;
+                const int v = sm.vlin[row];
+                if (v < 0) continue;
+                const float o = acc[r] * sm.inv[row];
+                if constexpr (OBF16) static_cast<__bf16*>(grid_feats_out)[(int64_t)v * C + c] = (__bf16)o;
+                else __builtin_nontemporal_store(o, static_cast<float*>(grid_feats_out) + (int64_t)v * C + c);
+            }
+        }
+    }
+}
+
 // OBF16: grid_feats is stored as bfloat16 (rounded to nearest even), else float.
 template <bool OBF16>
 __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
@@ -385,7 +520,7 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
     const float* __restrict__ cov_inv, const int* __restrict__ lb, const int* __restrict__ ub,
     const int* __restrict__ toff, const int* __restrict__ sorted_gauss, int M, int n, int Cp,
     const uint32_t* __restrict__ fpk, float* __restrict__ density,
-    void* __restrict__ grid_feats_out) {
+    void* __restrict__ grid_feats_out, int skip_le) {
     __shared__ FwdSmem sm;
     const int T = scene_tiles(G);
     // tb: the batch's tile (its list), tile: the scene's
@@ -399,6 +534,7 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
     }
     const int j0 = uniform(min(max(toff[tb], 0), M));
     const int Ng = uniform(min(max(toff[tb + 1], j0), M)) - j0;
+    if (Ng <= skip_le) return;   // k_fwd_short takes the tile
     if (Ng == 0) {   // no Gaussian touches the tile
         fwd_zero_tile<OBF16>(G, tile, C, density, grid_feats_out);
         return;
@@ -621,12 +757,18 @@ hipError_t launch_forward_feats(const Grid& G, int C, const float* means, const 
         G2V_LAUNCH(k_split_pack<float>, dim3(pblocks), dim3(256), 0, s, static_cast<const float*>(features), n, C,
                    Cp, fpk);
     const int blocks = (int)ceil_div(T, 8) * 8;
-    if (fdt == kDtBF16)
+    // lists of at most kFsMax Gaussians (empty ones included) in k_fwd_short, the others in k_fwd_feats
+    if (fdt == kDtBF16) {
+        G2V_LAUNCH(k_fwd_short<true>, dim3(blocks), dim3(kFsThreads), 0, s, G, C, means, opacity, cov_inv, lb, ub,
+                   tile_offsets, sorted_gauss, M, features, density, grid_feats);
         G2V_LAUNCH(k_fwd_feats<true>, dim3(blocks), dim3(kFwdThreads), 0, s, G, C, means, opacity, cov_inv, lb, ub,
-                   tile_offsets, sorted_gauss, M, n, Cp, (const uint32_t*)fpk, density, grid_feats);
-    else
+                   tile_offsets, sorted_gauss, M, n, Cp, (const uint32_t*)fpk, density, grid_feats, kFsMax);
+    } else {
+        G2V_LAUNCH(k_fwd_short<false>, dim3(blocks), dim3(kFsThreads), 0, s, G, C, means, opacity, cov_inv, lb, ub,
+                   tile_offsets, sorted_gauss, M, features, density, grid_feats);
         G2V_LAUNCH(k_fwd_feats<false>, dim3(blocks), dim3(kFwdThreads), 0, s, G, C, means, opacity, cov_inv, lb,
-                   ub, tile_offsets, sorted_gauss, M, n, Cp, (const uint32_t*)fpk, density, grid_feats);
+                   ub, tile_offsets, sorted_gauss, M, n, Cp, (const uint32_t*)fpk, density, grid_feats, kFsMax);
+    }
     return hipGetLastError();
 }
 
