@@ -355,13 +355,22 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
     const int* __restrict__ g2t_offsets, const int* __restrict__ toff,
     const int* __restrict__ sorted_gauss, int M, const float* __restrict__ density,
     const void* __restrict__ grid_feats, int gdt, const __bf16* __restrict__ fsp,
-    float* __restrict__ pair_partials, __bf16* __restrict__ wt, CosG cg, int skip_le) {
+    float* __restrict__ pair_partials, __bf16* __restrict__ wt, CosG cg, int skip_le,
+    const int* __restrict__ tlist, const int* __restrict__ tcount) {
     static_assert(!FU || (VEC && !BF), "the fused cosine gradient takes 16-byte float32 rows");
     __shared__ BtSmem<FU> sm;
     const int T = scene_tiles(G);
-    // tb: the batch's tile (its list), tile: the scene's
-    const int tb = uniform(xcd_remap(blockIdx.x, gridDim.x));
-    if (tb >= T * G.scenes) return;
+    // tb: the batch's tile (its list), tile: the scene's; with tlist, workgroup i takes the i-th
+    // long tile of the compacted list
+    int tb;
+    if (tlist) {
+        const int i = uniform(xcd_remap(blockIdx.x, gridDim.x));
+        if (i >= uniform(*tcount)) return;
+        tb = uniform(tlist[i]);
+    } else {
+        tb = uniform(xcd_remap(blockIdx.x, gridDim.x));
+        if (tb >= T * G.scenes) return;
+    }
     const int j0 = uniform(min(max(toff[tb], 0), M));
     const int Ng = uniform(min(max(toff[tb + 1], j0), M)) - j0;
     if (Ng <= skip_le) return;   // empty, or a short list that k_bwd_tile_short takes
@@ -963,22 +972,22 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
 }
 
 // ------------------------------------------------------------------------------------------
-// Phase A for short lists (1 .. kBsMax Gaussians).  k_bwd_tile holds one tile per CU (its LDS is
+// Phase A for short lists (1 .. smax <= kBsMax Gaussians).  k_bwd_tile holds one tile per CU (its LDS is
 // sized for 256-Gaussian passes), so a short list leaves that tile's chain of loads and barriers
 // bare; here a 4-wave workgroup with about 17 KB of LDS takes the tile and many run per CU.  The
 // per-pair results are those of k_bwd_tile up to float32 rounding: U = G F^T from float32 products
 // of gF and the split features' hi + lo (the matrix-core path leaves out lo x lo), t_v from U,
 // the same e (the same helper operations) and so the same split weights, and the moments summed
 // over the voxels in another order.  Which kernel takes a tile depends on its list length alone.
-// Thread = (voxel row lane, Gaussian slots 8 wave .. 8 wave + 7).
+// Thread = (voxel row lane, Gaussian slots wave + 4 i): the slots are dealt round robin over the waves.
 // ------------------------------------------------------------------------------------------
 constexpr int kBsThreads = 256;
-constexpr int kBsMax = 32;     // longest list taken
+constexpr int kBsMax = 64;     // longest list the kernel can take
 constexpr int kBsKc = 32;      // channels per staged chunk
 
 struct BsSmem {
     float g[64][kBsKc + 1];    // gF chunk, voxel-major; rows padded so that lanes (voxels) hit distinct banks
-    float f[kBsKc][kBsMax];    // feature chunk, channel-major: a wave reads its 8 Gaussians of a channel at once
+    float f[kBsKc][4][kBsMax / 4];   // feature chunk: [channel][wave][i] of slot wave + 4 i (a wave reads its slots at once)
     ParamTile<kBsMax> pt;
     int vlin[64];
     float gD[64], inv[64], D[64], tv[64];
@@ -1009,14 +1018,14 @@ __global__ void __launch_bounds__(kBsThreads) k_bwd_tile_short(
     const float* __restrict__ means, const float* __restrict__ opacity, const float* __restrict__ cov_inv,
     const int* __restrict__ lb, const int* __restrict__ ub, const int* __restrict__ g2t_offsets,
     const int* __restrict__ toff, const int* __restrict__ sorted_gauss, int M, const float* __restrict__ density,
-    const __bf16* __restrict__ fsp, float* __restrict__ pair_partials, __bf16* __restrict__ wt) {
+    const __bf16* __restrict__ fsp, float* __restrict__ pair_partials, __bf16* __restrict__ wt, int smax) {
     __shared__ BsSmem sm;
     const int T = scene_tiles(G);
     const int tb = uniform(xcd_remap(blockIdx.x, gridDim.x));   // the batch's tile (its list)
     if (tb >= T * G.scenes) return;
     const int j0 = uniform(min(max(toff[tb], 0), M));
     const int Ng = uniform(min(max(toff[tb + 1], j0), M)) - j0;
-    if (Ng <= 0 || Ng > kBsMax) return;
+    if (Ng <= 0 || Ng > smax) return;
     const int scene = uniform(tb / T), tile = tb - scene * T;
     typedef typename std::conditional<BF, __bf16, float>::type GT;   // element of grad_feats
     const GT* gF = static_cast<const GT*>(gF_);
@@ -1030,8 +1039,8 @@ __global__ void __launch_bounds__(kBsThreads) k_bwd_tile_short(
     int x, y, z;
     tile_voxel(G, tile, lane, x, y, z);   // voxel row lane of the tile
 
-    // Staging roles.  gF: voxel row sr, channels 8 sq .. 8 sq + 7 of a chunk.  Features: slot fs
-    // (the zero row past the list), channels 4 fo .. 4 fo + 3.  A chunk's values are loaded into
+    // Staging roles.  gF: voxel row sr, channels 8 sq .. 8 sq + 7 of a chunk.  Features: slots fs
+    // and fs + 32 (the zero row past the list), channels 4 fo .. 4 fo + 3.  A chunk's values are loaded into
     // registers one chunk ahead (the first chunk's loads go out with the tile's own), stored to
     // LDS at the chunk's start.
     const int sr = threadIdx.x >> 2, sq = threadIdx.x & 3;
@@ -1042,8 +1051,11 @@ __global__ void __launch_bounds__(kBsThreads) k_bwd_tile_short(
     const GT* gsrc = gF + (srok ? voxel_index(G, rx, ry, rz) : 0) * C;
     const bool gvec = (C & 7) == 0 && ((uintptr_t)gF & 15) == 0;   // 16-byte row pieces
     const int rowlen = nchk * 2 * kBtKc;                              // bf16 per split feature row
-    const __bf16* frow = fsp + (int64_t)(fs < Ng ? sorted_gauss[j0 + fs] : n) * rowlen;
-    float gv[8], fv[4];
+    const __bf16* frow[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+        frow[h] = fsp + (int64_t)(fs + 32 * h < Ng ? sorted_gauss[j0 + fs + 32 * h] : n) * rowlen;
+    float gv[8], fv[2][4];
     auto load_g = [&](int c0) {
         const int c = c0 + 8 * sq;
         if (gvec) {   // whole octets: C % 8 == 0
@@ -1074,20 +1086,23 @@ __global__ void __launch_bounds__(kBsThreads) k_bwd_tile_short(
         }
     };
     auto load_f = [&](int c0) {
-        if constexpr (BF) {   // the values themselves, 64-channel chunks: element c at offset c
-            const uint2 hv = *reinterpret_cast<const uint2*>(frow + c0 + 4 * fo);
-            fv[0] = __uint_as_float(hv.x << 16);
-            fv[1] = __uint_as_float(hv.x & 0xffff0000u);
-            fv[2] = __uint_as_float(hv.y << 16);
-            fv[3] = __uint_as_float(hv.y & 0xffff0000u);
-        } else {              // chunk c0 / 32: hi[32] then lo[32]
-            const __bf16* ck = frow + (c0 / kBtKc) * (2 * kBtKc);
-            const uint2 hv = *reinterpret_cast<const uint2*>(ck + 4 * fo);
-            const uint2 lv = *reinterpret_cast<const uint2*>(ck + kBtKc + 4 * fo);
-            fv[0] = __uint_as_float(hv.x << 16) + __uint_as_float(lv.x << 16);
-            fv[1] = __uint_as_float(hv.x & 0xffff0000u) + __uint_as_float(lv.x & 0xffff0000u);
-            fv[2] = __uint_as_float(hv.y << 16) + __uint_as_float(lv.y << 16);
-            fv[3] = __uint_as_float(hv.y & 0xffff0000u) + __uint_as_float(lv.y & 0xffff0000u);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            if constexpr (BF) {   // the values themselves, 64-channel chunks: element c at offset c
+                const uint2 hv = *reinterpret_cast<const uint2*>(frow[h] + c0 + 4 * fo);
+                fv[h][0] = __uint_as_float(hv.x << 16);
+                fv[h][1] = __uint_as_float(hv.x & 0xffff0000u);
+                fv[h][2] = __uint_as_float(hv.y << 16);
+                fv[h][3] = __uint_as_float(hv.y & 0xffff0000u);
+            } else {              // chunk c0 / 32: hi[32] then lo[32]
+                const __bf16* ck = frow[h] + (c0 / kBtKc) * (2 * kBtKc);
+                const uint2 hv = *reinterpret_cast<const uint2*>(ck + 4 * fo);
+                const uint2 lv = *reinterpret_cast<const uint2*>(ck + kBtKc + 4 * fo);
+                fv[h][0] = __uint_as_float(hv.x << 16) + __uint_as_float(lv.x << 16);
+                fv[h][1] = __uint_as_float(hv.x & 0xffff0000u) + __uint_as_float(lv.x & 0xffff0000u);
+                fv[h][2] = __uint_as_float(hv.y << 16) + __uint_as_float(lv.y << 16);
+                fv[h][3] = __uint_as_float(hv.y & 0xffff0000u) + __uint_as_float(lv.y & 0xffff0000u);
+            }
         }
     };
     load_g(0);
@@ -1102,15 +1117,21 @@ __global__ void __launch_bounds__(kBsThreads) k_bwd_tile_short(
     }
     stage_params(sm.pt, sorted_gauss + j0, Ng, means, cov_inv, opacity, lb, ub);
 
-    // U: thread (voxel lane, slots 8 wave + i) over 32-channel chunks staged in LDS
-    float u[8];
+    // U: thread (voxel lane, slots wave + 4 i) over 32-channel chunks staged in LDS; a wave
+    // multiplies only its slots' quads that hold list entries
+    const int nq = uniform((max(Ng - wave, 0) + 15) / 16);   // quads of 4 slots with an entry
+    float u[16];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) u[i] = 0.0f;
+    for (int i = 0; i < 16; ++i) u[i] = 0.0f;
     for (int c0 = 0; c0 < C; c0 += kBsKc) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) sm.g[sr][8 * sq + i] = srok ? gv[i] : 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sm.f[4 * fo + i][fs] = fv[i];
+        for (int h = 0; h < 2; ++h) {
+            const int sl = fs + 32 * h;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sm.f[4 * fo + i][sl & 3][sl >> 2] = fv[h][i];
+        }
         __syncthreads();   // also orders the tile's own values and parameters before their reads
         if (c0 + kBsKc < C) {   // the next chunk's loads run under this chunk's products
             load_g(c0 + kBsKc);
@@ -1119,16 +1140,16 @@ __global__ void __launch_bounds__(kBsThreads) k_bwd_tile_short(
 #pragma unroll 4
         for (int c = 0; c < kBsKc; ++c) {
             const float a = sm.g[lane][c];
-            const float4 f0 = *reinterpret_cast<const float4*>(&sm.f[c][8 * wave]);
-            const float4 f1 = *reinterpret_cast<const float4*>(&sm.f[c][8 * wave + 4]);
-            u[0] = fmaf(a, f0.x, u[0]);
-            u[1] = fmaf(a, f0.y, u[1]);
-            u[2] = fmaf(a, f0.z, u[2]);
-            u[3] = fmaf(a, f0.w, u[3]);
-            u[4] = fmaf(a, f1.x, u[4]);
-            u[5] = fmaf(a, f1.y, u[5]);
-            u[6] = fmaf(a, f1.z, u[6]);
-            u[7] = fmaf(a, f1.w, u[7]);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if (q < nq) {   // wave-uniform
+                    const float4 f4 = *reinterpret_cast<const float4*>(&sm.f[c][wave][4 * q]);
+                    u[4 * q] = fmaf(a, f4.x, u[4 * q]);
+                    u[4 * q + 1] = fmaf(a, f4.y, u[4 * q + 1]);
+                    u[4 * q + 2] = fmaf(a, f4.z, u[4 * q + 2]);
+                    u[4 * q + 3] = fmaf(a, f4.w, u[4 * q + 3]);
+                }
+            }
         }
         __syncthreads();
     }
@@ -1138,8 +1159,8 @@ __global__ void __launch_bounds__(kBsThreads) k_bwd_tile_short(
     const float inv = sm.inv[lane];
     float tsum = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int slot = 8 * wave + i;
+    for (int i = 0; i < 16; ++i) {
+        const int slot = wave + 4 * i;
         if (slot >= Ng) break;   // wave-uniform
         GaussParams p;
         read_params(sm.pt, slot, p);
@@ -1170,8 +1191,8 @@ __global__ void __launch_bounds__(kBsThreads) k_bwd_tile_short(
     const int tyz = G.tiles[1] * G.tiles[2];
     const int tx = tile / tyz, ty = (tile - tx * tyz) / G.tiles[2], tz = tile % G.tiles[2];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int slot = 8 * wave + i;
+    for (int i = 0; i < 16; ++i) {
+        const int slot = wave + 4 * i;
         if (slot >= Ng) break;   // wave-uniform
         GaussParams p;
         read_params(sm.pt, slot, p);
@@ -1862,6 +1883,7 @@ struct FeatBufs {
     int* roff;
     void* sort_ws;
     float* gpart;
+    int* tl;
     size_t bytes;
 };
 
@@ -1884,6 +1906,10 @@ static FeatBufs carve_feats(void* ws, const Grid& G, int n, int C, int64_t M, in
     b.roff = c.take<int>(nreg + 1);
     b.sort_ws = c.take<char>(sort_workspace(MR, nreg));
     b.gpart = c.take<float>(mr * (C > 0 ? C : 1));
+    {   // long-tile list of phase A: a count, then at most min(T, M) tiles
+        const int64_t T = (int64_t)scene_tiles(G) * G.scenes;
+        b.tl = c.take<int>(1 + (M < T ? M : T));
+    }
     b.bytes = c.off + 256;
     return b;
 }
@@ -1967,24 +1993,37 @@ hipError_t launch_backward_feats(const Grid& G, int n, int C, const float* grad_
         const int blocks = (int)ceil_div(T, 8) * 8;
         // 16-byte G loads: 4 float or 8 bfloat16 channels per load, rows 16-byte aligned
         const bool vec = (C & (fdt == kDtBF16 ? 7 : 3)) == 0 && ((uintptr_t)grad_feats & 15) == 0;
-        // lists of at most kBsMax Gaussians go to k_bwd_tile_short (not with the fused cosine
-        // gradient, whose tiles all take k_bwd_tile)
-        const int skip_le = cos ? 0 : kBsMax;
+        // lists of at most short_list_max(C) Gaussians go to k_bwd_tile_short (not with the fused
+        // cosine gradient, whose tiles all take k_bwd_tile).  When fewer tiles can be long than
+        // there are tiles (a sparse problem), k_bwd_tile walks a compacted list of the long ones.
+        const int skip_le = cos ? 0 : min(short_list_max(C), kBsMax);
+        const int nlong = long_tiles_bound(M, T, skip_le);
+        const int* tlist = nullptr;
+        const int* tcount = nullptr;
+        if (nlong < T && nlong > 0) {
+            const hipError_t e = launch_long_tiles(tile_offsets, T, (int)M, skip_le, b.tl, b.tl + 1, nlong, s);
+            if (e != hipSuccess) return e;
+            tcount = b.tl;
+            tlist = b.tl + 1;
+        }
+        const int lblocks = (int)ceil_div(nlong, 8) * 8;
         if (!cos) {
             if (fdt == kDtBF16)
                 G2V_LAUNCH(k_bwd_tile_short<true>, dim3(blocks), dim3(kBsThreads), 0, s, G, n, C, nchk, grad_density,
                            grad_feats, means, opacity, cov_inv, lb, ub, g2t_offsets, tile_offsets, sorted_gauss, (int)M,
-                           density, (const __bf16*)b.fsp, b.partials, b.wt);
+                           density, (const __bf16*)b.fsp, b.partials, b.wt, skip_le);
             else
                 G2V_LAUNCH(k_bwd_tile_short<false>, dim3(blocks), dim3(kBsThreads), 0, s, G, n, C, nchk, grad_density,
                            grad_feats, means, opacity, cov_inv, lb, ub, g2t_offsets, tile_offsets, sorted_gauss, (int)M,
-                           density, (const __bf16*)b.fsp, b.partials, b.wt);
+                           density, (const __bf16*)b.fsp, b.partials, b.wt, skip_le);
         }
 #define G2V_BT(V, F, FU)                                                                                      \
-    G2V_LAUNCH((k_bwd_tile<V, F, FU>), dim3(blocks), dim3(kBtThreads), 0, s, G, n, C, nchk, grad_density,          \
+    G2V_LAUNCH((k_bwd_tile<V, F, FU>), dim3(lblocks), dim3(kBtThreads), 0, s, G, n, C, nchk, grad_density,         \
                grad_feats, means, opacity, cov_inv, lb, ub, g2t_offsets, tile_offsets, sorted_gauss, (int)M, density,        \
-               grid_feats, fdt, (const __bf16*)b.fsp, b.partials, b.wt, cg, skip_le)
-        if (cos) {
+               grid_feats, fdt, (const __bf16*)b.fsp, b.partials, b.wt, cg, skip_le, tlist, tcount)
+        if (nlong == 0) {
+            // every list is short: k_bwd_tile_short took them all
+        } else if (cos) {
             G2V_BT(true, false, true);
         } else if (fdt == kDtBF16) {
             if (vec) G2V_BT(true, true, false);

@@ -65,6 +65,7 @@ struct SplatBufs {
     int* tile_offsets;
     void* sort_ws;
     uint32_t* fpk;      // features as packed bf16 (hi, lo) pairs, forward only
+    int* tl;            // long-tile list of the forward (count, then the list), forward only
     size_t bytes;
 };
 
@@ -80,6 +81,7 @@ SplatBufs carve_splat(void* ws, int n, int64_t M, const Grid& G, int feat_dim = 
     b.tile_offsets = c.take<int>(T + 1);
     b.sort_ws = c.take<char>(sort_workspace(M, T));
     b.fpk = feat_dim > 0 ? c.take<uint32_t>((int64_t)(n + 1) * packed_channels(feat_dim)) : nullptr;
+    b.tl = feat_dim > 0 ? c.take<int>(long_list_ints(M, T, feat_dim)) : nullptr;
     b.bytes = c.off + 256;
     return b;
 }
@@ -321,7 +323,7 @@ int splat_impl(const Grid& G, int n, int feat_dim, const float* means3D, const f
     if (feat_dim > 0)
         G2V_HIP(launch_forward_feats(G, feat_dim, means3D, opacity, cov_inv, valid_voxel_lb,
                                      valid_voxel_ub, b.tile_offsets, b.sorted_gauss, (int)num_pairs, n,
-                                     features, feat_dtype, b.fpk, density, grid_feats, s));
+                                     features, feat_dtype, b.fpk, density, grid_feats, b.tl, s));
     else
         G2V_HIP(launch_forward_density(G, means3D, opacity, cov_inv, valid_voxel_lb, valid_voxel_ub,
                                        b.tile_offsets, b.sorted_gauss, (int)num_pairs, density, s));

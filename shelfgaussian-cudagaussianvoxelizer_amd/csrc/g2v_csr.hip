@@ -643,6 +643,42 @@ hipError_t launch_tile_offsets(const int* sorted_keys, int64_t M, int T, int* ti
 }
 
 // ------------------------------------------------------------------------------------------
+// Long tiles: the tiles whose list holds more than smax Gaussians, compacted into list[0 .. *count)
+// (at most cap entries; a long tile holds at least smax + 1 of the M pairs, so the caller's cap of
+// M / (smax + 1) always suffices).  One atomic add per wave places the wave's long tiles, in tile
+// order within the wave; the order across waves is unspecified (each tile is computed alone, so the
+// order changes no result).  *count must be zero beforehand.
+// ------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) k_long_tiles(const int* __restrict__ toff, int T, int M, int smax,
+                                                    int* __restrict__ count, int* __restrict__ list, int cap) {
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    bool lng = false;
+    if (t < T) {
+        const int a = min(max(toff[t], 0), M);
+        const int b = min(max(toff[t + 1], a), M);
+        lng = b - a > smax;
+    }
+    const uint64_t m = __ballot(lng);
+    if (m == 0) return;
+    const int lane = threadIdx.x & 63;
+    int base = 0;
+    if (lane == __builtin_ctzll(m)) base = atomicAdd(count, __popcll(m));
+    base = __shfl(base, __builtin_ctzll(m), 64);
+    if (lng) {
+        const int pos = base + __popcll(m & ((1ull << lane) - 1ull));
+        if (pos < cap) list[pos] = t;
+    }
+}
+
+hipError_t launch_long_tiles(const int* toff, int T, int M, int smax, int* count, int* list, int cap,
+                             hipStream_t s) {
+    hipError_t e = launch_fill_i32(1, 0, count, s);
+    if (e != hipSuccess || T <= 0) return e;
+    G2V_LAUNCH(k_long_tiles, dim3((unsigned)ceil_div(T, 256)), dim3(256), 0, s, toff, T, M, smax, count, list, cap);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------------
 // Run-length encoding of the sorted tile ids (unique tiles, run lengths, run offsets, count).
 // ------------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) k_rle_flags(const int* __restrict__ toff, int T,

@@ -379,7 +379,7 @@ __device__ __forceinline__ void fwd_zero_tile(const Grid& G, int tile, int C, fl
 }
 
 // ------------------------------------------------------------------------------------------
-// Tiles whose list holds at most kFsMax Gaussians, empty ones included.  k_fwd_feats keeps two
+// Tiles whose list holds at most smax <= kFsMax Gaussians, empty ones included.  k_fwd_feats keeps two
 // tiles per CU (its LDS holds a 224-Gaussian K chunk), so a short list leaves that tile's chain of
 // loads and barriers bare; here a 4-wave workgroup with about 10 KB of LDS takes the tile and many
 // run per CU.  The weights are those of fwd_build_w (the same operations), the density their sum
@@ -388,7 +388,7 @@ __device__ __forceinline__ void fwd_zero_tile(const Grid& G, int tile, int C, fl
 // alone.
 // ------------------------------------------------------------------------------------------
 constexpr int kFsThreads = 256;
-constexpr int kFsMax = 32;          // longest list taken
+constexpr int kFsMax = 64;          // longest list the kernel can take
 constexpr int kFsStride = kFsMax + 4;   // weight row of a voxel: 16-byte aligned, few bank conflicts
 
 struct FsSmem {
@@ -404,14 +404,14 @@ __global__ void __launch_bounds__(kFsThreads) k_fwd_short(
     Grid G, int C, const float* __restrict__ means, const float* __restrict__ opacity,
     const float* __restrict__ cov_inv, const int* __restrict__ lb, const int* __restrict__ ub,
     const int* __restrict__ toff, const int* __restrict__ sorted_gauss, int M, const void* __restrict__ features,
-    float* __restrict__ density, void* __restrict__ grid_feats_out) {
+    float* __restrict__ density, void* __restrict__ grid_feats_out, int smax) {
     __shared__ FsSmem sm;
     const int T = scene_tiles(G);
     const int tb = uniform(xcd_remap(blockIdx.x, gridDim.x));   // the batch's tile (its list)
     if (tb >= T * G.scenes) return;
     const int j0 = uniform(min(max(toff[tb], 0), M));
     const int Ng = uniform(min(max(toff[tb + 1], j0), M)) - j0;
-    if (Ng > kFsMax) return;   // k_fwd_feats takes the tile
+    if (Ng > smax) return;   // k_fwd_feats takes the tile
     const int scene = uniform(tb / T), tile = tb - scene * T;
     {
         const int64_t vb = scene * scene_voxels(G);
@@ -429,11 +429,12 @@ __global__ void __launch_bounds__(kFsThreads) k_fwd_short(
     tile_voxel(G, tile, lane, x, y, z);   // voxel row lane of the tile
     const float cx = centre(G, 0, x), cy = centre(G, 1, y), cz = centre(G, 2, z);
 
-    // weights of voxel row lane against slots 8 wave .. 8 wave + 7 (fwd_build_w's operations)
+    // weights of voxel row lane against slots wave + 4 i (fwd_build_w's operations); every slot's
+    // weight is written, 0 past the list
     float dsum = 0.0f;
 #pragma unroll 1
-    for (int i = 0; i < 8; ++i) {
-        const int slot = 8 * wave + i;
+    for (int i = 0; i < kFsMax / 4; ++i) {
+        const int slot = wave + 4 * i;
         float wf = 0.0f;
         if (slot < Ng) {   // wave-uniform
             const int g = uniform(sorted_gauss[j0 + slot]);
@@ -520,12 +521,20 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
     const float* __restrict__ cov_inv, const int* __restrict__ lb, const int* __restrict__ ub,
     const int* __restrict__ toff, const int* __restrict__ sorted_gauss, int M, int n, int Cp,
     const uint32_t* __restrict__ fpk, float* __restrict__ density,
-    void* __restrict__ grid_feats_out, int skip_le) {
+    void* __restrict__ grid_feats_out, int skip_le, const int* __restrict__ tlist, const int* __restrict__ tcount) {
     __shared__ FwdSmem sm;
     const int T = scene_tiles(G);
-    // tb: the batch's tile (its list), tile: the scene's
-    const int tb = uniform(xcd_remap(blockIdx.x, gridDim.x));
-    if (tb >= T * G.scenes) return;
+    // tb: the batch's tile (its list), tile: the scene's; with tlist, workgroup i takes the i-th
+    // long tile of the compacted list
+    int tb;
+    if (tlist) {
+        const int i = uniform(xcd_remap(blockIdx.x, gridDim.x));
+        if (i >= uniform(*tcount)) return;
+        tb = uniform(tlist[i]);
+    } else {
+        tb = uniform(xcd_remap(blockIdx.x, gridDim.x));
+        if (tb >= T * G.scenes) return;
+    }
     const int scene = uniform(tb / T), tile = tb - scene * T;
     {
         const int64_t vb = scene * scene_voxels(G);
@@ -740,7 +749,7 @@ hipError_t launch_forward_feats(const Grid& G, int C, const float* means, const 
                                 const float* cov_inv, const int* lb, const int* ub,
                                 const int* tile_offsets, const int* sorted_gauss, int M, int n,
                                 const void* features, int fdt, uint32_t* fpk, float* density,
-                                void* grid_feats, hipStream_t s) {
+                                void* grid_feats, int* tl_ws, hipStream_t s) {
     const int T = scene_tiles(G) * G.scenes;
     if (T <= 0) return hipSuccess;
     if (C <= 0)
@@ -757,17 +766,35 @@ hipError_t launch_forward_feats(const Grid& G, int C, const float* means, const 
         G2V_LAUNCH(k_split_pack<float>, dim3(pblocks), dim3(256), 0, s, static_cast<const float*>(features), n, C,
                    Cp, fpk);
     const int blocks = (int)ceil_div(T, 8) * 8;
-    // lists of at most kFsMax Gaussians (empty ones included) in k_fwd_short, the others in k_fwd_feats
+    // lists of at most short_list_max(C) Gaussians (empty ones included) in k_fwd_short, the others
+    // in k_fwd_feats.  When fewer tiles can be long than there are tiles (a sparse problem),
+    // k_fwd_feats walks a compacted list of the long ones instead of the whole grid: at one
+    // workgroup per CU, a grid of mostly empty workgroups costs tens of microseconds.
+    const int smax = min(short_list_max(C), kFsMax);
+    const int nlong = long_tiles_bound(M, T, smax);
+    const int* tlist = nullptr;
+    const int* tcount = nullptr;
+    if (nlong < T && nlong > 0) {
+        const hipError_t e = launch_long_tiles(tile_offsets, T, M, smax, tl_ws, tl_ws + 1, nlong, s);
+        if (e != hipSuccess) return e;
+        tcount = tl_ws;
+        tlist = tl_ws + 1;
+    }
+    const int lblocks = (int)ceil_div(nlong, 8) * 8;
     if (fdt == kDtBF16) {
         G2V_LAUNCH(k_fwd_short<true>, dim3(blocks), dim3(kFsThreads), 0, s, G, C, means, opacity, cov_inv, lb, ub,
-                   tile_offsets, sorted_gauss, M, features, density, grid_feats);
-        G2V_LAUNCH(k_fwd_feats<true>, dim3(blocks), dim3(kFwdThreads), 0, s, G, C, means, opacity, cov_inv, lb, ub,
-                   tile_offsets, sorted_gauss, M, n, Cp, (const uint32_t*)fpk, density, grid_feats, kFsMax);
+                   tile_offsets, sorted_gauss, M, features, density, grid_feats, smax);
+        if (nlong > 0)
+            G2V_LAUNCH(k_fwd_feats<true>, dim3(lblocks), dim3(kFwdThreads), 0, s, G, C, means, opacity, cov_inv, lb,
+                       ub, tile_offsets, sorted_gauss, M, n, Cp, (const uint32_t*)fpk, density, grid_feats, smax, tlist,
+                       tcount);
     } else {
         G2V_LAUNCH(k_fwd_short<false>, dim3(blocks), dim3(kFsThreads), 0, s, G, C, means, opacity, cov_inv, lb, ub,
-                   tile_offsets, sorted_gauss, M, features, density, grid_feats);
-        G2V_LAUNCH(k_fwd_feats<false>, dim3(blocks), dim3(kFwdThreads), 0, s, G, C, means, opacity, cov_inv, lb,
-                   ub, tile_offsets, sorted_gauss, M, n, Cp, (const uint32_t*)fpk, density, grid_feats, kFsMax);
+                   tile_offsets, sorted_gauss, M, features, density, grid_feats, smax);
+        if (nlong > 0)
+            G2V_LAUNCH(k_fwd_feats<false>, dim3(lblocks), dim3(kFwdThreads), 0, s, G, C, means, opacity, cov_inv, lb,
+                       ub, tile_offsets, sorted_gauss, M, n, Cp, (const uint32_t*)fpk, density, grid_feats, smax, tlist,
+                       tcount);
     }
     return hipGetLastError();
 }

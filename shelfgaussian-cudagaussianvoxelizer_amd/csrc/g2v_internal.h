@@ -79,6 +79,16 @@ hipError_t launch_tile_offsets(const int* sorted_keys, int64_t M, int T, int* ti
 hipError_t launch_rle(const int* tile_offsets, int T, int* unique_tiles, int* counts,
                       int* runs_offsets, int* num_runs, void* ws, hipStream_t s);
 
+// The tiles whose list holds more than smax Gaussians (of the M pairs of T tiles), compacted into
+// list[0 .. *count), in unspecified order; count is zeroed first.  cap >= long_tiles_bound(...).
+hipError_t launch_long_tiles(const int* toff, int T, int M, int smax, int* count, int* list, int cap,
+                             hipStream_t s);
+// At most this many tiles hold more than smax of M pairs.
+inline int long_tiles_bound(int64_t M, int T, int smax) {
+    const int64_t b = M / (smax + 1);
+    return (int)(b < T ? b : T);
+}
+
 // n ints of value v (a kernel, not a memset node: safe where a stream may be captured).
 hipError_t launch_fill_i32(int64_t n, int v, int* dst, hipStream_t s);
 
@@ -96,6 +106,12 @@ inline bool region_offsets_fit(const Grid& G, int C) {
     return (int64_t)16 * G.dims[1] * G.dims[2] * C < ((int64_t)1 << 31);
 }
 
+// Longest tile list that the short-list kernels (k_fwd_short, k_bwd_tile_short) take; longer lists
+// go to the matrix-core kernels.  It depends on C alone (never on the rest of the problem), so a
+// tile takes the same kernel in every call: 64 Gaussians up to 256 channels, where the short
+// kernels' float32 products stay cheaper than a tile slot of the matrix-core kernels, 32 above.
+inline int short_list_max(int C) { return C <= 256 ? 64 : 32; }
+
 hipError_t launch_forward_density(const Grid& G, const float* means, const float* opacity,
                                   const float* cov_inv, const int* lb, const int* ub,
                                   const int* tile_offsets, const int* sorted_gauss, int M,
@@ -104,7 +120,9 @@ hipError_t launch_forward_feats(const Grid& G, int C, const float* means, const 
                                 const float* cov_inv, const int* lb, const int* ub,
                                 const int* tile_offsets, const int* sorted_gauss, int M, int n,
                                 const void* features, int fdt, uint32_t* fpk, float* density,
-                                void* grid_feats, hipStream_t s);
+                                void* grid_feats, int* tl_ws, hipStream_t s);
+// ints of the long-tile list workspace (tl_ws) of a forward or backward with features.
+inline int long_list_ints(int64_t M, int T, int C) { return 1 + long_tiles_bound(M, T, short_list_max(C)); }
 
 // ---- backward (g2v_backward.hip) ----------------------------------------------------------
 hipError_t launch_backward_density(const Grid& G, int n, const float* grad_density,
