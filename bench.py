@@ -52,6 +52,8 @@ def parse():
                     help="skip the covariance-construction and batched-scenes legs")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="also run a plain device copy of this size (PMC scale reference)")
+    ap.add_argument("--batched-only", action="store_true",
+                    help="run only the batched-scenes leg (the recorded batch) and print its result (profiling)")
     return ap.parse_args()
 
 
@@ -292,7 +294,7 @@ def covariance_leg(_C, n, steps):
             "note": "back-to-back calls; at this size launch-latency bound, not HBM bound"}
 
 
-def batched_leg(steps, warmup):
+def batched_leg(steps, warmup, per_scene=True):
     """B scenes per call against one call per scene, on the reference's recorded training batch
     (tests/golden/mmdet_debug_inputs.npz: 6 groups of 300 Gaussians, 200x200x16 grid) with
     synthetic 64-D features: fwd+bwd through the module, wall time per batch."""
@@ -318,7 +320,7 @@ def batched_leg(steps, warmup):
             torch.autograd.backward([d, g], [torch.ones_like(d), torch.ones_like(g)])
 
     res = {}
-    for name, fn in (("batched", batched), ("per_scene", looped)):
+    for name, fn in (("batched", batched), ("per_scene", looped))[:2 if per_scene else 1]:
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize()
@@ -374,6 +376,14 @@ def main():
     import torch
     from CudaGaussianVoxelizer import _C, _lib
     from tests import workloads as W
+
+    if args.batched_only:
+        torch.cuda.set_device(torch.device("cuda", 0))
+        res = batched_leg(max(args.steps, 5), args.warmup, per_scene=False)
+        print(json.dumps({"metric": "batched scenes fwd+bwd ms (recorded batch, 6 x 300 Gaussians, 64-D)",
+                          "value": res["batched_ms"], "unit": "ms", "higher_is_better": False,
+                          "batched_scenes": res}), flush=True)
+        return
 
     w = W.CONFIGS[args.config]
     dev = torch.device("cuda", 0)
