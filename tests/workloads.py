@@ -50,8 +50,9 @@ def generate(w: Workload, seed: int = 0):
         means, opacity, cov, _, _ = mmdet_fixture()
         feats = None if w.feat_dim is None else torch.randn(means.shape[0], w.feat_dim, generator=g)
         return means, opacity, cov, feats
-    lo = torch.tensor(w.voxel_range[:3], dtype=torch.float32) - w.mean_pad
-    hi = torch.tensor(w.voxel_range[3:], dtype=torch.float32) + w.mean_pad
+    box = w.extra.get("mean_box", w.voxel_range)   # means drawn in this box (default: the grid's range)
+    lo = torch.tensor(box[:3], dtype=torch.float32) - w.mean_pad
+    hi = torch.tensor(box[3:], dtype=torch.float32) + w.mean_pad
     means = torch.rand(w.n, 3, generator=g) * (hi - lo) + lo
     if w.num_outside:
         lo0 = torch.tensor(w.voxel_range[:3], dtype=torch.float32)
