@@ -89,7 +89,7 @@ constexpr int kFwdThreads = 256;               // 4 waves
 constexpr int kFwdWaves = kFwdThreads / 64;
 constexpr int kFwdChanPerWave = 128;
 constexpr int kFwdChanPerPass = kFwdChanPerWave * kFwdWaves;
-constexpr int kFwdKMax = 224;                  // Gaussians held in LDS per K chunk (multiple of 32)
+constexpr int kFwdKMax = 256;                  // Gaussians held in LDS per K chunk (multiple of 32)
 constexpr int kFwdKSteps = kFwdKMax / 16;
 
 static_assert(kFwdChanPerWave == kPackedChannelAlign, "packed rows are padded to one wave's channels");
@@ -217,18 +217,18 @@ hipError_t launch_forward_density(const Grid& G, const float* means, const float
 //     F = a00 dx^2 + a01 dx dy + a11 dy^2,  Gxy = a02 dx + a12 dy,  fz_c = kq A22 dz_c^2,
 // with dx, dy the offsets of the voxel centre from the mean, a00 = kq A00, a01 = kq (A01 + A10),
 // a11 = kq A11, a02 = kq (A02 + A20), a12 = kq (A12 + A21), kq = -log2(e)/2, so that
-// exp2(...) = exp(-dx^T A dx / 2) (reference .cu:911-921).  A voxel outside the box in z has
-// fz_c = -inf; one outside it in x or y (bit 4a+b of xymask clear) gets F = -inf; either way the
-// weight is exactly 0, as the reference's box test makes it.
+// exp2(...) = exp(-dx^T A dx / 2) (reference .cu:911-921), dz_c = (z centre of layer c) - mu2 and
+// a22 = kq A22 formed by the thread that reads the record.  A voxel outside the box in z (bit c of
+// zmask clear) has fz_c = -inf; one outside it in x or y (bit 4a+b of xymask clear) gets F = -inf;
+// either way the weight is exactly 0, as the reference's box test makes it.  48 bytes, so that
+// the records of a whole 256-entry chunk fit beside its W at two workgroups per CU.
 struct alignas(16) FwdRec {
     float mux, muy, o, a12;
     float a00, a01, a11, a02;
-    float dz[4];
-    float fz[4];
-    uint32_t xymask;
-    uint32_t pad[3];
+    float mu2, a22;
+    uint32_t xymask, zmask;
 };
-static_assert(sizeof(FwdRec) == 80, "FwdRec is five 16-byte words");
+static_assert(sizeof(FwdRec) == 48, "FwdRec is three 16-byte words");
 
 struct FwdSmem {
     bf16x8 whi[kFwdKSteps][2][64];   // A operand, hi part: [k step][voxel block][lane]
@@ -279,16 +279,16 @@ __device__ __forceinline__ void fwd_build_w(FwdSmem& sm, int j0, int kbeg, int k
             r.a11 = kq * A[4];
             r.a02 = kq * (A[2] + A[6]);
             r.a12 = kq * (A[5] + A[7]);
-            const float a22 = kq * A[8];
-            uint32_t xm = 0, ym = 0;
+            r.mu2 = mu2;
+            r.a22 = kq * A[8];
+            uint32_t xm = 0, ym = 0, zm = 0;
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                const float dz = cz[c] - mu2;
-                r.dz[c] = dz;
-                r.fz[c] = (z0 + c >= l[2] && z0 + c <= u[2]) ? a22 * dz * dz : -__builtin_inff();
+                zm |= (z0 + c >= l[2] && z0 + c <= u[2]) ? (1u << c) : 0u;
                 xm |= (x0 + c >= l[0] && x0 + c <= u[0]) ? (1u << c) : 0u;
                 ym |= (y0 + c >= l[1] && y0 + c <= u[1]) ? (1u << c) : 0u;
             }
+            r.zmask = zm;
             uint32_t m = 0;
 #pragma unroll
             for (int a = 0; a < 4; ++a) m |= (xm >> a) & 1u ? ym << (4 * a) : 0u;
@@ -297,15 +297,10 @@ __device__ __forceinline__ void fwd_build_w(FwdSmem& sm, int j0, int kbeg, int k
         } else {
             r.mux = r.muy = r.o = r.a12 = 0.0f;
             r.a00 = r.a01 = r.a11 = r.a02 = 0.0f;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                r.dz[c] = 0.0f;
-                r.fz[c] = -__builtin_inff();
-            }
-            r.xymask = 0;
+            r.mu2 = r.a22 = 0.0f;
+            r.xymask = r.zmask = 0;
             sm.roff[k] = zero_off;
         }
-        r.pad[0] = r.pad[1] = r.pad[2] = 0;
         sm.rec[k] = r;
     }
     __syncthreads();
@@ -316,16 +311,19 @@ __device__ __forceinline__ void fwd_build_w(FwdSmem& sm, int j0, int kbeg, int k
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const uint4* rp = reinterpret_cast<const uint4*>(&sm.rec[o * 8 + i]);   // 16 lanes each
-            const uint4 q0 = rp[0], q1 = rp[1], q2 = rp[2], q3 = rp[3];
-            const uint32_t m = sm.rec[o * 8 + i].xymask;
+            const uint4 q0 = rp[0], q1 = rp[1], q2 = rp[2];
+            const uint32_t m = q2.z, zm = q2.w;
             const float dx = cxl - __uint_as_float(q0.x), dy = cyl - __uint_as_float(q0.y);
             const float ro = __uint_as_float(q0.z), a12 = __uint_as_float(q0.w);
             const float a00 = __uint_as_float(q1.x), a01 = __uint_as_float(q1.y);
             const float a11 = __uint_as_float(q1.z), a02 = __uint_as_float(q1.w);
-            const float dz[4] = {__uint_as_float(q2.x), __uint_as_float(q2.y), __uint_as_float(q2.z),
-                                 __uint_as_float(q2.w)};
-            const float fz[4] = {__uint_as_float(q3.x), __uint_as_float(q3.y), __uint_as_float(q3.z),
-                                 __uint_as_float(q3.w)};
+            const float mu2 = __uint_as_float(q2.x), a22 = __uint_as_float(q2.y);
+            float dz[4], fz[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                dz[c] = cz[c] - mu2;
+                fz[c] = ((zm >> c) & 1u) ? a22 * dz[c] * dz[c] : -__builtin_inff();
+            }
             float F = fmaf(fmaf(a00, dx, a01 * dy), dx, a11 * dy * dy);
             F = ((m >> col) & 1u) ? F : -__builtin_inff();
             const float Gxy = fmaf(a02, dx, a12 * dy);
