@@ -460,8 +460,10 @@ hipError_t launch_fill_cells(int n, const int* lb, const int* ub, const int* off
 
 // ------------------------------------------------------------------------------------------
 // Stable LSD radix sort, digits of <= 8 bits, only ceil(log2 T) key bits.
-//   per pass: k_radix_hist (digit counts per 4096-key block, digit-major) -> exclusive scan
-//             -> k_radix_scatter (stable rank: ballot match inside a wave, LDS across waves)
+//   per pass: k_radix_hist (digit counts per 4096-key block, digit-major) -> k_radix_digit_scan
+//             (one workgroup per digit: exclusive scan over the blocks, and the digit's total)
+//             -> k_radix_scatter (digit bases from the totals; stable rank: ballot match inside a
+//             wave, LDS across waves)
 // ------------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(kSortThreads) k_radix_hist(const int* __restrict__ keys, int64_t M,
                                                              int shift, int dbits, int nblk,
@@ -481,17 +483,84 @@ __global__ void __launch_bounds__(kSortThreads) k_radix_hist(const int* __restri
     for (int d = threadIdx.x; d < radix; d += kSortThreads) ghist[(int64_t)d * nblk + blockIdx.x] = h[d];
 }
 
+// Workgroup d: exclusive scan of digit d's block counts (row d of the digit-major histogram, in
+// place) and the digit's total.  The rows are independent, so every digit's scan runs at once
+// (one workgroup scanning the whole histogram would walk nblk x radix counts serially).
+constexpr int kDigitItems = 8;   // counts per thread per round
+__global__ void __launch_bounds__(kSortThreads) k_radix_digit_scan(int* __restrict__ ghist, int nblk,
+                                                                   int* __restrict__ dtot) {
+    __shared__ int wsum[kSortThreads / 64];
+    const int d = blockIdx.x;
+    int* row = ghist + (int64_t)d * nblk;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int carry = 0;
+    for (int base = 0; base < nblk; base += kSortThreads * kDigitItems) {
+        // thread t takes counts base + 8t .. base + 8t + 7
+        const int i0 = base + (int)threadIdx.x * kDigitItems;
+        int v[kDigitItems];
+        int local = 0;
+#pragma unroll
+        for (int k = 0; k < kDigitItems; ++k) {
+            v[k] = i0 + k < nblk ? row[i0 + k] : 0;
+            local += v[k];
+        }
+        int x = local;   // inclusive scan of the thread totals within the wave
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int t = __shfl_up(x, off, 64);
+            if (lane >= off) x += t;
+        }
+        if (lane == 63) wsum[wave] = x;
+        __syncthreads();
+        int wc = 0, tot = 0;
+#pragma unroll
+        for (int w = 0; w < kSortThreads / 64; ++w) {
+            wc += w < wave ? wsum[w] : 0;
+            tot += wsum[w];
+        }
+        int run = carry + wc + x - local;
+#pragma unroll
+        for (int k = 0; k < kDigitItems; ++k) {
+            if (i0 + k < nblk) row[i0 + k] = run;
+            run += v[k];
+        }
+        carry += tot;
+        __syncthreads();   // wsum is rewritten by the next round
+    }
+    if (threadIdx.x == 0) dtot[d] = carry;
+}
+
 __global__ void __launch_bounds__(kSortThreads) k_radix_scatter(
     const int* __restrict__ keys_in, const int* __restrict__ vals_in, int* __restrict__ keys_out,
     int* __restrict__ vals_out, int64_t M, int shift, int dbits, int nblk,
-    const int* __restrict__ gscan) {
+    const int* __restrict__ gscan, const int* __restrict__ dtot) {
+    static_assert(kSortThreads == 256, "one digit per thread");
     __shared__ int wave_cnt[4][256];
     __shared__ int running[256];
+    __shared__ int dsum[kSortThreads / 64];
     const int radix = 1 << dbits;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (int d = threadIdx.x; d < radix; d += kSortThreads) {
-        running[d] = gscan[(int64_t)d * nblk + blockIdx.x];
-        wave_cnt[0][d] = wave_cnt[1][d] = wave_cnt[2][d] = wave_cnt[3][d] = 0;
+    {
+        // digit base: exclusive scan of the digit totals (digit = thread), plus the block's own
+        // exclusive offset within its digit
+        const int d = threadIdx.x;
+        const int t = d < radix ? dtot[d] : 0;
+        const int blk = d < radix ? gscan[(int64_t)d * nblk + blockIdx.x] : 0;
+        int x = t;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int u = __shfl_up(x, off, 64);
+            if (lane >= off) x += u;
+        }
+        if (lane == 63) dsum[wave] = x;
+        __syncthreads();
+        int wc = 0;
+#pragma unroll
+        for (int w = 0; w < kSortThreads / 64; ++w) wc += w < wave ? dsum[w] : 0;
+        if (d < radix) {
+            running[d] = wc + x - t + blk;
+            wave_cnt[0][d] = wave_cnt[1][d] = wave_cnt[2][d] = wave_cnt[3][d] = 0;
+        }
     }
     __syncthreads();
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
@@ -555,7 +624,7 @@ struct SortBufs {
     int* pk;
     int* pv;
     int* hist;
-    void* scan_ws;
+    int* dtot;    // digit totals of the pass
     size_t bytes;
 };
 
@@ -570,7 +639,7 @@ static SortBufs carve_sort(void* ws, int64_t M, int num_tiles) {
     b.pk = c.take<int>(m);
     b.pv = c.take<int>(m);
     b.hist = c.take<int>(hist_n);
-    b.scan_ws = c.take<char>(scan_workspace(hist_n));
+    b.dtot = c.take<int>(256);
     b.bytes = c.off + 256;
     return b;
 }
@@ -588,12 +657,11 @@ hipError_t radix_sort_pairs(const int* keys_in, const int* vals_in, int* keys_ou
         return hipMemcpyAsync(vals_out, vals_in, M * sizeof(int), hipMemcpyDeviceToDevice, s);
     }
     const int nblk = (int)ceil_div(M, kSortTile);
-    const int64_t hist_n = (int64_t)(1 << dbits) * nblk;
     const SortBufs b = carve_sort(ws, M, num_tiles);
     int* pk = b.pk;
     int* pv = b.pv;
     int* hist = b.hist;
-    void* scan_ws = b.scan_ws;
+    int* dtot = b.dtot;
     const int* src_k = keys_in;
     const int* src_v = vals_in;
     for (int p = 0; p < passes; ++p) {
@@ -604,10 +672,9 @@ hipError_t radix_sort_pairs(const int* keys_in, const int* vals_in, int* keys_ou
         const int shift = p * dbits;
         G2V_LAUNCH(k_radix_hist, dim3(nblk), dim3(kSortThreads), 0, s, src_k, M, shift, dbits,
                            nblk, hist);
-        hipError_t e = scan_i32(hist, hist, hist_n, false, nullptr, scan_ws, s);
-        if (e != hipSuccess) return e;
+        G2V_LAUNCH(k_radix_digit_scan, dim3(1 << dbits), dim3(kSortThreads), 0, s, hist, nblk, dtot);
         G2V_LAUNCH(k_radix_scatter, dim3(nblk), dim3(kSortThreads), 0, s, src_k, src_v, dk, dv,
-                           M, shift, dbits, nblk, (const int*)hist);
+                           M, shift, dbits, nblk, (const int*)hist, (const int*)dtot);
         src_k = dk;
         src_v = dv;
     }
