@@ -75,17 +75,28 @@ int g2v_forward_plan_async(int n, const float* means3D, const float* covariances
                            void* bwd_plan_workspace, size_t bwd_plan_workspace_bytes, long long* counts,
                            void* stream);
 
+/* g2v_forward_pack_features: the features as the matrix-core splat gathers them (bfloat16
+ * (hi, lo) pairs of float32 values, bfloat16 values as they are; rows padded, plus a zero row)
+ * into packed (g2v_forward_packed_bytes(n, feat_dim) bytes).  It depends on the features alone,
+ * so a caller queues it before waiting for the plan's pair count (g2v_forward_plan_async), and
+ * it runs while the host waits.  Part of the reference's forward (.cu:1634-1904), which gathers
+ * the float32 rows directly.  Asynchronous. */
+size_t g2v_forward_packed_bytes(int n, int feat_dim);
+int g2v_forward_pack_features(int n, int feat_dim, const void* features, int feat_dtype, void* packed,
+                              size_t packed_bytes, void* stream);
+
 /* g2v_forward_splat: G->T fill, radix sort into the Tile->Gaussian CSR, per-tile splat of the
  * density and, when feat_dim > 0, of the density-weighted feature average (reference
  * .cu:1634-1904).  density (X,Y,Z) and grid_feats (X,Y,Z,feat_dim) are written completely;
- * features may be NULL when feat_dim == 0.  When t2g_tiles, t2g_gauss (M each) and t2g_offsets
- * (T+1) are all non-NULL the Tile->Gaussian CSR is built there (and can be handed to
- * g2v_backward, which then skips rebuilding it); otherwise it lives in the workspace.
- * Asynchronous. */
+ * features and packed_features may be NULL when feat_dim == 0; otherwise packed_features holds
+ * g2v_forward_pack_features's output for the same features, queued before on the same stream.
+ * When t2g_tiles, t2g_gauss (M each) and t2g_offsets (T+1) are all non-NULL the
+ * Tile->Gaussian CSR is built there (and can be handed to g2v_backward, which then skips
+ * rebuilding it); otherwise it lives in the workspace.  Asynchronous. */
 size_t g2v_forward_splat_workspace(int n, int feat_dim, long long num_pairs, const float voxel_size[3],
                                    const float voxel_range[6]);
 int g2v_forward_splat(int n, int feat_dim, const float* means3D, const float* opacity,
-                      const void* features, int feat_dtype, const float voxel_size[3],
+                      const void* features, int feat_dtype, const void* packed_features, const float voxel_size[3],
                       const float voxel_range[6], const float* cov_inv, const int* valid_voxel_lb,
                       const int* valid_voxel_ub, const int* g2t_offsets, long long num_pairs,
                       int* g2t_tile_ids, float* density, void* grid_feats, int* t2g_tiles, int* t2g_gauss,

@@ -88,6 +88,7 @@ def _stream(device):
 
 
 _EVENTS = {}
+_READY = {}
 
 
 def _timing_events(device):
@@ -99,6 +100,17 @@ def _timing_events(device):
     if ev is None:
         ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
         _EVENTS[key] = ev
+    return ev
+
+
+def _ready_event(device):
+    """An event per device and thread that marks where a host wait ends (no timing)."""
+    import threading
+    key = (device.index, threading.get_ident())
+    ev = _READY.get(key)
+    if ev is None:
+        ev = torch.cuda.Event()
+        _READY[key] = ev
     return ev
 
 
@@ -170,34 +182,47 @@ def _forward(means3D, opacity, covariances, voxel_size, voxel_range, features, k
         nvox = torch.empty(n, **i32)
         g2t_offsets = torch.empty(n + 1, **i32)
         ws = torch.empty(lib.g2v_forward_plan_workspace(n), dtype=torch.uint8, device=dev)
-        # outputs whose size does not depend on the plan's count, allocated before its host wait
-        density = torch.empty(X, Y, Z, **f32)
-        fdtype = torch.float32 if feats is None else feats.dtype
-        fdt = _FEAT_DTYPES[fdtype]
-        grid_feats = torch.empty(X, Y, Z, C, dtype=fdtype, device=dev)
-        t2g_toff = torch.empty(Tx * Ty * Tz + 1, **i32) if keep_t2g else None
-        start, stop = _timing_events(dev)
-        start.record(cur)
-        M = ctypes.c_longlong(0)
-        MR = ctypes.c_longlong(0)
         # with keep_t2g the backward's plan (the (region, Gaussian) pair count) is done here too,
-        # on the same synchronisation
+        # on the same wait
         bplan = (torch.empty(max(1, lib.g2v_backward_plan_workspace(n)), dtype=torch.uint8, device=dev)
                  if keep_t2g else None)
-        _lib.check(lib.g2v_forward_plan(n, _ptr(means), _ptr(cov), vs, vr, _ptr(cov_inv), _ptr(lb),
-                                        _ptr(ub), _ptr(nvox), _ptr(g2t_offsets), _ptr(ws),
-                                        ws.numel(), ctypes.byref(M), _ptr(bplan),
-                                        0 if bplan is None else bplan.numel(), ctypes.byref(MR), stream),
+        counts = _pinned_counts(dev, 2)
+        start, stop = _timing_events(dev)
+        start.record(cur)
+        _lib.check(lib.g2v_forward_plan_async(n, _ptr(means), _ptr(cov), vs, vr, _ptr(cov_inv), _ptr(lb),
+                                              _ptr(ub), _ptr(nvox), _ptr(g2t_offsets), _ptr(ws), ws.numel(),
+                                              _ptr(bplan), 0 if bplan is None else bplan.numel(), _ptr(counts),
+                                              stream),
                    "gaussian_voxelizer_forward (plan)")
-        M = int(M.value)
+        ready = _ready_event(dev)
+        ready.record(cur)
+        # queued behind the plan, so that they run while this thread waits for the pair counts:
+        # the features packed for the splat; then the outputs whose size does not depend on the
+        # counts are allocated
+        fdtype = torch.float32 if feats is None else feats.dtype
+        fdt = _FEAT_DTYPES[fdtype]
+        packed = None
+        if feats is not None:
+            packed = torch.empty(lib.g2v_forward_packed_bytes(n, C), dtype=torch.uint8, device=dev)
+            _lib.check(lib.g2v_forward_pack_features(n, C, _ptr(feats), fdt, _ptr(packed), packed.numel(), stream),
+                       "gaussian_voxelizer_forward (features)")
+        density = torch.empty(X, Y, Z, **f32)
+        grid_feats = torch.empty(X, Y, Z, C, dtype=fdtype, device=dev)
+        t2g_toff = torch.empty(Tx * Ty * Tz + 1, **i32) if keep_t2g else None
+        ready.synchronize()
+        M, MR = (int(v) for v in counts.tolist())
+        for cnt, what in ((M, "Gaussian-tile"), (MR, "region-Gaussian")):
+            if cnt > 2147483647:
+                raise RuntimeError(f"gaussian_voxelizer_forward (plan): {cnt} {what} pairs exceed the int32 CSR "
+                                   "(limit 2^31-1)")
         g2t_tile_ids = torch.empty(M, **i32)
         ws2 = torch.empty(lib.g2v_forward_splat_workspace(n, C, M, vs, vr), dtype=torch.uint8, device=dev)
         t2g = None
         csr = (None, None, None)
         if keep_t2g:
             csr = (torch.empty(M, **i32), torch.empty(M, **i32), t2g_toff)
-            t2g = dict(csr=csr, plan=bplan, num_region_pairs=int(MR.value), vs=vs, vr=vr, dims=(X, Y, Z))
-        _lib.check(lib.g2v_forward_splat(n, C, _ptr(means), _ptr(op), _ptr(feats), fdt, vs, vr,
+            t2g = dict(csr=csr, plan=bplan, num_region_pairs=MR, vs=vs, vr=vr, dims=(X, Y, Z))
+        _lib.check(lib.g2v_forward_splat(n, C, _ptr(means), _ptr(op), _ptr(feats), fdt, _ptr(packed), vs, vr,
                                          _ptr(cov_inv), _ptr(lb), _ptr(ub), _ptr(g2t_offsets), M,
                                          _ptr(g2t_tile_ids), _ptr(density), _ptr(grid_feats),
                                          _ptr(csr[0]), _ptr(csr[1]), _ptr(csr[2]),

@@ -69,7 +69,9 @@ struct SplatBufs {
     size_t bytes;
 };
 
-SplatBufs carve_splat(void* ws, int n, int64_t M, const Grid& G, int feat_dim = 0) {
+// with_packed: room for the packed features (a caller that packs them with
+// g2v_forward_pack_features passes its own buffer instead).
+SplatBufs carve_splat(void* ws, int n, int64_t M, const Grid& G, int feat_dim = 0, bool with_packed = true) {
     const int64_t m = M > 0 ? M : 1;
     const int T = num_tiles(G);
     Carver c(ws, (size_t)-1);
@@ -80,7 +82,7 @@ SplatBufs carve_splat(void* ws, int n, int64_t M, const Grid& G, int feat_dim = 
     b.sorted_gauss = c.take<int>(m);
     b.tile_offsets = c.take<int>(T + 1);
     b.sort_ws = c.take<char>(sort_workspace(M, T));
-    b.fpk = feat_dim > 0 ? c.take<uint32_t>((int64_t)(n + 1) * packed_channels(feat_dim)) : nullptr;
+    b.fpk = feat_dim > 0 && with_packed ? c.take<uint32_t>((int64_t)(n + 1) * packed_channels(feat_dim)) : nullptr;
     b.tl = feat_dim > 0 ? c.take<int>(long_list_ints(M, T, feat_dim)) : nullptr;
     b.bytes = c.off + 256;
     return b;
@@ -140,7 +142,7 @@ extern "C" {
 
 const char* g2v_last_error(void) { return g_err; }
 
-int g2v_abi_version(void) { return 11; }
+int g2v_abi_version(void) { return 12; }
 
 int g2v_grid_dims(const float voxel_size[3], const float voxel_range[6], int dims[3], int tiles[3]) {
     Grid G;
@@ -278,7 +280,30 @@ size_t g2v_forward_splat_workspace(int n, int feat_dim, long long num_pairs, con
                                    const float voxel_range[6]) {
     Grid G;
     if (make_grid(voxel_size, voxel_range, G) != G2V_OK) return 0;
-    return carve_splat(nullptr, n, num_pairs, G, feat_dim).bytes;
+    return carve_splat(nullptr, n, num_pairs, G, feat_dim, false).bytes;
+}
+
+size_t g2v_forward_packed_bytes(int n, int feat_dim) {
+    if (n < 0 || feat_dim <= 0) return 0;
+    return (size_t)(n + 1) * packed_channels(feat_dim) * 4;
+}
+
+int g2v_forward_pack_features(int n, int feat_dim, const void* features, int feat_dtype, void* packed,
+                              size_t packed_bytes, void* stream) {
+    g_err[0] = 0;
+    if (feat_dtype != G2V_DTYPE_F32 && feat_dtype != G2V_DTYPE_BF16)
+        return fail(G2V_ERR_INVALID, "feat_dtype = %d (G2V_DTYPE_F32 or G2V_DTYPE_BF16)", feat_dtype);
+    if (n < 0 || feat_dim < 0) return fail(G2V_ERR_INVALID, "n = %d, feat_dim = %d", n, feat_dim);
+    if (feat_dim == 0) return G2V_OK;
+    if (!packed_fits(n, feat_dim))
+        return fail(G2V_ERR_LIMIT, "n = %d x feat_dim = %d exceeds the packed feature rows (4 GiB)", n, feat_dim);
+    if (!packed || (n > 0 && !features)) return fail(G2V_ERR_INVALID, "null features / packed pointer");
+    const size_t need = g2v_forward_packed_bytes(n, feat_dim);
+    if (packed_bytes < need)
+        return fail(G2V_ERR_INVALID, "packed features buffer too small: %zu bytes, need %zu", packed_bytes, need);
+    G2V_HIP(launch_split_pack(n, feat_dim, features, feat_dtype, static_cast<uint32_t*>(packed),
+                              static_cast<hipStream_t>(stream)));
+    return G2V_OK;
 }
 
 }  // extern "C"
@@ -287,8 +312,10 @@ namespace {
 
 // The splat of n Gaussians (every scene of a batch) on G.  g2t_tile_ids (scene-local tile ids) may
 // be null for a batch, whose sort keys are the batch's tile ids.
+// packed: the features as g2v_forward_pack_features wrote them (queued before on the stream), or
+// null: the splat packs them into its workspace (carved with_packed).
 int splat_impl(const Grid& G, int n, int feat_dim, const float* means3D, const float* opacity,
-               const void* features, int feat_dtype, const float* cov_inv, const int* valid_voxel_lb,
+               const void* features, int feat_dtype, const void* packed, const float* cov_inv, const int* valid_voxel_lb,
                const int* valid_voxel_ub, const int* g2t_offsets, long long num_pairs, int* g2t_tile_ids,
                float* density, void* grid_feats, int* t2g_tiles, int* t2g_gauss, int* t2g_offsets, void* workspace,
                size_t workspace_bytes, void* stream) {
@@ -307,16 +334,19 @@ int splat_impl(const Grid& G, int n, int feat_dim, const float* means3D, const f
         return fail(G2V_ERR_INVALID, "null input/output pointer");
     if ((double)scene_voxels(G) * G.scenes * (double)feat_dim >= 9.2e18)
         return fail(G2V_ERR_LIMIT, "grid_feats too large");
-    const SplatBufs need = carve_splat(nullptr, n, num_pairs, G, feat_dim);
+    const bool own_pack = packed == nullptr;
+    const SplatBufs need = carve_splat(nullptr, n, num_pairs, G, feat_dim, own_pack);
     int rc = check_ws(workspace, workspace_bytes, need.bytes, "splat");
     if (rc != G2V_OK) return rc;
-    SplatBufs b = carve_splat(workspace, n, num_pairs, G, feat_dim);
+    SplatBufs b = carve_splat(workspace, n, num_pairs, G, feat_dim, own_pack);
+    if (!own_pack) b.fpk = static_cast<uint32_t*>(const_cast<void*>(packed));
     if (t2g_tiles && t2g_gauss && t2g_offsets) {   // the caller keeps the Tile->Gaussian CSR
         b.sorted_tiles = t2g_tiles;
         b.sorted_gauss = t2g_gauss;
         b.tile_offsets = t2g_offsets;
     }
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (feat_dim > 0 && own_pack) G2V_HIP(launch_split_pack(n, feat_dim, features, feat_dtype, b.fpk, s));
     rc = build_t2g(G, n, valid_voxel_lb, valid_voxel_ub, g2t_offsets, g2t_tile_ids, nullptr,
                    num_pairs, b, s);
     if (rc != G2V_OK) return rc;
@@ -335,7 +365,7 @@ int splat_impl(const Grid& G, int n, int feat_dim, const float* means3D, const f
 extern "C" {
 
 int g2v_forward_splat(int n, int feat_dim, const float* means3D, const float* opacity,
-                      const void* features, int feat_dtype, const float voxel_size[3],
+                      const void* features, int feat_dtype, const void* packed_features, const float voxel_size[3],
                       const float voxel_range[6], const float* cov_inv, const int* valid_voxel_lb,
                       const int* valid_voxel_ub, const int* g2t_offsets, long long num_pairs,
                       int* g2t_tile_ids, float* density, void* grid_feats, int* t2g_tiles, int* t2g_gauss,
@@ -344,7 +374,9 @@ int g2v_forward_splat(int n, int feat_dim, const float* means3D, const float* op
     Grid G;
     const int rc = make_grid(voxel_size, voxel_range, G);
     if (rc != G2V_OK) return rc;
-    return splat_impl(G, n, feat_dim, means3D, opacity, features, feat_dtype, cov_inv, valid_voxel_lb, valid_voxel_ub,
+    if (feat_dim > 0 && !packed_features)
+        return fail(G2V_ERR_INVALID, "feat_dim = %d needs packed_features (g2v_forward_pack_features)", feat_dim);
+    return splat_impl(G, n, feat_dim, means3D, opacity, features, feat_dtype, packed_features, cov_inv, valid_voxel_lb, valid_voxel_ub,
                       g2t_offsets, num_pairs, g2t_tile_ids, density, grid_feats, t2g_tiles, t2g_gauss, t2g_offsets,
                       workspace, workspace_bytes, stream);
 }
@@ -854,7 +886,7 @@ int g2v_batch_forward_splat(int num_scenes, int n, int feat_dim, const float* me
     BatchPlan p;
     const int rc = batch_setup(num_scenes, n, voxel_size, voxel_range, plan_workspace, plan_workspace_bytes, G, p);
     if (rc != G2V_OK) return rc;
-    return splat_impl(G, num_scenes * n, feat_dim, means3D, opacity, features, feat_dtype, cov_inv, valid_voxel_lb,
+    return splat_impl(G, num_scenes * n, feat_dim, means3D, opacity, features, feat_dtype, nullptr, cov_inv, valid_voxel_lb,
                       valid_voxel_ub, p.goff, num_pairs, g2t_tile_ids, density, grid_feats, t2g_tiles, t2g_gauss,
                       t2g_offsets, workspace, workspace_bytes, stream);
 }

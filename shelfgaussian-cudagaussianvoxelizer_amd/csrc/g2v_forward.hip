@@ -743,16 +743,8 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
     }
 }
 
-hipError_t launch_forward_feats(const Grid& G, int C, const float* means, const float* opacity,
-                                const float* cov_inv, const int* lb, const int* ub,
-                                const int* tile_offsets, const int* sorted_gauss, int M, int n,
-                                const void* features, int fdt, uint32_t* fpk, float* density,
-                                void* grid_feats, int* tl_ws, hipStream_t s) {
-    const int T = scene_tiles(G) * G.scenes;
-    if (T <= 0) return hipSuccess;
-    if (C <= 0)
-        return launch_forward_density(G, means, opacity, cov_inv, lb, ub, tile_offsets, sorted_gauss,
-                                      M, density, s);
+hipError_t launch_split_pack(int n, int C, const void* features, int fdt, uint32_t* fpk, hipStream_t s) {
+    if (C <= 0 || n < 0) return hipSuccess;
     const int Cp = packed_channels(C);
     const int64_t count = (int64_t)(n + 1) * Cp;
     if (count * 4 > (int64_t)UINT32_MAX) return hipErrorInvalidValue;   // byte offsets are 32-bit
@@ -763,6 +755,21 @@ hipError_t launch_forward_feats(const Grid& G, int C, const float* means, const 
     else
         G2V_LAUNCH(k_split_pack<float>, dim3(pblocks), dim3(256), 0, s, static_cast<const float*>(features), n, C,
                    Cp, fpk);
+    return hipGetLastError();
+}
+
+hipError_t launch_forward_feats(const Grid& G, int C, const float* means, const float* opacity,
+                                const float* cov_inv, const int* lb, const int* ub,
+                                const int* tile_offsets, const int* sorted_gauss, int M, int n,
+                                const void* features, int fdt, const uint32_t* fpk, float* density,
+                                void* grid_feats, int* tl_ws, hipStream_t s) {
+    const int T = scene_tiles(G) * G.scenes;
+    if (T <= 0) return hipSuccess;
+    if (C <= 0)
+        return launch_forward_density(G, means, opacity, cov_inv, lb, ub, tile_offsets, sorted_gauss,
+                                      M, density, s);
+    const int Cp = packed_channels(C);
+    if ((int64_t)(n + 1) * Cp * 4 > (int64_t)UINT32_MAX) return hipErrorInvalidValue;   // byte offsets are 32-bit
     const int blocks = (int)ceil_div(T, 8) * 8;
     // lists of at most short_list_max(C) Gaussians (empty ones included) in k_fwd_short, the others
     // in k_fwd_feats.  When fewer tiles can be long than there are tiles (a sparse problem),

@@ -116,10 +116,14 @@ hipError_t launch_forward_density(const Grid& G, const float* means, const float
                                   const float* cov_inv, const int* lb, const int* ub,
                                   const int* tile_offsets, const int* sorted_gauss, int M,
                                   float* density, hipStream_t s);
+// The features as packed bf16 (hi, lo) pairs for k_fwd_feats (packed_channels(C) 32-bit words per
+// row, plus a zero row); it depends on the features alone.
+hipError_t launch_split_pack(int n, int C, const void* features, int fdt, uint32_t* fpk, hipStream_t s);
+// fpk: launch_split_pack's output for these features, queued before on s.
 hipError_t launch_forward_feats(const Grid& G, int C, const float* means, const float* opacity,
                                 const float* cov_inv, const int* lb, const int* ub,
                                 const int* tile_offsets, const int* sorted_gauss, int M, int n,
-                                const void* features, int fdt, uint32_t* fpk, float* density,
+                                const void* features, int fdt, const uint32_t* fpk, float* density,
                                 void* grid_feats, int* tl_ws, hipStream_t s);
 // ints of the long-tile list workspace (tl_ws) of a forward or backward with features.
 inline int long_list_ints(int64_t M, int T, int C) { return 1 + long_tiles_bound(M, T, short_list_max(C)); }

@@ -31,7 +31,7 @@ def test_header_symbols_exported():
 
 
 def test_abi_version():
-    assert _lib().load().g2v_abi_version() == _lib().ABI_VERSION == 11
+    assert _lib().load().g2v_abi_version() == _lib().ABI_VERSION == 12
 
 
 def test_loader_refuses_other_abi(monkeypatch):
@@ -74,17 +74,31 @@ def test_invalid_arguments_fail_before_any_launch():
                               ctypes.byref(M), None, 0, None, None)
     assert rc == 1 and b"n = -1" in lib.g2v_last_error()
     # too many pairs for the int32 CSR
-    rc = lib.g2v_forward_splat(1, 0, None, None, None, 0, vs, vr, None, None, None, None, 1 << 31,
+    rc = lib.g2v_forward_splat(1, 0, None, None, None, 0, None, vs, vr, None, None, None, None, 1 << 31,
                                None, None, None, None, None, None, None, 0, None)
     assert rc == 3
     # unknown feature type
-    rc = lib.g2v_forward_splat(1, 0, None, None, None, 7, vs, vr, None, None, None, None, 0,
+    rc = lib.g2v_forward_splat(1, 0, None, None, None, 7, None, vs, vr, None, None, None, None, 0,
                                None, None, None, None, None, None, None, 0, None)
     assert rc == 1 and b"feat_dtype" in lib.g2v_last_error()
     # missing workspace
-    rc = lib.g2v_forward_splat(0, 0, None, None, None, 0, vs, vr, None, None, None, None, 0, None,
+    rc = lib.g2v_forward_splat(0, 0, None, None, None, 0, None, vs, vr, None, None, None, None, 0, None,
                                ctypes.c_void_p(16), None, None, None, None, None, 0, None)
     assert rc == 1 and b"workspace" in lib.g2v_last_error()
+    # features without their packed rows
+    rc = lib.g2v_forward_splat(4, 8, None, None, ctypes.c_void_p(16), 0, None, vs, vr, None, None, None, None, 0,
+                               None, ctypes.c_void_p(16), ctypes.c_void_p(16), None, None, None, None, 0, None)
+    assert rc == 1 and b"packed_features" in lib.g2v_last_error()
+    # packing: buffer size, type and pointers are checked before anything is queued
+    need = lib.g2v_forward_packed_bytes(4, 8)   # 5 rows (a zero row last) of channels padded to 128
+    assert need == 5 * 128 * 4 and lib.g2v_forward_packed_bytes(4, 0) == 0
+    rc = lib.g2v_forward_pack_features(4, 8, ctypes.c_void_p(16), 0, ctypes.c_void_p(16), need - 1, None)
+    assert rc == 1 and b"too small" in lib.g2v_last_error()
+    rc = lib.g2v_forward_pack_features(4, 8, ctypes.c_void_p(16), 5, ctypes.c_void_p(16), need, None)
+    assert rc == 1 and b"feat_dtype" in lib.g2v_last_error()
+    rc = lib.g2v_forward_pack_features(4, 8, None, 0, ctypes.c_void_p(16), need, None)
+    assert rc == 1 and b"null" in lib.g2v_last_error()
+    assert lib.g2v_forward_pack_features(4, 0, None, 0, None, 0, None) == 0
     # features requested without tensors
     rc = lib.g2v_backward(4, 8, ctypes.c_void_p(16), None, ctypes.c_void_p(16), ctypes.c_void_p(16),
                           ctypes.c_void_p(16), vs, vr, ctypes.c_void_p(16), ctypes.c_void_p(16), None,
