@@ -1223,13 +1223,6 @@ __global__ void __launch_bounds__(kBsThreads) k_bwd_tile_short(
 // Region row of every Tile->Gaussian entry: the position of its Gaussian in the (ascending)
 // Gaussian list of the region that holds its tile.
 // ------------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) k_region_gids(int MR, const int* __restrict__ r_pairs_sorted,
-                                                     const int* __restrict__ r_gauss,
-                                                     int* __restrict__ r_gids) {
-    const int j = blockIdx.x * 256 + threadIdx.x;
-    if (j < MR) r_gids[j] = r_gauss[r_pairs_sorted[j]];
-}
-
 constexpr int kBrSlots = 16;   // tiles per region (2 x 2 x up to 4), slot ((tx&1)*2 + (ty&1))*RZ + tz%RZ
 
 // Fills n ints with v (also used where a stream may be captured: no memset nodes).
@@ -1242,6 +1235,22 @@ hipError_t launch_fill_i32(int64_t n, int v, int* dst, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     G2V_LAUNCH(k_fill_i32, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, s, n, v, dst);
     return hipGetLastError();
+}
+
+// Per region row k (the k-th pair of the region-sorted G->R CSR): the row's Gaussian r_gids[k],
+// the row's table entries set to M (absent pair: the zero row of the split weights), and, by
+// workgroup 0, that zero row itself (kWtRow bfloat16 zeros at wt_zero).
+__global__ void __launch_bounds__(256) k_region_rows(int MR, int M, const int* __restrict__ r_pairs_sorted,
+                                                     const int* __restrict__ r_gauss, int* __restrict__ r_gids,
+                                                     int* __restrict__ table, int* __restrict__ wt_zero) {
+    const int k = blockIdx.x * 256 + threadIdx.x;
+    if (blockIdx.x == 0 && threadIdx.x < kWtRow / 2) wt_zero[threadIdx.x] = 0;
+    if (k >= MR) return;
+    r_gids[k] = r_gauss[min(max(r_pairs_sorted[k], 0), MR - 1)];
+    int4* row = reinterpret_cast<int4*>(table + (int64_t)k * kBrSlots);
+    const int4 m = make_int4(M, M, M, M);
+#pragma unroll
+    for (int q = 0; q < kBrSlots / 4; ++q) row[q] = m;
 }
 
 // Row table of phase B: for region row r (its position in the region's ascending Gaussian list,
@@ -1951,11 +1960,8 @@ hipError_t launch_backward_prepare(const Grid& G, int n, int C, const void* feat
     e = launch_tile_offsets(b.r_cells_sorted, MR, nreg, b.roff, s);
     if (e != hipSuccess) return e;
     if (MR > 0 && M > 0) {
-        G2V_LAUNCH(k_region_gids, dim3((unsigned)ceil_div(MR, 256)), dim3(256), 0, s, (int)MR,
-                   (const int*)b.r_pairs_sorted, (const int*)b.r_gauss, b.r_gids);
-        const int64_t tcount = MR * kBrSlots;
-        G2V_LAUNCH(k_fill_i32, dim3((unsigned)ceil_div(tcount, 256)), dim3(256), 0, s, tcount, (int)M, b.table);
-        G2V_LAUNCH(k_fill_i32, dim3(1), dim3(256), 0, s, (int64_t)(kWtRow / 2), 0,
+        G2V_LAUNCH(k_region_rows, dim3((unsigned)ceil_div(MR, 256)), dim3(256), 0, s, (int)MR, (int)M,
+                   (const int*)b.r_pairs_sorted, (const int*)b.r_gauss, b.r_gids, b.table,
                    reinterpret_cast<int*>(b.wt + M * kWtRow));
         G2V_LAUNCH(k_region_table, dim3((unsigned)ceil_div(M, 256)), dim3(256), 0, s, G, RG, (int)M, (int)MR,
                    sorted_tiles, sorted_gauss, (const int*)b.roff, (const int*)b.r_gids, b.table);
