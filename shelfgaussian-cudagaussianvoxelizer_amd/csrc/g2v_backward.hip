@@ -1795,15 +1795,16 @@ __global__ void __launch_bounds__(kBgThreads) k_bwd_gauss(
     }
     const int r0 = min(max(g2r_offsets[g], 0), MR), r1 = min(max(g2r_offsets[g + 1], r0), MR);
     // region rows summed in ascending order per channel; a bfloat16 output is the float sum rounded
-    // to nearest even
+    // to nearest even.  The rows are read once: nontemporal loads keep them from displacing cached
+    // data (0.18 -> 0.15 ms at config 3)
     typedef typename std::conditional<OBF16, __bf16, float>::type OT;
     OT* out = static_cast<OT*>(grad_features_out) + (int64_t)g * C;
     if ((C & 3) == 0) {
         for (int c = threadIdx.x * 4; c < C; c += kBgThreads * 4) {
             float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
             for (int r = r0; r < r1; ++r) {
-                const float4 v = *reinterpret_cast<const float4*>(gpart + (int64_t)r * C + c);
-                s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+                const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(gpart + (int64_t)r * C + c));
+                s.x += v[0]; s.y += v[1]; s.z += v[2]; s.w += v[3];
             }
             const f32x4 nv = {s.x, s.y, s.z, s.w};
             if constexpr (OBF16) {
