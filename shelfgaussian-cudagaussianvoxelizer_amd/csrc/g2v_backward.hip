@@ -1220,8 +1220,8 @@ __global__ void __launch_bounds__(kBsThreads) k_bwd_tile_short(
 }
 
 // ------------------------------------------------------------------------------------------
-// Region row of every Tile->Gaussian entry: the position of its Gaussian in the (ascending)
-// Gaussian list of the region that holds its tile.
+// Phase B's row table: for every region row (a Gaussian of the region's ascending list) and
+// every tile slot of the region, the Tile->Gaussian entry of that (tile, Gaussian) pair.
 // ------------------------------------------------------------------------------------------
 constexpr int kBrSlots = 16;   // tiles per region (2 x 2 x up to 4), slot ((tx&1)*2 + (ty&1))*RZ + tz%RZ
 

@@ -18,7 +18,7 @@ from tests import workloads as W
 pytestmark = pytest.mark.gpu
 
 # kernels of the backward preparation (g2v_backward_prepare)
-_PREP = ("k_split_chunks", "k_fill_cells", "k_region_gids", "k_region_table")
+_PREP = ("k_split_chunks", "k_fill_cells", "k_region_rows", "k_region_table")
 
 
 def say(*a):
