@@ -51,7 +51,32 @@ def grid_dims(voxel_size, voxel_range):
     return tuple(dims), tuple(tiles)
 
 
+_GRIDS = {}
+
+
+def _grid_of(voxel_size, voxel_range):
+    """(vs, vr, dims, tiles) of a grid: the ctypes float arrays the C ABI takes and the grid and tile
+    dimensions, kept per distinct (voxel_size, voxel_range) values."""
+    vs_h = _host_values(voxel_size, 3, "voxel_size")
+    vr_h = _host_values(voxel_range, 6, "voxel_range")
+    key = tuple(vs_h) + tuple(vr_h)
+    g = _GRIDS.get(key)
+    if g is None:
+        dims, tiles = grid_dims(vs_h, vr_h)
+        g = (_lib.floats(vs_h), _lib.floats(vr_h), dims, tiles)
+        if len(_GRIDS) < 64:
+            _GRIDS[key] = g
+    return g
+
+
 def _f32_input(t, name, shape=None):
+    if isinstance(t, torch.Tensor) and t.dtype == torch.float32 \
+            and t.is_cuda and t.is_contiguous() and (shape is None or t.shape == shape):
+        return t.detach()   # already what the kernels read
+    return _f32_input_slow(t, name, shape)
+
+
+def _f32_input_slow(t, name, shape=None):
     if not isinstance(t, torch.Tensor):
         raise RuntimeError(f"{name} must be a tensor")
     if t.device.type != "cuda":
@@ -69,6 +94,8 @@ _FEAT_DTYPES = {torch.float32: _lib.G2V_DTYPE_F32, torch.bfloat16: _lib.G2V_DTYP
 def _feat_input(t, name):
     """Features: float32 or bfloat16 on the GPU (grid_feats and the feature gradient take the
     same type)."""
+    if isinstance(t, torch.Tensor) and t.dtype in _FEAT_DTYPES and t.is_cuda and t.is_contiguous():
+        return t.detach()
     if not isinstance(t, torch.Tensor):
         raise RuntimeError(f"{name} must be a tensor")
     if t.device.type != "cuda":
@@ -166,10 +193,7 @@ def _forward(means3D, opacity, covariances, voxel_size, voxel_range, features, k
         C = feats.shape[1]
         if C == 0:
             feats = None
-    vs_h = _host_values(voxel_size, 3, "voxel_size")
-    vr_h = _host_values(voxel_range, 6, "voxel_range")
-    vs, vr = _lib.floats(vs_h), _lib.floats(vr_h)
-    (X, Y, Z), (Tx, Ty, Tz) = grid_dims(vs_h, vr_h)
+    vs, vr, (X, Y, Z), (Tx, Ty, Tz) = _grid_of(voxel_size, voxel_range)
 
     with _OnDevice(dev):
         cur = torch.cuda.current_stream(dev)
@@ -181,11 +205,15 @@ def _forward(means3D, opacity, covariances, voxel_size, voxel_range, features, k
         ub = torch.empty(n, 3, **i32)
         nvox = torch.empty(n, **i32)
         g2t_offsets = torch.empty(n + 1, **i32)
-        ws = torch.empty(lib.g2v_forward_plan_workspace(n), dtype=torch.uint8, device=dev)
-        # with keep_t2g the backward's plan (the (region, Gaussian) pair count) is done here too,
-        # on the same wait
-        bplan = (torch.empty(max(1, lib.g2v_backward_plan_workspace(n)), dtype=torch.uint8, device=dev)
-                 if keep_t2g else None)
+        # the plan's workspace and, with keep_t2g, the backward plan's (the (region, Gaussian) pair
+        # count is done here too, on the same wait; the backward reads that workspace later), in
+        # one allocation
+        pws = lib.g2v_forward_plan_workspace(n)
+        pws_al = (pws + 255) & ~255
+        bws = max(1, lib.g2v_backward_plan_workspace(n)) if keep_t2g else 0
+        wsb = torch.empty(pws_al + bws, dtype=torch.uint8, device=dev)
+        ws = wsb[:pws]
+        bplan = wsb[pws_al:] if keep_t2g else None
         counts = _pinned_counts(dev, 2)
         start, stop = _timing_events(dev)
         start.record(cur)
