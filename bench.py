@@ -52,6 +52,8 @@ def parse():
                     help="skip the covariance-construction and batched-scenes legs")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="also run a plain device copy of this size (PMC scale reference)")
+    ap.add_argument("--copy-peak-mib", type=int, default=2048,
+                    help="size of the device-to-device copy timed in the same run as the measured HBM peak")
     ap.add_argument("--batched-only", action="store_true",
                     help="run only the batched-scenes leg (the recorded batch) and print its result (profiling)")
     return ap.parse_args()
@@ -140,6 +142,31 @@ def cpu_baseline(w, host, gpu_out, frac):
                        f"(measured {t_csr + t_fwd + t_bwd:.1f} s)"),
             "fwd_ms": round(1e3 * (t_csr + t_fwd * T / done_tiles), 1),
             "bwd_ms": round(1e3 * t_bwd * n / ng, 1)}
+
+
+def copy_peak(dev, mib, reps=10):
+    """Measured HBM peak of this box: a plain device-to-device copy (torch copy_, read + write of
+    `mib` MiB each way), best of `reps` after a warm-up, as GB/s of bytes moved."""
+    import torch
+    src = torch.empty(mib << 18, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    cur = torch.cuda.current_stream(dev)
+    best = None
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(cur)
+        dst.copy_(src)
+        b.record(cur)
+        b.synchronize()
+        t = a.elapsed_time(b)
+        best = t if best is None else min(best, t)
+    nbytes = 2 * src.numel() * 4
+    del src, dst
+    torch.cuda.empty_cache()
+    return {"gbps": round(nbytes / (best * 1e-3) / 1e9, 1), "bytes": nbytes, "ms": round(best, 4),
+            "method": f"torch copy_ of {mib} MiB device to device (read + write counted), best of {reps}"}
 
 
 def cosine_leg(_C, grid_feats, steps, warmup):
@@ -422,19 +449,26 @@ def main():
 
     for _ in range(args.warmup):
         step()
-    # timed region: K steps of the product path, no instrumentation
+    # timed region: K steps of the product path, no instrumentation beyond one event per step
+    # boundary on the current stream (for the median)
     fwd_s = bwd_s = 0.0
     torch.cuda.synchronize()
     resident = torch.cuda.memory_allocated(dev)     # inputs and upstream gradients
     torch.cuda.reset_peak_memory_stats(dev)
+    cur = torch.cuda.current_stream(dev)
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    marks[0].record(cur)
+    for i in range(args.steps):
         stats = step()
+        marks[i + 1].record(cur)
         fwd_s += float(stats[0])
         bwd_s += float(stats[1])
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms = (t1 - t0) * 1e3 / args.steps
+    step_ms = sorted(marks[i].elapsed_time(marks[i + 1]) for i in range(args.steps))
+    median_ms = step_ms[len(step_ms) // 2] if len(step_ms) % 2 else 0.5 * (step_ms[len(step_ms) // 2 - 1] + step_ms[len(step_ms) // 2])
     peak = torch.cuda.max_memory_allocated(dev)
     memory = {"peak_allocated_gb": round(peak / 1e9, 3), "resident_inputs_gb": round(resident / 1e9, 3),
               "step_peak_gb": round((peak - resident) / 1e9, 3),
@@ -477,6 +511,9 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
+    peak_copy = copy_peak(dev, args.copy_peak_mib) if args.copy_peak_mib > 0 else None
+    meas_peak = peak_copy["gbps"] if peak_copy else None
+
     kernels = {k: {"launches": n_, "avg_ms": round(t_ / max(n_, 1), 4), "total_ms_per_step": round(t_ / args.steps, 4)}
                for k, (n_, t_) in sorted(prof.items(), key=lambda kv: -kv[1][1])}
     dom = max(prof.items(), key=lambda kv: kv[1][1])[0] if prof else None
@@ -492,16 +529,21 @@ def main():
                 tr = json.load(fh).get(f"cfg{args.config}", {}).get(dom)
             if tr:
                 traffic = tr.get("bytes_per_launch")
-        if bytes_k is not None:
-            ach = bytes_k / avg_s / 1e9
-            comp = compulsory.get(dom.split("<")[0])
+        comp = compulsory.get(dom.split("<")[0])
+        if comp is not None:
+            # achieved = the launch's share of the step's compulsory bytes (each input read once,
+            # each output written once; no intermediates of the design, no second reads) / its
+            # average duration
+            ach = comp / avg_s / 1e9
             roofline = {"kernel": dom, "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
                         "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                        "algorithmic_bytes": bytes_k, "avg_ms": round(avg_s * 1e3, 4),
-                        # the same launch credited with its share of the step's compulsory bytes only
-                        # (no intermediates of the design, no second reads)
-                        "compulsory_bytes": comp,
-                        "compulsory_frac": None if comp is None else round(comp / avg_s / 1e9 / HBM_PEAK_GBPS, 4)}
+                        "algorithmic_bytes": comp, "avg_ms": round(avg_s * 1e3, 4),
+                        "measured_peak": meas_peak,
+                        "frac_measured_peak": None if not meas_peak else round(ach / meas_peak, 4),
+                        # the same launch credited with every byte its own inputs and outputs take
+                        # once, the design's intermediates included (split weights, pair partials)
+                        "design_bytes": bytes_k,
+                        "design_frac": None if bytes_k is None else round(bytes_k / avg_s / 1e9 / HBM_PEAK_GBPS, 4)}
 
     covariance = batched = bf16 = None
     if not args.no_extra and C > 0:
@@ -534,9 +576,16 @@ def main():
         "config": {"workload": w.name, "n_gaussians": N, "feat_dim": C, "grid": [X, Y, Z], "tiles": [Tx, Ty, Tz],
                    "g2t_pairs": M, "region_pairs": MR, "inbox_pairs": P, "upstream_grads": w.grads},
         "fwd_ms": round(fwd_s * 1e3 / args.steps, 4), "bwd_ms": round(bwd_s * 1e3 / args.steps, 4),
+        "median_ms_per_step": round(median_ms, 4),
+        "median_note": "median of the timed steps' intervals between HIP events recorded at each step boundary",
         "hbm_gbps": round(gbps, 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
+        "hbm_measured_peak": peak_copy,
+        "hbm_frac_measured_peak": None if not meas_peak else round(gbps / meas_peak, 4),
         "compulsory_bytes": fwd_b + bwd_b,
         "fp32_equiv_tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+        "fp32_frac": round(flops / (ms * 1e-3) / 1e12 / FP32_PEAK_TFLOPS, 4),
+        "fp32_note": ("F = 2 P C (forward) + 4 P C (backward) over the in-box pairs P, per step time, "
+                      "against the 157.3 TFLOP/s fp32 peak"),
         "roofline": roofline, "memory": memory, "kernels": kernels, "instrumented_ms_per_step": round(ms_instr, 4),
         "kernels_note": ("per-kernel HIP event pairs over K further steps run right after the timed "
                          "region (instrumented_ms_per_step is their wall time per step)"),

@@ -66,8 +66,10 @@ int g2v_forward_plan(int n, const float* means3D, const float* covariances,
 
 /* g2v_forward_plan_async: the same work without the synchronisation, for callers that plan
  * several scenes and wait once: the pair counts land in counts[0] (M) and counts[1] (the
- * (region, Gaussian) pair count when bwd_plan_workspace is given, else 0), a device-accessible
- * pointer (device or pinned host memory), when the stream reaches them.  No counterpart in the
+ * (region, Gaussian) pair count when bwd_plan_workspace is given, else 0) when the stream
+ * reaches them.  counts is device memory or pinned host memory (hipHostMalloc, or a pinned
+ * allocation of a framework's host allocator); for the latter the kernels write through the
+ * device address hipHostGetDevicePointer gives, and pageable host memory is rejected.  No counterpart in the
  * reference, which handles one scene per call. */
 int g2v_forward_plan_async(int n, const float* means3D, const float* covariances, const float voxel_size[3],
                            const float voxel_range[6], float* cov_inv, int* valid_voxel_lb, int* valid_voxel_ub,
@@ -89,18 +91,20 @@ int g2v_forward_pack_features(int n, int feat_dim, const void* features, int fea
  * density and, when feat_dim > 0, of the density-weighted feature average (reference
  * .cu:1634-1904).  density (X,Y,Z) and grid_feats (X,Y,Z,feat_dim) are written completely;
  * features and packed_features may be NULL when feat_dim == 0; otherwise packed_features holds
- * g2v_forward_pack_features's output for the same features, queued before on the same stream.
+ * g2v_forward_pack_features's output for the same features, queued before on the same stream,
+ * in packed_bytes >= g2v_forward_packed_bytes(n, feat_dim) bytes (a smaller buffer, one packed
+ * for fewer Gaussians or channels, is rejected with G2V_ERR_INVALID).
  * When t2g_tiles, t2g_gauss (M each) and t2g_offsets (T+1) are all non-NULL the
  * Tile->Gaussian CSR is built there (and can be handed to g2v_backward, which then skips
  * rebuilding it); otherwise it lives in the workspace.  Asynchronous. */
 size_t g2v_forward_splat_workspace(int n, int feat_dim, long long num_pairs, const float voxel_size[3],
                                    const float voxel_range[6]);
 int g2v_forward_splat(int n, int feat_dim, const float* means3D, const float* opacity,
-                      const void* features, int feat_dtype, const void* packed_features, const float voxel_size[3],
-                      const float voxel_range[6], const float* cov_inv, const int* valid_voxel_lb,
-                      const int* valid_voxel_ub, const int* g2t_offsets, long long num_pairs,
-                      int* g2t_tile_ids, float* density, void* grid_feats, int* t2g_tiles, int* t2g_gauss,
-                      int* t2g_offsets, void* workspace, size_t workspace_bytes, void* stream);
+                      const void* features, int feat_dtype, const void* packed_features, size_t packed_bytes,
+                      const float voxel_size[3], const float voxel_range[6], const float* cov_inv,
+                      const int* valid_voxel_lb, const int* valid_voxel_ub, const int* g2t_offsets,
+                      long long num_pairs, int* g2t_tile_ids, float* density, void* grid_feats, int* t2g_tiles,
+                      int* t2g_gauss, int* t2g_offsets, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- backward -----------------------------------------------------------------------------
  * Replaces cuda_gaussian_voxelizer_backward (src/cuda_gaussian_voxelizer.cu:1920-2057, bound at

@@ -250,7 +250,8 @@ def _forward(means3D, opacity, covariances, voxel_size, voxel_range, features, k
         if keep_t2g:
             csr = (torch.empty(M, **i32), torch.empty(M, **i32), t2g_toff)
             t2g = dict(csr=csr, plan=bplan, num_region_pairs=MR, vs=vs, vr=vr, dims=(X, Y, Z))
-        _lib.check(lib.g2v_forward_splat(n, C, _ptr(means), _ptr(op), _ptr(feats), fdt, _ptr(packed), vs, vr,
+        _lib.check(lib.g2v_forward_splat(n, C, _ptr(means), _ptr(op), _ptr(feats), fdt, _ptr(packed),
+                                         0 if packed is None else packed.numel(), vs, vr,
                                          _ptr(cov_inv), _ptr(lb), _ptr(ub), _ptr(g2t_offsets), M,
                                          _ptr(g2t_tile_ids), _ptr(density), _ptr(grid_feats),
                                          _ptr(csr[0]), _ptr(csr[1]), _ptr(csr[2]),

@@ -115,8 +115,10 @@ class _CudaGaussianVoxelizeCosineLossFunction(torch.autograd.Function):
     cosine loss on its grid_feats (:49-67), with the loss's gradient fused into the voxelizer's
     backward: the (X,Y,Z,C) gradient of grid_feats that the reference writes between the two
     backwards is formed per voxel inside the feature-gradient kernels (_C.gaussian_voxelizer_
-    backward_cosine).  grid_feats is returned without a gradient path of its own.  float32 inputs
-    with C % 4 == 0 take the fused kernels; other feature types chain the two backwards."""
+    backward_cosine).  float32 inputs with C % 4 == 0 take the fused kernels; other feature types
+    chain the two backwards.  grid_feats keeps its gradient path: when another use of it sends a
+    gradient back, that gradient is added to the loss's (materialised, as the chained modules do)
+    and the voxelizer's backward reads the sum."""
 
     @staticmethod
     def forward(ctx, means3D, opacity, covariances, voxel_size, voxel_range, features, voxel_label,
@@ -139,7 +141,7 @@ class _CudaGaussianVoxelizeCosineLossFunction(torch.autograd.Function):
         ctx.t2g = t2g
         ctx.count = count
         ctx.fused = fused
-        ctx.mark_non_differentiable(grid_feats, stats)
+        ctx.mark_non_differentiable(stats)
         # no zero-filled (X,Y,Z,C) gradient for grid_feats: unused outputs arrive as None
         ctx.set_materialize_grads(False)
         ctx.opacity_shape = opacity.shape
@@ -160,13 +162,15 @@ class _CudaGaussianVoxelizeCosineLossFunction(torch.autograd.Function):
         feats = features.detach().contiguous()
         saved = (means32, op32, cov_inv, voxsz32, voxrg32, valid_voxel_lb, valid_voxel_ub, num_valid_voxel,
                  g2t_offsets, g2t_tile_ids, density, grid_feats, feats)
-        if ctx.fused:
+        if ctx.fused and grad_grid_feats is None:
             res = _C._backward(gout32, None, *saved, t2g=ctx.t2g,
                                cosine=(gl32, pseudo_dino_gt, coef, ctx.count))
             bwd_sec = res[4]
-        else:   # chained: the loss's gradient of grid_feats, then the voxelizer's backward
+        else:   # chained: the loss's gradient of grid_feats (plus another use's), then the voxelizer's backward
             grad_grid, cos_sec = _C.CudaFeatsCosinelossBackward(gl32, voxel_label, occ_gt_mask_camera, grid_feats,
                                                                 pseudo_dino_gt, ctx.count)
+            if grad_grid_feats is not None:
+                grad_grid = grad_grid + grad_grid_feats.to(grad_grid.dtype)
             res = _C._backward(gout32, grad_grid, *saved, t2g=ctx.t2g)
             bwd_sec = res[4] + cos_sec
         grad_means3D, grad_cov, grad_opacity, grad_feats, _ = res

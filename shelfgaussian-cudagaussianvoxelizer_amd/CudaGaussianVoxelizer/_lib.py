@@ -13,7 +13,7 @@ LIB_PATH = os.path.join(_HERE, LIB_NAME)
 
 G2V_OK = 0
 # the ABI that SIGNATURES describes (g2v_abi_version() of a matching build)
-ABI_VERSION = 12
+ABI_VERSION = 13
 G2V_DTYPE_F32 = 0
 G2V_DTYPE_BF16 = 1
 _ERRORS = {1: "invalid argument", 2: "HIP runtime error", 3: "size limit exceeded"}
@@ -34,7 +34,7 @@ SIGNATURES = {
     "g2v_forward_splat_workspace": (_sz, [_i, _i, _ll, _f3, _f3]),
     "g2v_forward_packed_bytes": (_sz, [_i, _i]),
     "g2v_forward_pack_features": (_i, [_i, _i, _vp, _i, _vp, _sz, _vp]),
-    "g2v_forward_splat": (_i, [_i, _i, _vp, _vp, _vp, _i, _vp, _f3, _f3, _vp, _vp, _vp, _vp, _ll, _vp, _vp,
+    "g2v_forward_splat": (_i, [_i, _i, _vp, _vp, _vp, _i, _vp, _sz, _f3, _f3, _vp, _vp, _vp, _vp, _ll, _vp, _vp,
                                _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "g2v_backward_plan_workspace": (_sz, [_i]),
     "g2v_backward_plan": (_i, [_i, _i, _f3, _f3, _vp, _vp, _vp, _sz, _llp, _vp]),

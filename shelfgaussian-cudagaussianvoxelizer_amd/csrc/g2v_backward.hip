@@ -75,7 +75,12 @@ static Regions make_regions(const Grid& G) {
 }
 
 // ------------------------------------------------------------------------------------------
-// Density only: one wave per Gaussian walks the voxels of its box (z fastest).
+// Density only: one wave per Gaussian walks the voxels of its box (z fastest).  Per voxel, with
+// d = centre - mu, q = A d and r = gD e, e = exp(-d^T q / 2): the lane sums r, r q and r q q^T; the
+// Gaussian's gradients are d mu = o sum r q, d Sigma = o/2 sum r q q^T (symmetric), d o = sum r
+// (reference .cu:1304-1362 with gw = gD: sum gw w q, sum gw w q q^T / 2, sum gw e, w = o e), with
+// o and 1/2 applied once per Gaussian instead of per voxel.  d_a = x_a s_a + (r0_a + s_a/2 - mu_a):
+// one conversion and one fma per axis.
 // ------------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) k_bwd_density(Grid G, int n, const float* __restrict__ gD,
                                                      const float* __restrict__ means,
@@ -95,7 +100,10 @@ __global__ void __launch_bounds__(256) k_bwd_density(Grid G, int n, const float*
     const int ex = p.ub[0] - p.lb[0] + 1, ey = p.ub[1] - p.lb[1] + 1, ez = p.ub[2] - p.lb[2] + 1;
     const int nv = (ex > 0 && ey > 0 && ez > 0) ? ex * ey * ez : 0;
     const int eyz = ey * ez;
-    float gr[kNumGrads] = {};
+    float off[3];
+#pragma unroll
+    for (int a = 0; a < 3; ++a) off[a] = fmaf(0.5f, G.s[a], G.r0[a]) - p.mu[a];
+    float sr = 0.f, sq[3] = {0.f, 0.f, 0.f}, sqq[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     // Voxel i of the box (z fastest) sits at (ix, iy, iz) = the digits of i in radix (ey, ez).  A
     // lane visits i = lane, lane + 64, ...: its position is stepped by the digits (sx, sy, sz) of
     // 64, with at most one carry per digit, instead of divided out at every voxel.
@@ -110,9 +118,25 @@ __global__ void __launch_bounds__(256) k_bwd_density(Grid G, int n, const float*
     }
     for (int i = lane; i < nv; i += 64) {
         const int x = p.lb[0] + ix, y = p.lb[1] + iy, z = p.lb[2] + iz;
-        float qx, qy, qz;
-        const float e = eval_gauss(p, centre(G, 0, x), centre(G, 1, y), centre(G, 2, z), qx, qy, qz);
-        accumulate_grads(gr, gD[voxel_index(G, x, y, z)], e, p.o, qx, qy, qz);
+        const float dx = fmaf((float)x, G.s[0], off[0]);
+        const float dy = fmaf((float)y, G.s[1], off[1]);
+        const float dz = fmaf((float)z, G.s[2], off[2]);
+        const float qx = fmaf(p.A[0], dx, fmaf(p.A[1], dy, p.A[2] * dz));
+        const float qy = fmaf(p.A[3], dx, fmaf(p.A[4], dy, p.A[5] * dz));
+        const float qz = fmaf(p.A[6], dx, fmaf(p.A[7], dy, p.A[8] * dz));
+        const float m = fmaf(dx, qx, fmaf(dy, qy, dz * qz));
+        const float r = gD[voxel_index(G, x, y, z)] * __builtin_amdgcn_exp2f(kq * m);
+        sr += r;
+        const float rx = r * qx, ry = r * qy, rz = r * qz;
+        sq[0] += rx;
+        sq[1] += ry;
+        sq[2] += rz;
+        sqq[0] = fmaf(rx, qx, sqq[0]);
+        sqq[1] = fmaf(ry, qy, sqq[1]);
+        sqq[2] = fmaf(rz, qz, sqq[2]);
+        sqq[3] = fmaf(rx, qy, sqq[3]);
+        sqq[4] = fmaf(rx, qz, sqq[4]);
+        sqq[5] = fmaf(ry, qz, sqq[5]);
         iz += sz;
         const int cz = iz >= ez ? 1 : 0;
         iz -= cz * ez;
@@ -121,9 +145,27 @@ __global__ void __launch_bounds__(256) k_bwd_density(Grid G, int n, const float*
         iy -= cy * ey;
         ix += sx + cy;
     }
-#pragma unroll
-    for (int k = 0; k < kNumGrads; ++k) gr[k] = wave_sum(gr[k]);
-    if (lane == 0) write_grads(gr, g, grad_means, grad_cov, grad_opacity);
+    // the wave's sums: lanes 2k, 2k + 1 of each half hold value k after the transposed butterfly
+    float v[16] = {sq[0], sq[1], sq[2], sqq[0], sqq[1], sqq[2], sqq[3], sqq[4], sqq[5], sr, 0.f, 0.f, 0.f, 0.f,
+                   0.f, 0.f};
+    float t = transpose_sum16(v, lane & 31);
+    t += __shfl_xor(t, 32, 64);
+    // value k of lane 2k: mu xyz, cov xx yy zz xy xz yz, opacity (the order of write_grads)
+    const float h = 0.5f * p.o;
+    const int k = (lane & 31) >> 1;
+    const float gv = k < 3 ? p.o * t : (k < 9 ? h * t : t);
+    if (lane < 20 && (lane & 1) == 0) {
+        if (k < 3) grad_means[g * 3 + k] = gv;
+        else if (k == 9) grad_opacity[g] = gv;
+        else {
+            // symmetric 3x3: xx yy zz on the diagonal, xy xz yz on both sides
+            const int j = k - 3;
+            const int i0 = j < 3 ? 4 * j : (j == 3 ? 1 : (j == 4 ? 2 : 5));
+            const int i1 = j < 3 ? 4 * j : (j == 3 ? 3 : (j == 4 ? 6 : 7));
+            grad_cov[g * 9 + i0] = gv;
+            grad_cov[g * 9 + i1] = gv;
+        }
+    }
 }
 
 hipError_t launch_backward_density(const Grid& G, int n, const float* grad_density,

@@ -142,7 +142,7 @@ extern "C" {
 
 const char* g2v_last_error(void) { return g_err; }
 
-int g2v_abi_version(void) { return 12; }
+int g2v_abi_version(void) { return 13; }
 
 int g2v_grid_dims(const float voxel_size[3], const float voxel_range[6], int dims[3], int tiles[3]) {
     Grid G;
@@ -266,13 +266,33 @@ int g2v_forward_plan_async(int n, const float* means3D, const float* covariances
                            void* stream) {
     g_err[0] = 0;
     if (!counts) return fail(G2V_ERR_INVALID, "counts is null");
+    // the kernels write the counts through a device address: that of pinned host memory is
+    // looked up (it need not equal the host address), device memory is used as it is
+    long long* dcounts = counts;
+    {
+        hipPointerAttribute_t pa;
+        if (hipPointerGetAttributes(&pa, counts) != hipSuccess) {
+            (void)hipGetLastError();
+            return fail(G2V_ERR_INVALID, "counts is neither device memory nor pinned host memory");
+        }
+        if (pa.type == hipMemoryTypeHost) {
+            void* d = nullptr;
+            if (hipHostGetDevicePointer(&d, counts, 0) != hipSuccess || !d) {
+                (void)hipGetLastError();
+                return fail(G2V_ERR_INVALID, "counts: host memory without a device mapping");
+            }
+            dcounts = static_cast<long long*>(d);
+        } else if (pa.type != hipMemoryTypeDevice && pa.type != hipMemoryTypeManaged) {
+            return fail(G2V_ERR_INVALID, "counts is pageable host memory (needs device or pinned host memory)");
+        }
+    }
     Grid G;
     int rc = plan_checks(n, means3D, covariances, voxel_size, voxel_range, cov_inv, valid_voxel_lb, valid_voxel_ub,
                          num_voxels_per_gaussian, g2t_offsets, workspace, workspace_bytes, bwd_plan_workspace,
                          bwd_plan_workspace_bytes, G);
     if (rc != G2V_OK) return rc;
     return plan_launch(G, n, means3D, covariances, cov_inv, valid_voxel_lb, valid_voxel_ub, num_voxels_per_gaussian,
-                       g2t_offsets, workspace, workspace_bytes, bwd_plan_workspace, counts,
+                       g2t_offsets, workspace, workspace_bytes, bwd_plan_workspace, dcounts,
                        static_cast<hipStream_t>(stream));
 }
 
@@ -365,17 +385,20 @@ int splat_impl(const Grid& G, int n, int feat_dim, const float* means3D, const f
 extern "C" {
 
 int g2v_forward_splat(int n, int feat_dim, const float* means3D, const float* opacity,
-                      const void* features, int feat_dtype, const void* packed_features, const float voxel_size[3],
-                      const float voxel_range[6], const float* cov_inv, const int* valid_voxel_lb,
-                      const int* valid_voxel_ub, const int* g2t_offsets, long long num_pairs,
-                      int* g2t_tile_ids, float* density, void* grid_feats, int* t2g_tiles, int* t2g_gauss,
-                      int* t2g_offsets, void* workspace, size_t workspace_bytes, void* stream) {
+                      const void* features, int feat_dtype, const void* packed_features, size_t packed_bytes,
+                      const float voxel_size[3], const float voxel_range[6], const float* cov_inv,
+                      const int* valid_voxel_lb, const int* valid_voxel_ub, const int* g2t_offsets,
+                      long long num_pairs, int* g2t_tile_ids, float* density, void* grid_feats, int* t2g_tiles,
+                      int* t2g_gauss, int* t2g_offsets, void* workspace, size_t workspace_bytes, void* stream) {
     g_err[0] = 0;
     Grid G;
     const int rc = make_grid(voxel_size, voxel_range, G);
     if (rc != G2V_OK) return rc;
     if (feat_dim > 0 && !packed_features)
         return fail(G2V_ERR_INVALID, "feat_dim = %d needs packed_features (g2v_forward_pack_features)", feat_dim);
+    if (feat_dim > 0 && n > 0 && packed_bytes < g2v_forward_packed_bytes(n, feat_dim))
+        return fail(G2V_ERR_INVALID, "packed features buffer too small: %zu bytes, need %zu for n = %d, feat_dim = %d",
+                    packed_bytes, g2v_forward_packed_bytes(n, feat_dim), n, feat_dim);
     return splat_impl(G, n, feat_dim, means3D, opacity, features, feat_dtype, packed_features, cov_inv, valid_voxel_lb, valid_voxel_ub,
                       g2t_offsets, num_pairs, g2t_tile_ids, density, grid_feats, t2g_tiles, t2g_gauss, t2g_offsets,
                       workspace, workspace_bytes, stream);
@@ -820,14 +843,16 @@ BatchPlan carve_batch_plan(void* ws, int B, int n) {
 
 bool batch_sizes_ok(int B, int n) { return B >= 1 && n >= 0 && (int64_t)B * n < 2147483647ll; }
 
+// The batch's tile count fits the int32 tile ids (batch_setup's check, for the size queries).
+bool batch_tiles_ok(const Grid& G, int B) { return (int64_t)scene_tiles(G) * B < 2147483647ll; }
+
 // Grid of a batch of B scenes (n Gaussians each) and its plan workspace, checked.
 int batch_setup(int B, int n, const float* vs, const float* vr, const void* plan_ws, size_t plan_bytes, Grid& G,
                 BatchPlan& p) {
     if (!batch_sizes_ok(B, n)) return fail(G2V_ERR_INVALID, "num_scenes = %d, n = %d", B, n);
     int rc = make_grid(vs, vr, G);
     if (rc != G2V_OK) return rc;
-    if ((int64_t)scene_tiles(G) * B >= 2147483647ll)
-        return fail(G2V_ERR_LIMIT, "%d scenes x %d tiles exceed int32", B, scene_tiles(G));
+    if (!batch_tiles_ok(G, B)) return fail(G2V_ERR_LIMIT, "%d scenes x %d tiles exceed int32", B, scene_tiles(G));
     G.scenes = B;
     G.scene_n = n;
     rc = check_ws(plan_ws, plan_bytes, carve_batch_plan(nullptr, B, n).bytes, "batch plan");
@@ -870,6 +895,7 @@ size_t g2v_batch_forward_splat_workspace(int num_scenes, int n, int feat_dim, lo
                                          const float voxel_size[3], const float voxel_range[6]) {
     Grid G;
     if (!batch_sizes_ok(num_scenes, n) || make_grid(voxel_size, voxel_range, G) != G2V_OK) return 0;
+    if (!batch_tiles_ok(G, num_scenes)) return 0;   // the batch's tile ids would overflow int32
     G.scenes = num_scenes;
     G.scene_n = n;
     return carve_splat(nullptr, num_scenes * n, num_pairs, G, feat_dim).bytes;
@@ -895,6 +921,7 @@ size_t g2v_batch_backward_workspace(int num_scenes, int n, int feat_dim, long lo
                                     long long num_region_pairs, const float voxel_size[3], const float voxel_range[6]) {
     Grid G;
     if (!batch_sizes_ok(num_scenes, n) || make_grid(voxel_size, voxel_range, G) != G2V_OK) return 0;
+    if (!batch_tiles_ok(G, num_scenes)) return 0;   // the batch's tile ids would overflow int32
     G.scenes = num_scenes;
     G.scene_n = n;
     return backward_ws_bytes(G, num_scenes * n, feat_dim, num_pairs, num_region_pairs);

@@ -94,123 +94,6 @@ constexpr int kFwdKSteps = kFwdKMax / 16;
 
 static_assert(kFwdChanPerWave == kPackedChannelAlign, "packed rows are padded to one wave's channels");
 
-// Gaussian parameters of one list entry as one 80-byte LDS record (five 16-byte reads).
-struct alignas(16) FwdParam {
-    float mu[3];
-    float o;
-    float A[9];
-    int lb[3];
-    int ub[3];
-    int pad;
-};
-static_assert(sizeof(FwdParam) == 80, "FwdParam is five 16-byte words");
-
-// ------------------------------------------------------------------------------------------
-// Density only: one wave per tile, one voxel per lane.  The wave walks its tile's list in
-// ascending order, 64 entries at a time: lane k gathers entry k's parameters (those of the next
-// 64 entries are gathered into registers while the current ones are evaluated) and writes them
-// as one record into the wave's LDS slab; every lane then evaluates the 64 records branch-free
-// from broadcast reads and adds o e where the voxel lies in the entry's box (the sum of the
-// reference's kernel, .cu:7-136, in the same order).
-// ------------------------------------------------------------------------------------------
-constexpr int kDenWaves = 4;
-
-// LDS hand-off between the lanes of one wave: waits for the wave's LDS operations; the compiler
-// barriers keep the slab's reads and writes on their side of it.
-__device__ __forceinline__ void wave_lds_sync() {
-    __asm__ __volatile__("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt((15 << 0) | (7 << 4) | (0 << 8) | (3 << 14));   // lgkmcnt(0)
-    __builtin_amdgcn_wave_barrier();
-    __asm__ __volatile__("" ::: "memory");
-}
-
-__global__ void __launch_bounds__(kDenWaves * 64) k_fwd_density(Grid G, const float* __restrict__ means,
-                                                               const float* __restrict__ opacity,
-                                                               const float* __restrict__ cov_inv,
-                                                               const int* __restrict__ lb,
-                                                               const int* __restrict__ ub,
-                                                               const int* __restrict__ toff,
-                                                               const int* __restrict__ sorted_gauss,
-                                                               int M, float* __restrict__ density) {
-    __shared__ FwdParam slab[kDenWaves][64];
-    const int T = scene_tiles(G);
-    // tb: the batch's tile (its list), tile: the scene's
-    const int tb = uniform(xcd_remap(blockIdx.x, gridDim.x) * kDenWaves + (threadIdx.x >> 6));
-    if (tb >= T * G.scenes) return;   // whole waves; the kernel has no workgroup barrier
-    const int scene = uniform(tb / T), tile = tb - scene * T;
-    density += scene * scene_voxels(G);
-    const int lane = threadIdx.x & 63;
-    FwdParam* sl = slab[threadIdx.x >> 6];
-    int x, y, z;
-    tile_voxel(G, tile, lane, x, y, z);
-    const float cx = centre(G, 0, x), cy = centre(G, 1, y), cz = centre(G, 2, z);
-    const int j0 = uniform(min(max(toff[tb], 0), M));
-    const int j1 = uniform(min(max(toff[tb + 1], j0), M));
-    // parameters of list entry j (an empty box past the list)
-    auto fetch = [&](int j, FwdParam& r) {
-        if (j < j1) {
-            const int g = sorted_gauss[j];
-#pragma unroll
-            for (int a = 0; a < 3; ++a) {
-                r.mu[a] = means[g * 3 + a];
-                r.lb[a] = lb[g * 3 + a];
-                r.ub[a] = ub[g * 3 + a];
-            }
-#pragma unroll
-            for (int a = 0; a < 9; ++a) r.A[a] = cov_inv[g * 9 + a];
-            r.o = opacity[g];
-        } else {
-#pragma unroll
-            for (int a = 0; a < 3; ++a) { r.mu[a] = 0.0f; r.lb[a] = 1; r.ub[a] = 0; }
-#pragma unroll
-            for (int a = 0; a < 9; ++a) r.A[a] = 0.0f;
-            r.o = 0.0f;
-        }
-        r.pad = 0;
-    };
-    float acc = 0.0f;
-    FwdParam nxt;
-    fetch(j0 + lane, nxt);
-    for (int jb = j0; jb < j1; jb += 64) {
-        wave_lds_sync();   // the previous records are read
-        sl[lane] = nxt;
-        wave_lds_sync();
-        fetch(jb + 64 + lane, nxt);
-        const int cnt = uniform(min(64, j1 - jb));
-#pragma unroll 2
-        for (int k = 0; k < cnt; ++k) {
-            GaussParams p;
-            const FwdParam& r = sl[k];   // broadcast
-#pragma unroll
-            for (int a = 0; a < 3; ++a) {
-                p.mu[a] = r.mu[a];
-                p.lb[a] = r.lb[a];
-                p.ub[a] = r.ub[a];
-            }
-#pragma unroll
-            for (int a = 0; a < 9; ++a) p.A[a] = r.A[a];
-            p.o = r.o;
-            float qx, qy, qz;
-            const float e = eval_gauss(p, cx, cy, cz, qx, qy, qz);
-            acc += in_box(p, x, y, z) ? p.o * e : 0.0f;
-        }
-    }
-    if (in_grid(G, x, y, z)) density[voxel_index(G, x, y, z)] = acc;
-}
-
-hipError_t launch_forward_density(const Grid& G, const float* means, const float* opacity,
-                                  const float* cov_inv, const int* lb, const int* ub,
-                                  const int* tile_offsets, const int* sorted_gauss, int M,
-                                  float* density, hipStream_t s) {
-    const int T = scene_tiles(G) * G.scenes;
-    if (T <= 0) return hipSuccess;
-    const int groups = (int)ceil_div(T, kDenWaves);
-    const int blocks = (int)ceil_div(groups, 8) * 8;
-    G2V_LAUNCH(k_fwd_density, dim3(blocks), dim3(kDenWaves * 64), 0, s, G, means, opacity, cov_inv, lb,
-               ub, tile_offsets, sorted_gauss, M, density);
-    return hipGetLastError();
-}
-
 // One list entry as the W build reads it, relative to the tile's first voxel (x0, y0, z0): the
 // exponent of exp2 at voxel (x0+a, y0+b, z0+c) is
 //     F(a,b) + Gxy(a,b) dz_c + fz_c,
@@ -229,6 +112,219 @@ struct alignas(16) FwdRec {
     uint32_t xymask, zmask;
 };
 static_assert(sizeof(FwdRec) == 48, "FwdRec is three 16-byte words");
+
+// The record of Gaussian g for the tile whose first voxel is (x0, y0, z0).
+__device__ __forceinline__ FwdRec fwd_record(int g, const float* __restrict__ means, const float* __restrict__ opacity,
+                                             const float* __restrict__ cov_inv, const int* __restrict__ lb,
+                                             const int* __restrict__ ub, int x0, int y0, int z0) {
+    FwdRec r;
+    float A[9];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) A[i] = cov_inv[g * 9 + i];
+    int l[3], u[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        l[i] = lb[g * 3 + i];
+        u[i] = ub[g * 3 + i];
+    }
+    r.mux = means[g * 3 + 0];
+    r.muy = means[g * 3 + 1];
+    r.o = opacity[g];
+    r.a00 = kq * A[0];
+    r.a01 = kq * (A[1] + A[3]);
+    r.a11 = kq * A[4];
+    r.a02 = kq * (A[2] + A[6]);
+    r.a12 = kq * (A[5] + A[7]);
+    r.mu2 = means[g * 3 + 2];
+    r.a22 = kq * A[8];
+    uint32_t xm = 0, ym = 0, zm = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        zm |= (z0 + c >= l[2] && z0 + c <= u[2]) ? (1u << c) : 0u;
+        xm |= (x0 + c >= l[0] && x0 + c <= u[0]) ? (1u << c) : 0u;
+        ym |= (y0 + c >= l[1] && y0 + c <= u[1]) ? (1u << c) : 0u;
+    }
+    r.zmask = zm;
+    uint32_t m = 0;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) m |= (xm >> a) & 1u ? ym << (4 * a) : 0u;
+    r.xymask = m;
+    return r;
+}
+
+// A record past the list: every weight is exactly 0 (o = 0, empty masks).
+__device__ __forceinline__ FwdRec fwd_record_empty() {
+    FwdRec r;
+    r.mux = r.muy = r.o = r.a12 = 0.0f;
+    r.a00 = r.a01 = r.a11 = r.a02 = 0.0f;
+    r.mu2 = r.a22 = 0.0f;
+    r.xymask = r.zmask = 0;
+    return r;
+}
+
+// Weights o e of the four voxels (x0 + col / 4, y0 + col % 4, z0 + c) of column col against the
+// LDS record rec (three 16-byte reads): F and Gxy once per column, one fma, one add and one exp2
+// per voxel.  cxl, cyl: centre of the column; cz: centres of the tile's z layers.
+__device__ __forceinline__ void fwd_column_weights(const FwdRec* rec, int col, float cxl, float cyl,
+                                                   const float (&cz)[4], float (&w)[4]) {
+    const uint4* rp = reinterpret_cast<const uint4*>(rec);
+    const uint4 q0 = rp[0], q1 = rp[1], q2 = rp[2];
+    const uint32_t m = q2.z, zm = q2.w;
+    const float dx = cxl - __uint_as_float(q0.x), dy = cyl - __uint_as_float(q0.y);
+    const float ro = __uint_as_float(q0.z), a12 = __uint_as_float(q0.w);
+    const float a00 = __uint_as_float(q1.x), a01 = __uint_as_float(q1.y);
+    const float a11 = __uint_as_float(q1.z), a02 = __uint_as_float(q1.w);
+    const float mu2 = __uint_as_float(q2.x), a22 = __uint_as_float(q2.y);
+    float dz[4], fz[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        dz[c] = cz[c] - mu2;
+        fz[c] = ((zm >> c) & 1u) ? a22 * dz[c] * dz[c] : -__builtin_inff();
+    }
+    float F = fmaf(fmaf(a00, dx, a01 * dy), dx, a11 * dy * dy);
+    F = ((m >> col) & 1u) ? F : -__builtin_inff();
+    const float Gxy = fmaf(a02, dx, a12 * dy);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) w[c] = ro * __builtin_amdgcn_exp2f(fmaf(Gxy, dz[c], F) + fz[c]);
+}
+
+// ------------------------------------------------------------------------------------------
+// Density only: one wave per tile.  The wave walks its tile's list in ascending order, 64 entries
+// at a time: lane k turns entry k into its tile-relative record (the records of the next 64
+// entries are gathered while the current ones are evaluated) and writes it into the wave's LDS
+// slab.  Lane (col = lane % 16, ph = lane / 16) then takes the voxel column col and the entries
+// ph, ph + 4, ... of the slab, forming each entry's four weights of the column with the
+// operations of fwd_column_weights (so the weights of the feature splat); the z terms dz_c and
+// fz_c, the same for every column, are formed once per entry by the lane that builds its record.
+// The four lane groups' sums are added at the end.  The sum is the reference's (.cu:7-136) in
+// another order.
+// ------------------------------------------------------------------------------------------
+constexpr int kDenWaves = 4;
+
+// A FwdRec with its four z terms: dz_c = (centre of layer c) - mu2 and fz_c as fwd_column_weights
+// forms them (80 bytes).
+struct alignas(16) DenRec {
+    float mux, muy, o, a12;
+    float a00, a01, a11, a02;
+    float dz[4];
+    float fz[4];
+    uint32_t xymask, pad[3];
+};
+static_assert(sizeof(DenRec) == 80, "DenRec is five 16-byte words");
+
+__device__ __forceinline__ DenRec den_record(const FwdRec& r, const float (&cz)[4]) {
+    DenRec d;
+    d.mux = r.mux;
+    d.muy = r.muy;
+    d.o = r.o;
+    d.a12 = r.a12;
+    d.a00 = r.a00;
+    d.a01 = r.a01;
+    d.a11 = r.a11;
+    d.a02 = r.a02;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        d.dz[c] = cz[c] - r.mu2;
+        d.fz[c] = ((r.zmask >> c) & 1u) ? r.a22 * d.dz[c] * d.dz[c] : -__builtin_inff();
+    }
+    d.xymask = r.xymask;
+    d.pad[0] = d.pad[1] = d.pad[2] = 0;
+    return d;
+}
+
+// LDS hand-off between the lanes of one wave: waits for the wave's LDS operations; the compiler
+// barriers keep the slab's reads and writes on their side of it.
+__device__ __forceinline__ void wave_lds_sync() {
+    __asm__ __volatile__("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((15 << 0) | (7 << 4) | (0 << 8) | (3 << 14));   // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+    __asm__ __volatile__("" ::: "memory");
+}
+
+__global__ void __launch_bounds__(kDenWaves * 64) k_fwd_density(Grid G, const float* __restrict__ means,
+                                                               const float* __restrict__ opacity,
+                                                               const float* __restrict__ cov_inv,
+                                                               const int* __restrict__ lb,
+                                                               const int* __restrict__ ub,
+                                                               const int* __restrict__ toff,
+                                                               const int* __restrict__ sorted_gauss,
+                                                               int M, float* __restrict__ density) {
+    __shared__ DenRec slab[kDenWaves][64];
+    const int T = scene_tiles(G);
+    // tb: the batch's tile (its list), tile: the scene's
+    const int tb = uniform(xcd_remap(blockIdx.x, gridDim.x) * kDenWaves + (threadIdx.x >> 6));
+    if (tb >= T * G.scenes) return;   // whole waves; the kernel has no workgroup barrier
+    const int scene = uniform(tb / T), tile = tb - scene * T;
+    density += scene * scene_voxels(G);
+    const int lane = threadIdx.x & 63, col = lane & 15, ph = lane >> 4;
+    DenRec* sl = slab[threadIdx.x >> 6];
+    int x0, y0, z0;
+    tile_voxel(G, tile, 0, x0, y0, z0);
+    const float cxl = centre(G, 0, x0 + (col >> 2)), cyl = centre(G, 1, y0 + (col & 3));
+    float cz[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) cz[c] = centre(G, 2, z0 + c);
+    const int j0 = uniform(min(max(toff[tb], 0), M));
+    const int j1 = uniform(min(max(toff[tb + 1], j0), M));
+    auto fetch = [&](int j) {
+        return den_record(j < j1 ? fwd_record(sorted_gauss[j], means, opacity, cov_inv, lb, ub, x0, y0, z0)
+                                 : fwd_record_empty(), cz);
+    };
+    float dacc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    DenRec nxt = fetch(j0 + lane);
+    for (int jb = j0; jb < j1; jb += 64) {
+        wave_lds_sync();   // the previous records are read
+        sl[lane] = nxt;
+        wave_lds_sync();
+        nxt = fetch(jb + 64 + lane);
+        // slots past the list hold empty records (weight 0), so every lane group runs the same count
+        const int n4 = uniform((min(64, j1 - jb) + 3) >> 2);
+        for (int k4 = 0; k4 < n4; ++k4) {
+            // fwd_column_weights with the z terms read from the record
+            const uint4* rp = reinterpret_cast<const uint4*>(&sl[4 * k4 + ph]);
+            const uint4 q0 = rp[0], q1 = rp[1], q2 = rp[2], q3 = rp[3], q4 = rp[4];
+            const float dx = cxl - __uint_as_float(q0.x), dy = cyl - __uint_as_float(q0.y);
+            const float ro = __uint_as_float(q0.z), a12 = __uint_as_float(q0.w);
+            const float a00 = __uint_as_float(q1.x), a01 = __uint_as_float(q1.y);
+            const float a11 = __uint_as_float(q1.z), a02 = __uint_as_float(q1.w);
+            const float dz[4] = {__uint_as_float(q2.x), __uint_as_float(q2.y), __uint_as_float(q2.z),
+                                 __uint_as_float(q2.w)};
+            const float fz[4] = {__uint_as_float(q3.x), __uint_as_float(q3.y), __uint_as_float(q3.z),
+                                 __uint_as_float(q3.w)};
+            float F = fmaf(fmaf(a00, dx, a01 * dy), dx, a11 * dy * dy);
+            F = ((q4.x >> col) & 1u) ? F : -__builtin_inff();
+            const float Gxy = fmaf(a02, dx, a12 * dy);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) dacc[c] += ro * __builtin_amdgcn_exp2f(fmaf(Gxy, dz[c], F) + fz[c]);
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {   // the four lane groups: (ph 0 + ph 1) + (ph 2 + ph 3)
+        dacc[c] += xor_shfl<16>(dacc[c]);
+        dacc[c] += __shfl_xor(dacc[c], 32, 64);
+    }
+    const int x = x0 + (col >> 2), y = y0 + (col & 3);
+    if (ph == 0 && x < G.dims[0] && y < G.dims[1]) {
+        float* out = density + voxel_index(G, x, y, z0);
+        const int nz = min(kTile, G.dims[2] - z0);
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (c < nz) out[c] = dacc[c];
+    }
+}
+
+hipError_t launch_forward_density(const Grid& G, const float* means, const float* opacity,
+                                  const float* cov_inv, const int* lb, const int* ub,
+                                  const int* tile_offsets, const int* sorted_gauss, int M,
+                                  float* density, hipStream_t s) {
+    const int T = scene_tiles(G) * G.scenes;
+    if (T <= 0) return hipSuccess;
+    const int groups = (int)ceil_div(T, kDenWaves);
+    const int blocks = (int)ceil_div(groups, 8) * 8;
+    G2V_LAUNCH(k_fwd_density, dim3(blocks), dim3(kDenWaves * 64), 0, s, G, means, opacity, cov_inv, lb,
+               ub, tile_offsets, sorted_gauss, M, density);
+    return hipGetLastError();
+}
 
 struct FwdSmem {
     bf16x8 whi[kFwdKSteps][2][64];   // A operand, hi part: [k step][voxel block][lane]
@@ -258,50 +354,14 @@ __device__ __forceinline__ void fwd_build_w(FwdSmem& sm, int j0, int kbeg, int k
                                             const float (&cz)[4], float cxl, float cyl) {
     const int nslots = ksteps * 16;
     for (int k = threadIdx.x; k < nslots; k += kFwdThreads) {
-        FwdRec r;
         if (k < klen) {
             const int g = sorted_gauss[j0 + kbeg + k];
-            float A[9];
-#pragma unroll
-            for (int i = 0; i < 9; ++i) A[i] = cov_inv[g * 9 + i];
-            const float mu2 = means[g * 3 + 2];
-            int l[3], u[3];
-#pragma unroll
-            for (int i = 0; i < 3; ++i) {
-                l[i] = lb[g * 3 + i];
-                u[i] = ub[g * 3 + i];
-            }
-            r.mux = means[g * 3 + 0];
-            r.muy = means[g * 3 + 1];
-            r.o = opacity[g];
-            r.a00 = kq * A[0];
-            r.a01 = kq * (A[1] + A[3]);
-            r.a11 = kq * A[4];
-            r.a02 = kq * (A[2] + A[6]);
-            r.a12 = kq * (A[5] + A[7]);
-            r.mu2 = mu2;
-            r.a22 = kq * A[8];
-            uint32_t xm = 0, ym = 0, zm = 0;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                zm |= (z0 + c >= l[2] && z0 + c <= u[2]) ? (1u << c) : 0u;
-                xm |= (x0 + c >= l[0] && x0 + c <= u[0]) ? (1u << c) : 0u;
-                ym |= (y0 + c >= l[1] && y0 + c <= u[1]) ? (1u << c) : 0u;
-            }
-            r.zmask = zm;
-            uint32_t m = 0;
-#pragma unroll
-            for (int a = 0; a < 4; ++a) m |= (xm >> a) & 1u ? ym << (4 * a) : 0u;
-            r.xymask = m;
+            sm.rec[k] = fwd_record(g, means, opacity, cov_inv, lb, ub, x0, y0, z0);
             sm.roff[k] = (uint32_t)g * row_bytes;
         } else {
-            r.mux = r.muy = r.o = r.a12 = 0.0f;
-            r.a00 = r.a01 = r.a11 = r.a02 = 0.0f;
-            r.mu2 = r.a22 = 0.0f;
-            r.xymask = r.zmask = 0;
+            sm.rec[k] = fwd_record_empty();
             sm.roff[k] = zero_off;
         }
-        sm.rec[k] = r;
     }
     __syncthreads();
     const int col = threadIdx.x & 15;
@@ -310,28 +370,12 @@ __device__ __forceinline__ void fwd_build_w(FwdSmem& sm, int j0, int kbeg, int k
         float wv[4][8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const uint4* rp = reinterpret_cast<const uint4*>(&sm.rec[o * 8 + i]);   // 16 lanes each
-            const uint4 q0 = rp[0], q1 = rp[1], q2 = rp[2];
-            const uint32_t m = q2.z, zm = q2.w;
-            const float dx = cxl - __uint_as_float(q0.x), dy = cyl - __uint_as_float(q0.y);
-            const float ro = __uint_as_float(q0.z), a12 = __uint_as_float(q0.w);
-            const float a00 = __uint_as_float(q1.x), a01 = __uint_as_float(q1.y);
-            const float a11 = __uint_as_float(q1.z), a02 = __uint_as_float(q1.w);
-            const float mu2 = __uint_as_float(q2.x), a22 = __uint_as_float(q2.y);
-            float dz[4], fz[4];
+            float w[4];
+            fwd_column_weights(&sm.rec[o * 8 + i], col, cxl, cyl, cz, w);   // 16 lanes each
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                dz[c] = cz[c] - mu2;
-                fz[c] = ((zm >> c) & 1u) ? a22 * dz[c] * dz[c] : -__builtin_inff();
-            }
-            float F = fmaf(fmaf(a00, dx, a01 * dy), dx, a11 * dy * dy);
-            F = ((m >> col) & 1u) ? F : -__builtin_inff();
-            const float Gxy = fmaf(a02, dx, a12 * dy);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const float w = ro * __builtin_amdgcn_exp2f(fmaf(Gxy, dz[c], F) + fz[c]);
-                dacc[c] += w;
-                wv[c][i] = fmaxf(w, 0.0f);   // feature gate of the reference (.cu:936)
+                dacc[c] += w[c];
+                wv[c][i] = fmaxf(w[c], 0.0f);   // feature gate of the reference (.cu:936)
             }
         }
         // voxel (a, b, c) of the tile is row 16a + 4b + c of W: block a/2, row 16(a%2) + 4b + c

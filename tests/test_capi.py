@@ -31,7 +31,7 @@ def test_header_symbols_exported():
 
 
 def test_abi_version():
-    assert _lib().load().g2v_abi_version() == _lib().ABI_VERSION == 12
+    assert _lib().load().g2v_abi_version() == _lib().ABI_VERSION == 13
 
 
 def test_loader_refuses_other_abi(monkeypatch):
@@ -74,21 +74,27 @@ def test_invalid_arguments_fail_before_any_launch():
                               ctypes.byref(M), None, 0, None, None)
     assert rc == 1 and b"n = -1" in lib.g2v_last_error()
     # too many pairs for the int32 CSR
-    rc = lib.g2v_forward_splat(1, 0, None, None, None, 0, None, vs, vr, None, None, None, None, 1 << 31,
+    rc = lib.g2v_forward_splat(1, 0, None, None, None, 0, None, 0, vs, vr, None, None, None, None, 1 << 31,
                                None, None, None, None, None, None, None, 0, None)
     assert rc == 3
     # unknown feature type
-    rc = lib.g2v_forward_splat(1, 0, None, None, None, 7, None, vs, vr, None, None, None, None, 0,
+    rc = lib.g2v_forward_splat(1, 0, None, None, None, 7, None, 0, vs, vr, None, None, None, None, 0,
                                None, None, None, None, None, None, None, 0, None)
     assert rc == 1 and b"feat_dtype" in lib.g2v_last_error()
     # missing workspace
-    rc = lib.g2v_forward_splat(0, 0, None, None, None, 0, None, vs, vr, None, None, None, None, 0, None,
+    rc = lib.g2v_forward_splat(0, 0, None, None, None, 0, None, 0, vs, vr, None, None, None, None, 0, None,
                                ctypes.c_void_p(16), None, None, None, None, None, 0, None)
     assert rc == 1 and b"workspace" in lib.g2v_last_error()
     # features without their packed rows
-    rc = lib.g2v_forward_splat(4, 8, None, None, ctypes.c_void_p(16), 0, None, vs, vr, None, None, None, None, 0,
+    rc = lib.g2v_forward_splat(4, 8, None, None, ctypes.c_void_p(16), 0, None, 0, vs, vr, None, None, None, None, 0,
                                None, ctypes.c_void_p(16), ctypes.c_void_p(16), None, None, None, None, 0, None)
     assert rc == 1 and b"packed_features" in lib.g2v_last_error()
+    # packed rows of too few bytes for (n, feat_dim): rejected before anything is queued
+    need = lib.g2v_forward_packed_bytes(4, 8)
+    rc = lib.g2v_forward_splat(4, 8, None, None, ctypes.c_void_p(16), 0, ctypes.c_void_p(16), need - 1, vs, vr, None,
+                               None, None, None, 0, None, ctypes.c_void_p(16), ctypes.c_void_p(16), None, None, None,
+                               None, 0, None)
+    assert rc == 1 and b"packed features buffer too small" in lib.g2v_last_error()
     # packing: buffer size, type and pointers are checked before anything is queued
     need = lib.g2v_forward_packed_bytes(4, 8)   # 5 rows (a zero row last) of channels padded to 128
     assert need == 5 * 128 * 4 and lib.g2v_forward_packed_bytes(4, 0) == 0
@@ -179,6 +185,11 @@ def test_batch_arguments_and_workspaces():
     assert s6 > s1 >= lib.g2v_forward_splat_workspace(300, 64, 10_000, vs, vr)
     assert (lib.g2v_batch_backward_workspace(6, 300, 64, 10_000, 2000, vs, vr) >
             lib.g2v_batch_backward_workspace(1, 300, 64, 10_000, 2000, vs, vr))
+    # B x 10,000 tiles beyond int32 (B n still fits): no size, as the plan would refuse it
+    B = 300_000
+    assert lib.g2v_batch_plan_workspace(B, 1) > 0
+    assert lib.g2v_batch_forward_splat_workspace(B, 1, 64, 10_000, vs, vr) == 0
+    assert lib.g2v_batch_backward_workspace(B, 1, 64, 10_000, 2000, vs, vr) == 0
     cnt = (ctypes.c_longlong * 8)()
     rc = lib.g2v_batch_forward_plan(0, 300, one, one, vs, vr, one, one, one, one, one, one, 1 << 20, 1, cnt, None)
     assert rc == 1 and b"num_scenes = 0" in lib.g2v_last_error()

@@ -90,7 +90,7 @@ def _both(w, seed=0, valid_frac=0.7, gl=1.7, feats_dtype=torch.float32):
 
     b = [t.to(dev).requires_grad_() for t in (m, o, c, f)]
     d2, l2, g2, stats = fused(b[0], b[1], b[2], b[3], label, mask, target)
-    assert not g2.requires_grad
+    assert g2.requires_grad   # grid_feats keeps its gradient path (unused here: None reaches the backward)
     names, _ = _launched(lambda: torch.autograd.backward([d2, l2], [gD, glt]))
     assert stats[0] > 0 and stats[1] > 0
     return (d1, g1, l1), (d2, g2, l2), [t.grad for t in a], [t.grad for t in b], names, \
@@ -115,15 +115,15 @@ def test_fused_equals_chained(name):
     assert max(errs) < TOL, errs
 
 
-def test_fused_against_the_f64_oracle_chain():
-    from CudaGaussianVoxelizer import _C
-    w = CASES["c64"]
-    say("[cosine fused] float64 oracle chain, c64")
+@pytest.mark.parametrize("name", list(CASES))
+def test_fused_against_the_f64_oracle_chain(name):
+    w = CASES[name]
+    say(f"[cosine fused] float64 oracle chain, {name}")
     _, (d2, g2, l2), _, gb, _, (m, o, c, f, label, mask, target, gD) = _both(w, gl=2.3)
     vs, vr = np.array(w.voxel_size, np.float32), np.array(w.voxel_range, np.float32)
     bx = O.gaussian_boxes(m.numpy(), c.numpy(), vs, vr)
     lab, msk, tgt = label.cpu().numpy(), mask.cpu().numpy(), target.cpu().numpy()
-    gfe = g2.cpu().numpy()
+    gfe = g2.detach().cpu().numpy()
     count = int(O.cosine_valid(lab, msk).sum())
     gF = O.cosine_loss_grad_f64(2.3, lab, msk, gfe, tgt, count)
     ref = O.backward_f64(gD.cpu().numpy(), gF, m.numpy(), o.numpy(), c.numpy(), f.numpy(), bx["lb"], bx["ub"], vs, vr,
@@ -203,6 +203,35 @@ def test_fused_input_errors_raise():
         _C.gaussian_voxelizer_backward_cosine(*args(coef[:-1].contiguous(), target))
     with pytest.raises(RuntimeError):   # target of another shape
         _C.gaussian_voxelizer_backward_cosine(*args(coef, target[..., :32].contiguous()))
+
+
+def test_grid_feats_used_elsewhere_too():
+    """grid_feats of the fused module also feeds another loss: its gradient reaches the Gaussians
+    (the module then chains), and every input gradient equals the separate modules' with the same
+    second use."""
+    from CudaGaussianVoxelizer import (PyCudaFeatsCosineLoss, PyCudaGaussianVoxelizer,
+                                       PyCudaGaussianVoxelizerCosineLoss)
+    w = CASES["c64"]
+    dev = torch.device("cuda")
+    say("[cosine fused] grid_feats used by a second loss")
+    m, o, c, f = W.generate(w, seed=6)
+    label, mask, target, gD = _loss_inputs(W.grid_shape(w), f.shape[1], 7)
+    wgt = torch.randn(W.grid_shape(w) + (f.shape[1],), generator=torch.Generator().manual_seed(8)).to(dev)
+    a = [t.to(dev).requires_grad_() for t in (m, o, c, f)]
+    d1, g1, _ = PyCudaGaussianVoxelizer(list(w.voxel_size), list(w.voxel_range))(*a)
+    l1, _ = PyCudaFeatsCosineLoss()(label, mask, g1, target)
+    ((d1 * gD).sum() + 1.3 * l1 + (g1 * wgt).sum()).backward()
+    b = [t.to(dev).requires_grad_() for t in (m, o, c, f)]
+    d2, l2, g2, _ = PyCudaGaussianVoxelizerCosineLoss(list(w.voxel_size), list(w.voxel_range))(*b, label, mask, target)
+    ((d2 * gD).sum() + 1.3 * l2 + (g2 * wgt).sum()).backward()
+    errs = [O.rel_err(y.grad.cpu().numpy(), x.grad.cpu().numpy()) for x, y in zip(a, b)]
+    say(f"   rel err means/opacity/cov/features vs chained: {errs}")
+    assert max(errs) < TOL, errs
+    # the second use moves the gradients: without it they differ
+    c_ = [t.to(dev).requires_grad_() for t in (m, o, c, f)]
+    d3, l3, _, _ = PyCudaGaussianVoxelizerCosineLoss(list(w.voxel_size), list(w.voxel_range))(*c_, label, mask, target)
+    ((d3 * gD).sum() + 1.3 * l3).backward()
+    assert O.rel_err(c_[3].grad.cpu().numpy(), b[3].grad.cpu().numpy()) > 1e-2
 
 
 def test_loss_alone_backward():
