@@ -640,7 +640,14 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
         // four raw G values (stage gs), masks them (row outside the grid, channels past C),
         // splits them and writes hi and lo into A buffer ab: channels 4sq.. of the chunk are k
         // half sq/4, lane group (sq/2)&1, half sq&1 of the lane's 16-byte fragment.
-        const int sv = threadIdx.x >> 3, sq = threadIdx.x & 7;
+        // float: wave w writes the fragments of voxel block w&1, lane group (w/2)&1, k half w/4,
+        // lane (sv&31, sq&1): 32 whole 16-byte fragments, one contiguous 512-byte run per array, so
+        // the 8-byte writes are free of bank conflicts (a wave of 8 voxels x 8 quads would put four
+        // writes on every bank); its reads, 16 bytes of 32 consecutive rows at pieces sq and sq^1,
+        // stay conflict-free through the row swizzle.  bfloat16 rows are not swizzled, so there the
+        // wave keeps 8 voxels x 8 octets (each read covers whole rows).
+        const int sv = BF ? threadIdx.x >> 3 : (((threadIdx.x >> 6) & 1) << 5) | ((threadIdx.x & 63) >> 1);
+        const int sq = BF ? threadIdx.x & 7 : ((threadIdx.x >> 8) << 2) | (((threadIdx.x >> 7) & 1) << 1) | (threadIdx.x & 1);
         const bool svok = sm.vlin[sv] >= 0;
         auto write_a = [&](int ch, int gs, int ab) {
             const int lim = svok ? min(max(C - (ch * kKc + 4 * sq), 0), 4) : 0;
