@@ -317,16 +317,6 @@ __device__ __forceinline__ void wait_vm() {
 }
 
 
-// Workgroup barrier for LDS hand-offs only: waits for this wave's LDS operations and meets the
-// other waves, without the release fence of __syncthreads (that fence would also wait for every
-// outstanding global load, including the direct-to-LDS loads kept in flight on purpose).  The
-// caller has already waited (vmcnt) for the direct-to-LDS loads the next step reads.
-__device__ __forceinline__ void lds_barrier() {
-    __asm__ __volatile__("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt((15 << 0) | (7 << 4) | (0 << 8) | (3 << 14));   // lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
-    __asm__ __volatile__("" ::: "memory");
-}
 
 // Geometry of one lane's 16 epilogue elements against its Gaussian.  The elements of a lane are
 // the 2 x 2 x 4 voxel block x = x0 + a, y = y0 + 2b, z = z0 + c of the tile (a, b < 2, c < 4), so
@@ -587,9 +577,11 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
 
     for (int pbase = 0; pbase < Ng; pbase += kBtPass) {
         const int pcount = min(kBtPass, Ng - pbase);
-        __syncthreads();
+        // LDS-only barriers here and in the epilogues: the weight and partial stores (read by later
+        // kernels only) stay in flight while the next steps run
+        lds_barrier();
         stage_params(sm.pt, sorted_gauss + j0 + pbase, pcount, means, cov_inv, opacity, lb, ub);
-        __syncthreads();
+        lds_barrier();
 
         // F rows by direct-to-LDS loads: row group rg = wave + kBtWaves*i (8 rows, 1 KB) is
         // loaded by this wave; lane = (row rg*8 + lane/8, slot lane%8) and slot p carries the
@@ -933,14 +925,14 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
                 const int i = (lane >> 1) & 15;
                 sm.tpart[ngrp][mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3)] = rs;
             }
-            __syncthreads();
+            lds_barrier();
             if (threadIdx.x < 64) {
                 const int r = threadIdx.x;
                 const float s = ((sm.tpart[0][r] + sm.tpart[1][r]) + sm.tpart[2][r]) + sm.tpart[3][r];
                 // sum_g [w>0] w u / max(D, eps) = sum_c gF F; zero where D < eps (reference .cu:1450)
                 sm.tv[r] = (sm.vlin[r] >= 0 && sm.D[r] >= kEps) ? s : 0.0f;
             }
-            __syncthreads();
+            lds_barrier();
         }
 
         // ---- epilogue 2: r = gw e of every element (e from epilogue 1; an invalid element
@@ -1006,7 +998,7 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
                 for (int k = 0; k < kNumGrads; ++k) sm.u.xch[mb][slot][k] = gr[k];
             }
         }
-        __syncthreads();
+        lds_barrier();
         for (int slot = threadIdx.x; slot < pcount; slot += kBtThreads) {
             const int g = sm.pt.gid[slot];
             const int tx0 = sm.pt.lb[0][slot] / kTile, ty0 = sm.pt.lb[1][slot] / kTile, tz0 = sm.pt.lb[2][slot] / kTile;
@@ -1227,13 +1219,13 @@ __global__ void __launch_bounds__(kBsThreads) k_bwd_tile_short(
         tsum += (w > 0.0f) ? wtil * u[i] : 0.0f;
     }
     sm.tpart[wave][lane] = tsum;
-    __syncthreads();
+    lds_barrier();   // the weight stores stay in flight (later kernels read them)
     if (threadIdx.x < 64) {
         const float s = ((sm.tpart[0][lane] + sm.tpart[1][lane]) + sm.tpart[2][lane]) + sm.tpart[3][lane];
         // sum_g [w>0] w u / max(D, eps) = sum_c gF F; zero where D < eps (reference .cu:1450)
         sm.tv[lane] = (rowok && sm.D[lane] >= kEps) ? s : 0.0f;
     }
-    __syncthreads();
+    lds_barrier();
 
     // r = gw e and its moments over the tile's voxels (d = centre - mu), as k_bwd_tile stores them
     const float tv = sm.tv[lane], gd = sm.gD[lane];

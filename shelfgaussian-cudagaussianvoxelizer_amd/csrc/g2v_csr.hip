@@ -237,7 +237,7 @@ __global__ void __launch_bounds__(kScan1Threads) k_scan_single(ScanJob j0, ScanJ
             const int e = k * kScan1Threads + threadIdx.x;
             buf[(e / kScan1Items) * kScan1Row + e % kScan1Items] = (base + e < n) ? ld[k] : 0;
         }
-        __syncthreads();
+        lds_barrier();
         int* row = &buf[threadIdx.x * kScan1Row];
         long long local = 0;
 #pragma unroll
@@ -249,7 +249,7 @@ __global__ void __launch_bounds__(kScan1Threads) k_scan_single(ScanJob j0, ScanJ
             if (lane >= off) x += t;
         }
         if (lane == 63) wsum[wave] = x;
-        __syncthreads();
+        lds_barrier();
         long long wcarry = 0, tot = 0;
 #pragma unroll
         for (int w = 0; w < kScan1Threads / 64; ++w) {
@@ -264,13 +264,13 @@ __global__ void __launch_bounds__(kScan1Threads) k_scan_single(ScanJob j0, ScanJ
             row[r] = (int)(inclusive ? nxt : run);
             run = nxt;
         }
-        __syncthreads();
+        lds_barrier();
 #pragma unroll
         for (int k = 0; k < kScan1Items; ++k) {
             const int e = k * kScan1Threads + threadIdx.x;
             if (base + e < n) out[base + e] = buf[(e / kScan1Items) * kScan1Row + e % kScan1Items];
         }
-        __syncthreads();   // buf and wsum are rewritten by the next tile
+        lds_barrier();   // buf and wsum are rewritten by the next tile
         carry += tot;
     }
     if (threadIdx.x == 0 && total_dev) *total_dev = carry;
@@ -511,7 +511,7 @@ __global__ void __launch_bounds__(kSortThreads) k_radix_digit_scan(int* __restri
             if (lane >= off) x += t;
         }
         if (lane == 63) wsum[wave] = x;
-        __syncthreads();
+        lds_barrier();
         int wc = 0, tot = 0;
 #pragma unroll
         for (int w = 0; w < kSortThreads / 64; ++w) {
@@ -525,7 +525,7 @@ __global__ void __launch_bounds__(kSortThreads) k_radix_digit_scan(int* __restri
             run += v[k];
         }
         carry += tot;
-        __syncthreads();   // wsum is rewritten by the next round
+        lds_barrier();   // wsum is rewritten by the next round
     }
     if (threadIdx.x == 0) dtot[d] = carry;
 }
@@ -553,7 +553,7 @@ __global__ void __launch_bounds__(kSortThreads) k_radix_scatter(
             if (lane >= off) x += u;
         }
         if (lane == 63) dsum[wave] = x;
-        __syncthreads();
+        lds_barrier();
         int wc = 0;
 #pragma unroll
         for (int w = 0; w < kSortThreads / 64; ++w) wc += w < wave ? dsum[w] : 0;
@@ -562,7 +562,7 @@ __global__ void __launch_bounds__(kSortThreads) k_radix_scatter(
             wave_cnt[0][d] = wave_cnt[1][d] = wave_cnt[2][d] = wave_cnt[3][d] = 0;
         }
     }
-    __syncthreads();
+    lds_barrier();
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     const int64_t base = (int64_t)blockIdx.x * kSortTile;
     // the block's keys and values are all requested up front (indices clamped into the arrays):
@@ -591,19 +591,19 @@ __global__ void __launch_bounds__(kSortThreads) k_radix_scatter(
         }
         const int rank = __popcll(peers & lt_mask);
         if (valid && rank == 0) wave_cnt[wave][d] = __popcll(peers);
-        __syncthreads();
+        lds_barrier();
         if (valid) {
             int pos = running[d] + rank;
             for (int w = 0; w < wave; ++w) pos += wave_cnt[w][d];
             keys_out[pos] = k;
             vals_out[pos] = v;
         }
-        __syncthreads();
+        lds_barrier();
         for (int dd = threadIdx.x; dd < radix; dd += kSortThreads) {
             running[dd] += wave_cnt[0][dd] + wave_cnt[1][dd] + wave_cnt[2][dd] + wave_cnt[3][dd];
             wave_cnt[0][dd] = wave_cnt[1][dd] = wave_cnt[2][dd] = wave_cnt[3][dd] = 0;
         }
-        __syncthreads();
+        lds_barrier();
     }
 }
 

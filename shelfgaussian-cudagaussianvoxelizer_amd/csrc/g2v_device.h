@@ -46,6 +46,18 @@ __host__ __device__ __forceinline__ int scene_of(const Grid& G, int g) {
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
+// Workgroup barrier for LDS hand-offs only: waits for this wave's LDS operations and meets the
+// other waves, without the release fence of __syncthreads.  That fence also waits for every
+// outstanding global load and store of the wave (one in-order counter): direct-to-LDS loads kept in
+// flight on purpose, and stores that no thread of the kernel reads back.  A caller that needs loaded
+// data in LDS waits for it (vmcnt) before the barrier.
+__device__ __forceinline__ void lds_barrier() {
+    __asm__ __volatile__("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((15 << 0) | (7 << 4) | (0 << 8) | (3 << 14));   // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    __asm__ __volatile__("" ::: "memory");
+}
+
 // Voxel (x, y, z) of in-tile voxel index lv (x slowest, z fastest; reference .cu:43-55).
 __device__ __forceinline__ void tile_voxel(const Grid& G, int tile, int lv, int& x, int& y, int& z) {
     const int tyz = G.tiles[1] * G.tiles[2];
