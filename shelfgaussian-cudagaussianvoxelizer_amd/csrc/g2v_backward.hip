@@ -751,17 +751,22 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
         // The chunk loop, instantiated for the wave's group count NF (exact wait immediates;
         // waves of one workgroup may run different instantiations, with the same barriers).
         const int clast = nchk - 1;
+        // Odd passes walk the chunks backwards: a long list's next pass then starts on the G chunks
+        // the previous pass read last, which are still in L2 (forward order re-read the tile's G
+        // from HBM at every pass).  Chunk nchk (past the end) stays past the end.
+        const bool rev = ((pbase / kBtPass) & 1) != 0;
+        auto cm = [&](int c) { return (rev && c <= clast) ? clast - c : c; };
         auto chunk_loop = [&](auto nfc) {
             constexpr int NF = decltype(nfc)::value;
             constexpr int kLd = NF + kNG;   // loads per wave per chunk
-            dma_g(0, 0);
-            dma_f(0, 0, 0, NF);
-            dma_g(min(1, clast), 1);
-            dma_f(min(1, clast), 1, 0, NF);
-            dma_g(min(2, clast), 2);
+            dma_g(cm(0), 0);
+            dma_f(cm(0), 0, 0, NF);
+            dma_g(cm(min(1, clast)), 1);
+            dma_f(cm(min(1, clast)), 1, 0, NF);
+            dma_g(cm(min(2, clast)), 2);
             wait_vm<kLd>();               // G(0), F(0), G(1) complete
             lds_barrier();
-            write_a(0, 0, 0);
+            write_a(cm(0), 0, 0);
             lds_barrier();
             for (int ch = 0; ch < nchk; ++ch) {
                 const int st = ch % kBtStages, ab = ch & 1;
@@ -770,13 +775,13 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
                 asm volatile("" ::: "memory");   // every operand read issued before the first MFMA
                 mult(0, ops);
                 __builtin_amdgcn_sched_barrier(0);
-                write_a(ch + 1, (ch + 1) % kBtStages, ab ^ 1);
-                dma_f(min(ch + 2, clast), (ch + 2) % kBtStages, 0, min(NF, kBtDma / 2));
+                write_a(cm(ch + 1), (ch + 1) % kBtStages, ab ^ 1);
+                dma_f(cm(min(ch + 2, clast)), (ch + 2) % kBtStages, 0, min(NF, kBtDma / 2));
                 __builtin_amdgcn_sched_barrier(0);
                 mult(1, ops);
                 __builtin_amdgcn_sched_barrier(0);
-                dma_f(min(ch + 2, clast), (ch + 2) % kBtStages, kBtDma / 2, NF);
-                dma_g(min(ch + 3, clast), st);
+                dma_f(cm(min(ch + 2, clast)), (ch + 2) % kBtStages, kBtDma / 2, NF);
+                dma_g(cm(min(ch + 3, clast)), st);
                 wait_vm<kLd>();           // F(ch+1) and G(ch+2) complete
                 lds_barrier();
             }
@@ -786,27 +791,27 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
         auto chunk_loop_fu = [&](auto nfc) {
             constexpr int NF = decltype(nfc)::value;
             constexpr int kLg = kSrc * kNG;   // G loads per wave per chunk
-            dma_g(0, 0);
-            dma_f(0, 0, 0, NF);
-            dma_g(min(1, clast), 1);
-            dma_g(min(2, clast), 2);
+            dma_g(cm(0), 0);
+            dma_f(cm(0), 0, 0, NF);
+            dma_g(cm(min(1, clast)), 1);
+            dma_g(cm(min(2, clast)), 2);
             wait_vm<kLg>();               // G(0), F(0), G(1) complete
             lds_barrier();
-            write_a(0, 0, 0);
+            write_a(cm(0), 0, 0);
             lds_barrier();
             for (int ch = 0; ch < nchk; ++ch) {
                 const int st = ch % kBtStages, fb = ch & 1, ab = ch & 1;
-                dma_f(min(ch + 1, clast), fb ^ 1, 0, NF);
+                dma_f(cm(min(ch + 1, clast)), fb ^ 1, 0, NF);
                 StepOps ops;
                 load_ops(fb, ab, ops);
                 asm volatile("" ::: "memory");   // every operand read issued before the first MFMA
                 mult(0, ops);
                 __builtin_amdgcn_sched_barrier(0);
-                write_a(ch + 1, (ch + 1) % kBtStages, ab ^ 1);
+                write_a(cm(ch + 1), (ch + 1) % kBtStages, ab ^ 1);
                 __builtin_amdgcn_sched_barrier(0);
                 mult(1, ops);
                 __builtin_amdgcn_sched_barrier(0);
-                dma_g(min(ch + 3, clast), st);
+                dma_g(cm(min(ch + 3, clast)), st);
                 wait_vm<kLg>();           // F(ch+1) and G(ch+2) complete
                 lds_barrier();
             }
