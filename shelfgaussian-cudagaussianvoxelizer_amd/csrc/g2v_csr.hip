@@ -463,7 +463,7 @@ hipError_t launch_fill_cells(int n, const int* lb, const int* ub, const int* off
 //   per pass: k_radix_hist (digit counts per 4096-key block, digit-major) -> k_radix_digit_scan
 //             (one workgroup per digit: exclusive scan over the blocks, and the digit's total)
 //             -> k_radix_scatter (digit bases from the totals; stable rank: ballot match inside a
-//             wave, LDS across waves)
+//             wave, LDS across waves; the block's keys sorted in LDS, then written out run by run)
 // ------------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(kSortThreads) k_radix_hist(const int* __restrict__ keys, int64_t M,
                                                              int shift, int dbits, int nblk,
@@ -530,59 +530,76 @@ __global__ void __launch_bounds__(kSortThreads) k_radix_digit_scan(int* __restri
     if (threadIdx.x == 0) dtot[d] = carry;
 }
 
+// Wave w of a block owns its keys w*1024 .. w*1024 + 1023 (16 rounds of 64, in order).  Each wave
+// ranks its own keys on its own (ballot match inside a round, a per-wave LDS count of each digit
+// across its rounds), with no block barrier; the waves' digit counts then give every wave its base
+// within each digit (waves in order: stable), the keys are placed in LDS in sorted order, and the
+// block writes them out in that order: consecutive threads write consecutive positions of one
+// digit's run, so a store instruction touches a few cache lines instead of one per lane.
+constexpr int kSortWaveKeys = kSortTile / (kSortThreads / 64);
 __global__ void __launch_bounds__(kSortThreads) k_radix_scatter(
     const int* __restrict__ keys_in, const int* __restrict__ vals_in, int* __restrict__ keys_out,
     int* __restrict__ vals_out, int64_t M, int shift, int dbits, int nblk,
     const int* __restrict__ gscan, const int* __restrict__ dtot) {
-    static_assert(kSortThreads == 256, "one digit per thread");
-    __shared__ int wave_cnt[4][256];
-    __shared__ int running[256];
-    __shared__ int dsum[kSortThreads / 64];
+    static_assert(kSortThreads == 256 && kSortWaveKeys == 64 * kSortRounds, "one digit per thread");
+    __shared__ int wcnt[4][256];   // per wave: keys of each digit seen so far, then its base
+    __shared__ int gshift[256];    // global position - local position of the digit's keys
+    __shared__ int dsum[2][kSortThreads / 64];
+    __shared__ int lk[kSortTile], lv[kSortTile];
     const int radix = 1 << dbits;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    {
-        // digit base: exclusive scan of the digit totals (digit = thread), plus the block's own
-        // exclusive offset within its digit
-        const int d = threadIdx.x;
-        const int t = d < radix ? dtot[d] : 0;
-        const int blk = d < radix ? gscan[(int64_t)d * nblk + blockIdx.x] : 0;
-        int x = t;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const int u = __shfl_up(x, off, 64);
-            if (lane >= off) x += u;
-        }
-        if (lane == 63) dsum[wave] = x;
-        lds_barrier();
-        int wc = 0;
-#pragma unroll
-        for (int w = 0; w < kSortThreads / 64; ++w) wc += w < wave ? dsum[w] : 0;
-        if (d < radix) {
-            running[d] = wc + x - t + blk;
-            wave_cnt[0][d] = wave_cnt[1][d] = wave_cnt[2][d] = wave_cnt[3][d] = 0;
-        }
-    }
-    lds_barrier();
-    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     const int64_t base = (int64_t)blockIdx.x * kSortTile;
-    // the block's keys and values are all requested up front (indices clamped into the arrays):
-    // the rounds below then wait for their own load only the first time
+    const int cnt = (int)min((int64_t)kSortTile, M - base);   // keys of this block
+    const int w0 = wave * kSortWaveKeys;                       // the wave's first key in the block
+    // the wave's keys and values are all requested up front (indices clamped into the arrays)
     int kr[kSortRounds], vr[kSortRounds];
 #pragma unroll
     for (int r = 0; r < kSortRounds; ++r) {
-        const int64_t i = min(base + (int64_t)r * kSortThreads + threadIdx.x, M - 1);
+        const int64_t i = min(base + w0 + r * 64 + lane, M - 1);
         kr[r] = keys_in[i];
         vr[r] = vals_in[i];
     }
+    int lbase = 0;   // thread d: the digit's first local position
+    {
+        // digit d (= thread): global base = exclusive scan of the digit totals + the block's offset
+        // within the digit; local base = exclusive scan of the block's own digit counts (the
+        // difference of consecutive block offsets, or of the total for the last block)
+        const int d = threadIdx.x;
+        const int t = d < radix ? dtot[d] : 0;
+        const int blk = d < radix ? gscan[(int64_t)d * nblk + blockIdx.x] : 0;
+        const int nxt = d < radix ? (blockIdx.x + 1 < nblk ? gscan[(int64_t)d * nblk + blockIdx.x + 1] : t) : 0;
+        const int c = nxt - blk;
+        int x = t, y = c;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int u = __shfl_up(x, off, 64), w = __shfl_up(y, off, 64);
+            if (lane >= off) {
+                x += u;
+                y += w;
+            }
+        }
+        if (lane == 63) {
+            dsum[0][wave] = x;
+            dsum[1][wave] = y;
+        }
+        wcnt[0][d] = wcnt[1][d] = wcnt[2][d] = wcnt[3][d] = 0;
+        lds_barrier();
+        int wc = 0, wl = 0;
+#pragma unroll
+        for (int w = 0; w < kSortThreads / 64; ++w) {
+            wc += w < wave ? dsum[0][w] : 0;
+            wl += w < wave ? dsum[1][w] : 0;
+        }
+        lbase = wl + y - c;
+        gshift[d] = wc + x - t + blk - lbase;
+    }
+    // ranks inside the wave: pre[r] = keys of the same digit before this one among the wave's keys
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    int pre[kSortRounds];
 #pragma unroll
     for (int r = 0; r < kSortRounds; ++r) {
-        const int64_t rbase = base + (int64_t)r * kSortThreads;
-        if (rbase >= M) break;  // uniform across the block
-        const int64_t i = rbase + threadIdx.x;
-        const bool valid = i < M;
-        const int k = valid ? kr[r] : 0;
-        const int v = valid ? vr[r] : 0;
-        const int d = (k >> shift) & (radix - 1);
+        const bool valid = w0 + r * 64 + lane < cnt;
+        const int d = (kr[r] >> shift) & (radix - 1);
         uint64_t peers = __ballot(valid);
         for (int b = 0; b < dbits; ++b) {
             const bool bit = (d >> b) & 1;
@@ -590,20 +607,39 @@ __global__ void __launch_bounds__(kSortThreads) k_radix_scatter(
             peers &= bit ? m : ~m;
         }
         const int rank = __popcll(peers & lt_mask);
-        if (valid && rank == 0) wave_cnt[wave][d] = __popcll(peers);
-        lds_barrier();
-        if (valid) {
-            int pos = running[d] + rank;
-            for (int w = 0; w < wave; ++w) pos += wave_cnt[w][d];
-            keys_out[pos] = k;
-            vals_out[pos] = v;
+        const int seen = valid ? wcnt[wave][d] : 0;
+        pre[r] = seen + rank;
+        // the digit's lowest lane adds the round's count (one writer per digit; the wave's own
+        // LDS operations stay in order, so the next round reads the new count)
+        if (valid && rank == 0) wcnt[wave][d] = seen + __popcll(peers);
+    }
+    lds_barrier();
+    {
+        // thread d: the waves' bases within digit d, in wave order after the digit's local base
+        // (the thread reads and rewrites column d only)
+        const int d = threadIdx.x;
+        const int c0 = wcnt[0][d], c1 = wcnt[1][d], c2 = wcnt[2][d];
+        wcnt[0][d] = lbase;
+        wcnt[1][d] = lbase + c0;
+        wcnt[2][d] = lbase + c0 + c1;
+        wcnt[3][d] = lbase + c0 + c1 + c2;
+    }
+    lds_barrier();
+#pragma unroll
+    for (int r = 0; r < kSortRounds; ++r) {
+        if (w0 + r * 64 + lane < cnt) {
+            const int pos = wcnt[wave][(kr[r] >> shift) & (radix - 1)] + pre[r];
+            lk[pos] = kr[r];
+            lv[pos] = vr[r];
         }
-        lds_barrier();
-        for (int dd = threadIdx.x; dd < radix; dd += kSortThreads) {
-            running[dd] += wave_cnt[0][dd] + wave_cnt[1][dd] + wave_cnt[2][dd] + wave_cnt[3][dd];
-            wave_cnt[0][dd] = wave_cnt[1][dd] = wave_cnt[2][dd] = wave_cnt[3][dd] = 0;
-        }
-        lds_barrier();
+    }
+    lds_barrier();
+    // LDS position i holds the key of global position gshift[digit] + i
+    for (int i = threadIdx.x; i < cnt; i += kSortThreads) {
+        const int k = lk[i];
+        const int pos = gshift[(k >> shift) & (radix - 1)] + i;
+        keys_out[pos] = k;
+        vals_out[pos] = lv[i];
     }
 }
 
