@@ -113,7 +113,7 @@ hipError_t launch_boxes(const Grid& G, int n, const float* means, const float* c
 }
 
 // ------------------------------------------------------------------------------------------
-// Device-wide scan: per-tile reduce -> scan of tile totals -> per-tile scan with carry-in.
+// Device-wide scan: per-tile reduce -> per-tile scan with carry-in (each tile sums the totals before it).
 // ------------------------------------------------------------------------------------------
 
 // Inclusive scan of one value per thread over the block (256 threads = 4 waves).
@@ -150,27 +150,17 @@ __global__ void __launch_bounds__(kScanThreads) k_scan_reduce(const int* __restr
     if (threadIdx.x == 0) partials[blockIdx.x] = total;
 }
 
-// Exclusive scan of the per-tile totals by one workgroup, looping over chunks with a carry.
-__global__ void __launch_bounds__(kScanThreads) k_scan_partials(long long* __restrict__ partials,
-                                                                int64_t nb,
-                                                                long long* __restrict__ total_dev) {
-    __shared__ long long sh[4];
-    long long carry = 0;
-    for (int64_t base = 0; base < nb; base += kScanThreads) {
-        const int64_t i = base + threadIdx.x;
-        const long long v = i < nb ? partials[i] : 0;
-        long long total;
-        const long long inc = block_incl_scan(v, sh, total);
-        if (i < nb) partials[i] = carry + inc - v;
-        carry += total;
-    }
-    if (threadIdx.x == 0 && total_dev) *total_dev = carry;
-}
-
+// Each block forms its own prefix, the sum of the tile totals before it (a block-wide sum over at most
+// a few thousand values), so that no kernel scans the totals between the reduce and the apply; the
+// last block also writes the grand total.
 __global__ void __launch_bounds__(kScanThreads) k_scan_apply(const int* in, int* out, int64_t n,
                                                              const long long* __restrict__ partials,
-                                                             int inclusive) {
+                                                             int inclusive, long long* __restrict__ total_dev) {
     __shared__ long long sh[4];
+    long long pre = 0;
+    for (int64_t j = threadIdx.x; j < (int64_t)blockIdx.x; j += kScanThreads) pre += partials[j];
+    long long ptot;
+    block_incl_scan(pre, sh, ptot);   // ptot: the sum of the totals before this block
     const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
     int v[kScanItems];
     long long local = 0;
@@ -183,7 +173,7 @@ __global__ void __launch_bounds__(kScanThreads) k_scan_apply(const int* in, int*
     }
     long long total;
     const long long inc = block_incl_scan(local, sh, total);
-    long long run = partials[blockIdx.x] + inc - local;
+    long long run = ptot + inc - local;
 #pragma unroll
     for (int r = 0; r < kScanItems; ++r) {
         const int64_t i = base + r;
@@ -191,9 +181,10 @@ __global__ void __launch_bounds__(kScanThreads) k_scan_apply(const int* in, int*
         if (i < n) out[i] = (int)(inclusive ? nxt : run);
         run = nxt;
     }
+    if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0 && total_dev) *total_dev = ptot + total;
 }
 
-// Single-workgroup scan for inputs up to kScanSingleMax (two tiles: beyond that the three-kernel
+// Single-workgroup scan for inputs up to kScanSingleMax (two tiles: beyond that the two-kernel
 // scan, whose reduce and apply kernels spread over the whole chip, is faster; a tile takes one
 // workgroup about 5 us).  Tiles of 1024 x 32 values: coalesced
 // loads into LDS (row of 32 values per thread, padded to 33 words), a sequential scan of each
@@ -290,9 +281,8 @@ hipError_t scan_i32(const int* in, int* out, int64_t n, bool inclusive, long lon
     const int64_t nb = ceil_div(n > 0 ? n : 1, kScanTile);
     long long* partials = static_cast<long long*>(ws);
     G2V_LAUNCH(k_scan_reduce, dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, n, partials);
-    G2V_LAUNCH(k_scan_partials, dim3(1), dim3(kScanThreads), 0, s, partials, nb, total_dev);
     G2V_LAUNCH(k_scan_apply, dim3((unsigned)nb), dim3(kScanThreads), 0, s, in, out, n,
-                       (const long long*)partials, inclusive ? 1 : 0);
+               (const long long*)partials, inclusive ? 1 : 0, total_dev);
     return hipGetLastError();
 }
 
