@@ -210,10 +210,12 @@ def _forward(means3D, opacity, covariances, voxel_size, voxel_range, features, k
         # one allocation
         pws = lib.g2v_forward_plan_workspace(n)
         pws_al = (pws + 255) & ~255
-        bws = max(1, lib.g2v_backward_plan_workspace(n)) if keep_t2g else 0
+        # (without features the backward needs neither the CSR nor a plan: it walks the boxes)
+        keep_csr = keep_t2g and feats is not None
+        bws = max(1, lib.g2v_backward_plan_workspace(n)) if keep_csr else 0
         wsb = torch.empty(pws_al + bws, dtype=torch.uint8, device=dev)
         ws = wsb[:pws]
-        bplan = wsb[pws_al:] if keep_t2g else None
+        bplan = wsb[pws_al:] if keep_csr else None
         counts = _pinned_counts(dev, 2)
         start, stop = _timing_events(dev)
         start.record(cur)
@@ -236,7 +238,7 @@ def _forward(means3D, opacity, covariances, voxel_size, voxel_range, features, k
                        "gaussian_voxelizer_forward (features)")
         density = torch.empty(X, Y, Z, **f32)
         grid_feats = torch.empty(X, Y, Z, C, dtype=fdtype, device=dev)
-        t2g_toff = torch.empty(Tx * Ty * Tz + 1, **i32) if keep_t2g else None
+        t2g_toff = torch.empty(Tx * Ty * Tz + 1, **i32) if keep_csr else None
         ready.synchronize()
         M, MR = (int(v) for v in counts.tolist())
         for cnt, what in ((M, "Gaussian-tile"), (MR, "region-Gaussian")):
@@ -248,7 +250,8 @@ def _forward(means3D, opacity, covariances, voxel_size, voxel_range, features, k
         t2g = None
         csr = (None, None, None)
         if keep_t2g:
-            csr = (torch.empty(M, **i32), torch.empty(M, **i32), t2g_toff)
+            if keep_csr:
+                csr = (torch.empty(M, **i32), torch.empty(M, **i32), t2g_toff)
             t2g = dict(csr=csr, plan=bplan, num_region_pairs=MR, vs=vs, vr=vr, dims=(X, Y, Z))
         _lib.check(lib.g2v_forward_splat(n, C, _ptr(means), _ptr(op), _ptr(feats), fdt, _ptr(packed),
                                          0 if packed is None else packed.numel(), vs, vr,
@@ -263,7 +266,7 @@ def _forward(means3D, opacity, covariances, voxel_size, voxel_range, features, k
             t2g["grads"] = (torch.empty(n, 3, **f32), torch.empty(n, 9, **f32), torch.empty(n, **f32),
                             torch.empty(n, C, dtype=fdtype, device=dev))
             t2g["ws"] = torch.empty(max(1, lib.g2v_backward_workspace(n, C, M, t2g["num_region_pairs"], vs, vr)),
-                                    dtype=torch.uint8, device=dev)
+                                    dtype=torch.uint8, device=dev) if C > 0 else None
             # the backward's gradient-independent kernels, queued behind the forward (after its
             # stop event): they run while this thread waits and hands over to the backward
             if C > 0:
@@ -392,7 +395,9 @@ def _backward(grad_output, grad_feats_output, means3D, opacity, cov_inv, voxel_s
         if timed:
             start, stop = _timing_events(dev)
             start.record(cur)
-        if t2g is not None and C > 0:   # planned by the forward
+        if C == 0:   # the density-only backward walks the boxes: no plan, no workspace
+            plan_ws, MR = None, 0
+        elif t2g is not None:   # planned by the forward
             plan_ws, MR = t2g["plan"], t2g["num_region_pairs"]
         else:
             plan_ws = torch.empty(max(1, lib.g2v_backward_plan_workspace(n)), dtype=torch.uint8, device=dev)
@@ -401,7 +406,9 @@ def _backward(grad_output, grad_feats_output, means3D, opacity, cov_inv, voxel_s
                                              _ptr(plan_ws), plan_ws.numel(), ctypes.byref(MR), stream),
                        "gaussian_voxelizer_backward (plan)")
             MR = int(MR.value)
-        if trusted and C > 0:
+        if C == 0:
+            ws = None
+        elif trusted:
             ws = t2g["ws"]
         else:
             ws = torch.empty(max(1, lib.g2v_backward_workspace(n, C, M, MR, vs, vr)), dtype=torch.uint8, device=dev)
@@ -428,7 +435,7 @@ def _backward(grad_output, grad_feats_output, means3D, opacity, cov_inv, voxel_s
                              M, MR, _ptr(density), _ptr(grid_feats), _ptr(feats), fdt,
                              _ptr(grad_means), _ptr(grad_cov), _ptr(grad_opacity),
                              _ptr(grad_feats), _ptr(csr[0]), _ptr(csr[1]), _ptr(csr[2]),
-                             _ptr(plan_ws), _ptr(ws), ws.numel(), stream),
+                             _ptr(plan_ws), _ptr(ws), 0 if ws is None else ws.numel(), stream),
                        "gaussian_voxelizer_backward")
         bwd_sec = 0.0
         if timed:

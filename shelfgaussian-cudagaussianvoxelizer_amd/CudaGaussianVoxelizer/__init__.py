@@ -39,10 +39,11 @@ class _CudaGaussianVoxelizeFunction(torch.autograd.Function):
     def forward(ctx, means3D, opacity, covariances, voxel_size, voxel_range, features, need_backward=None):
         # with features the backward reuses the forward's Tile->Gaussian CSR (kept beside the
         # reference's saved tensors) instead of re-sorting the G->T pairs, and its workspace is
-        # prepared behind the forward; both only when a backward can follow (need_backward, or
-        # when not given, whether an input requires grad), so that an inference forward
-        # allocates and launches nothing for a backward that never runs
-        keep = features is not None and features.shape[-1] > 0 and _wants_backward(ctx, need_backward)
+        # prepared behind the forward; without features only the grid values and the gradient
+        # buffers are kept; all of it only when a backward can follow (need_backward, or when not
+        # given, whether an input requires grad), so that an inference forward allocates and
+        # launches nothing for a backward that never runs
+        keep = _wants_backward(ctx, need_backward)
         (density, cov_inv, valid_voxel_lb, valid_voxel_ub, num_valid_voxel, grid_feats, g2t_offsets,
          g2t_tile_ids, fwd_sec), t2g = _C._forward(means3D, opacity, covariances, voxel_size,
                                                    voxel_range, features, keep_t2g=keep)

@@ -197,15 +197,14 @@ int plan_launch(const Grid& G, int n, const float* means3D, const float* covaria
     int cell[3] = {1, 1, 1};
     void* plan_scan_ws = nullptr;
     int* cell_off = bwd_plan_workspace ? backward_plan_cells(G, bwd_plan_workspace, n, cell, &plan_scan_ws) : nullptr;
+    // the box kernel clears the counts that no scan writes: both without Gaussians, MR without the
+    // backward plan
+    long long* zero = n > 0 ? (cell_off ? nullptr : counts + 1) : counts;
     G2V_HIP(launch_boxes(G, n, means3D, covariances, cov_inv, lb, ub, nvox, g2t_offsets, cell_off ? cell : nullptr,
-                         cell_off, s));
-    if (n > 0) {
+                         cell_off, s, zero, n > 0 ? 1 : 2));
+    if (n > 0)
         G2V_HIP(scan_i32_pair(g2t_offsets + 1, g2t_offsets + 1, n, counts, scan_ws, cell_off ? cell_off + 1 : nullptr,
                               cell_off ? cell_off + 1 : nullptr, cell_off ? n : 0, counts + 1, plan_scan_ws, s));
-        if (!cell_off) G2V_HIP(launch_fill_i32(2, 0, reinterpret_cast<int*>(counts + 1), s));
-    } else {
-        G2V_HIP(launch_fill_i32(4, 0, reinterpret_cast<int*>(counts), s));
-    }
     return G2V_OK;
 }
 

@@ -27,19 +27,22 @@ __device__ __forceinline__ int cvt_sat(float f) {
 }
 
 // With cell_offsets, also the number of cells of cx x cy x cz voxels that the box meets, at
-// cell_offsets[g+1] (cell_offsets[0] = 0), as k_cell_count computes it from the box.
+// cell_offsets[g+1] (cell_offsets[0] = 0), as k_cell_count computes it from the box.  zero[0 ..
+// nzero) is cleared (counts that no scan of this launch sequence writes).
 __global__ void __launch_bounds__(256) k_boxes(Grid G, int n, const float* __restrict__ means,
                                                const float* __restrict__ cov,
                                                float* __restrict__ cov_inv, int* __restrict__ lb,
                                                int* __restrict__ ub, int* __restrict__ nvox,
                                                int* __restrict__ g2t_offsets, int cx, int cy, int cz,
-                                               int* __restrict__ cell_offsets) {
+                                               int* __restrict__ cell_offsets, long long* __restrict__ zero,
+                                               int nzero) {
 #pragma clang fp contract(off)
     const int g = blockIdx.x * 256 + threadIdx.x;
     if (g == 0) {
         g2t_offsets[0] = 0;
         if (cell_offsets) cell_offsets[0] = 0;
     }
+    if (g < nzero) zero[g] = 0;
     if (g >= n) return;
     int lo[3], hi[3];
     bool empty = false;
@@ -104,11 +107,11 @@ __global__ void __launch_bounds__(256) k_boxes(Grid G, int n, const float* __res
 
 hipError_t launch_boxes(const Grid& G, int n, const float* means, const float* cov, float* cov_inv,
                         int* lb, int* ub, int* nvox, int* g2t_offsets, const int* cell, int* cell_offsets,
-                        hipStream_t s) {
+                        hipStream_t s, long long* zero, int nzero) {
     const int blocks = (int)ceil_div(n > 0 ? n : 1, 256);
     const int cx = cell ? cell[0] : 1, cy = cell ? cell[1] : 1, cz = cell ? cell[2] : 1;
     G2V_LAUNCH(k_boxes, dim3(blocks), dim3(256), 0, s, G, n, means, cov, cov_inv, lb, ub,
-                       nvox, g2t_offsets, cx, cy, cz, cell ? cell_offsets : nullptr);
+                       nvox, g2t_offsets, cx, cy, cz, cell ? cell_offsets : nullptr, zero, zero ? nzero : 0);
     return hipGetLastError();
 }
 

@@ -50,7 +50,7 @@ hipError_t scan_i32_pair(const int* in_a, int* out_a, int64_t n_a, long long* to
 // the boxes into cell_offsets[1..n] (cell_offsets[0] = 0), as launch_cell_count writes them.
 hipError_t launch_boxes(const Grid& G, int n, const float* means, const float* cov, float* cov_inv,
                         int* lb, int* ub, int* nvox, int* g2t_offsets, const int* cell, int* cell_offsets,
-                        hipStream_t s);
+                        hipStream_t s, long long* zero = nullptr, int nzero = 0);
 // keys (optional): the batch's tile ids (sort keys) beside the scene-local tile_ids.
 hipError_t launch_fill_g2t(const Grid& G, int n, const int* lb, const int* ub,
                            const int* g2t_offsets, int* tile_ids, int* gauss_ids, hipStream_t s,
