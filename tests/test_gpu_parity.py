@@ -104,6 +104,12 @@ CSR_CASES = {
     "small_n70000": W.Workload("small_n70000", 70_000, None, var_range=(0.1, 0.6)),
     # the reference's recorded training batch (tests/golden/mmdet_debug_inputs.npz)
     "recorded_batch": W.mmdet_workload(),
+    # 50 x 50 x 16 = 40,000 tiles: the sort takes two passes of 8-bit digits (all 256 digit lanes)
+    "tiles_40000": W.Workload("tiles_40000", 6000, None, voxel_range=(-40.0, -40.0, -1.0, 40.0, 40.0, 24.6),
+                              var_range=(0.1, 0.6)),
+    # 100 x 100 x 8 = 80,000 tiles: three passes of 6-bit digits, more than 65,536 tile offsets
+    "tiles_80000": W.Workload("tiles_80000", 6000, None, voxel_range=(-80.0, -80.0, -1.0, 80.0, 80.0, 11.8),
+                              var_range=(0.3, 1.5)),
 }
 
 
