@@ -299,6 +299,7 @@ struct BtSmem {
     float gD[64], inv[64], tv[64], D[64];
     float kc[2][FU ? 64 : 1];  // FU: the voxel's k1, k2 (scaled by the loss's upstream gradient)
     ParamTile<kBtPass> pt;     // parameters of this pass's list entries
+    int pidx[kBtPass];         // G->T pair of each entry with this tile (-1: none)
     float tpart[kBtGroups][64];
 };
 static_assert(sizeof(float) * 2 * kBtNbw * 16 * 64 * kBtGroups <= BtSmem<true>::kFStages * kBtPass * kBtRowBytes,
@@ -580,21 +581,23 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
         // LDS-only barriers here and in the epilogues: the weight and partial stores (read by later
         // kernels only) stay in flight while the next steps run
         lds_barrier();
-        stage_params(sm.pt, sorted_gauss + j0 + pbase, pcount, means, cov_inv, opacity, lb, ub);
-        lds_barrier();
 
         // F rows by direct-to-LDS loads: row group rg = wave + kBtWaves*i (8 rows, 1 KB) is
         // loaded by this wave; lane = (row rg*8 + lane/8, slot lane%8) and slot p carries the
         // 16-byte piece p ^ swz(row) of the row's chunk.  Rows past the list read the zero row;
         // groups wholly past it are not loaded (no wave reads them).  A wave issues exactly
         // nld = (its groups within the list) + kNG loads per chunk, so the wait counts below are
-        // exact.
+        // exact.  The rows' Gaussians come straight from the list, so that the first chunks' loads
+        // are issued before the parameters are staged and both are in flight together.
+        const int* list = sorted_gauss + j0 + pbase;
+        const int kent = threadIdx.x;                        // this thread's list entry (staging)
+        const int gk = kent < pcount ? list[kent] : -1;
         uint32_t doff[kBtDma];
 #pragma unroll
         for (int i = 0; i < kBtDma; ++i) {
             const int rg = wave + kBtWaves * i;
             const int r = rg * 8 + (lane >> 3);
-            const int g = r < pcount ? sm.pt.gid[r] : n;
+            const int g = r < pcount ? list[r] : n;
             const int piece = (lane & 7) ^ swz(r);
             doff[i] = (rg * 8 < pcount) ? (uint32_t)g * fstride + (uint32_t)piece * 16u : (uint32_t)n * fstride;
         }
@@ -612,6 +615,55 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
                        uniform(lds_addr(&sm.u.frow[buf][rg * 8 * kBtRowBytes])));
             }
         };
+        const int clast = nchk - 1;
+        // Odd passes walk the chunks backwards: a long list's next pass then starts on the G chunks
+        // the previous pass read last, which are still in L2 (forward order re-read the tile's G
+        // from HBM at every pass).  Chunk nchk (past the end) stays past the end.
+        const bool rev = ((pbase / kBtPass) & 1) != 0;
+        auto cm = [&](int c) { return (rev && c <= clast) ? clast - c : c; };
+
+        // this thread's entry: parameters and its G->T pair with this tile, requested first
+        float emu[3] = {0.f, 0.f, 0.f}, eA[9] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, eo = 0.f;
+        int elb[3] = {0, 0, 0}, eub[3] = {0, 0, 0}, eoff = 0;
+        if (gk >= 0) {
+#pragma unroll
+            for (int q = 0; q < 3; ++q) {
+                emu[q] = means[gk * 3 + q];
+                elb[q] = lb[gk * 3 + q];
+                eub[q] = ub[gk * 3 + q];
+            }
+#pragma unroll
+            for (int q = 0; q < 9; ++q) eA[q] = cov_inv[gk * 9 + q];
+            eo = opacity[gk];
+            eoff = g2t_offsets[gk];
+        }
+        // the first chunks' loads (G three chunks ahead, F two, or one with FU), in flight with them
+        dma_g(cm(0), 0);
+        dma_f(cm(0), 0, 0, nf);
+        dma_g(cm(min(1, clast)), 1);
+        if constexpr (!FU) dma_f(cm(min(1, clast)), 1, 0, nf);
+        dma_g(cm(min(2, clast)), 2);
+        if (kent < kBtPass) {
+            sm.pt.gid[kent] = gk;
+            int pair = -1;
+            if (gk >= 0) {
+#pragma unroll
+                for (int q = 0; q < 3; ++q) {
+                    sm.pt.mu[q][kent] = emu[q];
+                    sm.pt.lb[q][kent] = elb[q];
+                    sm.pt.ub[q][kent] = eub[q];
+                }
+#pragma unroll
+                for (int q = 0; q < 9; ++q) sm.pt.A[q][kent] = eA[q];
+                sm.pt.o[kent] = eo;
+                const int tx0 = elb[0] / kTile, ty0 = elb[1] / kTile, tz0 = elb[2] / kTile;
+                const int dy = eub[1] / kTile - ty0 + 1, dz = eub[2] / kTile - tz0 + 1;
+                const int64_t pr = (int64_t)eoff + ((tx - tx0) * dy + (ty - ty0)) * dz + (tz - tz0);
+                pair = (pr >= 0 && pr < M) ? (int)pr : -1;   // malformed CSR: never write outside the buffer
+            }
+            sm.pidx[kent] = pair;
+        }
+        lds_barrier();
 
         // wave (ks, ngrp) accumulates k half ks of every chunk for both voxel blocks m and its N
         // blocks ngrp + 4j; the halves are added after the K loop
@@ -750,20 +802,10 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
         // A operand was written in the previous step.
         // The chunk loop, instantiated for the wave's group count NF (exact wait immediates;
         // waves of one workgroup may run different instantiations, with the same barriers).
-        const int clast = nchk - 1;
-        // Odd passes walk the chunks backwards: a long list's next pass then starts on the G chunks
-        // the previous pass read last, which are still in L2 (forward order re-read the tile's G
-        // from HBM at every pass).  Chunk nchk (past the end) stays past the end.
-        const bool rev = ((pbase / kBtPass) & 1) != 0;
-        auto cm = [&](int c) { return (rev && c <= clast) ? clast - c : c; };
         auto chunk_loop = [&](auto nfc) {
             constexpr int NF = decltype(nfc)::value;
             constexpr int kLd = NF + kNG;   // loads per wave per chunk
-            dma_g(cm(0), 0);
-            dma_f(cm(0), 0, 0, NF);
-            dma_g(cm(min(1, clast)), 1);
-            dma_f(cm(min(1, clast)), 1, 0, NF);
-            dma_g(cm(min(2, clast)), 2);
+            // G(0), F(0), G(1), F(1), G(2) were issued at the pass start
             wait_vm<kLd>();               // G(0), F(0), G(1) complete
             lds_barrier();
             write_a(cm(0), 0, 0);
@@ -791,10 +833,7 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
         auto chunk_loop_fu = [&](auto nfc) {
             constexpr int NF = decltype(nfc)::value;
             constexpr int kLg = kSrc * kNG;   // G loads per wave per chunk
-            dma_g(cm(0), 0);
-            dma_f(cm(0), 0, 0, NF);
-            dma_g(cm(min(1, clast)), 1);
-            dma_g(cm(min(2, clast)), 2);
+            // G(0), F(0), G(1), G(2) were issued at the pass start
             wait_vm<kLg>();               // G(0), F(0), G(1) complete
             lds_barrier();
             write_a(cm(0), 0, 0);
@@ -1005,12 +1044,9 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
         }
         lds_barrier();
         for (int slot = threadIdx.x; slot < pcount; slot += kBtThreads) {
-            const int g = sm.pt.gid[slot];
-            const int tx0 = sm.pt.lb[0][slot] / kTile, ty0 = sm.pt.lb[1][slot] / kTile, tz0 = sm.pt.lb[2][slot] / kTile;
-            const int dy = sm.pt.ub[1][slot] / kTile - ty0 + 1, dz = sm.pt.ub[2][slot] / kTile - tz0 + 1;
-            const int64_t pair = (int64_t)g2t_offsets[g] + ((tx - tx0) * dy + (ty - ty0)) * dz + (tz - tz0);
-            if (pair < 0 || pair >= M) continue;   // malformed CSR: never write outside the buffer
-            float* out = pair_partials + pair * kNumGrads;
+            const int pair = sm.pidx[slot];
+            if (pair < 0) continue;
+            float* out = pair_partials + (int64_t)pair * kNumGrads;
 #pragma unroll
             for (int k = 0; k < kNumGrads; ++k) out[k] = sm.u.xch[0][slot][k] + sm.u.xch[1][slot][k];
         }
