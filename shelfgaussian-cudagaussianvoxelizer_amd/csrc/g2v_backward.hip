@@ -290,6 +290,12 @@ struct BtSmem {
         // 16-byte bank groups
         unsigned char frow[kFStages][kBtPass * kBtRowBytes];
         float xch[2][kBtPass][kNumGrads];   // epilogue exchange, used after the K loop has drained
+        struct {
+            float xch_room[2][kBtPass][kNumGrads];
+            // the exponentials of epilogue 1, read again by epilogue 2: [wave][N block][q4][lane]
+            // (FU: no room beside the two F buffers; epilogue 2 evaluates them again)
+            float4 e[FU ? 1 : kBtWaves][kBtNbw][4][64];
+        } ep;
     } u;
     // G chunks as loaded (fp32, voxel-major, pieces at q ^ swz(v)); FU: [0] target, [1] grid_feats
     float graw[kBtStages][kSrc][64][kBtKc];
@@ -304,6 +310,8 @@ struct BtSmem {
 };
 static_assert(sizeof(float) * 2 * kBtNbw * 16 * 64 * kBtGroups <= BtSmem<true>::kFStages * kBtPass * kBtRowBytes,
               "the k-half exchange fits in the F buffers");
+static_assert(sizeof(BtSmem<false>::u) == sizeof(BtSmem<false>::u.frow) && sizeof(BtSmem<true>::u) == sizeof(BtSmem<true>::u.frow),
+              "the epilogue's exponentials fit in the F buffers");
 
 
 // s_waitcnt immediate that waits for vmcnt <= n and leaves the other counters alone.
@@ -663,6 +671,11 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
             }
             sm.pidx[kent] = pair;
         }
+        // Every load of the pass start complete (the first chunks' too: the parameter stores above
+        // already waited for most of them).  A thread that staged no entry would otherwise reach the
+        // K loop with the parameter loads still pending for the compiler's wait counts, which
+        // then wait for all loads inside the K loop wherever their registers are reused there.
+        wait_vm<0>();
         lds_barrier();
 
         // wave (ks, ngrp) accumulates k half ks of every chunk for both voxel blocks m and its N
@@ -907,9 +920,10 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
         // ---- epilogue 1: split weights w / max(D, eps) of every pair; t_v from U (single pass).
         // Lane = Gaussian column lane%32 of N block j; element i is the tile's voxel row
         // r = 32 mb + 8 (i/4) + 4 (lane/32) + i%4.  Branch-free: an element outside the grid, the
-        // Gaussian's box or the list gets e = 0 (and so w = 0).  The validity bits are kept for
-        // epilogue 2, which evaluates e again (cheaper than keeping 32 values per lane live across
-        // the t_v exchange).
+        // Gaussian's box or the list gets e = 0 (and so w = 0).  The validity bits are kept in
+        // registers and the exponentials in LDS (the F buffers are free after the K loop), where
+        // epilogue 2 reads them back instead of evaluating them again (FU: the two F buffers leave no
+        // room, and epilogue 2 evaluates them again).
         unsigned rowok = 0;   // bit i: row r of element i lies in the grid
 #pragma unroll
         for (int i = 0; i < 16; ++i)
@@ -934,6 +948,7 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
 #pragma unroll
             for (int q4 = 0; q4 < 4; ++q4) {
                 __bf16 hs[4], ls[4];
+                float ev[4];
                 const int a = q4 >> 1, b = q4 & 1;
 #pragma unroll
                 for (int ii = 0; ii < 4; ++ii) {
@@ -943,6 +958,7 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
                     const int r = mb * 32 + 8 * q4 + 4 * h + ii;
                     const bool ok = gok & (((rowok >> i) & (L.inx >> a) & (L.iny >> b) & (L.inz >> ii) & 1u) != 0u);
                     const float e = ok ? lane_e(E, L, a, b, ii) : 0.0f;
+                    ev[ii] = e;
                     okm[j] |= ok ? (1u << i) : 0u;
                     const float w = p.o * e;
                     const float wtil = w * sm.inv[r];
@@ -951,6 +967,7 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
                     // the unloaded F rows left in LDS
                     rowt[i] += (w > 0.0f) ? wtil * acc[j][i] : 0.0f;
                 }
+                if constexpr (!FU) sm.u.ep.e[wave][j][q4][lane] = make_float4(ev[0], ev[1], ev[2], ev[3]);
                 if (gok) {
                     const int r0 = mb * 32 + 8 * q4 + 4 * h;
                     typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
@@ -993,20 +1010,30 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
                 read_params(sm.pt, slot, p);
                 LaneGeom L;
                 lane_geom(G, p, tx * kTile + 2 * mb, ty * kTile + h, tz * kTile, L);
-                LaneExp E;   // e is evaluated again rather than kept across the t_v exchange
-                lane_exp(p, L, E);
+                // e from epilogue 1 (FU: evaluated again; no LDS is free to keep it)
+                LaneExp E;
+                if constexpr (FU) lane_exp(p, L, E);
                 float m0 = 0.f, mx = 0.f, my = 0.f, mz = 0.f, mxx = 0.f, myy = 0.f, mzz = 0.f, mxy = 0.f,
                       mxz = 0.f, myz = 0.f;
 #pragma unroll
                 for (int q4 = 0; q4 < 4; ++q4) {
                     const int a = q4 >> 1, b = q4 & 1;
+                    float ev[4] = {0.f, 0.f, 0.f, 0.f};
+                    if constexpr (!FU) {
+                        const float4 e4 = sm.u.ep.e[wave][j][q4][lane];
+                        ev[0] = e4.x;
+                        ev[1] = e4.y;
+                        ev[2] = e4.z;
+                        ev[3] = e4.w;
+                    }
                     float s0 = 0.f, sz = 0.f, szz = 0.f;
 #pragma unroll
                     for (int ii = 0; ii < 4; ++ii) {
                         const int i = q4 * 4 + ii;
                         const int r = mb * 32 + 8 * q4 + 4 * h + ii;
                         const float gw = sm.gD[r] + (acc[j][i] - sm.tv[r]) * sm.inv[r];
-                        const float rr = ((okm[j] >> i) & 1u) ? gw * lane_e(E, L, a, b, ii) : 0.0f;
+                        const float e = FU ? lane_e(E, L, a, b, ii) : ev[ii];
+                        const float rr = ((okm[j] >> i) & 1u) ? gw * e : 0.0f;
                         s0 += rr;
                         const float rz = rr * L.dz[ii];
                         sz += rz;
