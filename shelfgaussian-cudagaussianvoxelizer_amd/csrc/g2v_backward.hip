@@ -1687,37 +1687,49 @@ __device__ __forceinline__ void br_tiles(BrSmem<FU>& sm, const Grid& G, int C, i
     }
 }
 
+// A pass's row table (this thread's entries) and G->R slots, as loaded (rows past the pass read the
+// region's last row).
+constexpr int kBrPer = kBrPass * kBrSlots / kBrThreads;
+struct BrRows {
+    int tv[kBrPer];
+    int rs[2];
+};
+
+__device__ __forceinline__ void br_load_rows(BrRows& L, int rp, int KR, int M, int MR, int jr0,
+                                             const int* __restrict__ r_pairs, const int* __restrict__ table) {
+#pragma unroll
+    for (int e0 = 0; e0 < kBrPer; ++e0) {
+        const int e = threadIdx.x + e0 * kBrThreads;
+        const int r = min(rp + e / kBrSlots, KR - 1);
+        // clamped: a row table or slot list from a workspace that was not prepared for these
+        // Gaussians cannot send a load or a store outside the weights or the partial rows
+        L.tv[e0] = min(max(table[(int64_t)(jr0 + r) * kBrSlots + e % kBrSlots], 0), M);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int r = threadIdx.x + h * kBrThreads;
+        L.rs[h] = r < kBrPass ? min(max(r_pairs[jr0 + min(rp + r, KR - 1)], 0), MR - 1) : 0;
+    }
+}
+
 // One pass of phase B over rows rp .. rp + prow - 1 of the region (prow <= 384): stages the
-// pass's row table and G->R slots, then runs the tile loop with this wave's block count.
+// pass's row table and G->R slots (L, from br_load_rows; the first pass's are requested together with
+// the region's tile list), then runs the tile loop with this wave's block count.
 template <bool GB, bool P2, bool FU>
 __device__ __forceinline__ void br_pass(BrSmem<FU>& sm, const Grid& G, int C, int c0, int ntl, int rp,
                                         int KR, int M, int MR, int jr0, const void* __restrict__ gF,
                                         const void* __restrict__ gF2, const int* __restrict__ r_pairs,
                                         const int* __restrict__ table, const __bf16* __restrict__ wt,
-                                        float* __restrict__ gpart, bool interior) {
+                                        float* __restrict__ gpart, bool interior, const BrRows& L) {
     const int wave = threadIdx.x >> 6;
     const int prow = min(KR - rp, kBrPass);
     const int nblk = (prow + 15) >> 4;
     const int nb = uniform((nblk - wave + kBrWaves - 1) / kBrWaves);   // row blocks of this wave
     __syncthreads();   // the previous pass is done with both buffers and the row tables
     {
-        // all loads first, then the LDS stores (rows past the pass read the region's last row)
-        constexpr int kPer = kBrPass * kBrSlots / kBrThreads;
-        int tv[kPer];
-#pragma unroll
-        for (int e0 = 0; e0 < kPer; ++e0) {
-            const int e = threadIdx.x + e0 * kBrThreads;
-            const int r = min(rp + e / kBrSlots, KR - 1);
-            // clamped: a row table or slot list from a workspace that was not prepared for these
-            // Gaussians cannot send a load or a store outside the weights or the partial rows
-            tv[e0] = min(max(table[(int64_t)(jr0 + r) * kBrSlots + e % kBrSlots], 0), M);
-        }
-        int rs[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int r = threadIdx.x + h * kBrThreads;
-            rs[h] = r < kBrPass ? min(max(r_pairs[jr0 + min(rp + r, KR - 1)], 0), MR - 1) : 0;
-        }
+        constexpr int kPer = kBrPer;
+        const int (&tv)[kPer] = L.tv;
+        const int (&rs)[2] = L.rs;
 #pragma unroll
         for (int e0 = 0; e0 < kPer; ++e0) {
             const int e = threadIdx.x + e0 * kBrThreads;
@@ -1761,6 +1773,9 @@ __global__ void __launch_bounds__(kBrThreads, 1) k_bwd_region(
     const int jr0 = uniform(min(max(roff[Rb], 0), MR));
     const int KR = uniform(min(max(roff[Rb + 1], jr0), MR)) - jr0;
     if (KR <= 0) return;
+    // the first pass's row table, requested together with the region's tile list below
+    BrRows rows;
+    br_load_rows(rows, 0, KR, M, MR, jr0, r_pairs, table);
     const int scene = uniform(Rb / RG.total), R = Rb - scene * RG.total;   // R: the scene's region
     const int tbase = scene * scene_tiles(G);                               // its first tile in the batch
     if (scene > 0) {   // the scene's voxel rows
@@ -1836,9 +1851,14 @@ __global__ void __launch_bounds__(kBrThreads, 1) k_bwd_region(
         interior = uniform((rx + 1) * RG.cell[0] <= G.dims[0] && (ry + 1) * RG.cell[1] <= G.dims[1] &&
                            (rz + 1) * RG.cell[2] <= G.dims[2] && c0 + kBrCc <= C) != 0;
     }
-    for (int rp = 0; rp < KR; rp += kBrPass)
+    br_pass<GB, P2, FU>(sm, G, C, c0, ntl, 0, KR, M, MR, jr0, gF, grid_feats, r_pairs, table, wt, gpart,
+                        interior, rows);
+    for (int rp = kBrPass; rp < KR; rp += kBrPass) {
+        BrRows more;
+        br_load_rows(more, rp, KR, M, MR, jr0, r_pairs, table);
         br_pass<GB, P2, FU>(sm, G, C, c0, ntl, rp, KR, M, MR, jr0, gF, grid_feats, r_pairs, table, wt, gpart,
-                            interior);
+                            interior, more);
+    }
 }
 
 // ------------------------------------------------------------------------------------------
