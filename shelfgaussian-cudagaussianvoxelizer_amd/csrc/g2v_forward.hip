@@ -271,12 +271,18 @@ __global__ void __launch_bounds__(kDenWaves * 64) k_fwd_density(Grid G, const fl
                                  : fwd_record_empty(), cz);
     };
     float dacc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // The list entries run one batch ahead of the records: a batch's record loads then wait for one
+    // load latency (its entries arrived during the previous batch), not two.
     DenRec nxt = fetch(j0 + lane);
+    int gnext = j0 + 64 + lane < j1 ? sorted_gauss[j0 + 64 + lane] : -1;
     for (int jb = j0; jb < j1; jb += 64) {
         wave_lds_sync();   // the previous records are read
         sl[lane] = nxt;
         wave_lds_sync();
-        nxt = fetch(jb + 64 + lane);
+        const int gcur = gnext;
+        gnext = jb + 128 + lane < j1 ? sorted_gauss[jb + 128 + lane] : -1;
+        nxt = den_record(gcur >= 0 ? fwd_record(gcur, means, opacity, cov_inv, lb, ub, x0, y0, z0) : fwd_record_empty(),
+                         cz);
         // slots past the list hold empty records (weight 0), so every lane group runs the same count
         const int n4 = uniform((min(64, j1 - jb) + 3) >> 2);
         for (int k4 = 0; k4 < n4; ++k4) {
