@@ -189,15 +189,15 @@ __device__ __forceinline__ void fwd_column_weights(const FwdRec* rec, int col, f
 }
 
 // ------------------------------------------------------------------------------------------
-// Density only: one wave per tile.  The wave walks its tile's list in ascending order, 64 entries
-// at a time: lane k turns entry k into its tile-relative record (the records of the next 64
-// entries are gathered while the current ones are evaluated) and writes it into the wave's LDS
-// slab.  Lane (col = lane % 16, ph = lane / 16) then takes the voxel column col and the entries
+// Density only: two waves per tile, each walking every other batch of 64 entries of the tile's
+// list in ascending order: lane k turns entry k into its tile-relative record (the records of the
+// wave's next batch are gathered while the current ones are evaluated) and writes it into the
+// wave's LDS slab.  Lane (col = lane % 16, ph = lane / 16) then takes the voxel column col and the entries
 // ph, ph + 4, ... of the slab, forming each entry's four weights of the column with the
 // operations of fwd_column_weights (so the weights of the feature splat); the z terms dz_c and
 // fz_c, the same for every column, are formed once per entry by the lane that builds its record.
-// The four lane groups' sums are added at the end.  The sum is the reference's (.cu:7-136) in
-// another order.
+// The four lane groups' sums are added at the end, then the two waves' sums (first wave + second).
+// The sum is the reference's (.cu:7-136) in another order.
 // ------------------------------------------------------------------------------------------
 constexpr int kDenWaves = 4;
 
@@ -250,22 +250,26 @@ __global__ void __launch_bounds__(kDenWaves * 64) k_fwd_density(Grid G, const fl
                                                                const int* __restrict__ sorted_gauss,
                                                                int M, float* __restrict__ density) {
     __shared__ DenRec slab[kDenWaves][64];
+    __shared__ float half1[kDenWaves / 2][4][16];   // the second wave's column sums of each tile
     const int T = scene_tiles(G);
-    // tb: the batch's tile (its list), tile: the scene's
-    const int tb = uniform(xcd_remap(blockIdx.x, gridDim.x) * kDenWaves + (threadIdx.x >> 6));
-    if (tb >= T * G.scenes) return;   // whole waves; the kernel has no workgroup barrier
-    const int scene = uniform(tb / T), tile = tb - scene * T;
+    // Two waves per tile: wave half h takes the list's 64-entry batches h, h + 2, ... (twice the
+    // waves in flight for a kernel that mostly waits on its record loads); the tile's density is
+    // (half 0) + (half 1), added in that order.  tb: the batch's tile (its list), tile: the scene's.
+    const int wv = threadIdx.x >> 6, half = wv & 1;
+    const int tb = uniform(xcd_remap(blockIdx.x, gridDim.x) * (kDenWaves / 2) + (wv >> 1));
+    const bool live = tb < T * G.scenes;   // uniform per wave; every wave meets the barrier below
+    const int scene = uniform(live ? tb / T : 0), tile = live ? tb - scene * T : 0;
     density += scene * scene_voxels(G);
     const int lane = threadIdx.x & 63, col = lane & 15, ph = lane >> 4;
-    DenRec* sl = slab[threadIdx.x >> 6];
+    DenRec* sl = slab[wv];
     int x0, y0, z0;
     tile_voxel(G, tile, 0, x0, y0, z0);
     const float cxl = centre(G, 0, x0 + (col >> 2)), cyl = centre(G, 1, y0 + (col & 3));
     float cz[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) cz[c] = centre(G, 2, z0 + c);
-    const int j0 = uniform(min(max(toff[tb], 0), M));
-    const int j1 = uniform(min(max(toff[tb + 1], j0), M));
+    const int j0 = live ? uniform(min(max(toff[tb], 0), M)) : 0;
+    const int j1 = live ? uniform(min(max(toff[tb + 1], j0), M)) : 0;
     auto fetch = [&](int j) {
         return den_record(j < j1 ? fwd_record(sorted_gauss[j], means, opacity, cov_inv, lb, ub, x0, y0, z0)
                                  : fwd_record_empty(), cz);
@@ -273,14 +277,15 @@ __global__ void __launch_bounds__(kDenWaves * 64) k_fwd_density(Grid G, const fl
     float dacc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     // The list entries run one batch ahead of the records: a batch's record loads then wait for one
     // load latency (its entries arrived during the previous batch), not two.
-    DenRec nxt = fetch(j0 + lane);
-    int gnext = j0 + 64 + lane < j1 ? sorted_gauss[j0 + 64 + lane] : -1;
-    for (int jb = j0; jb < j1; jb += 64) {
+    const int jh = j0 + 64 * half;   // this wave's first batch
+    DenRec nxt = fetch(jh + lane);
+    int gnext = jh + 128 + lane < j1 ? sorted_gauss[jh + 128 + lane] : -1;
+    for (int jb = jh; jb < j1; jb += 128) {
         wave_lds_sync();   // the previous records are read
         sl[lane] = nxt;
         wave_lds_sync();
         const int gcur = gnext;
-        gnext = jb + 128 + lane < j1 ? sorted_gauss[jb + 128 + lane] : -1;
+        gnext = jb + 256 + lane < j1 ? sorted_gauss[jb + 256 + lane] : -1;
         nxt = den_record(gcur >= 0 ? fwd_record(gcur, means, opacity, cov_inv, lb, ub, x0, y0, z0) : fwd_record_empty(),
                          cz);
         // slots past the list hold empty records (weight 0), so every lane group runs the same count
@@ -309,13 +314,18 @@ __global__ void __launch_bounds__(kDenWaves * 64) k_fwd_density(Grid G, const fl
         dacc[c] += xor_shfl<16>(dacc[c]);
         dacc[c] += __shfl_xor(dacc[c], 32, 64);
     }
+    if (half == 1 && ph == 0) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) half1[wv >> 1][c][col] = dacc[c];
+    }
+    lds_barrier();
     const int x = x0 + (col >> 2), y = y0 + (col & 3);
-    if (ph == 0 && x < G.dims[0] && y < G.dims[1]) {
+    if (live && half == 0 && ph == 0 && x < G.dims[0] && y < G.dims[1]) {
         float* out = density + voxel_index(G, x, y, z0);
         const int nz = min(kTile, G.dims[2] - z0);
 #pragma unroll
         for (int c = 0; c < 4; ++c)
-            if (c < nz) out[c] = dacc[c];
+            if (c < nz) out[c] = dacc[c] + half1[wv >> 1][c][col];
     }
 }
 
@@ -325,7 +335,7 @@ hipError_t launch_forward_density(const Grid& G, const float* means, const float
                                   float* density, hipStream_t s) {
     const int T = scene_tiles(G) * G.scenes;
     if (T <= 0) return hipSuccess;
-    const int groups = (int)ceil_div(T, kDenWaves);
+    const int groups = (int)ceil_div(T, kDenWaves / 2);   // two waves per tile
     const int blocks = (int)ceil_div(groups, 8) * 8;
     G2V_LAUNCH(k_fwd_density, dim3(blocks), dim3(kDenWaves * 64), 0, s, G, means, opacity, cov_inv, lb,
                ub, tile_offsets, sorted_gauss, M, density);
