@@ -412,9 +412,6 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
         tb = uniform(xcd_remap(blockIdx.x, gridDim.x));
         if (tb >= T * G.scenes) return;
     }
-    const int j0 = uniform(min(max(toff[tb], 0), M));
-    const int Ng = uniform(min(max(toff[tb + 1], j0), M)) - j0;
-    if (Ng <= skip_le) return;   // empty, or a short list that k_bwd_tile_short takes
     const int scene = uniform(tb / T), tile = tb - scene * T;
     if (scene > 0) {   // the scene's voxel rows
         const int64_t vb = scene * scene_voxels(G);
@@ -435,15 +432,36 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
     const bool tile_in = (tx + 1) * kTile <= G.dims[0] && (ty + 1) * kTile <= G.dims[1] &&
                          (tz + 1) * kTile <= G.dims[2];
 
+    // the tile's voxel values are requested with its list bounds (they do not depend on them)
+    int vx = 0;
+    bool vok = false;
+    float vgd = 0.0f, vd = 0.0f;
     if (threadIdx.x < 64) {
         int x, y, z;
         tile_voxel(G, tile, threadIdx.x, x, y, z);
-        const bool ok = in_grid(G, x, y, z);
-        const int64_t v = ok ? voxel_index(G, x, y, z) : 0;
+        vok = in_grid(G, x, y, z);
+        vx = vok ? (int)voxel_index(G, x, y, z) : 0;
+        vgd = gD[vx];
+        vd = density[vx];
+    }
+    const int j0 = uniform(min(max(toff[tb], 0), M));
+    const int Ng = uniform(min(max(toff[tb + 1], j0), M)) - j0;
+    if (Ng <= skip_le) return;   // empty, or a short list that k_bwd_tile_short takes
+    // the first pass's list entries, requested before the voxel values are staged (raw values at
+    // clamped positions; the entries past the pass are selected away where they are used)
+    const int lwave = uniform(threadIdx.x >> 6), llane = threadIdx.x & 63;
+    const int pc0 = min(kBtPass, Ng);
+    const int l0 = sorted_gauss[j0 + min((int)threadIdx.x, pc0 - 1)];
+    int lrow0[kBtDma];
+#pragma unroll
+    for (int i = 0; i < kBtDma; ++i) lrow0[i] = sorted_gauss[j0 + min((lwave + kBtWaves * i) * 8 + (llane >> 3), pc0 - 1)];
+    if (threadIdx.x < 64) {
+        const bool ok = vok;
+        const int64_t v = vx;
         sm.vlin[threadIdx.x] = ok ? (int)v : -1;
-        sm.gD[threadIdx.x] = ok ? gD[v] : 0.0f;
-        sm.D[threadIdx.x] = ok ? density[v] : 0.0f;
-        sm.inv[threadIdx.x] = ok ? 1.0f / fmaxf(density[v], kEps) : 0.0f;
+        sm.gD[threadIdx.x] = ok ? vgd : 0.0f;
+        sm.D[threadIdx.x] = ok ? vd : 0.0f;
+        sm.inv[threadIdx.x] = ok ? 1.0f / fmaxf(vd, kEps) : 0.0f;
         sm.tv[threadIdx.x] = 0.0f;
         if constexpr (FU) {
             const float scale = cg.grad_loss[0] * cg.inv_count;   // as the loss's own backward forms it
@@ -599,15 +617,26 @@ __global__ void __launch_bounds__(kBtThreads, 1) k_bwd_tile(
         // are issued before the parameters are staged and both are in flight together.
         const int* list = sorted_gauss + j0 + pbase;
         const int kent = threadIdx.x;                        // this thread's list entry (staging)
-        const int gk = kent < pcount ? list[kent] : -1;
+        int gk, grow[kBtDma];
+        if (pbase == 0) {   // requested at the tile start
+            gk = kent < pcount ? l0 : -1;
+#pragma unroll
+            for (int i = 0; i < kBtDma; ++i) grow[i] = (wave + kBtWaves * i) * 8 + (lane >> 3) < pcount ? lrow0[i] : n;
+        } else {
+            gk = kent < pcount ? list[kent] : -1;
+#pragma unroll
+            for (int i = 0; i < kBtDma; ++i) {
+                const int r = (wave + kBtWaves * i) * 8 + (lane >> 3);
+                grow[i] = r < pcount ? list[r] : n;
+            }
+        }
         uint32_t doff[kBtDma];
 #pragma unroll
         for (int i = 0; i < kBtDma; ++i) {
             const int rg = wave + kBtWaves * i;
             const int r = rg * 8 + (lane >> 3);
-            const int g = r < pcount ? list[r] : n;
             const int piece = (lane & 7) ^ swz(r);
-            doff[i] = (rg * 8 < pcount) ? (uint32_t)g * fstride + (uint32_t)piece * 16u : (uint32_t)n * fstride;
+            doff[i] = (rg * 8 < pcount) ? (uint32_t)grow[i] * fstride + (uint32_t)piece * 16u : (uint32_t)n * fstride;
         }
         // the wave's groups within the list are its first nf (rg grows with i)
         int nf = 0;
