@@ -174,6 +174,8 @@ FWD_CASES = {
     "density_only": W.Workload("dens", 5000, None, var_range=(0.1, 0.6)),
     "wide_long_lists": W.Workload("wide", 4000, 32, var_range=(2.0, 12.0), mean_pad=4.0),
     "wide_channels_300": W.Workload("c300", 1500, 300, voxel_range=W.RANGE_SMALL),
+    "single_channel": W.Workload("c1", 1500, 1, voxel_range=W.RANGE_SMALL),
+    "two_channels_long_lists": W.Workload("c2wide", 3000, 2, var_range=(2.0, 12.0), mean_pad=4.0),
     # all Gaussians in a 40 x 40 x 16-voxel block of the 200 x 200 x 16 grid: lists of several hundred
     # there (two passes in phase A) and short or empty lists elsewhere, so the matrix-core kernels
     # walk the compacted list of long tiles
@@ -231,6 +233,8 @@ BWD_CASES = {
     "wide_long_lists": W.Workload("wide", 3000, 32, var_range=(2.0, 12.0), mean_pad=4.0),
     "odd_channels_13": W.Workload("odd13", 800, 13, voxel_range=W.RANGE_SMALL),
     "channels_300": W.Workload("c300", 800, 300, voxel_range=W.RANGE_SMALL),
+    "single_channel": W.Workload("c1", 800, 1, voxel_range=W.RANGE_SMALL),
+    "two_channels_long_lists": W.Workload("c2wide", 3000, 2, var_range=(2.0, 12.0), mean_pad=4.0),
     "clustered_long_lists": W.Workload("clustered", 2000, 16, grads="randn",
                                        extra={"mean_box": (-8.0, -8.0, -1.0, 8.0, 8.0, 5.4)}),
     "recorded_batch_density": W.mmdet_workload(),
