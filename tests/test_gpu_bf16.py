@@ -53,6 +53,7 @@ CASES = {
     "c256": W.Workload("bf_c256", 600, 256, voxel_range=W.RANGE_SMALL, var_range=(0.2, 1.5)),
     # 16-byte grad_feats loads need 8 bfloat16 channels per piece: C = 20 takes the element loads
     "c20_element_loads": W.Workload("bf_c20", 600, 20, voxel_range=W.RANGE_SMALL, var_range=(0.2, 1.5)),
+    "single_channel": W.Workload("bf_c1", 600, 1, voxel_range=W.RANGE_SMALL, var_range=(0.2, 1.5)),
 }
 
 

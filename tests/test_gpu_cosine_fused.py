@@ -8,7 +8,8 @@ instead of reading a materialised gradient of grid_feats.  Bars:
   writes that gradient and reads it back): forward outputs and loss identical, every input
   gradient within L2-relative 1e-4;
 * against the float64 oracle chain (cosine_loss_grad_f64 -> backward_f64): 1e-3, the backward bar.
-Cases: 64 channels on the 50 x 50 x 8 grid; 1024 channels (32 K chunks); lists longer than one
+Cases: 64 channels on the 50 x 50 x 8 grid; 1024 channels (32 K chunks); 4 channels (one 16-byte
+row piece); lists longer than one
 256-entry pass of phase A (its t_v from the rows); a grid whose dimensions are not multiples of 4
 (voxels past the grid in boundary tiles); no valid voxel (k = 0); the un-prepared entry point
 (CSR rebuilt from the reference's backward arguments); and types the fused kernels do not take
@@ -39,6 +40,7 @@ CASES = {
     "c1024": W.Workload("c1024", 900, 1024, voxel_range=W.RANGE_SMALL),
     "long_lists": W.Workload("wide", 3000, 32, var_range=(2.0, 12.0), mean_pad=4.0),
     "ragged_grid": W.Workload("ragged", 1200, 16, voxel_range=(-10.0, -10.0, -1.0, 9.6, 9.2, 1.8)),
+    "four_channels": W.Workload("c4", 1200, 4, voxel_range=W.RANGE_SMALL),
 }
 
 
