@@ -80,8 +80,20 @@ static Regions make_regions(const Grid& G) {
 // Gaussian's gradients are d mu = o sum r q, d Sigma = o/2 sum r q q^T (symmetric), d o = sum r
 // (reference .cu:1304-1362 with gw = gD: sum gw w q, sum gw w q q^T / 2, sum gw e, w = o e), with
 // o and 1/2 applied once per Gaussian instead of per voxel.  d_a = x_a s_a + (r0_a + s_a/2 - mu_a):
-// one conversion and one fma per axis.
+// one conversion and one fma per axis.  The lanes sum q' = kq q instead of q (exp(-m/2) =
+// exp2(d^T q')), and the factors kq and kq^2 come off with o and 1/2.
+// The walk is VALU-bound: the lane keeps its voxel's grid coordinates and its 32-bit voxel index
+// and steps both by the carries of the box digits (no multiplies per voxel), and the loop runs a
+// uniform count of full 64-voxel rounds with the partial round after it.
+// kNarrow: the scene's voxel byte offsets fit in 32 bits (loads from a scalar base and a 32-bit
+// offset).
 // ------------------------------------------------------------------------------------------
+
+// floor(a / b) for 0 <= a < 2^23, b > 0: the correctly rounded float quotient never reaches the
+// next integer for such a (its distance to it, at least 1/b, exceeds half an ulp of a/b).
+__device__ __forceinline__ int small_quot(int a, int b) { return (int)((float)a / (float)b); }
+
+template <bool kNarrow>
 __global__ void __launch_bounds__(256) k_bwd_density(Grid G, int n, const float* __restrict__ gD,
                                                      const float* __restrict__ means,
                                                      const float* __restrict__ opacity,
@@ -99,61 +111,75 @@ __global__ void __launch_bounds__(256) k_bwd_density(Grid G, int n, const float*
     load_params(p, g, means, cov_inv, opacity, lb, ub);
     const int ex = p.ub[0] - p.lb[0] + 1, ey = p.ub[1] - p.lb[1] + 1, ez = p.ub[2] - p.lb[2] + 1;
     const int nv = (ex > 0 && ey > 0 && ez > 0) ? ex * ey * ez : 0;
-    const int eyz = ey * ez;
-    float off[3];
+    float off[3], B[9];
 #pragma unroll
     for (int a = 0; a < 3; ++a) off[a] = fmaf(0.5f, G.s[a], G.r0[a]) - p.mu[a];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) B[k] = kq * p.A[k];
     float sr = 0.f, sq[3] = {0.f, 0.f, 0.f}, sqq[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    // Voxel i of the box (z fastest) sits at (ix, iy, iz) = the digits of i in radix (ey, ez).  A
-    // lane visits i = lane, lane + 64, ...: its position is stepped by the digits (sx, sy, sz) of
-    // 64, with at most one carry per digit, instead of divided out at every voxel.
-    int ix = 0, iy = 0, iz = 0, sx = 0, sy = 0, sz = 0;
     if (nv > 0) {
-        ix = lane / eyz;
-        iy = (lane - ix * eyz) / ez;
-        iz = lane - ix * eyz - iy * ez;
-        sx = 64 / eyz;
-        sy = (64 - sx * eyz) / ez;
-        sz = 64 - sx * eyz - sy * ez;
-    }
-    for (int i = lane; i < nv; i += 64) {
-        const int x = p.lb[0] + ix, y = p.lb[1] + iy, z = p.lb[2] + iz;
-        const float dx = fmaf((float)x, G.s[0], off[0]);
-        const float dy = fmaf((float)y, G.s[1], off[1]);
-        const float dz = fmaf((float)z, G.s[2], off[2]);
-        const float qx = fmaf(p.A[0], dx, fmaf(p.A[1], dy, p.A[2] * dz));
-        const float qy = fmaf(p.A[3], dx, fmaf(p.A[4], dy, p.A[5] * dz));
-        const float qz = fmaf(p.A[6], dx, fmaf(p.A[7], dy, p.A[8] * dz));
-        const float m = fmaf(dx, qx, fmaf(dy, qy, dz * qz));
-        const float r = gD[voxel_index(G, x, y, z)] * __builtin_amdgcn_exp2f(kq * m);
-        sr += r;
-        const float rx = r * qx, ry = r * qy, rz = r * qz;
-        sq[0] += rx;
-        sq[1] += ry;
-        sq[2] += rz;
-        sqq[0] = fmaf(rx, qx, sqq[0]);
-        sqq[1] = fmaf(ry, qy, sqq[1]);
-        sqq[2] = fmaf(rz, qz, sqq[2]);
-        sqq[3] = fmaf(rx, qy, sqq[3]);
-        sqq[4] = fmaf(rx, qz, sqq[4]);
-        sqq[5] = fmaf(ry, qz, sqq[5]);
-        iz += sz;
-        const int cz = iz >= ez ? 1 : 0;
-        iz -= cz * ez;
-        iy += sy + cz;
-        const int cy = iy >= ey ? 1 : 0;
-        iy -= cy * ey;
-        ix += sx + cy;
+        // Voxel i of the box (z fastest) has box digits (ix, iy, iz) in radix (ey, ez).  A lane
+        // visits i = lane, lane + 64, ...: its digits step by the digits (sx, sy, sz) of 64, with at
+        // most one carry per digit.
+        const int eyz = ey * ez;
+        const int ix = small_quot(lane, eyz);
+        const int iy = small_quot(lane - ix * eyz, ez);
+        const int iz = lane - ix * eyz - iy * ez;
+        const int sx = 64 / eyz;
+        const int sy = (64 - sx * eyz) / ez;
+        const int sz = 64 - sx * eyz - sy * ez;
+        const unsigned Y = (unsigned)G.dims[1], Z = (unsigned)G.dims[2];
+        int x = p.lb[0] + ix, y = p.lb[1] + iy, z = p.lb[2] + iz;
+        unsigned v = ((unsigned)x * Y + (unsigned)y) * Z + (unsigned)z;
+        const unsigned dv = ((unsigned)sx * Y + (unsigned)sy) * Z + (unsigned)sz;
+        const unsigned dvz = Z - (unsigned)ez, dvy = (Y - (unsigned)ey) * Z;   // carry corrections
+        const int zmax = p.ub[2], ymax = p.ub[1];
+        auto visit = [&]() {
+            const float gd = kNarrow ? *reinterpret_cast<const float*>(reinterpret_cast<const char*>(gD) + (v << 2))
+                                     : gD[v];
+            const float dx = fmaf((float)x, G.s[0], off[0]);
+            const float dy = fmaf((float)y, G.s[1], off[1]);
+            const float dz = fmaf((float)z, G.s[2], off[2]);
+            const float qx = fmaf(B[0], dx, fmaf(B[1], dy, B[2] * dz));
+            const float qy = fmaf(B[3], dx, fmaf(B[4], dy, B[5] * dz));
+            const float qz = fmaf(B[6], dx, fmaf(B[7], dy, B[8] * dz));
+            const float m = fmaf(dx, qx, fmaf(dy, qy, dz * qz));
+            const float r = gd * __builtin_amdgcn_exp2f(m);
+            sr += r;
+            const float rx = r * qx, ry = r * qy, rz = r * qz;
+            sq[0] += rx;
+            sq[1] += ry;
+            sq[2] += rz;
+            sqq[0] = fmaf(rx, qx, sqq[0]);
+            sqq[1] = fmaf(ry, qy, sqq[1]);
+            sqq[2] = fmaf(rz, qz, sqq[2]);
+            sqq[3] = fmaf(rx, qy, sqq[3]);
+            sqq[4] = fmaf(rx, qz, sqq[4]);
+            sqq[5] = fmaf(ry, qz, sqq[5]);
+        };
+        const int rounds = nv >> 6;
+        for (int k = 0; k < rounds; ++k) {
+            visit();
+            z += sz;
+            const bool cz = z > zmax;
+            z -= cz ? ez : 0;
+            y += sy + (cz ? 1 : 0);
+            const bool cy = y > ymax;
+            y -= cy ? ey : 0;
+            x += sx + (cy ? 1 : 0);
+            v += dv + (cz ? dvz : 0u) + (cy ? dvy : 0u);
+        }
+        if (lane < (nv & 63)) visit();
     }
     // the wave's sums: lanes 2k, 2k + 1 of each half hold value k after the transposed butterfly
-    float v[16] = {sq[0], sq[1], sq[2], sqq[0], sqq[1], sqq[2], sqq[3], sqq[4], sqq[5], sr, 0.f, 0.f, 0.f, 0.f,
-                   0.f, 0.f};
-    float t = transpose_sum16(v, lane & 31);
+    float vs[16] = {sq[0], sq[1], sq[2], sqq[0], sqq[1], sqq[2], sqq[3], sqq[4], sqq[5], sr, 0.f, 0.f, 0.f, 0.f,
+                    0.f, 0.f};
+    float t = transpose_sum16(vs, lane & 31);
     t += __shfl_xor(t, 32, 64);
     // value k of lane 2k: mu xyz, cov xx yy zz xy xz yz, opacity (the order of write_grads)
-    const float h = 0.5f * p.o;
+    const float fq = p.o / kq, fqq = 0.5f * p.o / (kq * kq);
     const int k = (lane & 31) >> 1;
-    const float gv = k < 3 ? p.o * t : (k < 9 ? h * t : t);
+    const float gv = k < 3 ? fq * t : (k < 9 ? fqq * t : t);
     if (lane < 20 && (lane & 1) == 0) {
         if (k < 3) grad_means[g * 3 + k] = gv;
         else if (k == 9) grad_opacity[g] = gv;
@@ -173,8 +199,13 @@ hipError_t launch_backward_density(const Grid& G, int n, const float* grad_densi
                                    const int* lb, const int* ub, float* grad_means, float* grad_cov,
                                    float* grad_opacity, hipStream_t s) {
     if (n <= 0) return hipSuccess;
-    G2V_LAUNCH(k_bwd_density, dim3((unsigned)ceil_div(n, 4)), dim3(256), 0, s, G, n, grad_density, means,
-               opacity, cov_inv, lb, ub, grad_means, grad_cov, grad_opacity);
+    const dim3 grid((unsigned)ceil_div(n, 4)), block(256);
+    if (scene_voxels(G) < (int64_t(1) << 30))
+        G2V_LAUNCH(k_bwd_density<true>, grid, block, 0, s, G, n, grad_density, means, opacity, cov_inv, lb, ub,
+                   grad_means, grad_cov, grad_opacity);
+    else
+        G2V_LAUNCH(k_bwd_density<false>, grid, block, 0, s, G, n, grad_density, means, opacity, cov_inv, lb, ub,
+                   grad_means, grad_cov, grad_opacity);
     return hipGetLastError();
 }
 
