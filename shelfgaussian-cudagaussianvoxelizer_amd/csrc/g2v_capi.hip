@@ -66,12 +66,15 @@ struct SplatBufs {
     void* sort_ws;
     uint32_t* fpk;      // features as packed bf16 (hi, lo) pairs, forward only
     int* tl;            // long-tile list of the forward (count, then the list), forward only
+    DenParams* drec;    // packed per-Gaussian records of the density-only forward
     size_t bytes;
 };
 
 // with_packed: room for the packed features (a caller that packs them with
-// g2v_forward_pack_features passes its own buffer instead).
-SplatBufs carve_splat(void* ws, int n, int64_t M, const Grid& G, int feat_dim = 0, bool with_packed = true) {
+// g2v_forward_pack_features passes its own buffer instead).  A density-only forward (feat_dim 0,
+// with_records) also carves the packed records of its Gaussians.
+SplatBufs carve_splat(void* ws, int n, int64_t M, const Grid& G, int feat_dim = 0, bool with_packed = true,
+                      bool with_records = false) {
     const int64_t m = M > 0 ? M : 1;
     const int T = num_tiles(G);
     Carver c(ws, (size_t)-1);
@@ -84,18 +87,22 @@ SplatBufs carve_splat(void* ws, int n, int64_t M, const Grid& G, int feat_dim = 
     b.sort_ws = c.take<char>(sort_workspace(M, T));
     b.fpk = feat_dim > 0 && with_packed ? c.take<uint32_t>((int64_t)(n + 1) * packed_channels(feat_dim)) : nullptr;
     b.tl = feat_dim > 0 ? c.take<int>(long_list_ints(M, T, feat_dim)) : nullptr;
+    b.drec = feat_dim == 0 && with_records ? c.take<DenParams>(n > 0 ? n : 1) : nullptr;
     b.bytes = c.off + 256;
     return b;
 }
 
 // G->T gauss ids, stable sort by tile, tile offsets: the Tile->Gaussian CSR.  A batch sorts by
-// the batch's tile ids (b.keys, written beside the scene-local g2t_tile_ids_out).
+// the batch's tile ids (b.keys, written beside the scene-local g2t_tile_ids_out).  With b.drec, the
+// G->T fill also packs the Gaussians' records (from means, opacity and cov_inv).
 int build_t2g(const Grid& G, int n, const int* lb, const int* ub, const int* g2t_offsets,
               int* g2t_tile_ids_out, const int* g2t_tile_ids_in, int64_t M, const SplatBufs& b,
-              hipStream_t s) {
+              hipStream_t s, const float* means = nullptr, const float* opacity = nullptr,
+              const float* cov_inv = nullptr) {
     const int T = num_tiles(G);
     if (M > 0) {
-        G2V_HIP(launch_fill_g2t(G, n, lb, ub, g2t_offsets, g2t_tile_ids_out, b.gauss_ids, s, b.keys));
+        G2V_HIP(launch_fill_g2t(G, n, lb, ub, g2t_offsets, g2t_tile_ids_out, b.gauss_ids, s, b.keys, means, opacity,
+                                cov_inv, b.drec));
         const int* keys = b.keys ? b.keys : g2t_tile_ids_out ? g2t_tile_ids_out : g2t_tile_ids_in;
         G2V_HIP(radix_sort_pairs(keys, b.gauss_ids, b.sorted_tiles, b.sorted_gauss, M, T, b.sort_ws, s));
     }
@@ -299,7 +306,7 @@ size_t g2v_forward_splat_workspace(int n, int feat_dim, long long num_pairs, con
                                    const float voxel_range[6]) {
     Grid G;
     if (make_grid(voxel_size, voxel_range, G) != G2V_OK) return 0;
-    return carve_splat(nullptr, n, num_pairs, G, feat_dim, false).bytes;
+    return carve_splat(nullptr, n, num_pairs, G, feat_dim, false, true).bytes;
 }
 
 size_t g2v_forward_packed_bytes(int n, int feat_dim) {
@@ -354,10 +361,10 @@ int splat_impl(const Grid& G, int n, int feat_dim, const float* means3D, const f
     if ((double)scene_voxels(G) * G.scenes * (double)feat_dim >= 9.2e18)
         return fail(G2V_ERR_LIMIT, "grid_feats too large");
     const bool own_pack = packed == nullptr;
-    const SplatBufs need = carve_splat(nullptr, n, num_pairs, G, feat_dim, own_pack);
+    const SplatBufs need = carve_splat(nullptr, n, num_pairs, G, feat_dim, own_pack, true);
     int rc = check_ws(workspace, workspace_bytes, need.bytes, "splat");
     if (rc != G2V_OK) return rc;
-    SplatBufs b = carve_splat(workspace, n, num_pairs, G, feat_dim, own_pack);
+    SplatBufs b = carve_splat(workspace, n, num_pairs, G, feat_dim, own_pack, true);
     if (!own_pack) b.fpk = static_cast<uint32_t*>(const_cast<void*>(packed));
     if (t2g_tiles && t2g_gauss && t2g_offsets) {   // the caller keeps the Tile->Gaussian CSR
         b.sorted_tiles = t2g_tiles;
@@ -367,15 +374,14 @@ int splat_impl(const Grid& G, int n, int feat_dim, const float* means3D, const f
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (feat_dim > 0 && own_pack) G2V_HIP(launch_split_pack(n, feat_dim, features, feat_dtype, b.fpk, s));
     rc = build_t2g(G, n, valid_voxel_lb, valid_voxel_ub, g2t_offsets, g2t_tile_ids, nullptr,
-                   num_pairs, b, s);
+                   num_pairs, b, s, means3D, opacity, cov_inv);
     if (rc != G2V_OK) return rc;
     if (feat_dim > 0)
         G2V_HIP(launch_forward_feats(G, feat_dim, means3D, opacity, cov_inv, valid_voxel_lb,
                                      valid_voxel_ub, b.tile_offsets, b.sorted_gauss, (int)num_pairs, n,
                                      features, feat_dtype, b.fpk, density, grid_feats, b.tl, s));
     else
-        G2V_HIP(launch_forward_density(G, means3D, opacity, cov_inv, valid_voxel_lb, valid_voxel_ub,
-                                       b.tile_offsets, b.sorted_gauss, (int)num_pairs, density, s));
+        G2V_HIP(launch_forward_density(G, b.drec, b.tile_offsets, b.sorted_gauss, (int)num_pairs, density, s));
     return G2V_OK;
 }
 
@@ -897,7 +903,7 @@ size_t g2v_batch_forward_splat_workspace(int num_scenes, int n, int feat_dim, lo
     if (!batch_tiles_ok(G, num_scenes)) return 0;   // the batch's tile ids would overflow int32
     G.scenes = num_scenes;
     G.scene_n = n;
-    return carve_splat(nullptr, num_scenes * n, num_pairs, G, feat_dim).bytes;
+    return carve_splat(nullptr, num_scenes * n, num_pairs, G, feat_dim, true, true).bytes;
 }
 
 int g2v_batch_forward_splat(int num_scenes, int n, int feat_dim, const float* means3D, const float* opacity,

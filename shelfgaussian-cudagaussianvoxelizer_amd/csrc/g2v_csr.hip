@@ -322,13 +322,37 @@ __global__ void __launch_bounds__(256) k_fill_g2t(Grid G, int n, const int* __re
                                                   const int* __restrict__ g2t_offsets,
                                                   int* __restrict__ tile_ids,
                                                   int* __restrict__ gauss_ids,
-                                                  int* __restrict__ keys) {
+                                                  int* __restrict__ keys,
+                                                  const float* __restrict__ means,
+                                                  const float* __restrict__ opacity,
+                                                  const float* __restrict__ cov_inv,
+                                                  DenParams* __restrict__ drec) {
     const int l = threadIdx.x & (kFillLanes - 1);
     const int g = blockIdx.x * (256 / kFillLanes) + threadIdx.x / kFillLanes;
     if (g >= n) return;
     const int base = g2t_offsets[g];
     const int cnt = g2t_offsets[g + 1] - base;
     if (cnt <= 0) return;
+    if (drec) {   // the Gaussian's packed record, one 32-bit word per lane (only listed Gaussians are read)
+        static_assert(kFillLanes == 16, "one lane per word of DenParams");
+        uint32_t w;
+        if (l < 3) {
+            w = __float_as_uint(means[g * 3 + l]);
+        } else if (l == 3) {
+            w = __float_as_uint(opacity[g]);
+        } else if (l < 10) {   // a00 a01 a11 a02 a12 a22: kq (A[i0] + A[i1]) off the diagonal
+            const int k = l - 4;
+            const int i0 = k == 0 ? 0 : k == 1 ? 1 : k == 2 ? 4 : k == 3 ? 2 : k == 4 ? 5 : 8;
+            const int i1 = k == 1 ? 3 : k == 3 ? 6 : k == 4 ? 7 : -1;
+            const float* A = cov_inv + g * 9;
+            w = __float_as_uint(i1 >= 0 ? kq * (A[i0] + A[i1]) : kq * A[i0]);
+        } else if (l < 13) {
+            w = (uint32_t)lb[g * 3 + l - 10];
+        } else {
+            w = (uint32_t)ub[g * 3 + l - 13];
+        }
+        reinterpret_cast<uint32_t*>(drec)[(size_t)g * 16 + l] = w;
+    }
     const int tx0 = lb[g * 3] / kTile, ty0 = lb[g * 3 + 1] / kTile, tz0 = lb[g * 3 + 2] / kTile;
     const int dy = ub[g * 3 + 1] / kTile - ty0 + 1;
     const int dz = ub[g * 3 + 2] / kTile - tz0 + 1;
@@ -356,10 +380,12 @@ __global__ void __launch_bounds__(256) k_fill_g2t(Grid G, int n, const int* __re
 }
 
 hipError_t launch_fill_g2t(const Grid& G, int n, const int* lb, const int* ub,
-                           const int* g2t_offsets, int* tile_ids, int* gauss_ids, hipStream_t s, int* keys) {
+                           const int* g2t_offsets, int* tile_ids, int* gauss_ids, hipStream_t s, int* keys,
+                           const float* means, const float* opacity, const float* cov_inv, DenParams* drec) {
     if (n <= 0) return hipSuccess;
+    if (drec && (!means || !opacity || !cov_inv)) return hipErrorInvalidValue;
     G2V_LAUNCH(k_fill_g2t, dim3((unsigned)ceil_div(n, 256 / kFillLanes)), dim3(256), 0, s, G, n, lb, ub,
-               g2t_offsets, tile_ids, gauss_ids, keys);
+               g2t_offsets, tile_ids, gauss_ids, keys, means, opacity, cov_inv, drec);
     return hipGetLastError();
 }
 

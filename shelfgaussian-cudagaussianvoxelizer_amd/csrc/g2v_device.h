@@ -176,6 +176,19 @@ __device__ __forceinline__ void gauss_q(const GaussParams& p, float cx, float cy
 
 constexpr float kq = -0.72134752044448170f;   // -log2(e)/2: exp(-m/2) = exp2(kq m)
 
+// One Gaussian's values as the density-only forward reads them, packed into one aligned 64-byte
+// record (written beside its G->T rows): mean, opacity, the exponent coefficients kq A00,
+// kq (A01 + A10), kq A11, kq (A02 + A20), kq (A12 + A21), kq A22, and the box.  A list entry then
+// costs one 64-byte gather instead of one from each of five arrays.
+struct alignas(16) DenParams {
+    float mux, muy, muz, o;
+    float a00, a01, a11, a02;
+    float a12, a22;
+    int lbx, lby;
+    int lbz, ubx, uby, ubz;
+};
+static_assert(sizeof(DenParams) == 64, "DenParams is four 16-byte words");
+
 __device__ __forceinline__ float centre(const Grid& G, int a, int i) {
     return fmaf((float)i + 0.5f, G.s[a], G.r0[a]);
 }

@@ -113,30 +113,33 @@ struct alignas(16) FwdRec {
 };
 static_assert(sizeof(FwdRec) == 48, "FwdRec is three 16-byte words");
 
-// The record of Gaussian g for the tile whose first voxel is (x0, y0, z0).
-__device__ __forceinline__ FwdRec fwd_record(int g, const float* __restrict__ means, const float* __restrict__ opacity,
-                                             const float* __restrict__ cov_inv, const int* __restrict__ lb,
-                                             const int* __restrict__ ub, int x0, int y0, int z0) {
-    FwdRec r;
+// The values of Gaussian g that its records are formed from, as loaded (19 words).
+struct FwdRaw {
     float A[9];
-#pragma unroll
-    for (int i = 0; i < 9; ++i) A[i] = cov_inv[g * 9 + i];
+    float mu[3];
+    float o;
     int l[3], u[3];
+};
+
+__device__ __forceinline__ FwdRaw fwd_raw(int g, const float* __restrict__ means, const float* __restrict__ opacity,
+                                          const float* __restrict__ cov_inv, const int* __restrict__ lb,
+                                          const int* __restrict__ ub) {
+    FwdRaw w;
+#pragma unroll
+    for (int i = 0; i < 9; ++i) w.A[i] = cov_inv[g * 9 + i];
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
-        l[i] = lb[g * 3 + i];
-        u[i] = ub[g * 3 + i];
+        w.l[i] = lb[g * 3 + i];
+        w.u[i] = ub[g * 3 + i];
+        w.mu[i] = means[g * 3 + i];
     }
-    r.mux = means[g * 3 + 0];
-    r.muy = means[g * 3 + 1];
-    r.o = opacity[g];
-    r.a00 = kq * A[0];
-    r.a01 = kq * (A[1] + A[3]);
-    r.a11 = kq * A[4];
-    r.a02 = kq * (A[2] + A[6]);
-    r.a12 = kq * (A[5] + A[7]);
-    r.mu2 = means[g * 3 + 2];
-    r.a22 = kq * A[8];
+    w.o = opacity[g];
+    return w;
+}
+
+// The box masks of a record for the tile whose first voxel is (x0, y0, z0) (box l..u).
+__device__ __forceinline__ void fwd_record_masks(FwdRec& r, const int (&l)[3], const int (&u)[3], int x0, int y0,
+                                                 int z0) {
     uint32_t xm = 0, ym = 0, zm = 0;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -149,7 +152,48 @@ __device__ __forceinline__ FwdRec fwd_record(int g, const float* __restrict__ me
 #pragma unroll
     for (int a = 0; a < 4; ++a) m |= (xm >> a) & 1u ? ym << (4 * a) : 0u;
     r.xymask = m;
+}
+
+// The record of a Gaussian (its loaded values w) for the tile whose first voxel is (x0, y0, z0).
+__device__ __forceinline__ FwdRec fwd_record_of(const FwdRaw& w, int x0, int y0, int z0) {
+    FwdRec r;
+    r.mux = w.mu[0];
+    r.muy = w.mu[1];
+    r.o = w.o;
+    r.a00 = kq * w.A[0];
+    r.a01 = kq * (w.A[1] + w.A[3]);
+    r.a11 = kq * w.A[4];
+    r.a02 = kq * (w.A[2] + w.A[6]);
+    r.a12 = kq * (w.A[5] + w.A[7]);
+    r.mu2 = w.mu[2];
+    r.a22 = kq * w.A[8];
+    fwd_record_masks(r, w.l, w.u, x0, y0, z0);
     return r;
+}
+
+// The same record from a packed DenParams (its coefficients already formed as above).
+__device__ __forceinline__ FwdRec fwd_record_packed(const DenParams& w, int x0, int y0, int z0) {
+    FwdRec r;
+    r.mux = w.mux;
+    r.muy = w.muy;
+    r.o = w.o;
+    r.a00 = w.a00;
+    r.a01 = w.a01;
+    r.a11 = w.a11;
+    r.a02 = w.a02;
+    r.a12 = w.a12;
+    r.mu2 = w.muz;
+    r.a22 = w.a22;
+    const int l[3] = {w.lbx, w.lby, w.lbz}, u[3] = {w.ubx, w.uby, w.ubz};
+    fwd_record_masks(r, l, u, x0, y0, z0);
+    return r;
+}
+
+// The record of Gaussian g for the tile whose first voxel is (x0, y0, z0).
+__device__ __forceinline__ FwdRec fwd_record(int g, const float* __restrict__ means, const float* __restrict__ opacity,
+                                             const float* __restrict__ cov_inv, const int* __restrict__ lb,
+                                             const int* __restrict__ ub, int x0, int y0, int z0) {
+    return fwd_record_of(fwd_raw(g, means, opacity, cov_inv, lb, ub), x0, y0, z0);
 }
 
 // A record past the list: every weight is exactly 0 (o = 0, empty masks).
@@ -241,11 +285,7 @@ __device__ __forceinline__ void wave_lds_sync() {
     __asm__ __volatile__("" ::: "memory");
 }
 
-__global__ void __launch_bounds__(kDenWaves * 64) k_fwd_density(Grid G, const float* __restrict__ means,
-                                                               const float* __restrict__ opacity,
-                                                               const float* __restrict__ cov_inv,
-                                                               const int* __restrict__ lb,
-                                                               const int* __restrict__ ub,
+__global__ void __launch_bounds__(kDenWaves * 64) k_fwd_density(Grid G, const DenParams* __restrict__ drec,
                                                                const int* __restrict__ toff,
                                                                const int* __restrict__ sorted_gauss,
                                                                int M, float* __restrict__ density) {
@@ -270,24 +310,30 @@ __global__ void __launch_bounds__(kDenWaves * 64) k_fwd_density(Grid G, const fl
     for (int c = 0; c < 4; ++c) cz[c] = centre(G, 2, z0 + c);
     const int j0 = live ? uniform(min(max(toff[tb], 0), M)) : 0;
     const int j1 = live ? uniform(min(max(toff[tb + 1], j0), M)) : 0;
-    auto fetch = [&](int j) {
-        return den_record(j < j1 ? fwd_record(sorted_gauss[j], means, opacity, cov_inv, lb, ub, x0, y0, z0)
-                                 : fwd_record_empty(), cz);
+    // A batch's packed records (one 64-byte gather per entry) are held across the previous batch's
+    // evaluation and turned into tile records after it, so the gathers' latency passes under that
+    // evaluation; the list entries run one batch further ahead.  graw < 0: past the list (an empty
+    // record).
+    auto load_raw = [&](int g, DenParams& w) {
+        if (g >= 0) w = drec[g];
+    };
+    auto record = [&](int g, const DenParams& w) {
+        return den_record(g >= 0 ? fwd_record_packed(w, x0, y0, z0) : fwd_record_empty(), cz);
     };
     float dacc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    // The list entries run one batch ahead of the records: a batch's record loads then wait for one
-    // load latency (its entries arrived during the previous batch), not two.
     const int jh = j0 + 64 * half;   // this wave's first batch
-    DenRec nxt = fetch(jh + lane);
+    DenParams raw = {};
+    int graw = jh + lane < j1 ? sorted_gauss[jh + lane] : -1;
+    load_raw(graw, raw);
     int gnext = jh + 128 + lane < j1 ? sorted_gauss[jh + 128 + lane] : -1;
     for (int jb = jh; jb < j1; jb += 128) {
+        const DenRec cur = record(graw, raw);
         wave_lds_sync();   // the previous records are read
-        sl[lane] = nxt;
+        sl[lane] = cur;
         wave_lds_sync();
-        const int gcur = gnext;
+        graw = gnext;
+        load_raw(graw, raw);   // before the next entry load: the counter of loads is in order
         gnext = jb + 256 + lane < j1 ? sorted_gauss[jb + 256 + lane] : -1;
-        nxt = den_record(gcur >= 0 ? fwd_record(gcur, means, opacity, cov_inv, lb, ub, x0, y0, z0) : fwd_record_empty(),
-                         cz);
         // slots past the list hold empty records (weight 0), so every lane group runs the same count
         const int n4 = uniform((min(64, j1 - jb) + 3) >> 2);
         for (int k4 = 0; k4 < n4; ++k4) {
@@ -329,16 +375,15 @@ __global__ void __launch_bounds__(kDenWaves * 64) k_fwd_density(Grid G, const fl
     }
 }
 
-hipError_t launch_forward_density(const Grid& G, const float* means, const float* opacity,
-                                  const float* cov_inv, const int* lb, const int* ub,
-                                  const int* tile_offsets, const int* sorted_gauss, int M,
-                                  float* density, hipStream_t s) {
+hipError_t launch_forward_density(const Grid& G, const DenParams* drec, const int* tile_offsets,
+                                  const int* sorted_gauss, int M, float* density, hipStream_t s) {
     const int T = scene_tiles(G) * G.scenes;
     if (T <= 0) return hipSuccess;
+    if (M > 0 && !drec) return hipErrorInvalidValue;
     const int groups = (int)ceil_div(T, kDenWaves / 2);   // two waves per tile
     const int blocks = (int)ceil_div(groups, 8) * 8;
-    G2V_LAUNCH(k_fwd_density, dim3(blocks), dim3(kDenWaves * 64), 0, s, G, means, opacity, cov_inv, lb,
-               ub, tile_offsets, sorted_gauss, M, density);
+    G2V_LAUNCH(k_fwd_density, dim3(blocks), dim3(kDenWaves * 64), 0, s, G, drec, tile_offsets, sorted_gauss, M,
+               density);
     return hipGetLastError();
 }
 
@@ -825,9 +870,7 @@ hipError_t launch_forward_feats(const Grid& G, int C, const float* means, const 
                                 void* grid_feats, int* tl_ws, hipStream_t s) {
     const int T = scene_tiles(G) * G.scenes;
     if (T <= 0) return hipSuccess;
-    if (C <= 0)
-        return launch_forward_density(G, means, opacity, cov_inv, lb, ub, tile_offsets, sorted_gauss,
-                                      M, density, s);
+    if (C <= 0) return hipErrorInvalidValue;   // density only: launch_forward_density
     const int Cp = packed_channels(C);
     if ((int64_t)(n + 1) * Cp * 4 > (int64_t)UINT32_MAX) return hipErrorInvalidValue;   // byte offsets are 32-bit
     const int blocks = (int)ceil_div(T, 8) * 8;

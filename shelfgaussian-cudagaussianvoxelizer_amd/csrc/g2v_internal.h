@@ -52,9 +52,12 @@ hipError_t launch_boxes(const Grid& G, int n, const float* means, const float* c
                         int* lb, int* ub, int* nvox, int* g2t_offsets, const int* cell, int* cell_offsets,
                         hipStream_t s, long long* zero = nullptr, int nzero = 0);
 // keys (optional): the batch's tile ids (sort keys) beside the scene-local tile_ids.
+// drec (optional, with means, opacity and cov_inv): the packed record of every Gaussian that has
+// G->T rows, for the density-only forward.
 hipError_t launch_fill_g2t(const Grid& G, int n, const int* lb, const int* ub,
                            const int* g2t_offsets, int* tile_ids, int* gauss_ids, hipStream_t s,
-                           int* keys = nullptr);
+                           int* keys = nullptr, const float* means = nullptr, const float* opacity = nullptr,
+                           const float* cov_inv = nullptr, DenParams* drec = nullptr);
 
 // A batch of B scenes of n Gaussians: the per-scene G->T row offsets out (B x (n + 1)) and pair
 // counts (counts[b], b < B; counts[B] = *mr_total, or 0 when mr_total is null) from the batch's
@@ -112,10 +115,9 @@ inline bool region_offsets_fit(const Grid& G, int C) {
 // kernels' float32 products stay cheaper than a tile slot of the matrix-core kernels, 32 above.
 inline int short_list_max(int C) { return C <= 256 ? 64 : 32; }
 
-hipError_t launch_forward_density(const Grid& G, const float* means, const float* opacity,
-                                  const float* cov_inv, const int* lb, const int* ub,
-                                  const int* tile_offsets, const int* sorted_gauss, int M,
-                                  float* density, hipStream_t s);
+// drec: the packed records launch_fill_g2t wrote.
+hipError_t launch_forward_density(const Grid& G, const DenParams* drec, const int* tile_offsets,
+                                  const int* sorted_gauss, int M, float* density, hipStream_t s);
 // The features as packed bf16 (hi, lo) pairs for k_fwd_feats (packed_channels(C) 32-bit words per
 // row, plus a zero row); it depends on the features alone.
 hipError_t launch_split_pack(int n, int C, const void* features, int fdt, uint32_t* fpk, hipStream_t s);

@@ -161,7 +161,9 @@ def test_workspace_queries_grow_with_problem():
     vs, vr = L.floats([0.4] * 3), L.floats(W.RANGE_PAPER)
     a = lib.g2v_forward_splat_workspace(1000, 0, 10_000, vs, vr)
     b = lib.g2v_forward_splat_workspace(1000, 0, 1_000_000, vs, vr)
-    assert lib.g2v_forward_splat_workspace(1000, 64, 10_000, vs, vr) > a
+    assert a >= 1000 * 64   # the density-only splat packs a 64-byte record per Gaussian
+    f1 = lib.g2v_forward_splat_workspace(1000, 64, 10_000, vs, vr)
+    assert 0 < f1 < lib.g2v_forward_splat_workspace(1000, 64, 1_000_000, vs, vr)
     assert 0 < a < b
     assert lib.g2v_backward_workspace(1000, 64, 10_000, 2000, vs, vr) > lib.g2v_backward_workspace(1000, 0, 10_000, 0, vs, vr)
     assert lib.g2v_backward_workspace(1000, 64, 10_000, 4000, vs, vr) > lib.g2v_backward_workspace(1000, 64, 10_000, 2000, vs, vr)
