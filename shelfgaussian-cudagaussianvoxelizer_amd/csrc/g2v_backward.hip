@@ -75,18 +75,19 @@ static Regions make_regions(const Grid& G) {
 }
 
 // ------------------------------------------------------------------------------------------
-// Density only: one wave per Gaussian walks the voxels of its box (z fastest).  Per voxel, with
-// d = centre - mu, q = A d and r = gD e, e = exp(-d^T q / 2): the lane sums r, r q and r q q^T; the
-// Gaussian's gradients are d mu = o sum r q, d Sigma = o/2 sum r q q^T (symmetric), d o = sum r
-// (reference .cu:1304-1362 with gw = gD: sum gw w q, sum gw w q q^T / 2, sum gw e, w = o e), with
-// o and 1/2 applied once per Gaussian instead of per voxel.  d_a = x_a s_a + (r0_a + s_a/2 - mu_a):
-// one conversion and one fma per axis.  The lanes sum q' = kq q instead of q (exp(-m/2) =
-// exp2(d^T q')), and the factors kq and kq^2 come off with o and 1/2.
-// The walk is VALU-bound: the lane keeps its voxel's grid coordinates and its 32-bit voxel index
-// and steps both by the carries of the box digits (no multiplies per voxel), and the loop runs a
-// uniform count of full 64-voxel rounds with the partial round after it.
-// kNarrow: the scene's voxel byte offsets fit in 32 bits (loads from a scalar base and a 32-bit
-// offset).
+// Density only: one wave per Gaussian walks the voxels of its box.  Per voxel, with d = centre - mu,
+// q = A d and r = gD e, e = exp(-d^T q / 2): the Gaussian's gradients are d mu = o sum r q,
+// d Sigma = o/2 sum r q q^T (symmetric), d o = sum r (reference .cu:1304-1362 with gw = gD:
+// sum gw w q, sum gw w q q^T / 2, sum gw e, w = o e), with o and 1/2 applied once per Gaussian.
+// The lanes take the box's (y, z) cells (z fastest, 64 at a time) and walk x.  Along a lane's
+// line only dx changes: with q' = kq q = q0 + b dx (b = kq A e_x, q0 = kq A (0, dy, dz)), the exponent
+// of exp2 is d^T q' = alpha + beta dx + gamma dx^2, and the line's sums of r, r q' and r q' q'^T
+// follow from R0 = sum r, R1 = sum r dx, R2 = sum r dx^2 (q0 R0 + b R1, q0 q0^T R0 +
+// (q0 b^T + b q0^T) R1 + b b^T R2), turned into them once per line.  A voxel then costs an exp2 and
+// about ten other operations.  dx = x s_x + (r0_x + s_x/2 - mu_x), x an exact float integer.  The
+// lane's gD loads run one chunk of four voxels ahead.  The factors kq and kq^2 come off with o and
+// 1/2.  kNarrow: the scene's voxel byte offsets fit in 32 bits (loads from a scalar base and a
+// 32-bit offset).
 // ------------------------------------------------------------------------------------------
 
 // floor(a / b) for 0 <= a < 2^23, b > 0: the correctly rounded float quotient never reaches the
@@ -103,6 +104,7 @@ __global__ void __launch_bounds__(256) k_bwd_density(Grid G, int n, const float*
                                                      float* __restrict__ grad_means,
                                                      float* __restrict__ grad_cov,
                                                      float* __restrict__ grad_opacity) {
+    constexpr int kChunk = 4;
     const int lane = threadIdx.x & 63;
     const int g = uniform(blockIdx.x * 4 + (threadIdx.x >> 6));
     if (g >= n) return;
@@ -110,66 +112,71 @@ __global__ void __launch_bounds__(256) k_bwd_density(Grid G, int n, const float*
     GaussParams p;
     load_params(p, g, means, cov_inv, opacity, lb, ub);
     const int ex = p.ub[0] - p.lb[0] + 1, ey = p.ub[1] - p.lb[1] + 1, ez = p.ub[2] - p.lb[2] + 1;
-    const int nv = (ex > 0 && ey > 0 && ez > 0) ? ex * ey * ez : 0;
+    const bool live = ex > 0 && ey > 0 && ez > 0;
     float off[3], B[9];
 #pragma unroll
     for (int a = 0; a < 3; ++a) off[a] = fmaf(0.5f, G.s[a], G.r0[a]) - p.mu[a];
 #pragma unroll
     for (int k = 0; k < 9; ++k) B[k] = kq * p.A[k];
+    const float bq[3] = {B[0], B[3], B[6]};   // q' per unit dx
     float sr = 0.f, sq[3] = {0.f, 0.f, 0.f}, sqq[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (nv > 0) {
-        // Voxel i of the box (z fastest) has box digits (ix, iy, iz) in radix (ey, ez).  A lane
-        // visits i = lane, lane + 64, ...: its digits step by the digits (sx, sy, sz) of 64, with at
-        // most one carry per digit.
-        const int eyz = ey * ez;
-        const int ix = small_quot(lane, eyz);
-        const int iy = small_quot(lane - ix * eyz, ez);
-        const int iz = lane - ix * eyz - iy * ez;
-        const int sx = 64 / eyz;
-        const int sy = (64 - sx * eyz) / ez;
-        const int sz = 64 - sx * eyz - sy * ez;
-        const unsigned Y = (unsigned)G.dims[1], Z = (unsigned)G.dims[2];
-        int x = p.lb[0] + ix, y = p.lb[1] + iy, z = p.lb[2] + iz;
-        unsigned v = ((unsigned)x * Y + (unsigned)y) * Z + (unsigned)z;
-        const unsigned dv = ((unsigned)sx * Y + (unsigned)sy) * Z + (unsigned)sz;
-        const unsigned dvz = Z - (unsigned)ez, dvy = (Y - (unsigned)ey) * Z;   // carry corrections
-        const int zmax = p.ub[2], ymax = p.ub[1];
-        auto visit = [&]() {
-            const float gd = kNarrow ? *reinterpret_cast<const float*>(reinterpret_cast<const char*>(gD) + (v << 2))
-                                     : gD[v];
-            const float dx = fmaf((float)x, G.s[0], off[0]);
-            const float dy = fmaf((float)y, G.s[1], off[1]);
-            const float dz = fmaf((float)z, G.s[2], off[2]);
-            const float qx = fmaf(B[0], dx, fmaf(B[1], dy, B[2] * dz));
-            const float qy = fmaf(B[3], dx, fmaf(B[4], dy, B[5] * dz));
-            const float qz = fmaf(B[6], dx, fmaf(B[7], dy, B[8] * dz));
-            const float m = fmaf(dx, qx, fmaf(dy, qy, dz * qz));
-            const float r = gd * __builtin_amdgcn_exp2f(m);
-            sr += r;
-            const float rx = r * qx, ry = r * qy, rz = r * qz;
-            sq[0] += rx;
-            sq[1] += ry;
-            sq[2] += rz;
-            sqq[0] = fmaf(rx, qx, sqq[0]);
-            sqq[1] = fmaf(ry, qy, sqq[1]);
-            sqq[2] = fmaf(rz, qz, sqq[2]);
-            sqq[3] = fmaf(rx, qy, sqq[3]);
-            sqq[4] = fmaf(rx, qz, sqq[4]);
-            sqq[5] = fmaf(ry, qz, sqq[5]);
-        };
-        const int rounds = nv >> 6;
-        for (int k = 0; k < rounds; ++k) {
-            visit();
-            z += sz;
-            const bool cz = z > zmax;
-            z -= cz ? ez : 0;
-            y += sy + (cz ? 1 : 0);
-            const bool cy = y > ymax;
-            y -= cy ? ey : 0;
-            x += sx + (cy ? 1 : 0);
-            v += dv + (cz ? dvz : 0u) + (cy ? dvy : 0u);
+    const int eyz = live ? ey * ez : 0;
+    const unsigned Y = (unsigned)G.dims[1], Z = (unsigned)G.dims[2], YZ = Y * Z;
+    const int nchunks = (ex + kChunk - 1) / kChunk;
+    auto gload = [&](unsigned v) {
+        return kNarrow ? *reinterpret_cast<const float*>(reinterpret_cast<const char*>(gD) + (v << 2)) : gD[v];
+    };
+    for (int s0 = 0; s0 < eyz; s0 += 64) {
+        const int sl = s0 + lane;
+        const bool act = sl < eyz;
+        const int iy = eyz < (1 << 22) ? small_quot(sl, ez) : sl / ez;   // sl < eyz + 64 < 2^23
+        const int iz = sl - iy * ez;
+        const float dy = fmaf((float)(p.lb[1] + iy), G.s[1], off[1]);
+        const float dz = fmaf((float)(p.lb[2] + iz), G.s[2], off[2]);
+        const float q0[3] = {fmaf(B[1], dy, B[2] * dz), fmaf(B[4], dy, B[5] * dz), fmaf(B[7], dy, B[8] * dz)};
+        const float alpha = fmaf(dy, q0[1], dz * q0[2]);
+        const float beta = fmaf(B[3], dy, fmaf(B[6], dz, q0[0]));
+        const float gamma = B[0];
+        float R0 = 0.f, R1 = 0.f, R2 = 0.f;
+        if (act) {
+            // every load is issued (a chunk past the line's end reloads its last voxel), so that the
+            // counter of loads stays exact across the uniform branches below
+            const unsigned vb = ((unsigned)p.lb[0] * Y + (unsigned)(p.lb[1] + iy)) * Z + (unsigned)(p.lb[2] + iz);
+            auto ld = [&](int xo) { return gload(vb + (unsigned)min(xo, ex - 1) * YZ); };
+            float fx = (float)p.lb[0];
+            float cur[kChunk];
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) cur[k] = ld(k);
+            for (int c = 0; c < nchunks; ++c) {
+                float nxt[kChunk];
+#pragma unroll
+                for (int k = 0; k < kChunk; ++k) nxt[k] = ld((c + 1) * kChunk + k);
+#pragma unroll
+                for (int k = 0; k < kChunk; ++k) {
+                    if (c * kChunk + k < ex) {
+                        const float dx = fmaf(fx, G.s[0], off[0]);
+                        const float r = cur[k] * __builtin_amdgcn_exp2f(fmaf(fmaf(gamma, dx, beta), dx, alpha));
+                        R0 += r;
+                        const float rdx = r * dx;
+                        R1 += rdx;
+                        R2 = fmaf(rdx, dx, R2);
+                        fx += 1.0f;
+                    }
+                }
+#pragma unroll
+                for (int k = 0; k < kChunk; ++k) cur[k] = nxt[k];
+            }
         }
-        if (lane < (nv & 63)) visit();
+        // the line's sums in q': q' = q0 + b dx
+        sr += R0;
+#pragma unroll
+        for (int a = 0; a < 3; ++a) sq[a] += fmaf(q0[a], R0, bq[a] * R1);
+        const int pi[6] = {0, 1, 2, 0, 0, 1}, pj[6] = {0, 1, 2, 1, 2, 2};   // xx yy zz xy xz yz
+#pragma unroll
+        for (int k = 0; k < 6; ++k) {
+            const int a = pi[k], b = pj[k];
+            sqq[k] += fmaf(q0[a] * q0[b], R0, fmaf(fmaf(q0[a], bq[b], bq[a] * q0[b]), R1, bq[a] * bq[b] * R2));
+        }
     }
     // the wave's sums: lanes 2k, 2k + 1 of each half hold value k after the transposed butterfly
     float vs[16] = {sq[0], sq[1], sq[2], sqq[0], sqq[1], sqq[2], sqq[3], sqq[4], sqq[5], sr, 0.f, 0.f, 0.f, 0.f,
