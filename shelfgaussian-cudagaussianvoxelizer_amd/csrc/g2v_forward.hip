@@ -234,9 +234,10 @@ __device__ __forceinline__ void fwd_column_weights(const FwdRec* rec, int col, f
 
 // ------------------------------------------------------------------------------------------
 // Density only: two waves per tile, each walking every other batch of 64 entries of the tile's
-// list in ascending order: lane k turns entry k into its tile-relative record (the records of the
-// wave's next batch are gathered while the current ones are evaluated) and writes it into the
-// wave's LDS slab.  Lane (col = lane % 16, ph = lane / 16) then takes the voxel column col and the entries
+// list in ascending order: lane k gathers entry k's packed 64-byte DenParams (written by the G->T
+// fill; one gather instead of one from each of five arrays, whose L2 misses bounded the kernel),
+// turns it into its tile-relative record and writes that into the wave's LDS slab (the packed
+// records of the wave's next batch are gathered while the current ones are evaluated).  Lane (col = lane % 16, ph = lane / 16) then takes the voxel column col and the entries
 // ph, ph + 4, ... of the slab, forming each entry's four weights of the column with the
 // operations of fwd_column_weights (so the weights of the feature splat); the z terms dz_c and
 // fz_c, the same for every column, are formed once per entry by the lane that builds its record.
