@@ -172,6 +172,10 @@ FWD_CASES = {
     "odd_channels_13": W.Workload("odd13", 1500, 13, voxel_range=W.RANGE_SMALL),
     "channels_40_outside": W.Workload("c40", 500, 40, num_outside=50),
     "density_only": W.Workload("dens", 5000, None, var_range=(0.1, 0.6)),
+    # density only with boxes up to ~30 voxels a side, some past the grid: lists of several hundred
+    # entries (many 64-entry batches per wave), and in the backward many rounds of 64 (y, z) lines
+    # and lines of many 4-voxel chunks
+    "density_wide": W.Workload("dens_wide", 1500, None, var_range=(2.0, 12.0), mean_pad=4.0, grads="randn"),
     "wide_long_lists": W.Workload("wide", 4000, 32, var_range=(2.0, 12.0), mean_pad=4.0),
     "wide_channels_300": W.Workload("c300", 1500, 300, voxel_range=W.RANGE_SMALL),
     "single_channel": W.Workload("c1", 1500, 1, voxel_range=W.RANGE_SMALL),
@@ -230,6 +234,7 @@ def test_backward_reference_harness_config():
 BWD_CASES = {
     "cfg1": W.CONFIGS[1],
     "density_only": W.Workload("dens", 3000, None, var_range=(0.1, 0.6)),
+    "density_wide": W.Workload("dens_wide", 1500, None, var_range=(2.0, 12.0), mean_pad=4.0, grads="randn"),
     "wide_long_lists": W.Workload("wide", 3000, 32, var_range=(2.0, 12.0), mean_pad=4.0),
     "odd_channels_13": W.Workload("odd13", 800, 13, voxel_range=W.RANGE_SMALL),
     "channels_300": W.Workload("c300", 800, 300, voxel_range=W.RANGE_SMALL),
