@@ -96,8 +96,8 @@ int g2v_forward_pack_features(int n, int feat_dim, const void* features, int fea
  * for fewer Gaussians or channels, is rejected with G2V_ERR_INVALID).
  * When t2g_tiles, t2g_gauss (M each) and t2g_offsets (T+1) are all non-NULL the
  * Tile->Gaussian CSR is built there (and can be handed to g2v_backward, which then skips
- * rebuilding it); otherwise it lives in the workspace.  With feat_dim == 0 the workspace also
- * holds a 64-byte packed record per Gaussian for the density splat (included in the size
+ * rebuilding it); otherwise it lives in the workspace.  The workspace also holds a 64-byte
+ * packed record per Gaussian that the splat's tile kernels gather (included in the size
  * g2v_forward_splat_workspace returns).  Asynchronous. */
 size_t g2v_forward_splat_workspace(int n, int feat_dim, long long num_pairs, const float voxel_size[3],
                                    const float voxel_range[6]);

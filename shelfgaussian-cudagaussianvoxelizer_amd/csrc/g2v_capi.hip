@@ -66,13 +66,13 @@ struct SplatBufs {
     void* sort_ws;
     uint32_t* fpk;      // features as packed bf16 (hi, lo) pairs, forward only
     int* tl;            // long-tile list of the forward (count, then the list), forward only
-    DenParams* drec;    // packed per-Gaussian records of the density-only forward
+    DenParams* drec;    // packed per-Gaussian records of the forward's tile kernels
     size_t bytes;
 };
 
 // with_packed: room for the packed features (a caller that packs them with
-// g2v_forward_pack_features passes its own buffer instead).  A density-only forward (feat_dim 0,
-// with_records) also carves the packed records of its Gaussians.
+// g2v_forward_pack_features passes its own buffer instead).  with_records: the forward's packed
+// per-Gaussian records (written by the G->T fill).
 SplatBufs carve_splat(void* ws, int n, int64_t M, const Grid& G, int feat_dim = 0, bool with_packed = true,
                       bool with_records = false) {
     const int64_t m = M > 0 ? M : 1;
@@ -87,7 +87,7 @@ SplatBufs carve_splat(void* ws, int n, int64_t M, const Grid& G, int feat_dim = 
     b.sort_ws = c.take<char>(sort_workspace(M, T));
     b.fpk = feat_dim > 0 && with_packed ? c.take<uint32_t>((int64_t)(n + 1) * packed_channels(feat_dim)) : nullptr;
     b.tl = feat_dim > 0 ? c.take<int>(long_list_ints(M, T, feat_dim)) : nullptr;
-    b.drec = feat_dim == 0 && with_records ? c.take<DenParams>(n > 0 ? n : 1) : nullptr;
+    b.drec = with_records ? c.take<DenParams>(n > 0 ? n : 1) : nullptr;
     b.bytes = c.off + 256;
     return b;
 }
@@ -379,7 +379,7 @@ int splat_impl(const Grid& G, int n, int feat_dim, const float* means3D, const f
     if (feat_dim > 0)
         G2V_HIP(launch_forward_feats(G, feat_dim, means3D, opacity, cov_inv, valid_voxel_lb,
                                      valid_voxel_ub, b.tile_offsets, b.sorted_gauss, (int)num_pairs, n,
-                                     features, feat_dtype, b.fpk, density, grid_feats, b.tl, s));
+                                     features, feat_dtype, b.fpk, b.drec, density, grid_feats, b.tl, s));
     else
         G2V_HIP(launch_forward_density(G, b.drec, b.tile_offsets, b.sorted_gauss, (int)num_pairs, density, s));
     return G2V_OK;

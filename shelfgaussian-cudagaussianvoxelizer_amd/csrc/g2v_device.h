@@ -176,7 +176,7 @@ __device__ __forceinline__ void gauss_q(const GaussParams& p, float cx, float cy
 
 constexpr float kq = -0.72134752044448170f;   // -log2(e)/2: exp(-m/2) = exp2(kq m)
 
-// One Gaussian's values as the density-only forward reads them, packed into one aligned 64-byte
+// One Gaussian's values as the forward's tile kernels read them, packed into one aligned 64-byte
 // record (written beside its G->T rows): mean, opacity, the exponent coefficients kq A00,
 // kq (A01 + A10), kq A11, kq (A02 + A20), kq (A12 + A21), kq A22, and the box.  A list entry then
 // costs one 64-byte gather instead of one from each of five arrays.

@@ -113,30 +113,6 @@ struct alignas(16) FwdRec {
 };
 static_assert(sizeof(FwdRec) == 48, "FwdRec is three 16-byte words");
 
-// The values of Gaussian g that its records are formed from, as loaded (19 words).
-struct FwdRaw {
-    float A[9];
-    float mu[3];
-    float o;
-    int l[3], u[3];
-};
-
-__device__ __forceinline__ FwdRaw fwd_raw(int g, const float* __restrict__ means, const float* __restrict__ opacity,
-                                          const float* __restrict__ cov_inv, const int* __restrict__ lb,
-                                          const int* __restrict__ ub) {
-    FwdRaw w;
-#pragma unroll
-    for (int i = 0; i < 9; ++i) w.A[i] = cov_inv[g * 9 + i];
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-        w.l[i] = lb[g * 3 + i];
-        w.u[i] = ub[g * 3 + i];
-        w.mu[i] = means[g * 3 + i];
-    }
-    w.o = opacity[g];
-    return w;
-}
-
 // The box masks of a record for the tile whose first voxel is (x0, y0, z0) (box l..u).
 __device__ __forceinline__ void fwd_record_masks(FwdRec& r, const int (&l)[3], const int (&u)[3], int x0, int y0,
                                                  int z0) {
@@ -154,24 +130,8 @@ __device__ __forceinline__ void fwd_record_masks(FwdRec& r, const int (&l)[3], c
     r.xymask = m;
 }
 
-// The record of a Gaussian (its loaded values w) for the tile whose first voxel is (x0, y0, z0).
-__device__ __forceinline__ FwdRec fwd_record_of(const FwdRaw& w, int x0, int y0, int z0) {
-    FwdRec r;
-    r.mux = w.mu[0];
-    r.muy = w.mu[1];
-    r.o = w.o;
-    r.a00 = kq * w.A[0];
-    r.a01 = kq * (w.A[1] + w.A[3]);
-    r.a11 = kq * w.A[4];
-    r.a02 = kq * (w.A[2] + w.A[6]);
-    r.a12 = kq * (w.A[5] + w.A[7]);
-    r.mu2 = w.mu[2];
-    r.a22 = kq * w.A[8];
-    fwd_record_masks(r, w.l, w.u, x0, y0, z0);
-    return r;
-}
-
-// The same record from a packed DenParams (its coefficients already formed as above).
+// The record of a Gaussian from its packed DenParams (the coefficients kq A00, kq (A01 + A10), ...
+// formed by the G->T fill) for the tile whose first voxel is (x0, y0, z0).
 __device__ __forceinline__ FwdRec fwd_record_packed(const DenParams& w, int x0, int y0, int z0) {
     FwdRec r;
     r.mux = w.mux;
@@ -187,13 +147,6 @@ __device__ __forceinline__ FwdRec fwd_record_packed(const DenParams& w, int x0, 
     const int l[3] = {w.lbx, w.lby, w.lbz}, u[3] = {w.ubx, w.uby, w.ubz};
     fwd_record_masks(r, l, u, x0, y0, z0);
     return r;
-}
-
-// The record of Gaussian g for the tile whose first voxel is (x0, y0, z0).
-__device__ __forceinline__ FwdRec fwd_record(int g, const float* __restrict__ means, const float* __restrict__ opacity,
-                                             const float* __restrict__ cov_inv, const int* __restrict__ lb,
-                                             const int* __restrict__ ub, int x0, int y0, int z0) {
-    return fwd_record_of(fwd_raw(g, means, opacity, cov_inv, lb, ub), x0, y0, z0);
 }
 
 // A record past the list: every weight is exactly 0 (o = 0, empty masks).
@@ -406,11 +359,7 @@ struct FwdSmem {
 // fragments (8 entries x 1 voxel each).  Adds the raw weights of the column's voxels to dacc
 // (a build repeated for a later channel pass adds them again; only the first pass reads dacc).
 __device__ __forceinline__ void fwd_build_w(FwdSmem& sm, int j0, int kbeg, int klen, int ksteps,
-                                            float (&dacc)[4],
-                                            const float* __restrict__ means,
-                                            const float* __restrict__ opacity,
-                                            const float* __restrict__ cov_inv,
-                                            const int* __restrict__ lb, const int* __restrict__ ub,
+                                            float (&dacc)[4], const DenParams* __restrict__ drec,
                                             const int* __restrict__ sorted_gauss, uint32_t row_bytes,
                                             uint32_t zero_off, int x0, int y0, int z0,
                                             const float (&cz)[4], float cxl, float cyl) {
@@ -418,7 +367,7 @@ __device__ __forceinline__ void fwd_build_w(FwdSmem& sm, int j0, int kbeg, int k
     for (int k = threadIdx.x; k < nslots; k += kFwdThreads) {
         if (k < klen) {
             const int g = sorted_gauss[j0 + kbeg + k];
-            sm.rec[k] = fwd_record(g, means, opacity, cov_inv, lb, ub, x0, y0, z0);
+            sm.rec[k] = fwd_record_packed(drec[g], x0, y0, z0);   // one 64-byte gather
             sm.roff[k] = (uint32_t)g * row_bytes;
         } else {
             sm.rec[k] = fwd_record_empty();
@@ -621,9 +570,7 @@ __global__ void __launch_bounds__(kFsThreads) k_fwd_short(
 // OBF16: grid_feats is stored as bfloat16 (rounded to nearest even), else float.
 template <bool OBF16>
 __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
-    Grid G, int C, const float* __restrict__ means, const float* __restrict__ opacity,
-    const float* __restrict__ cov_inv, const int* __restrict__ lb, const int* __restrict__ ub,
-    const int* __restrict__ toff, const int* __restrict__ sorted_gauss, int M, int n, int Cp,
+    Grid G, int C, const DenParams* __restrict__ drec, const int* __restrict__ toff, const int* __restrict__ sorted_gauss, int M, int n, int Cp,
     const uint32_t* __restrict__ fpk, float* __restrict__ density,
     void* __restrict__ grid_feats_out, int skip_le, const int* __restrict__ tlist, const int* __restrict__ tcount) {
     __shared__ FwdSmem sm;
@@ -704,8 +651,8 @@ __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
             const int ksteps = ((klen + 31) >> 5) * 2;   // even: the MFMA loop takes steps in pairs
             if (nkc > 1 || cbase == 0) {
                 __syncthreads();  // previous readers of W are done
-                fwd_build_w(sm, j0, kbeg, klen, ksteps, dacc, means, opacity, cov_inv, lb,
-                            ub, sorted_gauss, row_bytes, zero_off, x0, y0, z0, cz, cxl, cyl);
+                fwd_build_w(sm, j0, kbeg, klen, ksteps, dacc, drec, sorted_gauss, row_bytes, zero_off, x0, y0, z0,
+                            cz, cxl, cyl);
                 __syncthreads();
             }
             if (has_ch) {
@@ -867,11 +814,12 @@ hipError_t launch_split_pack(int n, int C, const void* features, int fdt, uint32
 hipError_t launch_forward_feats(const Grid& G, int C, const float* means, const float* opacity,
                                 const float* cov_inv, const int* lb, const int* ub,
                                 const int* tile_offsets, const int* sorted_gauss, int M, int n,
-                                const void* features, int fdt, const uint32_t* fpk, float* density,
-                                void* grid_feats, int* tl_ws, hipStream_t s) {
+                                const void* features, int fdt, const uint32_t* fpk, const DenParams* drec,
+                                float* density, void* grid_feats, int* tl_ws, hipStream_t s) {
     const int T = scene_tiles(G) * G.scenes;
     if (T <= 0) return hipSuccess;
     if (C <= 0) return hipErrorInvalidValue;   // density only: launch_forward_density
+    if (M > 0 && !drec) return hipErrorInvalidValue;
     const int Cp = packed_channels(C);
     if ((int64_t)(n + 1) * Cp * 4 > (int64_t)UINT32_MAX) return hipErrorInvalidValue;   // byte offsets are 32-bit
     const int blocks = (int)ceil_div(T, 8) * 8;
@@ -894,16 +842,14 @@ hipError_t launch_forward_feats(const Grid& G, int C, const float* means, const 
         G2V_LAUNCH(k_fwd_short<true>, dim3(blocks), dim3(kFsThreads), 0, s, G, C, means, opacity, cov_inv, lb, ub,
                    tile_offsets, sorted_gauss, M, features, density, grid_feats, smax);
         if (nlong > 0)
-            G2V_LAUNCH(k_fwd_feats<true>, dim3(lblocks), dim3(kFwdThreads), 0, s, G, C, means, opacity, cov_inv, lb,
-                       ub, tile_offsets, sorted_gauss, M, n, Cp, (const uint32_t*)fpk, density, grid_feats, smax, tlist,
-                       tcount);
+            G2V_LAUNCH(k_fwd_feats<true>, dim3(lblocks), dim3(kFwdThreads), 0, s, G, C, drec, tile_offsets,
+                       sorted_gauss, M, n, Cp, (const uint32_t*)fpk, density, grid_feats, smax, tlist, tcount);
     } else {
         G2V_LAUNCH(k_fwd_short<false>, dim3(blocks), dim3(kFsThreads), 0, s, G, C, means, opacity, cov_inv, lb, ub,
                    tile_offsets, sorted_gauss, M, features, density, grid_feats, smax);
         if (nlong > 0)
-            G2V_LAUNCH(k_fwd_feats<false>, dim3(lblocks), dim3(kFwdThreads), 0, s, G, C, means, opacity, cov_inv, lb,
-                       ub, tile_offsets, sorted_gauss, M, n, Cp, (const uint32_t*)fpk, density, grid_feats, smax, tlist,
-                       tcount);
+            G2V_LAUNCH(k_fwd_feats<false>, dim3(lblocks), dim3(kFwdThreads), 0, s, G, C, drec, tile_offsets,
+                       sorted_gauss, M, n, Cp, (const uint32_t*)fpk, density, grid_feats, smax, tlist, tcount);
     }
     return hipGetLastError();
 }

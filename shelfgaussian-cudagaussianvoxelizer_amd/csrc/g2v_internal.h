@@ -53,7 +53,7 @@ hipError_t launch_boxes(const Grid& G, int n, const float* means, const float* c
                         hipStream_t s, long long* zero = nullptr, int nzero = 0);
 // keys (optional): the batch's tile ids (sort keys) beside the scene-local tile_ids.
 // drec (optional, with means, opacity and cov_inv): the packed record of every Gaussian that has
-// G->T rows, for the density-only forward.
+// G->T rows, for the forward's tile kernels.
 hipError_t launch_fill_g2t(const Grid& G, int n, const int* lb, const int* ub,
                            const int* g2t_offsets, int* tile_ids, int* gauss_ids, hipStream_t s,
                            int* keys = nullptr, const float* means = nullptr, const float* opacity = nullptr,
@@ -125,8 +125,8 @@ hipError_t launch_split_pack(int n, int C, const void* features, int fdt, uint32
 hipError_t launch_forward_feats(const Grid& G, int C, const float* means, const float* opacity,
                                 const float* cov_inv, const int* lb, const int* ub,
                                 const int* tile_offsets, const int* sorted_gauss, int M, int n,
-                                const void* features, int fdt, const uint32_t* fpk, float* density,
-                                void* grid_feats, int* tl_ws, hipStream_t s);
+                                const void* features, int fdt, const uint32_t* fpk, const DenParams* drec,
+                                float* density, void* grid_feats, int* tl_ws, hipStream_t s);
 // ints of the long-tile list workspace (tl_ws) of a forward or backward with features.
 inline int long_list_ints(int64_t M, int T, int C) { return 1 + long_tiles_bound(M, T, short_list_max(C)); }
 
