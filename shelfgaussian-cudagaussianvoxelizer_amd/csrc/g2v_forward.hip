@@ -190,8 +190,9 @@ __device__ __forceinline__ void fwd_column_weights(const FwdRec* rec, int col, f
 // list in ascending order: lane k gathers entry k's packed 64-byte DenParams (written by the G->T
 // fill; one gather instead of one from each of five arrays, whose L2 misses bounded the kernel),
 // turns it into its tile-relative record and writes that into the wave's LDS slab (the packed
-// records of the wave's next batch are gathered while the current ones are evaluated).  Lane (col = lane % 16, ph = lane / 16) then takes the voxel column col and the entries
-// ph, ph + 4, ... of the slab, forming each entry's four weights of the column with the
+// records of the wave's next batch are gathered while the current ones are evaluated).  Lane
+// (col = lane % 16, ph = lane / 16) then takes the voxel column col and the entries ph, ph + 4, ...
+// of the slab, forming each entry's four weights of the column with the
 // operations of fwd_column_weights (so the weights of the feature splat); the z terms dz_c and
 // fz_c, the same for every column, are formed once per entry by the lane that builds its record.
 // The four lane groups' sums are added at the end, then the two waves' sums (first wave + second).
@@ -570,7 +571,8 @@ __global__ void __launch_bounds__(kFsThreads) k_fwd_short(
 // OBF16: grid_feats is stored as bfloat16 (rounded to nearest even), else float.
 template <bool OBF16>
 __global__ void __launch_bounds__(kFwdThreads, 2) k_fwd_feats(
-    Grid G, int C, const DenParams* __restrict__ drec, const int* __restrict__ toff, const int* __restrict__ sorted_gauss, int M, int n, int Cp,
+    Grid G, int C, const DenParams* __restrict__ drec, const int* __restrict__ toff,
+    const int* __restrict__ sorted_gauss, int M, int n, int Cp,
     const uint32_t* __restrict__ fpk, float* __restrict__ density,
     void* __restrict__ grid_feats_out, int skip_le, const int* __restrict__ tlist, const int* __restrict__ tcount) {
     __shared__ FwdSmem sm;
