@@ -213,3 +213,22 @@ def test_product_path_does_not_reference_oracle():
             if f.endswith((".py", ".hip", ".h", ".cpp")):
                 text = open(os.path.join(dirpath, f)).read()
                 assert "oracle" not in text.replace("reference", ""), f
+
+
+def test_float_quotient_of_small_integers_is_exact():
+    """The density backward finds a lane's box digits as int((float)a / (float)b) for 0 <= a < 2^23,
+    b >= 1 (csrc/g2v_backward.hip, small_quot): a correctly rounded float32 quotient of such integers,
+    truncated, is floor(a / b).  Checked with IEEE float32 division on random pairs, pairs just below
+    and at multiples of b, and the extremes of the range."""
+    rng = np.random.default_rng(7)
+    a = rng.integers(0, 1 << 23, 400_000, dtype=np.int64)
+    b = rng.integers(1, 1 << 23, 400_000, dtype=np.int64)
+    small_b = rng.integers(1, 4097, 400_000, dtype=np.int64)
+    q = rng.integers(0, 2048, 400_000, dtype=np.int64)
+    near = np.clip(q * small_b + rng.integers(-1, 2, 400_000), 0, (1 << 23) - 1)   # around multiples of b
+    edges_a = np.array([0, 1, (1 << 23) - 1, (1 << 23) - 2, (1 << 22), (1 << 22) - 1], dtype=np.int64)
+    edges_b = np.array([1, 2, 3, (1 << 23) - 1, (1 << 22) + 1, 4095], dtype=np.int64)
+    cases = [(a, b), (near, small_b), (a % 64, small_b)] + [(edges_a, np.full_like(edges_a, e)) for e in edges_b]
+    for aa, bb in cases:
+        got = (aa.astype(np.float32) / bb.astype(np.float32)).astype(np.int64)
+        assert np.array_equal(got, aa // bb)
